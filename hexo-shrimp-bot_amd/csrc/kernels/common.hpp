@@ -1,0 +1,77 @@
+// Shared device helpers for the MantisNet gfx950 kernels: bf16 <-> fp32,
+// 16-byte row-chunk loads/stores, and the launch/flag plumbing.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../../include/mantis_hip.h"
+
+namespace mantis {
+
+// bf16 is carried as raw uint16_t; widening is exact, narrowing rounds to
+// nearest even (NaN stays NaN).
+__device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float(uint32_t(b) << 16); }
+
+__device__ __forceinline__ uint16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return uint16_t(u >> 16);
+}
+
+// Eight consecutive elements of a row as fp32: one 16-byte load for bf16,
+// two for fp32.  `p` must be 16-byte aligned.
+__device__ __forceinline__ void load8(const uint16_t* p, float (&x)[8]) {
+  uint4 u = *reinterpret_cast<const uint4*>(p);
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    x[2 * i] = __uint_as_float(w[i] << 16);
+    x[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+
+__device__ __forceinline__ void load8(const float* p, float (&x)[8]) {
+  float4 a = reinterpret_cast<const float4*>(p)[0];
+  float4 b = reinterpret_cast<const float4*>(p)[1];
+  x[0] = a.x, x[1] = a.y, x[2] = a.z, x[3] = a.w;
+  x[4] = b.x, x[5] = b.y, x[6] = b.z, x[7] = b.w;
+}
+
+__device__ __forceinline__ void store8(float* p, const float (&x)[8]) {
+  reinterpret_cast<float4*>(p)[0] = make_float4(x[0], x[1], x[2], x[3]);
+  reinterpret_cast<float4*>(p)[1] = make_float4(x[4], x[5], x[6], x[7]);
+}
+
+__device__ __forceinline__ void store8(uint16_t* p, const float (&x)[8]) {
+  uint4 u;
+  u.x = uint32_t(f2bf(x[0])) | (uint32_t(f2bf(x[1])) << 16);
+  u.y = uint32_t(f2bf(x[2])) | (uint32_t(f2bf(x[3])) << 16);
+  u.z = uint32_t(f2bf(x[4])) | (uint32_t(f2bf(x[5])) << 16);
+  u.w = uint32_t(f2bf(x[6])) | (uint32_t(f2bf(x[7])) << 16);
+  *reinterpret_cast<uint4*>(p) = u;
+}
+
+__device__ __forceinline__ void raise_flag(int32_t* flag, int32_t bit) {
+  if (flag) atomicOr(flag, bit);
+}
+
+// A CSR segment clamped into [0, n_entries]: even an uninitialised or
+// corrupted pointer array can only yield an in-bounds (possibly empty) run.
+__device__ __forceinline__ void segment(const int64_t* ptr, int64_t row, int64_t n_entries,
+                                        int64_t& start, int64_t& end) {
+  int64_t a = ptr[row], b = ptr[row + 1];
+  a = a < 0 ? 0 : (a > n_entries ? n_entries : a);
+  b = b < a ? a : (b > n_entries ? n_entries : b);
+  start = a;
+  end = b;
+}
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline int32_t launched() { return hipGetLastError() == hipSuccess ? MANTIS_OK : MANTIS_E_LAUNCH; }
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace mantis

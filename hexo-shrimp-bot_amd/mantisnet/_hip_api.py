@@ -1,0 +1,32 @@
+"""ctypes signatures of libmantis_hip.so (include/mantis_hip.h)."""
+
+from __future__ import annotations
+
+import ctypes
+
+vp = ctypes.c_void_p
+i64 = ctypes.c_int64
+i32 = ctypes.c_int32
+f32p = ctypes.POINTER(ctypes.c_float)
+
+SIGNATURES = {
+    "mantis_hip_version": ([], i32),
+    "mantis_runs_to_ptr": ([vp, i64, i64, vp, vp, vp], i32),
+    "mantis_run_reduce": ([vp, i32, i64, i64, i64, vp, i64, vp, i64, vp, i32, vp, vp], i32),
+    "mantis_cell_attention": (
+        [vp, vp, vp, i32, vp, i64, vp, vp, vp, vp, i64, i64, i64, i32, i32, vp, vp, vp, vp, vp], i32),
+    "mantis_latent_read": ([vp, vp, vp, i32, vp, vp, i64, i64, i32, i32, vp, vp, vp, vp, vp], i32),
+    "mantis_latent_broadcast": ([vp, vp, vp, i32, vp, i64, i64, i32, i32, vp, vp, vp, vp, vp], i32),
+    "mantis_row_encode": ([vp, i32, i64, i64, vp, i64, vp, vp, i64, vp, i64, vp, vp, vp, vp, vp], i32),
+    "mantis_stone_attention": ([vp, vp, vp, vp, vp, vp, vp, i64, i32, i64, i32, vp, vp, vp, vp], i32),
+    "mantis_hex_neighbours": ([vp, vp, i64, i64, vp, vp, vp], i32),
+    "mantis_hex_aggregate_linear": ([vp, vp, i64, vp, vp, vp, vp, vp, vp], i32),
+}
+
+
+def bind(lib: ctypes.CDLL) -> ctypes.CDLL:
+    for name, (args, res) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = res
+    return lib

@@ -1,0 +1,169 @@
+/*
+ * mantis_hip.h — C ABI of the MantisNet HIP kernels for MI355X (gfx950),
+ * libmantis_hip.so.
+ *
+ * Conventions shared by every entry point:
+ *  - plain device pointers, element counts and a hipStream_t passed as void*
+ *    (NULL = the default stream); work is enqueued on that stream only;
+ *  - tensors are dense row-major; index and CSR-pointer arrays are int64;
+ *  - `dtype` arguments take MANTIS_F32 or MANTIS_BF16;
+ *  - CSR pointer arrays are clamped into [0, n_entries] on the device, so a
+ *    corrupted pointer can only shorten a run, never leave the entry arrays;
+ *  - every index is bounds-checked on the device: an out-of-range index is
+ *    skipped (never dereferenced) and recorded by atomically OR-ing a
+ *    MANTIS_FLAG_* bit into *err_flag (a device int32; may be NULL).  The
+ *    host wrapper reads the flag once per call sequence and raises;
+ *  - return value: 0 on a successful enqueue, else a MANTIS_E_* code;
+ *  - nothing allocates: outputs and workspaces are caller-owned.
+ */
+#ifndef MANTIS_HIP_H
+#define MANTIS_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MANTIS_F32 0
+#define MANTIS_BF16 1
+
+#define MANTIS_OK 0
+#define MANTIS_E_ARG 1    /* unsupported shape, dtype or null pointer */
+#define MANTIS_E_LAUNCH 2 /* the HIP launch itself failed */
+
+#define MANTIS_FLAG_INDEX 1  /* a gather/scatter index was out of range */
+#define MANTIS_FLAG_ORDER 2  /* a CSR/run view was not ascending */
+
+/* Library/ABI version. */
+int32_t mantis_hip_version(void);
+
+/*
+ * CSR pointers of an ascending destination array:
+ * ptr[d] = first entry with dest >= d, for d in [0, n_dest]
+ * (the searchsorted the reference's table derivations run,
+ *  python/mantisnet/mantisnet/cell_latents.py:142-153, cell_nodes.py:61-70).
+ */
+int32_t mantis_runs_to_ptr(const int64_t* dest, int64_t n_entries, int64_t n_dest,
+                           int64_t* ptr, int32_t* err_flag, void* stream);
+
+/*
+ * Run reduction: out[d, :] = sum over e in [ptr[d], ptr[d+1]) of
+ * values[gather[e], :], accumulated in fp32, cast to out_dtype.  Rows with
+ * no entries are written as zeros.  values is (n_src, ld) with the first `h`
+ * columns read.  Replaces mantisnet::aggregate_to_windows,
+ * aggregate_to_stones, class_row_sum and incidence_row_sum
+ * (python/mantisnet/mantisnet/message_passing.py:40-99, 191-227, 344-365).
+ */
+int32_t mantis_run_reduce(const void* values, int32_t values_dtype, int64_t n_src, int64_t ld,
+                          int64_t h, const int64_t* gather, int64_t n_entries,
+                          const int64_t* ptr, int64_t n_dest, void* out, int32_t out_dtype,
+                          int32_t* err_flag, void* stream);
+
+/*
+ * Typed segment attention, one query row per CSR segment:
+ *   score[e, a] = q[row, a, :] . k[src[e], a, :] / sqrt(hd) + bias[a, cls[e]]
+ *   out[row, a, :] = sum_e softmax_e(score) (v[src[e], a, :] + vcls[cls[e], a, :])
+ * fp32 scores, softmax and sums; a row without entries reads zero.  q/k/v are
+ * (n, heads, hd) in `dtype`; bias (heads, n_classes) fp32; vcls
+ * (n_classes, heads*hd) fp32 or NULL; out (n_q, heads, hd) fp32; m/l
+ * (n_q, heads) fp32 softmax statistics or NULL.  Supports heads*hd == 128.
+ * Replaces mantisnet::cell_attention / cell_attention_plain
+ * (python/mantisnet/mantisnet/cell_latents.py:213-285, 834-1001).
+ */
+int32_t mantis_cell_attention(const void* q, const void* k, const void* v, int32_t dtype,
+                              const float* bias, int64_t n_classes, const float* vcls,
+                              const int64_t* seg_ptr, const int64_t* src, const int64_t* cls,
+                              int64_t n_entries, int64_t n_q, int64_t n_k, int32_t heads,
+                              int32_t hd, float* out,
+                              float* m, float* l, int32_t* err_flag, void* stream);
+
+/*
+ * Window-latent read: four latent queries per position attend over the
+ * position's windows (rows order[offsets[p]:offsets[p+1]] of k/v).  q is
+ * (P, 4, heads, hd), k/v (n_w, heads, hd) in `dtype`; out (P, 4, heads, hd)
+ * fp32; m/l (P, 4, heads) or NULL.  An empty position reads zero.
+ * Replaces mantisnet::window_latent_read (window_latents.py:224-268, 553-577).
+ */
+int32_t mantis_latent_read(const void* q, const void* k, const void* v, int32_t dtype,
+                           const int64_t* offsets, const int64_t* order, int64_t n_pos,
+                           int64_t n_w, int32_t heads, int32_t hd, float* out, float* m, float* l,
+                           int32_t* err_flag, void* stream);
+
+/*
+ * Window-latent broadcast: every window attends over its position's four
+ * latents.  q (n_w, heads, hd), k/v (P, 4, heads, hd) in `dtype`; out
+ * (n_w, heads, hd) fp32; m/l (n_w, heads) or NULL.
+ * Replaces mantisnet::window_latent_broadcast (window_latents.py:350-381, 622-654).
+ */
+int32_t mantis_latent_broadcast(const void* q, const void* k, const void* v, int32_t dtype,
+                                const int64_t* window_pos, int64_t n_pos, int64_t n_w,
+                                int32_t heads, int32_t hd, float* out, float* m, float* l,
+                                int32_t* err_flag, void* stream);
+
+/*
+ * Action-row encoder: for every cell row c,
+ *   out[c, :] = sum over e in [cell_ptr[c], cell_ptr[c+1]) of
+ *               relu(pre[window[e], :] + table[cls[e], :])
+ *             + sum over o < 3 of empty_counts[c, o] * empty_rows[o, :]
+ * fp32.  pre (n_w, h) in `pre_dtype`; table (n_classes, h) fp32;
+ * empty_counts (n_cells, 3) int64 and empty_rows (3, h) fp32 may both be
+ * NULL.  Replaces mantisnet::action_row_encode plus the EMPTY-row regrouping
+ * of the caller (row_encoder.py:40-112, model.py:1031-1063).
+ */
+int32_t mantis_row_encode(const void* pre, int32_t pre_dtype, int64_t n_w, int64_t h,
+                          const float* table, int64_t n_classes, const int64_t* window,
+                          const int64_t* cls, int64_t n_entries, const int64_t* cell_ptr,
+                          int64_t n_cells,
+                          const int64_t* empty_counts, const float* empty_rows, float* out,
+                          int32_t* err_flag, void* stream);
+
+/*
+ * Ragged block-diagonal attention over each position's live prefix, bf16
+ * MFMA (gfx950 v_mfma_f32_16x16x32_bf16) with fp32 online softmax:
+ *   out[p, a, t, :] = softmax_{s < seq_lens[p]}(q[p,a,t,:] . k[p,a,s,:] / sqrt(hd)) v[p,a,s,:]
+ * for t < seq_lens[p]; rows t >= seq_lens[p] are written as exact zeros
+ * (lse 0).  q/k/v/out are bf16 with element strides (sp, sa, st, sd == 1)
+ * given per tensor, so the (P, T, A, hd) -> (P, A, T, hd) transposed views
+ * the model passes need no copy.  lse (P, heads, T) fp32 or NULL.
+ * hd must be 32.  Replaces mantisnet::fused_attention
+ * (python/mantisnet/mantisnet/attention.py:44-162, 719-753).
+ */
+int32_t mantis_stone_attention(const void* q, const int64_t* q_strides, const void* k,
+                               const int64_t* k_strides, const void* v, const int64_t* v_strides,
+                               const int32_t* seq_lens, int64_t n_pos, int32_t heads, int64_t t,
+                               int32_t hd, void* out, const int64_t* out_strides, float* lse,
+                               void* stream);
+
+/*
+ * Six-neighbour table of ragged cell graphs: graph j's cells are
+ * cells[graph_ptr[j]:graph_ptr[j+1]] given as (q, r) int32 pairs in ascending
+ * (q, r) order; nbr[i, s] is the global index of the cell at offset s of
+ * ((+1,0), (-1,0), (0,+1), (0,-1), (+1,-1), (-1,+1)) within the same graph,
+ * or -1.  The adjacency rule is the reference's
+ * (crates/models/mantisnet/src/encoder.rs:1001-1026, builder.py:458-471).
+ */
+int32_t mantis_hex_neighbours(const int32_t* cells_qr, const int64_t* graph_ptr, int64_t n_graphs,
+                              int64_t n_cells, int32_t* nbr, int32_t* err_flag, void* stream);
+
+/*
+ * Hex message passing over the six-neighbour table, fused with a linear
+ * layer: for every cell i with n_i present neighbours,
+ *   sum_i  = sum over present s of x[nbr[i, s], :]            (fp32)
+ *   mean_i = sum_i / n_i, or 0 when n_i == 0
+ *   out_sum[i]  = sum_i  @ W^T + b,   out_mean[i] = mean_i @ W^T + b
+ * x (n_cells, 128) bf16; W (128, 128) bf16 row-major (out, in); b (128) fp32;
+ * out_sum/out_mean (n_cells, 128) bf16.  fp32 accumulation throughout; the
+ * product runs on bf16 MFMA.  No counterpart kernel exists in the reference
+ * (its adjacency feeds typed attention, model.py:463-476); this is the
+ * synthetic message-passing workload of the benchmark configurations.
+ */
+int32_t mantis_hex_aggregate_linear(const void* x, const int32_t* nbr, int64_t n_cells,
+                                    const void* w, const float* b, void* out_sum, void* out_mean,
+                                    int32_t* err_flag, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,235 @@
+"""HIP kernels against the oracle's formulations (GPU).
+
+Each kernel is called through the C ABI (mantisnet.ops -> libmantis_hip.so)
+on seeded inputs and compared with the CPU fp32 oracle evaluated on the same
+(bf16-valued) inputs.  Tolerances are stated per test: fp32-math kernels on
+bf16 inputs agree to summation-order rounding; the MFMA attention rounds the
+softmax probabilities and its output to bf16 as the reference kernel does.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from mantisnet import ops
+from oracle import encoder as E
+from oracle import model_ref as R
+
+pytestmark = pytest.mark.gpu
+BF = torch.bfloat16
+
+
+def _g(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def _runs(n_dest, max_run, seed, allow_empty=True):
+    gen = _g(seed)
+    lo = 0 if allow_empty else 1
+    counts = torch.randint(lo, max_run + 1, (n_dest,), generator=gen)
+    dest = torch.repeat_interleave(torch.arange(n_dest), counts)
+    return dest, counts
+
+
+@pytest.mark.parametrize("vdt,odt,h", [(BF, BF, 128), (BF, torch.float32, 128), (torch.float32, torch.float32, 512),
+                                       (torch.float32, torch.float32, 256), (torch.float32, torch.float32, 20)])
+def test_run_reduce_matches_index_add(device, vdt, odt, h):
+    gen = _g(1)
+    n_src, n_dest = 300, 200
+    dest, _ = _runs(n_dest, 18, 2)
+    gather = torch.randint(0, n_src, (dest.numel(),), generator=gen)
+    values = torch.randn(n_src, h, generator=gen).to(vdt)
+    ptr = ops.runs_to_ptr(dest.to(device), n_dest)
+    assert torch.equal(ptr.cpu(), torch.searchsorted(dest, torch.arange(n_dest + 1)))
+    out = ops.run_reduce(values.to(device), gather.to(device), ptr, n_dest, odt)
+    ops.raise_on_device_error(device)
+    exp = R.run_sum(values.float(), gather, dest, n_dest)
+    tol = 2e-2 if odt == BF else 1e-5
+    torch.testing.assert_close(out.float().cpu(), exp, rtol=tol, atol=tol)
+
+
+def test_out_of_range_index_is_flagged_not_read(device):
+    dest = torch.tensor([0, 0, 1, 2])
+    gather = torch.tensor([0, 5, 1, 2])  # 5 is out of range for 3 source rows
+    values = torch.ones(3, 128, device=device)
+    ptr = ops.runs_to_ptr(dest.to(device), 3)
+    out = ops.run_reduce(values, gather.to(device), ptr, 3, torch.float32)
+    assert out[0, 0].item() == 1.0  # the bad entry was skipped
+    with pytest.raises(ValueError, match="out of range"):
+        ops.raise_on_device_error(device)
+    ops.raise_on_device_error(device)  # the flag was cleared
+
+
+def test_unsorted_runs_are_flagged(device):
+    ops.runs_to_ptr(torch.tensor([0, 2, 1], device=device), 3)
+    with pytest.raises(ValueError, match="ascending"):
+        ops.raise_on_device_error(device)
+
+
+@pytest.mark.parametrize("with_vcls", [True, False])
+@pytest.mark.parametrize("dtype", [BF, torch.float32])
+def test_cell_attention_matches_dense_oracle(device, with_vcls, dtype):
+    gen = _g(3)
+    n_q, n_k, classes = 257, 90, 726
+    dest, counts = _runs(n_q, 18, 4)
+    src = torch.randint(0, n_k, (dest.numel(),), generator=gen)
+    cls = torch.randint(0, classes, (dest.numel(),), generator=gen)
+    q = torch.randn(n_q, 4, 32, generator=gen).to(dtype)
+    k = torch.randn(n_k, 4, 32, generator=gen).to(dtype)
+    v = torch.randn(n_k, 4, 32, generator=gen).to(dtype)
+    bias = 0.3 * torch.randn(4, classes, generator=gen)
+    vcls = 0.1 * torch.randn(classes, 128, generator=gen) if with_vcls else None
+    ptr = torch.searchsorted(dest, torch.arange(n_q + 1))
+    d = lambda x: None if x is None else x.to(device)  # noqa: E731
+    out, m, l = ops.cell_attention(d(q), d(k), d(v), d(bias), d(vcls), d(ptr), d(src), d(cls), stats=True)
+    ops.raise_on_device_error(device)
+    exp = R.cell_attention(q.float(), k.float(), v.float(), bias, vcls, src, cls, dest)
+    torch.testing.assert_close(out.cpu(), exp, rtol=1e-4, atol=1e-5)
+    empty = counts == 0
+    assert empty.any() and torch.all(out.cpu()[empty] == 0)
+    assert torch.all(l.cpu()[empty] == 0) and torch.all(l.cpu()[~empty] > 0)
+
+
+def test_latent_read_and_broadcast_match_literal_loops(device):
+    gen = _g(5)
+    p = 7
+    counts = torch.tensor([0, 3, 40, 1, 17, 0, 70])
+    n_w = int(counts.sum())
+    window_pos = torch.repeat_interleave(torch.arange(p), counts)
+    perm = torch.randperm(n_w, generator=gen)
+    window_pos = window_pos[perm]  # not position-major: the order view carries it
+    offsets, order = R.window_layout(window_pos, p)
+    q = torch.randn(p, 4, 4, 32, generator=gen).to(BF)
+    k = torch.randn(n_w, 4, 32, generator=gen).to(BF)
+    v = torch.randn(n_w, 4, 32, generator=gen).to(BF)
+    out = ops.latent_read(q.to(device), k.to(device), v.to(device), offsets.to(device), order.to(device))
+    exp = R.latent_read_loops(q.float(), k.float(), v.float(), offsets, order)
+    torch.testing.assert_close(out.cpu(), exp, rtol=1e-4, atol=1e-5)
+    assert torch.all(out.cpu()[0] == 0) and torch.all(out.cpu()[5] == 0)
+    qb = torch.randn(n_w, 4, 32, generator=gen).to(BF)
+    kb = torch.randn(p, 4, 4, 32, generator=gen).to(BF)
+    vb = torch.randn(p, 4, 4, 32, generator=gen).to(BF)
+    outb = ops.latent_broadcast(qb.to(device), kb.to(device), vb.to(device), window_pos.to(device))
+    ops.raise_on_device_error(device)
+    expb = R.latent_broadcast_loops(qb.float(), kb.float(), vb.float(), window_pos)
+    torch.testing.assert_close(outb.cpu(), expb, rtol=1e-4, atol=1e-5)
+
+
+def test_row_encode_matches_literal(device):
+    gen = _g(6)
+    n_cells, n_w = 300, 120
+    dest, _ = _runs(n_cells, 18, 7)
+    window = torch.randint(0, n_w, (dest.numel(),), generator=gen)
+    cls = torch.randint(0, 729, (dest.numel(),), generator=gen)
+    pre = torch.randn(n_w, 128, generator=gen).to(BF)
+    table = torch.randn(729, 128, generator=gen)
+    counts = torch.randint(0, 7, (n_cells, 3), generator=gen)
+    rows = torch.randn(3, 128, generator=gen).relu()
+    ptr = torch.searchsorted(dest, torch.arange(n_cells + 1))
+    out = ops.row_encode(pre.to(device), table.to(device), window.to(device), cls.to(device), ptr.to(device),
+                         n_cells, counts.to(device), rows.to(device))
+    ops.raise_on_device_error(device)
+    exp = R.encode_rows(pre.float(), table, window, cls, dest, n_cells)
+    exp = exp + (counts.float().unsqueeze(-1) * rows.unsqueeze(0)).sum(1)
+    torch.testing.assert_close(out.cpu(), exp, rtol=1e-5, atol=1e-4)
+
+
+@pytest.mark.parametrize("p,t,heads", [(1, 2, 4), (3, 31, 4), (64, 64, 4), (3, 65, 4), (5, 200, 4),
+                                       (2, 513, 8), (16, 124, 4)])
+def test_stone_attention_matches_masked_sdpa(device, p, t, heads):
+    gen = _g(p * 1000 + t)
+    # the model's layout: (P, T, A, hd) storage viewed as (P, A, T, hd)
+    q = torch.randn(p, t, heads, 32, generator=gen).to(BF).transpose(1, 2)
+    k = torch.randn(p, t, heads, 32, generator=gen).to(BF).transpose(1, 2)
+    v = torch.randn(p, t, heads, 32, generator=gen).to(BF).transpose(1, 2)
+    seq = torch.randint(1, t + 1, (p,), generator=gen, dtype=torch.int32)
+    seq[0] = t
+    out, lse = ops.stone_attention(q.to(device), k.to(device), v.to(device), seq.to(device), want_lse=True)
+    assert out.stride() == q.stride()
+    exp = R.stone_attention(q.float(), k.float(), v.float(), seq)
+    got = out.float().cpu()
+    # bf16 probabilities and bf16 output, as the reference kernel (attention.py:149-155)
+    torch.testing.assert_close(got, exp, rtol=2e-2, atol=2e-2)
+    valid = torch.arange(t)[None, :] < seq[:, None]
+    assert torch.all(got.transpose(1, 2)[~valid] == 0)  # padded query rows are exact zeros
+    sc = torch.matmul(q.float(), k.float().transpose(-1, -2)) / math.sqrt(32)
+    sc = sc.masked_fill(~valid[:, None, None, :], -torch.inf)
+    exp_lse = torch.logsumexp(sc, -1).masked_fill(~valid[:, None, :], 0.0)
+    torch.testing.assert_close(lse.cpu(), exp_lse, rtol=1e-3, atol=1e-3)
+
+
+def test_stone_attention_pad_keys_get_zero_weight(device):
+    # garbage (huge) values past seq_len must not leak into live rows
+    gen = _g(9)
+    q = torch.randn(2, 4, 70, 32, generator=gen).to(BF)
+    k = torch.randn(2, 4, 70, 32, generator=gen).to(BF)
+    v = torch.randn(2, 4, 70, 32, generator=gen).to(BF)
+    seq = torch.tensor([40, 70], dtype=torch.int32)
+    k2, v2 = k.clone(), v.clone()
+    k2[0, :, 40:] = 1e4
+    v2[0, :, 40:] = float("nan")
+    a = ops.stone_attention(q.to(device), k.to(device), v.to(device), seq.to(device)).cpu()
+    b = ops.stone_attention(q.to(device), k2.to(device), v2.to(device), seq.to(device)).cpu()
+    assert torch.equal(a, b)
+
+
+def _hex_graphs(n_graphs, seed=0):
+    from mantisnet import builder as B
+    from mantisnet import synthetic as S
+
+    games = S.random_games(3, n_graphs)
+    cells, sizes = [], []
+    for j, g in enumerate(games):
+        legal, _, _ = B.legal_moves(g)
+        n = int(np.random.default_rng([3, j, 1]).integers(64, 513))
+        cells.append(legal[:n])
+        sizes.append(min(n, len(legal)))
+    return games, cells, sizes
+
+
+def test_hex_neighbours_bit_exact_vs_reference_adjacency(device):
+    games, cells, sizes = _hex_graphs(6)
+    qr = torch.from_numpy(np.concatenate(cells).astype(np.int32))
+    gptr = torch.from_numpy(np.concatenate([[0], np.cumsum(sizes)]).astype(np.int64))
+    nbr = ops.hex_neighbours(qr.to(device), gptr.to(device)).cpu()
+    ops.raise_on_device_error(device)
+    slot = {(0, 1): 0, (0, -1): 1, (1, 1): 2, (1, -1): 3, (2, 1): 4, (2, -1): 5}
+    axes = [(1, 0), (0, 1), (1, -1)]
+    for j, g in enumerate(games):
+        pos = E.Replayed([tuple(map(int, m)) for m in g])
+        graph = E.build_position(pos)
+        n = sizes[j]
+        exp = np.full((n, 6), -1, np.int64)
+        for dst, src, ax in zip(graph["adjacency_dst"], graph["adjacency_src"], graph["adjacency_axis"]):
+            if dst < n and src < n:
+                d = pos.legal_qr[dst] - pos.legal_qr[src]
+                sign = 1 if tuple(d) == axes[ax] else -1
+                exp[src, slot[(int(ax), sign)]] = dst + gptr[j]
+        assert np.array_equal(nbr[gptr[j]:gptr[j + 1]].numpy(), exp)
+
+
+def test_hex_aggregate_linear_closed_form(device):
+    gen = _g(11)
+    n = 1000
+    nbr = torch.randint(-1, n, (n, 6), generator=gen, dtype=torch.int32)
+    nbr[:7] = -1  # isolated cells: mean is zero by convention
+    x = torch.randn(n, 128, generator=gen).to(BF)
+    w = (torch.randn(128, 128, generator=gen) / math.sqrt(128)).to(BF)
+    b = 0.1 * torch.randn(128, generator=gen)
+    s, m = ops.hex_aggregate_linear(x.to(device), nbr.to(device), w.to(device), b.to(device))
+    ops.raise_on_device_error(device)
+    present = nbr >= 0
+    gathered = x.float()[nbr.clamp(min=0).long()] * present[..., None]
+    agg_sum = gathered.sum(1)
+    cnt = present.sum(1, keepdim=True).float()
+    agg_mean = torch.where(cnt > 0, agg_sum / cnt.clamp(min=1), torch.zeros_like(agg_sum))
+    # the kernel rounds the fp32 aggregates to bf16 MFMA operands
+    es = agg_sum.to(BF).float() @ w.float().t() + b
+    em = agg_mean.to(BF).float() @ w.float().t() + b
+    torch.testing.assert_close(s.float().cpu(), es, rtol=1e-2, atol=2e-2)
+    torch.testing.assert_close(m.float().cpu(), em, rtol=1e-2, atol=1e-2)
+    assert torch.allclose(m.float().cpu()[:7], b.to(BF).float().expand(7, -1), atol=1e-2)

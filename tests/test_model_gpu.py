@@ -1,0 +1,101 @@
+"""The MI355X MantisNet forward against the CPU fp32 oracle (GPU).
+
+Production configuration (cell_nodes, 5,195,909 parameters) with the seeded
+perturbed init; tolerances: policy logits max-abs <= 1e-2 and per-position
+softmax KL <= 1e-4, value max-abs <= 2e-3, q_values/q_score max-abs <= 1e-2
+(oracle/compare.py).
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from mantisnet import PRODUCTION, MantisConfig, MantisNet, collate_positions, synthetic
+from mantisnet.klent.train import KlentConfig, network_evaluate
+from oracle.compare import compare_outputs, oracle_forward
+
+pytestmark = pytest.mark.gpu
+
+
+def _model(device, cfg=PRODUCTION, seed=0):
+    net = MantisNet(cfg)
+    net.load_state_dict(synthetic.perturbed_state_dict(net, seed=seed))
+    return net.to(device).eval()
+
+
+@pytest.mark.parametrize("config,count", [(1, 8), (4, 12)])
+def test_forward_matches_oracle(device, config, count):
+    net = _model(device)
+    batch = collate_positions(synthetic.random_games(config, count))
+    with torch.no_grad():
+        out = net(batch.to(device), 0.2)
+    from mantisnet import ops
+
+    ops.raise_on_device_error(device)
+    rep = compare_outputs(out, oracle_forward(net, batch, 0.2), batch.legal_offsets)
+    print(rep)
+    assert rep["ok"], rep
+    assert out.value_dist.dtype == torch.float32
+    assert torch.allclose(out.value_dist.sum(-1), torch.ones(batch.n_pos, device=device), atol=1e-5)
+
+
+def test_uncovered_scope_matches_oracle(device):
+    cfg = MantisConfig(cell_latents=True, cell_nodes=True, cell_node_scope="uncovered")
+    net = _model(device, cfg, seed=3)
+    batch = collate_positions(synthetic.random_games(1, 5, start=100))
+    with torch.no_grad():
+        out = net(batch.to(device), 0.2)
+    rep = compare_outputs(out, oracle_forward(net, batch, 0.2), batch.legal_offsets)
+    assert rep["ok"], rep
+
+
+def test_ply_zero_and_single_stone_positions(device):
+    net = _model(device)
+    games = [[], [(0, 0)], [(0, 0), (1, 0), (2, 0)]]
+    batch = collate_positions(games)
+    with torch.no_grad():
+        out = net(batch.to(device), 0.2)
+    rep = compare_outputs(out, oracle_forward(net, batch, 0.2), batch.legal_offsets)
+    assert rep["ok"], rep
+
+
+def test_fresh_init_logits_and_values_are_exactly_zero(device):
+    torch.manual_seed(0)
+    net = MantisNet(PRODUCTION).to(device).eval()
+    batch = collate_positions(synthetic.random_games(1, 3))
+    with torch.no_grad():
+        out = net(batch.to(device), 0.2)
+    assert torch.count_nonzero(out.policy_logits) == 0
+    assert torch.count_nonzero(out.q_values) == 0
+
+
+def test_batching_equivalence(device):
+    net = _model(device, seed=5)
+    games = synthetic.random_games(4, 3, start=7)
+    with torch.no_grad():
+        joint = net(collate_positions(games).to(device), 0.2)
+        parts = [net(collate_positions([g]).to(device), 0.2) for g in games]
+    pol = torch.cat([p.policy_logits for p in parts])
+    assert (joint.policy_logits - pol).abs().max().item() < 1e-2
+    assert (joint.value - torch.cat([p.value for p in parts])).abs().max().item() < 2e-3
+
+
+def test_network_evaluate_seam(device):
+    net = _model(device)
+    batch = collate_positions(synthetic.random_games(1, 3))
+    policy, q_score, q_values = network_evaluate(net, KlentConfig(device="cuda"))(batch)
+    assert policy.device.type == "cpu" and policy.dtype == torch.float32
+    ref = oracle_forward(net, batch, 0.2)
+    assert (policy - ref["policy_logits"]).abs().max() <= 1e-2
+    assert (q_values - ref["q_values"]).abs().max() <= 1e-2
+
+
+def test_pyo3_style_single_argument_call_raises_like_the_reference(device):
+    # mantisnet_python.rs:105-120 calls model(batch) with one argument; the
+    # reference forward has no mass_floor default (model.py:1185), so the
+    # call raises TypeError there and here alike.
+    net = _model(device)
+    batch = collate_positions(synthetic.random_games(1, 1)).to(device)
+    with pytest.raises(TypeError):
+        net(batch)
