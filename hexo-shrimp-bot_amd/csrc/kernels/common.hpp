@@ -32,6 +32,29 @@ __device__ __forceinline__ void load8(const uint16_t* p, float (&x)[8]) {
   }
 }
 
+// fp16 rows: one 16-byte load, widened exactly.
+__device__ __forceinline__ void load8(const _Float16* p, float (&x)[8]) {
+  typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+  const h8 u = *reinterpret_cast<const h8*>(p);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) x[i] = float(u[i]);
+}
+
+// fp32 -> fp16 rounding to nearest even, saturating at the largest finite
+// fp16 instead of overflowing to infinity.
+__device__ __forceinline__ _Float16 f2h(float f) {
+  f = fminf(fmaxf(f, -65504.f), 65504.f);
+  return _Float16(f);
+}
+
+__device__ __forceinline__ void store8(_Float16* p, const float (&x)[8]) {
+  typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+  h8 u;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) u[i] = f2h(x[i]);
+  *reinterpret_cast<h8*>(p) = u;
+}
+
 __device__ __forceinline__ void load8(const float* p, float (&x)[8]) {
   float4 a = reinterpret_cast<const float4*>(p)[0];
   float4 b = reinterpret_cast<const float4*>(p)[1];
@@ -52,6 +75,14 @@ __device__ __forceinline__ void store8(uint16_t* p, const float (&x)[8]) {
   u.w = uint32_t(f2bf(x[6])) | (uint32_t(f2bf(x[7])) << 16);
   *reinterpret_cast<uint4*>(p) = u;
 }
+
+// Scalar widening/narrowing for the element types the kernels take.
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(_Float16 x) { return float(x); }
+__device__ __forceinline__ float to_f32(uint16_t x) { return bf2f(x); }
+__device__ __forceinline__ void from_f32(float& d, float x) { d = x; }
+__device__ __forceinline__ void from_f32(_Float16& d, float x) { d = f2h(x); }
+__device__ __forceinline__ void from_f32(uint16_t& d, float x) { d = f2bf(x); }
 
 __device__ __forceinline__ void raise_flag(int32_t* flag, int32_t bit) {
   if (flag) atomicOr(flag, bit);

@@ -93,11 +93,9 @@ run_reduce_scalar_kernel(const Tin* __restrict__ values, int64_t n_src, int64_t 
         raise_flag(flag, MANTIS_FLAG_INDEX);
         continue;
       }
-      if constexpr (sizeof(Tin) == 2) acc += bf2f(values[s * ld + c]);
-      else acc += values[s * ld + c];
+      acc += to_f32(values[s * ld + c]);
     }
-    if constexpr (sizeof(Tout) == 2) out[row * h + c] = f2bf(acc);
-    else out[row * h + c] = acc;
+    from_f32(out[row * h + c], acc);
   }
 }
 
@@ -337,6 +335,18 @@ row_encode_kernel(const Tin* __restrict__ pre, int64_t n_w, const float* __restr
 
 inline unsigned grid_rows(int64_t rows) { return unsigned((rows + kGroupsPerBlock - 1) / kGroupsPerBlock); }
 
+// Calls fn(T{}) with T the element type named by a MANTIS_* dtype code;
+// returns false for an unknown code.
+template <typename F>
+bool with_type(int32_t dtype, F&& fn) {
+  switch (dtype) {
+    case MANTIS_F32: fn(float{}); return true;
+    case MANTIS_BF16: fn(uint16_t{}); return true;
+    case MANTIS_F16: fn(_Float16{}); return true;
+    default: return false;
+  }
+}
+
 }  // namespace
 }  // namespace mantis
 
@@ -361,27 +371,27 @@ int32_t mantis_run_reduce(const void* values, int32_t values_dtype, int64_t n_sr
                           int32_t* err_flag, void* stream) {
   if (n_dest == 0) return MANTIS_OK;
   if (!values || !ptr || !out || h <= 0 || ld < h || n_dest < 0 || n_src < 0) return MANTIS_E_ARG;
-  if ((values_dtype != MANTIS_F32 && values_dtype != MANTIS_BF16) ||
-      (out_dtype != MANTIS_F32 && out_dtype != MANTIS_BF16))
-    return MANTIS_E_ARG;
+  if (out_dtype < MANTIS_F32 || out_dtype > MANTIS_F16) return MANTIS_E_ARG;
   if (n_entries < 0 || (n_entries > 0 && !gather)) return MANTIS_E_ARG;
   const bool vec = h % 8 == 0 && ld % 8 == 0 && aligned16(values) && aligned16(out);
   hipStream_t s = as_stream(stream);
   const dim3 grid(grid_rows(n_dest)), block(kBlock);
-#define MANTIS_RR(TI, TO)                                                                       \
-  if (vec)                                                                                      \
-    run_reduce_kernel<TI, TO><<<grid, block, 0, s>>>(static_cast<const TI*>(values), n_src, ld, \
-                                                     h, gather, ptr, n_dest, n_entries,         \
-                                                     static_cast<TO*>(out), err_flag);          \
-  else                                                                                          \
-    run_reduce_scalar_kernel<TI, TO><<<grid, block, 0, s>>>(                                    \
-        static_cast<const TI*>(values), n_src, ld, h, gather, ptr, n_dest, n_entries,           \
-        static_cast<TO*>(out), err_flag);
-  if (values_dtype == MANTIS_BF16 && out_dtype == MANTIS_BF16) { MANTIS_RR(uint16_t, uint16_t) }
-  else if (values_dtype == MANTIS_BF16) { MANTIS_RR(uint16_t, float) }
-  else if (out_dtype == MANTIS_BF16) { MANTIS_RR(float, uint16_t) }
-  else { MANTIS_RR(float, float) }
-#undef MANTIS_RR
+  bool out_ok = false;
+  const bool in_ok = with_type(values_dtype, [&](auto ti) {
+    using TI = decltype(ti);
+    out_ok = with_type(out_dtype, [&](auto to) {
+      using TO = decltype(to);
+      if (vec)
+        run_reduce_kernel<TI, TO><<<grid, block, 0, s>>>(static_cast<const TI*>(values), n_src, ld,
+                                                         h, gather, ptr, n_dest, n_entries,
+                                                         static_cast<TO*>(out), err_flag);
+      else
+        run_reduce_scalar_kernel<TI, TO><<<grid, block, 0, s>>>(
+            static_cast<const TI*>(values), n_src, ld, h, gather, ptr, n_dest, n_entries,
+            static_cast<TO*>(out), err_flag);
+    });
+  });
+  if (!in_ok || !out_ok) return MANTIS_E_ARG;
   return launched();
 }
 
@@ -402,18 +412,18 @@ int32_t mantis_cell_attention(const void* q, const void* k, const void* v, int32
   const float scale = 1.0f / sqrtf(float(hd));
   hipStream_t s = as_stream(stream);
   const dim3 grid(grid_rows(n_q)), block(kBlock);
-#define MANTIS_CA(T, V)                                                                        \
-  cell_attention_kernel<T, V><<<grid, block, 0, s>>>(                                          \
-      static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v), bias,     \
-      n_classes, vcls, seg_ptr, src, cls, n_q, n_k, n_entries, scale, out, m, l, err_flag);
-  if (dtype == MANTIS_BF16) {
-    if (vcls) { MANTIS_CA(uint16_t, true) } else { MANTIS_CA(uint16_t, false) }
-  } else if (dtype == MANTIS_F32) {
-    if (vcls) { MANTIS_CA(float, true) } else { MANTIS_CA(float, false) }
-  } else {
-    return MANTIS_E_ARG;
-  }
-#undef MANTIS_CA
+  const bool ok = with_type(dtype, [&](auto t) {
+    using T = decltype(t);
+    if (vcls)
+      cell_attention_kernel<T, true><<<grid, block, 0, s>>>(
+          static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v), bias,
+          n_classes, vcls, seg_ptr, src, cls, n_q, n_k, n_entries, scale, out, m, l, err_flag);
+    else
+      cell_attention_kernel<T, false><<<grid, block, 0, s>>>(
+          static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v), bias,
+          n_classes, vcls, seg_ptr, src, cls, n_q, n_k, n_entries, scale, out, m, l, err_flag);
+  });
+  if (!ok) return MANTIS_E_ARG;
   return launched();
 }
 
@@ -426,16 +436,13 @@ int32_t mantis_latent_read(const void* q, const void* k, const void* v, int32_t 
   if (n_w > 0 && (!k || !v || !order)) return MANTIS_E_ARG;
   const float scale = 1.0f / sqrtf(float(hd));
   hipStream_t s = as_stream(stream);
-  if (dtype == MANTIS_BF16)
-    latent_read_kernel<uint16_t><<<unsigned(n_pos), kBlock, 0, s>>>(
-        static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
-        static_cast<const uint16_t*>(v), offsets, order, n_pos, n_w, scale, out, m, l, err_flag);
-  else if (dtype == MANTIS_F32)
-    latent_read_kernel<float><<<unsigned(n_pos), kBlock, 0, s>>>(
-        static_cast<const float*>(q), static_cast<const float*>(k), static_cast<const float*>(v),
-        offsets, order, n_pos, n_w, scale, out, m, l, err_flag);
-  else
-    return MANTIS_E_ARG;
+  const bool ok = with_type(dtype, [&](auto tv) {
+    using T = decltype(tv);
+    latent_read_kernel<T><<<unsigned(n_pos), kBlock, 0, s>>>(
+        static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v), offsets,
+        order, n_pos, n_w, scale, out, m, l, err_flag);
+  });
+  if (!ok) return MANTIS_E_ARG;
   return launched();
 }
 
@@ -449,16 +456,13 @@ int32_t mantis_latent_broadcast(const void* q, const void* k, const void* v, int
   const float scale = 1.0f / sqrtf(float(hd));
   hipStream_t s = as_stream(stream);
   const dim3 grid(grid_rows(n_w)), block(kBlock);
-  if (dtype == MANTIS_BF16)
-    latent_broadcast_kernel<uint16_t><<<grid, block, 0, s>>>(
-        static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
-        static_cast<const uint16_t*>(v), window_pos, n_pos, n_w, scale, out, m, l, err_flag);
-  else if (dtype == MANTIS_F32)
-    latent_broadcast_kernel<float><<<grid, block, 0, s>>>(
-        static_cast<const float*>(q), static_cast<const float*>(k), static_cast<const float*>(v),
-        window_pos, n_pos, n_w, scale, out, m, l, err_flag);
-  else
-    return MANTIS_E_ARG;
+  const bool ok = with_type(dtype, [&](auto tv) {
+    using T = decltype(tv);
+    latent_broadcast_kernel<T><<<grid, block, 0, s>>>(
+        static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v), window_pos,
+        n_pos, n_w, scale, out, m, l, err_flag);
+  });
+  if (!ok) return MANTIS_E_ARG;
   return launched();
 }
 
@@ -474,16 +478,13 @@ int32_t mantis_row_encode(const void* pre, int32_t pre_dtype, int64_t n_w, int64
   if (n_entries < 0 || (n_entries > 0 && (!window || !cls))) return MANTIS_E_ARG;
   hipStream_t s = as_stream(stream);
   const dim3 grid(grid_rows(n_cells)), block(kBlock);
-  if (pre_dtype == MANTIS_BF16)
-    row_encode_kernel<uint16_t><<<grid, block, 0, s>>>(
-        static_cast<const uint16_t*>(pre), n_w, table, n_classes, window, cls, cell_ptr, n_cells,
-        n_entries, empty_counts, empty_rows, out, err_flag);
-  else if (pre_dtype == MANTIS_F32)
-    row_encode_kernel<float><<<grid, block, 0, s>>>(
-        static_cast<const float*>(pre), n_w, table, n_classes, window, cls, cell_ptr, n_cells,
-        n_entries, empty_counts, empty_rows, out, err_flag);
-  else
-    return MANTIS_E_ARG;
+  const bool ok = with_type(pre_dtype, [&](auto tv) {
+    using T = decltype(tv);
+    row_encode_kernel<T><<<grid, block, 0, s>>>(static_cast<const T*>(pre), n_w, table, n_classes,
+                                                window, cls, cell_ptr, n_cells, n_entries,
+                                                empty_counts, empty_rows, out, err_flag);
+  });
+  if (!ok) return MANTIS_E_ARG;
   return launched();
 }
 

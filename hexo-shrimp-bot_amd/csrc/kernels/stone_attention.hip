@@ -1,4 +1,4 @@
-// Ragged block-diagonal attention on bf16 MFMA for gfx950
+// Ragged block-diagonal attention on 16-bit MFMA (bf16 or fp16) for gfx950
 // (replaces the reference's Triton flash kernel, attention.py:44-162).
 //
 // Work split: one workgroup = one (position, head, 64-query tile); its four
@@ -26,6 +26,7 @@ constexpr int kQTile = 64;
 constexpr int kKChunk = 64;
 constexpr int kVtPitch = kKChunk + 8;  // bf16 elements per transposed-V row
 
+template <bool kHalf>
 __global__ void __launch_bounds__(256)
 stone_attention_kernel(const uint16_t* __restrict__ q, int64_t qsp, int64_t qsa, int64_t qst,
                        const uint16_t* __restrict__ k, int64_t ksp, int64_t ksa, int64_t kst,
@@ -61,7 +62,8 @@ stone_attention_kernel(const uint16_t* __restrict__ q, int64_t qsp, int64_t qsa,
   const bool q_live = qrow < L;
   const uint4 zero4 = make_uint4(0, 0, 0, 0);
   // B fragment of Q^T: query l16, dims 8g..8g+7.
-  const bf16x8_t qf = as_bf16x8(q_live ? *reinterpret_cast<const uint4*>(qp + qrow * qst + 8 * g) : zero4);
+  using FR = Frag<kHalf>;
+  const typename FR::vec qf = FR::cast(q_live ? *reinterpret_cast<const uint4*>(qp + qrow * qst + 8 * g) : zero4);
 
   float m = -INFINITY, lpart = 0.f;
   f32x4_t o0 = {0.f, 0.f, 0.f, 0.f}, o1 = {0.f, 0.f, 0.f, 0.f};
@@ -88,7 +90,7 @@ stone_attention_kernel(const uint16_t* __restrict__ q, int64_t qsp, int64_t qsa,
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) {
       const int64_t krow = kb + 16 * tt + l16;  // A-fragment row of this lane
-      const bf16x8_t kf = as_bf16x8(krow < L ? *reinterpret_cast<const uint4*>(kp + krow * kst + 8 * g) : zero4);
+      const typename FR::vec kf = FR::cast(krow < L ? *reinterpret_cast<const uint4*>(kp + krow * kst + 8 * g) : zero4);
       const f32x4_t d = mfma16x16x32(kf, qf, f32x4_t{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
@@ -116,20 +118,20 @@ stone_attention_kernel(const uint16_t* __restrict__ q, int64_t qsp, int64_t qsa,
         pr[t] = exp2f(s[tt][t] - m_new);
         lpart += pr[t];
       }
-      pw[tt][0] = pack_bf16x2(pr[0], pr[1]);
-      pw[tt][1] = pack_bf16x2(pr[2], pr[3]);
+      pw[tt][0] = FR::pack(pr[0], pr[1]);
+      pw[tt][1] = FR::pack(pr[2], pr[3]);
     }
     m = m_new;
     // O^T += V^T . P^T over two 32-key steps.
 #pragma unroll
     for (int sc = 0; sc < 2; ++sc) {
-      const bf16x8_t pf = as_bf16x8(make_uint4(pw[2 * sc][0], pw[2 * sc][1], pw[2 * sc + 1][0], pw[2 * sc + 1][1]));
+      const typename FR::vec pf = FR::cast(make_uint4(pw[2 * sc][0], pw[2 * sc][1], pw[2 * sc + 1][0], pw[2 * sc + 1][1]));
 #pragma unroll
       for (int dt = 0; dt < 2; ++dt) {
         const uint16_t* row = &vt[16 * dt + l16][32 * sc];
         const uint2 lo = *reinterpret_cast<const uint2*>(row + 4 * g);
         const uint2 hi = *reinterpret_cast<const uint2*>(row + 16 + 4 * g);
-        const bf16x8_t vf = as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
+        const typename FR::vec vf = FR::cast(make_uint4(lo.x, lo.y, hi.x, hi.y));
         if (dt == 0) o0 = mfma16x16x32(vf, pf, o0);
         else o1 = mfma16x16x32(vf, pf, o1);
       }
@@ -141,10 +143,10 @@ stone_attention_kernel(const uint16_t* __restrict__ q, int64_t qsp, int64_t qsa,
   if (qrow < T) {
     const float inv = (q_live && l > 0.f) ? 1.f / l : 0.f;
     uint2 w0, w1;
-    w0.x = pack_bf16x2(o0[0] * inv, o0[1] * inv);
-    w0.y = pack_bf16x2(o0[2] * inv, o0[3] * inv);
-    w1.x = pack_bf16x2(o1[0] * inv, o1[1] * inv);
-    w1.y = pack_bf16x2(o1[2] * inv, o1[3] * inv);
+    w0.x = FR::pack(o0[0] * inv, o0[1] * inv);
+    w0.y = FR::pack(o0[2] * inv, o0[3] * inv);
+    w1.x = FR::pack(o1[0] * inv, o1[1] * inv);
+    w1.y = FR::pack(o1[2] * inv, o1[3] * inv);
     *reinterpret_cast<uint2*>(op + qrow * ost + 4 * g) = w0;
     *reinterpret_cast<uint2*>(op + qrow * ost + 16 + 4 * g) = w1;
     if (lp && g == 0) lp[qrow] = q_live ? (m + log2f(l)) * 0.6931471805599453f : 0.f;
@@ -158,12 +160,13 @@ using namespace mantis;
 
 extern "C" int32_t mantis_stone_attention(const void* q, const int64_t* qs, const void* k,
                                           const int64_t* ks, const void* v, const int64_t* vs,
-                                          const int32_t* seq_lens, int64_t n_pos, int32_t heads,
-                                          int64_t t, int32_t hd, void* out, const int64_t* os,
-                                          float* lse, void* stream) {
+                                          int32_t dtype, const int32_t* seq_lens, int64_t n_pos,
+                                          int32_t heads, int64_t t, int32_t hd, void* out,
+                                          const int64_t* os, float* lse, void* stream) {
   if (n_pos == 0 || t == 0) return MANTIS_OK;
   if (!q || !k || !v || !out || !seq_lens || !qs || !ks || !vs || !os) return MANTIS_E_ARG;
   if (hd != kHd || heads <= 0 || n_pos < 0 || t < 0) return MANTIS_E_ARG;
+  if (dtype != MANTIS_BF16 && dtype != MANTIS_F16) return MANTIS_E_ARG;
   // The innermost (dim) stride must be 1 and every row start 16-byte aligned.
   for (const int64_t* st : {qs, ks, vs, os}) {
     if (st[3] != 1) return MANTIS_E_ARG;
@@ -173,7 +176,8 @@ extern "C" int32_t mantis_stone_attention(const void* q, const int64_t* qs, cons
   if (n_pos * heads > 2147483647LL) return MANTIS_E_ARG;
   const float scale_log2 = 1.4426950408889634f / sqrtf(float(hd));
   const dim3 grid(unsigned((t + kQTile - 1) / kQTile), unsigned(n_pos * heads));
-  stone_attention_kernel<<<grid, 256, 0, as_stream(stream)>>>(
+  auto kernel = dtype == MANTIS_F16 ? stone_attention_kernel<true> : stone_attention_kernel<false>;
+  kernel<<<grid, 256, 0, as_stream(stream)>>>(
       static_cast<const uint16_t*>(q), qs[0], qs[1], qs[2], static_cast<const uint16_t*>(k), ks[0],
       ks[1], ks[2], static_cast<const uint16_t*>(v), vs[0], vs[1], vs[2], seq_lens, heads, t,
       static_cast<uint16_t*>(out), os[0], os[1], os[2], lse, scale_log2);

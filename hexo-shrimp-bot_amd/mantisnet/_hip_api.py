@@ -18,7 +18,7 @@ SIGNATURES = {
     "mantis_latent_read": ([vp, vp, vp, i32, vp, vp, i64, i64, i32, i32, vp, vp, vp, vp, vp], i32),
     "mantis_latent_broadcast": ([vp, vp, vp, i32, vp, i64, i64, i32, i32, vp, vp, vp, vp, vp], i32),
     "mantis_row_encode": ([vp, i32, i64, i64, vp, i64, vp, vp, i64, vp, i64, vp, vp, vp, vp, vp], i32),
-    "mantis_stone_attention": ([vp, vp, vp, vp, vp, vp, vp, i64, i32, i64, i32, vp, vp, vp, vp], i32),
+    "mantis_stone_attention": ([vp, vp, vp, vp, vp, vp, i32, vp, i64, i32, i64, i32, vp, vp, vp, vp], i32),
     "mantis_hex_neighbours": ([vp, vp, i64, i64, vp, vp, vp], i32),
     "mantis_hex_aggregate_linear": ([vp, vp, i64, vp, vp, vp, vp, vp, vp], i32),
 }

@@ -33,6 +33,7 @@ from . import ops
 from .builder import Batch
 
 BF16 = torch.bfloat16
+HALF = torch.float16  # the MFMA operand type of every projection and attention
 GLOBAL_ROWS = 4
 ORBIT48 = 48
 
@@ -54,7 +55,7 @@ def _supported(model) -> None:
 
 
 class _Weights:
-    """bf16 copies of every matrix a GEMM reads, rebuilt when a parameter
+    """fp16 copies of every matrix a GEMM reads, rebuilt when a parameter
     changes (tracked through the tensors' version counters)."""
 
     def __init__(self, model):
@@ -67,7 +68,7 @@ class _Weights:
         key = tuple((n, p.data_ptr(), p._version) for n, p in params.items())
         if key == self.key:
             return
-        self.bf = {n: p.detach().to(BF16).contiguous() for n, p in params.items() if n.endswith(".weight") and p.ndim == 2}
+        self.bf = {n: p.detach().to(HALF).contiguous() for n, p in params.items() if n.endswith(".weight") and p.ndim == 2}
         self.key = key
 
 
@@ -87,15 +88,15 @@ class _Ctx:
         self.p = dict(model.named_parameters())
 
     def lin(self, x: Tensor, name: str, out_fp32: bool = False) -> Tensor:
-        """y = x W^T + b: bf16 operands, fp32 accumulation; bf16 result unless
+        """y = x W^T + b: fp16 operands, fp32 accumulation; fp16 result unless
         ``out_fp32`` (then the product and bias stay fp32)."""
         w = self.W.bf[name + ".weight"]
         b = self.p.get(name + ".bias")
         if out_fp32:
-            x2 = x.reshape(-1, x.shape[-1]).to(BF16)
+            x2 = x.reshape(-1, x.shape[-1]).to(HALF)
             y = _mm_fp32(x2, w).view(*x.shape[:-1], w.shape[0])
             return y + b if b is not None else y
-        return F.linear(x.to(BF16), w, None if b is None else b.to(BF16))
+        return F.linear(_half(x), w, None if b is None else b.to(HALF))
 
     def ln(self, x: Tensor, name: str) -> Tensor:
         return F.layer_norm(x.float(), (x.shape[-1],), self.p[name + ".weight"], self.p[name + ".bias"], 1e-5)
@@ -104,11 +105,18 @@ class _Ctx:
         return self.lin(F.relu(self.lin(a, name + ".lin_a") + self.lin(b, name + ".lin_b")), name + ".out")
 
 
+def _half(x: Tensor) -> Tensor:
+    """fp32 -> fp16 with saturation at +-65504 (no overflow to inf)."""
+    if x.dtype == HALF:
+        return x
+    return x.clamp(-65504.0, 65504.0).to(HALF)
+
+
 _MM_OUT_DTYPE: bool | None = None
 
 
 def _mm_fp32(x: Tensor, w: Tensor) -> Tensor:
-    """x @ w^T with bf16 operands and an fp32 result (no bf16 rounding of the
+    """x @ w^T with 16-bit operands and an fp32 result (no rounding of the
     product).  Uses the device GEMM's fp32 output when torch exposes it, else
     an fp32 GEMM over the same bf16-valued operands."""
     global _MM_OUT_DTYPE
@@ -264,8 +272,8 @@ def _block(C: _Ctx, i: int, plan: Plan, b: Batch, s, w, g, c, ws_rows, sw_rows, 
     p, max_t = plan.n_pos, plan.max_t
     # §5.1 windows <- stones
     x = C.lin(C.ln(s, pre + "ln_ws_s"), pre + "u")
-    agg = ops.run_reduce(x, b.inc_stone, plan.inc_win_ptr, plan.n_w, BF16)
-    agg = agg + ws_rows.to(BF16)
+    agg = ops.run_reduce(x, b.inc_stone, plan.inc_win_ptr, plan.n_w, torch.float32)
+    agg = agg + ws_rows
     w = w + C.pair_mlp(C.ln(w, pre + "ln_ws_w"), agg, pre + "mlp_w")
     # §5.1b cell stage
     w, c = _cell_stage(C, pre, plan, s, w, c)
@@ -379,12 +387,12 @@ def cell_head_logits(model, w: Tensor, g: Tensor, cells: Tensor, b: Batch):
                           b.act_empty, empty_rows)
     extra = ops.run_reduce(torch.cat((C.p["e_pw.weight"], C.p["e_qw.weight"]), 1), b.dec_class,
                            plan.dec_cell_ptr, n_c, torch.float32)
-    rows = cells.to(BF16)
-    acts_bf = acts.to(BF16)
+    rows = _half(cells)
+    acts_bf = _half(acts)
     outs = []
     for proj, ext, mlp, sl in (("p", "p_act", "mlp_p", slice(0, 128)), ("q", "q_act", "mlp_q", slice(128, 256))):
         g_half = C.lin(g, mlp + ".lin_b", True)
-        base = C.lin(rows, proj) + C.lin(acts_bf, ext) + extra[:, sl].to(BF16)
+        base = C.lin(rows, proj, True) + C.lin(acts_bf, ext, True) + extra[:, sl]
         pre = C.lin(base, mlp + ".lin_a", True)
         hid = F.relu(pre + g_half.index_select(0, b.cell_pos))
         outs.append(C.lin(hid, mlp + ".out", True))

@@ -17,7 +17,7 @@ from torch import Tensor
 
 from . import _native
 
-F32, BF16 = 0, 1
+F32, BF16, F16 = 0, 1, 2
 _FLAG_NAMES = {1: "an index was out of range", 2: "a CSR/run view was not ascending"}
 _flags: dict[int, Tensor] = {}
 
@@ -29,9 +29,11 @@ def _lib():
 def _dt(t: Tensor) -> int:
     if t.dtype == torch.bfloat16:
         return BF16
+    if t.dtype == torch.float16:
+        return F16
     if t.dtype == torch.float32:
         return F32
-    raise ValueError(f"unsupported dtype {t.dtype}; expected bfloat16 or float32")
+    raise ValueError(f"unsupported dtype {t.dtype}; expected float16, bfloat16 or float32")
 
 
 def _stream() -> int:
@@ -256,17 +258,17 @@ def _strides(t: Tensor):
 
 
 def stone_attention(q: Tensor, k: Tensor, v: Tensor, seq_lens: Tensor, want_lse: bool = False):
-    """Ragged attention over each position's live prefix (bf16 MFMA).
-    q/k/v (P, A, T, hd) bf16 with arbitrary row strides; the output has
-    ``empty_like(q)`` strides."""
+    """Ragged attention over each position's live prefix (16-bit MFMA).
+    q/k/v (P, A, T, hd) fp16 or bf16 with arbitrary row strides; the output
+    has ``empty_like(q)`` strides."""
     dev = _on_gpu(q, k, v, seq_lens)
     if q.ndim != 4 or q.shape != k.shape or q.shape != v.shape:
         raise ValueError("q, k, and v must have the same (P, A, T, D) shape")
     p, heads, t, hd = q.shape
     if seq_lens.shape != (p,) or seq_lens.dtype != torch.int32:
         raise ValueError("seq_lens must be int32 with shape (P,)")
-    if q.dtype != torch.bfloat16 or k.dtype != q.dtype or v.dtype != q.dtype:
-        raise ValueError("stone attention runs bf16 MFMA: q, k and v must be bfloat16")
+    if q.dtype not in (torch.float16, torch.bfloat16) or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("stone attention runs 16-bit MFMA: q, k and v must share float16 or bfloat16")
     if hd != 32:
         raise ValueError("stone attention supports head_dim 32")
     fix = lambda x: x if x.stride(3) == 1 and all(s % 8 == 0 for s in x.stride()[:3]) else x.contiguous()  # noqa: E731
@@ -279,7 +281,7 @@ def stone_attention(q: Tensor, k: Tensor, v: Tensor, seq_lens: Tensor, want_lse:
     qs, ks, vs, os_ = _strides(q), _strides(k), _strides(v), _strides(out)
     _check(
         _lib().mantis_stone_attention(
-            _ptr(q), qs, _ptr(k), ks, _ptr(v), vs, _ptr(seq_lens), p, heads, t, hd, _ptr(out), os_,
+            _ptr(q), qs, _ptr(k), ks, _ptr(v), vs, _dt(q), _ptr(seq_lens), p, heads, t, hd, _ptr(out), os_,
             _ptr(lse), _stream(),
         ),
         "stone_attention",

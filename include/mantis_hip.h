@@ -6,7 +6,8 @@
  *  - plain device pointers, element counts and a hipStream_t passed as void*
  *    (NULL = the default stream); work is enqueued on that stream only;
  *  - tensors are dense row-major; index and CSR-pointer arrays are int64;
- *  - `dtype` arguments take MANTIS_F32 or MANTIS_BF16;
+ *  - `dtype` arguments take MANTIS_F32, MANTIS_BF16 or MANTIS_F16 (fp16
+ *    narrowing rounds to nearest even and saturates at +-65504);
  *  - CSR pointer arrays are clamped into [0, n_entries] on the device, so a
  *    corrupted pointer can only shorten a run, never leave the entry arrays;
  *  - every index is bounds-checked on the device: an out-of-range index is
@@ -27,6 +28,7 @@ extern "C" {
 
 #define MANTIS_F32 0
 #define MANTIS_BF16 1
+#define MANTIS_F16 2
 
 #define MANTIS_OK 0
 #define MANTIS_E_ARG 1    /* unsupported shape, dtype or null pointer */
@@ -119,11 +121,12 @@ int32_t mantis_row_encode(const void* pre, int32_t pre_dtype, int64_t n_w, int64
                           int32_t* err_flag, void* stream);
 
 /*
- * Ragged block-diagonal attention over each position's live prefix, bf16
- * MFMA (gfx950 v_mfma_f32_16x16x32_bf16) with fp32 online softmax:
+ * Ragged block-diagonal attention over each position's live prefix on 16-bit
+ * MFMA (gfx950 v_mfma_f32_16x16x32_{bf16,f16}; `dtype` MANTIS_BF16 or
+ * MANTIS_F16) with fp32 online softmax:
  *   out[p, a, t, :] = softmax_{s < seq_lens[p]}(q[p,a,t,:] . k[p,a,s,:] / sqrt(hd)) v[p,a,s,:]
  * for t < seq_lens[p]; rows t >= seq_lens[p] are written as exact zeros
- * (lse 0).  q/k/v/out are bf16 with element strides (sp, sa, st, sd == 1)
+ * (lse 0).  q/k/v/out share `dtype`, with element strides (sp, sa, st, sd == 1)
  * given per tensor, so the (P, T, A, hd) -> (P, A, T, hd) transposed views
  * the model passes need no copy.  lse (P, heads, T) fp32 or NULL.
  * hd must be 32.  Replaces mantisnet::fused_attention
@@ -131,9 +134,9 @@ int32_t mantis_row_encode(const void* pre, int32_t pre_dtype, int64_t n_w, int64
  */
 int32_t mantis_stone_attention(const void* q, const int64_t* q_strides, const void* k,
                                const int64_t* k_strides, const void* v, const int64_t* v_strides,
-                               const int32_t* seq_lens, int64_t n_pos, int32_t heads, int64_t t,
-                               int32_t hd, void* out, const int64_t* out_strides, float* lse,
-                               void* stream);
+                               int32_t dtype, const int32_t* seq_lens, int64_t n_pos,
+                               int32_t heads, int64_t t, int32_t hd, void* out,
+                               const int64_t* out_strides, float* lse, void* stream);
 
 /*
  * Six-neighbour table of ragged cell graphs: graph j's cells are
