@@ -1,0 +1,359 @@
+// Fused row GEMM for gfx950: the LayerNorm -> Linear (-> ReLU -> Linear)
+// -> residual epilogues of the MantisNet blocks and heads in one pass over
+// the rows (replaces the reference's LayerNorm/Linear/elementwise chains,
+// model.py:246-260, 570-580, 608-619, 681-691, and the projections around
+// every attention op).
+//
+// For a tile of 16 rows per wavefront, with K = 128 input features:
+//   x-hat  = normalise(x)          (optional; the LayerNorm affine is folded
+//                                   into W1/b1 by the caller)
+//   h      = x-hat W1^T [+ x2 W2^T] + b1 [+ add1[row]] [+ add2[row_grp]] (N1 wide)
+//   h      = relu(h)               (optional)
+//   y      = h W3^T + b3           (optional second stage, 128 wide)
+//   out    = y (fp16 or fp32 store) or out += y (fp32 residual, in place)
+// Products run as v_mfma_f32_16x16x32_f16 in the transposed form
+// y^T = W . x^T: a lane owns one row and holds four consecutive output
+// features of each 16-wide tile, so the LayerNorm statistics are a 4-lane
+// reduction, every store is a 8/16-byte row chunk, and the stage-1 D
+// fragments are already the B fragments of stage 2 (K slots
+// {4g..4g+3, 16+4g..16+4g+3} of each 32-step, matched by the W3 reads).
+// The weights live in LDS for the whole (persistent) workgroup; rows stream
+// from HBM once.
+#include "common.hpp"
+#include "mfma.hpp"
+
+#include <algorithm>
+
+namespace mantis {
+namespace {
+
+constexpr int kK = 128;
+constexpr int kPitch = kK + 8;  // fp16 elements per LDS weight row (W1/W2)
+constexpr int kMaxLds = 160 * 1024;  // LDS per CU on gfx950
+
+enum OutMode { kStoreF16 = 0, kStoreF32 = 1, kAddF32 = 2 };
+
+struct Args {
+  const void* x;
+  int64_t ldx;
+  const int64_t* x_rows;
+  int64_t n_x;
+  int64_t m;
+  const void* x2;
+  int64_t ldx2;
+  const _Float16* w1;
+  const _Float16* w2;
+  const float* b1;
+  const float* add1;  // (m, n1) fp32 added before the activation, or null
+  int64_t ld_add1;
+  const float* add2;  // (n_grp, n1) fp32 added per row group, or null
+  const int64_t* add2_rows;  // (m,) group of each row
+  int64_t n_add2;
+  const _Float16* w3;
+  const float* b3;
+  int32_t n3;
+  void* out;
+  int64_t ldo;
+  int32_t* flag;
+};
+
+template <typename T>
+__device__ __forceinline__ void load_chunk(const T* p, float (&v)[8]) { load8(p, v); }
+
+// Four consecutive output features of one row: fp16/fp32 store or fp32 add.
+template <int kMode>
+__device__ __forceinline__ void store4(const Args& a, int64_t row, int f, const f32x4_t& v) {
+  if constexpr (kMode == kStoreF16) {
+    uint2 w;
+    w.x = pack_f16x2(v[0], v[1]);
+    w.y = pack_f16x2(v[2], v[3]);
+    *reinterpret_cast<uint2*>(static_cast<_Float16*>(a.out) + row * a.ldo + f) = w;
+  } else if constexpr (kMode == kStoreF32) {
+    *reinterpret_cast<float4*>(static_cast<float*>(a.out) + row * a.ldo + f) = make_float4(v[0], v[1], v[2], v[3]);
+  } else {
+    float4* o = reinterpret_cast<float4*>(static_cast<float*>(a.out) + row * a.ldo + f);
+    float4 r = *o;
+    r.x += v[0], r.y += v[1], r.z += v[2], r.w += v[3];
+    *o = r;
+  }
+}
+
+// LDS layout: W1 (N1 rows), W2 (N1 rows, with a second input), W3 (n3 rows
+// of N1 + 8, with a second stage); n3 is a launch parameter.
+template <int N1, bool kStage2, bool kX2>
+struct Smem {
+  static constexpr int w1 = N1 * kPitch;
+  static constexpr int w2 = kX2 ? N1 * kPitch : 0;
+  static constexpr int p3 = N1 + 8;
+  static int bytes(int n3) { return (w1 + w2 + (kStage2 ? n3 * p3 : 0)) * 2; }
+};
+
+template <typename TX, typename TX2, bool kLN, int N1, bool kX2, bool kRelu, bool kStage2, int kMode>
+__global__ void __launch_bounds__(256) fused_linear_kernel(Args a) {
+  extern __shared__ __attribute__((aligned(16))) _Float16 smem[];
+  using S = Smem<N1, kStage2, kX2>;
+  _Float16* sw1 = smem;
+  _Float16* sw2 = smem + S::w1;
+  _Float16* sw3 = smem + S::w1 + S::w2;
+  constexpr int NT1 = N1 / 16;
+
+  // Stage the weights (16-byte chunks).
+  for (int i = threadIdx.x; i < N1 * (kK / 8); i += blockDim.x) {
+    const int r = i / (kK / 8), c = (i % (kK / 8)) * 8;
+    *reinterpret_cast<uint4*>(sw1 + r * kPitch + c) = *reinterpret_cast<const uint4*>(a.w1 + r * kK + c);
+    if constexpr (kX2)
+      *reinterpret_cast<uint4*>(sw2 + r * kPitch + c) = *reinterpret_cast<const uint4*>(a.w2 + r * kK + c);
+  }
+  if constexpr (kStage2) {
+    for (int i = threadIdx.x; i < a.n3 * (N1 / 8); i += blockDim.x) {
+      const int r = i / (N1 / 8), c = (i % (N1 / 8)) * 8;
+      *reinterpret_cast<uint4*>(sw3 + r * S::p3 + c) = *reinterpret_cast<const uint4*>(a.w3 + r * N1 + c);
+    }
+  }
+  __syncthreads();
+
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+  const int l16 = lane % 16, g = lane / 16;
+  const int64_t n_tiles = (a.m + 63) / 64;
+  const TX* xp = static_cast<const TX*>(a.x);
+
+  for (int64_t tile = blockIdx.x; tile < n_tiles; tile += gridDim.x) {
+    const int64_t row = tile * 64 + wave * 16 + l16;
+    const bool live = row < a.m;
+    // ---- prologue: this lane's 32 features of its row (4 chunks of 8)
+    int64_t src = row;
+    if (live && a.x_rows) {
+      src = a.x_rows[row];
+      if (src >= a.n_x) {
+        raise_flag(a.flag, MANTIS_FLAG_INDEX);
+        src = -1;
+      }
+    }
+    float xv[4][8];
+    const bool have = live && src >= 0;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      if (have) load_chunk(xp + src * a.ldx + 32 * ks + 8 * g, xv[ks]);
+      else
+#pragma unroll
+        for (int t = 0; t < 8; ++t) xv[ks][t] = 0.f;
+    }
+    if constexpr (kLN) {
+      float s = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) s += xv[ks][t];
+      s += __shfl_xor(s, 16);
+      s += __shfl_xor(s, 32);
+      const float mean = s * (1.f / kK);
+      float q = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          const float d = xv[ks][t] - mean;
+          q += d * d;
+        }
+      q += __shfl_xor(q, 16);
+      q += __shfl_xor(q, 32);
+      const float rstd = rsqrtf(q * (1.f / kK) + 1e-5f);
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) xv[ks][t] = (xv[ks][t] - mean) * rstd;
+    }
+    f16x8_t xb[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int t = 0; t < 8; ++t) xb[ks][t] = f2h(xv[ks][t]);
+    f16x8_t x2b[4];
+    if constexpr (kX2) {
+      const TX2* x2p = static_cast<const TX2*>(a.x2);
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        float v2[8];
+        if (live) load_chunk(x2p + row * a.ldx2 + 32 * ks + 8 * g, v2);
+        else
+#pragma unroll
+          for (int t = 0; t < 8; ++t) v2[t] = 0.f;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) x2b[ks][t] = f2h(v2[t]);
+      }
+    }
+    // ---- stage 1: h^T (N1 x 16 rows) = W1 . x-hat^T (+ W2 . x2^T)
+    f32x4_t acc[NT1];
+#pragma unroll
+    for (int nt = 0; nt < NT1; ++nt) {
+      acc[nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const f16x8_t wf = *reinterpret_cast<const f16x8_t*>(sw1 + (16 * nt + l16) * kPitch + 32 * ks + 8 * g);
+        acc[nt] = mfma16x16x32(wf, xb[ks], acc[nt]);
+        if constexpr (kX2) {
+          const f16x8_t wf2 = *reinterpret_cast<const f16x8_t*>(sw2 + (16 * nt + l16) * kPitch + 32 * ks + 8 * g);
+          acc[nt] = mfma16x16x32(wf2, x2b[ks], acc[nt]);
+        }
+      }
+    }
+    // ---- epilogue 1: bias, row adds, activation (features 16nt + 4g + t)
+    int64_t grp = -1;
+    if (live && a.add2) {
+      grp = a.add2_rows[row];
+      if (grp < 0 || grp >= a.n_add2) {
+        raise_flag(a.flag, MANTIS_FLAG_INDEX);
+        grp = -1;
+      }
+    }
+#pragma unroll
+    for (int nt = 0; nt < NT1; ++nt) {
+      const int f = 16 * nt + 4 * g;
+      float4 add = a.b1 ? *reinterpret_cast<const float4*>(a.b1 + f) : make_float4(0.f, 0.f, 0.f, 0.f);
+      if (live && a.add1) {
+        const float4 r = *reinterpret_cast<const float4*>(a.add1 + row * a.ld_add1 + f);
+        add.x += r.x, add.y += r.y, add.z += r.z, add.w += r.w;
+      }
+      if (grp >= 0) {
+        const float4 r = *reinterpret_cast<const float4*>(a.add2 + grp * N1 + f);
+        add.x += r.x, add.y += r.y, add.z += r.z, add.w += r.w;
+      }
+      acc[nt][0] += add.x, acc[nt][1] += add.y, acc[nt][2] += add.z, acc[nt][3] += add.w;
+      if constexpr (kRelu)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[nt][t] = fmaxf(acc[nt][t], 0.f);
+    }
+    if constexpr (!kStage2) {
+      if (live) {
+#pragma unroll
+        for (int nt = 0; nt < NT1; ++nt) store4<kMode>(a, row, 16 * nt + 4 * g, acc[nt]);
+      }
+    } else {
+      // ---- stage 2: y^T (n3 x 16) = W3 . h^T, h^T fed straight from acc
+      f16x8_t hb[N1 / 32];
+#pragma unroll
+      for (int ks = 0; ks < N1 / 32; ++ks)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          hb[ks][t] = f2h(acc[2 * ks][t]);
+          hb[ks][4 + t] = f2h(acc[2 * ks + 1][t]);
+        }
+      const int NT3 = a.n3 / 16;
+      for (int ot = 0; ot < NT3; ++ot) {
+        f32x4_t y = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < N1 / 32; ++ks) {
+          const _Float16* wr = sw3 + (16 * ot + l16) * S::p3 + 32 * ks;
+          const uint2 lo = *reinterpret_cast<const uint2*>(wr + 4 * g);
+          const uint2 hi = *reinterpret_cast<const uint2*>(wr + 16 + 4 * g);
+          const f16x8_t wf = __builtin_bit_cast(f16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
+          y = mfma16x16x32(wf, hb[ks], y);
+        }
+        if (live) {
+          const int f = 16 * ot + 4 * g;
+          const float4 bb = a.b3 ? *reinterpret_cast<const float4*>(a.b3 + f) : make_float4(0.f, 0.f, 0.f, 0.f);
+          y[0] += bb.x, y[1] += bb.y, y[2] += bb.z, y[3] += bb.w;
+          store4<kMode>(a, row, f, y);
+        }
+      }
+    }
+  }
+}
+
+int g_cus = 0;
+
+int cu_count() {
+  if (!g_cus) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&g_cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || g_cus <= 0)
+      g_cus = 256;
+  }
+  return g_cus;
+}
+
+template <typename TX, typename TX2, bool kLN, int N1, bool kX2, bool kRelu, bool kStage2, int kMode>
+int32_t launch(const Args& a, hipStream_t stream) {
+  using S = Smem<N1, kStage2, kX2>;
+  auto kernel = fused_linear_kernel<TX, TX2, kLN, N1, kX2, kRelu, kStage2, kMode>;
+  const int bytes = S::bytes(a.n3);
+  if (bytes > kMaxLds) return MANTIS_E_ARG;
+  static bool configured = false;
+  if (!configured) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            kMaxLds) != hipSuccess)
+      return MANTIS_E_LAUNCH;
+    configured = true;
+  }
+  const int64_t tiles = (a.m + 63) / 64;
+  const int per_cu = std::max(1, std::min(4, kMaxLds / std::max(bytes, 1)));
+  const int64_t grid = std::min<int64_t>(tiles, int64_t(cu_count()) * per_cu);
+  kernel<<<unsigned(grid), 256, bytes, stream>>>(a);
+  return launched();
+}
+
+}  // namespace
+}  // namespace mantis
+
+using namespace mantis;
+
+extern "C" int32_t mantis_fused_linear(const void* x, int32_t x_dtype, int64_t ldx,
+                                       const int64_t* x_rows, int64_t n_x, int64_t m,
+                                       int32_t layer_norm, const void* x2, int32_t x2_dtype,
+                                       int64_t ldx2, const void* w1, const void* w2,
+                                       const float* b1, int32_t n1, const float* add1,
+                                       int64_t ld_add1, const float* add2,
+                                       const int64_t* add2_rows, int64_t n_add2, int32_t relu,
+                                       const void* w3, const float* b3, int32_t n3,
+                                       int32_t out_mode, void* out, int64_t ldo,
+                                       int32_t* err_flag, void* stream) {
+  if (m == 0) return MANTIS_OK;
+  if (!x || !w1 || !out || m < 0 || n_x < 0) return MANTIS_E_ARG;
+  if ((x2 == nullptr) != (w2 == nullptr) || (w3 == nullptr) != (n3 == 0)) return MANTIS_E_ARG;
+  if (add2 && !add2_rows) return MANTIS_E_ARG;
+  const int width = w3 ? n3 : n1;
+  if (ldx % 8 || (x2 && ldx2 % 8) || ldo % 4 || ldo < width || ldx < kK || (add1 && ld_add1 % 4))
+    return MANTIS_E_ARG;
+  if (!aligned16(x) || !aligned16(w1) || !aligned16(out) || (x2 && (!aligned16(x2) || !aligned16(w2))) ||
+      (w3 && !aligned16(w3)) || (b1 && !aligned16(b1)) || (b3 && !aligned16(b3)) ||
+      (add1 && !aligned16(add1)) || (add2 && !aligned16(add2)))
+    return MANTIS_E_ARG;
+  if (w3 && (n3 % 16 || n3 > 128)) return MANTIS_E_ARG;
+  Args a{x, ldx, x_rows, x_rows ? n_x : m, m, x2, ldx2, static_cast<const _Float16*>(w1),
+         static_cast<const _Float16*>(w2), b1, add1, ld_add1, add2, add2_rows, n_add2,
+         static_cast<const _Float16*>(w3), b3, n3, out, ldo, err_flag};
+  hipStream_t s = as_stream(stream);
+  const bool ln = layer_norm != 0, r = relu != 0, st2 = w3 != nullptr, hx2 = x2 != nullptr;
+  const int mode = out_mode;
+  // The supported combinations: projections, residual projections, and the
+  // two-layer MLP residuals of the blocks and heads.
+  if (!hx2 && !st2) {
+    if (x_dtype == MANTIS_F32 && ln && !r && mode == 0) {
+      if (n1 == 128) return launch<float, float, true, 128, false, false, false, 0>(a, s);
+      if (n1 == 256) return launch<float, float, true, 256, false, false, false, 0>(a, s);
+      if (n1 == 384) return launch<float, float, true, 384, false, false, false, 0>(a, s);
+    }
+    if (x_dtype == MANTIS_F32 && ln && !r && mode == 1 && n1 == 128)
+      return launch<float, float, true, 128, false, false, false, 1>(a, s);
+    if (!ln && !r && mode == 2 && n1 == 128) {
+      if (x_dtype == MANTIS_F32) return launch<float, float, false, 128, false, false, false, 2>(a, s);
+      if (x_dtype == MANTIS_F16) return launch<_Float16, float, false, 128, false, false, false, 2>(a, s);
+    }
+    if (!ln && !r && mode == 1 && n1 == 128 && x_dtype == MANTIS_F32)
+      return launch<float, float, false, 128, false, false, false, 1>(a, s);
+    if (!ln && !r && mode == 0 && n1 == 128 && x_dtype == MANTIS_F32)
+      return launch<float, float, false, 128, false, false, false, 0>(a, s);
+  }
+  if (st2 && r && mode == 2 && x_dtype == MANTIS_F32 && ln) {
+    if (hx2 && n1 == 128 && x2_dtype == MANTIS_F32)
+      return launch<float, float, true, 128, true, true, true, 2>(a, s);
+    if (hx2 && n1 == 128 && x2_dtype == MANTIS_F16)
+      return launch<float, _Float16, true, 128, true, true, true, 2>(a, s);
+    if (!hx2 && n1 == 256) return launch<float, float, true, 256, false, true, true, 2>(a, s);
+  }
+  if (st2 && r && mode == 1 && hx2 && n1 == 256 && x2_dtype == MANTIS_F32) {
+    if (x_dtype == MANTIS_F32 && ln) return launch<float, float, true, 256, true, true, true, 1>(a, s);
+    if (x_dtype == MANTIS_F16 && !ln) return launch<_Float16, float, false, 256, true, true, true, 1>(a, s);
+  }
+  return MANTIS_E_ARG;
+}

@@ -104,7 +104,8 @@ run_reduce_scalar_kernel(const Tin* __restrict__ values, int64_t n_src, int64_t 
 template <typename Tin, bool kVcls>
 __global__ void __launch_bounds__(kBlock)
 cell_attention_kernel(const Tin* __restrict__ q, const Tin* __restrict__ k,
-                      const Tin* __restrict__ v, const float* __restrict__ bias, int64_t n_classes,
+                      const Tin* __restrict__ v, int64_t ldq, int64_t ldk, int64_t ldv,
+                      const float* __restrict__ bias, int64_t n_classes,
                       const float* __restrict__ vcls, const int64_t* __restrict__ seg_ptr,
                       const int64_t* __restrict__ src, const int64_t* __restrict__ cls,
                       int64_t n_q, int64_t n_k, int64_t n_entries, float scale,
@@ -115,7 +116,7 @@ cell_attention_kernel(const Tin* __restrict__ q, const Tin* __restrict__ k,
   const int head = lane >> 2;
   if (row >= n_q) return;
   float qv[8];
-  load8(q + row * kRow + lane * 8, qv);
+  load8(q + row * ldq + lane * 8, qv);
   int64_t start, end;
   segment(seg_ptr, row, n_entries, start, end);
   float m = -INFINITY, l = 0.f;
@@ -127,8 +128,8 @@ cell_attention_kernel(const Tin* __restrict__ q, const Tin* __restrict__ k,
       continue;
     }
     float kv[8], vv[8];
-    load8(k + s * kRow + lane * 8, kv);
-    load8(v + s * kRow + lane * 8, vv);
+    load8(k + s * ldk + lane * 8, kv);
+    load8(v + s * ldv + lane * 8, vv);
     float dot = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) dot = fmaf(qv[i], kv[i], dot);
@@ -165,7 +166,8 @@ cell_attention_kernel(const Tin* __restrict__ q, const Tin* __restrict__ k,
 template <typename Tin>
 __global__ void __launch_bounds__(kBlock)
 latent_read_kernel(const Tin* __restrict__ q, const Tin* __restrict__ k,
-                   const Tin* __restrict__ v, const int64_t* __restrict__ offsets,
+                   const Tin* __restrict__ v, int64_t ldq, int64_t ldk, int64_t ldv,
+                   const int64_t* __restrict__ offsets,
                    const int64_t* __restrict__ order, int64_t n_pos, int64_t n_w, float scale,
                    float* __restrict__ out, float* __restrict__ m_out, float* __restrict__ l_out,
                    int32_t* flag) {
@@ -178,7 +180,7 @@ latent_read_kernel(const Tin* __restrict__ q, const Tin* __restrict__ k,
   const int head = lane >> 2;
   float qv[4][8];
 #pragma unroll
-  for (int s = 0; s < 4; ++s) load8(q + (pos * 4 + s) * kRow + lane * 8, qv[s]);
+  for (int s = 0; s < 4; ++s) load8(q + (pos * 4 + s) * ldq + lane * 8, qv[s]);
   int64_t a = offsets[pos], b = offsets[pos + 1];
   a = a < 0 ? 0 : (a > n_w ? n_w : a);
   b = b < a ? a : (b > n_w ? n_w : b);
@@ -197,8 +199,8 @@ latent_read_kernel(const Tin* __restrict__ q, const Tin* __restrict__ k,
       continue;
     }
     float kv[8], vv[8];
-    load8(k + w * kRow + lane * 8, kv);
-    load8(v + w * kRow + lane * 8, vv);
+    load8(k + w * ldk + lane * 8, kv);
+    load8(v + w * ldv + lane * 8, vv);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       float dot = 0.f;
@@ -248,7 +250,8 @@ latent_read_kernel(const Tin* __restrict__ q, const Tin* __restrict__ k,
 template <typename Tin>
 __global__ void __launch_bounds__(kBlock)
 latent_broadcast_kernel(const Tin* __restrict__ q, const Tin* __restrict__ k,
-                        const Tin* __restrict__ v, const int64_t* __restrict__ window_pos,
+                        const Tin* __restrict__ v, int64_t ldq, int64_t ldk, int64_t ldv,
+                        const int64_t* __restrict__ window_pos,
                         int64_t n_pos, int64_t n_w, float scale, float* __restrict__ out,
                         float* __restrict__ m_out, float* __restrict__ l_out, int32_t* flag) {
   const int64_t w = int64_t(blockIdx.x) * kGroupsPerBlock + threadIdx.x / kGroup;
@@ -262,11 +265,11 @@ latent_broadcast_kernel(const Tin* __restrict__ q, const Tin* __restrict__ k,
     raise_flag(flag, MANTIS_FLAG_INDEX);
   } else {
     float qv[8], sc[4];
-    load8(q + w * kRow + lane * 8, qv);
+    load8(q + w * ldq + lane * 8, qv);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       float kv[8];
-      load8(k + (p * 4 + s) * kRow + lane * 8, kv);
+      load8(k + (p * 4 + s) * ldk + lane * 8, kv);
       float dot = 0.f;
 #pragma unroll
       for (int j = 0; j < 8; ++j) dot = fmaf(qv[j], kv[j], dot);
@@ -278,7 +281,7 @@ latent_broadcast_kernel(const Tin* __restrict__ q, const Tin* __restrict__ k,
       const float e = __expf(sc[s] - mx);
       den += e;
       float vv[8];
-      load8(v + (p * 4 + s) * kRow + lane * 8, vv);
+      load8(v + (p * 4 + s) * ldv + lane * 8, vv);
 #pragma unroll
       for (int j = 0; j < 8; ++j) res[j] = fmaf(e, vv[j], res[j]);
     }
@@ -334,6 +337,11 @@ row_encode_kernel(const Tin* __restrict__ pre, int64_t n_w, const float* __restr
 }
 
 inline unsigned grid_rows(int64_t rows) { return unsigned((rows + kGroupsPerBlock - 1) / kGroupsPerBlock); }
+
+// Row strides of 128-wide operand rows: whole rows, 16-byte aligned.
+inline bool lds_ok(int64_t a, int64_t b, int64_t c) {
+  return a >= kRow && b >= kRow && c >= kRow && a % 8 == 0 && b % 8 == 0 && c % 8 == 0;
+}
 
 // Calls fn(T{}) with T the element type named by a MANTIS_* dtype code;
 // returns false for an unknown code.
@@ -396,7 +404,7 @@ int32_t mantis_run_reduce(const void* values, int32_t values_dtype, int64_t n_sr
 }
 
 int32_t mantis_cell_attention(const void* q, const void* k, const void* v, int32_t dtype,
-                              const float* bias, int64_t n_classes, const float* vcls,
+                              int64_t ldq, int64_t ldk, int64_t ldv, const float* bias, int64_t n_classes, const float* vcls,
                               const int64_t* seg_ptr, const int64_t* src, const int64_t* cls,
                               int64_t n_entries, int64_t n_q, int64_t n_k, int32_t heads,
                               int32_t hd, float* out, float* m, float* l, int32_t* err_flag,
@@ -406,7 +414,7 @@ int32_t mantis_cell_attention(const void* q, const void* k, const void* v, int32
       n_k < 0 || n_classes <= 0)
     return MANTIS_E_ARG;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out) ||
-      (vcls && !aligned16(vcls)))
+      (vcls && !aligned16(vcls)) || !lds_ok(ldq, ldk, ldv))
     return MANTIS_E_ARG;
   if (n_entries < 0 || (n_entries > 0 && (!src || !cls))) return MANTIS_E_ARG;
   const float scale = 1.0f / sqrtf(float(hd));
@@ -416,51 +424,56 @@ int32_t mantis_cell_attention(const void* q, const void* k, const void* v, int32
     using T = decltype(t);
     if (vcls)
       cell_attention_kernel<T, true><<<grid, block, 0, s>>>(
-          static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v), bias,
-          n_classes, vcls, seg_ptr, src, cls, n_q, n_k, n_entries, scale, out, m, l, err_flag);
+          static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v), ldq, ldk,
+          ldv, bias, n_classes, vcls, seg_ptr, src, cls, n_q, n_k, n_entries, scale, out, m, l,
+          err_flag);
     else
       cell_attention_kernel<T, false><<<grid, block, 0, s>>>(
-          static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v), bias,
-          n_classes, vcls, seg_ptr, src, cls, n_q, n_k, n_entries, scale, out, m, l, err_flag);
+          static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v), ldq, ldk,
+          ldv, bias, n_classes, vcls, seg_ptr, src, cls, n_q, n_k, n_entries, scale, out, m, l,
+          err_flag);
   });
   if (!ok) return MANTIS_E_ARG;
   return launched();
 }
 
 int32_t mantis_latent_read(const void* q, const void* k, const void* v, int32_t dtype,
-                           const int64_t* offsets, const int64_t* order, int64_t n_pos,
+                           int64_t ldq, int64_t ldk, int64_t ldv, const int64_t* offsets, const int64_t* order, int64_t n_pos,
                            int64_t n_w, int32_t heads, int32_t hd, float* out, float* m, float* l,
                            int32_t* err_flag, void* stream) {
   if (n_pos == 0) return MANTIS_OK;
   if (!q || !offsets || !out || heads != 4 || hd != 32 || n_pos < 0 || n_w < 0) return MANTIS_E_ARG;
+  if (!lds_ok(ldq, ldk, ldv) || !aligned16(q) || (n_w > 0 && (!aligned16(k) || !aligned16(v))))
+    return MANTIS_E_ARG;
   if (n_w > 0 && (!k || !v || !order)) return MANTIS_E_ARG;
   const float scale = 1.0f / sqrtf(float(hd));
   hipStream_t s = as_stream(stream);
   const bool ok = with_type(dtype, [&](auto tv) {
     using T = decltype(tv);
     latent_read_kernel<T><<<unsigned(n_pos), kBlock, 0, s>>>(
-        static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v), offsets,
-        order, n_pos, n_w, scale, out, m, l, err_flag);
+        static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v), ldq, ldk, ldv,
+        offsets, order, n_pos, n_w, scale, out, m, l, err_flag);
   });
   if (!ok) return MANTIS_E_ARG;
   return launched();
 }
 
 int32_t mantis_latent_broadcast(const void* q, const void* k, const void* v, int32_t dtype,
-                                const int64_t* window_pos, int64_t n_pos, int64_t n_w,
+                                int64_t ldq, int64_t ldk, int64_t ldv, const int64_t* window_pos, int64_t n_pos, int64_t n_w,
                                 int32_t heads, int32_t hd, float* out, float* m, float* l,
                                 int32_t* err_flag, void* stream) {
   if (n_w == 0) return MANTIS_OK;
   if (!q || !k || !v || !window_pos || !out || heads != 4 || hd != 32 || n_w < 0 || n_pos < 0)
     return MANTIS_E_ARG;
+  if (!lds_ok(ldq, ldk, ldv) || !aligned16(q) || !aligned16(k) || !aligned16(v)) return MANTIS_E_ARG;
   const float scale = 1.0f / sqrtf(float(hd));
   hipStream_t s = as_stream(stream);
   const dim3 grid(grid_rows(n_w)), block(kBlock);
   const bool ok = with_type(dtype, [&](auto tv) {
     using T = decltype(tv);
     latent_broadcast_kernel<T><<<grid, block, 0, s>>>(
-        static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v), window_pos,
-        n_pos, n_w, scale, out, m, l, err_flag);
+        static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v), ldq, ldk, ldv,
+        window_pos, n_pos, n_w, scale, out, m, l, err_flag);
   });
   if (!ok) return MANTIS_E_ARG;
   return launched();

@@ -1,0 +1,224 @@
+// Row LayerNorm, the value-head readout and the acting-Q composition for
+// gfx950 (replaces model.py:973-985 ln_out, value_head 1160-1183 and
+// compose_q / compose_acting_q 177-220 with segments.py:24-31).
+#include "common.hpp"
+
+namespace mantis {
+namespace {
+
+constexpr int kRow = 128;
+
+__device__ __forceinline__ float group16_sum(float x) {
+  x += __shfl_xor(x, 1);
+  x += __shfl_xor(x, 2);
+  x += __shfl_xor(x, 4);
+  x += __shfl_xor(x, 8);
+  return x;
+}
+
+// LayerNorm over rows of 128 (eps 1e-5, biased variance), 16 lanes per row.
+template <typename TO>
+__global__ void __launch_bounds__(256)
+layer_norm_kernel(const float* __restrict__ x, int64_t ldx, int64_t m, const float* __restrict__ gamma,
+                  const float* __restrict__ beta, TO* __restrict__ out, int64_t ldo) {
+  const int64_t row = int64_t(blockIdx.x) * 16 + threadIdx.x / 16;
+  const int lane = threadIdx.x % 16;
+  if (row >= m) return;
+  float v[8], gm[8], bt[8];
+  load8(x + row * ldx + lane * 8, v);
+  load8(gamma + lane * 8, gm);
+  load8(beta + lane * 8, bt);
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) s += v[i];
+  const float mean = group16_sum(s) * (1.f / kRow);
+  float q = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    v[i] -= mean;
+    q += v[i] * v[i];
+  }
+  const float rstd = rsqrtf(group16_sum(q) * (1.f / kRow) + 1e-5f);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = v[i] * rstd * gm[i] + bt[i];
+  store8(out + row * ldo + lane * 8, v);
+}
+
+// Value readout: per position, Q learned queries attend (one 128-wide head,
+// scale 1/sqrt(128)) over [LN(token); LN(windows of the position)], where
+// every key/value row is LayerNorm(src row) computed on the fly.  One
+// workgroup per position; 16 lane-groups stride over the rows and merge
+// their online-softmax states through LDS.  Empty positions read the token.
+__global__ void __launch_bounds__(256)
+value_read_kernel(const float* __restrict__ token, const float* __restrict__ rows, int64_t n_rows,
+                  const int64_t* __restrict__ offsets, const int64_t* __restrict__ order,
+                  const float* __restrict__ gamma, const float* __restrict__ beta,
+                  const float* __restrict__ queries, float* __restrict__ out, int32_t* flag) {
+  constexpr int kQ = 4;
+  __shared__ float s_m[16][kQ], s_l[16][kQ];
+  __shared__ float s_acc[16][kQ][kRow];
+  const int64_t p = blockIdx.x;
+  const int grp = threadIdx.x / 16, lane = threadIdx.x % 16;
+  float gm[8], bt[8], qv[kQ][8];
+  load8(gamma + lane * 8, gm);
+  load8(beta + lane * 8, bt);
+#pragma unroll
+  for (int q = 0; q < kQ; ++q) load8(queries + q * kRow + lane * 8, qv[q]);
+  const float scale = 0.08838834764831845f;  // 1/sqrt(128)
+  float m[kQ], l[kQ], acc[kQ][8];
+#pragma unroll
+  for (int q = 0; q < kQ; ++q) {
+    m[q] = -INFINITY;
+    l[q] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[q][i] = 0.f;
+  }
+  int64_t a = offsets[p], b = offsets[p + 1];
+  a = a < 0 ? 0 : (a > n_rows ? n_rows : a);
+  b = b < a ? a : (b > n_rows ? n_rows : b);
+  // index -1 is the position's token row
+  for (int64_t i = a - 1 + grp; i < b; i += 16) {
+    const float* src;
+    if (i < a) {
+      src = token + p * kRow;
+    } else {
+      const int64_t r = order[i];
+      if (r < 0 || r >= n_rows) {
+        raise_flag(flag, MANTIS_FLAG_INDEX);
+        continue;
+      }
+      src = rows + r * kRow;
+    }
+    float v[8];
+    load8(src + lane * 8, v);
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s += v[j];
+    const float mean = group16_sum(s) * (1.f / kRow);
+    float sq = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      v[j] -= mean;
+      sq += v[j] * v[j];
+    }
+    const float rstd = rsqrtf(group16_sum(sq) * (1.f / kRow) + 1e-5f);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = v[j] * rstd * gm[j] + bt[j];
+#pragma unroll
+    for (int q = 0; q < kQ; ++q) {
+      float d = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) d = fmaf(qv[q][j], v[j], d);
+      const float score = group16_sum(d) * scale;
+      const float mn = fmaxf(m[q], score);
+      const float al = __expf(m[q] - mn), pr = __expf(score - mn);
+      l[q] = l[q] * al + pr;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[q][j] = fmaf(pr, v[j], acc[q][j] * al);
+      m[q] = mn;
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < kQ; ++q) {
+    if (lane == 0) {
+      s_m[grp][q] = m[q];
+      s_l[grp][q] = l[q];
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s_acc[grp][q][lane * 8 + j] = acc[q][j];
+  }
+  __syncthreads();
+  for (int o = threadIdx.x; o < kQ * kRow; o += 256) {
+    const int q = o / kRow, d = o % kRow;
+    float mx = -INFINITY;
+    for (int g2 = 0; g2 < 16; ++g2) mx = fmaxf(mx, s_m[g2][q]);
+    float lt = 0.f, at = 0.f;
+    for (int g2 = 0; g2 < 16; ++g2) {
+      if (s_m[g2][q] == -INFINITY) continue;
+      const float f = __expf(s_m[g2][q] - mx);
+      lt = fmaf(s_l[g2][q], f, lt);
+      at = fmaf(s_acc[g2][q][d], f, at);
+    }
+    out[(p * kQ + q) * kRow + d] = lt > 0.f ? at / lt : 0.f;
+  }
+}
+
+// Per position: p = softmax(critic logits) per cell, Q = p_pos - p_neg,
+// M = max over the position's cells of p_pos + p_neg, score = Q / max(M, floor).
+__global__ void __launch_bounds__(256)
+compose_q_kernel(const float* __restrict__ critic, int64_t ld, const int64_t* __restrict__ offsets,
+                 int64_t n_cells, float mass_floor, float* __restrict__ q_values,
+                 float* __restrict__ q_score) {
+  __shared__ float s_max[256];
+  const int64_t p = blockIdx.x;
+  int64_t a = offsets[p], b = offsets[p + 1];
+  a = a < 0 ? 0 : (a > n_cells ? n_cells : a);
+  b = b < a ? a : (b > n_cells ? n_cells : b);
+  float mx = -3.402823466e38f;
+  for (int64_t i = a + threadIdx.x; i < b; i += 256) {
+    const float z0 = critic[i * ld], z1 = critic[i * ld + 1], z2 = critic[i * ld + 2];
+    const float zm = fmaxf(z0, fmaxf(z1, z2));
+    const float e0 = __expf(z0 - zm), e1 = __expf(z1 - zm), e2 = __expf(z2 - zm);
+    const float inv = 1.f / (e0 + e1 + e2);
+    const float pp = e0 * inv, pn = e1 * inv;
+    q_values[i] = pp - pn;
+    mx = fmaxf(mx, pp + pn);
+  }
+  s_max[threadIdx.x] = mx;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if (threadIdx.x < w) s_max[threadIdx.x] = fmaxf(s_max[threadIdx.x], s_max[threadIdx.x + w]);
+    __syncthreads();
+  }
+  const float inv_scale = 1.f / fmaxf(s_max[0], mass_floor);
+  for (int64_t i = a + threadIdx.x; i < b; i += 256) q_score[i] = q_values[i] * inv_scale;
+}
+
+}  // namespace
+}  // namespace mantis
+
+using namespace mantis;
+
+extern "C" {
+
+int32_t mantis_layer_norm(const float* x, int64_t ldx, int64_t m, const float* gamma, const float* beta,
+                          void* out, int32_t out_dtype, int64_t ldo, void* stream) {
+  if (m == 0) return MANTIS_OK;
+  if (!x || !gamma || !beta || !out || m < 0 || ldx < kRow || ldo < kRow || ldx % 8 || ldo % 8)
+    return MANTIS_E_ARG;
+  if (!aligned16(x) || !aligned16(gamma) || !aligned16(beta) || !aligned16(out)) return MANTIS_E_ARG;
+  const unsigned grid = unsigned((m + 15) / 16);
+  hipStream_t s = as_stream(stream);
+  if (out_dtype == MANTIS_F32)
+    layer_norm_kernel<float><<<grid, 256, 0, s>>>(x, ldx, m, gamma, beta, static_cast<float*>(out), ldo);
+  else if (out_dtype == MANTIS_F16)
+    layer_norm_kernel<_Float16><<<grid, 256, 0, s>>>(x, ldx, m, gamma, beta, static_cast<_Float16*>(out), ldo);
+  else
+    return MANTIS_E_ARG;
+  return launched();
+}
+
+int32_t mantis_value_read(const float* token, const float* rows, int64_t n_rows, const int64_t* offsets,
+                          const int64_t* order, int64_t n_pos, const float* gamma, const float* beta,
+                          const float* queries, int32_t n_queries, float* out, int32_t* err_flag,
+                          void* stream) {
+  if (n_pos == 0) return MANTIS_OK;
+  if (!token || !offsets || !gamma || !beta || !queries || !out || n_queries != 4 || n_pos < 0 ||
+      n_rows < 0 || (n_rows > 0 && (!rows || !order)))
+    return MANTIS_E_ARG;
+  value_read_kernel<<<unsigned(n_pos), 256, 0, as_stream(stream)>>>(token, rows, n_rows, offsets, order,
+                                                                    gamma, beta, queries, out, err_flag);
+  return launched();
+}
+
+int32_t mantis_compose_q(const float* critic, int64_t ld, const int64_t* offsets, int64_t n_pos,
+                         int64_t n_cells, float mass_floor, float* q_values, float* q_score,
+                         void* stream) {
+  if (n_pos == 0) return MANTIS_OK;
+  if (!critic || !offsets || !q_values || !q_score || ld < 3 || n_pos < 0 || n_cells < 0) return MANTIS_E_ARG;
+  compose_q_kernel<<<unsigned(n_pos), 256, 0, as_stream(stream)>>>(critic, ld, offsets, n_cells, mass_floor,
+                                                                   q_values, q_score);
+  return launched();
+}
+
+}  // extern "C"

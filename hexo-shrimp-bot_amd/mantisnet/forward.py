@@ -3,21 +3,39 @@
 Composition follows the reference exactly (python/mantisnet/mantisnet/
 model.py: trunk 898-985, _Block.forward 543-692, _cell_stage 397-490,
 _window_latent_cycle 492-541, value_head 1160-1183, cell_head_logits
-1111-1139, _action_contribution 1031-1063, _cell_scores 1065-1091).
-Every reference custom op runs as a HIP kernel of libmantis_hip.so
-(:mod:`mantisnet.ops`); the dense projections run as bf16 GEMMs with fp32
-accumulation, LayerNorms and softmax statistics in fp32, residual streams in
-fp32 — the arithmetic the reference runs under its bf16 autocast
-(klent/train.py:108), except that the head output layers, the latent/value
-readouts and the last block's four-query read stay fp32 end to end.
+1111-1139, _action_contribution 1031-1063, _cell_scores 1065-1091); the
+arithmetic is regrouped into fused HIP kernels (libmantis_hip.so via
+:mod:`mantisnet.ops`):
+
+* every LayerNorm -> Linear pair is one ``fused_linear`` launch with the
+  LayerNorm affine folded into the weights (W' = W diag(gamma),
+  b' = b + W beta); projections that share an input run as one wide GEMM
+  (k|v, q|k|v) whose halves feed the attention kernels as strided rows;
+* ``_PairMlp`` and the FFN run as one launch each: stage 1, ReLU and stage
+  2 in registers, added into the fp32 residual stream in place;
+* the per-class terms of the message passing are precomposed with the
+  layer that consumes them (``counts @ e_ws @ lin_b^T`` per window pattern,
+  ``e_sw @ lin_b^T`` run-reduced per stone), as the reference precomposes
+  ``counts @ e_ws`` (model.py:937-955);
+* the two cell heads run as one two-layer launch: ``lin_a`` is composed into
+  the projection, extension and class tables (lin_a(p x + p_act a + sum e) =
+  (lin_a p) x + (lin_a p_act) a + sum (e lin_a^T)), the g half is a per-
+  position row add, and both output layers are one block-diagonal stage 2.
+
+Precision: every GEMM and attention operand is fp16 with fp32 accumulation;
+LayerNorm statistics, softmax, the residual streams (s, w, g, c) and the head
+outputs are fp32.  The reference runs under bf16 autocast
+(klent/train.py:108); fp16 runs at the same MFMA rate with three more
+mantissa bits, which keeps the policy logits within 1e-2 of the fp32
+reference (bf16 operands drift to ~5e-2 over four blocks).
 
 Per-batch index views (the reference's incidence_plan, window_latent_layout,
-cell_tables and cell_node_edge_tables) are derived once per forward on the
-device and shared by every block.
+cell_tables and cell_node_edge_tables) are derived once per batch on the
+device and shared by the trunk and the heads.
 
 Scope: the production cell-state configuration (``cell_nodes=True``, either
-node scope) with H = 128 and 4 heads of 32.  Other knob combinations raise
-``NotImplementedError``; the forward is inference-only.
+node scope), H = 128, 4 heads of 32, 4 value queries.  Other knob
+combinations raise ``NotImplementedError``; the forward is inference-only.
 """
 
 from __future__ import annotations
@@ -32,103 +50,137 @@ from torch import Tensor
 from . import ops
 from .builder import Batch
 
-BF16 = torch.bfloat16
-HALF = torch.float16  # the MFMA operand type of every projection and attention
+HALF = torch.float16
+F32 = torch.float32
 GLOBAL_ROWS = 4
 ORBIT48 = 48
 
 
-def _supported(model) -> None:
+def _supported(model) -> torch.device:
     cfg = model.cfg
     if not (cfg.cell_nodes and cfg.uses_cell_state):
         raise NotImplementedError("the MI355X forward implements the cell-node configuration (cell_nodes=True)")
     if cfg.cell_adjacency or cfg.cell_structure or cfg.action_tactical:
         raise NotImplementedError("cell_adjacency / cell_structure / action_tactical are not implemented")
-    if cfg.h != 128 or cfg.heads != 4 or cfg.value_queries != 4:
-        raise NotImplementedError("the MI355X kernels are built for H=128 with 4 heads and 4 value queries")
+    if cfg.h != 128 or cfg.heads != 4 or cfg.value_queries != 4 or cfg.ffn_factor != 2 or cfg.policy_hidden != 128:
+        raise NotImplementedError("the MI355X kernels are built for H=128, 4 heads, FFN 256, 4 value queries")
     dev = next(model.parameters()).device
     if dev.type != "cuda":
         raise RuntimeError("MantisNet runs on the MI355X HIP path only: move the model to a cuda device")
+    return dev
 
 
-# ----------------------------------------------------------------- weights
+# ----------------------------------------------------------------- prepared weights
 
 
-class _Weights:
-    """fp16 copies of every matrix a GEMM reads, rebuilt when a parameter
-    changes (tracked through the tensors' version counters)."""
+class Prepared:
+    """fp16 GEMM operands with folded LayerNorms and composed class tables,
+    rebuilt whenever a parameter changes (tracked by version counters)."""
 
     def __init__(self, model):
-        self.key = None
         self.model = model
-        self.bf: dict[str, Tensor] = {}
+        self.key = None
+        self.t: dict[str, Tensor] = {}
 
     def refresh(self):
         params = dict(self.model.named_parameters())
         key = tuple((n, p.data_ptr(), p._version) for n, p in params.items())
-        if key == self.key:
-            return
-        self.bf = {n: p.detach().to(HALF).contiguous() for n, p in params.items() if n.endswith(".weight") and p.ndim == 2}
-        self.key = key
+        if key != self.key:
+            with torch.no_grad():
+                self.t = _prepare(self.model, {n: p.detach().float() for n, p in params.items()})
+            self.key = key
+        return self
+
+    def __getitem__(self, k):
+        return self.t[k]
 
 
-def _weights(model) -> _Weights:
-    w = getattr(model, "_mi355x_weights", None)
+def _fold(P, ln: str | None, lins: list[str]):
+    """(W' fp16, b' fp32) for LN -> concat(lins); ln None = no LayerNorm."""
+    ws, bs = [], []
+    for name in lins:
+        w = P[name + ".weight"]
+        b = P.get(name + ".bias", torch.zeros(w.shape[0], device=w.device))
+        if ln is not None:
+            g, be = P[ln + ".weight"], P[ln + ".bias"]
+            b = b + w @ be
+            w = w * g[None, :]
+        ws.append(w)
+        bs.append(b)
+    return torch.cat(ws).to(HALF).contiguous(), torch.cat(bs).float().contiguous()
+
+
+def _prepare(model, P) -> dict[str, Tensor]:
+    cfg = model.cfg
+    t: dict[str, Tensor] = {}
+
+    def put(key, pair):
+        t[key + ".w"], t[key + ".b"] = pair
+
+    counts = model.pattern_counts.float()
+    for i in range(cfg.blocks):
+        pb = f"blocks.{i}."
+        put(pb + "u", _fold(P, pb + "ln_ws_s", [pb + "u"]))
+        put(pb + "mlp_w1", _fold(P, pb + "ln_ws_w", [pb + "mlp_w.lin_a"]))
+        t[pb + "mlp_w2.w"] = P[pb + "mlp_w.lin_b.weight"].to(HALF).contiguous()
+        put(pb + "mlp_w3", _fold(P, None, [pb + "mlp_w.out"]))
+        # window class term composed with lin_b: counts @ e_ws @ lin_b^T, per pattern
+        t[pb + "ws_tab"] = (counts @ (P[pb + "e_ws.weight"] @ P[pb + "mlp_w.lin_b.weight"].t())).contiguous()
+        put(pb + "cr_q", _fold(P, pb + "ln_cr_c", [pb + "cr_wq"]))
+        put(pb + "cr_kv", _fold(P, pb + "ln_cr_w", [pb + "cr_wk", pb + "cr_wv"]))
+        put(pb + "cr_o", _fold(P, None, [pb + "cr_wo"]))
+        put(pb + "rad_q", _fold(P, pb + "ln_radius_c", [pb + "radius_wq"]))
+        put(pb + "rad_kv", _fold(P, pb + "ln_radius_s", [pb + "radius_wk", pb + "radius_wv"]))
+        put(pb + "rad_o", _fold(P, None, [pb + "radius_wo"]))
+        put(pb + "wr_q", _fold(P, pb + "ln_wr_w", [pb + "wr_wq"]))
+        put(pb + "wr_kv", _fold(P, pb + "ln_wr_c", [pb + "wr_wk", pb + "wr_wv"]))
+        put(pb + "wr_o", _fold(P, None, [pb + "wr_wo"]))
+        put(pb + "v", _fold(P, pb + "ln_sw_w", [pb + "v"]))
+        put(pb + "mlp_s1", _fold(P, pb + "ln_sw_s", [pb + "mlp_s.lin_a"]))
+        t[pb + "mlp_s2.w"] = P[pb + "mlp_s.lin_b.weight"].to(HALF).contiguous()
+        put(pb + "mlp_s3", _fold(P, None, [pb + "mlp_s.out"]))
+        t[pb + "sw_tab"] = (P[pb + "e_sw.weight"] @ P[pb + "mlp_s.lin_b.weight"].t()).contiguous()
+        put(pb + "qkv", _fold(P, pb + "ln_attn", [pb + "wq", pb + "wk", pb + "wv"]))
+        put(pb + "attn_o", _fold(P, None, [pb + "wo"]))
+        put(pb + "lq_read", _fold(P, pb + "latent_ln_read_q", [pb + "latent_wq_read"]))
+        put(pb + "lkv_read", _fold(P, pb + "latent_ln_read_w", [pb + "latent_wk_read", pb + "latent_wv_read"]))
+        put(pb + "lo_read", _fold(P, None, [pb + "latent_wo_read"]))
+        put(pb + "lq_bcast", _fold(P, pb + "latent_ln_bcast_q", [pb + "latent_wq_bcast"]))
+        put(pb + "lkv_bcast", _fold(P, pb + "latent_ln_bcast_l", [pb + "latent_wk_bcast", pb + "latent_wv_bcast"]))
+        put(pb + "lo_bcast", _fold(P, None, [pb + "latent_wo_bcast"]))
+        put(pb + "ffn1", _fold(P, pb + "ln_ffn", [pb + "ffn.0"]))
+        put(pb + "ffn2", _fold(P, None, [pb + "ffn.2"]))
+    t["sw_all"] = torch.cat([t[f"blocks.{i}.sw_tab"] for i in range(cfg.blocks)], 1).contiguous()
+    # heads: act_proj reads ln_out(w)
+    put("act_proj", _fold(P, None, ["act_proj"]))
+    h1, h2, hb, tabs = [], [], [], []
+    for proj, ext, mlp, emb in (("p", "p_act", "mlp_p", "e_pw"), ("q", "q_act", "mlp_q", "e_qw")):
+        la = P[mlp + ".lin_a.weight"]
+        h1.append(la @ P[proj + ".weight"])
+        h2.append(la @ P[ext + ".weight"])
+        hb.append(P[mlp + ".lin_a.bias"])
+        tabs.append(P[emb + ".weight"] @ la.t())
+    t["head1.w"] = torch.cat(h1).to(HALF).contiguous()
+    t["head2.w"] = torch.cat(h2).to(HALF).contiguous()
+    t["head1.b"] = torch.cat(hb).contiguous()
+    t["head_tab"] = torch.cat(tabs, 1).contiguous()  # (726, 256)
+    w3 = torch.zeros(16, 256, device=la.device)
+    w3[0, :128] = P["mlp_p.out.weight"][0]
+    w3[1:4, 128:] = P["mlp_q.out.weight"]
+    b3 = torch.zeros(16, device=la.device)
+    b3[0] = P["mlp_p.out.bias"][0]
+    b3[1:4] = P["mlp_q.out.bias"]
+    t["head3.w"], t["head3.b"] = w3.to(HALF).contiguous(), b3
+    t["glin_b"] = torch.cat([P["mlp_p.lin_b.weight"], P["mlp_q.lin_b.weight"]]).contiguous()  # (256, 128)
+    return t
+
+
+def _prepared(model) -> Prepared:
+    w = getattr(model, "_mi355x_prepared", None)
     if w is None:
-        w = _Weights(model)
-        object.__setattr__(model, "_mi355x_weights", w)
-    w.refresh()
-    return w
-
-
-class _Ctx:
-    def __init__(self, model):
-        self.m = model
-        self.W = _weights(model)
-        self.p = dict(model.named_parameters())
-
-    def lin(self, x: Tensor, name: str, out_fp32: bool = False) -> Tensor:
-        """y = x W^T + b: fp16 operands, fp32 accumulation; fp16 result unless
-        ``out_fp32`` (then the product and bias stay fp32)."""
-        w = self.W.bf[name + ".weight"]
-        b = self.p.get(name + ".bias")
-        if out_fp32:
-            x2 = x.reshape(-1, x.shape[-1]).to(HALF)
-            y = _mm_fp32(x2, w).view(*x.shape[:-1], w.shape[0])
-            return y + b if b is not None else y
-        return F.linear(_half(x), w, None if b is None else b.to(HALF))
-
-    def ln(self, x: Tensor, name: str) -> Tensor:
-        return F.layer_norm(x.float(), (x.shape[-1],), self.p[name + ".weight"], self.p[name + ".bias"], 1e-5)
-
-    def pair_mlp(self, a: Tensor, b: Tensor, name: str) -> Tensor:
-        return self.lin(F.relu(self.lin(a, name + ".lin_a") + self.lin(b, name + ".lin_b")), name + ".out")
-
-
-def _half(x: Tensor) -> Tensor:
-    """fp32 -> fp16 with saturation at +-65504 (no overflow to inf)."""
-    if x.dtype == HALF:
-        return x
-    return x.clamp(-65504.0, 65504.0).to(HALF)
-
-
-_MM_OUT_DTYPE: bool | None = None
-
-
-def _mm_fp32(x: Tensor, w: Tensor) -> Tensor:
-    """x @ w^T with 16-bit operands and an fp32 result (no rounding of the
-    product).  Uses the device GEMM's fp32 output when torch exposes it, else
-    an fp32 GEMM over the same bf16-valued operands."""
-    global _MM_OUT_DTYPE
-    if _MM_OUT_DTYPE is None:
-        try:
-            torch.mm(x[:1], w.t(), out_dtype=torch.float32)
-            _MM_OUT_DTYPE = True
-        except (RuntimeError, TypeError):
-            _MM_OUT_DTYPE = False
-    if _MM_OUT_DTYPE:
-        return torch.mm(x, w.t(), out_dtype=torch.float32)
-    return torch.mm(x.float(), w.float().t())
+        w = Prepared(model)
+        object.__setattr__(model, "_mi355x_prepared", w)
+    return w.refresh()
 
 
 # ----------------------------------------------------------------- per-batch plan
@@ -145,7 +197,6 @@ class Plan:
     n_w: int
     n_c: int
     inc_win_ptr: Tensor  # window-major incidence CSR (aggregate_to_windows)
-    run_stone: Tensor
     run_window: Tensor
     run_class: Tensor
     inc_stone_ptr: Tensor  # stone-major incidence CSR (aggregate_to_stones)
@@ -163,8 +214,9 @@ class Plan:
     radius_src: Tensor
     radius_class: Tensor
     seq_lens: Tensor
-    global_slot: Tensor
-    dec_cell_ptr: Tensor  # CSR of the batch's own decoder order (row encoder / class sums)
+    attn_src: Tensor  # padded attention slot -> row of [s; g] (or -1)
+    attn_back: Tensor  # row of [s; g] -> padded attention slot
+    dec_cell_ptr: Tensor  # CSR of the batch's own decoder order
 
 
 def _stable_order(key: Tensor) -> Tensor:
@@ -198,120 +250,24 @@ def make_plan(model, b: Batch) -> Plan:
         src, dst, classes = src[keep], dst[keep], classes[keep]
     rorder = _stable_order(dst)
     radius_ptr = ops.runs_to_ptr(dst[rorder].contiguous(), n_c)
+    # attention rows [latents; stones] per position over the [s; g] buffer
     gslot = (torch.arange(p, device=dev)[:, None] * max_t + torch.arange(GLOBAL_ROWS, device=dev)[None, :]).reshape(-1)
+    attn_src = torch.full((p * max_t,), -1, dtype=torch.long, device=dev)
+    attn_src[b.stone_slot] = torch.arange(n_s, device=dev)
+    attn_src[gslot] = n_s + torch.arange(p * GLOBAL_ROWS, device=dev)
+    attn_back = torch.cat([b.stone_slot, gslot])
     return Plan(
         n_pos=p, max_t=max_t, max_w=max_w, n_s=n_s, n_w=n_w, n_c=n_c,
         inc_win_ptr=ops.runs_to_ptr(b.inc_window, n_w),
-        run_stone=run_stone, run_window=run_window, run_class=run_class,
+        run_window=run_window, run_class=run_class,
         inc_stone_ptr=ops.runs_to_ptr(run_stone.contiguous(), n_s),
         window_pos=window_pos, layout_offsets=offsets, layout_order=lorder,
         covered_mask=covered, cell_ptr=cell_ptr, edge_window=edge_window, edge_class=edge_class,
         win_ptr=win_ptr, edge_wcell=edge_cell[worder], edge_wclass=edge_class[worder],
         radius_ptr=radius_ptr, radius_src=src[rorder], radius_class=classes[rorder],
-        seq_lens=b.attn_valid.sum(dim=1, dtype=torch.int32), global_slot=gslot,
+        seq_lens=b.attn_valid.sum(dim=1, dtype=torch.int32), attn_src=attn_src, attn_back=attn_back,
         dec_cell_ptr=ops.runs_to_ptr(b.dec_cell, n_c),
     )
-
-
-# ----------------------------------------------------------------- blocks
-
-
-def _cell_stage(C: _Ctx, pre: str, plan: Plan, s, w, c):
-    n_c, n_w, n_s = plan.n_c, plan.n_w, plan.n_s
-    zc, zw = C.ln(c, pre + "ln_cr_c"), C.ln(w, pre + "ln_cr_w")
-    read = ops.cell_attention(
-        C.lin(zc, pre + "cr_wq").view(n_c, 4, 32), C.lin(zw, pre + "cr_wk").view(n_w, 4, 32),
-        C.lin(zw, pre + "cr_wv").view(n_w, 4, 32), C.p[pre + "cr_bias"], C.p[pre + "cr_vclass.weight"],
-        plan.cell_ptr, plan.edge_window, plan.edge_class,
-    )
-    c = c + C.lin(read.view(n_c, 128), pre + "cr_wo")
-    zc, zs = C.ln(c, pre + "ln_radius_c"), C.ln(s, pre + "ln_radius_s")
-    read = ops.cell_attention(
-        C.lin(zc, pre + "radius_wq").view(n_c, 4, 32), C.lin(zs, pre + "radius_wk").view(n_s, 4, 32),
-        C.lin(zs, pre + "radius_wv").view(n_s, 4, 32), C.p[pre + "radius_bias"],
-        C.p[pre + "radius_vclass.weight"], plan.radius_ptr, plan.radius_src, plan.radius_class,
-    )
-    c = c + C.lin(read.view(n_c, 128), pre + "radius_wo")
-    zw, zc = C.ln(w, pre + "ln_wr_w"), C.ln(c, pre + "ln_wr_c")
-    back = ops.cell_attention(
-        C.lin(zw, pre + "wr_wq").view(n_w, 4, 32), C.lin(zc, pre + "wr_wk").view(n_c, 4, 32),
-        C.lin(zc, pre + "wr_wv").view(n_c, 4, 32), C.p[pre + "wr_bias"], None,
-        plan.win_ptr, plan.edge_wcell, plan.edge_wclass,
-    )
-    w = w + C.lin(back.view(n_w, 128), pre + "wr_wo")
-    return w, c
-
-
-def _latent_cycle(C: _Ctx, pre: str, plan: Plan, w, g):
-    p = plan.n_pos
-    q = C.lin(C.ln(g, pre + "latent_ln_read_q"), pre + "latent_wq_read").view(p, 4, 4, 32)
-    rows = C.ln(w, pre + "latent_ln_read_w")
-    k = C.lin(rows, pre + "latent_wk_read").view(-1, 4, 32)
-    v = C.lin(rows, pre + "latent_wv_read").view(-1, 4, 32)
-    read = ops.latent_read(q, k, v, plan.layout_offsets, plan.layout_order)
-    g = g + C.lin(read.view(p, 4, 128), pre + "latent_wo_read", out_fp32=True)
-    # 4 x 4 latent self-mix, fp32 (all four slots live)
-    z = C.ln(g, pre + "latent_ln_mix")
-    qm = C.lin(z, pre + "latent_wq_mix", True).view(p, 4, 4, 32).transpose(1, 2)
-    km = C.lin(z, pre + "latent_wk_mix", True).view(p, 4, 4, 32).transpose(1, 2)
-    vm = C.lin(z, pre + "latent_wv_mix", True).view(p, 4, 4, 32).transpose(1, 2)
-    att = (torch.matmul(qm, km.transpose(-1, -2)) / math.sqrt(32)).softmax(-1)
-    mixed = torch.matmul(att, vm).transpose(1, 2).reshape(p, 4, 128)
-    g = g + C.lin(mixed, pre + "latent_wo_mix", True)
-    lat = C.ln(g, pre + "latent_ln_bcast_l")
-    qb = C.lin(C.ln(w, pre + "latent_ln_bcast_q"), pre + "latent_wq_bcast").view(-1, 4, 32)
-    kb = C.lin(lat, pre + "latent_wk_bcast").view(p, 4, 4, 32)
-    vb = C.lin(lat, pre + "latent_wv_bcast").view(p, 4, 4, 32)
-    out = ops.latent_broadcast(qb, kb, vb, plan.window_pos)
-    w = w + C.lin(out.view(-1, 128), pre + "latent_wo_bcast")
-    return w, g
-
-
-def _block(C: _Ctx, i: int, plan: Plan, b: Batch, s, w, g, c, ws_rows, sw_rows, update_stones: bool):
-    pre = f"blocks.{i}."
-    p, max_t = plan.n_pos, plan.max_t
-    # §5.1 windows <- stones
-    x = C.lin(C.ln(s, pre + "ln_ws_s"), pre + "u")
-    agg = ops.run_reduce(x, b.inc_stone, plan.inc_win_ptr, plan.n_w, torch.float32)
-    agg = agg + ws_rows
-    w = w + C.pair_mlp(C.ln(w, pre + "ln_ws_w"), agg, pre + "mlp_w")
-    # §5.1b cell stage
-    w, c = _cell_stage(C, pre, plan, s, w, c)
-    # §5.2 stones <- windows (fp32 aggregate)
-    y = C.lin(C.ln(w, pre + "ln_sw_w"), pre + "v")
-    agg = ops.run_reduce(y, plan.run_window, plan.inc_stone_ptr, plan.n_s, torch.float32) + sw_rows
-    s = s + C.pair_mlp(C.ln(s, pre + "ln_sw_s"), agg, pre + "mlp_s")
-    # §5.3 attention over [latents; stones]
-    rows = torch.zeros(p * max_t, 128, dtype=torch.float32, device=s.device)
-    rows.index_copy_(0, plan.global_slot, g.reshape(-1, 128))
-    rows.index_copy_(0, b.stone_slot, s)
-    z = C.ln(rows.view(p, max_t, 128), pre + "ln_attn")
-    k = C.lin(z, pre + "wk").view(p, max_t, 4, 32).transpose(1, 2)
-    v = C.lin(z, pre + "wv").view(p, max_t, 4, 32).transpose(1, 2)
-    if update_stones:
-        q = C.lin(z, pre + "wq").view(p, max_t, 4, 32).transpose(1, 2)
-        out = ops.stone_attention(q, k, v, plan.seq_lens)
-        out = C.lin(out.transpose(1, 2).reshape(p, max_t, 128), pre + "wo").view(p * max_t, 128)
-        s = s + out.index_select(0, b.stone_slot)
-        g = g + out.index_select(0, plan.global_slot).view(p, GLOBAL_ROWS, 128)
-    else:
-        # the last block reads only the four latent rows: fp32 four-query read
-        q = C.lin(z[:, :GLOBAL_ROWS], pre + "wq", True).view(p, GLOBAL_ROWS, 4, 32).transpose(1, 2)
-        sc = torch.matmul(q, k.float().transpose(-1, -2)) / math.sqrt(32)
-        sc = sc.masked_fill(~b.attn_valid[:, None, None, :], -torch.inf)
-        read = torch.matmul(sc.softmax(-1), v.float())
-        g = g + C.lin(read.transpose(1, 2).reshape(p, GLOBAL_ROWS, 128), pre + "wo", True)
-    # §5.4 latent cycle
-    w, g = _latent_cycle(C, pre, plan, w, g)
-    # FFN over [stones; latents]
-    gf = g.reshape(-1, 128)
-    if update_stones:
-        s = s + C.lin(F.relu(C.lin(C.ln(s, pre + "ln_ffn"), pre + "ffn.0")), pre + "ffn.2")
-    gf = gf + C.lin(F.relu(C.lin(C.ln(gf, pre + "ln_ffn"), pre + "ffn.0", True)), pre + "ffn.2", True)
-    return s, w, gf.view(p, GLOBAL_ROWS, 128), c
-
-
-# ----------------------------------------------------------------- public entry points
 
 
 def _plan_for(model, batch: Batch) -> tuple[Batch, Plan]:
@@ -328,72 +284,175 @@ def _plan_for(model, batch: Batch) -> tuple[Batch, Plan]:
     return b, plan
 
 
+# ----------------------------------------------------------------- blocks
+
+FL = ops.fused_linear
+
+
+def _proj(W, key, x, **kw):
+    return FL(x, W[key + ".w"], W[key + ".b"], layer_norm=True, **kw)
+
+
+def _resid(W, key, x, out, **kw):
+    return FL(x, W[key + ".w"], W[key + ".b"], out=out, residual=True, **kw)
+
+
+def _cell_stage(W, P, pb, plan: Plan, s, w, c):
+    n_c, n_w = plan.n_c, plan.n_w
+    q = _proj(W, pb + "cr_q", c)
+    kv = _proj(W, pb + "cr_kv", w)
+    read = ops.cell_attention(q, kv[:, :128], kv[:, 128:], P[pb + "cr_bias"], P[pb + "cr_vclass.weight"],
+                              plan.cell_ptr, plan.edge_window, plan.edge_class)
+    _resid(W, pb + "cr_o", read.view(n_c, 128), c)
+    q = _proj(W, pb + "rad_q", c)
+    kv = _proj(W, pb + "rad_kv", s)
+    read = ops.cell_attention(q, kv[:, :128], kv[:, 128:], P[pb + "radius_bias"], P[pb + "radius_vclass.weight"],
+                              plan.radius_ptr, plan.radius_src, plan.radius_class)
+    _resid(W, pb + "rad_o", read.view(n_c, 128), c)
+    q = _proj(W, pb + "wr_q", w)
+    kv = _proj(W, pb + "wr_kv", c)
+    back = ops.cell_attention(q, kv[:, :128], kv[:, 128:], P[pb + "wr_bias"], None,
+                              plan.win_ptr, plan.edge_wcell, plan.edge_wclass)
+    _resid(W, pb + "wr_o", back.view(n_w, 128), w)
+
+
+def _latent_cycle(W, P, pb, plan: Plan, w, g2):
+    p = plan.n_pos
+    q = _proj(W, pb + "lq_read", g2)
+    kv = _proj(W, pb + "lkv_read", w)
+    read = ops.latent_read(q.view(p, 4, 4, 32), kv[:, :128], kv[:, 128:], plan.layout_offsets, plan.layout_order)
+    _resid(W, pb + "lo_read", read.view(p * 4, 128), g2)
+    # 4 x 4 latent self-mix, fp32 (all four slots live; model.py:516-526)
+    z = F.layer_norm(g2, (128,), P[pb + "latent_ln_mix.weight"], P[pb + "latent_ln_mix.bias"], 1e-5)
+    qm = F.linear(z, P[pb + "latent_wq_mix.weight"], P[pb + "latent_wq_mix.bias"]).view(p, 4, 4, 32).transpose(1, 2)
+    km = F.linear(z, P[pb + "latent_wk_mix.weight"]).view(p, 4, 4, 32).transpose(1, 2)
+    vm = F.linear(z, P[pb + "latent_wv_mix.weight"], P[pb + "latent_wv_mix.bias"]).view(p, 4, 4, 32).transpose(1, 2)
+    att = (torch.matmul(qm, km.transpose(-1, -2)) / math.sqrt(32)).softmax(-1)
+    mixed = torch.matmul(att, vm).transpose(1, 2).reshape(p * 4, 128)
+    g2.add_(F.linear(mixed, P[pb + "latent_wo_mix.weight"], P[pb + "latent_wo_mix.bias"]))
+    qb = _proj(W, pb + "lq_bcast", w)
+    kvb = _proj(W, pb + "lkv_bcast", g2)
+    out = ops.latent_broadcast_rows(qb, kvb, plan.window_pos)
+    _resid(W, pb + "lo_bcast", out.view(plan.n_w, 128), w)
+
+
+def _block(W, P, i: int, plan: Plan, b: Batch, sg, w, c, sw_all, update_stones: bool):
+    pb = f"blocks.{i}."
+    p, max_t, n_s = plan.n_pos, plan.max_t, plan.n_s
+    s = sg[:n_s]
+    g2 = sg[n_s:]
+    # §5.1 windows <- stones: w += mlp_w(LN w, agg + class term)
+    x = _proj(W, pb + "u", s)
+    agg = ops.run_reduce(x, b.inc_stone, plan.inc_win_ptr, plan.n_w, HALF)
+    FL(w, W[pb + "mlp_w1.w"], W[pb + "mlp_w1.b"], layer_norm=True, x2=agg, w2=W[pb + "mlp_w2.w"],
+       add2=W[pb + "ws_tab"], add2_rows=b.window_feat, relu=True, w3=W[pb + "mlp_w3.w"], b3=W[pb + "mlp_w3.b"],
+       out=w, residual=True)
+    # §5.1b cell stage
+    _cell_stage(W, P, pb, plan, s, w, c)
+    # §5.2 stones <- windows: s += mlp_s(LN s, agg + class term)
+    y = _proj(W, pb + "v", w)
+    agg = ops.run_reduce(y, plan.run_window, plan.inc_stone_ptr, n_s, F32)
+    FL(s, W[pb + "mlp_s1.w"], W[pb + "mlp_s1.b"], layer_norm=True, x2=agg, w2=W[pb + "mlp_s2.w"],
+       add1=sw_all[:, 128 * i:128 * (i + 1)], relu=True, w3=W[pb + "mlp_s3.w"], b3=W[pb + "mlp_s3.b"],
+       out=s, residual=True)
+    # §5.3 attention over [latents; stones], block-diagonal per position
+    qkv = _proj(W, pb + "qkv", sg, x_rows=plan.attn_src)  # (P*T, 384)
+
+    def view(j):
+        return qkv[:, 128 * j:128 * (j + 1)].view(p, max_t, 4, 32).transpose(1, 2)
+
+    if update_stones:
+        rows = torch.empty((p, max_t, 4, 32), dtype=HALF, device=w.device)
+        ops.stone_attention(view(0), view(1), view(2), plan.seq_lens, out=rows.transpose(1, 2))
+        _resid(W, pb + "attn_o", rows.view(p * max_t, 128), sg, x_rows=plan.attn_back)
+    else:
+        # last block: only the four latent rows are read downstream (fp32 read)
+        q = view(0)[:, :, :GLOBAL_ROWS].float()
+        sc = torch.matmul(q, view(1).float().transpose(-1, -2)) / math.sqrt(32)
+        sc = sc.masked_fill(~b.attn_valid[:, None, None, :], -torch.inf)
+        read = torch.matmul(sc.softmax(-1), view(2).float()).transpose(1, 2).reshape(p * GLOBAL_ROWS, 128)
+        _resid(W, pb + "attn_o", read.contiguous(), g2)
+    # §5.4 latent cycle
+    _latent_cycle(W, P, pb, plan, w, g2)
+    # FFN over [stones; latents] (latents only in the last block)
+    tgt = sg if update_stones else g2
+    FL(tgt, W[pb + "ffn1.w"], W[pb + "ffn1.b"], layer_norm=True, relu=True, w3=W[pb + "ffn2.w"],
+       b3=W[pb + "ffn2.b"], out=tgt, residual=True)
+
+
+# ----------------------------------------------------------------- public entry points
+
+
 @torch.no_grad()
-def trunk(model, b: Batch):
+def trunk(model, batch: Batch):
+    """(ln_out(w) fp32 (N_w, H), mean_j ln_out(g) fp32 (P, H), ln_out(c) fp16 (N_c, H))."""
     _supported(model)
-    C = _Ctx(model)
+    W = _prepared(model)
+    P = dict(model.named_parameters())
     cfg = model.cfg
-    b, plan = _plan_for(model, b)
-    P = C.p
-    s = P["stone_table.weight"].index_select(0, b.stone_own)
+    b, plan = _plan_for(model, batch)
+    n_s, p = plan.n_s, plan.n_pos
+    # residual streams: s and g share one buffer so the attention and FFN
+    # launches cover both with one row range
+    sg = torch.empty((n_s + p * GLOBAL_ROWS, 128), dtype=F32, device=b.stone_own.device)
+    sg[:n_s] = P["stone_table.weight"].index_select(0, b.stone_own)
+    sg[n_s:] = (P["latent_base"][None] + P["token_moves.weight"].index_select(0, b.moves_idx)[:, None]).reshape(-1, 128)
     w = P["window_table.weight"].index_select(0, b.window_feat)
-    g = P["latent_base"][None] + P["token_moves.weight"].index_select(0, b.moves_idx)[:, None]
     near = P["cell_nearest_table.weight"].index_select(0, b.cell_nearest)
-    c = torch.where(plan.covered_mask[:, None], P["cell_base"][None, :], near)
-    # every block's class terms at once (model.py:937-955)
-    ws_tables = torch.cat([P[f"blocks.{i}.e_ws.weight"] for i in range(cfg.blocks)], 1)
-    ws_all = (model.pattern_counts @ ws_tables).index_select(0, b.window_feat)
-    sw_all = ops.run_reduce(
-        torch.cat([P[f"blocks.{i}.e_sw.weight"] for i in range(cfg.blocks)], 1),
-        plan.run_class, plan.inc_stone_ptr, plan.n_s, torch.float32,
-    )
+    c = torch.where(plan.covered_mask[:, None], P["cell_base"][None, :], near).contiguous()
+    sw_all = ops.run_reduce(W["sw_all"], plan.run_class, plan.inc_stone_ptr, n_s, F32)
     for i in range(cfg.blocks):
-        sl = slice(i * 128, (i + 1) * 128)
-        s, w, g, c = _block(C, i, plan, b, s, w, g, c, ws_all[:, sl], sw_all[:, sl], i + 1 < cfg.blocks)
-    return C.ln(w, "ln_out"), C.ln(g, "ln_out").mean(dim=1), C.ln(c, "ln_out")
+        _block(W, P, i, plan, b, sg, w, c, sw_all, i + 1 < cfg.blocks)
+    g = sg[n_s:].view(p, GLOBAL_ROWS, 128)
+    w_out = ops.layer_norm(w, P["ln_out.weight"], P["ln_out.bias"], F32)
+    g_out = F.layer_norm(g, (128,), P["ln_out.weight"], P["ln_out.bias"], 1e-5).mean(dim=1)
+    cells = ops.layer_norm(c, P["ln_out.weight"], P["ln_out.bias"], HALF)
+    return w_out, g_out, cells
 
 
 @torch.no_grad()
-def value_head(model, w: Tensor, g: Tensor, b: Batch):
+def value_head(model, w: Tensor, g: Tensor, batch: Batch):
     _supported(model)
-    C = _Ctx(model)
-    b, _ = _plan_for(model, b)
-    p, max_w = b.value_valid.shape
-    rows = torch.zeros(p * max_w, 128, dtype=torch.float32, device=w.device)
-    rows.index_copy_(0, torch.arange(p, device=w.device) * max_w, C.ln(g, "ln_value"))
-    if b.window_slot.numel():
-        rows.index_copy_(0, b.window_slot, C.ln(w, "ln_value"))
-    kv = rows.view(p, max_w, 128)
-    sc = torch.matmul(kv, C.p["value_queries"].float().t()).transpose(1, 2) / math.sqrt(128)
-    sc = sc.masked_fill(~b.value_valid[:, None, :], torch.finfo(torch.float32).min)
-    r = torch.matmul(sc.softmax(-1), kv)
-    hidden = F.relu(C.lin(r.reshape(p, -1), "mlp_v.0", True))
-    logits = C.lin(hidden, "mlp_v.2", True)
+    P = dict(model.named_parameters())
+    b, plan = _plan_for(model, batch)
+    r = ops.value_read(g.float().contiguous(), w.float().contiguous(), plan.layout_offsets, plan.layout_order,
+                       P["ln_value.weight"], P["ln_value.bias"], P["value_queries"])
+    hidden = F.relu(F.linear(r.reshape(plan.n_pos, -1), P["mlp_v.0.weight"], P["mlp_v.0.bias"]))
+    logits = F.linear(hidden, P["mlp_v.2.weight"], P["mlp_v.2.bias"])
     dist = logits.softmax(-1)
     return dist @ model.bin_centers, dist, logits
 
 
 @torch.no_grad()
-def cell_head_logits(model, w: Tensor, g: Tensor, cells: Tensor, b: Batch):
+def _head_rows(model, w: Tensor, g: Tensor, cells: Tensor, batch: Batch) -> Tensor:
+    """(N_c, 16) fp32: column 0 the policy logit, 1..3 the critic logits."""
     _supported(model)
     if cells is None:
         raise ValueError("cell state is on but the trunk's cell rows were not passed to the decoder")
-    C = _Ctx(model)
-    b, plan = _plan_for(model, b)
+    W = _prepared(model)
+    P = dict(model.named_parameters())
+    b, plan = _plan_for(model, batch)
     n_c = plan.n_c
-    pre_w = C.lin(w, "act_proj")
-    empty_rows = F.relu(C.p["act_empty_base"].float() + C.p["act_table.weight"].index_select(0, model.act_empty_classes).float())
-    acts = ops.row_encode(pre_w, C.p["act_table.weight"], b.dec_window, b.act_class, plan.dec_cell_ptr, n_c,
+    pre = FL(w.float().contiguous(), W["act_proj.w"], W["act_proj.b"])  # act_proj(w), fp16
+    empty_rows = F.relu(P["act_empty_base"] + P["act_table.weight"].index_select(0, model.act_empty_classes))
+    acts = ops.row_encode(pre, P["act_table.weight"], b.dec_window, b.act_class, plan.dec_cell_ptr, n_c,
                           b.act_empty, empty_rows)
-    extra = ops.run_reduce(torch.cat((C.p["e_pw.weight"], C.p["e_qw.weight"]), 1), b.dec_class,
-                           plan.dec_cell_ptr, n_c, torch.float32)
-    rows = _half(cells)
-    acts_bf = _half(acts)
-    outs = []
-    for proj, ext, mlp, sl in (("p", "p_act", "mlp_p", slice(0, 128)), ("q", "q_act", "mlp_q", slice(128, 256))):
-        g_half = C.lin(g, mlp + ".lin_b", True)
-        base = C.lin(rows, proj, True) + C.lin(acts_bf, ext, True) + extra[:, sl]
-        pre = C.lin(base, mlp + ".lin_a", True)
-        hid = F.relu(pre + g_half.index_select(0, b.cell_pos))
-        outs.append(C.lin(hid, mlp + ".out", True))
-    return outs[0].squeeze(-1), outs[1]
+    extra = ops.run_reduce(W["head_tab"], b.dec_class, plan.dec_cell_ptr, n_c, F32)  # (N_c, 256)
+    g_half = F.linear(g.float(), W["glin_b"]).contiguous()  # (P, 256)
+    x = cells if cells.dtype in (HALF, F32) else cells.float()
+    return FL(x.contiguous(), W["head1.w"], W["head1.b"], x2=acts, w2=W["head2.w"], add1=extra, add2=g_half,
+              add2_rows=b.cell_pos, relu=True, w3=W["head3.w"], b3=W["head3.b"], out_dtype=F32)
+
+
+@torch.no_grad()
+def cell_head_logits(model, w: Tensor, g: Tensor, cells: Tensor, batch: Batch):
+    rows = _head_rows(model, w, g, cells, batch)
+    return rows[:, 0].contiguous(), rows[:, 1:4]
+
+
+@torch.no_grad()
+def cell_heads(model, w: Tensor, g: Tensor, cells: Tensor, batch: Batch, mass_floor: float):
+    rows = _head_rows(model, w, g, cells, batch)
+    b, _ = _plan_for(model, batch)
+    q_values, q_score = ops.compose_q(rows[:, 1:], b.legal_offsets, mass_floor)
+    return rows[:, 0].contiguous(), q_score, q_values

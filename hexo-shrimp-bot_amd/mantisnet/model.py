@@ -158,13 +158,14 @@ def compose_q(critic_logits: Tensor) -> Tensor:
 
 
 def compose_acting_q(critic_logits: Tensor, offsets: Tensor, mass_floor: float) -> Tensor:
-    """Q over the position's floored maximum committed mass (model.py:203-220)."""
-    from .segments import segment_ids, segment_max
+    """Q over the position's floored maximum committed mass (model.py:203-220),
+    one HIP launch (per-position softmax, segment max, scale)."""
+    from . import ops
 
-    p_pos, p_neg = return_mass(critic_logits)
-    seg = segment_ids(offsets)
-    scale = segment_max(p_pos + p_neg, seg, offsets.shape[0] - 1).clamp(min=mass_floor)
-    return (p_pos - p_neg) / scale.index_select(0, seg)
+    critic = critic_logits.float()
+    if critic.stride(-1) != 1:
+        critic = critic.contiguous()
+    return ops.compose_q(critic, offsets.to(critic.device), mass_floor)[1]
 
 
 def _mlp(d_in: int, d_hidden: int, d_out: int) -> nn.Sequential:
@@ -368,12 +369,10 @@ class MantisNet(nn.Module):
         return fwd.value_head(self, w, g, batch)
 
     def cell_heads(self, w, g, cells, batch: Batch, mass_floor: float):
-        policy_logits, critic_logits = self.cell_head_logits(w, g, cells, batch)
-        return (
-            policy_logits,
-            compose_acting_q(critic_logits, batch.legal_offsets.to(critic_logits.device), mass_floor),
-            compose_q(critic_logits),
-        )
+        """Policy logits, acting scores and values in legal order (model.py:1141-1158)."""
+        from . import forward as fwd
+
+        return fwd.cell_heads(self, w, g, cells, batch, mass_floor)
 
     def forward(self, batch: Batch, mass_floor: float) -> ModelOutput:
         """Every head (model.py:1185-1200)."""

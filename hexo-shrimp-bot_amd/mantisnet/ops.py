@@ -89,6 +89,28 @@ def _check(status: int, what: str) -> None:
         raise RuntimeError(f"{what}: HIP launch failed (status {status})")
 
 
+def _rows128(t: Tensor, name: str) -> tuple[Tensor, int]:
+    """A tensor of 128-wide rows — (n, 128) or (n, ..., 128 split as heads x
+    dims) — as (tensor, row stride); copies only when the rows themselves are
+    not dense or aligned."""
+    n = t.shape[0]
+    if t.numel() != n * 128:
+        raise ValueError(f"{name} must hold 128 features per row")
+    if t.ndim > 2:
+        dense = all(t.stride(i) == t.stride(i + 1) * t.shape[i + 1] for i in range(1, t.ndim - 1))
+        if not dense or t.stride(-1) != 1:
+            t = t.contiguous()
+        ld = t.stride(0)
+    else:
+        if t.stride(1) != 1:
+            t = t.contiguous()
+        ld = t.stride(0)
+    if n and (ld % 8 or ld < 128 or t.data_ptr() % 16):
+        t = t.reshape(n, 128).contiguous()
+        ld = 128
+    return t, ld
+
+
 def _i64(t: Tensor, name: str) -> Tensor:
     if t.dtype != torch.int64:
         raise ValueError(f"{name} must have dtype int64")
@@ -142,20 +164,26 @@ def run_reduce(values: Tensor, gather: Tensor, ptr: Tensor, n_dest: int, out_dty
 
 def cell_attention(q: Tensor, k: Tensor, v: Tensor, bias: Tensor, vcls: Tensor | None,
                    seg_ptr: Tensor, src: Tensor, cls: Tensor, stats: bool = False):
-    """Typed segment attention; returns fp32 (n_q, heads, hd) [and m, l]."""
+    """Typed segment attention; q/k/v are 128-wide rows (heads=4 x hd=32),
+    possibly strided views; returns fp32 (n_q, 4, 32) [and m, l]."""
     dev = _on_gpu(q, k, v, bias, vcls, seg_ptr, src, cls)
-    if q.ndim != 3 or k.shape != v.shape or q.shape[1:] != k.shape[1:]:
-        raise ValueError("q and k/v must share (heads, head_dim)")
-    n_q, heads, hd = q.shape
+    heads, hd = 4, 32
+    n_q = q.shape[0]
+    if q.shape[-2:] not in ((heads, hd),) and q.shape[-1] != 128:
+        raise ValueError("q rows must be heads x head_dim = 4 x 32")
+    if k.shape != v.shape:
+        raise ValueError("k and v must have one shape")
     if bias.ndim != 2 or bias.shape[0] != heads:
         raise ValueError("bias must have shape (heads, classes)")
     if seg_ptr.numel() != n_q + 1:
         raise ValueError("seg_ptr must have one entry per query row plus one")
     if src.shape != cls.shape or src.ndim != 1:
         raise ValueError("the edge views must have one length")
-    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
     if k.dtype != q.dtype or v.dtype != q.dtype:
         raise ValueError("q, k and v must have one dtype")
+    q, ldq = _rows128(q, "q")
+    k, ldk = _rows128(k, "k")
+    v, ldv = _rows128(v, "v")
     bias = bias.float().contiguous()
     if vcls is not None:
         if vcls.shape != (bias.shape[1], heads * hd):
@@ -168,7 +196,7 @@ def cell_attention(q: Tensor, k: Tensor, v: Tensor, bias: Tensor, vcls: Tensor |
     if n_q:
         _check(
             _lib().mantis_cell_attention(
-                _ptr(q), _ptr(k), _ptr(v), _dt(q), _ptr(bias), bias.shape[1], _ptr(vcls),
+                _ptr(q), _ptr(k), _ptr(v), _dt(q), ldq, ldk, ldv, _ptr(bias), bias.shape[1], _ptr(vcls),
                 _ptr(seg_ptr), _ptr(src), _ptr(cls), src.numel(), n_q, k.shape[0], heads, hd,
                 _ptr(out), _ptr(m), _ptr(l), _ptr(error_flag(dev)), _stream(),
             ),
@@ -178,24 +206,29 @@ def cell_attention(q: Tensor, k: Tensor, v: Tensor, bias: Tensor, vcls: Tensor |
 
 
 def latent_read(q: Tensor, k: Tensor, v: Tensor, offsets: Tensor, order: Tensor, stats: bool = False):
+    """Four latent queries per position over its windows; q (P, 4, ...) and
+    k/v 128-wide rows; returns fp32 (P, 4, 4, 32) [and m, l]."""
     dev = _on_gpu(q, k, v, offsets, order)
-    if q.ndim != 4 or q.shape[1] != 4:
-        raise ValueError("read q must have shape (P, 4, heads, head_dim)")
-    if k.ndim != 3 or k.shape != v.shape or q.shape[2:] != k.shape[1:]:
-        raise ValueError("read k and v must share shape (N_w, heads, head_dim)")
-    p, _, heads, hd = q.shape
-    if offsets.numel() != p + 1 or order.numel() != k.shape[0]:
+    p = q.shape[0]
+    if q.numel() != p * 4 * 128:
+        raise ValueError("read q must have shape (P, 4, heads, head_dim) with heads x head_dim = 128")
+    if k.shape != v.shape:
+        raise ValueError("read k and v must share one shape")
+    n_w = k.shape[0]
+    if offsets.numel() != p + 1 or order.numel() != n_w:
         raise ValueError("offsets must be (P + 1,) and order (N_w,)")
-    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    q2, ldq = _rows128(q.reshape(p * 4, -1) if q.is_contiguous() else q.contiguous().view(p * 4, -1), "q")
+    k, ldk = _rows128(k, "k")
+    v, ldv = _rows128(v, "v")
     offsets, order = _i64(offsets, "offsets"), _i64(order, "order")
-    out = torch.empty(q.shape, dtype=torch.float32, device=dev)
-    m = torch.empty(q.shape[:-1], dtype=torch.float32, device=dev) if stats else None
-    l = torch.empty(q.shape[:-1], dtype=torch.float32, device=dev) if stats else None
+    out = torch.empty((p, 4, 4, 32), dtype=torch.float32, device=dev)
+    m = torch.empty((p, 4, 4), dtype=torch.float32, device=dev) if stats else None
+    l = torch.empty((p, 4, 4), dtype=torch.float32, device=dev) if stats else None
     if p:
         _check(
             _lib().mantis_latent_read(
-                _ptr(q), _ptr(k), _ptr(v), _dt(q), _ptr(offsets), _ptr(order), p, k.shape[0],
-                heads, hd, _ptr(out), _ptr(m), _ptr(l), _ptr(error_flag(dev)), _stream(),
+                _ptr(q2), _ptr(k), _ptr(v), _dt(q2), ldq, ldk, ldv, _ptr(offsets), _ptr(order), p, n_w,
+                4, 32, _ptr(out), _ptr(m), _ptr(l), _ptr(error_flag(dev)), _stream(),
             ),
             "latent_read",
         )
@@ -203,26 +236,50 @@ def latent_read(q: Tensor, k: Tensor, v: Tensor, offsets: Tensor, order: Tensor,
 
 
 def latent_broadcast(q: Tensor, k: Tensor, v: Tensor, window_pos: Tensor, stats: bool = False):
+    """Every window attends over its position's four latents; q 128-wide
+    window rows, k/v (P, 4, ...) latent rows; returns fp32 (N_w, 4, 32)."""
     dev = _on_gpu(q, k, v, window_pos)
-    if q.ndim != 3 or k.ndim != 4 or k.shape != v.shape or k.shape[1] != 4 or q.shape[1:] != k.shape[2:]:
-        raise ValueError("broadcast q must be (N_w, heads, hd) and k/v (P, 4, heads, hd)")
-    if window_pos.numel() != q.shape[0]:
+    n_w = q.shape[0]
+    p = k.shape[0]
+    if k.shape != v.shape or k.numel() != p * 4 * 128:
+        raise ValueError("broadcast k/v must have shape (P, 4, heads, head_dim)")
+    if window_pos.numel() != n_w:
         raise ValueError("window_pos must have one entry per window")
-    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    q, ldq = _rows128(q, "q")
+    k2, ldk = _rows128(k.reshape(p * 4, -1) if k.is_contiguous() else k.contiguous().view(p * 4, -1), "k")
+    v2, ldv = _rows128(v.reshape(p * 4, -1) if v.is_contiguous() else v.contiguous().view(p * 4, -1), "v")
     window_pos = _i64(window_pos, "window_pos")
-    n_w, heads, hd = q.shape
-    out = torch.empty(q.shape, dtype=torch.float32, device=dev)
-    m = torch.empty(q.shape[:-1], dtype=torch.float32, device=dev) if stats else None
-    l = torch.empty(q.shape[:-1], dtype=torch.float32, device=dev) if stats else None
+    out = torch.empty((n_w, 4, 32), dtype=torch.float32, device=dev)
+    m = torch.empty((n_w, 4), dtype=torch.float32, device=dev) if stats else None
+    l = torch.empty((n_w, 4), dtype=torch.float32, device=dev) if stats else None
     if n_w:
         _check(
             _lib().mantis_latent_broadcast(
-                _ptr(q), _ptr(k), _ptr(v), _dt(q), _ptr(window_pos), k.shape[0], n_w, heads, hd,
+                _ptr(q), _ptr(k2), _ptr(v2), _dt(q), ldq, ldk, ldv, _ptr(window_pos), p, n_w, 4, 32,
                 _ptr(out), _ptr(m), _ptr(l), _ptr(error_flag(dev)), _stream(),
             ),
             "latent_broadcast",
         )
     return (out, m, l) if stats else out
+
+
+def latent_broadcast_rows(q: Tensor, kv: Tensor, window_pos: Tensor) -> Tensor:
+    """Broadcast with k/v the two 128-wide halves of (P*4, 256) rows."""
+    dev = _on_gpu(q, kv, window_pos)
+    n_w = q.shape[0]
+    p = kv.shape[0] // 4
+    q, ldq = _rows128(q, "q")
+    out = torch.empty((n_w, 4, 32), dtype=torch.float32, device=dev)
+    if n_w:
+        _check(
+            _lib().mantis_latent_broadcast(
+                _ptr(q), kv.data_ptr(), kv[:, 128:].data_ptr(), _dt(q), ldq, kv.stride(0), kv.stride(0),
+                _ptr(_i64(window_pos, "window_pos")), p, n_w, 4, 32, _ptr(out), None, None,
+                _ptr(error_flag(dev)), _stream(),
+            ),
+            "latent_broadcast",
+        )
+    return out
 
 
 def row_encode(pre: Tensor, table: Tensor, window: Tensor, cls: Tensor, cell_ptr: Tensor,
@@ -257,7 +314,8 @@ def _strides(t: Tensor):
     return (ctypes.c_int64 * 4)(*t.stride())
 
 
-def stone_attention(q: Tensor, k: Tensor, v: Tensor, seq_lens: Tensor, want_lse: bool = False):
+def stone_attention(q: Tensor, k: Tensor, v: Tensor, seq_lens: Tensor, want_lse: bool = False,
+                    out: Tensor | None = None):
     """Ragged attention over each position's live prefix (16-bit MFMA).
     q/k/v (P, A, T, hd) fp16 or bf16 with arbitrary row strides; the output
     has ``empty_like(q)`` strides."""
@@ -274,9 +332,12 @@ def stone_attention(q: Tensor, k: Tensor, v: Tensor, seq_lens: Tensor, want_lse:
     fix = lambda x: x if x.stride(3) == 1 and all(s % 8 == 0 for s in x.stride()[:3]) else x.contiguous()  # noqa: E731
     q, k, v = fix(q), fix(k), fix(v)
     seq_lens = seq_lens.contiguous()
-    out = torch.empty_like(q)
-    if out.stride(3) != 1:
-        out = torch.empty(q.shape, dtype=q.dtype, device=dev)
+    if out is None:
+        out = torch.empty_like(q)
+        if out.stride(3) != 1 or any(s % 8 for s in out.stride()[:3]):
+            out = torch.empty(q.shape, dtype=q.dtype, device=dev)
+    elif out.shape != q.shape or out.dtype != q.dtype or out.stride(3) != 1 or any(s % 8 for s in out.stride()[:3]):
+        raise ValueError("out must match q's shape and dtype with 16-byte aligned rows")
     lse = torch.empty((p, heads, t), dtype=torch.float32, device=dev) if want_lse else None
     qs, ks, vs, os_ = _strides(q), _strides(k), _strides(v), _strides(out)
     _check(
@@ -287,6 +348,113 @@ def stone_attention(q: Tensor, k: Tensor, v: Tensor, seq_lens: Tensor, want_lse:
         "stone_attention",
     )
     return (out, lse) if want_lse else out
+
+
+# ----------------------------------------------------------------- fused row GEMM
+
+_MODES = {torch.float16: 0, torch.float32: 1}
+
+
+def fused_linear(x: Tensor, w1: Tensor, b1: Tensor | None = None, *, layer_norm: bool = False,
+                 x_rows: Tensor | None = None, x2: Tensor | None = None, w2: Tensor | None = None,
+                 add1: Tensor | None = None, add2: Tensor | None = None, add2_rows: Tensor | None = None,
+                 relu: bool = False, w3: Tensor | None = None, b3: Tensor | None = None,
+                 out: Tensor | None = None, out_dtype: torch.dtype = torch.float16,
+                 residual: bool = False) -> Tensor:
+    """One fused row-GEMM launch (see mantis_fused_linear in
+    include/mantis_hip.h).  ``residual=True`` adds into ``out`` (fp32, in
+    place); otherwise a new (m, width) tensor of ``out_dtype`` is returned."""
+    dev = _on_gpu(x, w1, b1, x_rows, x2, w2, add1, add2, add2_rows, w3, b3, out)
+    if x.ndim != 2 or x.shape[1] < 128 or x.stride(1) != 1:
+        raise ValueError("x must be (n, >=128) rows with unit column stride")
+    m = x_rows.numel() if x_rows is not None else x.shape[0]
+    n1 = w1.shape[0]
+    width = w3.shape[0] if w3 is not None else n1
+    for t, name in ((w1, "w1"), (w2, "w2"), (w3, "w3")):
+        if t is not None and (t.dtype != torch.float16 or not t.is_contiguous()):
+            raise ValueError(f"{name} must be contiguous float16")
+    if w1.shape[1] != 128 or (w2 is not None and w2.shape != w1.shape):
+        raise ValueError("w1/w2 must be (n1, 128)")
+    if w3 is not None and w3.shape[1] != n1:
+        raise ValueError("w3 must be (n3, n1)")
+    for t, n, name in ((b1, n1, "b1"), (b3, width, "b3")):
+        if t is not None and (t.shape != (n,) or t.dtype != torch.float32 or not t.is_contiguous()):
+            raise ValueError(f"{name} must be a contiguous fp32 vector of {n}")
+    if add1 is not None and add1.shape[1] != n1:
+        raise ValueError("add1 must be (m, n1)")
+    if add2_rows is not None and add2_rows.numel() != m:
+        raise ValueError("add2_rows must have one entry per row")
+    if residual:
+        if out is None or out.dtype != torch.float32 or out.shape[0] != m or out.stride(1) != 1:
+            raise ValueError("a residual launch needs an fp32 (m, width) out tensor")
+        mode = 2
+    else:
+        mode = _MODES[out_dtype]
+        if out is None:
+            out = torch.empty((m, width), dtype=out_dtype, device=dev)
+    if x2 is not None and (x2.shape[0] != m or x2.stride(1) != 1):
+        raise ValueError("x2 must be (m, 128) rows")
+    if add1 is not None and (add1.shape[0] != m or add1.stride(1) != 1 or add1.dtype != torch.float32):
+        raise ValueError("add1 must be fp32 (m, n1) rows")
+    if add2 is not None and (not add2.is_contiguous() or add2.shape[1] != n1 or add2.dtype != torch.float32):
+        raise ValueError("add2 must be a contiguous fp32 (groups, n1) table")
+    x_rows = None if x_rows is None else _i64(x_rows, "x_rows")
+    add2_rows = None if add2_rows is None else _i64(add2_rows, "add2_rows")
+    st = _lib().mantis_fused_linear(
+        _ptr(x), _dt(x), x.stride(0), _ptr(x_rows), x.shape[0], m, int(layer_norm),
+        _ptr(x2), _dt(x2) if x2 is not None else 0, x2.stride(0) if x2 is not None else 0,
+        _ptr(w1), _ptr(w2), _ptr(b1), n1, _ptr(add1), add1.stride(0) if add1 is not None else 0,
+        _ptr(add2), _ptr(add2_rows), add2.shape[0] if add2 is not None else 0, int(relu),
+        _ptr(w3), _ptr(b3), width if w3 is not None else 0, mode, _ptr(out), out.stride(0),
+        _ptr(error_flag(dev)), _stream(),
+    )
+    _check(st, "fused_linear")
+    return out
+
+
+def layer_norm(x: Tensor, gamma: Tensor, beta: Tensor, out_dtype: torch.dtype = torch.float32) -> Tensor:
+    dev = _on_gpu(x, gamma, beta)
+    if x.ndim != 2 or x.shape[1] != 128 or x.dtype != torch.float32 or x.stride(1) != 1:
+        raise ValueError("layer_norm takes fp32 (n, 128) rows")
+    out = torch.empty(x.shape, dtype=out_dtype, device=dev)
+    _check(_lib().mantis_layer_norm(_ptr(x), x.stride(0), x.shape[0], _ptr(gamma.float().contiguous()),
+                                    _ptr(beta.float().contiguous()), _ptr(out), _MODES_LN[out_dtype], 128,
+                                    _stream()), "layer_norm")
+    return out
+
+
+_MODES_LN = {torch.float32: 0, torch.float16: 2}
+
+
+def value_read(token: Tensor, rows: Tensor, offsets: Tensor, order: Tensor, gamma: Tensor, beta: Tensor,
+               queries: Tensor) -> Tensor:
+    dev = _on_gpu(token, rows, offsets, order, gamma, beta, queries)
+    p = token.shape[0]
+    for t in (token, rows):
+        if t.dtype != torch.float32 or not t.is_contiguous() or t.shape[-1] != 128:
+            raise ValueError("value_read takes contiguous fp32 rows of 128")
+    if queries.shape != (4, 128):
+        raise ValueError("value_read takes four 128-wide queries")
+    out = torch.empty((p, 4, 128), dtype=torch.float32, device=dev)
+    _check(_lib().mantis_value_read(_ptr(token), _ptr(rows), rows.shape[0], _ptr(_i64(offsets, "offsets")),
+                                    _ptr(_i64(order, "order")), p, _ptr(gamma.float().contiguous()),
+                                    _ptr(beta.float().contiguous()), _ptr(queries.float().contiguous()), 4,
+                                    _ptr(out), _ptr(error_flag(dev)), _stream()), "value_read")
+    return out
+
+
+def compose_q(critic: Tensor, offsets: Tensor, mass_floor: float) -> tuple[Tensor, Tensor]:
+    """(q_values, q_score) from fp32 critic logits rows (n, >=3)."""
+    dev = _on_gpu(critic, offsets)
+    if critic.dtype != torch.float32 or critic.stride(1) != 1 or critic.shape[1] < 3:
+        raise ValueError("critic logits must be fp32 rows of at least 3")
+    n = critic.shape[0]
+    qv = torch.empty(n, dtype=torch.float32, device=dev)
+    qs = torch.empty(n, dtype=torch.float32, device=dev)
+    _check(_lib().mantis_compose_q(_ptr(critic), critic.stride(0), _ptr(_i64(offsets, "offsets")),
+                                   offsets.numel() - 1, n, float(mass_floor), _ptr(qv), _ptr(qs), _stream()),
+           "compose_q")
+    return qv, qs
 
 
 # ----------------------------------------------------------------- hex message passing

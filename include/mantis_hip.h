@@ -67,14 +67,15 @@ int32_t mantis_run_reduce(const void* values, int32_t values_dtype, int64_t n_sr
  *   score[e, a] = q[row, a, :] . k[src[e], a, :] / sqrt(hd) + bias[a, cls[e]]
  *   out[row, a, :] = sum_e softmax_e(score) (v[src[e], a, :] + vcls[cls[e], a, :])
  * fp32 scores, softmax and sums; a row without entries reads zero.  q/k/v are
- * (n, heads, hd) in `dtype`; bias (heads, n_classes) fp32; vcls
+ * (n, heads*hd) rows in `dtype` with row strides ldq/ldk/ldv (elements,
+ * multiples of 8; k and v may be the two halves of one (n, 256) buffer); bias (heads, n_classes) fp32; vcls
  * (n_classes, heads*hd) fp32 or NULL; out (n_q, heads, hd) fp32; m/l
  * (n_q, heads) fp32 softmax statistics or NULL.  Supports heads*hd == 128.
  * Replaces mantisnet::cell_attention / cell_attention_plain
  * (python/mantisnet/mantisnet/cell_latents.py:213-285, 834-1001).
  */
 int32_t mantis_cell_attention(const void* q, const void* k, const void* v, int32_t dtype,
-                              const float* bias, int64_t n_classes, const float* vcls,
+                              int64_t ldq, int64_t ldk, int64_t ldv, const float* bias, int64_t n_classes, const float* vcls,
                               const int64_t* seg_ptr, const int64_t* src, const int64_t* cls,
                               int64_t n_entries, int64_t n_q, int64_t n_k, int32_t heads,
                               int32_t hd, float* out,
@@ -83,23 +84,25 @@ int32_t mantis_cell_attention(const void* q, const void* k, const void* v, int32
 /*
  * Window-latent read: four latent queries per position attend over the
  * position's windows (rows order[offsets[p]:offsets[p+1]] of k/v).  q is
- * (P, 4, heads, hd), k/v (n_w, heads, hd) in `dtype`; out (P, 4, heads, hd)
+ * (P*4, heads*hd), k/v (n_w, heads*hd) rows in `dtype` with row strides
+ * ldq/ldk/ldv; out (P, 4, heads, hd)
  * fp32; m/l (P, 4, heads) or NULL.  An empty position reads zero.
  * Replaces mantisnet::window_latent_read (window_latents.py:224-268, 553-577).
  */
 int32_t mantis_latent_read(const void* q, const void* k, const void* v, int32_t dtype,
-                           const int64_t* offsets, const int64_t* order, int64_t n_pos,
+                           int64_t ldq, int64_t ldk, int64_t ldv, const int64_t* offsets, const int64_t* order, int64_t n_pos,
                            int64_t n_w, int32_t heads, int32_t hd, float* out, float* m, float* l,
                            int32_t* err_flag, void* stream);
 
 /*
  * Window-latent broadcast: every window attends over its position's four
- * latents.  q (n_w, heads, hd), k/v (P, 4, heads, hd) in `dtype`; out
+ * latents.  q (n_w, heads*hd), k/v (P*4, heads*hd) rows in `dtype` with
+ * row strides ldq/ldk/ldv; out
  * (n_w, heads, hd) fp32; m/l (n_w, heads) or NULL.
  * Replaces mantisnet::window_latent_broadcast (window_latents.py:350-381, 622-654).
  */
 int32_t mantis_latent_broadcast(const void* q, const void* k, const void* v, int32_t dtype,
-                                const int64_t* window_pos, int64_t n_pos, int64_t n_w,
+                                int64_t ldq, int64_t ldk, int64_t ldv, const int64_t* window_pos, int64_t n_pos, int64_t n_w,
                                 int32_t heads, int32_t hd, float* out, float* m, float* l,
                                 int32_t* err_flag, void* stream);
 
@@ -137,6 +140,66 @@ int32_t mantis_stone_attention(const void* q, const int64_t* q_strides, const vo
                                int32_t dtype, const int32_t* seq_lens, int64_t n_pos,
                                int32_t heads, int64_t t, int32_t hd, void* out,
                                const int64_t* out_strides, float* lse, void* stream);
+
+/*
+ * Fused row GEMM over rows of K = 128 features (LayerNorm -> Linear ->
+ * ReLU -> Linear -> residual, replacing the reference's nn.LayerNorm /
+ * nn.Linear / _PairMlp / FFN chains, python/mantisnet/mantisnet/model.py:
+ * 246-260, 570-580, 608-619, 681-691, 1065-1091):
+ *   x-hat[i] = layer_norm ? (x[r] - mean) / sqrt(var + 1e-5) : x[r]
+ *              with r = x_rows ? x_rows[i] : i (r == -1 reads a zero row)
+ *   h[i]     = x-hat[i] W1^T (+ x2[i] W2^T) + b1 (+ add1[i]) (+ add2[add2_rows[i]])
+ *   h[i]     = relu(h[i])                      if relu
+ *   y[i]     = h[i] W3^T + b3                  if w3 (n3 outputs), else h[i]
+ *   out[i]   = y[i] (out_mode 0: fp16 store, 1: fp32 store) or out[i] += y[i]
+ *              (out_mode 2: fp32 residual, in place)
+ * The LayerNorm affine is folded into W1/b1 by the caller.  x is fp32 or
+ * fp16 (rows of stride ldx), x2 fp32 or fp16; W1/W2 (n1, 128), W3 (n3, n1)
+ * fp16 row-major; b1/add1/add2 (.., n1) and b3 (n3) fp32.  fp16 MFMA with
+ * fp32 accumulation and fp32 LayerNorm statistics.  Supported shapes: the
+ * projection (n1 in 128/256/384, fp16 out), the residual projection
+ * (n1 = 128, add), the two-layer residual MLPs (n1 = 128 with x2, n1 = 256
+ * without) and the two-layer head (n1 = 256 with x2, fp32 out).
+ */
+int32_t mantis_fused_linear(const void* x, int32_t x_dtype, int64_t ldx, const int64_t* x_rows,
+                            int64_t n_x, int64_t m, int32_t layer_norm, const void* x2,
+                            int32_t x2_dtype, int64_t ldx2, const void* w1, const void* w2,
+                            const float* b1, int32_t n1, const float* add1, int64_t ld_add1,
+                            const float* add2, const int64_t* add2_rows, int64_t n_add2,
+                            int32_t relu, const void* w3, const float* b3, int32_t n3,
+                            int32_t out_mode, void* out, int64_t ldo, int32_t* err_flag,
+                            void* stream);
+
+/*
+ * Row LayerNorm over rows of 128 features (eps 1e-5, biased variance), fp32
+ * in, fp32 or fp16 out (nn.LayerNorm as the trunk's shared ln_out applies
+ * it, python/mantisnet/mantisnet/model.py:973-985).
+ */
+int32_t mantis_layer_norm(const float* x, int64_t ldx, int64_t m, const float* gamma,
+                          const float* beta, void* out, int32_t out_dtype, int64_t ldo,
+                          void* stream);
+
+/*
+ * Value-head readout (model.py:1160-1183): per position p, n_queries (= 4)
+ * learned 128-wide queries attend with scale 1/sqrt(128) over
+ * [LN(token[p]); LN(rows[order[offsets[p]:offsets[p+1]]])], LN with
+ * gamma/beta computed on the fly; out (n_pos, 4, 128) fp32 holds the
+ * softmax-weighted sums.  fp32 throughout.
+ */
+int32_t mantis_value_read(const float* token, const float* rows, int64_t n_rows,
+                          const int64_t* offsets, const int64_t* order, int64_t n_pos,
+                          const float* gamma, const float* beta, const float* queries,
+                          int32_t n_queries, float* out, int32_t* err_flag, void* stream);
+
+/*
+ * Critic composition (model.py:177-220, segments.py:24-31): for the critic
+ * logits (n_cells, 3) at row stride ld, q_values = p_pos - p_neg of the
+ * per-cell softmax and q_score = q_values / max(mass_floor, max over the
+ * position's cells of p_pos + p_neg), positions given by CSR offsets.
+ */
+int32_t mantis_compose_q(const float* critic, int64_t ld, const int64_t* offsets, int64_t n_pos,
+                         int64_t n_cells, float mass_floor, float* q_values, float* q_score,
+                         void* stream);
 
 /*
  * Six-neighbour table of ragged cell graphs: graph j's cells are

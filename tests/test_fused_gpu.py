@@ -1,0 +1,176 @@
+"""Fused row-GEMM, LayerNorm, value readout and critic composition kernels
+against closed-form fp32 references (GPU).
+
+The references evaluate the same arithmetic in fp32 on the CPU from the
+same fp16-valued operands (weights, normalised inputs, stage-1 activations
+rounded to fp16 where the kernel feeds MFMA), so the tolerance covers fp32
+summation order plus one fp16 rounding of the output.
+"""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from mantisnet import ops
+
+pytestmark = pytest.mark.gpu
+H16 = torch.float16
+
+
+def _g(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def _w(n, k, gen, scale=None):
+    return (torch.randn(n, k, generator=gen) / math.sqrt(k) if scale is None else scale * torch.randn(n, k, generator=gen)).to(H16)
+
+
+def _ln(x):
+    mu = x.mean(-1, keepdim=True)
+    var = ((x - mu) ** 2).mean(-1, keepdim=True)
+    return (x - mu) / torch.sqrt(var + 1e-5)
+
+
+def _h(x):
+    return x.to(H16).float()
+
+
+@pytest.mark.parametrize("n1", [128, 256, 384])
+def test_projection_with_layer_norm(device, n1):
+    gen = _g(n1)
+    m = 1000
+    x = 3 * torch.randn(m, 128, generator=gen) + 1
+    w = _w(n1, 128, gen)
+    b = 0.1 * torch.randn(n1, generator=gen)
+    rows = torch.randint(-1, m, (777,), generator=gen)
+    out = ops.fused_linear(x.to(device), w.to(device), b.to(device), layer_norm=True, x_rows=rows.to(device))
+    ops.raise_on_device_error(device)
+    xs = torch.where(rows[:, None] >= 0, x[rows.clamp(min=0)], torch.zeros(1, 128))
+    exp = _h(_ln(xs)) @ w.float().t() + b
+    torch.testing.assert_close(out.float().cpu(), exp, rtol=2e-3, atol=2e-3)
+
+
+@pytest.mark.parametrize("xdt", [torch.float32, H16])
+def test_residual_projection(device, xdt):
+    gen = _g(2)
+    m = 513
+    x = torch.randn(m, 128, generator=gen).to(xdt)
+    w = _w(128, 128, gen)
+    b = 0.1 * torch.randn(128, generator=gen)
+    r = torch.randn(m, 128, generator=gen)
+    out = r.to(device)
+    ops.fused_linear(x.to(device), w.to(device), b.to(device), out=out, residual=True)
+    exp = r + _h(x.float()) @ w.float().t() + b
+    torch.testing.assert_close(out.cpu(), exp, rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("x2dt", [torch.float32, H16])
+def test_pair_mlp_residual(device, x2dt):
+    gen = _g(3)
+    m, groups = 700, 37
+    r = torch.randn(m, 128, generator=gen)
+    x2 = torch.randn(m, 128, generator=gen).to(x2dt)
+    w1, w2, w3 = _w(128, 128, gen), _w(128, 128, gen), _w(128, 128, gen)
+    b1, b3 = 0.1 * torch.randn(128, generator=gen), 0.1 * torch.randn(128, generator=gen)
+    add2 = torch.randn(groups, 128, generator=gen)
+    rows = torch.randint(0, groups, (m,), generator=gen)
+    out = r.to(device)
+    ops.fused_linear(out, w1.to(device), b1.to(device), layer_norm=True, x2=x2.to(device), w2=w2.to(device),
+                     add2=add2.to(device), add2_rows=rows.to(device), relu=True, w3=w3.to(device), b3=b3.to(device),
+                     out=out, residual=True)
+    ops.raise_on_device_error(device)
+    hid = F.relu(_h(_ln(r)) @ w1.float().t() + _h(x2.float()) @ w2.float().t() + b1 + add2[rows])
+    exp = r + _h(hid) @ w3.float().t() + b3
+    torch.testing.assert_close(out.cpu(), exp, rtol=2e-3, atol=2e-3)
+
+
+def test_ffn_residual_with_add1(device):
+    gen = _g(4)
+    m = 300
+    r = torch.randn(m, 128, generator=gen)
+    w1, w3 = _w(256, 128, gen), _w(128, 256, gen)
+    b1, b3 = 0.1 * torch.randn(256, generator=gen), 0.1 * torch.randn(128, generator=gen)
+    out = r.to(device)
+    ops.fused_linear(out, w1.to(device), b1.to(device), layer_norm=True, relu=True, w3=w3.to(device),
+                     b3=b3.to(device), out=out, residual=True)
+    hid = F.relu(_h(_ln(r)) @ w1.float().t() + b1)
+    exp = r + _h(hid) @ w3.float().t() + b3
+    torch.testing.assert_close(out.cpu(), exp, rtol=2e-3, atol=2e-3)
+
+
+def test_two_layer_head(device):
+    gen = _g(5)
+    m, p = 1000, 9
+    x = torch.randn(m, 128, generator=gen).to(H16)
+    x2 = 4 * torch.randn(m, 128, generator=gen).relu()
+    w1, w2 = _w(256, 128, gen), _w(256, 128, gen)
+    w3 = torch.zeros(16, 256)
+    w3[0, :128] = 0.05 * torch.randn(128, generator=gen)
+    w3[1:4, 128:] = 0.05 * torch.randn(3, 128, generator=gen)
+    w3 = w3.to(H16)
+    b1, b3 = 0.1 * torch.randn(256, generator=gen), 0.1 * torch.randn(16, generator=gen)
+    add1 = torch.randn(m, 256, generator=gen)
+    add2 = torch.randn(p, 256, generator=gen)
+    rows = torch.randint(0, p, (m,), generator=gen)
+    out = ops.fused_linear(x.to(device), w1.to(device), b1.to(device), x2=x2.to(device), w2=w2.to(device),
+                           add1=add1.to(device), add2=add2.to(device), add2_rows=rows.to(device), relu=True,
+                           w3=w3.to(device), b3=b3.to(device), out_dtype=torch.float32)
+    hid = F.relu(x.float() @ w1.float().t() + _h(x2) @ w2.float().t() + b1 + add1 + add2[rows])
+    exp = _h(hid) @ w3.float().t() + b3
+    torch.testing.assert_close(out.cpu(), exp, rtol=2e-3, atol=2e-3)
+
+
+def test_layer_norm_rows(device):
+    gen = _g(6)
+    x = 5 * torch.randn(333, 128, generator=gen) - 2
+    g, b = 1 + 0.1 * torch.randn(128, generator=gen), 0.1 * torch.randn(128, generator=gen)
+    out = ops.layer_norm(x.to(device), g.to(device), b.to(device))
+    torch.testing.assert_close(out.cpu(), F.layer_norm(x, (128,), g, b, 1e-5), rtol=1e-5, atol=1e-5)
+    out16 = ops.layer_norm(x.to(device), g.to(device), b.to(device), H16)
+    torch.testing.assert_close(out16.float().cpu(), F.layer_norm(x, (128,), g, b, 1e-5), rtol=2e-3, atol=2e-3)
+
+
+def test_value_read_matches_padded_masked_softmax(device):
+    gen = _g(7)
+    counts = torch.tensor([3, 0, 40, 17, 1])
+    p = counts.numel()
+    rows = torch.randn(int(counts.sum()), 128, generator=gen)
+    token = torch.randn(p, 128, generator=gen)
+    g, b = 1 + 0.1 * torch.randn(128, generator=gen), 0.1 * torch.randn(128, generator=gen)
+    queries = 0.5 * torch.randn(4, 128, generator=gen)
+    offsets = torch.cat([torch.zeros(1, dtype=torch.long), counts.cumsum(0)])
+    order = torch.arange(rows.shape[0])
+    out = ops.value_read(token.to(device), rows.to(device), offsets.to(device), order.to(device), g.to(device),
+                         b.to(device), queries.to(device))
+    ops.raise_on_device_error(device)
+    # the reference's padded formulation (model.py:1160-1183)
+    max_w = int(counts.max()) + 1
+    pad = torch.zeros(p, max_w, 128)
+    valid = torch.zeros(p, max_w, dtype=torch.bool)
+    for i in range(p):
+        pad[i, 0] = F.layer_norm(token[i], (128,), g, b, 1e-5)
+        seg = rows[offsets[i]:offsets[i + 1]]
+        pad[i, 1:1 + len(seg)] = F.layer_norm(seg, (128,), g, b, 1e-5)
+        valid[i, :1 + len(seg)] = True
+    sc = torch.einsum("qh,pth->pqt", queries, pad) / math.sqrt(128)
+    sc = sc.masked_fill(~valid[:, None, :], torch.finfo(torch.float32).min)
+    exp = torch.einsum("pqt,pth->pqh", sc.softmax(-1), pad)
+    torch.testing.assert_close(out.cpu(), exp, rtol=1e-4, atol=1e-5)
+
+
+def test_compose_q_matches_reference_formula(device):
+    gen = _g(8)
+    counts = torch.tensor([5, 1, 300, 17])
+    offsets = torch.cat([torch.zeros(1, dtype=torch.long), counts.cumsum(0)])
+    logits = 2 * torch.randn(int(counts.sum()), 16, generator=gen)
+    qv, qs = ops.compose_q(logits[:, 1:].to(device), offsets.to(device), 0.2)
+    pr = logits[:, 1:4].softmax(-1)
+    q = pr[:, 0] - pr[:, 1]
+    seg = torch.repeat_interleave(torch.arange(4), counts)
+    mass = torch.zeros(4).index_reduce_(0, seg, pr[:, 0] + pr[:, 1], "amax", include_self=False)
+    torch.testing.assert_close(qv.cpu(), q, rtol=1e-5, atol=1e-6)
+    torch.testing.assert_close(qs.cpu(), q / mass.clamp(min=0.2)[seg], rtol=1e-5, atol=1e-6)
