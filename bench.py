@@ -1,0 +1,277 @@
+"""MantisNet leaf-evaluation benchmark on one MI355X.
+
+Workload: the production MantisNet configuration
+(cell_latents + cell_nodes, 5,195,909 parameters, seeded perturbed init)
+evaluating B = 512 seeded random legal positions of 40-120 stones.  One step
+is one full forward — trunk, value head, both cell heads and the acting-Q
+composition, with the per-forward index tables derived inside the step —
+over the device-resident batch.  The reference's own method is followed
+(python/mantisnet/mantisnet/lab/bench.py:124-142): warm-up forwards, then
+device-synchronised timed forwards; positions/s = B / (seconds per step).
+
+The JSON line also carries
+* ``roofline`` — the dominant kernel of the timed steps (largest summed
+  duration among the traced kernels), its algorithmic bytes per launch over
+  its average HIP-event duration on the launching stream, against 8 TB/s;
+* ``cpu_baseline`` — the CPU fp32 oracle (oracle/model_ref.py, the
+  restatement of the reference's CPU formulations) timed on a bounded sample
+  of the same batch on this host;
+* ``attention`` / ``message_passing`` — the isolated-kernel configurations
+  (configs[1] ragged attention, configs[2] hex message passing) with MFMA and
+  HBM fractions.
+
+Only one GPU is supported: ``--gpus N`` with N > 1 exits with a message.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (str(ROOT), str(ROOT / "hexo-shrimp-bot_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBPS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
+
+
+def _args():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--batch", type=int, default=512)
+    ap.add_argument("--config", type=int, default=4, choices=(4, 5))
+    ap.add_argument("--cpu-sample", type=int, default=32, help="positions in the CPU-baseline sample")
+    ap.add_argument("--cpu-reps", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-isolated", action="store_true", help="skip the isolated attention/message-passing lines")
+    return ap.parse_args()
+
+
+def _log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def _traffic():
+    """Measured HBM bytes per launch of the dominant kernel, from the
+    committed rocprofv3 PMC summary (FETCH_SIZE + WRITE_SIZE, calibrated)."""
+    f = ROOT / "profiles" / "traffic.json"
+    if f.exists():
+        try:
+            return json.loads(f.read_text())
+        except ValueError:
+            return None
+    return None
+
+
+def isolated_attention(torch, ops, dev, reps=20):
+    """B=256 sequences, L ~ U{64..512}, 8 heads, hd 32, N(0,1)."""
+    import numpy as np
+
+    rng = np.random.default_rng([2, 0])
+    b, h, t = 256, 8, 512
+    lens = torch.from_numpy(rng.integers(64, 513, b).astype(np.int32))
+    gen = torch.Generator(device="cpu").manual_seed(2)
+    res = {}
+    for dtype, name in ((torch.float16, "fp16"), (torch.bfloat16, "bf16")):
+        qkv = [torch.randn(b, t, h, 32, generator=gen).to(dtype).to(dev).transpose(1, 2) for _ in range(3)]
+        sl = lens.to(dev)
+        ops.register_seq_lens(sl)
+        for _ in range(3):
+            ops.stone_attention(*qkv, sl)
+        with ops.trace("stone_attention") as tr:
+            for _ in range(reps):
+                ops.stone_attention(*qkv, sl)
+        s = tr.summary()["stone_attention"]
+        res[name] = {
+            "avg_us": round(s["avg_us"], 2),
+            "tflops": round(s["tflops"], 1),
+            "mfma_frac": round(s["tflops"] / MFMA_F16_PEAK_TFLOPS, 4),
+            "gbps": round(s["gbps"], 1),
+            "gflop_per_launch": round(s["flops_per_launch"] / 1e9, 2),
+            "mb_per_launch": round(s["bytes_per_launch"] / 1e6, 1),
+        }
+    return {"config": "B=256, L~U{64..512}, H=8, hd=32, key-padding mask, no bias (warm L2/MALL)", **res}
+
+
+def isolated_message_passing(torch, ops, dev, reps=20):
+    """256 graphs = first N_j ~ U{64..512} legal cells of seeded
+    40-120-stone positions; 6-neighbour sum and mean, Linear(128,128), bf16."""
+    import numpy as np
+
+    from mantisnet import builder, synthetic
+
+    games = synthetic.random_games(3, 256)
+    cells, sizes = [], []
+    for j, g in enumerate(games):
+        legal, _, _ = builder.legal_moves(g)
+        n = int(np.random.default_rng([3, j, 1]).integers(64, 513))
+        cells.append(legal[:n])
+        sizes.append(min(n, len(legal)))
+    qr = torch.from_numpy(np.concatenate(cells).astype(np.int32)).to(dev)
+    gptr = torch.from_numpy(np.concatenate([[0], np.cumsum(sizes)]).astype(np.int64)).to(dev)
+    n = qr.shape[0]
+    gen = torch.Generator(device="cpu").manual_seed(3)
+    x = torch.randn(n, 128, generator=gen).to(torch.bfloat16).to(dev)
+    w = (torch.randn(128, 128, generator=gen) / math.sqrt(128)).to(dev)
+    bias = (0.02 * torch.randn(128, generator=gen)).to(dev)
+    nbr = ops.hex_neighbours(qr, gptr)
+    for _ in range(3):
+        ops.hex_aggregate_linear(x, nbr, w, bias)
+    with ops.trace("hex_aggregate_linear") as tr:
+        for _ in range(reps):
+            ops.hex_aggregate_linear(x, nbr, w, bias)
+    s = tr.summary()["hex_aggregate_linear"]
+    ops.raise_on_device_error(dev)
+    return {
+        "config": f"256 graphs, N={n} cells, 6 axial neighbours, sum+mean then Linear(128,128), bf16",
+        "avg_us": round(s["avg_us"], 2),
+        "gbps": round(s["gbps"], 1),
+        "hbm_frac": round(s["gbps"] / HBM_PEAK_GBPS, 4),
+        "mb_per_launch": round(s["bytes_per_launch"] / 1e6, 2),
+    }
+
+
+def cpu_baseline(torch, net, games, sample: int, reps: int):
+    """The CPU fp32 oracle on the first `sample` positions of the batch."""
+    from mantisnet import collate_positions
+    from oracle.compare import oracle_forward
+
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    sub = collate_positions(games[:sample])
+    oracle_forward(net, sub, 0.2)  # warm-up
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        oracle_forward(net, sub, 0.2)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {
+        "value": round(sample / med, 2),
+        "unit": "positions/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{sample} of the {len(games)} benchmark positions, fp32 oracle forward, median of {reps}",
+    }
+
+
+def main() -> int:
+    args = _args()
+    if args.gpus != 1:
+        print(
+            f"bench.py measures one MI355X only; --gpus {args.gpus} is not supported "
+            "(the MantisNet leaf evaluation shards by position with no exchange; see DESIGN.md)",
+            file=sys.stderr,
+        )
+        return 2
+    import torch
+
+    from mantisnet import PRODUCTION, MantisNet, collate_positions, ops, synthetic
+
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    net = MantisNet(PRODUCTION)
+    net.load_state_dict(synthetic.perturbed_state_dict(net, seed=0))
+    net = net.to(dev).eval()
+
+    t0 = time.perf_counter()
+    games = synthetic.random_games(args.config, args.batch)
+    t_gen = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    batch = collate_positions(games)
+    t_enc = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    bd = batch.to(dev)
+    torch.cuda.synchronize()
+    t_h2d = time.perf_counter() - t0
+    _log(f"config {args.config}: B={args.batch} cells={batch.n_cells} windows={batch.window_feat.numel()} "
+         f"stones={batch.stone_own.numel()} (generate {t_gen:.2f}s, encode {t_enc:.2f}s, h2d {t_h2d:.3f}s)")
+
+    with torch.no_grad():
+        for _ in range(args.warmup):
+            net(bd, 0.2)
+        torch.cuda.synchronize()
+        ops.raise_on_device_error(dev)
+        _log(f"warm-up done ({args.warmup} steps)")
+        traced = ("cell_attention", "fused_linear_proj", "fused_linear_residual", "fused_linear_mlp")
+        per_step = []
+        with ops.trace(*traced) as tr:
+            torch.cuda.synchronize()
+            t_start = time.perf_counter()
+            for _ in range(args.steps):
+                s0 = time.perf_counter()
+                net(bd, 0.2)
+                torch.cuda.synchronize()
+                per_step.append(time.perf_counter() - s0)
+            torch.cuda.synchronize()
+            elapsed = time.perf_counter() - t_start
+        kernels = tr.summary()
+        ops.raise_on_device_error(dev)
+    ms = 1e3 * elapsed / args.steps
+    value = args.batch * args.steps / elapsed
+    _log(f"timed {args.steps} steps: {ms:.3f} ms/step, {value:.1f} positions/s")
+
+    dom_name, dom = max(kernels.items(), key=lambda kv: kv[1]["total_ms"])
+    traffic = _traffic()
+    roofline = {
+        "kernel": dom_name,
+        "bound": "hbm",
+        "achieved": round(dom["gbps"], 1),
+        "peak": HBM_PEAK_GBPS,
+        "unit": "GB/s",
+        "frac": round(dom["gbps"] / HBM_PEAK_GBPS, 4),
+        "traffic": (traffic or {}).get(dom_name),
+        "avg_us": round(dom["avg_us"], 2),
+        "launches_per_step": dom["launches"] // args.steps,
+        "share_of_step": round(dom["total_ms"] / args.steps / ms, 4),
+    }
+    line = {
+        "metric": "positions evaluated/sec (MantisNet fwd, B=512)",
+        "value": round(value, 2),
+        "unit": "positions/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "median_ms_per_step": round(1e3 * statistics.median(per_step), 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic: seeded random legal positions, seeded perturbed random-init weights",
+        "config": {
+            "workload": f"MantisNet production forward (cell_nodes), configs[{args.config - 1}]",
+            "batch_positions": args.batch,
+            "stones": "40-120" if args.config == 4 else "150-250",
+            "cells": int(batch.n_cells),
+            "windows": int(batch.window_feat.numel()),
+            "encode_s": round(t_enc, 3),
+            "h2d_s": round(t_h2d, 4),
+        },
+        "roofline": roofline,
+        "kernels": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in kernels.items()},
+    }
+    if not args.no_isolated:
+        _log("isolated attention (configs[1])")
+        line["attention"] = isolated_attention(torch, ops, dev)
+        _log("isolated message passing (configs[2])")
+        line["message_passing"] = isolated_message_passing(torch, ops, dev)
+    if not args.no_cpu_baseline:
+        _log(f"cpu baseline: oracle on {args.cpu_sample} positions x {args.cpu_reps}")
+        line["cpu_baseline"] = cpu_baseline(torch, net, games, args.cpu_sample, args.cpu_reps)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -387,10 +387,14 @@ def _block(W, P, i: int, plan: Plan, b: Batch, sg, w, c, sw_all, update_stones: 
 def trunk(model, batch: Batch):
     """(ln_out(w) fp32 (N_w, H), mean_j ln_out(g) fp32 (P, H), ln_out(c) fp16 (N_c, H))."""
     _supported(model)
+    b, plan = _plan_for(model, batch)
+    return _trunk(model, b, plan)
+
+
+def _trunk(model, b: Batch, plan: Plan):
     W = _prepared(model)
     P = dict(model.named_parameters())
     cfg = model.cfg
-    b, plan = _plan_for(model, batch)
     n_s, p = plan.n_s, plan.n_pos
     # residual streams: s and g share one buffer so the attention and FFN
     # launches cover both with one row range
@@ -413,8 +417,12 @@ def trunk(model, batch: Batch):
 @torch.no_grad()
 def value_head(model, w: Tensor, g: Tensor, batch: Batch):
     _supported(model)
-    P = dict(model.named_parameters())
     b, plan = _plan_for(model, batch)
+    return _value_head(model, w, g, b, plan)
+
+
+def _value_head(model, w: Tensor, g: Tensor, b: Batch, plan: Plan):
+    P = dict(model.named_parameters())
     r = ops.value_read(g.float().contiguous(), w.float().contiguous(), plan.layout_offsets, plan.layout_order,
                        P["ln_value.weight"], P["ln_value.bias"], P["value_queries"])
     hidden = F.relu(F.linear(r.reshape(plan.n_pos, -1), P["mlp_v.0.weight"], P["mlp_v.0.bias"]))
@@ -423,15 +431,12 @@ def value_head(model, w: Tensor, g: Tensor, batch: Batch):
     return dist @ model.bin_centers, dist, logits
 
 
-@torch.no_grad()
-def _head_rows(model, w: Tensor, g: Tensor, cells: Tensor, batch: Batch) -> Tensor:
+def _head_rows(model, w: Tensor, g: Tensor, cells: Tensor, b: Batch, plan: Plan) -> Tensor:
     """(N_c, 16) fp32: column 0 the policy logit, 1..3 the critic logits."""
-    _supported(model)
     if cells is None:
         raise ValueError("cell state is on but the trunk's cell rows were not passed to the decoder")
     W = _prepared(model)
     P = dict(model.named_parameters())
-    b, plan = _plan_for(model, batch)
     n_c = plan.n_c
     pre = FL(w.float().contiguous(), W["act_proj.w"], W["act_proj.b"])  # act_proj(w), fp16
     empty_rows = F.relu(P["act_empty_base"] + P["act_table.weight"].index_select(0, model.act_empty_classes))
@@ -446,13 +451,36 @@ def _head_rows(model, w: Tensor, g: Tensor, cells: Tensor, batch: Batch) -> Tens
 
 @torch.no_grad()
 def cell_head_logits(model, w: Tensor, g: Tensor, cells: Tensor, batch: Batch):
-    rows = _head_rows(model, w, g, cells, batch)
+    _supported(model)
+    b, plan = _plan_for(model, batch)
+    rows = _head_rows(model, w, g, cells, b, plan)
     return rows[:, 0].contiguous(), rows[:, 1:4]
 
 
 @torch.no_grad()
 def cell_heads(model, w: Tensor, g: Tensor, cells: Tensor, batch: Batch, mass_floor: float):
-    rows = _head_rows(model, w, g, cells, batch)
-    b, _ = _plan_for(model, batch)
+    _supported(model)
+    b, plan = _plan_for(model, batch)
+    return _cell_heads(model, w, g, cells, b, plan, mass_floor)
+
+
+def _cell_heads(model, w, g, cells, b: Batch, plan: Plan, mass_floor: float):
+    rows = _head_rows(model, w, g, cells, b, plan)
     q_values, q_score = ops.compose_q(rows[:, 1:], b.legal_offsets, mass_floor)
     return rows[:, 0].contiguous(), q_score, q_values
+
+
+@torch.no_grad()
+def forward(model, batch: Batch, mass_floor: float):
+    """Every head of one evaluation (model.py:1185-1200).  The index plan is
+    derived inside every call, as the reference derives its tables inside
+    every forward; nothing is cached between calls except the prepared
+    weights."""
+    _supported(model)
+    dev = next(model.parameters()).device
+    b = batch if batch.stone_own.device == dev else batch.to(dev)
+    plan = make_plan(model, b)
+    w, g, cells = _trunk(model, b, plan)
+    value, value_dist, value_logits = _value_head(model, w, g, b, plan)
+    policy, q_score, q_values = _cell_heads(model, w, g, cells, b, plan, mass_floor)
+    return policy, q_score, q_values, value, value_dist, value_logits

@@ -376,9 +376,9 @@ class MantisNet(nn.Module):
 
     def forward(self, batch: Batch, mass_floor: float) -> ModelOutput:
         """Every head (model.py:1185-1200)."""
-        w, g, cells = self.trunk(batch)
-        value, value_dist, value_logits = self.value_head(w, g, batch)
-        policy_logits, q_score, q_values = self.cell_heads(w, g, cells, batch, mass_floor)
+        from . import forward as fwd
+
+        policy_logits, q_score, q_values, value, value_dist, value_logits = fwd.forward(self, batch, mass_floor)
         return ModelOutput(
             policy_logits=policy_logits,
             q_score=q_score,

@@ -26,6 +26,69 @@ def _lib():
     return _native.hip()
 
 
+# ----------------------------------------------------------------- launch tracing
+
+_TRACE = None
+
+
+class trace:
+    """Time chosen kernels with HIP events on the launching stream.
+
+    ``with ops.trace("cell_attention") as t: ...`` records, for every launch
+    of a named kernel inside the block, a start/end event pair plus the
+    launch's algorithmic bytes and flops; ``t.summary()`` synchronises and
+    returns per-kernel launch counts, average duration and achieved rates.
+    """
+
+    def __init__(self, *names: str):
+        self.names = set(names)
+        self.records: dict[str, list] = {n: [] for n in names}
+
+    def __enter__(self):
+        global _TRACE
+        _TRACE = self
+        return self
+
+    def __exit__(self, *exc):
+        global _TRACE
+        _TRACE = None
+        return False
+
+    def summary(self) -> dict:
+        torch.cuda.synchronize()
+        out = {}
+        for name, recs in self.records.items():
+            if not recs:
+                continue
+            ms = [a.elapsed_time(b) for a, b, _, _ in recs]
+            total_ms = sum(ms)
+            nbytes = sum(r[2] for r in recs)
+            flops = sum(r[3] for r in recs)
+            out[name] = {
+                "launches": len(recs),
+                "total_ms": total_ms,
+                "avg_us": 1e3 * total_ms / len(recs),
+                "bytes_per_launch": nbytes / len(recs),
+                "flops_per_launch": flops / len(recs),
+                "gbps": nbytes / (total_ms * 1e-3) / 1e9 if total_ms else 0.0,
+                "tflops": flops / (total_ms * 1e-3) / 1e12 if total_ms else 0.0,
+            }
+        return out
+
+
+def _launch(name: str, nbytes: float, flops: float, fn):
+    t = _TRACE
+    if t is None or name not in t.names:
+        return fn()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    res = fn()
+    e1.record()
+    t.records[name].append((e0, e1, float(nbytes), float(flops)))
+    return res
+
+
 def _dt(t: Tensor) -> int:
     if t.dtype == torch.bfloat16:
         return BF16
@@ -194,14 +257,20 @@ def cell_attention(q: Tensor, k: Tensor, v: Tensor, bias: Tensor, vcls: Tensor |
     m = torch.empty((n_q, heads), dtype=torch.float32, device=dev) if stats else None
     l = torch.empty((n_q, heads), dtype=torch.float32, device=dev) if stats else None
     if n_q:
-        _check(
+        e = src.numel()
+        # algorithmic bytes: q and out rows once, each source's k and v rows
+        # once, the CSR pointers and the per-edge (src, cls) indices
+        nbytes = n_q * (128 * q.element_size() + out[0].numel() * 4 + 8) + e * 16 + \
+            k.shape[0] * 128 * (k.element_size() + v.element_size())
+        flops = e * 4 * 128 * 2  # score dot + weighted value sum per edge and head
+        _launch("cell_attention", nbytes, flops, lambda: _check(
             _lib().mantis_cell_attention(
                 _ptr(q), _ptr(k), _ptr(v), _dt(q), ldq, ldk, ldv, _ptr(bias), bias.shape[1], _ptr(vcls),
-                _ptr(seg_ptr), _ptr(src), _ptr(cls), src.numel(), n_q, k.shape[0], heads, hd,
+                _ptr(seg_ptr), _ptr(src), _ptr(cls), e, n_q, k.shape[0], heads, hd,
                 _ptr(out), _ptr(m), _ptr(l), _ptr(error_flag(dev)), _stream(),
             ),
             "cell_attention",
-        )
+        ))
     return (out, m, l) if stats else out
 
 
@@ -310,6 +379,15 @@ def row_encode(pre: Tensor, table: Tensor, window: Tensor, cls: Tensor, cell_ptr
     return out
 
 
+# host copies of seq_lens registered by a benchmark, so a traced launch can
+# count its algorithmic work without a device synchronisation
+_STONE_LENS: dict[int, Tensor] = {}
+
+
+def register_seq_lens(seq_lens: Tensor) -> None:
+    _STONE_LENS[seq_lens.data_ptr()] = seq_lens.detach().cpu().to(torch.int64)
+
+
 def _strides(t: Tensor):
     return (ctypes.c_int64 * 4)(*t.stride())
 
@@ -340,13 +418,19 @@ def stone_attention(q: Tensor, k: Tensor, v: Tensor, seq_lens: Tensor, want_lse:
         raise ValueError("out must match q's shape and dtype with 16-byte aligned rows")
     lse = torch.empty((p, heads, t), dtype=torch.float32, device=dev) if want_lse else None
     qs, ks, vs, os_ = _strides(q), _strides(k), _strides(v), _strides(out)
-    _check(
+    lens = _STONE_LENS.get(seq_lens.data_ptr()) if _TRACE is not None else None
+    nbytes = flops = 0.0
+    if lens is not None:
+        # packed live rows of q, k, v, out; 4 L^2 hd flops per head
+        nbytes = float(lens.sum()) * heads * hd * q.element_size() * 4
+        flops = float((lens.double() ** 2).sum()) * 4 * heads * hd
+    _launch("stone_attention", nbytes, flops, lambda: _check(
         _lib().mantis_stone_attention(
             _ptr(q), qs, _ptr(k), ks, _ptr(v), vs, _dt(q), _ptr(seq_lens), p, heads, t, hd, _ptr(out), os_,
             _ptr(lse), _stream(),
         ),
         "stone_attention",
-    )
+    ))
     return (out, lse) if want_lse else out
 
 
@@ -400,14 +484,21 @@ def fused_linear(x: Tensor, w1: Tensor, b1: Tensor | None = None, *, layer_norm:
         raise ValueError("add2 must be a contiguous fp32 (groups, n1) table")
     x_rows = None if x_rows is None else _i64(x_rows, "x_rows")
     add2_rows = None if add2_rows is None else _i64(add2_rows, "add2_rows")
-    st = _lib().mantis_fused_linear(
+    # algorithmic bytes: every input row once, every output row once (twice
+    # for a residual read-modify-write); flops: the GEMM stages
+    row_bytes = 128 * x.element_size() + (128 * x2.element_size() if x2 is not None else 0) + \
+        (n1 * 4 if add1 is not None else 0) + width * out.element_size() * (2 if residual else 1)
+    nbytes = m * row_bytes + w1.numel() * 2 * (2 if w2 is not None else 1) + (w3.numel() * 2 if w3 is not None else 0)
+    flops = 2 * m * (128 * n1 * (2 if w2 is not None else 1) + (n1 * width if w3 is not None else 0))
+    name = "fused_linear" + ("_mlp" if w3 is not None else ("_residual" if residual else "_proj"))
+    st = _launch(name, nbytes, flops, lambda: _lib().mantis_fused_linear(
         _ptr(x), _dt(x), x.stride(0), _ptr(x_rows), x.shape[0], m, int(layer_norm),
         _ptr(x2), _dt(x2) if x2 is not None else 0, x2.stride(0) if x2 is not None else 0,
         _ptr(w1), _ptr(w2), _ptr(b1), n1, _ptr(add1), add1.stride(0) if add1 is not None else 0,
         _ptr(add2), _ptr(add2_rows), add2.shape[0] if add2 is not None else 0, int(relu),
         _ptr(w3), _ptr(b3), width if w3 is not None else 0, mode, _ptr(out), out.stride(0),
         _ptr(error_flag(dev)), _stream(),
-    )
+    ))
     _check(st, "fused_linear")
     return out
 
@@ -488,10 +579,14 @@ def hex_aggregate_linear(x: Tensor, nbr: Tensor, weight: Tensor, bias: Tensor):
     out_sum = torch.empty_like(x)
     out_mean = torch.empty_like(x)
     if x.shape[0]:
-        _check(
-            _lib().mantis_hex_aggregate_linear(_ptr(x), _ptr(nbr), x.shape[0], _ptr(w), _ptr(b),
+        n = x.shape[0]
+        # x once, the neighbour table once, both outputs once, the layer once
+        nbytes = n * (128 * 2 + 6 * 4 + 2 * 128 * 2) + 128 * 128 * 2 + 128 * 4
+        flops = 2 * (2 * n * 128 * 128) + n * 6 * 128
+        _launch("hex_aggregate_linear", nbytes, flops, lambda: _check(
+            _lib().mantis_hex_aggregate_linear(_ptr(x), _ptr(nbr), n, _ptr(w), _ptr(b),
                                                _ptr(out_sum), _ptr(out_mean), _ptr(error_flag(dev)),
                                                _stream()),
             "hex_aggregate_linear",
-        )
+        ))
     return out_sum, out_mean
