@@ -88,8 +88,11 @@ struct Smem {
   static int bytes(int n3) { return (w1 + w2 + (kStage2 ? n3 * p3 : 0)) * 2; }
 };
 
+constexpr int kThreads = 512;  // 8 wavefronts share one LDS copy of the weights
+constexpr int kTileRows = 16 * (kThreads / 64);
+
 template <typename TX, typename TX2, bool kLN, int N1, bool kX2, bool kRelu, bool kStage2, int kMode>
-__global__ void __launch_bounds__(256) fused_linear_kernel(Args a) {
+__global__ void __launch_bounds__(kThreads) fused_linear_kernel(Args a) {
   extern __shared__ __attribute__((aligned(16))) _Float16 smem[];
   using S = Smem<N1, kStage2, kX2>;
   _Float16* sw1 = smem;
@@ -114,11 +117,11 @@ __global__ void __launch_bounds__(256) fused_linear_kernel(Args a) {
 
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
   const int l16 = lane % 16, g = lane / 16;
-  const int64_t n_tiles = (a.m + 63) / 64;
+  const int64_t n_tiles = (a.m + kTileRows - 1) / kTileRows;
   const TX* xp = static_cast<const TX*>(a.x);
 
   for (int64_t tile = blockIdx.x; tile < n_tiles; tile += gridDim.x) {
-    const int64_t row = tile * 64 + wave * 16 + l16;
+    const int64_t row = tile * kTileRows + wave * 16 + l16;
     const bool live = row < a.m;
     // ---- prologue: this lane's 32 features of its row (4 chunks of 8)
     int64_t src = row;
@@ -182,22 +185,7 @@ __global__ void __launch_bounds__(256) fused_linear_kernel(Args a) {
         for (int t = 0; t < 8; ++t) x2b[ks][t] = f2h(v2[t]);
       }
     }
-    // ---- stage 1: h^T (N1 x 16 rows) = W1 . x-hat^T (+ W2 . x2^T)
-    f32x4_t acc[NT1];
-#pragma unroll
-    for (int nt = 0; nt < NT1; ++nt) {
-      acc[nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const f16x8_t wf = *reinterpret_cast<const f16x8_t*>(sw1 + (16 * nt + l16) * kPitch + 32 * ks + 8 * g);
-        acc[nt] = mfma16x16x32(wf, xb[ks], acc[nt]);
-        if constexpr (kX2) {
-          const f16x8_t wf2 = *reinterpret_cast<const f16x8_t*>(sw2 + (16 * nt + l16) * kPitch + 32 * ks + 8 * g);
-          acc[nt] = mfma16x16x32(wf2, x2b[ks], acc[nt]);
-        }
-      }
-    }
-    // ---- epilogue 1: bias, row adds, activation (features 16nt + 4g + t)
+    // ---- row-group offset of the per-group add (validated once per row)
     int64_t grp = -1;
     if (live && a.add2) {
       grp = a.add2_rows[row];
@@ -206,8 +194,20 @@ __global__ void __launch_bounds__(256) fused_linear_kernel(Args a) {
         grp = -1;
       }
     }
+    // ---- stage 1, one 16-feature tile at a time: h^T = W1 . x-hat^T (+ W2 . x2^T),
+    // then bias / row adds / activation; without a second stage the tile is
+    // stored at once, with one it is packed to fp16 as stage 2's B fragment.
+    auto feature_tile = [&](int nt) -> f32x4_t {
+      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int nt = 0; nt < NT1; ++nt) {
+      for (int ks = 0; ks < 4; ++ks) {
+        const f16x8_t wf = *reinterpret_cast<const f16x8_t*>(sw1 + (16 * nt + l16) * kPitch + 32 * ks + 8 * g);
+        acc = mfma16x16x32(wf, xb[ks], acc);
+        if constexpr (kX2) {
+          const f16x8_t wf2 = *reinterpret_cast<const f16x8_t*>(sw2 + (16 * nt + l16) * kPitch + 32 * ks + 8 * g);
+          acc = mfma16x16x32(wf2, x2b[ks], acc);
+        }
+      }
       const int f = 16 * nt + 4 * g;
       float4 add = a.b1 ? *reinterpret_cast<const float4*>(a.b1 + f) : make_float4(0.f, 0.f, 0.f, 0.f);
       if (live && a.add1) {
@@ -218,26 +218,37 @@ __global__ void __launch_bounds__(256) fused_linear_kernel(Args a) {
         const float4 r = *reinterpret_cast<const float4*>(a.add2 + grp * N1 + f);
         add.x += r.x, add.y += r.y, add.z += r.z, add.w += r.w;
       }
-      acc[nt][0] += add.x, acc[nt][1] += add.y, acc[nt][2] += add.z, acc[nt][3] += add.w;
+      acc[0] += add.x, acc[1] += add.y, acc[2] += add.z, acc[3] += add.w;
       if constexpr (kRelu)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) acc[nt][t] = fmaxf(acc[nt][t], 0.f);
-    }
-    if constexpr (!kStage2) {
-      if (live) {
+        for (int t = 0; t < 4; ++t) acc[t] = fmaxf(acc[t], 0.f);
+      return acc;
+    };
+    f16x8_t hb[kStage2 ? N1 / 32 : 1];
+    if constexpr (kStage2) {
+      // tile nt holds hidden features 16nt + 4g + t: K slots (nt & 1) * 4 + t
+      // of stage 2's 32-wide step nt / 2
 #pragma unroll
-        for (int nt = 0; nt < NT1; ++nt) store4<kMode>(a, row, 16 * nt + 4 * g, acc[nt]);
-      }
-    } else {
-      // ---- stage 2: y^T (n3 x 16) = W3 . h^T, h^T fed straight from acc
-      f16x8_t hb[N1 / 32];
-#pragma unroll
-      for (int ks = 0; ks < N1 / 32; ++ks)
+      for (int k = 0; k < N1 / 32; ++k) {
+        const f32x4_t lo = feature_tile(2 * k);
+        const f32x4_t hi = feature_tile(2 * k + 1);
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-          hb[ks][t] = f2h(acc[2 * ks][t]);
-          hb[ks][4 + t] = f2h(acc[2 * ks + 1][t]);
+          hb[k][t] = f2h(lo[t]);
+          hb[k][4 + t] = f2h(hi[t]);
         }
+        // keep each step's weight loads next to its products (bounded live range)
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {
+#pragma unroll 2
+      for (int nt = 0; nt < NT1; ++nt) {
+        const f32x4_t acc = feature_tile(nt);
+        if (live) store4<kMode>(a, row, 16 * nt + 4 * g, acc);
+      }
+    }
+    if constexpr (kStage2) {
+      // ---- stage 2: y^T (n3 x 16) = W3 . h^T
       const int NT3 = a.n3 / 16;
       for (int ot = 0; ot < NT3; ++ot) {
         f32x4_t y = {0.f, 0.f, 0.f, 0.f};
@@ -285,10 +296,10 @@ int32_t launch(const Args& a, hipStream_t stream) {
       return MANTIS_E_LAUNCH;
     configured = true;
   }
-  const int64_t tiles = (a.m + 63) / 64;
+  const int64_t tiles = (a.m + kTileRows - 1) / kTileRows;
   const int per_cu = std::max(1, std::min(4, kMaxLds / std::max(bytes, 1)));
   const int64_t grid = std::min<int64_t>(tiles, int64_t(cu_count()) * per_cu);
-  kernel<<<unsigned(grid), 256, bytes, stream>>>(a);
+  kernel<<<unsigned(grid), kThreads, bytes, stream>>>(a);
   return launched();
 }
 

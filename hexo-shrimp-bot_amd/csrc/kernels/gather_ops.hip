@@ -101,7 +101,7 @@ run_reduce_scalar_kernel(const Tin* __restrict__ values, int64_t n_src, int64_t 
 
 // ------------------------------------------------------------ typed attention
 
-template <typename Tin, bool kVcls>
+template <typename Tin, typename Tout, bool kVcls>
 __global__ void __launch_bounds__(kBlock)
 cell_attention_kernel(const Tin* __restrict__ q, const Tin* __restrict__ k,
                       const Tin* __restrict__ v, int64_t ldq, int64_t ldk, int64_t ldv,
@@ -109,7 +109,7 @@ cell_attention_kernel(const Tin* __restrict__ q, const Tin* __restrict__ k,
                       const float* __restrict__ vcls, const int64_t* __restrict__ seg_ptr,
                       const int64_t* __restrict__ src, const int64_t* __restrict__ cls,
                       int64_t n_q, int64_t n_k, int64_t n_entries, float scale,
-                      float* __restrict__ out, float* __restrict__ m_out,
+                      Tout* __restrict__ out, float* __restrict__ m_out,
                       float* __restrict__ l_out, int32_t* flag) {
   const int64_t row = int64_t(blockIdx.x) * kGroupsPerBlock + threadIdx.x / kGroup;
   const int lane = threadIdx.x % kGroup;
@@ -121,13 +121,16 @@ cell_attention_kernel(const Tin* __restrict__ q, const Tin* __restrict__ k,
   segment(seg_ptr, row, n_entries, start, end);
   float m = -INFINITY, l = 0.f;
   float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  for (int64_t e = start; e < end; ++e) {
-    const int64_t s = src[e], c = cls[e];
-    if (s < 0 || s >= n_k || c < 0 || c >= n_classes) {
+  // one edge's score and value row; an out-of-range index scores -inf
+  auto edge = [&](int64_t e, float (&vv)[8]) -> float {
+    int64_t s = src[e], c = cls[e];
+    const bool ok = s >= 0 && s < n_k && c >= 0 && c < n_classes;
+    if (!ok) {
       raise_flag(flag, MANTIS_FLAG_INDEX);
-      continue;
+      s = 0;
+      c = 0;
     }
-    float kv[8], vv[8];
+    float kv[8];
     load8(k + s * ldk + lane * 8, kv);
     load8(v + s * ldv + lane * 8, vv);
     float dot = 0.f;
@@ -140,13 +143,34 @@ cell_attention_kernel(const Tin* __restrict__ q, const Tin* __restrict__ k,
 #pragma unroll
       for (int i = 0; i < 8; ++i) vv[i] += cv[i];
     }
-    const float m_new = fmaxf(m, score);
+    return ok ? score : -INFINITY;
+  };
+  // two edges in flight per step: both rows' loads issue before either's math
+  int64_t e = start;
+  for (; e + 1 < end; e += 2) {
+    float v0[8], v1[8];
+    const float s0 = edge(e, v0), s1 = edge(e + 1, v1);
+    const float m_new = fmaxf(m, fmaxf(s0, s1));
+    if (m_new == -INFINITY) continue;
     const float alpha = __expf(m - m_new);
-    const float p = __expf(score - m_new);
-    l = l * alpha + p;
+    const float p0 = __expf(s0 - m_new), p1 = __expf(s1 - m_new);
+    l = l * alpha + p0 + p1;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] = fmaf(p, vv[i], acc[i] * alpha);
+    for (int i = 0; i < 8; ++i) acc[i] = fmaf(p1, v1[i], fmaf(p0, v0[i], acc[i] * alpha));
     m = m_new;
+  }
+  if (e < end) {
+    float v0[8];
+    const float s0 = edge(e, v0);
+    const float m_new = fmaxf(m, s0);
+    if (m_new != -INFINITY) {
+      const float alpha = __expf(m - m_new);
+      const float p0 = __expf(s0 - m_new);
+      l = l * alpha + p0;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] = fmaf(p0, v0[i], acc[i] * alpha);
+      m = m_new;
+    }
   }
   const float inv = l > 0.f ? 1.f / l : 1.f;
 #pragma unroll
@@ -247,12 +271,12 @@ latent_read_kernel(const Tin* __restrict__ q, const Tin* __restrict__ k,
   }
 }
 
-template <typename Tin>
+template <typename Tin, typename Tout>
 __global__ void __launch_bounds__(kBlock)
 latent_broadcast_kernel(const Tin* __restrict__ q, const Tin* __restrict__ k,
                         const Tin* __restrict__ v, int64_t ldq, int64_t ldk, int64_t ldv,
                         const int64_t* __restrict__ window_pos,
-                        int64_t n_pos, int64_t n_w, float scale, float* __restrict__ out,
+                        int64_t n_pos, int64_t n_w, float scale, Tout* __restrict__ out,
                         float* __restrict__ m_out, float* __restrict__ l_out, int32_t* flag) {
   const int64_t w = int64_t(blockIdx.x) * kGroupsPerBlock + threadIdx.x / kGroup;
   const int lane = threadIdx.x % kGroup;
@@ -407,8 +431,8 @@ int32_t mantis_cell_attention(const void* q, const void* k, const void* v, int32
                               int64_t ldq, int64_t ldk, int64_t ldv, const float* bias, int64_t n_classes, const float* vcls,
                               const int64_t* seg_ptr, const int64_t* src, const int64_t* cls,
                               int64_t n_entries, int64_t n_q, int64_t n_k, int32_t heads,
-                              int32_t hd, float* out, float* m, float* l, int32_t* err_flag,
-                              void* stream) {
+                              int32_t hd, void* out, int32_t out_dtype, float* m, float* l,
+                              int32_t* err_flag, void* stream) {
   if (n_q == 0) return MANTIS_OK;
   if (!q || !k || !v || !bias || !seg_ptr || !out || heads != 4 || hd != 32 || n_q < 0 ||
       n_k < 0 || n_classes <= 0)
@@ -420,18 +444,25 @@ int32_t mantis_cell_attention(const void* q, const void* k, const void* v, int32
   const float scale = 1.0f / sqrtf(float(hd));
   hipStream_t s = as_stream(stream);
   const dim3 grid(grid_rows(n_q)), block(kBlock);
+  if (out_dtype != MANTIS_F32 && out_dtype != MANTIS_F16) return MANTIS_E_ARG;
   const bool ok = with_type(dtype, [&](auto t) {
     using T = decltype(t);
-    if (vcls)
-      cell_attention_kernel<T, true><<<grid, block, 0, s>>>(
-          static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v), ldq, ldk,
-          ldv, bias, n_classes, vcls, seg_ptr, src, cls, n_q, n_k, n_entries, scale, out, m, l,
-          err_flag);
-    else
-      cell_attention_kernel<T, false><<<grid, block, 0, s>>>(
-          static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v), ldq, ldk,
-          ldv, bias, n_classes, vcls, seg_ptr, src, cls, n_q, n_k, n_entries, scale, out, m, l,
-          err_flag);
+    auto go = [&](auto o) {
+      using TO = decltype(o);
+      TO* op = static_cast<TO*>(out);
+      if (vcls)
+        cell_attention_kernel<T, TO, true><<<grid, block, 0, s>>>(
+            static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v), ldq, ldk,
+            ldv, bias, n_classes, vcls, seg_ptr, src, cls, n_q, n_k, n_entries, scale, op, m, l,
+            err_flag);
+      else
+        cell_attention_kernel<T, TO, false><<<grid, block, 0, s>>>(
+            static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v), ldq, ldk,
+            ldv, bias, n_classes, vcls, seg_ptr, src, cls, n_q, n_k, n_entries, scale, op, m, l,
+            err_flag);
+    };
+    if (out_dtype == MANTIS_F16) go(_Float16{});
+    else go(float{});
   });
   if (!ok) return MANTIS_E_ARG;
   return launched();
@@ -459,9 +490,10 @@ int32_t mantis_latent_read(const void* q, const void* k, const void* v, int32_t 
 }
 
 int32_t mantis_latent_broadcast(const void* q, const void* k, const void* v, int32_t dtype,
-                                int64_t ldq, int64_t ldk, int64_t ldv, const int64_t* window_pos, int64_t n_pos, int64_t n_w,
-                                int32_t heads, int32_t hd, float* out, float* m, float* l,
-                                int32_t* err_flag, void* stream) {
+                                int64_t ldq, int64_t ldk, int64_t ldv, const int64_t* window_pos,
+                                int64_t n_pos, int64_t n_w, int32_t heads, int32_t hd, void* out,
+                                int32_t out_dtype, float* m, float* l, int32_t* err_flag,
+                                void* stream) {
   if (n_w == 0) return MANTIS_OK;
   if (!q || !k || !v || !window_pos || !out || heads != 4 || hd != 32 || n_w < 0 || n_pos < 0)
     return MANTIS_E_ARG;
@@ -469,11 +501,17 @@ int32_t mantis_latent_broadcast(const void* q, const void* k, const void* v, int
   const float scale = 1.0f / sqrtf(float(hd));
   hipStream_t s = as_stream(stream);
   const dim3 grid(grid_rows(n_w)), block(kBlock);
+  if (out_dtype != MANTIS_F32 && out_dtype != MANTIS_F16) return MANTIS_E_ARG;
   const bool ok = with_type(dtype, [&](auto tv) {
     using T = decltype(tv);
-    latent_broadcast_kernel<T><<<grid, block, 0, s>>>(
-        static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v), ldq, ldk, ldv,
-        window_pos, n_pos, n_w, scale, out, m, l, err_flag);
+    if (out_dtype == MANTIS_F16)
+      latent_broadcast_kernel<T, _Float16><<<grid, block, 0, s>>>(
+          static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v), ldq, ldk, ldv,
+          window_pos, n_pos, n_w, scale, static_cast<_Float16*>(out), m, l, err_flag);
+    else
+      latent_broadcast_kernel<T, float><<<grid, block, 0, s>>>(
+          static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v), ldq, ldk, ldv,
+          window_pos, n_pos, n_w, scale, static_cast<float*>(out), m, l, err_flag);
   });
   if (!ok) return MANTIS_E_ARG;
   return launched();

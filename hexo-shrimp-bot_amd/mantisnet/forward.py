@@ -302,17 +302,17 @@ def _cell_stage(W, P, pb, plan: Plan, s, w, c):
     q = _proj(W, pb + "cr_q", c)
     kv = _proj(W, pb + "cr_kv", w)
     read = ops.cell_attention(q, kv[:, :128], kv[:, 128:], P[pb + "cr_bias"], P[pb + "cr_vclass.weight"],
-                              plan.cell_ptr, plan.edge_window, plan.edge_class)
+                              plan.cell_ptr, plan.edge_window, plan.edge_class, out_dtype=HALF)
     _resid(W, pb + "cr_o", read.view(n_c, 128), c)
     q = _proj(W, pb + "rad_q", c)
     kv = _proj(W, pb + "rad_kv", s)
     read = ops.cell_attention(q, kv[:, :128], kv[:, 128:], P[pb + "radius_bias"], P[pb + "radius_vclass.weight"],
-                              plan.radius_ptr, plan.radius_src, plan.radius_class)
+                              plan.radius_ptr, plan.radius_src, plan.radius_class, out_dtype=HALF)
     _resid(W, pb + "rad_o", read.view(n_c, 128), c)
     q = _proj(W, pb + "wr_q", w)
     kv = _proj(W, pb + "wr_kv", c)
     back = ops.cell_attention(q, kv[:, :128], kv[:, 128:], P[pb + "wr_bias"], None,
-                              plan.win_ptr, plan.edge_wcell, plan.edge_wclass)
+                              plan.win_ptr, plan.edge_wcell, plan.edge_wclass, out_dtype=HALF)
     _resid(W, pb + "wr_o", back.view(n_w, 128), w)
 
 
@@ -332,7 +332,7 @@ def _latent_cycle(W, P, pb, plan: Plan, w, g2):
     g2.add_(F.linear(mixed, P[pb + "latent_wo_mix.weight"], P[pb + "latent_wo_mix.bias"]))
     qb = _proj(W, pb + "lq_bcast", w)
     kvb = _proj(W, pb + "lkv_bcast", g2)
-    out = ops.latent_broadcast_rows(qb, kvb, plan.window_pos)
+    out = ops.latent_broadcast_rows(qb, kvb, plan.window_pos, out_dtype=HALF)
     _resid(W, pb + "lo_bcast", out.view(plan.n_w, 128), w)
 
 

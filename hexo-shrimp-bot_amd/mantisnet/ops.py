@@ -226,9 +226,11 @@ def run_reduce(values: Tensor, gather: Tensor, ptr: Tensor, n_dest: int, out_dty
 
 
 def cell_attention(q: Tensor, k: Tensor, v: Tensor, bias: Tensor, vcls: Tensor | None,
-                   seg_ptr: Tensor, src: Tensor, cls: Tensor, stats: bool = False):
+                   seg_ptr: Tensor, src: Tensor, cls: Tensor, stats: bool = False,
+                   out_dtype: torch.dtype = torch.float32):
     """Typed segment attention; q/k/v are 128-wide rows (heads=4 x hd=32),
-    possibly strided views; returns fp32 (n_q, 4, 32) [and m, l]."""
+    possibly strided views; returns (n_q, 4, 32) in out_dtype (fp32 or
+    fp16; the math is fp32 either way) [and m, l]."""
     dev = _on_gpu(q, k, v, bias, vcls, seg_ptr, src, cls)
     heads, hd = 4, 32
     n_q = q.shape[0]
@@ -253,21 +255,23 @@ def cell_attention(q: Tensor, k: Tensor, v: Tensor, bias: Tensor, vcls: Tensor |
             raise ValueError("vcls must have shape (classes, heads * head_dim)")
         vcls = vcls.float().contiguous()
     seg_ptr, src, cls = _i64(seg_ptr, "seg_ptr"), _i64(src, "src"), _i64(cls, "cls")
-    out = torch.empty((n_q, heads, hd), dtype=torch.float32, device=dev)
+    if out_dtype not in (torch.float32, torch.float16):
+        raise ValueError("cell attention writes fp32 or fp16")
+    out = torch.empty((n_q, heads, hd), dtype=out_dtype, device=dev)
     m = torch.empty((n_q, heads), dtype=torch.float32, device=dev) if stats else None
     l = torch.empty((n_q, heads), dtype=torch.float32, device=dev) if stats else None
     if n_q:
         e = src.numel()
         # algorithmic bytes: q and out rows once, each source's k and v rows
         # once, the CSR pointers and the per-edge (src, cls) indices
-        nbytes = n_q * (128 * q.element_size() + out[0].numel() * 4 + 8) + e * 16 + \
+        nbytes = n_q * (128 * q.element_size() + 128 * out.element_size() + 8) + e * 16 + \
             k.shape[0] * 128 * (k.element_size() + v.element_size())
         flops = e * 4 * 128 * 2  # score dot + weighted value sum per edge and head
         _launch("cell_attention", nbytes, flops, lambda: _check(
             _lib().mantis_cell_attention(
                 _ptr(q), _ptr(k), _ptr(v), _dt(q), ldq, ldk, ldv, _ptr(bias), bias.shape[1], _ptr(vcls),
                 _ptr(seg_ptr), _ptr(src), _ptr(cls), e, n_q, k.shape[0], heads, hd,
-                _ptr(out), _ptr(m), _ptr(l), _ptr(error_flag(dev)), _stream(),
+                _ptr(out), _dt(out), _ptr(m), _ptr(l), _ptr(error_flag(dev)), _stream(),
             ),
             "cell_attention",
         ))
@@ -304,9 +308,11 @@ def latent_read(q: Tensor, k: Tensor, v: Tensor, offsets: Tensor, order: Tensor,
     return (out, m, l) if stats else out
 
 
-def latent_broadcast(q: Tensor, k: Tensor, v: Tensor, window_pos: Tensor, stats: bool = False):
+def latent_broadcast(q: Tensor, k: Tensor, v: Tensor, window_pos: Tensor, stats: bool = False,
+                     out_dtype: torch.dtype = torch.float32):
     """Every window attends over its position's four latents; q 128-wide
-    window rows, k/v (P, 4, ...) latent rows; returns fp32 (N_w, 4, 32)."""
+    window rows, k/v (P, 4, ...) latent rows; returns (N_w, 4, 32) in
+    out_dtype (fp32 or fp16)."""
     dev = _on_gpu(q, k, v, window_pos)
     n_w = q.shape[0]
     p = k.shape[0]
@@ -318,32 +324,41 @@ def latent_broadcast(q: Tensor, k: Tensor, v: Tensor, window_pos: Tensor, stats:
     k2, ldk = _rows128(k.reshape(p * 4, -1) if k.is_contiguous() else k.contiguous().view(p * 4, -1), "k")
     v2, ldv = _rows128(v.reshape(p * 4, -1) if v.is_contiguous() else v.contiguous().view(p * 4, -1), "v")
     window_pos = _i64(window_pos, "window_pos")
-    out = torch.empty((n_w, 4, 32), dtype=torch.float32, device=dev)
+    if out_dtype not in (torch.float32, torch.float16):
+        raise ValueError("latent broadcast writes fp32 or fp16")
+    out = torch.empty((n_w, 4, 32), dtype=out_dtype, device=dev)
     m = torch.empty((n_w, 4), dtype=torch.float32, device=dev) if stats else None
     l = torch.empty((n_w, 4), dtype=torch.float32, device=dev) if stats else None
     if n_w:
         _check(
             _lib().mantis_latent_broadcast(
                 _ptr(q), _ptr(k2), _ptr(v2), _dt(q), ldq, ldk, ldv, _ptr(window_pos), p, n_w, 4, 32,
-                _ptr(out), _ptr(m), _ptr(l), _ptr(error_flag(dev)), _stream(),
+                _ptr(out), _dt(out), _ptr(m), _ptr(l), _ptr(error_flag(dev)), _stream(),
             ),
             "latent_broadcast",
         )
     return (out, m, l) if stats else out
 
 
-def latent_broadcast_rows(q: Tensor, kv: Tensor, window_pos: Tensor) -> Tensor:
+def latent_broadcast_rows(q: Tensor, kv: Tensor, window_pos: Tensor,
+                          out_dtype: torch.dtype = torch.float32) -> Tensor:
     """Broadcast with k/v the two 128-wide halves of (P*4, 256) rows."""
     dev = _on_gpu(q, kv, window_pos)
     n_w = q.shape[0]
     p = kv.shape[0] // 4
+    if kv.shape != (4 * p, 256) or kv.stride(1) != 1 or kv.dtype != q.dtype:
+        raise ValueError("kv must be (P*4, 256) rows of q's dtype")
+    if out_dtype not in (torch.float32, torch.float16):
+        raise ValueError("latent broadcast writes fp32 or fp16")
+    if window_pos.numel() != n_w:
+        raise ValueError("window_pos must have one entry per window")
     q, ldq = _rows128(q, "q")
-    out = torch.empty((n_w, 4, 32), dtype=torch.float32, device=dev)
+    out = torch.empty((n_w, 4, 32), dtype=out_dtype, device=dev)
     if n_w:
         _check(
             _lib().mantis_latent_broadcast(
                 _ptr(q), kv.data_ptr(), kv[:, 128:].data_ptr(), _dt(q), ldq, kv.stride(0), kv.stride(0),
-                _ptr(_i64(window_pos, "window_pos")), p, n_w, 4, 32, _ptr(out), None, None,
+                _ptr(_i64(window_pos, "window_pos")), p, n_w, 4, 32, _ptr(out), _dt(out), None, None,
                 _ptr(error_flag(dev)), _stream(),
             ),
             "latent_broadcast",

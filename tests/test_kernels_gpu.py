@@ -71,9 +71,10 @@ def test_unsorted_runs_are_flagged(device):
         ops.raise_on_device_error(device)
 
 
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16])
 @pytest.mark.parametrize("with_vcls", [True, False])
 @pytest.mark.parametrize("dtype", [torch.float16, BF, torch.float32])
-def test_cell_attention_matches_dense_oracle(device, with_vcls, dtype):
+def test_cell_attention_matches_dense_oracle(device, with_vcls, dtype, out_dtype):
     gen = _g(3)
     n_q, n_k, classes = 257, 90, 726
     dest, counts = _runs(n_q, 18, 4)
@@ -86,10 +87,14 @@ def test_cell_attention_matches_dense_oracle(device, with_vcls, dtype):
     vcls = 0.1 * torch.randn(classes, 128, generator=gen) if with_vcls else None
     ptr = torch.searchsorted(dest, torch.arange(n_q + 1))
     d = lambda x: None if x is None else x.to(device)  # noqa: E731
-    out, m, l = ops.cell_attention(d(q), d(k), d(v), d(bias), d(vcls), d(ptr), d(src), d(cls), stats=True)
+    out, m, l = ops.cell_attention(d(q), d(k), d(v), d(bias), d(vcls), d(ptr), d(src), d(cls), stats=True,
+                                   out_dtype=out_dtype)
     ops.raise_on_device_error(device)
+    assert out.dtype == out_dtype
     exp = R.cell_attention(q.float(), k.float(), v.float(), bias, vcls, src, cls, dest)
-    torch.testing.assert_close(out.cpu(), exp, rtol=1e-4, atol=1e-5)
+    if out_dtype == torch.float16:  # fp32 math, one rounding of the stored value
+        exp = exp.to(torch.float16).float()
+    torch.testing.assert_close(out.float().cpu(), exp, rtol=1e-3, atol=1e-4)
     empty = counts == 0
     assert empty.any() and torch.all(out.cpu()[empty] == 0)
     assert torch.all(l.cpu()[empty] == 0) and torch.all(l.cpu()[~empty] > 0)
@@ -119,6 +124,9 @@ def test_latent_read_and_broadcast_match_literal_loops(device, dt):
     ops.raise_on_device_error(device)
     expb = R.latent_broadcast_loops(qb.float(), kb.float(), vb.float(), window_pos)
     torch.testing.assert_close(outb.cpu(), expb, rtol=1e-4, atol=1e-5)
+    outh = ops.latent_broadcast(qb.to(device), kb.to(device), vb.to(device), window_pos.to(device),
+                                out_dtype=torch.float16)
+    torch.testing.assert_close(outh.float().cpu(), expb.to(torch.float16).float(), rtol=1e-3, atol=1e-4)
 
 
 def test_row_encode_matches_literal(device):
