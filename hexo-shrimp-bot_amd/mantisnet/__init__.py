@@ -18,6 +18,7 @@ from .builder import (
     collate_prefixes,
 )
 from .model import PRODUCTION, MantisConfig, MantisNet, ModelOutput, compose_acting_q, compose_q
+from . import library  # noqa: E402,F401  registers the mantisnet:: operators
 
 __all__ = [
     "MODEL_REPR_VERSION",

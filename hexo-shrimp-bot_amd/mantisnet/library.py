@@ -1,0 +1,328 @@
+"""The ``mantisnet::*`` operator namespace, re-registered on the HIP kernels.
+
+Every operator keeps the reference's qualified name, argument list and
+output structure, so code written against the reference's ``torch.ops``
+surface runs unchanged.  Each has a fake (meta) implementation for tracing.
+Only the forward is provided: this is the inference path, and asking for a
+gradient raises.
+
+Differences from the reference, all deliberate:
+
+* no fallback: a CPU tensor, a dtype or shape the kernels do not cover
+  raises instead of silently composing torch ops;
+* the attention-family kernels are specialised to the model's geometry —
+  4 heads x 32 dims (128-wide rows); ``fused_attention`` takes head_dim 32;
+* ``aggregate_to_windows`` writes zero rows for windows without entries
+  (the reference leaves them uninitialised; windows are never empty).
+
+Reference registrations (python/mantisnet/mantisnet/...):
+attention.py:719-760, message_passing.py:191-227 and 344-365,
+cell_latents.py:168-208 and 834-952, cell_nodes.py:97-147,
+window_latents.py:38-64, 553-587 and 648-664, row_encoder.py:368-380.
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import Tensor
+
+from . import ops, tables
+
+_NS = "mantisnet"
+
+
+def _no_grad(name):
+    def backward(ctx, *grads):
+        raise RuntimeError(f"{_NS}::{name} is inference-only on this build (no backward kernel)")
+
+    return backward
+
+
+def _register_inference_only(op, name: str) -> None:
+    op.register_autograd(_no_grad(name), setup_context=lambda ctx, inputs, output: None)
+
+
+# ----------------------------------------------------------------- stone attention
+
+
+@torch.library.custom_op(f"{_NS}::fused_attention", mutates_args=())
+def fused_attention(q: Tensor, k: Tensor, v: Tensor, seq_lens: Tensor) -> tuple[Tensor, Tensor]:
+    """Ragged attention over each position's live prefix; pad query rows are
+    exactly zero.  q/k/v (P, A, T, 32) fp16/bf16; returns (out like q, lse
+    (P, A, T) fp32 — natural-log softmax normaliser of each live row)."""
+    out, lse = ops.stone_attention(q, k, v, seq_lens, want_lse=True)
+    return out, lse
+
+
+@fused_attention.register_fake
+def _(q, k, v, seq_lens):
+    return torch.empty_like(q), q.new_empty(q.shape[:3], dtype=torch.float32)
+
+
+# ----------------------------------------------------------------- run reductions
+
+
+def _check_incidence(values: Tensor, *idx: Tensor) -> None:
+    if values.ndim != 2:
+        raise ValueError("values must have shape (N, H)")
+    if idx[0].ndim != 1 or any(t.shape != idx[0].shape for t in idx):
+        raise ValueError("the incidence views must be one length")
+    if any(t.dtype != torch.int64 for t in idx):
+        raise ValueError("incidence tensors must have dtype int64")
+    if not values.is_floating_point():
+        raise ValueError("values must have floating-point dtype")
+
+
+def _run_sum(values: Tensor, gather: Tensor, runs: Tensor, n_dest: int, dtype: torch.dtype) -> Tensor:
+    if n_dest < 0:
+        raise ValueError(f"destination count must be nonnegative, got {n_dest}")
+    return ops.run_reduce(values, gather, ops.runs_to_ptr(runs, n_dest), n_dest, dtype)
+
+
+@torch.library.custom_op(f"{_NS}::aggregate_to_windows", mutates_args=())
+def aggregate_to_windows(values: Tensor, inc_stone: Tensor, inc_window: Tensor, run_stone: Tensor,
+                         run_window: Tensor, n_windows: int) -> Tensor:
+    """out[w] = sum of values[inc_stone[e]] over the window-major run of w,
+    fp32 accumulation, one cast to values.dtype."""
+    _check_incidence(values, inc_stone, inc_window, run_stone, run_window)
+    return _run_sum(values, inc_stone, inc_window, n_windows, values.dtype)
+
+
+@aggregate_to_windows.register_fake
+def _(values, inc_stone, inc_window, run_stone, run_window, n_windows):
+    return values.new_empty((n_windows, values.shape[1]))
+
+
+@torch.library.custom_op(f"{_NS}::aggregate_to_stones", mutates_args=())
+def aggregate_to_stones(values: Tensor, inc_stone: Tensor, inc_window: Tensor, run_stone: Tensor,
+                        run_window: Tensor, n_stones: int) -> Tensor:
+    """out[s] = sum of values[run_window[e]] over the stone-major run of s, fp32."""
+    _check_incidence(values, inc_stone, inc_window, run_stone, run_window)
+    return _run_sum(values, run_window, run_stone, n_stones, torch.float32)
+
+
+@aggregate_to_stones.register_fake
+def _(values, inc_stone, inc_window, run_stone, run_window, n_stones):
+    return values.new_empty((n_stones, values.shape[1]), dtype=torch.float32)
+
+
+@torch.library.custom_op(f"{_NS}::class_row_sum", mutates_args=())
+def class_row_sum(weight: Tensor, gather: Tensor, runs: Tensor, n_dest: int, run_len: int) -> Tensor:
+    """out[d] = sum of weight[gather[e]] over the ascending run of d, fp32."""
+    _check_incidence(weight, gather, runs)
+    return _run_sum(weight, gather, runs, n_dest, torch.float32)
+
+
+@class_row_sum.register_fake
+def _(weight, gather, runs, n_dest, run_len):
+    return weight.new_empty((n_dest, weight.shape[1]), dtype=torch.float32)
+
+
+@torch.library.custom_op(f"{_NS}::incidence_row_sum", mutates_args=())
+def incidence_row_sum(values: Tensor, gather: Tensor, runs: Tensor, rev_gather: Tensor, rev_runs: Tensor,
+                      n_dest: int, run_len: int, rev_run_len: int) -> Tensor:
+    """out[d] = sum of values[gather[e]] over the ascending run of d, fp32
+    (the reverse views serve the reference's backward only)."""
+    _check_incidence(values, gather, runs)
+    return _run_sum(values, gather, runs, n_dest, torch.float32)
+
+
+@incidence_row_sum.register_fake
+def _(values, gather, runs, rev_gather, rev_runs, n_dest, run_len, rev_run_len):
+    return values.new_empty((n_dest, values.shape[1]), dtype=torch.float32)
+
+
+# ----------------------------------------------------------------- typed cell attention
+
+
+def _check_cell_attention(q, k, v, bias, seg_ptr, src, cls, qid, sseg_ptr, sqid, scls) -> None:
+    if q.ndim != 3 or k.shape != v.shape or q.shape[1:] != k.shape[1:]:
+        raise ValueError("q and k/v must share (heads, head_dim)")
+    if bias.ndim != 2 or bias.shape[0] != q.shape[1]:
+        raise ValueError("bias must have shape (heads, classes)")
+    if seg_ptr.numel() != q.shape[0] + 1:
+        raise ValueError("seg_ptr must have one entry per query row plus one")
+    if sseg_ptr.numel() != k.shape[0] + 1:
+        raise ValueError("sseg_ptr must have one entry per source row plus one")
+    if src.ndim != 1 or any(t.shape != src.shape for t in (cls, qid, sqid, scls)):
+        raise ValueError("the edge views must have one length")
+    if q.shape[1:] != (4, 32):
+        raise ValueError("the typed-attention kernel covers 4 heads x 32 dims")
+
+
+@torch.library.custom_op(f"{_NS}::cell_attention", mutates_args=())
+def cell_attention(q: Tensor, k: Tensor, v: Tensor, bias: Tensor, vcls: Tensor, seg_ptr: Tensor, src: Tensor,
+                   cls: Tensor, qid: Tensor, sseg_ptr: Tensor, sqid: Tensor, scls: Tensor, cptr: Tensor,
+                   cedge_q: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+    """Per query row and head: softmax over its entry run of
+    q.k/sqrt(hd) + bias[head, cls], values v[src] + vcls[cls]; an empty run
+    gives out 0, m -inf, l 0.  Returns fp32 (out, m, l)."""
+    _check_cell_attention(q, k, v, bias, seg_ptr, src, cls, qid, sseg_ptr, sqid, scls)
+    if vcls.shape != (bias.shape[1], q.shape[1] * q.shape[2]):
+        raise ValueError("vcls must have shape (classes, heads * head_dim)")
+    return ops.cell_attention(q, k, v, bias, vcls, seg_ptr, src, cls, stats=True)
+
+
+@cell_attention.register_fake
+def _(q, k, v, bias, vcls, seg_ptr, src, cls, qid, sseg_ptr, sqid, scls, cptr, cedge_q):
+    n_q, heads, hd = q.shape
+    return (q.new_empty((n_q, heads, hd), dtype=torch.float32), q.new_empty((n_q, heads), dtype=torch.float32),
+            q.new_empty((n_q, heads), dtype=torch.float32))
+
+
+@torch.library.custom_op(f"{_NS}::cell_attention_plain", mutates_args=())
+def cell_attention_plain(q: Tensor, k: Tensor, v: Tensor, bias: Tensor, seg_ptr: Tensor, src: Tensor,
+                         cls: Tensor, qid: Tensor, sseg_ptr: Tensor, sqid: Tensor, scls: Tensor, cptr: Tensor,
+                         cedge_q: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+    """Typed segment attention with the score bias only (window read-back)."""
+    _check_cell_attention(q, k, v, bias, seg_ptr, src, cls, qid, sseg_ptr, sqid, scls)
+    return ops.cell_attention(q, k, v, bias, None, seg_ptr, src, cls, stats=True)
+
+
+@cell_attention_plain.register_fake
+def _(q, k, v, bias, seg_ptr, src, cls, qid, sseg_ptr, sqid, scls, cptr, cedge_q):
+    n_q, heads, hd = q.shape
+    return (q.new_empty((n_q, heads, hd), dtype=torch.float32), q.new_empty((n_q, heads), dtype=torch.float32),
+            q.new_empty((n_q, heads), dtype=torch.float32))
+
+
+# ----------------------------------------------------------------- window latents
+
+
+def _check_layout(offsets: Tensor, order: Tensor, positions: int, windows: int) -> None:
+    if offsets.ndim != 1 or offsets.shape[0] != positions + 1:
+        raise ValueError("offsets must have shape (P + 1,)")
+    if order.ndim != 1 or order.shape[0] != windows:
+        raise ValueError("order must have shape (N_w,)")
+
+
+@torch.library.custom_op(f"{_NS}::window_latent_read", mutates_args=())
+def window_latent_read(q: Tensor, k: Tensor, v: Tensor, window_pos: Tensor, offsets: Tensor,
+                       order: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+    """Four latent queries (P, 4, heads, hd) per position over its windows'
+    k/v (N_w, heads, hd); fp32 (out, m, l); a position without windows reads 0."""
+    if q.ndim != 4 or q.shape[1] != 4:
+        raise ValueError("read q must have shape (P, slots=4, heads, head_dim)")
+    if k.ndim != 3 or k.shape != v.shape or q.shape[2:] != k.shape[1:]:
+        raise ValueError("read q, k, and v must share heads and head_dim")
+    if window_pos.ndim != 1 or window_pos.shape[0] != k.shape[0]:
+        raise ValueError("window_pos must have one entry per window")
+    _check_layout(offsets, order, q.shape[0], k.shape[0])
+    return ops.latent_read(q, k, v, offsets, order, stats=True)
+
+
+@window_latent_read.register_fake
+def _(q, k, v, window_pos, offsets, order):
+    return (q.new_empty(q.shape, dtype=torch.float32), q.new_empty(q.shape[:-1], dtype=torch.float32),
+            q.new_empty(q.shape[:-1], dtype=torch.float32))
+
+
+@torch.library.custom_op(f"{_NS}::window_latent_broadcast", mutates_args=())
+def window_latent_broadcast(q: Tensor, k: Tensor, v: Tensor, window_pos: Tensor, offsets: Tensor,
+                            order: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+    """Each window (N_w, heads, hd) attends over its position's four latents
+    (P, 4, heads, hd); fp32 (out, m, l)."""
+    if q.ndim != 3:
+        raise ValueError("broadcast q must have shape (N_w, heads, head_dim)")
+    if k.ndim != 4 or k.shape != v.shape or k.shape[1] != 4 or q.shape[1:] != k.shape[2:]:
+        raise ValueError("broadcast k and v must share shape (P, slots=4, heads, head_dim)")
+    if window_pos.ndim != 1 or window_pos.shape[0] != q.shape[0]:
+        raise ValueError("window_pos must have one entry per window")
+    _check_layout(offsets, order, k.shape[0], q.shape[0])
+    return ops.latent_broadcast(q, k, v, window_pos, stats=True)
+
+
+@window_latent_broadcast.register_fake
+def _(q, k, v, window_pos, offsets, order):
+    return (q.new_empty(q.shape, dtype=torch.float32), q.new_empty(q.shape[:-1], dtype=torch.float32),
+            q.new_empty(q.shape[:-1], dtype=torch.float32))
+
+
+# ----------------------------------------------------------------- action rows
+
+
+@torch.library.custom_op(f"{_NS}::action_row_encode", mutates_args=())
+def action_row_encode(pre_w: Tensor, table: Tensor, edge_window: Tensor, edge_class: Tensor, edge_cell: Tensor,
+                      edge_rev: Tensor, n_cells: int) -> Tensor:
+    """out[c] = sum over the cell-major run of c of
+    relu(pre_w[edge_window[e]] + table[edge_class[e]]), fp32; cells without
+    entries are zero."""
+    if pre_w.ndim != 2 or table.ndim != 2 or pre_w.shape[1] != table.shape[1]:
+        raise ValueError("pre_w and table must be (N, H) with one width")
+    idx = (edge_window, edge_class, edge_cell, edge_rev)
+    if edge_window.ndim != 1 or any(t.shape != edge_window.shape for t in idx):
+        raise ValueError("the edge views must have one length")
+    if n_cells < 0:
+        raise ValueError("n_cells must be nonnegative")
+    return ops.row_encode(pre_w, table, edge_window, edge_class, ops.runs_to_ptr(edge_cell, n_cells), n_cells)
+
+
+@action_row_encode.register_fake
+def _(pre_w, table, edge_window, edge_class, edge_cell, edge_rev, n_cells):
+    return pre_w.new_empty((n_cells, pre_w.shape[1]), dtype=torch.float32)
+
+
+# ----------------------------------------------------------------- table derivation
+
+
+@torch.library.custom_op(f"{_NS}::cell_tables", mutates_args=())
+def cell_tables(dec_cell: Tensor, dec_window: Tensor, dec_class: Tensor, n_windows: int, n_classes: int,
+                n_cells: int) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor,
+                                       Tensor, Tensor, Tensor]:
+    """The decoder incidence's twelve cell-, window- and class-major views."""
+    return tuple(tables.cell_tables(dec_cell, dec_window, dec_class, n_windows, n_classes, n_cells))
+
+
+@cell_tables.register_fake
+def _(dec_cell, dec_window, dec_class, n_windows, n_classes, n_cells):
+    ctx = torch.library.get_ctx()
+    n_cov = ctx.new_dynamic_size()
+    e = dec_cell.shape[0]
+    edges = lambda: dec_cell.new_empty((e,), dtype=torch.long)  # noqa: E731
+    return (dec_cell.new_empty((n_cov,), dtype=torch.long),
+            dec_cell.new_empty((n_cov + 1 if n_cells < 0 else n_cells + 1,), dtype=torch.long),
+            edges(), edges(), edges(), dec_cell.new_empty((n_windows + 1,), dtype=torch.long),
+            edges(), edges(), edges(), dec_cell.new_empty((n_classes + 1,), dtype=torch.long), edges(), edges())
+
+
+@torch.library.custom_op(f"{_NS}::cell_node_edge_tables", mutates_args=())
+def cell_node_edge_tables(src: Tensor, dst: Tensor, cls: Tensor, covered_destinations: Tensor, n_sources: int,
+                          n_destinations: int, n_classes: int, uncovered_only: bool
+                          ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor,
+                                     Tensor, Tensor, Tensor]:
+    """One typed edge family's twelve destination-, source- and class-major views."""
+    return tuple(tables.edge_tables(src, dst, cls, covered_destinations, n_sources, n_destinations, n_classes,
+                                    uncovered_only))
+
+
+@cell_node_edge_tables.register_fake
+def _(src, dst, cls, covered_destinations, n_sources, n_destinations, n_classes, uncovered_only):
+    ctx = torch.library.get_ctx()
+    n_cov = ctx.new_dynamic_size()
+    e = ctx.new_dynamic_size() if uncovered_only else src.shape[0]
+    edges = lambda: src.new_empty((e,), dtype=torch.long)  # noqa: E731
+    return (src.new_empty((n_cov,), dtype=torch.long), src.new_empty((n_destinations + 1,), dtype=torch.long),
+            edges(), edges(), edges(), src.new_empty((n_sources + 1,), dtype=torch.long), edges(), edges(),
+            edges(), src.new_empty((n_classes + 1,), dtype=torch.long), edges(), edges())
+
+
+@torch.library.custom_op(f"{_NS}::window_latent_layout", mutates_args=())
+def window_latent_layout(window_pos: Tensor, positions: int) -> tuple[Tensor, Tensor]:
+    """Position CSR offsets and the stable position-major window order."""
+    return tables.window_latent_layout(window_pos, positions)
+
+
+@window_latent_layout.register_fake
+def _(window_pos, positions):
+    return (window_pos.new_empty((positions + 1,), dtype=torch.long),
+            window_pos.new_empty(window_pos.shape, dtype=torch.long))
+
+
+OPERATORS = (
+    "fused_attention", "aggregate_to_windows", "aggregate_to_stones", "class_row_sum", "incidence_row_sum",
+    "cell_attention", "cell_attention_plain", "window_latent_read", "window_latent_broadcast",
+    "action_row_encode", "cell_tables", "cell_node_edge_tables", "window_latent_layout",
+)
+
+for _name in OPERATORS[:10]:
+    _register_inference_only(globals()[_name], _name)

@@ -17,8 +17,8 @@ What each function follows (python/mantisnet/mantisnet/...):
 * ``run_sum`` ................................. message_passing.py:102-118, 331-339
 * ``incidence_plan`` .......................... message_passing.py:495-517
 * ``cell_attention`` .......................... cell_latents.py:546-567
-* ``cell_tables`` ............................. cell_latents.py:96-165
-* ``edge_tables`` ............................. cell_nodes.py:23-94
+* ``cell_tables`` / ``cell_tables_full`` ...... cell_latents.py:96-165
+* ``edge_tables`` / ``edge_tables_full`` ...... cell_nodes.py:23-94
 * ``window_layout`` ........................... window_latents.py:38-56
 * ``latent_read`` / ``latent_broadcast`` ...... window_latents.py:102-129, 166-188
   (vectorised; ``latent_read_loops`` / ``latent_broadcast_loops`` are the
@@ -110,6 +110,57 @@ def cell_tables(dec_cell, dec_window, dec_class, n_windows, n_cells):
         edge_cell=edge_cell, win_ptr=win_ptr, edge_wcell=edge_cell[worder],
         edge_wclass=edge_class[worder], edge_wwin=edge_window[worder],
     )
+
+
+CELL_TABLE_FIELDS = ("covered", "cell_ptr", "edge_window", "edge_class", "edge_cell", "win_ptr", "edge_wcell",
+                     "edge_wclass", "edge_wwin", "cls_ptr", "cedge_cell", "cedge_win")
+EDGE_TABLE_FIELDS = ("covered", "dst_ptr", "edge_src", "edge_class", "edge_dst", "source_ptr", "edge_sdst",
+                     "edge_sclass", "edge_ssrc", "cls_ptr", "cedge_dst", "cedge_src")
+
+
+def cell_tables_full(dec_cell, dec_window, dec_class, n_windows, n_classes, n_cells=-1):
+    """All twelve views of ``mantisnet::cell_tables`` (cell_latents.py:96-165):
+    cell-major, window-major and class-major orders of the decoder incidence.
+    With n_cells < 0 covered cells are relabelled compactly 0..N_cov-1."""
+    order = torch.argsort(dec_cell, stable=True)
+    edge_window, edge_class = dec_window[order], dec_class[order]
+    covered, counts = torch.unique_consecutive(dec_cell[order], return_counts=True)
+    if n_cells < 0:
+        cell_ptr = torch.cat([torch.zeros(1, dtype=torch.long), counts.cumsum(0)])
+        edge_cell = torch.repeat_interleave(torch.arange(counts.numel()), counts)
+    else:
+        edge_cell = dec_cell[order]
+        cell_ptr = torch.searchsorted(edge_cell, torch.arange(n_cells + 1))
+    worder = torch.argsort(edge_window, stable=True)
+    win_ptr = torch.searchsorted(edge_window[worder], torch.arange(n_windows + 1))
+    edge_wclass = edge_class[worder]
+    cedge_cell = torch.argsort(edge_class.to(torch.int32), stable=True)
+    cedge_win = torch.argsort(edge_wclass.to(torch.int32), stable=True)
+    cls_ptr = torch.searchsorted(edge_class[cedge_cell], torch.arange(n_classes + 1))
+    return dict(zip(CELL_TABLE_FIELDS, (
+        covered, cell_ptr, edge_window, edge_class, edge_cell, win_ptr, edge_cell[worder], edge_wclass,
+        edge_window[worder], cls_ptr, cedge_cell, cedge_win)))
+
+
+def edge_tables_full(src, dst, cls, covered_destinations, n_sources, n_destinations, n_classes, uncovered_only):
+    """All twelve views of ``mantisnet::cell_node_edge_tables``
+    (cell_nodes.py:23-94): destination-, source- and class-major orders."""
+    if uncovered_only:
+        keep = ~torch.isin(dst, covered_destinations)
+        src, dst, cls = src[keep], dst[keep], cls[keep]
+    order = torch.argsort(dst, stable=True)
+    edge_dst, edge_src, edge_class = dst[order], src[order], cls[order]
+    covered = torch.unique_consecutive(edge_dst)
+    dst_ptr = torch.searchsorted(edge_dst, torch.arange(n_destinations + 1))
+    sorder = torch.argsort(edge_src, stable=True)
+    source_ptr = torch.searchsorted(edge_src[sorder], torch.arange(n_sources + 1))
+    edge_sclass = edge_class[sorder]
+    cedge_dst = torch.argsort(edge_class.to(torch.int32), stable=True)
+    cedge_src = torch.argsort(edge_sclass.to(torch.int32), stable=True)
+    cls_ptr = torch.searchsorted(edge_class[cedge_dst], torch.arange(n_classes + 1))
+    return dict(zip(EDGE_TABLE_FIELDS, (
+        covered, dst_ptr, edge_src, edge_class, edge_dst, source_ptr, edge_dst[sorder], edge_sclass,
+        edge_src[sorder], cls_ptr, cedge_dst, cedge_src)))
 
 
 def edge_tables(src, dst, cls, covered, n_dst, uncovered_only):

@@ -1,0 +1,48 @@
+"""The C-ABI libraries load and export every function their headers declare
+(CPU: no kernel is launched), and the ctypes signature table agrees with the
+header's parameter lists."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from mantisnet import _hip_api, _native
+
+INCLUDE = Path(__file__).resolve().parents[1] / "include"
+
+
+def _declarations(header: str) -> dict[str, int]:
+    """Function name -> parameter count for every prototype in the header."""
+    text = (INCLUDE / header).read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    text = re.sub(r"//[^\n]*", "", text)
+    out = {}
+    for m in re.finditer(r"\b(?:int32_t|void)\s+(\w+)\s*\(([^)]*)\)\s*;", text):
+        params = m.group(2).strip()
+        out[m.group(1)] = 0 if params in ("", "void") else params.count(",") + 1
+    return out
+
+
+@pytest.mark.parametrize("header,lib", [("hexo_encoder.h", _native.ENCODER_LIB), ("mantis_hip.h", _native.HIP_LIB)])
+def test_library_exports_every_declared_symbol(header, lib):
+    decls = _declarations(header)
+    assert len(decls) >= 9, decls
+    so = ctypes.CDLL(str(lib))
+    missing = [name for name in decls if not hasattr(so, name)]
+    assert not missing, missing
+
+
+def test_ctypes_signatures_match_header():
+    decls = _declarations("mantis_hip.h")
+    assert set(_hip_api.SIGNATURES) == set(decls)
+    for name, (args, _res) in _hip_api.SIGNATURES.items():
+        assert len(args) == decls[name], name
+
+
+def test_versions_answer_without_a_gpu():
+    assert _native.encoder().hexo_repr_version() == 9
+    assert _native.hip().mantis_hip_version() > 0
