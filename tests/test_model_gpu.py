@@ -99,3 +99,35 @@ def test_pyo3_style_single_argument_call_raises_like_the_reference(device):
     batch = collate_positions(synthetic.random_games(1, 1)).to(device)
     with pytest.raises(TypeError):
         net(batch)
+
+
+def test_forward_is_d6_invariant_to_fp16_tolerance(device):
+    # the reference holds exact D6 invariance to 1e-5 in fp32
+    # (test_symmetry.py:23-45); the fp16-operand path holds it to the policy
+    # and value tolerances above
+    from oracle import encoder as E
+
+    net = _model(device, seed=4)
+    moves = [(0, 0), (3, 0), (-2, 2), (0, 3), (1, -2), (-1, 3), (4, -4), (-3, 0)]
+
+    def rot(m, k):
+        q, r = m
+        for _ in range(k):
+            q, r = -r, q + r
+        return q, r
+
+    transforms = [lambda m, k=k: rot(m, k) for k in range(1, 6)] + [lambda m, k=k: rot((m[1], m[0]), k)
+                                                                     for k in range(6)]
+    games = [moves] + [[t(m) for m in moves] for t in transforms]
+    with torch.no_grad():
+        out = net(collate_positions(games).to(device), 0.2)
+    pol = out.policy_logits.cpu()
+    n = E.Replayed(moves).legal_qr.shape[0]
+    base = dict(zip(map(tuple, E.Replayed(moves).legal_qr.tolist()), pol[:n].tolist()))
+    off = n
+    for t, g in zip(transforms, games[1:]):
+        legal = E.Replayed(g).legal_qr
+        got = dict(zip(map(tuple, legal.tolist()), pol[off:off + legal.shape[0]].tolist()))
+        off += legal.shape[0]
+        assert max(abs(got[t(m)] - v) for m, v in base.items()) <= 1e-2
+    assert (out.value - out.value[0]).abs().max().item() <= 2e-3
