@@ -54,6 +54,8 @@ def _args():
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-isolated", action="store_true", help="skip the isolated attention/message-passing lines")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="only copy MIB mebibytes device-to-device once and exit (HBM counter calibration)")
     return ap.parse_args()
 
 
@@ -176,9 +178,19 @@ def main() -> int:
         return 2
     import torch
 
+    dev = torch.device("cuda:0")
+    if args.copy_probe:
+        n = args.copy_probe * 2**20 // 4
+        x = torch.ones(n, dtype=torch.float32, device=dev)
+        y = torch.empty_like(x)
+        torch.cuda.synchronize()
+        y.copy_(x)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes_read": 4 * n, "copy_probe_bytes_written": 4 * n}), flush=True)
+        return 0
+
     from mantisnet import PRODUCTION, MantisNet, collate_positions, ops, synthetic
 
-    dev = torch.device("cuda:0")
     torch.manual_seed(0)
     net = MantisNet(PRODUCTION)
     net.load_state_dict(synthetic.perturbed_state_dict(net, seed=0))
@@ -203,7 +215,7 @@ def main() -> int:
         torch.cuda.synchronize()
         ops.raise_on_device_error(dev)
         _log(f"warm-up done ({args.warmup} steps)")
-        traced = ("cell_attention", "fused_linear_proj", "fused_linear_residual", "fused_linear_mlp")
+        traced = ("cell_attention", "fused_linear")
         per_step = []
         with ops.trace(*traced) as tr:
             torch.cuda.synchronize()
@@ -230,7 +242,7 @@ def main() -> int:
         "peak": HBM_PEAK_GBPS,
         "unit": "GB/s",
         "frac": round(dom["gbps"] / HBM_PEAK_GBPS, 4),
-        "traffic": (traffic or {}).get(dom_name),
+        "traffic": ((traffic or {}).get(dom_name) or {}).get("bytes"),
         "avg_us": round(dom["avg_us"], 2),
         "launches_per_step": dom["launches"] // args.steps,
         "share_of_step": round(dom["total_ms"] / args.steps / ms, 4),

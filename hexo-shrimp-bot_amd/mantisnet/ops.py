@@ -35,14 +35,20 @@ class trace:
     """Time chosen kernels with HIP events on the launching stream.
 
     ``with ops.trace("cell_attention") as t: ...`` records, for every launch
-    of a named kernel inside the block, a start/end event pair plus the
-    launch's algorithmic bytes and flops; ``t.summary()`` synchronises and
-    returns per-kernel launch counts, average duration and achieved rates.
+    whose kernel name starts with one of the given prefixes, a start/end
+    event pair plus the launch's algorithmic bytes and flops.  Names
+    distinguish kernel instantiations (e.g. ``cell_attention_vcls``,
+    ``fused_linear_proj_f32_n256``), so each summary line covers one
+    compiled kernel.  ``t.summary()`` synchronises and returns per-kernel
+    launch counts, average duration and achieved rates.
     """
 
-    def __init__(self, *names: str):
-        self.names = set(names)
-        self.records: dict[str, list] = {n: [] for n in names}
+    def __init__(self, *prefixes: str):
+        self.prefixes = tuple(prefixes)
+        self.records: dict[str, list] = {}
+
+    def wants(self, name: str) -> bool:
+        return name.startswith(self.prefixes)
 
     def __enter__(self):
         global _TRACE
@@ -78,15 +84,18 @@ class trace:
 
 def _launch(name: str, nbytes: float, flops: float, fn):
     t = _TRACE
-    if t is None or name not in t.names:
+    if t is None or not t.wants(name):
         return fn()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     e0.record()
     res = fn()
     e1.record()
-    t.records[name].append((e0, e1, float(nbytes), float(flops)))
+    t.records.setdefault(name, []).append((e0, e1, float(nbytes), float(flops)))
     return res
+
+
+_SHORT = {torch.float32: "f32", torch.float16: "f16", torch.bfloat16: "bf16"}
 
 
 def _dt(t: Tensor) -> int:
@@ -267,7 +276,7 @@ def cell_attention(q: Tensor, k: Tensor, v: Tensor, bias: Tensor, vcls: Tensor |
         nbytes = n_q * (128 * q.element_size() + 128 * out.element_size() + 8) + e * 16 + \
             k.shape[0] * 128 * (k.element_size() + v.element_size())
         flops = e * 4 * 128 * 2  # score dot + weighted value sum per edge and head
-        _launch("cell_attention", nbytes, flops, lambda: _check(
+        _launch("cell_attention_vcls" if vcls is not None else "cell_attention_plain", nbytes, flops, lambda: _check(
             _lib().mantis_cell_attention(
                 _ptr(q), _ptr(k), _ptr(v), _dt(q), ldq, ldk, ldv, _ptr(bias), bias.shape[1], _ptr(vcls),
                 _ptr(seg_ptr), _ptr(src), _ptr(cls), e, n_q, k.shape[0], heads, hd,
@@ -505,7 +514,8 @@ def fused_linear(x: Tensor, w1: Tensor, b1: Tensor | None = None, *, layer_norm:
         (n1 * 4 if add1 is not None else 0) + width * out.element_size() * (2 if residual else 1)
     nbytes = m * row_bytes + w1.numel() * 2 * (2 if w2 is not None else 1) + (w3.numel() * 2 if w3 is not None else 0)
     flops = 2 * m * (128 * n1 * (2 if w2 is not None else 1) + (n1 * width if w3 is not None else 0))
-    name = "fused_linear" + ("_mlp" if w3 is not None else ("_residual" if residual else "_proj"))
+    kind = "mlp" if w3 is not None else ("residual" if residual else "proj")
+    name = f"fused_linear_{kind}_{_SHORT[x.dtype]}" + (f"_{_SHORT[x2.dtype]}" if x2 is not None else "") + f"_n{n1}"
     st = _launch(name, nbytes, flops, lambda: _lib().mantis_fused_linear(
         _ptr(x), _dt(x), x.stride(0), _ptr(x_rows), x.shape[0], m, int(layer_norm),
         _ptr(x2), _dt(x2) if x2 is not None else 0, x2.stride(0) if x2 is not None else 0,
