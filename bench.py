@@ -41,6 +41,15 @@ for _p in (str(ROOT), str(ROOT / "hexo-shrimp-bot_amd")):
 
 HBM_PEAK_GBPS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0
+# GPU-side spin before an isolated timing loop: the host enqueues every
+# launch while the device is held, so the per-launch events bracket kernels
+# that run back to back instead of host launch gaps.
+HOLD_CYCLES = 20_000_000
+
+
+def _hold(torch):
+    torch.cuda.synchronize()
+    torch.cuda._sleep(HOLD_CYCLES)
 
 
 def _args():
@@ -54,6 +63,8 @@ def _args():
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-isolated", action="store_true", help="skip the isolated attention/message-passing lines")
+    ap.add_argument("--isolated-only", action="store_true",
+                    help="run only the isolated attention and message-passing lines (for kernel profiling)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only copy MIB mebibytes device-to-device once and exit (HBM counter calibration)")
     return ap.parse_args()
@@ -90,6 +101,7 @@ def isolated_attention(torch, ops, dev, reps=20):
         ops.register_seq_lens(sl)
         for _ in range(3):
             ops.stone_attention(*qkv, sl)
+        _hold(torch)
         with ops.trace("stone_attention") as tr:
             for _ in range(reps):
                 ops.stone_attention(*qkv, sl)
@@ -129,6 +141,7 @@ def isolated_message_passing(torch, ops, dev, reps=20):
     nbr = ops.hex_neighbours(qr, gptr)
     for _ in range(3):
         ops.hex_aggregate_linear(x, nbr, w, bias)
+    _hold(torch)
     with ops.trace("hex_aggregate_linear") as tr:
         for _ in range(reps):
             ops.hex_aggregate_linear(x, nbr, w, bias)
@@ -190,6 +203,11 @@ def main() -> int:
         return 0
 
     from mantisnet import PRODUCTION, MantisNet, collate_positions, ops, synthetic
+
+    if args.isolated_only:
+        print(json.dumps({"attention": isolated_attention(torch, ops, dev),
+                          "message_passing": isolated_message_passing(torch, ops, dev)}), flush=True)
+        return 0
 
     torch.manual_seed(0)
     net = MantisNet(PRODUCTION)

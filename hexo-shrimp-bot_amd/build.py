@@ -25,6 +25,9 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 HIP_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in VGPRs (the unified register file), not AGPRs: saves the
+    # accvgpr copies between the matrix products and the softmax/epilogue math
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 
 

@@ -20,6 +20,27 @@ __device__ __forceinline__ uint16_t f2bf(float f) {
   return uint16_t(u >> 16);
 }
 
+// Two fp32 values narrowed as one packed pair (low half first): a single
+// v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32 on gfx950, round to nearest even.
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
+}
+
+// fp16 pair without saturation: for values known to lie in fp16 range
+// (softmax probabilities, convex combinations of fp16 rows).
+__device__ __forceinline__ uint32_t pack_f16x2_unit(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, f16x2_t));
+}
+
+// fp16 pair saturating at the largest finite fp16 instead of overflowing.
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
+  return pack_f16x2_unit(fminf(fmaxf(lo, -65504.f), 65504.f), fminf(fmaxf(hi, -65504.f), 65504.f));
+}
+
 // Eight consecutive elements of a row as fp32: one 16-byte load for bf16,
 // two for fp32.  `p` must be 16-byte aligned.
 __device__ __forceinline__ void load8(const uint16_t* p, float (&x)[8]) {
@@ -69,10 +90,10 @@ __device__ __forceinline__ void store8(float* p, const float (&x)[8]) {
 
 __device__ __forceinline__ void store8(uint16_t* p, const float (&x)[8]) {
   uint4 u;
-  u.x = uint32_t(f2bf(x[0])) | (uint32_t(f2bf(x[1])) << 16);
-  u.y = uint32_t(f2bf(x[2])) | (uint32_t(f2bf(x[3])) << 16);
-  u.z = uint32_t(f2bf(x[4])) | (uint32_t(f2bf(x[5])) << 16);
-  u.w = uint32_t(f2bf(x[6])) | (uint32_t(f2bf(x[7])) << 16);
+  u.x = pack_bf16x2(x[0], x[1]);
+  u.y = pack_bf16x2(x[2], x[3]);
+  u.z = pack_bf16x2(x[4], x[5]);
+  u.w = pack_bf16x2(x[6], x[7]);
   *reinterpret_cast<uint4*>(p) = u;
 }
 

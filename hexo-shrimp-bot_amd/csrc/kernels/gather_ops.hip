@@ -8,6 +8,8 @@
 // 4 heads x 32 dims a head is 4 consecutive lanes, so a per-head dot product
 // is an 8-term FMA chain plus two xor-shuffles — no LDS, no atomics; every
 // reduction runs in a fixed order and is bitwise deterministic.
+#include <algorithm>
+
 #include "common.hpp"
 
 namespace mantis {
@@ -101,84 +103,244 @@ run_reduce_scalar_kernel(const Tin* __restrict__ values, int64_t n_src, int64_t 
 
 // ------------------------------------------------------------ typed attention
 
-template <typename Tin, typename Tout, bool kVcls>
+// An 8-element row chunk held in its storage format until the math needs
+// it, so a batch of rows can be requested before any is converted.
+template <typename T>
+struct Chunk8 {
+  float f[8];
+  __device__ __forceinline__ void load(const T* p) { load8(p, f); }
+  __device__ __forceinline__ float operator[](int i) const { return f[i]; }
+};
+
+template <>
+struct Chunk8<uint16_t> {  // bf16
+  uint4 u;
+  __device__ __forceinline__ void load(const uint16_t* p) { u = *reinterpret_cast<const uint4*>(p); }
+  __device__ __forceinline__ float operator[](int i) const {
+    const uint32_t w = (i < 2) ? u.x : (i < 4) ? u.y : (i < 6) ? u.z : u.w;
+    return __uint_as_float((i & 1) ? (w & 0xffff0000u) : (w << 16));
+  }
+};
+
+template <>
+struct Chunk8<_Float16> {
+  uint4 u;
+  __device__ __forceinline__ void load(const _Float16* p) { u = *reinterpret_cast<const uint4*>(p); }
+  __device__ __forceinline__ float operator[](int i) const {
+    typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+    return float(__builtin_bit_cast(h8, u)[i]);
+  }
+};
+
+// Per-edge arithmetic on row chunks.  The generic forms widen every
+// element; the fp16 forms work on the packed pairs: the q.k partial dot is
+// four v_dot2 (fp16 pairs, fp32 accumulate) and the value update folds the
+// widening into v_fma_mix.
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+
+template <typename T>
+__device__ __forceinline__ float chunk_dot(const Chunk8<T>& a, const Chunk8<T>& b) {
+  float d = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) d = fmaf(a[i], b[i], d);
+  return d;
+}
+
+__device__ __forceinline__ float chunk_dot(const Chunk8<_Float16>& a, const Chunk8<_Float16>& b) {
+  float d = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_t, a.u.x), __builtin_bit_cast(h2_t, b.u.x), 0.f, false);
+  d = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_t, a.u.y), __builtin_bit_cast(h2_t, b.u.y), d, false);
+  d = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_t, a.u.z), __builtin_bit_cast(h2_t, b.u.z), d, false);
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_t, a.u.w), __builtin_bit_cast(h2_t, b.u.w), d, false);
+}
+
+// acc[i] += p * (v[i] (+ c[i]))
+template <bool kAdd, typename T, typename Tv>
+__device__ __forceinline__ void chunk_axpy(float (&acc)[8], float p, const Chunk8<T>& v, const Chunk8<Tv>& c) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float val = v[i];
+    if constexpr (kAdd) val += c[i];
+    acc[i] = fmaf(p, val, acc[i]);
+  }
+}
+
+template <bool kAdd>
+__device__ __forceinline__ void chunk_axpy(float (&acc)[8], float p, const Chunk8<_Float16>& v,
+                                           const Chunk8<_Float16>& c) {
+  // two v_fma_mix per element keep the class-value sum in fp32
+  const uint32_t vw[4] = {v.u.x, v.u.y, v.u.z, v.u.w};
+  const uint32_t cw[4] = {c.u.x, c.u.y, c.u.z, c.u.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const h2_t vv = __builtin_bit_cast(h2_t, vw[i]);
+    acc[2 * i] = fmaf(p, float(vv[0]), acc[2 * i]);
+    acc[2 * i + 1] = fmaf(p, float(vv[1]), acc[2 * i + 1]);
+    if constexpr (kAdd) {
+      const h2_t cv = __builtin_bit_cast(h2_t, cw[i]);
+      acc[2 * i] = fmaf(p, float(cv[0]), acc[2 * i]);
+      acc[2 * i + 1] = fmaf(p, float(cv[1]), acc[2 * i + 1]);
+    }
+  }
+}
+
+// One 16-lane group per query row, rows visited grid-stride.  The group
+// reads up to 16 of a row's (src, cls) entries at once — one per lane — and
+// broadcasts them with shuffles; the k, v (and class-value) rows of kBatch
+// entries are requested before any score is formed.  Rows are software
+// pipelined: while row r computes, the entry indices of the next row and
+// the CSR pointers and query chunk of the one after are already in flight,
+// so the three dependent round trips of a row (pointers -> indices -> rows)
+// overlap the previous rows' work.  Loads are issued in the order their
+// results are needed (the current batch's rows first, then the
+// prefetches), which the in-order completion counter requires.
+constexpr int kBatch = 4;
+
+template <typename Tin, typename Tout, bool kVcls, typename Tv>
 __global__ void __launch_bounds__(kBlock)
 cell_attention_kernel(const Tin* __restrict__ q, const Tin* __restrict__ k,
                       const Tin* __restrict__ v, int64_t ldq, int64_t ldk, int64_t ldv,
                       const float* __restrict__ bias, int64_t n_classes,
-                      const float* __restrict__ vcls, const int64_t* __restrict__ seg_ptr,
+                      const Tv* __restrict__ vcls, const int64_t* __restrict__ seg_ptr,
                       const int64_t* __restrict__ src, const int64_t* __restrict__ cls,
                       int64_t n_q, int64_t n_k, int64_t n_entries, float scale,
                       Tout* __restrict__ out, float* __restrict__ m_out,
                       float* __restrict__ l_out, int32_t* flag) {
-  const int64_t row = int64_t(blockIdx.x) * kGroupsPerBlock + threadIdx.x / kGroup;
   const int lane = threadIdx.x % kGroup;
   const int head = lane >> 2;
+  const int64_t stride = int64_t(gridDim.x) * kGroupsPerBlock;
+  int64_t row = int64_t(blockIdx.x) * kGroupsPerBlock + threadIdx.x / kGroup;
   if (row >= n_q) return;
-  float qv[8];
-  load8(q + row * ldq + lane * 8, qv);
-  int64_t start, end;
-  segment(seg_ptr, row, n_entries, start, end);
-  float m = -INFINITY, l = 0.f;
-  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  // one edge's score and value row; an out-of-range index scores -inf
-  auto edge = [&](int64_t e, float (&vv)[8]) -> float {
-    int64_t s = src[e], c = cls[e];
-    const bool ok = s >= 0 && s < n_k && c >= 0 && c < n_classes;
-    if (!ok) {
-      raise_flag(flag, MANTIS_FLAG_INDEX);
-      s = 0;
-      c = 0;
-    }
-    float kv[8];
-    load8(k + s * ldk + lane * 8, kv);
-    load8(v + s * ldv + lane * 8, vv);
-    float dot = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) dot = fmaf(qv[i], kv[i], dot);
-    const float score = head_sum(dot) * scale + bias[head * n_classes + c];
-    if constexpr (kVcls) {
-      float cv[8];
-      load8(vcls + c * kRow + lane * 8, cv);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) vv[i] += cv[i];
-    }
-    return ok ? score : -INFINITY;
+
+  auto clamp_seg = [&](int64_t a, int64_t b, int64_t& st, int64_t& en) {
+    a = a < 0 ? 0 : (a > n_entries ? n_entries : a);
+    b = b < a ? a : (b > n_entries ? n_entries : b);
+    st = a;
+    en = b;
   };
-  // two edges in flight per step: both rows' loads issue before either's math
-  int64_t e = start;
-  for (; e + 1 < end; e += 2) {
-    float v0[8], v1[8];
-    const float s0 = edge(e, v0), s1 = edge(e + 1, v1);
-    const float m_new = fmaxf(m, fmaxf(s0, s1));
-    if (m_new == -INFINITY) continue;
-    const float alpha = __expf(m - m_new);
-    const float p0 = __expf(s0 - m_new), p1 = __expf(s1 - m_new);
-    l = l * alpha + p0 + p1;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] = fmaf(p1, v1[i], fmaf(p0, v0[i], acc[i] * alpha));
-    m = m_new;
-  }
-  if (e < end) {
-    float v0[8];
-    const float s0 = edge(e, v0);
-    const float m_new = fmaxf(m, s0);
-    if (m_new != -INFINITY) {
-      const float alpha = __expf(m - m_new);
-      const float p0 = __expf(s0 - m_new);
-      l = l * alpha + p0;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i] = fmaf(p0, v0[i], acc[i] * alpha);
-      m = m_new;
+  // raw index pair of entry e (lane-distributed), validated when consumed
+  auto fetch_idx = [&](int64_t e, int64_t en, int64_t& rs, int64_t& rc) {
+    if (e < en) {
+      rs = src[e];
+      rc = cls[e];
+    } else {
+      rs = -1;
+      rc = -1;
     }
+  };
+
+  // pipeline registers: cur (being computed), nxt (pointers + query known,
+  // indices in flight), nx2 (pointers + query in flight)
+  Chunk8<Tin> q_cur, q_nxt, q_nx2;
+  int64_t pa_nxt = 0, pb_nxt = 0, pa_nx2 = 0, pb_nx2 = 0;
+  int64_t st_cur, en_cur, st_nxt = 0, en_nxt = 0;
+  int64_t rs_cur, rc_cur, rs_nxt = -1, rc_nxt = -1;
+
+  // prologue: row, then the next two rows' pointers and query chunks
+  q_cur.load(q + row * ldq + lane * 8);
+  clamp_seg(seg_ptr[row], seg_ptr[row + 1], st_cur, en_cur);
+  fetch_idx(st_cur + lane, en_cur, rs_cur, rc_cur);
+  int64_t nxt = row + stride, nx2 = row + 2 * stride;
+  if (nxt < n_q) {
+    q_nxt.load(q + nxt * ldq + lane * 8);
+    pa_nxt = seg_ptr[nxt];
+    pb_nxt = seg_ptr[nxt + 1];
   }
-  const float inv = l > 0.f ? 1.f / l : 1.f;
+  if (nx2 < n_q) {
+    q_nx2.load(q + nx2 * ldq + lane * 8);
+    pa_nx2 = seg_ptr[nx2];
+    pb_nx2 = seg_ptr[nx2 + 1];
+  }
+  if (nxt < n_q) {
+    clamp_seg(pa_nxt, pb_nxt, st_nxt, en_nxt);
+    fetch_idx(st_nxt + lane, en_nxt, rs_nxt, rc_nxt);
+  }
+
+  while (true) {
+    float m = -INFINITY, l = 0.f;
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int64_t base = st_cur; base < en_cur; base += kGroup) {
+      const int cnt = int(en_cur - base < kGroup ? en_cur - base : kGroup);
+      if (base != st_cur) fetch_idx(base + lane, en_cur, rs_cur, rc_cur);  // long segments only
+      int32_t my_s = 0, my_c = 0, my_ok = 0;
+      if (lane < cnt) {
+        if (rs_cur >= 0 && rs_cur < n_k && rc_cur >= 0 && rc_cur < n_classes) {
+          my_s = int32_t(rs_cur);
+          my_c = int32_t(rc_cur);
+          my_ok = 1;
+        } else {
+          raise_flag(flag, MANTIS_FLAG_INDEX);
+        }
+      }
+      for (int j = 0; j < cnt; j += kBatch) {
+        Chunk8<Tin> kc[kBatch], vc[kBatch];
+        Chunk8<Tv> cc[kBatch];
+        float bs[kBatch];
+        bool ok[kBatch];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) acc[i] *= inv;
-  store8(out + row * kRow + lane * 8, acc);
-  if ((lane & 3) == 0) {
-    if (m_out) m_out[row * 4 + head] = m;
-    if (l_out) l_out[row * 4 + head] = l;
+        for (int u = 0; u < kBatch; ++u) {
+          const int idx = j + u < kGroup ? j + u : kGroup - 1;
+          const int s_ = __shfl(my_s, idx, kGroup), c_ = __shfl(my_c, idx, kGroup);
+          ok[u] = j + u < cnt && __shfl(my_ok, idx, kGroup) != 0;
+          // element offsets fit 32 bits (checked by the host)
+          const uint32_t sr = ok[u] ? uint32_t(s_) : 0u, cr = ok[u] ? uint32_t(c_) : 0u;
+          kc[u].load(k + (sr * uint32_t(ldk) + uint32_t(lane * 8)));
+          vc[u].load(v + (sr * uint32_t(ldv) + uint32_t(lane * 8)));
+          bs[u] = bias[uint32_t(head) * uint32_t(n_classes) + cr];
+          if constexpr (kVcls) cc[u].load(vcls + (cr * uint32_t(kRow) + uint32_t(lane * 8)));
+        }
+        float sc[kBatch];
+        float m_new = m;
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+          sc[u] = ok[u] ? fmaf(head_sum(chunk_dot(q_cur, kc[u])), scale, bs[u]) : -INFINITY;
+          m_new = fmaxf(m_new, sc[u]);
+        }
+        if (m_new == -INFINITY) continue;  // nothing valid yet
+        const float alpha = __expf(m - m_new);
+        float pr[kBatch];
+        l *= alpha;
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+          pr[u] = __expf(sc[u] - m_new);
+          l += pr[u];
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] *= alpha;
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) chunk_axpy<kVcls>(acc, pr[u], vc[u], cc[u]);
+        m = m_new;
+      }
+    }
+    const float inv = l > 0.f ? 1.f / l : 1.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] *= inv;
+    store8(out + row * kRow + lane * 8, acc);
+    if ((lane & 3) == 0) {
+      if (m_out) m_out[row * 4 + head] = m;
+      if (l_out) l_out[row * 4 + head] = l;
+    }
+    // rotate the pipeline
+    row = nxt;
+    if (row >= n_q) break;
+    q_cur = q_nxt;
+    st_cur = st_nxt;
+    en_cur = en_nxt;
+    rs_cur = rs_nxt;
+    rc_cur = rc_nxt;
+    nxt = nx2;
+    q_nxt = q_nx2;
+    pa_nxt = pa_nx2;
+    pb_nxt = pb_nx2;
+    nx2 = nxt + stride;
+    if (nxt < n_q) {
+      clamp_seg(pa_nxt, pb_nxt, st_nxt, en_nxt);
+      fetch_idx(st_nxt + lane, en_nxt, rs_nxt, rc_nxt);
+    }
+    if (nx2 < n_q) {
+      q_nx2.load(q + nx2 * ldq + lane * 8);
+      pa_nx2 = seg_ptr[nx2];
+      pb_nx2 = seg_ptr[nx2 + 1];
+    }
   }
 }
 
@@ -362,6 +524,34 @@ row_encode_kernel(const Tin* __restrict__ pre, int64_t n_w, const float* __restr
 
 inline unsigned grid_rows(int64_t rows) { return unsigned((rows + kGroupsPerBlock - 1) / kGroupsPerBlock); }
 
+// Workgroups of `kernel` that are resident on the whole device at once
+// (CUs x occupancy), computed once per kernel instantiation.  Grid-stride
+// kernels launch exactly this many, so no workgroup waits for a slot and
+// every group's pipeline stays full until the rows run out.
+template <typename K>
+unsigned resident_grid(K kernel) {
+  static unsigned cached = 0;
+  if (cached == 0) {
+    int dev = 0, cus = 0, per = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, kBlock, 0) != hipSuccess || cus <= 0 ||
+        per <= 0) {
+      cus = 256;
+      per = 2;
+    }
+    cached = unsigned(cus) * unsigned(per);
+  }
+  return cached;
+}
+
+// Launch a grid-stride row kernel on min(rows / 16, resident) workgroups.
+template <typename K, typename... A>
+void launch_rows(K kernel, int64_t rows, dim3 block, hipStream_t s, A... args) {
+  const unsigned grid = std::min(grid_rows(rows), resident_grid(kernel));
+  kernel<<<dim3(grid), block, 0, s>>>(args...);
+}
+
 // Row strides of 128-wide operand rows: whole rows, 16-byte aligned.
 inline bool lds_ok(int64_t a, int64_t b, int64_t c) {
   return a >= kRow && b >= kRow && c >= kRow && a % 8 == 0 && b % 8 == 0 && c % 8 == 0;
@@ -428,7 +618,8 @@ int32_t mantis_run_reduce(const void* values, int32_t values_dtype, int64_t n_sr
 }
 
 int32_t mantis_cell_attention(const void* q, const void* k, const void* v, int32_t dtype,
-                              int64_t ldq, int64_t ldk, int64_t ldv, const float* bias, int64_t n_classes, const float* vcls,
+                              int64_t ldq, int64_t ldk, int64_t ldv, const float* bias, int64_t n_classes,
+                              const void* vcls, int32_t vcls_dtype,
                               const int64_t* seg_ptr, const int64_t* src, const int64_t* cls,
                               int64_t n_entries, int64_t n_q, int64_t n_k, int32_t heads,
                               int32_t hd, void* out, int32_t out_dtype, float* m, float* l,
@@ -440,25 +631,36 @@ int32_t mantis_cell_attention(const void* q, const void* k, const void* v, int32
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out) ||
       (vcls && !aligned16(vcls)) || !lds_ok(ldq, ldk, ldv))
     return MANTIS_E_ARG;
-  if (n_entries < 0 || (n_entries > 0 && (!src || !cls))) return MANTIS_E_ARG;
+  if (n_entries < 0 || (n_entries > 0 && (!src || !cls || n_k <= 0))) return MANTIS_E_ARG;
+  // gathered rows are addressed with 32-bit element offsets
+  auto fits32 = [](int64_t rows, int64_t ld) { return rows <= 0 || (rows - 1) * ld + kRow <= 4294967295LL; };
+  if (n_k > 2147483647LL || !fits32(n_k, ldk) || !fits32(n_k, ldv) || !fits32(n_classes, kRow) ||
+      4 * n_classes > 4294967295LL)
+    return MANTIS_E_ARG;
   const float scale = 1.0f / sqrtf(float(hd));
   hipStream_t s = as_stream(stream);
-  const dim3 grid(grid_rows(n_q)), block(kBlock);
+  const dim3 block(kBlock);
   if (out_dtype != MANTIS_F32 && out_dtype != MANTIS_F16) return MANTIS_E_ARG;
+  if (vcls && vcls_dtype != MANTIS_F32 && vcls_dtype != MANTIS_F16) return MANTIS_E_ARG;
   const bool ok = with_type(dtype, [&](auto t) {
     using T = decltype(t);
     auto go = [&](auto o) {
       using TO = decltype(o);
       TO* op = static_cast<TO*>(out);
-      if (vcls)
-        cell_attention_kernel<T, TO, true><<<grid, block, 0, s>>>(
+      if (vcls && vcls_dtype == MANTIS_F16)
+        launch_rows(cell_attention_kernel<T, TO, true, _Float16>, n_q, block, s,
             static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v), ldq, ldk,
-            ldv, bias, n_classes, vcls, seg_ptr, src, cls, n_q, n_k, n_entries, scale, op, m, l,
-            err_flag);
+            ldv, bias, n_classes, static_cast<const _Float16*>(vcls), seg_ptr, src, cls, n_q, n_k,
+            n_entries, scale, op, m, l, err_flag);
+      else if (vcls)
+        launch_rows(cell_attention_kernel<T, TO, true, float>, n_q, block, s,
+            static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v), ldq, ldk,
+            ldv, bias, n_classes, static_cast<const float*>(vcls), seg_ptr, src, cls, n_q, n_k,
+            n_entries, scale, op, m, l, err_flag);
       else
-        cell_attention_kernel<T, TO, false><<<grid, block, 0, s>>>(
+        launch_rows(cell_attention_kernel<T, TO, false, float>, n_q, block, s,
             static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v), ldq, ldk,
-            ldv, bias, n_classes, vcls, seg_ptr, src, cls, n_q, n_k, n_entries, scale, op, m, l,
+            ldv, bias, n_classes, nullptr, seg_ptr, src, cls, n_q, n_k, n_entries, scale, op, m, l,
             err_flag);
     };
     if (out_dtype == MANTIS_F16) go(_Float16{});

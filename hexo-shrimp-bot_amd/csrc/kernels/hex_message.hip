@@ -6,16 +6,7 @@
 // binary search inside the graph's own slice — no hashing, bit-exact with the
 // reference adjacency rule (encoder.rs:1001-1026).
 //
-// Aggregate + linear: one wavefront per 16 cells.  Each lane gathers, for
-// its cell (lane % 16), the dims {32ks + 8g .. +8} of every present
-// neighbour row (16-byte bf16 loads, fp32 sums) — exactly the B-fragment
-// chunks of agg^T for the four 32-wide K steps — then the products
-//   out^T (16 outs x 16 cells) = W (16 x 128) . agg^T (128 x 16)
-// run as 8 output tiles x 4 K steps of v_mfma_f32_16x16x32_bf16 for the sum
-// and the mean.  The D fragment gives each lane four consecutive output
-// features of one cell, stored as one 8-byte write.  HBM traffic is the
-// compulsory minimum (x once, the table once, both outputs once); repeated
-// neighbour reads hit L2.
+// Aggregate + linear: see hex_aggregate_linear_kernel.
 #include "common.hpp"
 #include "mfma.hpp"
 
@@ -63,76 +54,117 @@ __global__ void hex_neighbours_kernel(const int32_t* __restrict__ qr,
   }
 }
 
+// One wavefront per tile of 16 cells; 4 wavefronts per workgroup share the
+// layer, staged once per workgroup in LDS.
+//
+// Gather: the wavefront works in row layout — 16 lanes per cell, 8 dims per
+// lane — so every 16-byte load of a neighbour row is part of a 256-byte
+// contiguous row read (4 full rows per load instruction).  All 24 loads of
+// the tile (4 passes x 6 neighbours) are issued before any is consumed;
+// a missing neighbour reads the cell's own row and is masked in the fp32
+// sum.  The sums go to LDS as bf16, where the MFMA B fragments of sum^T are
+// read back (lane = cell l16, dims 32ks + 8g .. +8).
+//
+// Product: y^T (16 outs x 16 cells) = W (16 x 128) . sum^T (128 x 16), one
+// per output tile, serves both outputs by linearity:
+//   out_sum = y + b,   out_mean = y / count + b   (0 neighbours: b).
+// LDS rows are padded to 272 bytes so the 16 rows of a fragment read fall in
+// distinct banks.  HBM traffic is the compulsory minimum (x once, the table
+// once, both outputs once); repeated neighbour reads hit L2/MALL.
+constexpr int kPitch = kDim + 8;  // bf16 per staged LDS row
+constexpr int kWaves = 4;
+
 __global__ void __launch_bounds__(256)
 hex_aggregate_linear_kernel(const uint16_t* __restrict__ x, const int32_t* __restrict__ nbr,
                             int64_t n_cells, const uint16_t* __restrict__ w,
                             const float* __restrict__ bias, uint16_t* __restrict__ out_sum,
                             uint16_t* __restrict__ out_mean, int32_t* flag) {
+  __shared__ __align__(16) uint16_t sw[kDim * kPitch];
+  __shared__ __align__(16) uint16_t sagg[kWaves][16 * kPitch];
+  __shared__ float scount[kWaves][16];
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
-  const int l16 = lane % 16, g = lane / 16;
-  const int64_t c0 = (int64_t(blockIdx.x) * 4 + wave) * 16;
-  if (c0 >= n_cells) return;
-  const int64_t cell = c0 + l16;
-  const bool live = cell < n_cells;
-  float acc[4][8];
+  const int64_t c0 = (int64_t(blockIdx.x) * kWaves + wave) * 16;
+  // ---- gather in row layout: pass p covers cells c0 + 4p + lane/16
+  {
+    const int sub = lane / 16, d8 = (lane % 16) * 8;
+    int32_t js[4][6];
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks)
+    for (int p = 0; p < 4; ++p) {
+      const int64_t cell = c0 + 4 * p + sub;
 #pragma unroll
-    for (int t = 0; t < 8; ++t) acc[ks][t] = 0.f;
-  int present = 0;
-  if (live) {
+      for (int s = 0; s < 6; ++s) js[p][s] = cell < n_cells ? nbr[cell * 6 + s] : -1;
+    }
+    uint4 raw[4][6];
 #pragma unroll
-    for (int s = 0; s < 6; ++s) {
-      const int32_t j = nbr[cell * 6 + s];
-      if (j < 0) continue;
-      if (j >= n_cells) {
-        raise_flag(flag, MANTIS_FLAG_INDEX);
-        continue;
-      }
-      ++present;
+    for (int p = 0; p < 4; ++p) {
+      const int64_t cell = c0 + 4 * p + sub;
+      const int64_t self = cell < n_cells ? cell : 0;
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        float xv[8];
-        load8(x + int64_t(j) * kDim + 32 * ks + 8 * g, xv);
-#pragma unroll
-        for (int t = 0; t < 8; ++t) acc[ks][t] += xv[t];
+      for (int s = 0; s < 6; ++s) {
+        const bool ok = js[p][s] >= 0 && js[p][s] < n_cells;
+        raw[p][s] = *reinterpret_cast<const uint4*>(x + (ok ? int64_t(js[p][s]) : self) * kDim + d8);
       }
     }
-  }
-  const float inv = present ? 1.f / float(present) : 0.f;
-  bf16x8_t fs[4], fm[4];
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    uint4 us, um;
-    us.x = pack_bf16x2(acc[ks][0], acc[ks][1]);
-    us.y = pack_bf16x2(acc[ks][2], acc[ks][3]);
-    us.z = pack_bf16x2(acc[ks][4], acc[ks][5]);
-    us.w = pack_bf16x2(acc[ks][6], acc[ks][7]);
-    um.x = pack_bf16x2(acc[ks][0] * inv, acc[ks][1] * inv);
-    um.y = pack_bf16x2(acc[ks][2] * inv, acc[ks][3] * inv);
-    um.z = pack_bf16x2(acc[ks][4] * inv, acc[ks][5] * inv);
-    um.w = pack_bf16x2(acc[ks][6] * inv, acc[ks][7] * inv);
-    fs[ks] = as_bf16x8(us);
-    fm[ks] = as_bf16x8(um);
+    for (int p = 0; p < 4; ++p) {
+      float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+      int present = 0;
+#pragma unroll
+      for (int s = 0; s < 6; ++s) {
+        const int32_t j = js[p][s];
+        const bool ok = j >= 0 && j < n_cells;
+        if (j >= n_cells && (lane % 16) == 0) raise_flag(flag, MANTIS_FLAG_INDEX);
+        present += ok ? 1 : 0;
+        const float mk = ok ? 1.f : 0.f;
+        const uint32_t w4[4] = {raw[p][s].x, raw[p][s].y, raw[p][s].z, raw[p][s].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          acc[2 * i] = fmaf(__uint_as_float(w4[i] << 16), mk, acc[2 * i]);
+          acc[2 * i + 1] = fmaf(__uint_as_float(w4[i] & 0xffff0000u), mk, acc[2 * i + 1]);
+        }
+      }
+      uint4 packed;
+      packed.x = pack_bf16x2(acc[0], acc[1]);
+      packed.y = pack_bf16x2(acc[2], acc[3]);
+      packed.z = pack_bf16x2(acc[4], acc[5]);
+      packed.w = pack_bf16x2(acc[6], acc[7]);
+      *reinterpret_cast<uint4*>(&sagg[wave][(4 * p + sub) * kPitch + d8]) = packed;
+      if (lane % 16 == 0) scount[wave][4 * p + sub] = float(present);
+    }
   }
+  for (int i = threadIdx.x; i < kDim * kDim / 8; i += kWaves * 64) {
+    const int r = i / (kDim / 8), c = i % (kDim / 8);
+    *reinterpret_cast<uint4*>(sw + r * kPitch + 8 * c) = *reinterpret_cast<const uint4*>(w + r * kDim + 8 * c);
+  }
+  __syncthreads();
+  if (c0 >= n_cells) return;
+  // ---- product in MFMA layout: lane = cell l16, K group g
+  const int l16 = lane % 16, g = lane / 16;
+  const int64_t cell = c0 + l16;
+  const bool live = cell < n_cells;
+  const float cnt = scount[wave][l16];
+  const float inv = cnt > 0.f ? 1.f / cnt : 0.f;
+  bf16x8_t fs[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+    fs[ks] = as_bf16x8(*reinterpret_cast<const uint4*>(&sagg[wave][l16 * kPitch + 32 * ks + 8 * g]));
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) {
-    f32x4_t ds = {0.f, 0.f, 0.f, 0.f}, dm = {0.f, 0.f, 0.f, 0.f};
+    f32x4_t d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       // A fragment: W[16nt + l16][32ks + 8g .. +8]
-      const bf16x8_t wf = as_bf16x8(*reinterpret_cast<const uint4*>(w + (16 * nt + l16) * kDim + 32 * ks + 8 * g));
-      ds = mfma16x16x32(wf, fs[ks], ds);
-      dm = mfma16x16x32(wf, fm[ks], dm);
+      const bf16x8_t wf = as_bf16x8(*reinterpret_cast<const uint4*>(sw + (16 * nt + l16) * kPitch + 32 * ks + 8 * g));
+      d = mfma16x16x32(wf, fs[ks], d);
     }
     if (live) {
       const int o = 16 * nt + 4 * g;
       const float4 b = *reinterpret_cast<const float4*>(bias + o);
       uint2 ws, wm;
-      ws.x = pack_bf16x2(ds[0] + b.x, ds[1] + b.y);
-      ws.y = pack_bf16x2(ds[2] + b.z, ds[3] + b.w);
-      wm.x = pack_bf16x2(dm[0] + b.x, dm[1] + b.y);
-      wm.y = pack_bf16x2(dm[2] + b.z, dm[3] + b.w);
+      ws.x = pack_bf16x2(d[0] + b.x, d[1] + b.y);
+      ws.y = pack_bf16x2(d[2] + b.z, d[3] + b.w);
+      wm.x = pack_bf16x2(fmaf(d[0], inv, b.x), fmaf(d[1], inv, b.y));
+      wm.y = pack_bf16x2(fmaf(d[2], inv, b.z), fmaf(d[3], inv, b.w));
       *reinterpret_cast<uint2*>(out_sum + cell * kDim + o) = ws;
       *reinterpret_cast<uint2*>(out_mean + cell * kDim + o) = wm;
     }
@@ -162,8 +194,8 @@ int32_t mantis_hex_aggregate_linear(const void* x, const int32_t* nbr, int64_t n
   if (!x || !nbr || !w || !b || !out_sum || !out_mean || n_cells < 0) return MANTIS_E_ARG;
   if (!aligned16(x) || !aligned16(w) || !aligned16(b) || !aligned16(out_sum) || !aligned16(out_mean))
     return MANTIS_E_ARG;
-  const int64_t blocks = (n_cells + 63) / 64;
-  hex_aggregate_linear_kernel<<<unsigned(blocks), 256, 0, as_stream(stream)>>>(
+  const int64_t blocks = (n_cells + 16 * kWaves - 1) / (16 * kWaves);
+  hex_aggregate_linear_kernel<<<unsigned(blocks), kWaves * 64, 0, as_stream(stream)>>>(
       static_cast<const uint16_t*>(x), nbr, n_cells, static_cast<const uint16_t*>(w), b,
       static_cast<uint16_t*>(out_sum), static_cast<uint16_t*>(out_mean), err_flag);
   return launched();

@@ -25,9 +25,6 @@ __device__ __forceinline__ f32x4_t mfma16x16x32(bf16x8_t a, bf16x8_t b, f32x4_t 
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return uint32_t(f2bf(lo)) | (uint32_t(f2bf(hi)) << 16);
-}
 
 // fp16 fragments: v_mfma_f32_16x16x32_f16, same lane layout as bf16.
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
@@ -36,10 +33,6 @@ __device__ __forceinline__ f32x4_t mfma16x16x32(f16x8_t a, f16x8_t b, f32x4_t c)
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
-  const _Float16 a = f2h(lo), b = f2h(hi);
-  return uint32_t(__builtin_bit_cast(uint16_t, a)) | (uint32_t(__builtin_bit_cast(uint16_t, b)) << 16);
-}
 
 // Element-type traits of the 16-bit MFMA operand formats.
 template <bool kHalf>
@@ -50,6 +43,7 @@ struct Frag<false> {
   typedef bf16x8_t vec;
   static __device__ __forceinline__ vec cast(uint4 u) { return __builtin_bit_cast(vec, u); }
   static __device__ __forceinline__ uint32_t pack(float lo, float hi) { return pack_bf16x2(lo, hi); }
+  static __device__ __forceinline__ uint32_t pack_unit(float lo, float hi) { return pack_bf16x2(lo, hi); }
 };
 
 template <>
@@ -57,6 +51,7 @@ struct Frag<true> {
   typedef f16x8_t vec;
   static __device__ __forceinline__ vec cast(uint4 u) { return __builtin_bit_cast(vec, u); }
   static __device__ __forceinline__ uint32_t pack(float lo, float hi) { return pack_f16x2(lo, hi); }
+  static __device__ __forceinline__ uint32_t pack_unit(float lo, float hi) { return pack_f16x2_unit(lo, hi); }
 };
 
 }  // namespace mantis

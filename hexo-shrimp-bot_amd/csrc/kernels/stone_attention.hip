@@ -1,20 +1,27 @@
 // Ragged block-diagonal attention on 16-bit MFMA (bf16 or fp16) for gfx950
 // (replaces the reference's Triton flash kernel, attention.py:44-162).
 //
-// Work split: one workgroup = one (position, head, 64-query tile); its four
-// wavefronts own 16 queries each and stream the position's live keys in
-// 64-key chunks.  Per chunk and wavefront:
-//   S^T (16 keys x 16 queries) = K (16 x 32) . Q^T (32 x 16)   4 MFMAs
-//   O^T (32 dims x 16 queries) += V^T (32 x 64) . P^T (64 x 16) 4 MFMAs
-// Computing the transposed products keeps every lane on one query: its
-// softmax statistics stay in registers and the probabilities of a D fragment
-// are the B fragment of the next product (the two 16-key tiles of a 32-key
-// step interleave as K-slots {4g..4g+3, 16+4g..16+4g+3}; V^T is read from
-// LDS in that same order).  K fragments are 16-byte row loads straight from
-// global memory; V is staged once per chunk, transposed, in LDS.  Scores
-// are pre-scaled by log2(e)/sqrt(hd) so the online softmax runs on exp2.
-// Keys at or past seq_len are never read (zero-filled, probability 0) and
-// query rows past seq_len are written as exact zeros.
+// Work split: one workgroup = one (position, head, 128-query tile); each of
+// its four wavefronts owns 32 queries (two 16-query sub-tiles).  The
+// workgroup streams the position's live keys in 64-key chunks through LDS,
+// double-buffered: while a chunk is consumed the next one is already in
+// registers, and one barrier per chunk separates the buffers.  Per chunk,
+// sub-tile and wavefront:
+//   S^T (16 keys x 16 queries) = K (16 x 32) . Q^T (32 x 16)    4 MFMAs
+//   O^T (32 dims x 16 queries) += V^T (32 x 64) . P^T (64 x 16)  4 MFMAs
+// Each K fragment read from LDS serves both sub-tiles.  Computing the
+// transposed products keeps every lane on one query: its softmax statistics
+// stay in registers and the probabilities of a D fragment are the B fragment
+// of the next product (the two 16-key tiles of a 32-key step interleave as
+// K-slots {4g..4g+3, 16+4g..16+4g+3}; V^T is staged in LDS so its A
+// fragment reads the same order).  The online softmax tracks the raw-score
+// maximum and evaluates exp2(s*c - m*c) with c = log2(e)/sqrt(hd): one FMA
+// and one exp2 per score; the row sums come from one more product per
+// 32-key step with an all-ones A operand, so the normaliser sums exactly the
+// rounded probabilities the numerator uses.  Keys at or past seq_len are staged as zeros and
+// masked (only the last chunk can hold them); query rows past seq_len are
+// written as exact zeros.  LDS rows are padded (K 80 B, V^T 144 B) so the
+// 16 rows of a fragment read fall in distinct banks.
 #include "common.hpp"
 #include "mfma.hpp"
 
@@ -22,9 +29,12 @@ namespace mantis {
 namespace {
 
 constexpr int kHd = 32;
-constexpr int kQTile = 64;
+constexpr int kWaves = 4;
+constexpr int kQPerWave = 32;
+constexpr int kQTile = kWaves * kQPerWave;  // 128
 constexpr int kKChunk = 64;
-constexpr int kVtPitch = kKChunk + 8;  // bf16 elements per transposed-V row
+constexpr int kKPitch = kHd + 8;        // 16-bit elements per staged K row
+constexpr int kVtPitch = kKChunk + 8;   // 16-bit elements per staged V^T row
 
 template <bool kHalf>
 __global__ void __launch_bounds__(256)
@@ -33,8 +43,9 @@ stone_attention_kernel(const uint16_t* __restrict__ q, int64_t qsp, int64_t qsa,
                        const uint16_t* __restrict__ v, int64_t vsp, int64_t vsa, int64_t vst,
                        const int32_t* __restrict__ seq_lens, int heads, int64_t T,
                        uint16_t* __restrict__ out, int64_t osp, int64_t osa, int64_t ost,
-                       float* __restrict__ lse, float scale_log2) {
-  __shared__ __attribute__((aligned(16))) uint16_t vt[kHd][kVtPitch];
+                       float* __restrict__ lse, float c_log2) {
+  __shared__ __attribute__((aligned(16))) uint16_t sk[2][kKChunk * kKPitch];
+  __shared__ __attribute__((aligned(16))) uint16_t svt[2][kHd * kVtPitch];
   const int64_t pa = blockIdx.y;
   const int64_t p = pa / heads, a = pa % heads;
   int64_t L = seq_lens[p];
@@ -45,111 +56,161 @@ stone_attention_kernel(const uint16_t* __restrict__ q, int64_t qsp, int64_t qsa,
   const uint16_t* vp = v + p * vsp + a * vsa;
   uint16_t* op = out + p * osp + a * osa;
   float* lp = lse ? lse + (p * heads + a) * T : nullptr;
+  const uint4 zero4 = make_uint4(0, 0, 0, 0);
 
   if (q0 >= L) {  // a tile past the live prefix does no key work
-    const int64_t row = q0 + threadIdx.x / 4;
-    const int c = (threadIdx.x % 4) * 8;
-    if (row < T) {
-      *reinterpret_cast<uint4*>(op + row * ost + c) = make_uint4(0, 0, 0, 0);
-      if (lp && c == 0) lp[row] = 0.f;
+    for (int i = threadIdx.x; i < kQTile * 4; i += 256) {
+      const int64_t row = q0 + i / 4;
+      const int c = (i % 4) * 8;
+      if (row < T) {
+        *reinterpret_cast<uint4*>(op + row * ost + c) = zero4;
+        if (lp && c == 0) lp[row] = 0.f;
+      }
     }
     return;
   }
 
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
   const int l16 = lane % 16, g = lane / 16;
-  const int64_t qrow = q0 + wave * 16 + l16;
-  const bool q_live = qrow < L;
-  const uint4 zero4 = make_uint4(0, 0, 0, 0);
-  // B fragment of Q^T: query l16, dims 8g..8g+7.
   using FR = Frag<kHalf>;
-  const typename FR::vec qf = FR::cast(q_live ? *reinterpret_cast<const uint4*>(qp + qrow * qst + 8 * g) : zero4);
+  typename FR::vec qf[2];
+  int64_t qrow[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    qrow[j] = q0 + wave * kQPerWave + 16 * j + l16;
+    // B fragment of Q^T: query l16, dims 8g..8g+7
+    qf[j] = FR::cast(qrow[j] < L ? *reinterpret_cast<const uint4*>(qp + qrow[j] * qst + 8 * g) : zero4);
+  }
 
-  float m = -INFINITY, lpart = 0.f;
-  f32x4_t o0 = {0.f, 0.f, 0.f, 0.f}, o1 = {0.f, 0.f, 0.f, 0.f};
+  // staging role of this thread: one 16-byte piece of one key's K and V rows
+  const int st_key = threadIdx.x / 4, st_d = (threadIdx.x % 4) * 8;
+  uint4 kreg, vreg;
+  auto fetch = [&](int64_t kb) {
+    const int64_t kk = kb + st_key;
+    kreg = kk < L ? *reinterpret_cast<const uint4*>(kp + kk * kst + st_d) : zero4;
+    vreg = kk < L ? *reinterpret_cast<const uint4*>(vp + kk * vst + st_d) : zero4;
+  };
+  auto stage = [&](int buf) {
+    *reinterpret_cast<uint4*>(&sk[buf][st_key * kKPitch + st_d]) = kreg;
+    const uint32_t w[4] = {vreg.x, vreg.y, vreg.z, vreg.w};
+    uint16_t* col = &svt[buf][st_d * kVtPitch + st_key];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      col[(2 * i) * kVtPitch] = uint16_t(w[i] & 0xffffu);
+      col[(2 * i + 1) * kVtPitch] = uint16_t(w[i] >> 16);
+    }
+  };
+
+  // per sub-tile: running raw-score maximum, O^T accumulators (two 16-dim
+  // tiles) and the row sums, accumulated by an extra product with an
+  // all-ones A operand (every D row holds the sum of the probabilities)
+  float m[2] = {-INFINITY, -INFINITY};
+  f32x4_t o[2][2], lsum[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    lsum[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt) o[j][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+  const uint32_t one2 = FR::pack_unit(1.f, 1.f);
+  const typename FR::vec ones = FR::cast(make_uint4(one2, one2, one2, one2));
+
   const int64_t n_chunks = (L + kKChunk - 1) / kKChunk;
+  fetch(0);
+  stage(0);
+  __syncthreads();
   for (int64_t ch = 0; ch < n_chunks; ++ch) {
+    const int buf = int(ch & 1);
     const int64_t kb = ch * kKChunk;
-    __syncthreads();  // the previous chunk's V^T reads are done
-    {
-      const int key = threadIdx.x / 4, d0 = (threadIdx.x % 4) * 8;
-      const int64_t kk = kb + key;
-      uint4 u = kk < L ? *reinterpret_cast<const uint4*>(vp + kk * vst + d0) : zero4;
-      const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        vt[d0 + 2 * i][key] = uint16_t(w[i] & 0xffffu);
-        vt[d0 + 2 * i + 1][key] = uint16_t(w[i] >> 16);
-      }
-    }
-    __syncthreads();
+    const bool more = ch + 1 < n_chunks;
+    if (more) fetch(kb + kKChunk);
 
-    // S^T tiles: keys kb + 16*tt + (4g + t) for query l16.
-    float s[4][4];
-    float cmax = -INFINITY;
+    // S^T tiles: keys kb + 16*tt + (4g + t) for query l16 of sub-tile j
+    f32x4_t s[2][4];
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) {
-      const int64_t krow = kb + 16 * tt + l16;  // A-fragment row of this lane
-      const typename FR::vec kf = FR::cast(krow < L ? *reinterpret_cast<const uint4*>(kp + krow * kst + 8 * g) : zero4);
-      const f32x4_t d = mfma16x16x32(kf, qf, f32x4_t{0.f, 0.f, 0.f, 0.f});
+      const typename FR::vec kf = FR::cast(*reinterpret_cast<const uint4*>(&sk[buf][(16 * tt + l16) * kKPitch + 8 * g]));
+#pragma unroll
+      for (int j = 0; j < 2; ++j) s[j][tt] = mfma16x16x32(kf, qf[j], f32x4_t{0.f, 0.f, 0.f, 0.f});
+    }
+    const int lim = int(L - kb);  // keys at or past lim are padding
+    if (lim < kKChunk) {           // only the last chunk can hold them
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          if (16 * tt + 4 * g + t >= lim) {
+            s[0][tt][t] = -INFINITY;
+            s[1][tt][t] = -INFINITY;
+          }
+    }
+    typename FR::vec pf[2][2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      float cmax = m[j];
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) cmax = fmaxf(cmax, s[j][tt][t]);
+      cmax = fmaxf(cmax, __shfl_xor(cmax, 16));
+      cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
+      // exp2 arguments are <= 0 (or -inf): the raw v_exp_f32 is exact enough
+      // and flushes results below 2^-126 to zero
+      const float alpha = __builtin_amdgcn_exp2f((m[j] - cmax) * c_log2);
+      const float mc = cmax * c_log2;
+      m[j] = cmax;
+      uint32_t pw[4][2];
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        float pr[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) pr[t] = __builtin_amdgcn_exp2f(fmaf(s[j][tt][t], c_log2, -mc));
+        pw[tt][0] = FR::pack_unit(pr[0], pr[1]);
+        pw[tt][1] = FR::pack_unit(pr[2], pr[3]);
+      }
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        const int64_t key = kb + 16 * tt + 4 * g + t;
-        s[tt][t] = key < L ? d[t] * scale_log2 : -INFINITY;
-        cmax = fmaxf(cmax, s[tt][t]);
+        lsum[j][t] *= alpha;
+        o[j][0][t] *= alpha;
+        o[j][1][t] *= alpha;
       }
-    }
-    cmax = fmaxf(cmax, __shfl_xor(cmax, 16));
-    cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
-    const float m_new = fmaxf(m, cmax);
-    const float alpha = exp2f(m - m_new);
-    lpart *= alpha;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      o0[t] *= alpha;
-      o1[t] *= alpha;
+      for (int sc = 0; sc < 2; ++sc)
+        pf[j][sc] = FR::cast(make_uint4(pw[2 * sc][0], pw[2 * sc][1], pw[2 * sc + 1][0], pw[2 * sc + 1][1]));
     }
-    uint32_t pw[4][2];
-#pragma unroll
-    for (int tt = 0; tt < 4; ++tt) {
-      float pr[4];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        pr[t] = exp2f(s[tt][t] - m_new);
-        lpart += pr[t];
-      }
-      pw[tt][0] = FR::pack(pr[0], pr[1]);
-      pw[tt][1] = FR::pack(pr[2], pr[3]);
-    }
-    m = m_new;
-    // O^T += V^T . P^T over two 32-key steps.
+    // O^T += V^T . P^T over two 32-key steps; each V^T fragment serves both sub-tiles
 #pragma unroll
     for (int sc = 0; sc < 2; ++sc) {
-      const typename FR::vec pf = FR::cast(make_uint4(pw[2 * sc][0], pw[2 * sc][1], pw[2 * sc + 1][0], pw[2 * sc + 1][1]));
 #pragma unroll
       for (int dt = 0; dt < 2; ++dt) {
-        const uint16_t* row = &vt[16 * dt + l16][32 * sc];
+        const uint16_t* row = &svt[buf][(16 * dt + l16) * kVtPitch + 32 * sc];
         const uint2 lo = *reinterpret_cast<const uint2*>(row + 4 * g);
         const uint2 hi = *reinterpret_cast<const uint2*>(row + 16 + 4 * g);
         const typename FR::vec vf = FR::cast(make_uint4(lo.x, lo.y, hi.x, hi.y));
-        if (dt == 0) o0 = mfma16x16x32(vf, pf, o0);
-        else o1 = mfma16x16x32(vf, pf, o1);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) o[j][dt] = mfma16x16x32(vf, pf[j][sc], o[j][dt]);
       }
+#pragma unroll
+      for (int j = 0; j < 2; ++j) lsum[j] = mfma16x16x32(ones, pf[j][sc], lsum[j]);
     }
+    if (more) stage(buf ^ 1);
+    __syncthreads();
   }
-  float l = lpart;
-  l += __shfl_xor(l, 16);
-  l += __shfl_xor(l, 32);
-  if (qrow < T) {
-    const float inv = (q_live && l > 0.f) ? 1.f / l : 0.f;
-    uint2 w0, w1;
-    w0.x = FR::pack(o0[0] * inv, o0[1] * inv);
-    w0.y = FR::pack(o0[2] * inv, o0[3] * inv);
-    w1.x = FR::pack(o1[0] * inv, o1[1] * inv);
-    w1.y = FR::pack(o1[2] * inv, o1[3] * inv);
-    *reinterpret_cast<uint2*>(op + qrow * ost + 4 * g) = w0;
-    *reinterpret_cast<uint2*>(op + qrow * ost + 16 + 4 * g) = w1;
-    if (lp && g == 0) lp[qrow] = q_live ? (m + log2f(l)) * 0.6931471805599453f : 0.f;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const float lt = lsum[j][0];
+    if (qrow[j] < T) {
+      const bool live = qrow[j] < L;
+      const float inv = (live && lt > 0.f) ? 1.f / lt : 0.f;
+      uint2 w0, w1;
+      w0.x = FR::pack_unit(o[j][0][0] * inv, o[j][0][1] * inv);
+      w0.y = FR::pack_unit(o[j][0][2] * inv, o[j][0][3] * inv);
+      w1.x = FR::pack_unit(o[j][1][0] * inv, o[j][1][1] * inv);
+      w1.y = FR::pack_unit(o[j][1][2] * inv, o[j][1][3] * inv);
+      *reinterpret_cast<uint2*>(op + qrow[j] * ost + 4 * g) = w0;
+      *reinterpret_cast<uint2*>(op + qrow[j] * ost + 16 + 4 * g) = w1;
+      if (lp && g == 0) lp[qrow[j]] = live ? (m[j] * c_log2 + log2f(lt)) * 0.6931471805599453f : 0.f;
+    }
   }
 }
 
@@ -174,12 +235,12 @@ extern "C" int32_t mantis_stone_attention(const void* q, const int64_t* qs, cons
   }
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out)) return MANTIS_E_ARG;
   if (n_pos * heads > 2147483647LL) return MANTIS_E_ARG;
-  const float scale_log2 = 1.4426950408889634f / sqrtf(float(hd));
+  const float c_log2 = 1.4426950408889634f / sqrtf(float(hd));
   const dim3 grid(unsigned((t + kQTile - 1) / kQTile), unsigned(n_pos * heads));
   auto kernel = dtype == MANTIS_F16 ? stone_attention_kernel<true> : stone_attention_kernel<false>;
   kernel<<<grid, 256, 0, as_stream(stream)>>>(
       static_cast<const uint16_t*>(q), qs[0], qs[1], qs[2], static_cast<const uint16_t*>(k), ks[0],
       ks[1], ks[2], static_cast<const uint16_t*>(v), vs[0], vs[1], vs[2], seq_lens, heads, t,
-      static_cast<uint16_t*>(out), os[0], os[1], os[2], lse, scale_log2);
+      static_cast<uint16_t*>(out), os[0], os[1], os[2], lse, c_log2);
   return launched();
 }

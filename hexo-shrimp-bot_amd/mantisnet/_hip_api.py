@@ -14,7 +14,7 @@ SIGNATURES = {
     "mantis_runs_to_ptr": ([vp, i64, i64, vp, vp, vp], i32),
     "mantis_run_reduce": ([vp, i32, i64, i64, i64, vp, i64, vp, i64, vp, i32, vp, vp], i32),
     "mantis_cell_attention": (
-        [vp, vp, vp, i32, i64, i64, i64, vp, i64, vp, vp, vp, vp, i64, i64, i64, i32, i32, vp, i32, vp, vp, vp, vp],
+        [vp, vp, vp, i32, i64, i64, i64, vp, i64, vp, i32, vp, vp, vp, i64, i64, i64, i32, i32, vp, i32, vp, vp, vp, vp],
         i32),
     "mantis_latent_read": ([vp, vp, vp, i32, i64, i64, i64, vp, vp, i64, i64, i32, i32, vp, vp, vp, vp, vp], i32),
     "mantis_latent_broadcast": ([vp, vp, vp, i32, i64, i64, i64, vp, i64, i64, i32, i32, vp, i32, vp, vp, vp, vp],

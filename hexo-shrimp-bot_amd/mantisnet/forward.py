@@ -129,9 +129,12 @@ def _prepare(model, P) -> dict[str, Tensor]:
         put(pb + "cr_q", _fold(P, pb + "ln_cr_c", [pb + "cr_wq"]))
         put(pb + "cr_kv", _fold(P, pb + "ln_cr_w", [pb + "cr_wk", pb + "cr_wv"]))
         put(pb + "cr_o", _fold(P, None, [pb + "cr_wo"]))
+        # class-value rows gathered once per edge: fp16 halves their bytes
+        t[pb + "cr_vcls"] = P[pb + "cr_vclass.weight"].to(HALF).contiguous()
         put(pb + "rad_q", _fold(P, pb + "ln_radius_c", [pb + "radius_wq"]))
         put(pb + "rad_kv", _fold(P, pb + "ln_radius_s", [pb + "radius_wk", pb + "radius_wv"]))
         put(pb + "rad_o", _fold(P, None, [pb + "radius_wo"]))
+        t[pb + "rad_vcls"] = P[pb + "radius_vclass.weight"].to(HALF).contiguous()
         put(pb + "wr_q", _fold(P, pb + "ln_wr_w", [pb + "wr_wq"]))
         put(pb + "wr_kv", _fold(P, pb + "ln_wr_c", [pb + "wr_wk", pb + "wr_wv"]))
         put(pb + "wr_o", _fold(P, None, [pb + "wr_wo"]))
@@ -301,12 +304,12 @@ def _cell_stage(W, P, pb, plan: Plan, s, w, c):
     n_c, n_w = plan.n_c, plan.n_w
     q = _proj(W, pb + "cr_q", c)
     kv = _proj(W, pb + "cr_kv", w)
-    read = ops.cell_attention(q, kv[:, :128], kv[:, 128:], P[pb + "cr_bias"], P[pb + "cr_vclass.weight"],
+    read = ops.cell_attention(q, kv[:, :128], kv[:, 128:], P[pb + "cr_bias"], W[pb + "cr_vcls"],
                               plan.cell_ptr, plan.edge_window, plan.edge_class, out_dtype=HALF)
     _resid(W, pb + "cr_o", read.view(n_c, 128), c)
     q = _proj(W, pb + "rad_q", c)
     kv = _proj(W, pb + "rad_kv", s)
-    read = ops.cell_attention(q, kv[:, :128], kv[:, 128:], P[pb + "radius_bias"], P[pb + "radius_vclass.weight"],
+    read = ops.cell_attention(q, kv[:, :128], kv[:, 128:], P[pb + "radius_bias"], W[pb + "rad_vcls"],
                               plan.radius_ptr, plan.radius_src, plan.radius_class, out_dtype=HALF)
     _resid(W, pb + "rad_o", read.view(n_c, 128), c)
     q = _proj(W, pb + "wr_q", w)

@@ -262,7 +262,7 @@ def cell_attention(q: Tensor, k: Tensor, v: Tensor, bias: Tensor, vcls: Tensor |
     if vcls is not None:
         if vcls.shape != (bias.shape[1], heads * hd):
             raise ValueError("vcls must have shape (classes, heads * head_dim)")
-        vcls = vcls.float().contiguous()
+        vcls = (vcls if vcls.dtype == torch.float16 else vcls.float()).contiguous()
     seg_ptr, src, cls = _i64(seg_ptr, "seg_ptr"), _i64(src, "src"), _i64(cls, "cls")
     if out_dtype not in (torch.float32, torch.float16):
         raise ValueError("cell attention writes fp32 or fp16")
@@ -273,13 +273,14 @@ def cell_attention(q: Tensor, k: Tensor, v: Tensor, bias: Tensor, vcls: Tensor |
         e = src.numel()
         # algorithmic bytes: q and out rows once, each source's k and v rows
         # once, the CSR pointers and the per-edge (src, cls) indices
+        # (class-value rows are L2-resident and not counted)
         nbytes = n_q * (128 * q.element_size() + 128 * out.element_size() + 8) + e * 16 + \
             k.shape[0] * 128 * (k.element_size() + v.element_size())
         flops = e * 4 * 128 * 2  # score dot + weighted value sum per edge and head
         _launch("cell_attention_vcls" if vcls is not None else "cell_attention_plain", nbytes, flops, lambda: _check(
             _lib().mantis_cell_attention(
                 _ptr(q), _ptr(k), _ptr(v), _dt(q), ldq, ldk, ldv, _ptr(bias), bias.shape[1], _ptr(vcls),
-                _ptr(seg_ptr), _ptr(src), _ptr(cls), e, n_q, k.shape[0], heads, hd,
+                _dt(vcls) if vcls is not None else 0, _ptr(seg_ptr), _ptr(src), _ptr(cls), e, n_q, k.shape[0], heads, hd,
                 _ptr(out), _dt(out), _ptr(m), _ptr(l), _ptr(error_flag(dev)), _stream(),
             ),
             "cell_attention",

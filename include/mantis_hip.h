@@ -69,15 +69,16 @@ int32_t mantis_run_reduce(const void* values, int32_t values_dtype, int64_t n_sr
  * fp32 scores, softmax and sums; a row without entries reads zero.  q/k/v are
  * (n, heads*hd) rows in `dtype` with row strides ldq/ldk/ldv (elements,
  * multiples of 8; k and v may be the two halves of one (n, 256) buffer); bias (heads, n_classes) fp32; vcls
- * (n_classes, heads*hd) fp32 or NULL; out (n_q, heads, hd) in out_dtype (fp32
+ * (n_classes, heads*hd) in vcls_dtype (fp32 or fp16) or NULL; out (n_q, heads, hd) in out_dtype (fp32
  * or fp16); m/l
  * (n_q, heads) fp32 softmax statistics or NULL.  Supports heads*hd == 128.
  * Replaces mantisnet::cell_attention / cell_attention_plain
  * (python/mantisnet/mantisnet/cell_latents.py:213-285, 834-1001).
  */
 int32_t mantis_cell_attention(const void* q, const void* k, const void* v, int32_t dtype,
-                              int64_t ldq, int64_t ldk, int64_t ldv, const float* bias, int64_t n_classes, const float* vcls,
-                              const int64_t* seg_ptr, const int64_t* src, const int64_t* cls,
+                              int64_t ldq, int64_t ldk, int64_t ldv, const float* bias, int64_t n_classes,
+                              const void* vcls, int32_t vcls_dtype, const int64_t* seg_ptr,
+                              const int64_t* src, const int64_t* cls,
                               int64_t n_entries, int64_t n_q, int64_t n_k, int32_t heads,
                               int32_t hd, void* out, int32_t out_dtype, float* m, float* l,
                               int32_t* err_flag, void* stream);

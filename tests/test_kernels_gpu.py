@@ -72,7 +72,7 @@ def test_unsorted_runs_are_flagged(device):
 
 
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16])
-@pytest.mark.parametrize("with_vcls", [True, False])
+@pytest.mark.parametrize("with_vcls", [None, torch.float32, torch.float16])
 @pytest.mark.parametrize("dtype", [torch.float16, BF, torch.float32])
 def test_cell_attention_matches_dense_oracle(device, with_vcls, dtype, out_dtype):
     gen = _g(3)
@@ -84,14 +84,15 @@ def test_cell_attention_matches_dense_oracle(device, with_vcls, dtype, out_dtype
     k = torch.randn(n_k, 4, 32, generator=gen).to(dtype)
     v = torch.randn(n_k, 4, 32, generator=gen).to(dtype)
     bias = 0.3 * torch.randn(4, classes, generator=gen)
-    vcls = 0.1 * torch.randn(classes, 128, generator=gen) if with_vcls else None
+    vcls = (0.1 * torch.randn(classes, 128, generator=gen)).to(with_vcls) if with_vcls else None
     ptr = torch.searchsorted(dest, torch.arange(n_q + 1))
     d = lambda x: None if x is None else x.to(device)  # noqa: E731
     out, m, l = ops.cell_attention(d(q), d(k), d(v), d(bias), d(vcls), d(ptr), d(src), d(cls), stats=True,
                                    out_dtype=out_dtype)
     ops.raise_on_device_error(device)
     assert out.dtype == out_dtype
-    exp = R.cell_attention(q.float(), k.float(), v.float(), bias, vcls, src, cls, dest)
+    exp = R.cell_attention(q.float(), k.float(), v.float(), bias, None if vcls is None else vcls.float(), src, cls,
+                           dest)
     if out_dtype == torch.float16:  # fp32 math, one rounding of the stored value
         exp = exp.to(torch.float16).float()
     torch.testing.assert_close(out.float().cpu(), exp, rtol=1e-3, atol=1e-4)
