@@ -300,23 +300,22 @@ def _resid(W, key, x, out, **kw):
     return FL(x, W[key + ".w"], W[key + ".b"], out=out, residual=True, **kw)
 
 
+def _substage(W, P, pb, key, x, kv, bias, vcls, ptr, src, cls):
+    """x += o-projection of the typed attention of LN(x)'s queries, fused."""
+    return ops.attention_substage(x, W[pb + key + "_q.w"], W[pb + key + "_q.b"], kv, P[pb + bias], vcls, ptr, src,
+                                  cls, W[pb + key + "_o.w"], W[pb + key + "_o.b"])
+
+
 def _cell_stage(W, P, pb, plan: Plan, s, w, c):
-    n_c, n_w = plan.n_c, plan.n_w
-    q = _proj(W, pb + "cr_q", c)
-    kv = _proj(W, pb + "cr_kv", w)
-    read = ops.cell_attention(q, kv[:, :128], kv[:, 128:], P[pb + "cr_bias"], W[pb + "cr_vcls"],
-                              plan.cell_ptr, plan.edge_window, plan.edge_class, out_dtype=HALF)
-    _resid(W, pb + "cr_o", read.view(n_c, 128), c)
-    q = _proj(W, pb + "rad_q", c)
-    kv = _proj(W, pb + "rad_kv", s)
-    read = ops.cell_attention(q, kv[:, :128], kv[:, 128:], P[pb + "radius_bias"], W[pb + "rad_vcls"],
-                              plan.radius_ptr, plan.radius_src, plan.radius_class, out_dtype=HALF)
-    _resid(W, pb + "rad_o", read.view(n_c, 128), c)
-    q = _proj(W, pb + "wr_q", w)
-    kv = _proj(W, pb + "wr_kv", c)
-    back = ops.cell_attention(q, kv[:, :128], kv[:, 128:], P[pb + "wr_bias"], None,
-                              plan.win_ptr, plan.edge_wcell, plan.edge_wclass, out_dtype=HALF)
-    _resid(W, pb + "wr_o", back.view(n_w, 128), w)
+    # cells <- windows (decoder classes, class values), cells <- stones (radius
+    # classes, class values), windows <- cells (decoder classes): each one
+    # fused LN -> q -> attention -> o -> residual launch over the query rows
+    _substage(W, P, pb, "cr", c, _proj(W, pb + "cr_kv", w), "cr_bias", W[pb + "cr_vcls"], plan.cell_ptr,
+              plan.edge_window, plan.edge_class)
+    _substage(W, P, pb, "rad", c, _proj(W, pb + "rad_kv", s), "radius_bias", W[pb + "rad_vcls"], plan.radius_ptr,
+              plan.radius_src, plan.radius_class)
+    _substage(W, P, pb, "wr", w, _proj(W, pb + "wr_kv", c), "wr_bias", None, plan.win_ptr, plan.edge_wcell,
+              plan.edge_wclass)
 
 
 def _latent_cycle(W, P, pb, plan: Plan, w, g2):

@@ -198,8 +198,9 @@ def runs_to_ptr(dest: Tensor, n_dest: int) -> Tensor:
     dest = _i64(dest, "dest")
     ptr = torch.empty(n_dest + 1, dtype=torch.int64, device=dev)
     if n_dest >= 0:
-        _check(_lib().mantis_runs_to_ptr(_ptr(dest), dest.numel(), n_dest, _ptr(ptr),
-                                         _ptr(error_flag(dev)), _stream()), "runs_to_ptr")
+        _launch("runs_to_ptr", 8 * (dest.numel() + n_dest + 1), 0, lambda: _check(
+            _lib().mantis_runs_to_ptr(_ptr(dest), dest.numel(), n_dest, _ptr(ptr), _ptr(error_flag(dev)),
+                                      _stream()), "runs_to_ptr"))
     return ptr
 
 
@@ -221,13 +222,16 @@ def run_reduce(values: Tensor, gather: Tensor, ptr: Tensor, n_dest: int, out_dty
     out = torch.empty((n_dest, h), dtype=out_dtype, device=dev)
     if n_dest == 0 or h == 0:
         return out
-    _check(
+    # each gathered source row once, its index once, each destination row once
+    e = gather.numel()
+    nbytes = e * (8 + h * values.element_size()) + n_dest * (8 + h * out.element_size())
+    _launch(f"run_reduce_{_SHORT[values.dtype]}_{_SHORT[out_dtype]}", nbytes, e * h, lambda: _check(
         _lib().mantis_run_reduce(
             _ptr(values), _dt(values), values.shape[0], values.stride(0), h, _ptr(gather),
             gather.numel(), _ptr(ptr), n_dest, _ptr(out), _dt(out), _ptr(error_flag(dev)), _stream(),
         ),
         "run_reduce",
-    )
+    ))
     return out
 
 
@@ -288,6 +292,55 @@ def cell_attention(q: Tensor, k: Tensor, v: Tensor, bias: Tensor, vcls: Tensor |
     return (out, m, l) if stats else out
 
 
+def attention_substage(x: Tensor, wq: Tensor, bq: Tensor, kv: Tensor, bias: Tensor, vcls: Tensor | None,
+                       seg_ptr: Tensor, src: Tensor, cls: Tensor, wo: Tensor, bo: Tensor) -> Tensor:
+    """In place on the fp32 residual rows x (n, 128):
+    x += fp16(attend(fp16(LN(x) wq^T + bq))) wo^T + bo, the attention typed
+    by (bias, vcls) over the CSR entries (seg_ptr, src, cls) with k/v the two
+    halves of the fp16 (n_src, 256) rows kv.  One launch."""
+    dev = _on_gpu(x, wq, bq, kv, bias, vcls, seg_ptr, src, cls, wo, bo)
+    n = x.shape[0]
+    if x.ndim != 2 or x.shape[1] != 128 or x.dtype != torch.float32 or x.stride(1) != 1:
+        raise ValueError("x must be fp32 (n, 128) rows")
+    for t, name in ((wq, "wq"), (wo, "wo")):
+        if t.shape != (128, 128) or t.dtype != torch.float16 or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous fp16 (128, 128) matrix")
+    for t, name in ((bq, "bq"), (bo, "bo")):
+        if t.shape != (128,) or t.dtype != torch.float32 or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous fp32 vector of 128")
+    if kv.ndim != 2 or kv.shape[1] != 256 or kv.dtype != torch.float16 or kv.stride(1) != 1:
+        raise ValueError("kv must be fp16 (n_src, 256) rows")
+    if bias.ndim != 2 or bias.shape[0] != 4:
+        raise ValueError("bias must have shape (4, classes)")
+    bias = bias.float().contiguous()
+    if vcls is not None:
+        if vcls.shape != (bias.shape[1], 128):
+            raise ValueError("vcls must have shape (classes, 128)")
+        vcls = vcls.to(torch.float16).contiguous()
+    if seg_ptr.numel() != n + 1:
+        raise ValueError("seg_ptr must have one entry per row plus one")
+    if src.shape != cls.shape or src.ndim != 1:
+        raise ValueError("the entry views must have one length")
+    seg_ptr, src, cls = _i64(seg_ptr, "seg_ptr"), _i64(src, "src"), _i64(cls, "cls")
+    if n:
+        e = src.numel()
+        # x read and written once, the CSR pointers and entry indices once,
+        # each source's k and v rows once
+        nbytes = n * (128 * 4 * 2 + 8) + e * 16 + kv.shape[0] * 256 * 2
+        flops = 2 * n * 128 * 128 * 2 + e * 4 * 128 * 2
+        _launch("attention_substage_vcls" if vcls is not None else "attention_substage_plain", nbytes, flops,
+                lambda: _check(
+                    _lib().mantis_attention_substage(
+                        _ptr(x), x.stride(0), n, _ptr(wq), _ptr(bq), kv.data_ptr(), kv[:, 128:].data_ptr(),
+                        kv.stride(0), kv.stride(0), kv.shape[0], _ptr(bias), bias.shape[1], _ptr(vcls),
+                        _ptr(seg_ptr), _ptr(src), _ptr(cls), e, _ptr(wo), _ptr(bo), _ptr(error_flag(dev)),
+                        _stream(),
+                    ),
+                    "attention_substage",
+                ))
+    return x
+
+
 def latent_read(q: Tensor, k: Tensor, v: Tensor, offsets: Tensor, order: Tensor, stats: bool = False):
     """Four latent queries per position over its windows; q (P, 4, ...) and
     k/v 128-wide rows; returns fp32 (P, 4, 4, 32) [and m, l]."""
@@ -308,13 +361,15 @@ def latent_read(q: Tensor, k: Tensor, v: Tensor, offsets: Tensor, order: Tensor,
     m = torch.empty((p, 4, 4), dtype=torch.float32, device=dev) if stats else None
     l = torch.empty((p, 4, 4), dtype=torch.float32, device=dev) if stats else None
     if p:
-        _check(
+        # queries and outputs once, each window's k, v rows and order entry once
+        nbytes = p * 4 * 128 * (q2.element_size() + 4) + n_w * (256 * k.element_size() + 8) + 8 * (p + 1)
+        _launch("latent_read", nbytes, n_w * 4 * 4 * 128 * 2, lambda: _check(
             _lib().mantis_latent_read(
                 _ptr(q2), _ptr(k), _ptr(v), _dt(q2), ldq, ldk, ldv, _ptr(offsets), _ptr(order), p, n_w,
                 4, 32, _ptr(out), _ptr(m), _ptr(l), _ptr(error_flag(dev)), _stream(),
             ),
             "latent_read",
-        )
+        ))
     return (out, m, l) if stats else out
 
 
@@ -365,14 +420,16 @@ def latent_broadcast_rows(q: Tensor, kv: Tensor, window_pos: Tensor,
     q, ldq = _rows128(q, "q")
     out = torch.empty((n_w, 4, 32), dtype=out_dtype, device=dev)
     if n_w:
-        _check(
+        # window queries, outputs and positions once, the latents' k/v once
+        nbytes = n_w * (128 * q.element_size() + 128 * out.element_size() + 8) + 4 * p * 256 * kv.element_size()
+        _launch("latent_broadcast", nbytes, n_w * 4 * 128 * 2 * 2, lambda: _check(
             _lib().mantis_latent_broadcast(
                 _ptr(q), kv.data_ptr(), kv[:, 128:].data_ptr(), _dt(q), ldq, kv.stride(0), kv.stride(0),
                 _ptr(_i64(window_pos, "window_pos")), p, n_w, 4, 32, _ptr(out), _dt(out), None, None,
                 _ptr(error_flag(dev)), _stream(),
             ),
             "latent_broadcast",
-        )
+        ))
     return out
 
 
@@ -393,14 +450,17 @@ def row_encode(pre: Tensor, table: Tensor, window: Tensor, cls: Tensor, cell_ptr
         empty_rows = empty_rows.float().contiguous()
     out = torch.empty((n_cells, pre.shape[1]), dtype=torch.float32, device=dev)
     if n_cells:
-        _check(
+        # per entry: its indices and the pre row; per cell: the output row
+        e = window.numel()
+        nbytes = e * (16 + pre.shape[1] * pre.element_size()) + n_cells * (8 + 4 * pre.shape[1])
+        _launch("row_encode", nbytes, 2 * e * pre.shape[1], lambda: _check(
             _lib().mantis_row_encode(
                 _ptr(pre), _dt(pre), pre.shape[0], pre.shape[1], _ptr(table), table.shape[0],
                 _ptr(window), _ptr(cls), window.numel(), _ptr(cell_ptr), n_cells,
                 _ptr(empty_counts), _ptr(empty_rows), _ptr(out), _ptr(error_flag(dev)), _stream(),
             ),
             "row_encode",
-        )
+        ))
     return out
 
 
@@ -534,9 +594,10 @@ def layer_norm(x: Tensor, gamma: Tensor, beta: Tensor, out_dtype: torch.dtype = 
     if x.ndim != 2 or x.shape[1] != 128 or x.dtype != torch.float32 or x.stride(1) != 1:
         raise ValueError("layer_norm takes fp32 (n, 128) rows")
     out = torch.empty(x.shape, dtype=out_dtype, device=dev)
-    _check(_lib().mantis_layer_norm(_ptr(x), x.stride(0), x.shape[0], _ptr(gamma.float().contiguous()),
-                                    _ptr(beta.float().contiguous()), _ptr(out), _MODES_LN[out_dtype], 128,
-                                    _stream()), "layer_norm")
+    g32, b32 = gamma.float().contiguous(), beta.float().contiguous()
+    _launch(f"layer_norm_{_SHORT[out_dtype]}", x.shape[0] * 128 * (4 + out.element_size()), 0, lambda: _check(
+        _lib().mantis_layer_norm(_ptr(x), x.stride(0), x.shape[0], _ptr(g32), _ptr(b32), _ptr(out),
+                                 _MODES_LN[out_dtype], 128, _stream()), "layer_norm"))
     return out
 
 
@@ -553,10 +614,13 @@ def value_read(token: Tensor, rows: Tensor, offsets: Tensor, order: Tensor, gamm
     if queries.shape != (4, 128):
         raise ValueError("value_read takes four 128-wide queries")
     out = torch.empty((p, 4, 128), dtype=torch.float32, device=dev)
-    _check(_lib().mantis_value_read(_ptr(token), _ptr(rows), rows.shape[0], _ptr(_i64(offsets, "offsets")),
-                                    _ptr(_i64(order, "order")), p, _ptr(gamma.float().contiguous()),
-                                    _ptr(beta.float().contiguous()), _ptr(queries.float().contiguous()), 4,
-                                    _ptr(out), _ptr(error_flag(dev)), _stream()), "value_read")
+    offsets, order = _i64(offsets, "offsets"), _i64(order, "order")
+    g32, b32, q32 = gamma.float().contiguous(), beta.float().contiguous(), queries.float().contiguous()
+    nbytes = (rows.shape[0] + p) * (512 + 8) + p * 4 * 512
+    _launch("value_read", nbytes, 0, lambda: _check(
+        _lib().mantis_value_read(_ptr(token), _ptr(rows), rows.shape[0], _ptr(offsets), _ptr(order), p, _ptr(g32),
+                                 _ptr(b32), _ptr(q32), 4, _ptr(out), _ptr(error_flag(dev)), _stream()),
+        "value_read"))
     return out
 
 
@@ -568,9 +632,10 @@ def compose_q(critic: Tensor, offsets: Tensor, mass_floor: float) -> tuple[Tenso
     n = critic.shape[0]
     qv = torch.empty(n, dtype=torch.float32, device=dev)
     qs = torch.empty(n, dtype=torch.float32, device=dev)
-    _check(_lib().mantis_compose_q(_ptr(critic), critic.stride(0), _ptr(_i64(offsets, "offsets")),
-                                   offsets.numel() - 1, n, float(mass_floor), _ptr(qv), _ptr(qs), _stream()),
-           "compose_q")
+    offsets = _i64(offsets, "offsets")
+    _launch("compose_q", n * (12 + 8), 0, lambda: _check(
+        _lib().mantis_compose_q(_ptr(critic), critic.stride(0), _ptr(offsets), offsets.numel() - 1, n,
+                                float(mass_floor), _ptr(qv), _ptr(qs), _stream()), "compose_q"))
     return qv, qs
 
 

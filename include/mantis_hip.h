@@ -84,6 +84,29 @@ int32_t mantis_cell_attention(const void* q, const void* k, const void* v, int32
                               int32_t* err_flag, void* stream);
 
 /*
+ * Fused typed-attention sub-stage over the rows of an fp32 residual stream
+ * x (n_rows, 128) with row stride ldx, in place:
+ *   q  = fp16(LN(x) Wq^T + bq)       (LayerNorm without affine: fold it into Wq/bq)
+ *   a  = fp16(typed segment attention of q, as mantis_cell_attention, 4 heads x 32)
+ *   x += a Wo^T + bo
+ * Wq, Wo: (128, 128) fp16 row-major (out x in); bq, bo: (128,) fp32.  k and v:
+ * fp16 (n_src, 128) rows with strides ldk/ldv (typically the two halves of one
+ * (n_src, 256) buffer); bias (4, n_classes) fp32; vcls (n_classes, 128) fp16
+ * or NULL; seg_ptr (n_rows + 1) CSR over the entries (src, cls).  Same
+ * numerics as mantis_fused_linear (projection) -> mantis_cell_attention ->
+ * mantis_fused_linear (residual), in one pass over x.
+ * Replaces the q projection, cell_read/window_read and output projection of
+ * the reference's _cell_stage (model.py:397-490; kernels
+ * cell_latents.py:213-285, 834-1001).
+ */
+int32_t mantis_attention_substage(float* x, int64_t ldx, int64_t n_rows, const void* wq, const float* bq,
+                                  const void* k, const void* v, int64_t ldk, int64_t ldv, int64_t n_src,
+                                  const float* bias, int64_t n_classes, const void* vcls,
+                                  const int64_t* seg_ptr, const int64_t* src, const int64_t* cls,
+                                  int64_t n_entries, const void* wo, const float* bo, int32_t* err_flag,
+                                  void* stream);
+
+/*
  * Window-latent read: four latent queries per position attend over the
  * position's windows (rows order[offsets[p]:offsets[p+1]] of k/v).  q is
  * (P*4, heads*hd), k/v (n_w, heads*hd) rows in `dtype` with row strides

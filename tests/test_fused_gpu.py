@@ -174,3 +174,36 @@ def test_compose_q_matches_reference_formula(device):
     mass = torch.zeros(4).index_reduce_(0, seg, pr[:, 0] + pr[:, 1], "amax", include_self=False)
     torch.testing.assert_close(qv.cpu(), q, rtol=1e-5, atol=1e-6)
     torch.testing.assert_close(qs.cpu(), q / mass.clamp(min=0.2)[seg], rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("with_vcls", [True, False])
+def test_attention_substage_matches_the_three_step_composition(device, with_vcls):
+    # the fused sub-stage must reproduce projection -> typed attention ->
+    # output projection + residual as separate launches compute them
+    gen = _g(9)
+    n, n_src, classes = 1003, 97, 726
+    counts = torch.randint(0, 9, (n,), generator=gen)
+    counts[::7] = 0  # rows without entries read zero
+    counts[5] = 40   # a row longer than one 16-entry chunk
+    dest = torch.repeat_interleave(torch.arange(n), counts)
+    src = torch.randint(0, n_src, (dest.numel(),), generator=gen)
+    cls = torch.randint(0, classes, (dest.numel(),), generator=gen)
+    ptr = torch.searchsorted(dest, torch.arange(n + 1))
+    x = 2 * torch.randn(n, 128, generator=gen) + 0.5
+    kv = torch.randn(n_src, 256, generator=gen).to(H16)
+    wq, wo = _w(128, 128, gen), _w(128, 128, gen)
+    bq, bo = 0.1 * torch.randn(128, generator=gen), 0.1 * torch.randn(128, generator=gen)
+    bias = 0.3 * torch.randn(4, classes, generator=gen)
+    vcls = (0.1 * torch.randn(classes, 128, generator=gen)).to(H16) if with_vcls else None
+    d = lambda t: None if t is None else t.to(device)  # noqa: E731
+    q = ops.fused_linear(d(x), d(wq), d(bq), layer_norm=True)
+    kvd = d(kv)
+    a = ops.cell_attention(q, kvd[:, :128], kvd[:, 128:], d(bias), d(vcls), d(ptr), d(src), d(cls),
+                           out_dtype=H16)
+    ref = d(x)
+    ops.fused_linear(a.view(n, 128), d(wo), d(bo), out=ref, residual=True)
+    got = d(x)
+    ops.attention_substage(got, d(wq), d(bq), kvd, d(bias), d(vcls), d(ptr), d(src), d(cls), d(wo), d(bo))
+    ops.raise_on_device_error(device)
+    torch.testing.assert_close(got.cpu(), ref.cpu(), rtol=1e-5, atol=2e-5)
+    assert not torch.equal(got.cpu(), x)
