@@ -226,33 +226,71 @@ def _stable_order(key: Tensor) -> Tensor:
     return torch.argsort(key, stable=True)
 
 
+def _canonical_orders(b: Batch, window_pos: Tensor) -> bool:
+    """Whether the batch arrives in the encoder's canonical orders, so the
+    stable sorts of the table derivation are identities (or, for the
+    window-major decoder view, equal to the batch's act_rev permutation):
+    dec_cell, radius_dst and window_pos ascending, and act_rev exactly the
+    stable argsort of dec_window — checked as strict lexicographic ascent of
+    (dec_window[act_rev[i]], act_rev[i]) with act_rev in range, which holds
+    for that permutation and no other.  One 4-byte device-to-host read."""
+    def ascending(x):
+        return (x[1:] >= x[:-1]).all() if x.numel() > 1 else torch.ones((), dtype=torch.bool, device=x.device)
+
+    e = b.dec_window.numel()
+    rev = b.act_rev
+    flags = [ascending(b.dec_cell), ascending(b.radius_dst), ascending(window_pos)]
+    if rev.shape != (e,):
+        return False
+    if e:
+        in_range = ((rev >= 0) & (rev < e)).all()
+        r = rev.clamp(0, e - 1)
+        kw = b.dec_window.index_select(0, r)
+        strict = ((kw[1:] > kw[:-1]) | ((kw[1:] == kw[:-1]) & (r[1:] > r[:-1]))).all() if e > 1 else in_range
+        flags += [in_range, strict]
+    return bool(torch.stack(flags).all().item())
+
+
 def make_plan(model, b: Batch) -> Plan:
     cfg = model.cfg
     dev = b.stone_own.device
     p, max_t, max_w = b.attn_valid.shape[0], b.attn_valid.shape[1], b.value_valid.shape[1]
     n_s, n_w, n_c = b.stone_own.shape[0], b.window_feat.shape[0], b.cell_pos.shape[0]
+    window_pos = torch.div(b.window_slot, max_w, rounding_mode="floor")
+    canonical = _canonical_orders(b, window_pos)
     # incidence plan (message_passing.py:495-517)
     order = _stable_order(b.inc_stone.to(torch.int32))
     run_stone, run_window, run_class = b.inc_stone[order], b.inc_window[order], b.inc_class[order]
-    # window-latent layout (window_latents.py:38-56)
-    window_pos = torch.div(b.window_slot, max_w, rounding_mode="floor")
-    lorder = _stable_order(window_pos.to(torch.int32))
-    offsets = ops.runs_to_ptr(window_pos[lorder].contiguous(), p)
-    # decoder cell tables over all legal cells (cell_latents.py:96-165)
-    corder = _stable_order(b.dec_cell)
-    edge_window, edge_class, edge_cell = b.dec_window[corder], b.dec_class[corder], b.dec_cell[corder]
-    cell_ptr = ops.runs_to_ptr(edge_cell.contiguous(), n_c)
-    covered = cell_ptr[1:] > cell_ptr[:-1]
-    worder = _stable_order(edge_window)
-    win_ptr = ops.runs_to_ptr(edge_window[worder].contiguous(), n_w)
-    # radius edge tables (cell_nodes.py:23-94, model.py:843-859)
     classes = b.radius_orbit + ORBIT48 * (b.radius_own + 2 * b.radius_on_axis)
     src, dst = b.radius_src, b.radius_dst
+    if canonical:
+        # the sorts below are identities on canonical batches (and act_rev is
+        # the window-major one): the same tables without them
+        lorder = torch.arange(n_w, device=dev)
+        offsets = ops.runs_to_ptr(window_pos, p)
+        edge_window, edge_class, edge_cell = b.dec_window, b.dec_class, b.dec_cell
+        worder = b.act_rev
+    else:
+        # window-latent layout (window_latents.py:38-56)
+        lorder = _stable_order(window_pos.to(torch.int32))
+        offsets = ops.runs_to_ptr(window_pos[lorder].contiguous(), p)
+        # decoder cell tables over all legal cells (cell_latents.py:96-165)
+        corder = _stable_order(b.dec_cell)
+        edge_window, edge_class, edge_cell = b.dec_window[corder], b.dec_class[corder], b.dec_cell[corder]
+        worder = _stable_order(edge_window)
+    cell_ptr = ops.runs_to_ptr(edge_cell.contiguous(), n_c)
+    covered = cell_ptr[1:] > cell_ptr[:-1]
+    win_ptr = ops.runs_to_ptr(edge_window[worder].contiguous(), n_w)
+    # radius edge tables (cell_nodes.py:23-94, model.py:843-859)
     if cfg.cell_node_scope == "uncovered":
         keep = ~covered[dst]
         src, dst, classes = src[keep], dst[keep], classes[keep]
-    rorder = _stable_order(dst)
-    radius_ptr = ops.runs_to_ptr(dst[rorder].contiguous(), n_c)
+    if canonical:
+        radius_src, radius_dst, radius_class = src, dst, classes
+    else:
+        rorder = _stable_order(dst)
+        radius_src, radius_dst, radius_class = src[rorder], dst[rorder], classes[rorder]
+    radius_ptr = ops.runs_to_ptr(radius_dst.contiguous(), n_c)
     # attention rows [latents; stones] per position over the [s; g] buffer
     gslot = (torch.arange(p, device=dev)[:, None] * max_t + torch.arange(GLOBAL_ROWS, device=dev)[None, :]).reshape(-1)
     attn_src = torch.full((p * max_t,), -1, dtype=torch.long, device=dev)
@@ -267,9 +305,9 @@ def make_plan(model, b: Batch) -> Plan:
         window_pos=window_pos, layout_offsets=offsets, layout_order=lorder,
         covered_mask=covered, cell_ptr=cell_ptr, edge_window=edge_window, edge_class=edge_class,
         win_ptr=win_ptr, edge_wcell=edge_cell[worder], edge_wclass=edge_class[worder],
-        radius_ptr=radius_ptr, radius_src=src[rorder], radius_class=classes[rorder],
+        radius_ptr=radius_ptr, radius_src=radius_src, radius_class=radius_class,
         seq_lens=b.attn_valid.sum(dim=1, dtype=torch.int32), attn_src=attn_src, attn_back=attn_back,
-        dec_cell_ptr=ops.runs_to_ptr(b.dec_cell, n_c),
+        dec_cell_ptr=cell_ptr if canonical else ops.runs_to_ptr(b.dec_cell, n_c),
     )
 
 

@@ -131,3 +131,20 @@ def test_forward_is_d6_invariant_to_fp16_tolerance(device):
         off += legal.shape[0]
         assert max(abs(got[t(m)] - v) for m, v in base.items()) <= 1e-2
     assert (out.value - out.value[0]).abs().max().item() <= 2e-3
+
+
+def test_non_canonical_edge_order_takes_the_sorting_path(device):
+    # a batch whose radius edges are not destination-major (legal for the
+    # reference, which sorts them) must give the canonical batch's outputs
+    net = _model(device, seed=6)
+    batch = collate_positions(synthetic.random_games(1, 3, start=11))
+    perm = torch.randperm(batch.radius_src.numel(), generator=torch.Generator().manual_seed(0))
+    shuffled = collate_positions(synthetic.random_games(1, 3, start=11))
+    for f in ("radius_src", "radius_dst", "radius_orbit", "radius_own", "radius_on_axis"):
+        setattr(shuffled, f, getattr(shuffled, f)[perm])
+    with torch.no_grad():
+        out = net(shuffled.to(device), 0.2)
+    # the oracle sorts the edges itself, so both batches have one reference;
+    # the GPU path's summation order differs, so hold it to the tolerances
+    rep = compare_outputs(out, oracle_forward(net, batch, 0.2), batch.legal_offsets)
+    assert rep["ok"], rep

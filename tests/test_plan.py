@@ -1,0 +1,43 @@
+"""The forward's table derivation detects canonical batches (CPU: the check
+is plain tensor arithmetic) and only then skips its stable sorts."""
+
+from __future__ import annotations
+
+import torch
+
+from mantisnet import collate_positions, synthetic
+from mantisnet.forward import _canonical_orders
+
+
+def _batch():
+    return collate_positions(synthetic.random_games(1, 4, start=3))
+
+
+def _window_pos(b):
+    return b.window_slot // b.value_valid.shape[1]
+
+
+def test_encoder_batches_are_canonical():
+    b = _batch()
+    assert _canonical_orders(b, _window_pos(b))
+    # act_rev is exactly the stable window-major argsort of the decoder entries
+    assert torch.equal(b.act_rev, torch.argsort(b.dec_window, stable=True))
+
+
+def test_any_deviation_is_detected():
+    b = _batch()
+    perm = torch.randperm(b.radius_dst.numel(), generator=torch.Generator().manual_seed(1))
+    b.radius_dst = b.radius_dst[perm]
+    assert not _canonical_orders(b, _window_pos(b))
+    b = _batch()
+    rev = b.act_rev.clone()
+    # swap two entries of one window run: still window-sorted, no longer stable
+    w = b.dec_window[rev]
+    i = int(torch.nonzero(w[1:] == w[:-1])[0])
+    rev[i], rev[i + 1] = rev[i + 1].clone(), rev[i].clone()
+    b.act_rev = rev
+    assert not _canonical_orders(b, _window_pos(b))
+    b = _batch()
+    b.act_rev = b.act_rev.clone()
+    b.act_rev[0] = b.act_rev.numel()  # out of range
+    assert not _canonical_orders(b, _window_pos(b))
