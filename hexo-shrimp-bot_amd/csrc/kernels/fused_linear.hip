@@ -18,7 +18,7 @@
 // fragments are already the B fragments of stage 2 (K slots
 // {4g..4g+3, 16+4g..16+4g+3} of each 32-step, matched by the W3 reads).
 // The weights live in LDS for the whole (persistent) workgroup; rows stream
-// from HBM once.
+// from HBM once, the next tile's rows in flight while the current computes.
 #include "common.hpp"
 #include "mfma.hpp"
 
@@ -120,27 +120,39 @@ __global__ void __launch_bounds__(kThreads) fused_linear_kernel(Args a) {
   const int64_t n_tiles = (a.m + kTileRows - 1) / kTileRows;
   const TX* xp = static_cast<const TX*>(a.x);
 
-  for (int64_t tile = blockIdx.x; tile < n_tiles; tile += gridDim.x) {
-    const int64_t row = tile * kTileRows + wave * 16 + l16;
-    const bool live = row < a.m;
-    // ---- prologue: this lane's 32 features of its row (4 chunks of 8)
-    int64_t src = row;
-    if (live && a.x_rows) {
-      src = a.x_rows[row];
+  // This lane's 32 features of its row of tile t (4 chunks of 8), through
+  // the optional row gather.  Software pipeline: the next tile's chunks are
+  // requested before the current tile computes, so its HBM latency overlaps
+  // the LayerNorm, the products and the stores.
+  auto fetch = [&](int64_t t, float (&dst)[4][8]) {
+    const int64_t r = t * kTileRows + wave * 16 + l16;
+    int64_t src = (t < n_tiles && r < a.m) ? r : -1;
+    if (src >= 0 && a.x_rows) {
+      src = a.x_rows[r];
       if (src >= a.n_x) {
         raise_flag(a.flag, MANTIS_FLAG_INDEX);
         src = -1;
       }
     }
-    float xv[4][8];
-    const bool have = live && src >= 0;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      if (have) load_chunk(xp + src * a.ldx + 32 * ks + 8 * g, xv[ks]);
+      if (src >= 0) load_chunk(xp + src * a.ldx + 32 * ks + 8 * g, dst[ks]);
       else
 #pragma unroll
-        for (int t = 0; t < 8; ++t) xv[ks][t] = 0.f;
+        for (int t2 = 0; t2 < 8; ++t2) dst[ks][t2] = 0.f;
     }
+  };
+  float xn[4][8];
+  fetch(blockIdx.x, xn);
+  for (int64_t tile = blockIdx.x; tile < n_tiles; tile += gridDim.x) {
+    const int64_t row = tile * kTileRows + wave * 16 + l16;
+    const bool live = row < a.m;
+    float xv[4][8];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int t = 0; t < 8; ++t) xv[ks][t] = xn[ks][t];
+    fetch(tile + gridDim.x, xn);
     if constexpr (kLN) {
       float s = 0.f;
 #pragma unroll
