@@ -94,6 +94,33 @@ __global__ void __launch_bounds__(kThreads) attn_substage_kernel(SubArgs a) {
 
   for (int64_t tile = t_begin + int64_t(blockIdx.x / kXcds) * kWaves + wave; tile < t_end; tile += waves_here) {
     const int64_t r0 = tile * 16;
+    // ---- 0. the attention's CSR pointers for this group's four rows, then
+    // the first 16 entry indices of each: requested now so that their two
+    // dependent round trips overlap step 1
+    // (32-bit: entry counts, sources and classes are < 2^31, checked by the host)
+    int32_t st[4], en[4], rs[4], rc[4];
+    {
+      int64_t pa[4], pb[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t row = r0 + grp + 4 * j;
+        pa[j] = row < a.n_rows ? a.seg_ptr[row] : 0;
+        pb[j] = row < a.n_rows ? a.seg_ptr[row + 1] : 0;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t lo = pa[j] < 0 ? 0 : (pa[j] > a.n_entries ? a.n_entries : pa[j]);
+        const int64_t hi = pb[j] < lo ? lo : (pb[j] > a.n_entries ? a.n_entries : pb[j]);
+        st[j] = int32_t(lo);
+        en[j] = int32_t(hi);
+        rs[j] = -1;
+        rc[j] = -1;
+        if (lo + gl < hi) {
+          rs[j] = int32_t(a.src[lo + gl]);
+          rc[j] = int32_t(a.cls[lo + gl]);
+        }
+      }
+    }
     // ---- 1. LayerNorm + Q projection (MFMA layout)
     {
       const int64_t row = r0 + l16;
@@ -148,27 +175,29 @@ __global__ void __launch_bounds__(kThreads) attn_substage_kernel(SubArgs a) {
     }
     wave_lds_fence();
     // ---- 2. attention (row layout): group grp takes tile rows grp, grp+4, grp+8, grp+12
-#pragma unroll 1
+#pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int lr = grp + 4 * j;
       const int64_t row = r0 + lr;
       if (row >= a.n_rows) break;
       Chunk8<_Float16> qc;
       qc.u = *reinterpret_cast<const uint4*>(buf + lr * kPitch + gl * 8);
-      int64_t st, en;
-      segment(a.seg_ptr, row, a.n_entries, st, en);
       float m = -INFINITY, l = 0.f;
       float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-      for (int64_t base = st; base < en; base += kGroup) {
-        const int cnt = int(en - base < kGroup ? en - base : kGroup);
-        int64_t rs = -1, rc = -1;
-        if (base + gl < en) {
-          rs = a.src[base + gl];
-          rc = a.cls[base + gl];
+      for (int64_t base = st[j]; base < en[j]; base += kGroup) {
+        const int cnt = int(en[j] - base < kGroup ? en[j] - base : kGroup);
+        int64_t ri = rs[j], ci = rc[j];  // (a negative 32-bit value stays invalid)
+        if (base != st[j]) {  // entries past the first 16 (long rows only)
+          ri = -1;
+          ci = -1;
+          if (base + gl < en[j]) {
+            ri = a.src[base + gl];
+            ci = a.cls[base + gl];
+          }
         }
-        // three entries in flight with class values, four without: what fits
-        // the 128-VGPR budget of 4 wavefronts per SIMD
-        attend_chunk<kVcls, kVcls ? 3 : 4>(qc, cnt, rs, rc, a.k, a.v, a.ldk, a.ldv, a.bias, a.n_classes, a.vcls, a.n_src,
+        // three entries in flight: what fits the 128-VGPR budget of 4
+        // wavefronts per SIMD next to the prefetched indices
+        attend_chunk<kVcls, 3>(qc, cnt, ri, ci, a.k, a.v, a.ldk, a.ldv, a.bias, a.n_classes, a.vcls, a.n_src,
                             a.scale, gl, a.flag, m, l, acc);
       }
       const float inv = l > 0.f ? 1.f / l : 1.f;
@@ -234,7 +263,7 @@ extern "C" int32_t mantis_attention_substage(float* x, int64_t ldx, int64_t n_ro
     return MANTIS_E_ARG;
   // gathered rows use 32-bit element offsets
   auto fits32 = [](int64_t rows, int64_t ld) { return rows <= 0 || (rows - 1) * ld + kK <= 4294967295LL; };
-  if (n_src > 2147483647LL || !fits32(n_src, ldk) || !fits32(n_src, ldv) || !fits32(n_classes, kK) ||
+  if (n_entries > 2147483647LL || n_classes > 2147483647LL || n_src > 2147483647LL || !fits32(n_src, ldk) || !fits32(n_src, ldv) || !fits32(n_classes, kK) ||
       4 * n_classes > 4294967295LL)
     return MANTIS_E_ARG;
   SubArgs a{x, ldx, n_rows, static_cast<const _Float16*>(wq), bq, static_cast<const _Float16*>(k),
