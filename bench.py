@@ -233,7 +233,7 @@ def main() -> int:
         torch.cuda.synchronize()
         ops.raise_on_device_error(dev)
         _log(f"warm-up done ({args.warmup} steps)")
-        traced = ("attention_substage", "cell_attention", "fused_linear", "stone_attention", "run_reduce",
+        traced = ("attention_substage", "cell_attention", "cell_heads", "fused_linear", "stone_attention", "run_reduce",
                   "runs_to_ptr", "latent_", "row_encode", "layer_norm", "value_read", "compose_q")
         per_step = []
         with ops.trace(*traced) as tr:

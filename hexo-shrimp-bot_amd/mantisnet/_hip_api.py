@@ -18,6 +18,9 @@ SIGNATURES = {
         i32),
     "mantis_attention_substage": (
         [vp, i64, i64, vp, vp, vp, vp, i64, i64, i64, vp, i64, vp, vp, vp, vp, i64, vp, vp, vp, vp], i32),
+    "mantis_cell_heads": (
+        [vp, i32, i32, i64, i64, vp, vp, vp, vp, vp, vp, i64, vp, i64, vp, vp, vp, i64, vp, i64, vp, vp, vp, vp, vp,
+         i64, vp, vp, vp], i32),
     "mantis_latent_read": ([vp, vp, vp, i32, i64, i64, i64, vp, vp, i64, i64, i32, i32, vp, vp, vp, vp, vp], i32),
     "mantis_latent_broadcast": ([vp, vp, vp, i32, i64, i64, i64, vp, i64, i64, i32, i32, vp, i32, vp, vp, vp, vp],
                                 i32),

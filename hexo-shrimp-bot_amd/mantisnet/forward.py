@@ -163,7 +163,11 @@ def _prepare(model, P) -> dict[str, Tensor]:
         h2.append(la @ P[ext + ".weight"])
         hb.append(P[mlp + ".lin_a.bias"])
         tabs.append(P[emb + ".weight"] @ la.t())
-    t["head1.w"] = torch.cat(h1).to(HALF).contiguous()
+    h1w = torch.cat(h1)
+    t["head1.w"] = h1w.to(HALF).contiguous()
+    # the same first layer reading raw cell rows: ln_out's affine folded in
+    t["head1ln.w"] = (h1w * P["ln_out.weight"][None, :]).to(HALF).contiguous()
+    t["head1ln.b"] = (torch.cat(hb) + h1w @ P["ln_out.bias"]).contiguous()
     t["head2.w"] = torch.cat(h2).to(HALF).contiguous()
     t["head1.b"] = torch.cat(hb).contiguous()
     t["head_tab"] = torch.cat(tabs, 1).contiguous()  # (726, 256)
@@ -431,7 +435,9 @@ def trunk(model, batch: Batch):
     return _trunk(model, b, plan)
 
 
-def _trunk(model, b: Batch, plan: Plan):
+def _trunk(model, b: Batch, plan: Plan, raw_cells: bool = False):
+    """(w_out, g_out, cells): cells are ln_out(c) in fp16, or with raw_cells
+    the fp32 cell state itself (the fused heads normalise it on the fly)."""
     W = _prepared(model)
     P = dict(model.named_parameters())
     cfg = model.cfg
@@ -450,7 +456,7 @@ def _trunk(model, b: Batch, plan: Plan):
     g = sg[n_s:].view(p, GLOBAL_ROWS, 128)
     w_out = ops.layer_norm(w, P["ln_out.weight"], P["ln_out.bias"], F32)
     g_out = F.layer_norm(g, (128,), P["ln_out.weight"], P["ln_out.bias"], 1e-5).mean(dim=1)
-    cells = ops.layer_norm(c, P["ln_out.weight"], P["ln_out.bias"], HALF)
+    cells = c if raw_cells else ops.layer_norm(c, P["ln_out.weight"], P["ln_out.bias"], HALF)
     return w_out, g_out, cells
 
 
@@ -471,22 +477,21 @@ def _value_head(model, w: Tensor, g: Tensor, b: Batch, plan: Plan):
     return dist @ model.bin_centers, dist, logits
 
 
-def _head_rows(model, w: Tensor, g: Tensor, cells: Tensor, b: Batch, plan: Plan) -> Tensor:
-    """(N_c, 16) fp32: column 0 the policy logit, 1..3 the critic logits."""
+def _head_rows(model, w: Tensor, g: Tensor, cells: Tensor, b: Batch, plan: Plan, raw_cells: bool = False) -> Tensor:
+    """(N_c, 16) fp32: column 0 the policy logit, 1..3 the critic logits.
+    ``cells`` are ln_out(c) rows, or with raw_cells the fp32 cell state."""
     if cells is None:
         raise ValueError("cell state is on but the trunk's cell rows were not passed to the decoder")
     W = _prepared(model)
     P = dict(model.named_parameters())
-    n_c = plan.n_c
     pre = FL(w.float().contiguous(), W["act_proj.w"], W["act_proj.b"])  # act_proj(w), fp16
     empty_rows = F.relu(P["act_empty_base"] + P["act_table.weight"].index_select(0, model.act_empty_classes))
-    acts = ops.row_encode(pre, P["act_table.weight"], b.dec_window, b.act_class, plan.dec_cell_ptr, n_c,
-                          b.act_empty, empty_rows)
-    extra = ops.run_reduce(W["head_tab"], b.dec_class, plan.dec_cell_ptr, n_c, F32)  # (N_c, 256)
     g_half = F.linear(g.float(), W["glin_b"]).contiguous()  # (P, 256)
     x = cells if cells.dtype in (HALF, F32) else cells.float()
-    return FL(x.contiguous(), W["head1.w"], W["head1.b"], x2=acts, w2=W["head2.w"], add1=extra, add2=g_half,
-              add2_rows=b.cell_pos, relu=True, w3=W["head3.w"], b3=W["head3.b"], out_dtype=F32)
+    key = "head1ln" if raw_cells else "head1"
+    return ops.cell_heads(x.contiguous(), W[key + ".w"], W[key + ".b"], W["head2.w"], W["head3.w"], W["head3.b"], pre,
+                          P["act_table.weight"], empty_rows, b.act_empty, W["head_tab"], g_half, b.cell_pos,
+                          plan.dec_cell_ptr, b.dec_window, b.act_class, b.dec_class, layer_norm=raw_cells)
 
 
 @torch.no_grad()
@@ -504,8 +509,8 @@ def cell_heads(model, w: Tensor, g: Tensor, cells: Tensor, batch: Batch, mass_fl
     return _cell_heads(model, w, g, cells, b, plan, mass_floor)
 
 
-def _cell_heads(model, w, g, cells, b: Batch, plan: Plan, mass_floor: float):
-    rows = _head_rows(model, w, g, cells, b, plan)
+def _cell_heads(model, w, g, cells, b: Batch, plan: Plan, mass_floor: float, raw_cells: bool = False):
+    rows = _head_rows(model, w, g, cells, b, plan, raw_cells)
     q_values, q_score = ops.compose_q(rows[:, 1:], b.legal_offsets, mass_floor)
     return rows[:, 0].contiguous(), q_score, q_values
 
@@ -520,7 +525,7 @@ def forward(model, batch: Batch, mass_floor: float):
     dev = next(model.parameters()).device
     b = batch if batch.stone_own.device == dev else batch.to(dev)
     plan = make_plan(model, b)
-    w, g, cells = _trunk(model, b, plan)
+    w, g, c = _trunk(model, b, plan, raw_cells=True)
     value, value_dist, value_logits = _value_head(model, w, g, b, plan)
-    policy, q_score, q_values = _cell_heads(model, w, g, cells, b, plan, mass_floor)
+    policy, q_score, q_values = _cell_heads(model, w, g, c, b, plan, mass_floor, raw_cells=True)
     return policy, q_score, q_values, value, value_dist, value_logits

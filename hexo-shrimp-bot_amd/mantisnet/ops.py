@@ -341,6 +341,56 @@ def attention_substage(x: Tensor, wq: Tensor, bq: Tensor, kv: Tensor, bias: Tens
     return x
 
 
+def cell_heads(c: Tensor, w1: Tensor, b1: Tensor, w2: Tensor, w3: Tensor, b3: Tensor, pre: Tensor,
+               act_table: Tensor, empty_rows: Tensor, act_empty: Tensor, head_tab: Tensor, g_half: Tensor,
+               cell_pos: Tensor, dec_ptr: Tensor, dec_window: Tensor, act_class: Tensor, dec_class: Tensor,
+               layer_norm: bool) -> Tensor:
+    """(n_cells, 16) fp32 head rows of every cell in one launch (see
+    mantis_cell_heads in include/mantis_hip.h): column 0 the policy logit,
+    1..3 the critic logits."""
+    dev = _on_gpu(c, w1, b1, w2, w3, b3, pre, act_table, empty_rows, act_empty, head_tab, g_half, cell_pos, dec_ptr,
+                  dec_window, act_class, dec_class)
+    n = c.shape[0]
+    if c.ndim != 2 or c.shape[1] != 128 or c.stride(1) != 1 or c.dtype not in (torch.float32, torch.float16):
+        raise ValueError("c must be (n_cells, 128) fp32 or fp16 rows")
+    if layer_norm and c.dtype != torch.float32:
+        raise ValueError("the fused LayerNorm reads fp32 rows")
+    for t, shape, name in ((w1, (256, 128), "w1"), (w2, (256, 128), "w2"), (w3, (16, 256), "w3")):
+        if t.shape != shape or t.dtype != torch.float16 or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous fp16 {shape} matrix")
+    if pre.ndim != 2 or pre.shape[1] != 128 or pre.dtype != torch.float16 or not pre.is_contiguous():
+        raise ValueError("pre must be contiguous fp16 (n_w, 128) rows")
+    f32 = lambda t: t.float().contiguous()  # noqa: E731
+    b1, b3, act_table, empty_rows, head_tab, g_half = map(f32, (b1, b3, act_table, empty_rows, head_tab, g_half))
+    if empty_rows.shape != (3, 128) or head_tab.shape[1] != 256 or g_half.shape[1] != 256:
+        raise ValueError("empty_rows (3, 128), head_tab (n, 256) and g_half (P, 256) expected")
+    act_empty = _i64(act_empty, "act_empty")
+    cell_pos, dec_ptr = _i64(cell_pos, "cell_pos"), _i64(dec_ptr, "dec_ptr")
+    dec_window, act_class, dec_class = _i64(dec_window, "dec_window"), _i64(act_class, "act_class"), \
+        _i64(dec_class, "dec_class")
+    if act_empty.shape != (n, 3) or cell_pos.numel() != n or dec_ptr.numel() != n + 1:
+        raise ValueError("act_empty (n, 3), cell_pos (n,) and dec_ptr (n + 1,) expected")
+    if not (dec_window.shape == act_class.shape == dec_class.shape) or dec_window.ndim != 1:
+        raise ValueError("the decoder entry views must have one length")
+    out = torch.empty((n, 16), dtype=torch.float32, device=dev)
+    if n:
+        e = dec_window.numel()
+        # the cell rows once, the output rows once, per entry its three
+        # indices, each action-projection row once
+        nbytes = n * (128 * c.element_size() + 64 + 16 + 24) + e * 24 + pre.shape[0] * 256
+        flops = n * 2 * (2 * 256 * 128 + 16 * 256)
+        _launch("cell_heads", nbytes, flops, lambda: _check(
+            _lib().mantis_cell_heads(
+                _ptr(c), _dt(c), int(layer_norm), c.stride(0), n, _ptr(w1), _ptr(b1), _ptr(w2), _ptr(w3), _ptr(b3),
+                _ptr(pre), pre.shape[0], _ptr(act_table), act_table.shape[0], _ptr(empty_rows), _ptr(act_empty),
+                _ptr(head_tab), head_tab.shape[0], _ptr(g_half), g_half.shape[0], _ptr(cell_pos), _ptr(dec_ptr),
+                _ptr(dec_window), _ptr(act_class), _ptr(dec_class), e, _ptr(out), _ptr(error_flag(dev)), _stream(),
+            ),
+            "cell_heads",
+        ))
+    return out
+
+
 def latent_read(q: Tensor, k: Tensor, v: Tensor, offsets: Tensor, order: Tensor, stats: bool = False):
     """Four latent queries per position over its windows; q (P, 4, ...) and
     k/v 128-wide rows; returns fp32 (P, 4, 4, 32) [and m, l]."""

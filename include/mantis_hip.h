@@ -107,6 +107,30 @@ int32_t mantis_attention_substage(float* x, int64_t ldx, int64_t n_rows, const v
                                   void* stream);
 
 /*
+ * Fused cell heads: for every legal cell r (position cell_pos[r]) with
+ * decoder entries e in [dec_ptr[r], dec_ptr[r+1]):
+ *   x    = fp16(LN(c[r])) if layer_norm (no affine: fold it into w1/b1), else fp16(c[r])
+ *   acts = sum_e relu(pre[dec_window[e]] + act_table[act_class[e]]) + sum_k act_empty[r,k] * empty_rows[k]
+ *   h    = relu(w1 x + w2 fp16(acts) + b1 + sum_e head_tab[dec_class[e]] + g_half[cell_pos[r]])
+ *   out[r] = w3 fp16(h) + b3
+ * c: (n_cells, 128) rows in c_dtype (fp32, or fp16 without layer_norm), row
+ * stride ldc; w1, w2: (256, 128) fp16; b1 (256); w3 (16, 256) fp16; b3 (16);
+ * pre (n_w, 128) fp16; act_table (n_acls, 128), empty_rows (3, 128),
+ * head_tab (n_dcls, 256), g_half (n_pos, 256) fp32; act_empty (n_cells, 3)
+ * and the index arrays int64; out (n_cells, 16) fp32.
+ * Replaces the reference's _action_contribution / encode_rows / class_row_sum
+ * and the first layers of mlp_p and mlp_q (model.py:1031-1091,
+ * row_encoder.py:40-112, message_passing.py:331-339).
+ */
+int32_t mantis_cell_heads(const void* c, int32_t c_dtype, int32_t layer_norm, int64_t ldc, int64_t n_cells,
+                          const void* w1, const float* b1, const void* w2, const void* w3, const float* b3,
+                          const void* pre, int64_t n_w, const float* act_table, int64_t n_acls,
+                          const float* empty_rows, const int64_t* act_empty, const float* head_tab, int64_t n_dcls,
+                          const float* g_half, int64_t n_pos, const int64_t* cell_pos, const int64_t* dec_ptr,
+                          const int64_t* dec_window, const int64_t* act_class, const int64_t* dec_class,
+                          int64_t n_entries, float* out, int32_t* err_flag, void* stream);
+
+/*
  * Window-latent read: four latent queries per position attend over the
  * position's windows (rows order[offsets[p]:offsets[p+1]] of k/v).  q is
  * (P*4, heads*hd), k/v (n_w, heads*hd) rows in `dtype` with row strides

@@ -207,3 +207,45 @@ def test_attention_substage_matches_the_three_step_composition(device, with_vcls
     ops.raise_on_device_error(device)
     torch.testing.assert_close(got.cpu(), ref.cpu(), rtol=1e-5, atol=2e-5)
     assert not torch.equal(got.cpu(), x)
+
+
+@pytest.mark.parametrize("mode", ["layer_norm", "fp16_rows", "fp32_rows"])
+def test_cell_heads_match_the_unfused_composition(device, mode):
+    # fused heads = row_encode + class_row_sum + the two-layer head GEMM
+    gen = _g(10)
+    n, n_w, p, acls, dcls = 1500, 300, 7, 729, 726
+    counts = torch.randint(0, 7, (n,), generator=gen)
+    counts[3] = 19  # longest decoder run
+    dest = torch.repeat_interleave(torch.arange(n), counts)
+    e = dest.numel()
+    win = torch.randint(0, n_w, (e,), generator=gen)
+    acl = torch.randint(0, acls, (e,), generator=gen)
+    dcl = torch.randint(0, dcls, (e,), generator=gen)
+    ptr = torch.searchsorted(dest, torch.arange(n + 1))
+    cell_pos = torch.sort(torch.randint(0, p, (n,), generator=gen)).values
+    c = 2 * torch.randn(n, 128, generator=gen) + 0.3
+    pre = torch.randn(n_w, 128, generator=gen).to(H16)
+    table = 0.5 * torch.randn(acls, 128, generator=gen)
+    empty_rows = torch.randn(3, 128, generator=gen).relu()
+    act_empty = torch.randint(0, 6, (n, 3), generator=gen)
+    head_tab = 0.2 * torch.randn(dcls, 256, generator=gen)
+    g_half = torch.randn(p, 256, generator=gen)
+    w1, w2 = _w(256, 128, gen), _w(256, 128, gen)
+    w3 = torch.zeros(16, 256)
+    w3[0, :128] = 0.05 * torch.randn(128, generator=gen)
+    w3[1:4, 128:] = 0.05 * torch.randn(3, 128, generator=gen)
+    w3 = w3.to(H16)
+    b1, b3 = 0.1 * torch.randn(256, generator=gen), 0.1 * torch.randn(16, generator=gen)
+    d = lambda t: t.to(device)  # noqa: E731
+    x = {"layer_norm": c, "fp16_rows": c.to(H16), "fp32_rows": c}[mode]
+    got = ops.cell_heads(d(x), d(w1), d(b1), d(w2), d(w3), d(b3), d(pre), d(table), d(empty_rows), d(act_empty),
+                         d(head_tab), d(g_half), d(cell_pos), d(ptr), d(win), d(acl), d(dcl),
+                         layer_norm=mode == "layer_norm")
+    ops.raise_on_device_error(device)
+    acts = ops.row_encode(d(pre), d(table), d(win), d(acl), d(ptr), n, d(act_empty), d(empty_rows))
+    ext = ops.run_reduce(d(head_tab), d(dcl), d(ptr), n, torch.float32)
+    # (fp32 rows enter the products as fp16, exactly as fp16 rows do)
+    xin = ops.layer_norm(d(c), d(torch.ones(128)), d(torch.zeros(128)), H16) if mode == "layer_norm" else d(c.to(H16))
+    ref = ops.fused_linear(xin, d(w1), d(b1), x2=acts, w2=d(w2), add1=ext, add2=d(g_half), add2_rows=d(cell_pos),
+                           relu=True, w3=d(w3), b3=d(b3), out_dtype=torch.float32)
+    torch.testing.assert_close(got.cpu(), ref.cpu(), rtol=1e-4, atol=1e-4)
