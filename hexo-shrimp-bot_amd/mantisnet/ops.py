@@ -222,9 +222,10 @@ def run_reduce(values: Tensor, gather: Tensor, ptr: Tensor, n_dest: int, out_dty
     out = torch.empty((n_dest, h), dtype=out_dtype, device=dev)
     if n_dest == 0 or h == 0:
         return out
-    # each gathered source row once, its index once, each destination row once
+    # each index once, each destination row once, and each source row at most once:
+    # a gather from a small table (class rows) costs the table, not one row per entry
     e = gather.numel()
-    nbytes = e * (8 + h * values.element_size()) + n_dest * (8 + h * out.element_size())
+    nbytes = e * 8 + min(e, values.shape[0]) * h * values.element_size() + n_dest * (8 + h * out.element_size())
     _launch(f"run_reduce_{_SHORT[values.dtype]}_{_SHORT[out_dtype]}", nbytes, e * h, lambda: _check(
         _lib().mantis_run_reduce(
             _ptr(values), _dt(values), values.shape[0], values.stride(0), h, _ptr(gather),
