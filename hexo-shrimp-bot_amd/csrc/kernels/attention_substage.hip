@@ -1,32 +1,38 @@
-// Fused typed-attention sub-stage for gfx950: for every row of a residual
-// stream x (cells or windows),
-//   q   = fp16( LN(x) Wq^T + bq )           LayerNorm affine folded into Wq/bq
-//   a   = fp16( attend(q, k/v rows of its CSR entries, class bias [, class values]) )
-//   x  += a Wo^T + bo                        (fp32, in place)
-// in one pass (replaces the q projection, cell_read/window_read attention and
-// output projection + residual of the reference's _cell_stage,
-// model.py:397-490, with the kernels of cell_latents.py:213-285 / 834-1001).
-// The numerics are those of the three separate steps: the same fp16
-// roundings of q and a, fp32 statistics, softmax and accumulation.
+// Fused typed-attention sub-stages for gfx950: for every row of a residual
+// stream x (cells or windows) and each of one or two stages s in order,
+//   q   = fp16( LN(x) Wq_s^T + bq_s )         LayerNorm affine folded into Wq/bq
+//   a   = fp16( attend(q, k/v rows of the row's CSR entries of stage s,
+//                      class bias [, class values]) )
+//   x  += a Wo_s^T + bo_s                     (fp32)
+// in one pass over x (replaces the q projection, cell_read/window_read
+// attention and output projection + residual of the reference's
+// _cell_stage, model.py:397-490, with the kernels of
+// cell_latents.py:213-285 / 834-1001; the two cell sub-stages, cells <-
+// windows then cells <- stones, run as the two stages of one launch).
+// The numerics are those of the separate steps: the same fp16 roundings of
+// q and a, fp32 statistics, softmax and accumulation.
 //
-// Work split: a wavefront owns a tile of 16 rows and carries it through all
-// three steps with no workgroup synchronisation:
-//   1. LayerNorm + Q projection in MFMA layout (lane = row l16, K group g:
-//      the lane loads its own row's 32 features, the statistics are a
-//      4-lane reduction, q^T = Wq . x-hat^T runs as v_mfma_f32_16x16x32_f16);
-//      q goes to a wavefront-private LDS tile in row layout;
-//   2. attention in row layout (16 lanes per row, 4 rows at a time, entry
-//      rows gathered in batches — the same arithmetic as cell_attention);
-//      a overwrites q in the LDS tile;
-//   3. o^T = Wo . a^T from the LDS tile; each lane adds four consecutive
-//      output features of its row to x (16-byte read-modify-write).
-// Wq and Wo live in LDS for the whole persistent workgroup (16 wavefronts,
-// one workgroup per CU).  Tiles are dealt out XCD-contiguously: the
-// workgroups of one XCD (dispatch is round-robin over the 8 XCDs) sweep
-// one contiguous eighth of the rows, so the gathered k/v rows of a
-// position stay in that XCD's L2.
+// Work split: a wavefront owns a tile of 16 rows.  Lane (g, r) = (lane/16,
+// lane%16) owns row r of the tile and attention head g for the whole pass,
+// so neither the residual nor any intermediate leaves the registers:
+//   x      lane holds x[r][32 ks + 8 g + t]   (ks 0..3, t 0..7; the B operand
+//          layout of v_mfma_f32_16x16x32_f16 for x^T)
+//   q      q^T = Wq' . LN(x)^T with the rows of Wq permuted so that the
+//          accumulator of lane (g, r) is q[r][32 g + 0..31] = head g
+//   attend the lane walks its row's entries and gathers the 64-byte head-g
+//          slices of k, v (and the class value).  Those rows are stored
+//          head-interleaved (element 32 w + 8 g + t is dim 8 w + t of head g),
+//          so the 16-byte load w of the four lanes of a row covers 64
+//          contiguous bytes and a row costs two L1 lines per 128 bytes, not four
+//   o      o^T = Wo' . a^T with the K order chosen so that the B fragment of
+//          lane (g, r) is its own head's output, and the rows of Wo permuted
+//          so that the accumulator lands on the lane's x registers.
+// Weights live in LDS (permuted while they are staged) for the persistent
+// workgroup, one workgroup per CU.  Tiles are dealt out XCD-contiguously:
+// the workgroups of one XCD (dispatch is round-robin over the 8 XCDs) sweep
+// one contiguous eighth of the rows, so the gathered k/v rows of a position
+// stay in that XCD's L2.
 #include "common.hpp"
-#include "gather.hpp"
 #include "mfma.hpp"
 
 namespace mantis {
@@ -34,14 +40,12 @@ namespace {
 
 constexpr int kK = 128;
 constexpr int kPitch = kK + 8;  // fp16 per staged LDS row (272 bytes: conflict-free fragment reads)
-constexpr int kWaves = 16;
+constexpr int kWaves = 12;
 constexpr int kThreads = kWaves * 64;
 constexpr int kXcds = 8;
+constexpr int kB = 1;  // entries whose rows are in flight together
 
-struct SubArgs {
-  float* x;
-  int64_t ldx;
-  int64_t n_rows;
+struct Stage {
   const _Float16* wq;
   const float* bq;
   const _Float16* k;
@@ -58,33 +62,86 @@ struct SubArgs {
   int64_t n_entries;
   const _Float16* wo;
   const float* bo;
+};
+
+struct SubArgs {
+  float* x;
+  int64_t ldx;
+  int64_t n_rows;
+  Stage st[2];
   float scale;
   int32_t* flag;
 };
 
-// This wavefront's LDS writes are complete and visible to its other lanes.
-__device__ __forceinline__ void wave_lds_fence() {
-  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-  __builtin_amdgcn_wave_barrier();
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+// LDS row r of the staged q weights holds Wq row qrow(r): the accumulator
+// row 16 nt + 4 g + t of lane group g is feature 32 g + 4 nt + t.
+__device__ __forceinline__ int qrow(int r) {
+  const int nt = r >> 4, j = r & 15;
+  return 32 * (j >> 2) + 4 * nt + (j & 3);
+}
+// LDS row r of the staged o weights holds Wo row orow(r): the accumulator
+// row 16 nt + 4 g + t is feature 32 (nt/2) + 8 g + 4 (nt%2) + t, the
+// lane's x register [nt/2][4 (nt%2) + t].
+__device__ __forceinline__ int orow(int r) {
+  const int nt = r >> 4, j = r & 15;
+  return 32 * (nt >> 1) + 8 * (j >> 2) + 4 * (nt & 1) + (j & 3);
 }
 
-template <bool kVcls>
+__device__ __forceinline__ float dot32(const uint32_t (&q)[16], const uint4 (&k)[4]) {
+  float d0 = 0.f, d1 = 0.f;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    d0 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, q[4 * w]), __builtin_bit_cast(f16x2_t, k[w].x), d0, false);
+    d1 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, q[4 * w + 1]), __builtin_bit_cast(f16x2_t, k[w].y), d1, false);
+    d0 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, q[4 * w + 2]), __builtin_bit_cast(f16x2_t, k[w].z), d0, false);
+    d1 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, q[4 * w + 3]), __builtin_bit_cast(f16x2_t, k[w].w), d1, false);
+  }
+  return d0 + d1;
+}
+
+// acc[i] += p * h[i] for the 32 fp16 values of four 16-byte chunks (v_fma_mix)
+__device__ __forceinline__ void axpy32(float (&acc)[32], float p, const uint4 (&h)[4]) {
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const uint32_t u[4] = {h[w].x, h[w].y, h[w].z, h[w].w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f16x2_t v = __builtin_bit_cast(f16x2_t, u[i]);
+      acc[8 * w + 2 * i] = fmaf(p, float(v[0]), acc[8 * w + 2 * i]);
+      acc[8 * w + 2 * i + 1] = fmaf(p, float(v[1]), acc[8 * w + 2 * i + 1]);
+    }
+  }
+}
+
+// the value v of lane `src` (all lanes active)
+__device__ __forceinline__ int32_t from_lane(int src, int32_t v) { return __builtin_amdgcn_ds_bpermute(src << 2, v); }
+
+// head g's 32 values of a head-interleaved row: chunk w sits at 32 w + 8 g
+__device__ __forceinline__ void load_head(const _Float16* row_g, uint4 (&h)[4]) {
+#pragma unroll
+  for (int w = 0; w < 4; ++w) h[w] = *reinterpret_cast<const uint4*>(row_g + 32 * w);
+}
+
+template <int kStages, bool kVcls>
 __global__ void __launch_bounds__(kThreads) attn_substage_kernel(SubArgs a) {
-  __shared__ __attribute__((aligned(16))) _Float16 swq[kK * kPitch];
-  __shared__ __attribute__((aligned(16))) _Float16 swo[kK * kPitch];
-  __shared__ __attribute__((aligned(16))) _Float16 sbuf[kWaves][16 * kPitch];
-  for (int i = threadIdx.x; i < kK * (kK / 8); i += kThreads) {
-    const int r = i / (kK / 8), c = (i % (kK / 8)) * 8;
-    *reinterpret_cast<uint4*>(swq + r * kPitch + c) = *reinterpret_cast<const uint4*>(a.wq + r * kK + c);
-    *reinterpret_cast<uint4*>(swo + r * kPitch + c) = *reinterpret_cast<const uint4*>(a.wo + r * kK + c);
+  __shared__ __attribute__((aligned(16))) _Float16 sw[kStages][2][kK * kPitch];  // [stage][q, o]
+#pragma unroll
+  for (int s = 0; s < kStages; ++s) {
+    for (int i = threadIdx.x; i < kK * (kK / 8); i += kThreads) {
+      const int r = i / (kK / 8), c = (i % (kK / 8)) * 8;
+      *reinterpret_cast<uint4*>(&sw[s][0][r * kPitch + c]) =
+          *reinterpret_cast<const uint4*>(a.st[s].wq + qrow(r) * kK + c);
+      *reinterpret_cast<uint4*>(&sw[s][1][r * kPitch + c]) =
+          *reinterpret_cast<const uint4*>(a.st[s].wo + orow(r) * kK + c);
+    }
   }
   __syncthreads();
 
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
-  const int l16 = lane % 16, g = lane / 16;  // MFMA layout
-  const int grp = lane / 16, gl = lane % 16;  // row layout: 4 groups of 16 lanes
-  _Float16* buf = sbuf[wave];
+  const int l16 = lane % 16, g = lane / 16;       // MFMA layout: row l16, head / K group g
+  const int ag = lane & 3;                        // attention layout: row lane / 4, head ag
+  const int src_m = 16 * (lane & 3) + (lane >> 2);  // MFMA lane of this attention lane's (row, head)
+  const int src_a = 4 * (lane & 15) + (lane >> 4);  // attention lane of this MFMA lane's (row, head)
 
   const int64_t n_tiles = (a.n_rows + 15) / 16;
   const int xcd = int(blockIdx.x % kXcds);
@@ -92,154 +149,242 @@ __global__ void __launch_bounds__(kThreads) attn_substage_kernel(SubArgs a) {
   const int64_t waves_here = wgs_here * kWaves;
   const int64_t t_begin = n_tiles * xcd / kXcds, t_end = n_tiles * (xcd + 1) / kXcds;
 
+  // The look-ahead loads below (the next batch's entries) are issued
+  // unconditionally from a clamped, valid address and validated only where
+  // their values are used: a check right after the load would make the
+  // wavefront wait for it there, and with in-order load counters also for
+  // every row load issued before it.
   for (int64_t tile = t_begin + int64_t(blockIdx.x / kXcds) * kWaves + wave; tile < t_end; tile += waves_here) {
-    const int64_t r0 = tile * 16;
-    // ---- 0. the attention's CSR pointers for this group's four rows, then
-    // the first 16 entry indices of each: requested now so that their two
-    // dependent round trips overlap step 1
-    // (32-bit: entry counts, sources and classes are < 2^31, checked by the host)
-    int32_t st[4], en[4], rs[4], rc[4];
-    {
-      int64_t pa[4], pb[4];
+    // an offset the compiler cannot see through: keeps the weight-fragment
+    // reads inside the loop instead of hoisting all of them into registers
+    int lds_off = 0;
+    asm volatile("" : "+s"(lds_off));
+    const int64_t row = tile * 16 + l16;
+    const bool live = row < a.n_rows;
+    const int64_t rc = live ? row : 0;  // dead lanes read a real row and store nothing
+    // the entry walk's pointers first (the first entries depend on them), then x
+    int64_t pa[kStages], pb[kStages];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int64_t row = r0 + grp + 4 * j;
-        pa[j] = row < a.n_rows ? a.seg_ptr[row] : 0;
-        pb[j] = row < a.n_rows ? a.seg_ptr[row + 1] : 0;
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int64_t lo = pa[j] < 0 ? 0 : (pa[j] > a.n_entries ? a.n_entries : pa[j]);
-        const int64_t hi = pb[j] < lo ? lo : (pb[j] > a.n_entries ? a.n_entries : pb[j]);
-        st[j] = int32_t(lo);
-        en[j] = int32_t(hi);
-        rs[j] = -1;
-        rc[j] = -1;
-        if (lo + gl < hi) {
-          rs[j] = int32_t(a.src[lo + gl]);
-          rc[j] = int32_t(a.cls[lo + gl]);
-        }
-      }
+    for (int s = 0; s < kStages; ++s) {
+      pa[s] = a.st[s].seg_ptr[rc];
+      pb[s] = a.st[s].seg_ptr[rc + 1];
     }
-    // ---- 1. LayerNorm + Q projection (MFMA layout)
-    {
-      const int64_t row = r0 + l16;
-      const bool live = row < a.n_rows;
-      float xv[4][8];
+    float xv[4][8];
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        if (live) load8(a.x + row * a.ldx + 32 * ks + 8 * g, xv[ks]);
-        else
+    for (int ks = 0; ks < 4; ++ks) load8(a.x + rc * a.ldx + 32 * ks + 8 * g, xv[ks]);
+    int64_t lo[kStages], hi[kStages];
 #pragma unroll
-          for (int t = 0; t < 8; ++t) xv[ks][t] = 0.f;
-      }
-      float s = 0.f;
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-        for (int t = 0; t < 8; ++t) s += xv[ks][t];
-      s += __shfl_xor(s, 16);
-      s += __shfl_xor(s, 32);
-      const float mean = s * (1.f / kK);
-      float sq = 0.f;
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-          const float d = xv[ks][t] - mean;
-          sq += d * d;
-        }
-      sq += __shfl_xor(sq, 16);
-      sq += __shfl_xor(sq, 32);
-      const float rstd = rsqrtf(sq * (1.f / kK) + 1e-5f);
-      f16x8_t xb[4];
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-        for (int t = 0; t < 8; ++t) xb[ks][t] = f2h((xv[ks][t] - mean) * rstd);
-#pragma unroll
-      for (int nt = 0; nt < 8; ++nt) {
-        f32x4_t d = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          const f16x8_t wf = *reinterpret_cast<const f16x8_t*>(swq + (16 * nt + l16) * kPitch + 32 * ks + 8 * g);
-          d = mfma16x16x32(wf, xb[ks], d);
-        }
-        const int f = 16 * nt + 4 * g;
-        const float4 b = *reinterpret_cast<const float4*>(a.bq + f);
-        uint2 w;
-        w.x = pack_f16x2(d[0] + b.x, d[1] + b.y);
-        w.y = pack_f16x2(d[2] + b.z, d[3] + b.w);
-        *reinterpret_cast<uint2*>(buf + l16 * kPitch + f) = w;
-      }
+    for (int s = 0; s < kStages; ++s) {
+      const int64_t n_e = a.st[s].n_entries;
+      lo[s] = pa[s] < 0 ? 0 : (pa[s] > n_e ? n_e : pa[s]);
+      hi[s] = pb[s] < lo[s] ? lo[s] : (pb[s] > n_e ? n_e : pb[s]);
     }
-    wave_lds_fence();
-    // ---- 2. attention (row layout): group grp takes tile rows grp, grp+4, grp+8, grp+12
+
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int lr = grp + 4 * j;
-      const int64_t row = r0 + lr;
-      if (row >= a.n_rows) break;
-      Chunk8<_Float16> qc;
-      qc.u = *reinterpret_cast<const uint4*>(buf + lr * kPitch + gl * 8);
+    for (int s = 0; s < kStages; ++s) {
+      const Stage& S = a.st[s];
+      const _Float16* swq = sw[s][0] + lds_off;
+      const _Float16* swo = sw[s][1] + lds_off;
+      // entry count of this lane's row, and the wavefront's longest row
+      const int cnt = live ? int(hi[s] - lo[s]) : 0;
+      int maxc = cnt;
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) maxc = max(maxc, __shfl_xor(maxc, o));
+      // The attention runs with lane 4 r + g on (row r, head g): the four
+      // lanes of a row are adjacent, so each 16-byte gather of a quad covers
+      // 64 contiguous bytes of a head-interleaved row.  q moves there and the
+      // output back by lane permutes.
+      const int acnt = from_lane(src_m, cnt);
+      const int64_t alo = int64_t((uint64_t(uint32_t(from_lane(src_m, int32_t(uint64_t(lo[s]) >> 32)))) << 32) |
+                                  uint32_t(from_lane(src_m, int32_t(lo[s]))));
+      // raw (source, class) of the batch's entries; a lane past its row's
+      // end reads entry 0 (there is one: some row of the tile has entries)
+      int64_t es[kB], ec[kB];
+      auto fetch = [&](int j0) {
+#pragma unroll
+        for (int u = 0; u < kB; ++u) {
+          const int64_t e = j0 + u < acnt ? alo + j0 + u : 0;
+          es[u] = S.src[e];
+          ec[u] = S.cls[e];
+        }
+      };
+      // the first batch's entries, requested before the projection
+      if (maxc > 0) fetch(0);
+      // ---- LayerNorm + Q projection
+      uint32_t qh[16];
+      {
+        float sum = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+          for (int t = 0; t < 8; ++t) sum += xv[ks][t];
+        sum += __shfl_xor(sum, 16);
+        sum += __shfl_xor(sum, 32);
+        const float mean = sum * (1.f / kK);
+        float sq = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+          for (int t = 0; t < 8; ++t) {
+            const float d = xv[ks][t] - mean;
+            sq += d * d;
+          }
+        sq += __shfl_xor(sq, 16);
+        sq += __shfl_xor(sq, 32);
+        const float rstd = rsqrtf(sq * (1.f / kK) + 1e-5f);
+        f16x8_t xb[4];
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+          for (int t = 0; t < 8; ++t) xb[ks][t] = f2h((xv[ks][t] - mean) * rstd);
+#pragma unroll
+        for (int nt = 0; nt < 8; ++nt) {
+          f32x4_t d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int ks = 0; ks < 4; ++ks) {
+            const f16x8_t wf = *reinterpret_cast<const f16x8_t*>(swq + (16 * nt + l16) * kPitch + 32 * ks + 8 * g);
+            d = mfma16x16x32(wf, xb[ks], d);
+          }
+          const float4 b = *reinterpret_cast<const float4*>(S.bq + 32 * g + 4 * nt);
+          qh[2 * nt] = pack_f16x2(d[0] + b.x, d[1] + b.y);
+          qh[2 * nt + 1] = pack_f16x2(d[2] + b.z, d[3] + b.w);
+        }
+      }
+      // ---- typed attention of head ag over row ar's entries
+      uint32_t qa[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) qa[i] = uint32_t(from_lane(src_m, int32_t(qh[i])));
+      float acc[32];
+#pragma unroll
+      for (int i = 0; i < 32; ++i) acc[i] = 0.f;
       float m = -INFINITY, l = 0.f;
-      float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-      for (int64_t base = st[j]; base < en[j]; base += kGroup) {
-        const int cnt = int(en[j] - base < kGroup ? en[j] - base : kGroup);
-        int64_t ri = rs[j], ci = rc[j];  // (a negative 32-bit value stays invalid)
-        if (base != st[j]) {  // entries past the first 16 (long rows only)
-          ri = -1;
-          ci = -1;
-          if (base + gl < en[j]) {
-            ri = a.src[base + gl];
-            ci = a.cls[base + gl];
+      // Rows are fetched by the lanes whose entry exists only (a short row's
+      // lanes sit out the longer rows' batches without costing the address
+      // unit anything); a lane that sits out keeps the last finite values it
+      // held and weighs them by p = 0.
+      uint4 kr[kB][4], vr[kB][4], cr[kB][4];
+      float bs[kB];
+#pragma unroll
+      for (int u = 0; u < kB; ++u) {
+        bs[u] = 0.f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) kr[u][w] = vr[u][w] = cr[u][w] = make_uint4(0u, 0u, 0u, 0u);
+      }
+      for (int j = 0; j < maxc; j += kB) {
+        bool ok[kB];
+#pragma unroll
+        for (int u = 0; u < kB; ++u) {
+          const bool in = j + u < acnt;
+          ok[u] = in && es[u] >= 0 && es[u] < S.n_src && ec[u] >= 0 && ec[u] < S.n_classes;
+          if (in && !ok[u]) raise_flag(a.flag, MANTIS_FLAG_INDEX);
+          if (ok[u]) {
+            const uint32_t sr = uint32_t(es[u]), cc = uint32_t(ec[u]);
+            load_head(S.k + (sr * uint32_t(S.ldk) + uint32_t(8 * ag)), kr[u]);
+            load_head(S.v + (sr * uint32_t(S.ldv) + uint32_t(8 * ag)), vr[u]);
+            if constexpr (kVcls) load_head(S.vcls + (cc * uint32_t(kK) + uint32_t(8 * ag)), cr[u]);
+            bs[u] = S.bias[uint32_t(ag) * uint32_t(S.n_classes) + cc];
           }
         }
-        // three entries in flight: what fits the 128-VGPR budget of 4
-        // wavefronts per SIMD next to the prefetched indices
-        attend_chunk<kVcls, 3>(qc, cnt, ri, ci, a.k, a.v, a.ldk, a.ldv, a.bias, a.n_classes, a.vcls, a.n_src,
-                            a.scale, gl, a.flag, m, l, acc);
+        if (j + kB < maxc) fetch(j + kB);  // the next batch's entries, under this batch's rows
+        float sc[kB];
+        float m_new = m;
+#pragma unroll
+        for (int u = 0; u < kB; ++u) {
+          sc[u] = ok[u] ? fmaf(dot32(qa, kr[u]), a.scale, bs[u]) : -INFINITY;
+          m_new = fmaxf(m_new, sc[u]);
+        }
+        const bool any = m_new != -INFINITY;
+        const float alpha = any ? __expf(m - m_new) : 1.f;
+        l *= alpha;
+        float pr[kB];
+#pragma unroll
+        for (int u = 0; u < kB; ++u) {
+          pr[u] = any ? __expf(sc[u] - m_new) : 0.f;
+          l += pr[u];
+        }
+#pragma unroll
+        for (int i = 0; i < 32; ++i) acc[i] *= alpha;
+#pragma unroll
+        for (int u = 0; u < kB; ++u) {
+          axpy32(acc, pr[u], vr[u]);
+          if constexpr (kVcls) axpy32(acc, pr[u], cr[u]);
+        }
+        m = any ? m_new : m;
       }
-      const float inv = l > 0.f ? 1.f / l : 1.f;
-      uint4 w;
-      w.x = pack_f16x2(acc[0] * inv, acc[1] * inv);
-      w.y = pack_f16x2(acc[2] * inv, acc[3] * inv);
-      w.z = pack_f16x2(acc[4] * inv, acc[5] * inv);
-      w.w = pack_f16x2(acc[6] * inv, acc[7] * inv);
-      *reinterpret_cast<uint4*>(buf + lr * kPitch + gl * 8) = w;
-    }
-    wave_lds_fence();
-    // ---- 3. output projection + residual (MFMA layout)
-    {
-      const int64_t row = r0 + l16;
-      const bool live = row < a.n_rows;
-      f16x8_t ab[4];
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
-        ab[ks] = *reinterpret_cast<const f16x8_t*>(buf + l16 * kPitch + 32 * ks + 8 * g);
-#pragma unroll
-      for (int nt = 0; nt < 8; ++nt) {
-        f32x4_t d = {0.f, 0.f, 0.f, 0.f};
+      // ---- output projection + residual, into the x registers
+      {
+        const float inv = l > 0.f ? 1.f / l : 1.f;
+        f16x8_t ab[4];
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-          const f16x8_t wf = *reinterpret_cast<const f16x8_t*>(swo + (16 * nt + l16) * kPitch + 32 * ks + 8 * g);
-          d = mfma16x16x32(wf, ab[ks], d);
+          // packed on the attention lane, read back by the lane of the MFMA layout
+          uint4 w;
+          w.x = uint32_t(from_lane(src_a, int32_t(pack_f16x2(acc[8 * ks] * inv, acc[8 * ks + 1] * inv))));
+          w.y = uint32_t(from_lane(src_a, int32_t(pack_f16x2(acc[8 * ks + 2] * inv, acc[8 * ks + 3] * inv))));
+          w.z = uint32_t(from_lane(src_a, int32_t(pack_f16x2(acc[8 * ks + 4] * inv, acc[8 * ks + 5] * inv))));
+          w.w = uint32_t(from_lane(src_a, int32_t(pack_f16x2(acc[8 * ks + 6] * inv, acc[8 * ks + 7] * inv))));
+          ab[ks] = __builtin_bit_cast(f16x8_t, w);
         }
-        if (live) {
-          const int f = 16 * nt + 4 * g;
-          const float4 b = *reinterpret_cast<const float4*>(a.bo + f);
-          float4* xp = reinterpret_cast<float4*>(a.x + row * a.ldx + f);
-          float4 r = *xp;
-          r.x += d[0] + b.x;
-          r.y += d[1] + b.y;
-          r.z += d[2] + b.z;
-          r.w += d[3] + b.w;
-          *xp = r;
+#pragma unroll
+        for (int nt = 0; nt < 8; ++nt) {
+          f32x4_t d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int ks = 0; ks < 4; ++ks) {
+            // K position 8 g' + t of chunk ks is feature 32 g' + 8 ks + t
+            const f16x8_t wf = *reinterpret_cast<const f16x8_t*>(swo + (16 * nt + l16) * kPitch + 32 * g + 8 * ks);
+            d = mfma16x16x32(wf, ab[ks], d);
+          }
+          const float4 b = *reinterpret_cast<const float4*>(S.bo + 32 * (nt >> 1) + 8 * g + 4 * (nt & 1));
+          float* xr = xv[nt >> 1] + 4 * (nt & 1);
+          xr[0] += d[0] + b.x;
+          xr[1] += d[1] + b.y;
+          xr[2] += d[2] + b.z;
+          xr[3] += d[3] + b.w;
         }
       }
     }
-    wave_lds_fence();  // the tile buffer is rewritten by the next tile's q
+    if (live) {
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) store8(a.x + row * a.ldx + 32 * ks + 8 * g, xv[ks]);
+    }
   }
+}
+
+template <int kStages, bool kVcls>
+int32_t launch(const SubArgs& a, void* stream) {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                              hipSuccess || cus <= 0)
+    cus = 256;
+  // one persistent workgroup per CU, a multiple of the XCD count
+  const int64_t tiles = (a.n_rows + 15) / 16;
+  int64_t grid = ((int64_t(cus) + kXcds - 1) / kXcds) * kXcds;
+  const int64_t need = ((tiles + kWaves - 1) / kWaves + kXcds - 1) / kXcds * kXcds;
+  if (need < grid) grid = need;
+  attn_substage_kernel<kStages, kVcls><<<dim3(unsigned(grid)), dim3(kThreads), 0, as_stream(stream)>>>(a);
+  return launched();
+}
+
+bool stage_ok(const mantis_substage& d) {
+  if (!d.wq || !d.bq || !d.k || !d.v || !d.bias || !d.seg_ptr || !d.wo || !d.bo || d.n_src < 0 ||
+      d.n_classes <= 0 || d.ldk < kK || d.ldv < kK || d.ldk % 8 || d.ldv % 8)
+    return false;
+  if (d.n_entries < 0 || (d.n_entries > 0 && (!d.src || !d.cls || d.n_src <= 0))) return false;
+  if (!aligned16(d.wq) || !aligned16(d.bq) || !aligned16(d.k) || !aligned16(d.v) || !aligned16(d.wo) ||
+      !aligned16(d.bo) || (d.vcls && !aligned16(d.vcls)))
+    return false;
+  // gathered rows use 32-bit element offsets, counts fit int32
+  auto fits32 = [](int64_t rows, int64_t ld) { return rows <= 0 || (rows - 1) * ld + kK <= 4294967295LL; };
+  return d.n_entries <= 2147483647LL && d.n_classes <= 2147483647LL && d.n_src <= 2147483647LL &&
+         fits32(d.n_src, d.ldk) && fits32(d.n_src, d.ldv) && fits32(d.n_classes, kK) &&
+         4 * d.n_classes <= 4294967295LL;
+}
+
+Stage to_stage(const mantis_substage& d) {
+  return Stage{static_cast<const _Float16*>(d.wq), d.bq, static_cast<const _Float16*>(d.k),
+               static_cast<const _Float16*>(d.v), d.ldk, d.ldv, d.n_src, d.bias, d.n_classes,
+               static_cast<const _Float16*>(d.vcls), d.seg_ptr, d.src, d.cls, d.n_entries,
+               static_cast<const _Float16*>(d.wo), d.bo};
 }
 
 }  // namespace
@@ -247,41 +392,33 @@ __global__ void __launch_bounds__(kThreads) attn_substage_kernel(SubArgs a) {
 
 using namespace mantis;
 
+extern "C" int32_t mantis_attention_substages(float* x, int64_t ldx, int64_t n_rows, const mantis_substage* stages,
+                                              int32_t n_stages, int32_t* err_flag, void* stream) {
+  if (n_rows < 0 || !stages || n_stages < 1 || n_stages > 2) return MANTIS_E_ARG;
+  if (n_rows == 0) return MANTIS_OK;
+  for (int s = 0; s < n_stages; ++s)
+    if (!stage_ok(stages[s])) return MANTIS_E_ARG;
+  // both stages of a pass carry class values, or neither does
+  if (n_stages == 2 && (stages[0].vcls == nullptr) != (stages[1].vcls == nullptr)) return MANTIS_E_ARG;
+  if (!x || ldx < kK || ldx % 4 || !aligned16(x)) return MANTIS_E_ARG;
+  SubArgs a{};
+  a.x = x;
+  a.ldx = ldx;
+  a.n_rows = n_rows;
+  for (int s = 0; s < n_stages; ++s) a.st[s] = to_stage(stages[s]);
+  a.scale = 0.17677669529663687f;  // 1/sqrt(32)
+  a.flag = err_flag;
+  const bool vc = stages[0].vcls != nullptr;
+  if (n_stages == 2) return vc ? launch<2, true>(a, stream) : launch<2, false>(a, stream);
+  return vc ? launch<1, true>(a, stream) : launch<1, false>(a, stream);
+}
+
 extern "C" int32_t mantis_attention_substage(float* x, int64_t ldx, int64_t n_rows, const void* wq, const float* bq,
                                              const void* k, const void* v, int64_t ldk, int64_t ldv, int64_t n_src,
                                              const float* bias, int64_t n_classes, const void* vcls,
                                              const int64_t* seg_ptr, const int64_t* src, const int64_t* cls,
                                              int64_t n_entries, const void* wo, const float* bo,
                                              int32_t* err_flag, void* stream) {
-  if (n_rows == 0) return MANTIS_OK;
-  if (!x || !wq || !bq || !k || !v || !bias || !seg_ptr || !wo || !bo || n_rows < 0 || n_src < 0 ||
-      n_classes <= 0 || ldx < kK || ldx % 4 || ldk < kK || ldv < kK || ldk % 8 || ldv % 8)
-    return MANTIS_E_ARG;
-  if (n_entries < 0 || (n_entries > 0 && (!src || !cls || n_src <= 0))) return MANTIS_E_ARG;
-  if (!aligned16(x) || !aligned16(wq) || !aligned16(bq) || !aligned16(k) || !aligned16(v) || !aligned16(wo) ||
-      !aligned16(bo) || (vcls && !aligned16(vcls)))
-    return MANTIS_E_ARG;
-  // gathered rows use 32-bit element offsets
-  auto fits32 = [](int64_t rows, int64_t ld) { return rows <= 0 || (rows - 1) * ld + kK <= 4294967295LL; };
-  if (n_entries > 2147483647LL || n_classes > 2147483647LL || n_src > 2147483647LL || !fits32(n_src, ldk) || !fits32(n_src, ldv) || !fits32(n_classes, kK) ||
-      4 * n_classes > 4294967295LL)
-    return MANTIS_E_ARG;
-  SubArgs a{x, ldx, n_rows, static_cast<const _Float16*>(wq), bq, static_cast<const _Float16*>(k),
-            static_cast<const _Float16*>(v), ldk, ldv, n_src, bias, n_classes, static_cast<const _Float16*>(vcls),
-            seg_ptr, src, cls, n_entries, static_cast<const _Float16*>(wo), bo, 0.17677669529663687f, err_flag};
-  int dev = 0, cus = 0;
-  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
-                                              hipSuccess || cus <= 0)
-    cus = 256;
-  // one persistent workgroup per CU, a multiple of the XCD count
-  const int64_t tiles = (n_rows + 15) / 16;
-  int64_t grid = ((int64_t(cus) + kXcds - 1) / kXcds) * kXcds;
-  const int64_t need = ((tiles + kWaves - 1) / kWaves + kXcds - 1) / kXcds * kXcds;
-  if (need < grid) grid = need;
-  hipStream_t s = as_stream(stream);
-  if (vcls)
-    attn_substage_kernel<true><<<dim3(unsigned(grid)), dim3(kThreads), 0, s>>>(a);
-  else
-    attn_substage_kernel<false><<<dim3(unsigned(grid)), dim3(kThreads), 0, s>>>(a);
-  return launched();
+  const mantis_substage d{wq, bq, k, v, ldk, ldv, n_src, bias, n_classes, vcls, seg_ptr, src, cls, n_entries, wo, bo};
+  return mantis_attention_substages(x, ldx, n_rows, &d, 1, err_flag, stream);
 }

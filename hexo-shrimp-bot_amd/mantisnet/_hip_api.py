@@ -9,6 +9,19 @@ i64 = ctypes.c_int64
 i32 = ctypes.c_int32
 f32p = ctypes.POINTER(ctypes.c_float)
 
+
+
+class MantisSubstage(ctypes.Structure):
+    """`mantis_substage` of include/mantis_hip.h: one stage of
+    mantis_attention_substages (device pointers, sizes)."""
+
+    _fields_ = [
+        ("wq", vp), ("bq", vp), ("k", vp), ("v", vp), ("ldk", i64), ("ldv", i64), ("n_src", i64),
+        ("bias", vp), ("n_classes", i64), ("vcls", vp), ("seg_ptr", vp), ("src", vp), ("cls", vp),
+        ("n_entries", i64), ("wo", vp), ("bo", vp),
+    ]
+
+
 SIGNATURES = {
     "mantis_hip_version": ([], i32),
     "mantis_runs_to_ptr": ([vp, i64, i64, vp, vp, vp], i32),
@@ -18,6 +31,7 @@ SIGNATURES = {
         i32),
     "mantis_attention_substage": (
         [vp, i64, i64, vp, vp, vp, vp, i64, i64, i64, vp, i64, vp, vp, vp, vp, i64, vp, vp, vp, vp], i32),
+    "mantis_attention_substages": ([vp, i64, i64, vp, i32, vp, vp], i32),
     "mantis_cell_heads": (
         [vp, i32, i32, i64, i64, vp, vp, vp, vp, vp, vp, i64, vp, i64, vp, vp, vp, i64, vp, i64, vp, vp, vp, vp, vp,
          i64, vp, vp, vp], i32),

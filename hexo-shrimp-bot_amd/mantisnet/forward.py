@@ -110,6 +110,13 @@ def _fold(P, ln: str | None, lins: list[str]):
     return torch.cat(ws).to(HALF).contiguous(), torch.cat(bs).float().contiguous()
 
 
+def _interleaved(pair):
+    """(W, b) of a k|v projection with its output rows head-interleaved."""
+    w, b = pair
+    idx = torch.cat([ops.HEAD_INTERLEAVE, 128 + ops.HEAD_INTERLEAVE]).to(w.device)
+    return w.index_select(0, idx).contiguous(), b.index_select(0, idx).contiguous()
+
+
 def _prepare(model, P) -> dict[str, Tensor]:
     cfg = model.cfg
     t: dict[str, Tensor] = {}
@@ -126,17 +133,19 @@ def _prepare(model, P) -> dict[str, Tensor]:
         put(pb + "mlp_w3", _fold(P, None, [pb + "mlp_w.out"]))
         # window class term composed with lin_b: counts @ e_ws @ lin_b^T, per pattern
         t[pb + "ws_tab"] = (counts @ (P[pb + "e_ws.weight"] @ P[pb + "mlp_w.lin_b.weight"].t())).contiguous()
+        # the sub-stages read k/v and class-value rows head-interleaved: the
+        # k/v projections emit that layout (output rows permuted)
         put(pb + "cr_q", _fold(P, pb + "ln_cr_c", [pb + "cr_wq"]))
-        put(pb + "cr_kv", _fold(P, pb + "ln_cr_w", [pb + "cr_wk", pb + "cr_wv"]))
+        put(pb + "cr_kv", _interleaved(_fold(P, pb + "ln_cr_w", [pb + "cr_wk", pb + "cr_wv"])))
         put(pb + "cr_o", _fold(P, None, [pb + "cr_wo"]))
         # class-value rows gathered once per edge: fp16 halves their bytes
-        t[pb + "cr_vcls"] = P[pb + "cr_vclass.weight"].to(HALF).contiguous()
+        t[pb + "cr_vcls"] = ops.interleave_heads(P[pb + "cr_vclass.weight"]).to(HALF).contiguous()
         put(pb + "rad_q", _fold(P, pb + "ln_radius_c", [pb + "radius_wq"]))
-        put(pb + "rad_kv", _fold(P, pb + "ln_radius_s", [pb + "radius_wk", pb + "radius_wv"]))
+        put(pb + "rad_kv", _interleaved(_fold(P, pb + "ln_radius_s", [pb + "radius_wk", pb + "radius_wv"])))
         put(pb + "rad_o", _fold(P, None, [pb + "radius_wo"]))
-        t[pb + "rad_vcls"] = P[pb + "radius_vclass.weight"].to(HALF).contiguous()
+        t[pb + "rad_vcls"] = ops.interleave_heads(P[pb + "radius_vclass.weight"]).to(HALF).contiguous()
         put(pb + "wr_q", _fold(P, pb + "ln_wr_w", [pb + "wr_wq"]))
-        put(pb + "wr_kv", _fold(P, pb + "ln_wr_c", [pb + "wr_wk", pb + "wr_wv"]))
+        put(pb + "wr_kv", _interleaved(_fold(P, pb + "ln_wr_c", [pb + "wr_wk", pb + "wr_wv"])))
         put(pb + "wr_o", _fold(P, None, [pb + "wr_wo"]))
         put(pb + "v", _fold(P, pb + "ln_sw_w", [pb + "v"]))
         put(pb + "mlp_s1", _fold(P, pb + "ln_sw_s", [pb + "mlp_s.lin_a"]))
@@ -342,22 +351,25 @@ def _resid(W, key, x, out, **kw):
     return FL(x, W[key + ".w"], W[key + ".b"], out=out, residual=True, **kw)
 
 
-def _substage(W, P, pb, key, x, kv, bias, vcls, ptr, src, cls):
-    """x += o-projection of the typed attention of LN(x)'s queries, fused."""
-    return ops.attention_substage(x, W[pb + key + "_q.w"], W[pb + key + "_q.b"], kv, P[pb + bias], vcls, ptr, src,
-                                  cls, W[pb + key + "_o.w"], W[pb + key + "_o.b"])
+def _substage(W, P, pb, key, kv, bias, vcls, ptr, src, cls) -> ops.SubStage:
+    """x += o-projection of the typed attention of LN(x)'s queries."""
+    return ops.SubStage(W[pb + key + "_q.w"], W[pb + key + "_q.b"], kv, P[pb + bias], vcls, ptr, src, cls,
+                        W[pb + key + "_o.w"], W[pb + key + "_o.b"])
 
 
 def _cell_stage(W, P, pb, plan: Plan, s, w, c):
-    # cells <- windows (decoder classes, class values), cells <- stones (radius
-    # classes, class values), windows <- cells (decoder classes): each one
-    # fused LN -> q -> attention -> o -> residual launch over the query rows
-    _substage(W, P, pb, "cr", c, _proj(W, pb + "cr_kv", w), "cr_bias", W[pb + "cr_vcls"], plan.cell_ptr,
-              plan.edge_window, plan.edge_class)
-    _substage(W, P, pb, "rad", c, _proj(W, pb + "rad_kv", s), "radius_bias", W[pb + "rad_vcls"], plan.radius_ptr,
-              plan.radius_src, plan.radius_class)
-    _substage(W, P, pb, "wr", w, _proj(W, pb + "wr_kv", c), "wr_bias", None, plan.win_ptr, plan.edge_wcell,
-              plan.edge_wclass)
+    # cells <- windows (decoder classes, class values) then cells <- stones
+    # (radius classes, class values): one fused pass over the cell rows, the
+    # rows staying on chip between the two sub-stages; then windows <- cells
+    # (decoder classes). Each sub-stage is LN -> q -> attention -> o -> residual.
+    cr = _substage(W, P, pb, "cr", _proj(W, pb + "cr_kv", w), "cr_bias", W[pb + "cr_vcls"], plan.cell_ptr,
+                   plan.edge_window, plan.edge_class)
+    rad = _substage(W, P, pb, "rad", _proj(W, pb + "rad_kv", s), "radius_bias", W[pb + "rad_vcls"],
+                    plan.radius_ptr, plan.radius_src, plan.radius_class)
+    ops.attention_substages(c, [cr, rad])
+    wr = _substage(W, P, pb, "wr", _proj(W, pb + "wr_kv", c), "wr_bias", None, plan.win_ptr, plan.edge_wcell,
+                   plan.edge_wclass)
+    ops.attention_substages(w, [wr])
 
 
 def _latent_cycle(W, P, pb, plan: Plan, w, g2):

@@ -11,11 +11,12 @@ is no CPU or PyTorch fallback: a CPU tensor is refused.
 from __future__ import annotations
 
 import ctypes
+from typing import NamedTuple
 
 import torch
 from torch import Tensor
 
-from . import _native
+from . import _hip_api, _native
 
 F32, BF16, F16 = 0, 1, 2
 _FLAG_NAMES = {1: "an index was out of range", 2: "a CSR/run view was not ascending"}
@@ -293,53 +294,114 @@ def cell_attention(q: Tensor, k: Tensor, v: Tensor, bias: Tensor, vcls: Tensor |
     return (out, m, l) if stats else out
 
 
-def attention_substage(x: Tensor, wq: Tensor, bq: Tensor, kv: Tensor, bias: Tensor, vcls: Tensor | None,
-                       seg_ptr: Tensor, src: Tensor, cls: Tensor, wo: Tensor, bo: Tensor) -> Tensor:
-    """In place on the fp32 residual rows x (n, 128):
-    x += fp16(attend(fp16(LN(x) wq^T + bq))) wo^T + bo, the attention typed
-    by (bias, vcls) over the CSR entries (seg_ptr, src, cls) with k/v the two
-    halves of the fp16 (n_src, 256) rows kv.  One launch."""
-    dev = _on_gpu(x, wq, bq, kv, bias, vcls, seg_ptr, src, cls, wo, bo)
-    n = x.shape[0]
-    if x.ndim != 2 or x.shape[1] != 128 or x.dtype != torch.float32 or x.stride(1) != 1:
-        raise ValueError("x must be fp32 (n, 128) rows")
-    for t, name in ((wq, "wq"), (wo, "wo")):
+def _head_interleave_index() -> Tensor:
+    i = torch.arange(128)
+    w, g, t = i // 32, (i // 8) % 4, i % 8
+    return 32 * g + 8 * w + t
+
+
+# column j of a head-interleaved 128-wide row holds natural column
+# HEAD_INTERLEAVE[j]: element 32 w + 8 g + t is dim 8 w + t of head g (an
+# involution: applying it twice restores the natural order)
+HEAD_INTERLEAVE = _head_interleave_index()
+
+
+def interleave_heads(t: Tensor) -> Tensor:
+    """Head-interleave the 128-wide column groups of t's last dimension (a
+    multiple of 128): the k/v/class-value row layout of the sub-stages."""
+    if t.shape[-1] % 128:
+        raise ValueError("the last dimension must be a multiple of 128")
+    idx = torch.cat([HEAD_INTERLEAVE + 128 * j for j in range(t.shape[-1] // 128)]).to(t.device)
+    return t.index_select(-1, idx)
+
+
+class SubStage(NamedTuple):
+    """One typed-attention sub-stage over residual rows: weights (wq, bq, wo,
+    bo), the fp16 (n_src, 256) k|v rows, the class bias (4, classes) and
+    optional class values (classes, 128), and the CSR entries (seg_ptr, src,
+    cls) of every residual row.  kv and vcls rows are head-interleaved
+    (interleave_heads)."""
+
+    wq: Tensor
+    bq: Tensor
+    kv: Tensor
+    bias: Tensor
+    vcls: Tensor | None
+    seg_ptr: Tensor
+    src: Tensor
+    cls: Tensor
+    wo: Tensor
+    bo: Tensor
+
+
+def _substage_struct(st: SubStage, n: int):
+    """Validate one stage against n residual rows; (ctypes struct, the
+    tensors it points into, entry count)."""
+    for t, name in ((st.wq, "wq"), (st.wo, "wo")):
         if t.shape != (128, 128) or t.dtype != torch.float16 or not t.is_contiguous():
             raise ValueError(f"{name} must be a contiguous fp16 (128, 128) matrix")
-    for t, name in ((bq, "bq"), (bo, "bo")):
+    for t, name in ((st.bq, "bq"), (st.bo, "bo")):
         if t.shape != (128,) or t.dtype != torch.float32 or not t.is_contiguous():
             raise ValueError(f"{name} must be a contiguous fp32 vector of 128")
+    kv = st.kv
     if kv.ndim != 2 or kv.shape[1] != 256 or kv.dtype != torch.float16 or kv.stride(1) != 1:
         raise ValueError("kv must be fp16 (n_src, 256) rows")
-    if bias.ndim != 2 or bias.shape[0] != 4:
+    if st.bias.ndim != 2 or st.bias.shape[0] != 4:
         raise ValueError("bias must have shape (4, classes)")
-    bias = bias.float().contiguous()
+    bias = st.bias.float().contiguous()
+    vcls = st.vcls
     if vcls is not None:
         if vcls.shape != (bias.shape[1], 128):
             raise ValueError("vcls must have shape (classes, 128)")
         vcls = vcls.to(torch.float16).contiguous()
-    if seg_ptr.numel() != n + 1:
+    if st.seg_ptr.numel() != n + 1:
         raise ValueError("seg_ptr must have one entry per row plus one")
-    if src.shape != cls.shape or src.ndim != 1:
+    if st.src.shape != st.cls.shape or st.src.ndim != 1:
         raise ValueError("the entry views must have one length")
-    seg_ptr, src, cls = _i64(seg_ptr, "seg_ptr"), _i64(src, "src"), _i64(cls, "cls")
+    seg_ptr, src, cls = _i64(st.seg_ptr, "seg_ptr"), _i64(st.src, "src"), _i64(st.cls, "cls")
+    e = src.numel()
+    d = _hip_api.MantisSubstage(
+        _ptr(st.wq), _ptr(st.bq), kv.data_ptr(), kv[:, 128:].data_ptr(), kv.stride(0), kv.stride(0), kv.shape[0],
+        _ptr(bias), bias.shape[1], _ptr(vcls), _ptr(seg_ptr), _ptr(src), _ptr(cls), e, _ptr(st.wo), _ptr(st.bo))
+    return d, (bias, vcls, seg_ptr, src, cls), e
+
+
+def attention_substages(x: Tensor, stages: list[SubStage]) -> Tensor:
+    """In place on the fp32 residual rows x (n, 128), for each stage in order:
+    x += fp16(attend(fp16(LN(x) wq^T + bq))) wo^T + bo, the attention typed
+    by (bias, vcls) over the stage's CSR entries with k/v the two halves of
+    its kv rows.  One launch for one or two stages (x stays on chip between
+    them); both stages carry class values or neither does."""
+    if not 1 <= len(stages) <= 2:
+        raise ValueError("one or two stages per launch")
+    dev = _on_gpu(x, *[t for st in stages for t in st])
+    n = x.shape[0]
+    if x.ndim != 2 or x.shape[1] != 128 or x.dtype != torch.float32 or x.stride(1) != 1:
+        raise ValueError("x must be fp32 (n, 128) rows")
+    if len({st.vcls is None for st in stages}) != 1:
+        raise ValueError("the stages of one launch all carry class values or none does")
+    built = [_substage_struct(st, n) for st in stages]
     if n:
-        e = src.numel()
-        # x read and written once, the CSR pointers and entry indices once,
-        # each source's k and v rows once
-        nbytes = n * (128 * 4 * 2 + 8) + e * 16 + kv.shape[0] * 256 * 2
-        flops = 2 * n * 128 * 128 * 2 + e * 4 * 128 * 2
-        _launch("attention_substage_vcls" if vcls is not None else "attention_substage_plain", nbytes, flops,
-                lambda: _check(
-                    _lib().mantis_attention_substage(
-                        _ptr(x), x.stride(0), n, _ptr(wq), _ptr(bq), kv.data_ptr(), kv[:, 128:].data_ptr(),
-                        kv.stride(0), kv.stride(0), kv.shape[0], _ptr(bias), bias.shape[1], _ptr(vcls),
-                        _ptr(seg_ptr), _ptr(src), _ptr(cls), e, _ptr(wo), _ptr(bo), _ptr(error_flag(dev)),
-                        _stream(),
-                    ),
-                    "attention_substage",
-                ))
+        arr = (_hip_api.MantisSubstage * len(built))(*[d for d, _, _ in built])
+        # x read and written once; per stage the CSR pointers and entry
+        # indices once and each source's k and v rows once
+        nbytes = n * 128 * 4 * 2 + sum(n * 8 + e * 16 + st.kv.shape[0] * 256 * 2 for st, (_, _, e) in
+                                       zip(stages, built))
+        flops = sum(2 * n * 128 * 128 * 2 + e * 4 * 128 * 2 for _, _, e in built)
+        kind = "vcls" if stages[0].vcls is not None else "plain"
+        name = f"attention_substage_{kind}" if len(stages) == 1 else f"attention_substages{len(stages)}_{kind}"
+        _launch(name, nbytes, flops, lambda: _check(
+            _lib().mantis_attention_substages(_ptr(x), x.stride(0), n, ctypes.cast(arr, ctypes.c_void_p), len(built),
+                                              _ptr(error_flag(dev)), _stream()),
+            "attention_substages",
+        ))
     return x
+
+
+def attention_substage(x: Tensor, wq: Tensor, bq: Tensor, kv: Tensor, bias: Tensor, vcls: Tensor | None,
+                       seg_ptr: Tensor, src: Tensor, cls: Tensor, wo: Tensor, bo: Tensor) -> Tensor:
+    """One sub-stage (see attention_substages), in place on x."""
+    return attention_substages(x, [SubStage(wq, bq, kv, bias, vcls, seg_ptr, src, cls, wo, bo)])
 
 
 def cell_heads(c: Tensor, w1: Tensor, b1: Tensor, w2: Tensor, w3: Tensor, b3: Tensor, pre: Tensor,

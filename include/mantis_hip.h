@@ -85,7 +85,10 @@ int32_t mantis_cell_attention(const void* q, const void* k, const void* v, int32
 
 /*
  * Fused typed-attention sub-stage over the rows of an fp32 residual stream
- * x (n_rows, 128) with row stride ldx, in place:
+ * x (n_rows, 128) with row stride ldx, in place (k, v and vcls rows are
+ * head-interleaved: element 32*w + 8*g + t of a row holds dim 8*w + t of
+ * head g, w, g in 0..3, t in 0..7; mantisnet.ops.interleave_heads makes
+ * that layout, and projecting with row-permuted weights produces it):
  *   q  = fp16(LN(x) Wq^T + bq)       (LayerNorm without affine: fold it into Wq/bq)
  *   a  = fp16(typed segment attention of q, as mantis_cell_attention, 4 heads x 32)
  *   x += a Wo^T + bo
@@ -105,6 +108,39 @@ int32_t mantis_attention_substage(float* x, int64_t ldx, int64_t n_rows, const v
                                   const int64_t* seg_ptr, const int64_t* src, const int64_t* cls,
                                   int64_t n_entries, const void* wo, const float* bo, int32_t* err_flag,
                                   void* stream);
+
+/*
+ * One to two fused sub-stages (as mantis_attention_substage) applied in order
+ * to the same rows of x in one pass: x stays on chip between the stages, so
+ * x crosses HBM once (read and written) for all of them.  Each stage reads
+ * its own weights, k/v rows, class tables and CSR entries; the stages of one
+ * call either all carry class values (vcls) or none does.  The fields of
+ * mantis_substage are the per-stage arguments of mantis_attention_substage.
+ * Replaces the two cell sub-stages of the reference's _cell_stage (cells <-
+ * windows, then cells <- stones; model.py:397-490, kernels
+ * cell_latents.py:213-285, 834-1001).
+ */
+typedef struct mantis_substage {
+  const void* wq;
+  const float* bq;
+  const void* k;
+  const void* v;
+  int64_t ldk;
+  int64_t ldv;
+  int64_t n_src;
+  const float* bias;
+  int64_t n_classes;
+  const void* vcls;
+  const int64_t* seg_ptr;
+  const int64_t* src;
+  const int64_t* cls;
+  int64_t n_entries;
+  const void* wo;
+  const float* bo;
+} mantis_substage;
+
+int32_t mantis_attention_substages(float* x, int64_t ldx, int64_t n_rows, const mantis_substage* stages,
+                                   int32_t n_stages, int32_t* err_flag, void* stream);
 
 /*
  * Fused cell heads: for every legal cell r (position cell_pos[r]) with

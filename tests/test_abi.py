@@ -43,6 +43,15 @@ def test_ctypes_signatures_match_header():
         assert len(args) == decls[name], name
 
 
+def test_substage_struct_matches_header():
+    text = (INCLUDE / "mantis_hip.h").read_text()
+    body = re.search(r"typedef struct mantis_substage \{(.*?)\} mantis_substage;", text, flags=re.S).group(1)
+    fields = re.findall(r"(\w+);", body)
+    assert fields == [name for name, _ in _hip_api.MantisSubstage._fields_]
+    # every field is a pointer or an int64: 8 bytes each, no padding
+    assert ctypes.sizeof(_hip_api.MantisSubstage) == 8 * len(fields)
+
+
 def test_versions_answer_without_a_gpu():
     assert _native.encoder().hexo_repr_version() == 9
     assert _native.hip().mantis_hip_version() > 0

@@ -3,6 +3,7 @@ is plain tensor arithmetic) and only then skips its stable sorts."""
 
 from __future__ import annotations
 
+import pytest
 import torch
 
 from mantisnet import collate_positions, synthetic
@@ -41,3 +42,19 @@ def test_any_deviation_is_detected():
     b.act_rev = b.act_rev.clone()
     b.act_rev[0] = b.act_rev.numel()  # out of range
     assert not _canonical_orders(b, _window_pos(b))
+
+
+def test_head_interleave_layout():
+    # element 32 w + 8 g + t of an interleaved row is dim 8 w + t of head g
+    # (heads are the 32-wide column groups of the natural row)
+    from mantisnet import ops
+    row = torch.arange(256).float()[None]
+    inter = ops.interleave_heads(row)[0]
+    for half in (0, 128):
+        for w in range(4):
+            for g in range(4):
+                for t in range(8):
+                    assert inter[half + 32 * w + 8 * g + t] == half + 32 * g + 8 * w + t
+    assert torch.equal(ops.interleave_heads(ops.interleave_heads(row)), row)
+    with pytest.raises(ValueError):
+        ops.interleave_heads(torch.zeros(3, 100))
