@@ -95,8 +95,8 @@ class Prepared:
         return self.t[k]
 
 
-def _fold(P, ln: str | None, lins: list[str]):
-    """(W' fp16, b' fp32) for LN -> concat(lins); ln None = no LayerNorm."""
+def _fold32(P, ln: str | None, lins: list[str]):
+    """(W', b') in fp32 for LN -> concat(lins); ln None = no LayerNorm."""
     ws, bs = [], []
     for name in lins:
         w = P[name + ".weight"]
@@ -107,7 +107,13 @@ def _fold(P, ln: str | None, lins: list[str]):
             w = w * g[None, :]
         ws.append(w)
         bs.append(b)
-    return torch.cat(ws).to(HALF).contiguous(), torch.cat(bs).float().contiguous()
+    return torch.cat(ws).float().contiguous(), torch.cat(bs).float().contiguous()
+
+
+def _fold(P, ln: str | None, lins: list[str]):
+    """(W' fp16, b' fp32) for LN -> concat(lins); ln None = no LayerNorm."""
+    w, b = _fold32(P, ln, lins)
+    return w.to(HALF).contiguous(), b
 
 
 def _interleaved(pair):
@@ -160,6 +166,11 @@ def _prepare(model, P) -> dict[str, Tensor]:
         put(pb + "lq_bcast", _fold(P, pb + "latent_ln_bcast_q", [pb + "latent_wq_bcast"]))
         put(pb + "lkv_bcast", _fold(P, pb + "latent_ln_bcast_l", [pb + "latent_wk_bcast", pb + "latent_wv_bcast"]))
         put(pb + "lo_bcast", _fold(P, None, [pb + "latent_wo_bcast"]))
+        # the latent mix runs in fp32: transposed fp32 weights, LN folded in
+        wqkv, bqkv = _fold32(P, pb + "latent_ln_mix", [pb + "latent_wq_mix", pb + "latent_wk_mix", pb + "latent_wv_mix"])
+        t[pb + "mix_qkv.wt"], t[pb + "mix_qkv.b"] = wqkv.t().contiguous(), bqkv
+        t[pb + "mix_o.wt"] = P[pb + "latent_wo_mix.weight"].t().contiguous()
+        t[pb + "mix_o.b"] = P[pb + "latent_wo_mix.bias"].contiguous()
         put(pb + "ffn1", _fold(P, pb + "ln_ffn", [pb + "ffn.0"]))
         put(pb + "ffn2", _fold(P, None, [pb + "ffn.2"]))
     t["sw_all"] = torch.cat([t[f"blocks.{i}.sw_tab"] for i in range(cfg.blocks)], 1).contiguous()
@@ -379,13 +390,7 @@ def _latent_cycle(W, P, pb, plan: Plan, w, g2):
     read = ops.latent_read(q.view(p, 4, 4, 32), kv[:, :128], kv[:, 128:], plan.layout_offsets, plan.layout_order)
     _resid(W, pb + "lo_read", read.view(p * 4, 128), g2)
     # 4 x 4 latent self-mix, fp32 (all four slots live; model.py:516-526)
-    z = F.layer_norm(g2, (128,), P[pb + "latent_ln_mix.weight"], P[pb + "latent_ln_mix.bias"], 1e-5)
-    qm = F.linear(z, P[pb + "latent_wq_mix.weight"], P[pb + "latent_wq_mix.bias"]).view(p, 4, 4, 32).transpose(1, 2)
-    km = F.linear(z, P[pb + "latent_wk_mix.weight"]).view(p, 4, 4, 32).transpose(1, 2)
-    vm = F.linear(z, P[pb + "latent_wv_mix.weight"], P[pb + "latent_wv_mix.bias"]).view(p, 4, 4, 32).transpose(1, 2)
-    att = (torch.matmul(qm, km.transpose(-1, -2)) / math.sqrt(32)).softmax(-1)
-    mixed = torch.matmul(att, vm).transpose(1, 2).reshape(p * 4, 128)
-    g2.add_(F.linear(mixed, P[pb + "latent_wo_mix.weight"], P[pb + "latent_wo_mix.bias"]))
+    ops.latent_mix(g2, W[pb + "mix_qkv.wt"], W[pb + "mix_qkv.b"], W[pb + "mix_o.wt"], W[pb + "mix_o.b"])
     qb = _proj(W, pb + "lq_bcast", w)
     kvb = _proj(W, pb + "lkv_bcast", g2)
     out = ops.latent_broadcast_rows(qb, kvb, plan.window_pos, out_dtype=HALF)
@@ -460,8 +465,10 @@ def _trunk(model, b: Batch, plan: Plan, raw_cells: bool = False):
     sg[:n_s] = P["stone_table.weight"].index_select(0, b.stone_own)
     sg[n_s:] = (P["latent_base"][None] + P["token_moves.weight"].index_select(0, b.moves_idx)[:, None]).reshape(-1, 128)
     w = P["window_table.weight"].index_select(0, b.window_feat)
-    near = P["cell_nearest_table.weight"].index_select(0, b.cell_nearest)
-    c = torch.where(plan.covered_mask[:, None], P["cell_base"][None, :], near).contiguous()
+    # covered cells start from cell_base, the others from their nearest-stone
+    # row: one gather from the table [nearest rows; cell_base]
+    table = torch.cat([P["cell_nearest_table.weight"], P["cell_base"][None, :]])
+    c = table.index_select(0, torch.where(plan.covered_mask, table.shape[0] - 1, b.cell_nearest))
     sw_all = ops.run_reduce(W["sw_all"], plan.run_class, plan.inc_stone_ptr, n_s, F32)
     for i in range(cfg.blocks):
         _block(W, P, i, plan, b, sg, w, c, sw_all, i + 1 < cfg.blocks)

@@ -518,6 +518,30 @@ def latent_broadcast(q: Tensor, k: Tensor, v: Tensor, window_pos: Tensor, stats:
     return (out, m, l) if stats else out
 
 
+def latent_mix(g: Tensor, wqkv_t: Tensor, bqkv: Tensor, wo_t: Tensor, bo: Tensor) -> Tensor:
+    """In place on the fp32 latent rows g (P*4, 128): the four latents of each
+    position attend to each other (LN -> q|k|v -> per-head 4x4 softmax ->
+    output projection -> residual), fp32 throughout.  wqkv_t (128, 384) and
+    bqkv carry the LayerNorm affine; wo_t is (128, 128)."""
+    dev = _on_gpu(g, wqkv_t, bqkv, wo_t, bo)
+    if g.ndim != 2 or g.shape[1] != 128 or g.shape[0] % 4 or g.dtype != torch.float32 or g.stride(1) != 1:
+        raise ValueError("g must be fp32 (P*4, 128) rows")
+    for t, shape, name in ((wqkv_t, (128, 384), "wqkv_t"), (bqkv, (384,), "bqkv"), (wo_t, (128, 128), "wo_t"),
+                           (bo, (128,), "bo")):
+        if t.shape != shape or t.dtype != torch.float32 or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous fp32 tensor of shape {shape}")
+    p = g.shape[0] // 4
+    if p:
+        # the latent rows read and written once, the weights once
+        nbytes = p * 4 * 128 * 4 * 2 + (128 * 384 + 384 + 128 * 128 + 128) * 4
+        _launch("latent_mix", nbytes, p * 4 * 2 * 128 * 512, lambda: _check(
+            _lib().mantis_latent_mix(_ptr(g), g.stride(0), p, _ptr(wqkv_t), _ptr(bqkv), _ptr(wo_t), _ptr(bo),
+                                     _stream()),
+            "latent_mix",
+        ))
+    return g
+
+
 def latent_broadcast_rows(q: Tensor, kv: Tensor, window_pos: Tensor,
                           out_dtype: torch.dtype = torch.float32) -> Tensor:
     """Broadcast with k/v the two 128-wide halves of (P*4, 256) rows."""

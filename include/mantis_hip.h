@@ -167,6 +167,18 @@ int32_t mantis_cell_heads(const void* c, int32_t c_dtype, int32_t layer_norm, in
                           int64_t n_entries, float* out, int32_t* err_flag, void* stream);
 
 /*
+ * Latent self-mix, in place on the fp32 latent rows g (n_pos * 4 rows of
+ * 128, row stride ldg), per position p in fp32:
+ *   z = LN(g_p) (no affine: fold it into wqkv_t / bqkv),
+ *   [q | k | v] = z wqkv_t + bqkv,  wqkv_t (128, 384) = [Wq; Wk; Wv]^T,
+ *   a = per head of 32: softmax(q_h k_h^T / sqrt(32)) v_h,
+ *   g_p += a wo_t + bo,  wo_t (128, 128) = Wo^T.
+ * Replaces the reference's latent mix (model.py:516-526).
+ */
+int32_t mantis_latent_mix(float* g, int64_t ldg, int64_t n_pos, const float* wqkv_t, const float* bqkv,
+                          const float* wo_t, const float* bo, void* stream);
+
+/*
  * Window-latent read: four latent queries per position attend over the
  * position's windows (rows order[offsets[p]:offsets[p+1]] of k/v).  q is
  * (P*4, heads*hd), k/v (n_w, heads*hd) rows in `dtype` with row strides

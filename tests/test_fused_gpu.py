@@ -306,3 +306,26 @@ def test_cell_heads_match_the_unfused_composition(device, mode):
     ref = ops.fused_linear(xin, d(w1), d(b1), x2=acts, w2=d(w2), add1=ext, add2=d(g_half), add2_rows=d(cell_pos),
                            relu=True, w3=d(w3), b3=d(b3), out_dtype=torch.float32)
     torch.testing.assert_close(got.cpu(), ref.cpu(), rtol=1e-4, atol=1e-4)
+
+
+def test_latent_mix_matches_the_fp32_formulation(device):
+    # the four latents of a position attend to each other (model.py:516-526)
+    gen = _g(13)
+    p = 37
+    g = 2 * torch.randn(p * 4, 128, generator=gen) + 0.2
+    gam, bet = 1 + 0.1 * torch.randn(128, generator=gen), 0.05 * torch.randn(128, generator=gen)
+    wq, wk, wv, wo = [torch.randn(128, 128, generator=gen) / math.sqrt(128) for _ in range(4)]
+    bq, bv, bo = [0.05 * torch.randn(128, generator=gen) for _ in range(3)]
+    z = F.layer_norm(g, (128,), gam, bet, 1e-5)
+    q = (z @ wq.t() + bq).view(p, 4, 4, 32)
+    k = (z @ wk.t()).view(p, 4, 4, 32)
+    v = (z @ wv.t() + bv).view(p, 4, 4, 32)
+    sc = torch.einsum("pqhd,pkhd->phqk", q, k) / math.sqrt(32)
+    mixed = torch.einsum("phqk,pkhd->pqhd", sc.softmax(-1), v).reshape(p * 4, 128)
+    ref = g + mixed @ wo.t() + bo
+    # LayerNorm affine folded into the stacked projection, weights transposed
+    w = torch.cat([wq, wk, wv]) * gam[None, :]
+    b = torch.cat([bq, torch.zeros(128), bv]) + torch.cat([wq, wk, wv]) @ bet
+    got = g.to(device)
+    ops.latent_mix(got, w.t().contiguous().to(device), b.to(device), wo.t().contiguous().to(device), bo.to(device))
+    torch.testing.assert_close(got.cpu(), ref, rtol=1e-5, atol=2e-5)
