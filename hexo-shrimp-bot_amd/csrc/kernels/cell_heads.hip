@@ -13,8 +13,10 @@
 //
 // Layout: the MFMA layout of the row GEMMs — a wavefront owns 16 cells, lane
 // (l16, g) holds features {32ks + 8g .. +8} of cell l16 for the K = 128
-// inputs and features {16nt + 4g .. +4} of the 256 hidden ones, so each
-// lane gathers exactly the chunks it feeds to the products.  The hidden
+// inputs and features {16nt + 4g .. +4} of the 256 hidden ones.  The
+// decoder walk gathers the same feature groups on lane 4 l16 + g instead (a
+// cell's four lanes adjacent, so the gathers coalesce per quad) and hands
+// the sums to the MFMA lanes by lane permutes.  The hidden
 // tiles are packed to fp16 as the second product's B fragments (K slots
 // {4g..4g+3, 16+4g..16+4g+3} of each 32-step, matched by the W3 reads).
 // W1, W2 and W3 live in LDS for the persistent workgroup (8 wavefronts,
@@ -24,6 +26,9 @@
 
 namespace mantis {
 namespace {
+
+// the value v of lane `src` (all lanes active)
+__device__ __forceinline__ int32_t from_lane(int src, int32_t v) { return __builtin_amdgcn_ds_bpermute(src << 2, v); }
 
 constexpr int kK = 128;
 constexpr int kN1 = 256;
@@ -44,11 +49,11 @@ struct HeadArgs {
   const float* b3;
   const _Float16* pre;
   int64_t n_w;
-  const float* act_table;
+  const _Float16* act_table;  // (n_acls, 128)
   int64_t n_acls;
   const float* empty_rows;   // (3, 128)
   const int64_t* act_empty;  // (n_cells, 3)
-  const float* head_tab;     // (n_dcls, 256)
+  const _Float16* head_tab;   // (n_dcls, 256), lane-blocked columns
   int64_t n_dcls;
   const float* g_half;       // (n_pos, 256)
   int64_t n_pos;
@@ -79,33 +84,55 @@ __global__ void __launch_bounds__(kThreads) cell_heads_kernel(HeadArgs a) {
   __syncthreads();
 
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
-  const int l16 = lane % 16, g = lane / 16;
+  const int l16 = lane % 16, g = lane / 16;        // MFMA layout: cell l16, feature group g
+  const int ar = lane >> 2, aq = lane & 3;         // walk layout: cell ar, feature group aq
+  const int src_m = 16 * aq + ar;                  // MFMA lane of this walk lane's (cell, group)
+  const int src_a = 4 * l16 + g;                   // walk lane of this MFMA lane's (cell, group)
   const int64_t n_tiles = (a.n_cells + 15) / 16;
   for (int64_t tile = int64_t(blockIdx.x) * kWaves + wave; tile < n_tiles; tile += int64_t(gridDim.x) * kWaves) {
+    // an offset the compiler cannot see through: keeps the weight-fragment
+    // reads inside the loop instead of hoisting them into registers
+    int lds_off = 0;
+    asm volatile("" : "+s"(lds_off));
+    const _Float16* w1s = sw1 + lds_off;
+    const _Float16* w2s = sw2 + lds_off;
+    const _Float16* w3s = sw3 + lds_off;
     const int64_t row = tile * 16 + l16;
     const bool live = row < a.n_cells;
-    // ---- the cell's decoder run and position
-    int64_t st = 0, en = 0, pos = -1;
-    if (live) {
-      st = a.dec_ptr[row];
-      en = a.dec_ptr[row + 1];
-      st = st < 0 ? 0 : (st > a.n_entries ? a.n_entries : st);
-      en = en < st ? st : (en > a.n_entries ? a.n_entries : en);
-      pos = a.cell_pos[row];
-      if (pos < 0 || pos >= a.n_pos) {
-        raise_flag(a.flag, MANTIS_FLAG_INDEX);
-        pos = -1;
-      }
-    }
-    // ---- x = LN(c) in B layout
+    const int64_t rc = live ? row : 0;  // dead lanes read a real row and store nothing
+    // ---- the cell's decoder run and position, then its row
+    int64_t st = a.dec_ptr[rc], en = a.dec_ptr[rc + 1];
+    const int64_t pos_raw = a.cell_pos[rc];
     float xv[4][8];
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      if (live) load8(static_cast<const Tin*>(a.c) + row * a.ldc + 32 * ks + 8 * g, xv[ks]);
-      else
+    for (int ks = 0; ks < 4; ++ks) load8(static_cast<const Tin*>(a.c) + rc * a.ldc + 32 * ks + 8 * g, xv[ks]);
+    st = st < 0 ? 0 : (st > a.n_entries ? a.n_entries : st);
+    en = en < st ? st : (en > a.n_entries ? a.n_entries : en);
+    const int cnt = live ? int(en - st) : 0;
+    int maxc = cnt;
 #pragma unroll
-        for (int t = 0; t < 8; ++t) xv[ks][t] = 0.f;
+    for (int o = 1; o < 16; o <<= 1) maxc = max(maxc, __shfl_xor(maxc, o));
+    // The decoder walk runs on the walk layout: the four lanes of a cell are
+    // adjacent, so a quad's 16-byte gathers cover 64 contiguous bytes.  Each
+    // entry's three indices are requested one entry ahead, unconditionally
+    // (entry 0 for a lane past its run) and checked where they are used.
+    const int acnt = from_lane(src_m, cnt);
+    const int64_t ast = int64_t((uint64_t(uint32_t(from_lane(src_m, int32_t(uint64_t(st) >> 32)))) << 32) |
+                                uint32_t(from_lane(src_m, int32_t(st))));
+    int64_t iw = 0, ia = 0, id = 0;
+    auto fetch = [&](int j) {
+      const int64_t e = j < acnt ? ast + j : 0;
+      iw = a.dec_window[e];
+      ia = a.act_class[e];
+      id = a.dec_class[e];
+    };
+    if (maxc > 0) fetch(0);
+    int64_t pos = -1;
+    if (live) {
+      if (pos_raw < 0 || pos_raw >= a.n_pos) raise_flag(a.flag, MANTIS_FLAG_INDEX);
+      else pos = pos_raw;
     }
+    // ---- x = LN(c) in B layout
     if constexpr (kLN) {
       float s = 0.f;
 #pragma unroll
@@ -136,67 +163,80 @@ __global__ void __launch_bounds__(kThreads) cell_heads_kernel(HeadArgs a) {
     for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
       for (int t = 0; t < 8; ++t) xb[ks][t] = f2h(xv[ks][t]);
-    // ---- action rows in B layout: relu(pre[win] + table[cls]) summed over the run
-    float av[4][8];
+    // ---- the walk: action rows relu(pre[win] + table[acls]) (features
+    // 32 i + 8 aq + t) and class rows head_tab[dcls] (features 16 nt + 4 aq + t,
+    // stored lane-blocked: this lane's 64 values are contiguous)
+    float av[32], ev[64];
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
+    for (int i = 0; i < 32; ++i) av[i] = 0.f;
 #pragma unroll
-      for (int t = 0; t < 8; ++t) av[ks][t] = 0.f;
-    for (int64_t e = st; e < en; ++e) {
-      const int64_t w = a.dec_window[e], c = a.act_class[e];
-      if (w < 0 || w >= a.n_w || c < 0 || c >= a.n_acls) {
-        raise_flag(a.flag, MANTIS_FLAG_INDEX);
-        continue;
+    for (int i = 0; i < 64; ++i) ev[i] = 0.f;
+    uint4 pr[4], at[4], ht[8];
+    for (int j = 0; j < maxc; ++j) {
+      const bool in = j < acnt;
+      const bool ok = in && iw >= 0 && iw < a.n_w && ia >= 0 && ia < a.n_acls && id >= 0 && id < a.n_dcls;
+      if (in && !ok) raise_flag(a.flag, MANTIS_FLAG_INDEX);
+      if (ok) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          pr[i] = *reinterpret_cast<const uint4*>(a.pre + (uint32_t(iw) * uint32_t(kK) + uint32_t(32 * i + 8 * aq)));
+          at[i] = *reinterpret_cast<const uint4*>(a.act_table + (uint32_t(ia) * uint32_t(kK) + uint32_t(32 * i + 8 * aq)));
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+          ht[k] = *reinterpret_cast<const uint4*>(a.head_tab + (uint32_t(id) * uint32_t(kN1) + uint32_t(64 * aq + 8 * k)));
       }
+      if (j + 1 < maxc) fetch(j + 1);
+      if (ok) {
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        float pv[8], tv[8];
-        load8(a.pre + w * kK + 32 * ks + 8 * g, pv);
-        load8(a.act_table + c * kK + 32 * ks + 8 * g, tv);
+        for (int i = 0; i < 4; ++i) {
+          const f16x8_t pv = __builtin_bit_cast(f16x8_t, pr[i]), tv = __builtin_bit_cast(f16x8_t, at[i]);
 #pragma unroll
-        for (int t = 0; t < 8; ++t) av[ks][t] += fmaxf(pv[t] + tv[t], 0.f);
-      }
-    }
-    if (live) {
+          for (int t = 0; t < 8; ++t) av[8 * i + t] += fmaxf(float(pv[t]) + float(tv[t]), 0.f);
+        }
 #pragma unroll
-      for (int o = 0; o < 3; ++o) {
-        const float n = float(a.act_empty[row * 3 + o]);
+        for (int k = 0; k < 8; ++k) {
+          const f16x8_t hv = __builtin_bit_cast(f16x8_t, ht[k]);
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          float r[8];
-          load8(a.empty_rows + o * kK + 32 * ks + 8 * g, r);
-#pragma unroll
-          for (int t = 0; t < 8; ++t) av[ks][t] = fmaf(n, r[t], av[ks][t]);
+          for (int t = 0; t < 8; ++t) ev[8 * k + t] += float(hv[t]);
         }
       }
     }
-    f16x8_t ab[4];
+    // EMPTY-class action rows, weighted by the cell's counts
+    {
+      const int64_t arow = tile * 16 + ar;
+      if (arow < a.n_cells) {
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
+        for (int o = 0; o < 3; ++o) {
+          const float n = float(a.act_empty[arow * 3 + o]);
 #pragma unroll
-      for (int t = 0; t < 8; ++t) ab[ks][t] = f2h(av[ks][t]);
-    // ---- class sums in D layout (features 16nt + 4g .. +4 of the 256): all
-    // 16 chunks of an entry's row are requested together
-    f32x4_t ext[kN1 / 16];
+          for (int i = 0; i < 4; ++i) {
+            float r[8];
+            load8(a.empty_rows + o * kK + 32 * i + 8 * aq, r);
 #pragma unroll
-    for (int nt = 0; nt < kN1 / 16; ++nt) ext[nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    for (int64_t e = st; e < en; ++e) {
-      const int64_t c = a.dec_class[e];
-      if (c < 0 || c >= a.n_dcls) {
-        raise_flag(a.flag, MANTIS_FLAG_INDEX);
-        continue;
-      }
-      float4 r[kN1 / 16];
-#pragma unroll
-      for (int nt = 0; nt < kN1 / 16; ++nt) r[nt] = *reinterpret_cast<const float4*>(a.head_tab + c * kN1 + 16 * nt + 4 * g);
-#pragma unroll
-      for (int nt = 0; nt < kN1 / 16; ++nt) {
-        ext[nt][0] += r[nt].x;
-        ext[nt][1] += r[nt].y;
-        ext[nt][2] += r[nt].z;
-        ext[nt][3] += r[nt].w;
+            for (int t = 0; t < 8; ++t) av[8 * i + t] = fmaf(n, r[t], av[8 * i + t]);
+          }
+        }
       }
     }
+    // ---- back to the MFMA layout: the action rows as fp16 B fragments, the
+    // class sums as the fp32 addends of the hidden tiles
+    f16x8_t ab[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      uint4 w;
+      w.x = uint32_t(from_lane(src_a, int32_t(pack_f16x2(av[8 * ks], av[8 * ks + 1]))));
+      w.y = uint32_t(from_lane(src_a, int32_t(pack_f16x2(av[8 * ks + 2], av[8 * ks + 3]))));
+      w.z = uint32_t(from_lane(src_a, int32_t(pack_f16x2(av[8 * ks + 4], av[8 * ks + 5]))));
+      w.w = uint32_t(from_lane(src_a, int32_t(pack_f16x2(av[8 * ks + 6], av[8 * ks + 7]))));
+      ab[ks] = __builtin_bit_cast(f16x8_t, w);
+    }
+    f32x4_t ext[kN1 / 16];
+#pragma unroll
+    for (int nt = 0; nt < kN1 / 16; ++nt)
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        ext[nt][t] = __int_as_float(from_lane(src_a, __float_as_int(ev[4 * nt + t])));
     // ---- hidden tiles: h^T = W1 . x^T + W2 . acts^T + b1 + ext + g_half[pos]
     f16x8_t hb[kN1 / 32];
 #pragma unroll
@@ -208,9 +248,9 @@ __global__ void __launch_bounds__(kThreads) cell_heads_kernel(HeadArgs a) {
         f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-          const f16x8_t wf = *reinterpret_cast<const f16x8_t*>(sw1 + (16 * nt + l16) * kPitch + 32 * ks + 8 * g);
+          const f16x8_t wf = *reinterpret_cast<const f16x8_t*>(w1s + (16 * nt + l16) * kPitch + 32 * ks + 8 * g);
           acc = mfma16x16x32(wf, xb[ks], acc);
-          const f16x8_t wf2 = *reinterpret_cast<const f16x8_t*>(sw2 + (16 * nt + l16) * kPitch + 32 * ks + 8 * g);
+          const f16x8_t wf2 = *reinterpret_cast<const f16x8_t*>(w2s + (16 * nt + l16) * kPitch + 32 * ks + 8 * g);
           acc = mfma16x16x32(wf2, ab[ks], acc);
         }
         const int f = 16 * nt + 4 * g;
@@ -237,7 +277,7 @@ __global__ void __launch_bounds__(kThreads) cell_heads_kernel(HeadArgs a) {
     f32x4_t y = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < kN1 / 32; ++ks) {
-      const _Float16* wr = sw3 + l16 * kP3 + 32 * ks;
+      const _Float16* wr = w3s + l16 * kP3 + 32 * ks;
       const uint2 lo = *reinterpret_cast<const uint2*>(wr + 4 * g);
       const uint2 hi = *reinterpret_cast<const uint2*>(wr + 16 + 4 * g);
       const f16x8_t wf = __builtin_bit_cast(f16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
@@ -259,8 +299,8 @@ using namespace mantis;
 extern "C" int32_t mantis_cell_heads(const void* c, int32_t c_dtype, int32_t layer_norm, int64_t ldc, int64_t n_cells,
                                      const void* w1, const float* b1,
                                      const void* w2, const void* w3, const float* b3, const void* pre, int64_t n_w,
-                                     const float* act_table, int64_t n_acls, const float* empty_rows,
-                                     const int64_t* act_empty, const float* head_tab, int64_t n_dcls,
+                                     const void* act_table, int64_t n_acls, const float* empty_rows,
+                                     const int64_t* act_empty, const void* head_tab, int64_t n_dcls,
                                      const float* g_half, int64_t n_pos, const int64_t* cell_pos,
                                      const int64_t* dec_ptr, const int64_t* dec_window, const int64_t* act_class,
                                      const int64_t* dec_class, int64_t n_entries, float* out, int32_t* err_flag,
@@ -272,15 +312,18 @@ extern "C" int32_t mantis_cell_heads(const void* c, int32_t c_dtype, int32_t lay
     return MANTIS_E_ARG;
   if (n_entries < 0 || (n_entries > 0 && (!dec_window || !act_class || !dec_class || !pre || n_w <= 0)))
     return MANTIS_E_ARG;
+  // gathered rows use 32-bit element offsets
+  if (n_w > 4294967295LL / kK || n_acls > 4294967295LL / kK || n_dcls > 4294967295LL / kN1) return MANTIS_E_ARG;
   for (const void* p : {c, w1, static_cast<const void*>(b1), w2, w3,
-                        static_cast<const void*>(b3), static_cast<const void*>(act_table),
-                        static_cast<const void*>(empty_rows), static_cast<const void*>(head_tab),
+                        static_cast<const void*>(b3), act_table,
+                        static_cast<const void*>(empty_rows), head_tab,
                         static_cast<const void*>(g_half), static_cast<const void*>(out)})
     if (!aligned16(p)) return MANTIS_E_ARG;
   if (pre && !aligned16(pre)) return MANTIS_E_ARG;
   HeadArgs a{c, ldc, n_cells, static_cast<const _Float16*>(w1), b1, static_cast<const _Float16*>(w2),
-             static_cast<const _Float16*>(w3), b3, static_cast<const _Float16*>(pre), n_w, act_table, n_acls,
-             empty_rows, act_empty, head_tab, n_dcls, g_half, n_pos, cell_pos, dec_ptr, dec_window, act_class,
+             static_cast<const _Float16*>(w3), b3, static_cast<const _Float16*>(pre), n_w,
+             static_cast<const _Float16*>(act_table), n_acls, empty_rows, act_empty,
+             static_cast<const _Float16*>(head_tab), n_dcls, g_half, n_pos, cell_pos, dec_ptr, dec_window, act_class,
              dec_class, n_entries, out, err_flag};
   int dev = 0, cus = 0;
   if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=

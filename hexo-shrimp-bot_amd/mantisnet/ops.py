@@ -315,6 +315,18 @@ def interleave_heads(t: Tensor) -> Tensor:
     return t.index_select(-1, idx)
 
 
+def _head_tab_blocked_index() -> Tensor:
+    j = torch.arange(256)
+    q, nt, t = j // 64, (j // 4) % 16, j % 4
+    return 16 * nt + 4 * q + t
+
+
+# column j of the cell heads' lane-blocked class table holds natural column
+# HEAD_TAB_BLOCKED[j]: lane group q's 64 features (16 nt + 4 q + t) are the
+# contiguous columns 64 q .. 64 q + 63
+HEAD_TAB_BLOCKED = _head_tab_blocked_index()
+
+
 class SubStage(NamedTuple):
     """One typed-attention sub-stage over residual rows: weights (wq, bq, wo,
     bo), the fp16 (n_src, 256) k|v rows, the class bias (4, classes) and
@@ -424,9 +436,14 @@ def cell_heads(c: Tensor, w1: Tensor, b1: Tensor, w2: Tensor, w3: Tensor, b3: Te
     if pre.ndim != 2 or pre.shape[1] != 128 or pre.dtype != torch.float16 or not pre.is_contiguous():
         raise ValueError("pre must be contiguous fp16 (n_w, 128) rows")
     f32 = lambda t: t.float().contiguous()  # noqa: E731
-    b1, b3, act_table, empty_rows, head_tab, g_half = map(f32, (b1, b3, act_table, empty_rows, head_tab, g_half))
-    if empty_rows.shape != (3, 128) or head_tab.shape[1] != 256 or g_half.shape[1] != 256:
+    b1, b3, empty_rows, g_half = map(f32, (b1, b3, empty_rows, g_half))
+    if empty_rows.shape != (3, 128) or head_tab.ndim != 2 or head_tab.shape[1] != 256 or g_half.shape[1] != 256:
         raise ValueError("empty_rows (3, 128), head_tab (n, 256) and g_half (P, 256) expected")
+    if act_table.ndim != 2 or act_table.shape[1] != 128:
+        raise ValueError("act_table must be (n, 128)")
+    # the kernel gathers both tables in fp16, the class table lane-blocked
+    act_table = act_table.to(torch.float16).contiguous()
+    head_tab = head_tab.index_select(1, HEAD_TAB_BLOCKED.to(head_tab.device)).to(torch.float16).contiguous()
     act_empty = _i64(act_empty, "act_empty")
     cell_pos, dec_ptr = _i64(cell_pos, "cell_pos"), _i64(dec_ptr, "dec_ptr")
     dec_window, act_class, dec_class = _i64(dec_window, "dec_window"), _i64(act_class, "act_class"), \

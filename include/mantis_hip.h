@@ -151,17 +151,18 @@ int32_t mantis_attention_substages(float* x, int64_t ldx, int64_t n_rows, const 
  *   out[r] = w3 fp16(h) + b3
  * c: (n_cells, 128) rows in c_dtype (fp32, or fp16 without layer_norm), row
  * stride ldc; w1, w2: (256, 128) fp16; b1 (256); w3 (16, 256) fp16; b3 (16);
- * pre (n_w, 128) fp16; act_table (n_acls, 128), empty_rows (3, 128),
- * head_tab (n_dcls, 256), g_half (n_pos, 256) fp32; act_empty (n_cells, 3)
- * and the index arrays int64; out (n_cells, 16) fp32.
+ * pre (n_w, 128) and act_table (n_acls, 128) fp16; head_tab (n_dcls, 256)
+ * fp16 with lane-blocked columns (column 64*q + 4*nt + t holds feature
+ * 16*nt + 4*q + t); empty_rows (3, 128), g_half (n_pos, 256) fp32;
+ * act_empty (n_cells, 3) and the index arrays int64; out (n_cells, 16) fp32.
  * Replaces the reference's _action_contribution / encode_rows / class_row_sum
  * and the first layers of mlp_p and mlp_q (model.py:1031-1091,
  * row_encoder.py:40-112, message_passing.py:331-339).
  */
 int32_t mantis_cell_heads(const void* c, int32_t c_dtype, int32_t layer_norm, int64_t ldc, int64_t n_cells,
                           const void* w1, const float* b1, const void* w2, const void* w3, const float* b3,
-                          const void* pre, int64_t n_w, const float* act_table, int64_t n_acls,
-                          const float* empty_rows, const int64_t* act_empty, const float* head_tab, int64_t n_dcls,
+                          const void* pre, int64_t n_w, const void* act_table, int64_t n_acls,
+                          const float* empty_rows, const int64_t* act_empty, const void* head_tab, int64_t n_dcls,
                           const float* g_half, int64_t n_pos, const int64_t* cell_pos, const int64_t* dec_ptr,
                           const int64_t* dec_window, const int64_t* act_class, const int64_t* dec_class,
                           int64_t n_entries, float* out, int32_t* err_flag, void* stream);

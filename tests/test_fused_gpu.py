@@ -299,13 +299,19 @@ def test_cell_heads_match_the_unfused_composition(device, mode):
                          d(head_tab), d(g_half), d(cell_pos), d(ptr), d(win), d(acl), d(dcl),
                          layer_norm=mode == "layer_norm")
     ops.raise_on_device_error(device)
-    acts = ops.row_encode(d(pre), d(table), d(win), d(acl), d(ptr), n, d(act_empty), d(empty_rows))
-    ext = ops.run_reduce(d(head_tab), d(dcl), d(ptr), n, torch.float32)
+    # the fused kernel gathers the two class tables in fp16: the reference
+    # composition gets the same fp16-rounded tables
+    t16, h16 = table.to(H16).float(), head_tab.to(H16).float()
+    acts = ops.row_encode(d(pre), d(t16), d(win), d(acl), d(ptr), n, d(act_empty), d(empty_rows))
+    ext = ops.run_reduce(d(h16), d(dcl), d(ptr), n, torch.float32)
     # (fp32 rows enter the products as fp16, exactly as fp16 rows do)
     xin = ops.layer_norm(d(c), d(torch.ones(128)), d(torch.zeros(128)), H16) if mode == "layer_norm" else d(c.to(H16))
     ref = ops.fused_linear(xin, d(w1), d(b1), x2=acts, w2=d(w2), add1=ext, add2=d(g_half), add2_rows=d(cell_pos),
                            relu=True, w3=d(w3), b3=d(b3), out_dtype=torch.float32)
-    torch.testing.assert_close(got.cpu(), ref.cpu(), rtol=1e-4, atol=1e-4)
+    # the action-row sums (|acts| up to ~10) are rounded to fp16 for the
+    # second product; summed in another order than row_encode's, a rare sum
+    # lands one fp16 unit (up to 8e-3) apart, a few 1e-4 in the outputs
+    torch.testing.assert_close(got.cpu(), ref.cpu(), rtol=1e-4, atol=1e-3)
 
 
 def test_latent_mix_matches_the_fp32_formulation(device):

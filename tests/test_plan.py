@@ -58,3 +58,14 @@ def test_head_interleave_layout():
     assert torch.equal(ops.interleave_heads(ops.interleave_heads(row)), row)
     with pytest.raises(ValueError):
         ops.interleave_heads(torch.zeros(3, 100))
+
+
+def test_head_tab_blocked_layout():
+    # lane group q's 64 features 16 nt + 4 q + t are columns 64 q .. 64 q + 63
+    from mantisnet import ops
+    idx = ops.HEAD_TAB_BLOCKED
+    assert sorted(idx.tolist()) == list(range(256))
+    for q in range(4):
+        for nt in range(16):
+            for t in range(4):
+                assert idx[64 * q + 4 * nt + t] == 16 * nt + 4 * q + t
