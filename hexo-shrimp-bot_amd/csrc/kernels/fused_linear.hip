@@ -88,11 +88,15 @@ struct Smem {
   static int bytes(int n3) { return (w1 + w2 + (kStage2 ? n3 * p3 : 0)) * 2; }
 };
 
-constexpr int kThreads = 512;  // 8 wavefronts share one LDS copy of the weights
-constexpr int kTileRows = 16 * (kThreads / 64);
+// Wavefronts sharing one LDS copy of the weights: 8, or 16 for the widest
+// projection, whose 139 KB of weights leave room for one workgroup per CU
+// (the extra wavefronts keep more rows in flight)
+template <int N1>
+constexpr int threads_for() { return N1 >= 512 ? 1024 : 512; }
 
 template <typename TX, typename TX2, bool kLN, int N1, bool kX2, bool kRelu, bool kStage2, int kMode>
-__global__ void __launch_bounds__(kThreads) fused_linear_kernel(Args a) {
+__global__ void __launch_bounds__(threads_for<N1>()) fused_linear_kernel(Args a) {
+  constexpr int kTileRows = 16 * (threads_for<N1>() / 64);
   extern __shared__ __attribute__((aligned(16))) _Float16 smem[];
   using S = Smem<N1, kStage2, kX2>;
   _Float16* sw1 = smem;
@@ -308,10 +312,11 @@ int32_t launch(const Args& a, hipStream_t stream) {
       return MANTIS_E_LAUNCH;
     configured = true;
   }
+  constexpr int kTileRows = 16 * (threads_for<N1>() / 64);
   const int64_t tiles = (a.m + kTileRows - 1) / kTileRows;
   const int per_cu = std::max(1, std::min(4, kMaxLds / std::max(bytes, 1)));
   const int64_t grid = std::min<int64_t>(tiles, int64_t(cu_count()) * per_cu);
-  kernel<<<unsigned(grid), kThreads, bytes, stream>>>(a);
+  kernel<<<unsigned(grid), threads_for<N1>(), bytes, stream>>>(a);
   return launched();
 }
 
@@ -355,6 +360,7 @@ extern "C" int32_t mantis_fused_linear(const void* x, int32_t x_dtype, int64_t l
       if (n1 == 128) return launch<float, float, true, 128, false, false, false, 0>(a, s);
       if (n1 == 256) return launch<float, float, true, 256, false, false, false, 0>(a, s);
       if (n1 == 384) return launch<float, float, true, 384, false, false, false, 0>(a, s);
+      if (n1 == 512) return launch<float, float, true, 512, false, false, false, 0>(a, s);
     }
     if (x_dtype == MANTIS_F32 && ln && !r && mode == 1 && n1 == 128)
       return launch<float, float, true, 128, false, false, false, 1>(a, s);

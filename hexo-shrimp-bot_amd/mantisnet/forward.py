@@ -153,7 +153,14 @@ def _prepare(model, P) -> dict[str, Tensor]:
         put(pb + "wr_q", _fold(P, pb + "ln_wr_w", [pb + "wr_wq"]))
         put(pb + "wr_kv", _interleaved(_fold(P, pb + "ln_wr_c", [pb + "wr_wk", pb + "wr_wv"])))
         put(pb + "wr_o", _fold(P, None, [pb + "wr_wo"]))
-        put(pb + "v", _fold(P, pb + "ln_sw_w", [pb + "v"]))
+        # the three projections of the same window state (stones <- windows
+        # values, latent-read keys/values, latent-broadcast queries) in one
+        # 512-wide launch: one read of w instead of three
+        wv_, bv_ = _fold(P, pb + "ln_sw_w", [pb + "v"])
+        wr_, br_ = _fold(P, pb + "latent_ln_read_w", [pb + "latent_wk_read", pb + "latent_wv_read"])
+        wb_, bb_ = _fold(P, pb + "latent_ln_bcast_q", [pb + "latent_wq_bcast"])
+        t[pb + "wproj.w"] = torch.cat([wv_, wr_, wb_]).contiguous()
+        t[pb + "wproj.b"] = torch.cat([bv_, br_, bb_]).contiguous()
         put(pb + "mlp_s1", _fold(P, pb + "ln_sw_s", [pb + "mlp_s.lin_a"]))
         t[pb + "mlp_s2.w"] = P[pb + "mlp_s.lin_b.weight"].to(HALF).contiguous()
         put(pb + "mlp_s3", _fold(P, None, [pb + "mlp_s.out"]))
@@ -161,9 +168,7 @@ def _prepare(model, P) -> dict[str, Tensor]:
         put(pb + "qkv", _fold(P, pb + "ln_attn", [pb + "wq", pb + "wk", pb + "wv"]))
         put(pb + "attn_o", _fold(P, None, [pb + "wo"]))
         put(pb + "lq_read", _fold(P, pb + "latent_ln_read_q", [pb + "latent_wq_read"]))
-        put(pb + "lkv_read", _fold(P, pb + "latent_ln_read_w", [pb + "latent_wk_read", pb + "latent_wv_read"]))
         put(pb + "lo_read", _fold(P, None, [pb + "latent_wo_read"]))
-        put(pb + "lq_bcast", _fold(P, pb + "latent_ln_bcast_q", [pb + "latent_wq_bcast"]))
         put(pb + "lkv_bcast", _fold(P, pb + "latent_ln_bcast_l", [pb + "latent_wk_bcast", pb + "latent_wv_bcast"]))
         put(pb + "lo_bcast", _fold(P, None, [pb + "latent_wo_bcast"]))
         # the latent mix runs in fp32: transposed fp32 weights, LN folded in
@@ -383,15 +388,15 @@ def _cell_stage(W, P, pb, plan: Plan, s, w, c):
     ops.attention_substages(w, [wr])
 
 
-def _latent_cycle(W, P, pb, plan: Plan, w, g2):
+def _latent_cycle(W, P, pb, plan: Plan, w, g2, kv, qb):
+    """kv: the windows' latent-read keys|values, qb: their broadcast queries
+    (both projected from w with the stones' values, see _block)."""
     p = plan.n_pos
     q = _proj(W, pb + "lq_read", g2)
-    kv = _proj(W, pb + "lkv_read", w)
     read = ops.latent_read(q.view(p, 4, 4, 32), kv[:, :128], kv[:, 128:], plan.layout_offsets, plan.layout_order)
     _resid(W, pb + "lo_read", read.view(p * 4, 128), g2)
     # 4 x 4 latent self-mix, fp32 (all four slots live; model.py:516-526)
     ops.latent_mix(g2, W[pb + "mix_qkv.wt"], W[pb + "mix_qkv.b"], W[pb + "mix_o.wt"], W[pb + "mix_o.b"])
-    qb = _proj(W, pb + "lq_bcast", w)
     kvb = _proj(W, pb + "lkv_bcast", g2)
     out = ops.latent_broadcast_rows(qb, kvb, plan.window_pos, out_dtype=HALF)
     _resid(W, pb + "lo_bcast", out.view(plan.n_w, 128), w)
@@ -410,9 +415,11 @@ def _block(W, P, i: int, plan: Plan, b: Batch, sg, w, c, sw_all, update_stones: 
        out=w, residual=True)
     # §5.1b cell stage
     _cell_stage(W, P, pb, plan, s, w, c)
-    # §5.2 stones <- windows: s += mlp_s(LN s, agg + class term)
-    y = _proj(W, pb + "v", w)
-    agg = ops.run_reduce(y, plan.run_window, plan.inc_stone_ptr, n_s, F32)
+    # §5.2 stones <- windows: s += mlp_s(LN s, agg + class term); w does not
+    # change again until the latent broadcast, so its latent-read keys/values
+    # and broadcast queries are projected here in the same launch
+    wp = _proj(W, pb + "wproj", w)  # (n_w, 512): v | latent k | latent v | broadcast q
+    agg = ops.run_reduce(wp[:, :128], plan.run_window, plan.inc_stone_ptr, n_s, F32)
     FL(s, W[pb + "mlp_s1.w"], W[pb + "mlp_s1.b"], layer_norm=True, x2=agg, w2=W[pb + "mlp_s2.w"],
        add1=sw_all[:, 128 * i:128 * (i + 1)], relu=True, w3=W[pb + "mlp_s3.w"], b3=W[pb + "mlp_s3.b"],
        out=s, residual=True)
@@ -434,7 +441,7 @@ def _block(W, P, i: int, plan: Plan, b: Batch, sg, w, c, sw_all, update_stones: 
         read = torch.matmul(sc.softmax(-1), view(2).float()).transpose(1, 2).reshape(p * GLOBAL_ROWS, 128)
         _resid(W, pb + "attn_o", read.contiguous(), g2)
     # §5.4 latent cycle
-    _latent_cycle(W, P, pb, plan, w, g2)
+    _latent_cycle(W, P, pb, plan, w, g2, wp[:, 128:384], wp[:, 384:])
     # FFN over [stones; latents] (latents only in the last block)
     tgt = sg if update_stones else g2
     FL(tgt, W[pb + "ffn1.w"], W[pb + "ffn1.b"], layer_norm=True, relu=True, w3=W[pb + "ffn2.w"],
