@@ -3,7 +3,7 @@
 ``network_evaluate(model, cfg)(batch)`` returns flat fp32 CPU tensors —
 policy logits, the acting score and the action value — exactly as the
 reference does, serialised through one module-level ``_gpu_lock``.  The MI355X
-forward fixes its own precision (bf16 GEMM operands, fp32 accumulation,
+forward fixes its own precision (fp16 GEMM operands, fp32 accumulation,
 softmax and head outputs), so ``cfg.autocast`` and ``cfg.compile`` are
 accepted and have no effect: there is no traced graph to compile and no
 autocast region to enter.

@@ -559,6 +559,39 @@ def latent_mix(g: Tensor, wqkv_t: Tensor, bqkv: Tensor, wo_t: Tensor, bo: Tensor
     return g
 
 
+def improve_policy(policy_logits: Tensor, q_score: Tensor, q_value: Tensor, offsets: Tensor, tau: float,
+                   lam: float) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """(probs (N,), v_hat, kl, norm_entropy (P,)) of the KLENT closed-form
+    improvement per position (see mantis_improve_policy), in the inputs'
+    promoted dtype (float32, or float64 when an input is float64)."""
+    dev = _on_gpu(policy_logits, q_score, q_value, offsets)
+    if not (policy_logits.ndim == q_score.ndim == q_value.ndim == 1):
+        raise ValueError("policy_logits, q_score and q_value must be flat (N,) tensors")
+    if not (policy_logits.shape == q_score.shape == q_value.shape):
+        raise ValueError("policy_logits, q_score and q_value must have one shape")
+    dt = torch.promote_types(torch.promote_types(torch.promote_types(policy_logits.dtype, q_score.dtype),
+                                                 q_value.dtype), torch.float32)
+    if dt not in (torch.float32, torch.float64):
+        raise ValueError(f"unsupported dtype {dt}")
+    logits, score, q = (t.to(dt).contiguous() for t in (policy_logits, q_score, q_value))
+    offsets = _i64(offsets, "offsets")
+    p, n = offsets.numel() - 1, logits.numel()
+    if p < 0:
+        raise ValueError("offsets must hold P + 1 entries")
+    probs = torch.empty(n, dtype=dt, device=dev)
+    v_hat, kl, ent = (torch.empty(p, dtype=dt, device=dev) for _ in range(3))
+    if p:
+        es = logits.element_size()
+        _launch("improve_policy", n * 4 * es + (p + 1) * 8 + p * 3 * es, 12 * n, lambda: _check(
+            _lib().mantis_improve_policy(
+                _ptr(logits), _ptr(score), _ptr(q), 0 if dt == torch.float32 else 3, _ptr(offsets), p, n,
+                float(tau), float(lam), _ptr(probs), _ptr(v_hat), _ptr(kl), _ptr(ent), _ptr(error_flag(dev)),
+                _stream()),
+            "improve_policy",
+        ))
+    return probs, v_hat, kl, ent
+
+
 def latent_broadcast_rows(q: Tensor, kv: Tensor, window_pos: Tensor,
                           out_dtype: torch.dtype = torch.float32) -> Tensor:
     """Broadcast with k/v the two 128-wide halves of (P*4, 256) rows."""

@@ -29,6 +29,7 @@ extern "C" {
 #define MANTIS_F32 0
 #define MANTIS_BF16 1
 #define MANTIS_F16 2
+#define MANTIS_F64 3 /* only where an entry point says so */
 
 #define MANTIS_OK 0
 #define MANTIS_E_ARG 1    /* unsupported shape, dtype or null pointer */
@@ -178,6 +179,27 @@ int32_t mantis_cell_heads(const void* c, int32_t c_dtype, int32_t layer_norm, in
  */
 int32_t mantis_latent_mix(float* g, int64_t ldg, int64_t n_pos, const float* wqkv_t, const float* bqkv,
                           const float* wo_t, const float* bo, void* stream);
+
+/*
+ * KLENT closed-form policy improvement over the legal cells of n_pos
+ * positions (CSR offsets (n_pos + 1) into the n flat cells), per position:
+ *   log_pi = log_softmax(policy_logits), log_imp = log_softmax((q_score +
+ *   tau * log_pi) / (tau + lam)), probs = exp(log_imp), and with
+ *   mass = sum(probs): v_hat = sum(probs * q_value) / mass,
+ *   kl = sum(probs * (log_imp - log_pi)) / mass, norm_entropy =
+ *   sum(-probs * log_imp) / mass / log(count) (0 for one cell).
+ * Inputs and outputs in dtype, MANTIS_F32 or MANTIS_F64 (the reference
+ * computes in the promoted input type); probs (n), the rest (n_pos).
+ * tau, lam >= 0 with tau + lam > 0.  A bad offset is clamped and raises
+ * MANTIS_FLAG_ORDER.
+ * Replaces mantisnet.klent.improve.improved_policy (klent/improve.py:27-69)
+ * and the per-row improve_policy of the Rust evaluator seam
+ * (crates/models/mantisnet/src/improvement.rs:104-175, seam.rs:35-79).
+ */
+int32_t mantis_improve_policy(const void* policy_logits, const void* q_score, const void* q_value, int32_t dtype,
+                              const int64_t* offsets, int64_t n_pos, int64_t n, double tau, double lam,
+                              void* probs, void* v_hat, void* kl, void* norm_entropy, int32_t* err_flag,
+                              void* stream);
 
 /*
  * Window-latent read: four latent queries per position attend over the
