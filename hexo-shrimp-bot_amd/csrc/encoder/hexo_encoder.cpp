@@ -19,6 +19,8 @@
 #include "../../../include/hexo_encoder.h"
 
 #include <algorithm>
+#include <cmath>
+#include <cstdint>
 #include <array>
 #include <atomic>
 #include <cstdio>
@@ -35,6 +37,9 @@ namespace {
 constexpr int kWin = 6;
 constexpr int kRadius = 8;
 constexpr int kTactical = 11;
+// vocabulary sizes (encoder.rs:127-137, :274): window ranks, occupancy,
+// decoder and post-placement classes
+constexpr int64_t kTernPatterns = 377, kTernOcc = 1458, kTernDec = 726, kTernPost1 = 729;
 constexpr int kThreatCap = 8;
 constexpr int kDecClasses = 726;
 constexpr int kGlobalRows = 4;
@@ -291,7 +296,13 @@ struct Graph {
   std::vector<int64_t> dec_cell, dec_window, dec_class, act_class, act_empty;
   std::vector<int64_t> act_rev_local;  // window-major stable order of this position's decoder
   std::vector<float> tactical;
+  // the dense action rows, legal-cell-major, then axis, then slot (18 per
+  // cell): source window or -1, post-placement class, pre-placement status
+  std::vector<int64_t> action_window, action_post1, action_status;
 };
+
+constexpr int64_t kStatusOwn = 0, kStatusOpp = 1, kStatusEmpty = 2, kStatusMixed = 3;
+constexpr int kRowsPerCell = 18;
 
 Graph build(const Position& pos) {
   const Vocab& V = vocab();
@@ -428,6 +439,12 @@ Graph build(const Position& pos) {
                         ? widx.v[(size_t(sq - widx.q0) * widx.nr + (sr - widx.r0)) * 3 + a]
                         : -1;
         int pre = w >= 0 ? wpattern[w] : 0, own = w >= 0 ? wown[w] : 0, opp = w >= 0 ? wopp[w] : 0;
+        g.action_window.push_back(w);
+        g.action_post1.push_back(V.post1[pre + V.pow3[k]][k]);
+        g.action_status.push_back(w < 0 ? kStatusEmpty
+                                  : own && opp ? kStatusMixed
+                                  : own        ? kStatusOwn
+                                               : kStatusOpp);
         if (w >= 0) {
           if (V.digit(pre, k) != 0) fail(HEXO_E_INTERNAL, "a legal action cell is occupied");
           int dc = V.dec[pre][k];
@@ -702,6 +719,243 @@ int32_t guarded(char* err, int64_t len, F&& fn) {
   }
 }
 
+// ------------------------------------------------------------- wire format
+//
+// One live position as the versioned worker-to-batcher item of
+// encoder.rs:539-621 (every integer little-endian):
+//   magic "MANTIS\0\1", version u32, moves_remaining u8, 3 zero bytes,
+//   counts u32 x 7 (stones, windows, incidences, legal, decoder, radius,
+//   adjacency), then the per-position arrays in the order written below.
+
+constexpr uint8_t kWireMagic[8] = {'M', 'A', 'N', 'T', 'I', 'S', 0, 1};
+constexpr int64_t kWireHeader = 8 + 4 + 4 + 7 * 4;
+constexpr uint32_t kReprVersion = 9;
+
+struct WireOut {
+  std::vector<uint8_t>& b;
+  template <typename T>
+  void put(T v) {
+    uint8_t raw[sizeof(T)];
+    std::memcpy(raw, &v, sizeof(T));  // little-endian host (x86-64, gfx hosts)
+    b.insert(b.end(), raw, raw + sizeof(T));
+  }
+  template <typename T>
+  void put_all(const std::vector<T>& v) {
+    for (const T& x : v) put(x);
+  }
+};
+
+// payload bytes after the header, or -1 on overflow
+int64_t wire_payload(int64_t s, int64_t w, int64_t inc, int64_t l, int64_t d, int64_t r, int64_t a) {
+  const int64_t n8 = s + 3 * w + w + 3 * inc + 3 * d + l + 5 * r + 3 * a + 3 * kRowsPerCell * l;
+  if (n8 < 0 || n8 > (int64_t(1) << 58)) return -1;
+  return 8 * n8 + 8 * s + 4 * int64_t(kTactical) * l;
+}
+
+void encode(const Graph& g, std::vector<uint8_t>& out) {
+  const int64_t counts[7] = {g.n_s, g.n_w, int64_t(g.inc_stone.size()), g.n_l, int64_t(g.dec_cell.size()),
+                             int64_t(g.radius_src.size()), int64_t(g.adj_src.size())};
+  for (int64_t c : counts)
+    if (c > int64_t(UINT32_MAX)) fail(HEXO_E_LIMIT, "a wire count exceeds u32");
+  out.reserve(out.size() + size_t(kWireHeader + wire_payload(counts[0], counts[1], counts[2], counts[3], counts[4],
+                                                             counts[5], counts[6])));
+  WireOut o{out};
+  out.insert(out.end(), kWireMagic, kWireMagic + 8);
+  o.put(kReprVersion);
+  o.put(uint8_t(g.moves_remaining));
+  o.put(uint8_t(0)), o.put(uint8_t(0)), o.put(uint8_t(0));
+  for (int64_t c : counts) o.put(uint32_t(c));
+  o.put_all(g.stone_own);
+  for (int64_t i = 0; i < g.n_s; ++i) o.put(int32_t(g.stone_q[size_t(i)])), o.put(int32_t(g.stone_r[size_t(i)]));
+  o.put_all(g.window_feat);
+  o.put_all(g.window_id);
+  o.put_all(g.inc_stone), o.put_all(g.inc_window), o.put_all(g.inc_class);
+  o.put_all(g.dec_cell), o.put_all(g.dec_window), o.put_all(g.dec_class);
+  o.put_all(g.cell_nearest);
+  o.put_all(g.radius_src), o.put_all(g.radius_dst), o.put_all(g.radius_orbit), o.put_all(g.radius_own),
+      o.put_all(g.radius_on_axis);
+  o.put_all(g.adj_src), o.put_all(g.adj_dst), o.put_all(g.adj_axis);
+  o.put_all(g.action_window), o.put_all(g.action_post1), o.put_all(g.action_status);
+  o.put_all(g.tactical);
+}
+
+struct WireIn {
+  const uint8_t* p;
+  int64_t n, at = 0;
+  template <typename T>
+  T get(const char* field) {
+    if (n - at < int64_t(sizeof(T))) fail(HEXO_E_WIRE, std::string("truncated payload at ") + field);
+    T v;
+    std::memcpy(&v, p + at, sizeof(T));
+    at += int64_t(sizeof(T));
+    return v;
+  }
+  std::vector<int64_t> vec(int64_t count, const char* field) {
+    std::vector<int64_t> v(static_cast<size_t>(count));
+    for (auto& x : v) x = get<int64_t>(field);
+    return v;
+  }
+};
+
+[[noreturn]] void wire_fail(const std::string& msg) { fail(HEXO_E_WIRE, msg); }
+
+std::string feature_error(const char* field, size_t i, int64_t v) {
+  return std::string(field) + "[" + std::to_string(i) + "] has invalid feature " + std::to_string(v);
+}
+
+void check_range(const std::vector<int64_t>& v, int64_t lo, int64_t hi, const char* field) {
+  for (size_t i = 0; i < v.size(); ++i)
+    if (v[i] < lo || v[i] >= hi) wire_fail(feature_error(field, i, v[i]));
+}
+
+void check_index(const std::vector<int64_t>& v, int64_t upper, const char* field) {
+  for (size_t i = 0; i < v.size(); ++i)
+    if (v[i] < 0 || v[i] >= upper)
+      wire_fail(std::string(field) + "[" + std::to_string(i) + "] index " + std::to_string(v[i]) +
+                " is outside 0.." + std::to_string(upper));
+}
+
+// Parse and validate one item (the checks and their order of encoder.rs:666-941)
+// into the graph build() would have produced.
+Graph decode(const uint8_t* bytes, int64_t len) {
+  const Vocab& V = vocab();
+  WireIn in{bytes, len};
+  if (len < 8 || std::memcmp(bytes, kWireMagic, 8) != 0) wire_fail("wrong magic");
+  in.at = 8;
+  const uint32_t version = in.get<uint32_t>("MODEL_REPR_VERSION");
+  if (version != kReprVersion)
+    wire_fail("MODEL_REPR_VERSION " + std::to_string(version) + " does not match " + std::to_string(kReprVersion));
+  Graph g;
+  const uint8_t mr = in.get<uint8_t>("moves_remaining");
+  if (mr != 1 && mr != 2) wire_fail("moves_remaining must be 1 or 2, got " + std::to_string(mr));
+  g.moves_remaining = mr;
+  for (int i = 0; i < 3; ++i)
+    if (in.get<uint8_t>("reserved bytes") != 0) wire_fail("reserved bytes are nonzero");
+  const char* names[7] = {"stones", "windows", "incidences", "legal cells", "decoder incidences", "radius edges",
+                          "adjacency edges"};
+  int64_t c[7];
+  for (int i = 0; i < 7; ++i) {
+    c[i] = int64_t(in.get<uint32_t>(names[i]));
+    // every count is capped at the item length before anything is sized by it
+    if (c[i] > len)
+      wire_fail(std::string(names[i]) + " count " + std::to_string(c[i]) + " exceeds item length " +
+                std::to_string(len));
+  }
+  const int64_t S = c[0], W = c[1], I = c[2], L = c[3], D = c[4], R = c[5], A = c[6];
+  if (L == 0) wire_fail("a live position must have a legal cell");
+  const int64_t payload = wire_payload(S, W, I, L, D, R, A);
+  if (payload < 0) wire_fail("payload length overflows");
+  const int64_t expected = kWireHeader + payload;
+  if (len < expected)
+    wire_fail("truncated payload: header describes " + std::to_string(expected) + " bytes, got " +
+              std::to_string(len));
+  if (len > expected)
+    wire_fail("trailing bytes: header describes " + std::to_string(expected) + " bytes, got " + std::to_string(len));
+  g.n_s = S, g.n_w = W, g.n_l = L;
+
+  g.stone_own = in.vec(S, "stone_own");
+  check_range(g.stone_own, 0, 2, "stone_own");
+  g.stone_q.resize(size_t(S)), g.stone_r.resize(size_t(S));
+  for (int64_t i = 0; i < S; ++i) {
+    const int32_t q = in.get<int32_t>("stone_qr.q"), r = in.get<int32_t>("stone_qr.r");
+    if (q < INT16_MIN || q > INT16_MAX)
+      wire_fail("stone_qr[" + std::to_string(i) + "].q is out of range: " + std::to_string(q));
+    if (r < INT16_MIN || r > INT16_MAX)
+      wire_fail("stone_qr[" + std::to_string(i) + "].r is out of range: " + std::to_string(r));
+    if (std::abs(q) > kCoordLimit || std::abs(r) > kCoordLimit || std::abs(q + r) > kCoordLimit)
+      wire_fail("stone_qr[" + std::to_string(i) + "] is not a valid engine coordinate: (" + std::to_string(q) +
+                ", " + std::to_string(r) + ")");
+    g.stone_q[size_t(i)] = q, g.stone_r[size_t(i)] = r;
+  }
+  g.window_feat = in.vec(W, "window_feat");
+  check_range(g.window_feat, 0, kTernPatterns, "window_feat");
+  g.window_id = in.vec(3 * W, "window_id");
+  for (int64_t w = 0; w < W; ++w)
+    if (g.window_id[size_t(3 * w)] < 0 || g.window_id[size_t(3 * w)] > 2)
+      wire_fail(feature_error("window_id", size_t(w), g.window_id[size_t(3 * w)]));
+  g.inc_stone = in.vec(I, "inc_stone");
+  g.inc_window = in.vec(I, "inc_window");
+  g.inc_class = in.vec(I, "inc_class");
+  check_index(g.inc_stone, S, "inc_stone");
+  check_index(g.inc_window, W, "inc_window");
+  check_range(g.inc_class, 0, kTernOcc, "inc_class");
+  g.dec_cell = in.vec(D, "dec_cell");
+  g.dec_window = in.vec(D, "dec_window");
+  g.dec_class = in.vec(D, "dec_class");
+  check_index(g.dec_cell, L, "dec_cell");
+  check_index(g.dec_window, W, "dec_window");
+  check_range(g.dec_class, 0, kTernDec, "dec_class");
+  g.cell_nearest = in.vec(L, "cell_nearest");
+  check_range(g.cell_nearest, 0, kRadius + 2, "cell_nearest");
+  g.radius_src = in.vec(R, "radius_src");
+  g.radius_dst = in.vec(R, "radius_dst");
+  g.radius_orbit = in.vec(R, "radius_orbit");
+  g.radius_own = in.vec(R, "radius_own");
+  g.radius_on_axis = in.vec(R, "radius_on_axis");
+  check_index(g.radius_src, S, "radius_src");
+  check_index(g.radius_dst, L, "radius_dst");
+  check_range(g.radius_orbit, 0, 48, "radius_orbit");
+  check_range(g.radius_own, 0, 2, "radius_own");
+  check_range(g.radius_on_axis, 0, 2, "radius_on_axis");
+  g.adj_src = in.vec(A, "adjacency_src");
+  g.adj_dst = in.vec(A, "adjacency_dst");
+  g.adj_axis = in.vec(A, "adjacency_axis");
+  check_index(g.adj_src, L, "adjacency_src");
+  check_index(g.adj_dst, L, "adjacency_dst");
+  check_range(g.adj_axis, 0, 3, "adjacency_axis");
+  g.action_window = in.vec(kRowsPerCell * L, "action_window_index");
+  g.action_post1 = in.vec(kRowsPerCell * L, "action_post1_class");
+  g.action_status = in.vec(kRowsPerCell * L, "action_pre_status");
+  check_range(g.action_post1, 0, kTernPost1, "action_post1_class");
+  // the kept rows, in order, are exactly the decoder incidences
+  size_t edge = 0;
+  for (size_t f = 0; f < g.action_window.size(); ++f) {
+    const int64_t st = g.action_status[f], w = g.action_window[f];
+    if (st < kStatusOwn || st > kStatusMixed) wire_fail(feature_error("action_pre_status", f, st));
+    const bool kept = st != kStatusEmpty;
+    if (kept != (w >= 0) || w >= W)
+      wire_fail("action_window_index[" + std::to_string(f) + "]=" + std::to_string(w) + " disagrees with status " +
+                std::to_string(st));
+    if (kept) {
+      if (edge >= g.dec_cell.size() || g.dec_cell[edge] != int64_t(f / kRowsPerCell) || g.dec_window[edge] != w)
+        wire_fail("action row " + std::to_string(f) + " disagrees with decoder incidence " + std::to_string(edge));
+      ++edge;
+    }
+  }
+  if (edge != g.dec_cell.size())
+    wire_fail(std::to_string(edge) + " kept action rows do not match " + std::to_string(g.dec_cell.size()) +
+              " decoder incidences");
+  g.tactical.resize(size_t(kTactical * L));
+  for (size_t i = 0; i < g.tactical.size(); ++i) {
+    const float v = in.get<float>("action_tactical");
+    if (!std::isfinite(v) || v < 0.f || v > 1.f)
+      wire_fail("action_tactical[" + std::to_string(i) + "] must be a finite value in [0, 1], got " +
+                std::to_string(v));
+    g.tactical[i] = v;
+  }
+  // the last tactical column is the nonempty-row fraction: demand bit equality
+  for (int64_t j = 0; j < L; ++j) {
+    int nonempty = 0;
+    for (int k = 0; k < kRowsPerCell; ++k) nonempty += g.action_status[size_t(j * kRowsPerCell + k)] != kStatusEmpty;
+    const float want = float(nonempty) / 18.f, got = g.tactical[size_t(j * kTactical + kTactical - 1)];
+    if (std::memcmp(&want, &got, sizeof(float)) != 0)
+      wire_fail("action_tactical[" + std::to_string(j) + "] nonempty column disagrees with the row statuses");
+  }
+  // the collated action fields: kept rows' classes, EMPTY rows per slot orbit
+  g.act_empty.assign(size_t(3 * L), 0);
+  for (size_t f = 0; f < g.action_status.size(); ++f) {
+    const int k = int(f % kRowsPerCell) % kWin;
+    if (g.action_status[f] == kStatusEmpty) ++g.act_empty[size_t(3 * int64_t(f / kRowsPerCell) + std::min(k, kWin - 1 - k))];
+    else g.act_class.push_back(g.action_post1[f]);
+  }
+  std::vector<int64_t> start(size_t(W) + 1, 0);
+  for (int64_t w : g.dec_window) ++start[size_t(w) + 1];
+  for (int64_t w = 0; w < W; ++w) start[size_t(w) + 1] += start[size_t(w)];
+  g.act_rev_local.resize(g.dec_window.size());
+  for (size_t e = 0; e < g.dec_window.size(); ++e) g.act_rev_local[size_t(start[size_t(g.dec_window[e])]++)] = int64_t(e);
+  return g;
+}
+
 }  // namespace
 
 extern "C" {
@@ -882,6 +1136,41 @@ int32_t hexo_tables(int32_t* rank, int32_t* dec, int32_t* occ, int32_t* post1, i
     if (orbit)
       for (int i = 0; i < 625; ++i) orbit[i] = V.orbit[i / 25][i % 25];
     if (pattern_counts) std::copy(V.counts.begin(), V.counts.end(), pattern_counts);
+  });
+}
+
+int32_t hexo_encode_position(int64_t n_moves, const int16_t* moves_qr, uint8_t* out, int64_t cap, int64_t* len,
+                             char* err, int64_t err_len) {
+  return guarded(err, err_len, [&] {
+    if (!len || n_moves < 0 || (n_moves > 0 && !moves_qr) || cap < 0 || (cap > 0 && !out))
+      fail(HEXO_E_ARG, "null argument or negative size");
+    std::vector<uint8_t> bytes;
+    encode(build(replay(moves_qr, n_moves)), bytes);
+    *len = int64_t(bytes.size());
+    if (cap >= *len) std::memcpy(out, bytes.data(), bytes.size());
+    else if (cap > 0) fail(HEXO_E_ARG, "output buffer of " + std::to_string(cap) + " bytes holds less than the " +
+                                       std::to_string(*len) + "-byte item");
+  });
+}
+
+int32_t hexo_decode_batch(int64_t n_items, const uint8_t* bytes, const int64_t* item_offsets, int32_t n_threads,
+                          HexoBatch** out, char* err, int64_t err_len) {
+  return guarded(err, err_len, [&] {
+    if (!out || n_items <= 0 || !item_offsets || !bytes) fail(HEXO_E_ARG, "empty batch or null argument");
+    *out = nullptr;
+    for (int64_t i = 0; i < n_items; ++i)
+      if (item_offsets[i] < 0 || item_offsets[i + 1] < item_offsets[i])
+        fail(HEXO_E_ARG, "item offsets must be non-negative and ascending");
+    (void)vocab();
+    std::vector<Graph> graphs(static_cast<size_t>(n_items));
+    parallel_for(n_items, n_threads, [&](int64_t i) {
+      try {
+        graphs[size_t(i)] = decode(bytes + item_offsets[i], item_offsets[i + 1] - item_offsets[i]);
+      } catch (const Failure& f) {
+        fail(f.code, "item " + std::to_string(i) + ": " + f.what());
+      }
+    });
+    *out = collate(graphs, n_threads);
   });
 }
 

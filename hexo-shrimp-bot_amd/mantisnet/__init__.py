@@ -16,6 +16,8 @@ from .builder import (
     build_batch_prefixes,
     collate_positions,
     collate_prefixes,
+    decode_batch,
+    encode_position,
 )
 from .model import PRODUCTION, MantisConfig, MantisNet, ModelOutput, compose_acting_q, compose_q
 from . import library  # noqa: E402,F401  registers the mantisnet:: operators
@@ -30,6 +32,8 @@ __all__ = [
     "build_batch_prefixes",
     "collate_positions",
     "collate_prefixes",
+    "decode_batch",
+    "encode_position",
     "MantisConfig",
     "MantisNet",
     "ModelOutput",

@@ -75,6 +75,12 @@ def encoder() -> ctypes.CDLL:
         lib.hexo_random_game.restype = ctypes.c_int32
         lib.hexo_tables.argtypes = [c_i32p, c_i32p, c_i32p, c_i32p, c_i32p, c_f32p]
         lib.hexo_tables.restype = ctypes.c_int32
+        lib.hexo_encode_position.argtypes = [ctypes.c_int64, c_i16p, vp, ctypes.c_int64, c_i64p, ctypes.c_char_p,
+                                             ctypes.c_int64]
+        lib.hexo_encode_position.restype = ctypes.c_int32
+        lib.hexo_decode_batch.argtypes = [ctypes.c_int64, vp, c_i64p, ctypes.c_int32, ctypes.POINTER(vp),
+                                          ctypes.c_char_p, ctypes.c_int64]
+        lib.hexo_decode_batch.restype = ctypes.c_int32
         _encoder = lib
     return _encoder
 
@@ -91,7 +97,7 @@ def hip() -> ctypes.CDLL:
 def check(status: int, err: ctypes.Array | None = None, what: str = "") -> None:
     if status != 0:
         detail = err.value.decode(errors="replace") if err is not None else ""
-        if status in (1, 2, 3):
+        if status in (1, 2, 3, 6):  # bad arguments, illegal move, terminal position, invalid wire item
             raise ValueError(f"{what}: {detail}" if what else detail)
         raise NativeError(f"{what} failed with status {status}: {detail}")
 

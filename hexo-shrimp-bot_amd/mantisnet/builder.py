@@ -203,6 +203,11 @@ def build_batch_prefixes(games, ts, threads: int = 0, with_relay: bool = True) -
         ),
         err, "build_batch",
     )
+    return _take_arrays(lib, handle, with_relay)
+
+
+def _take_arrays(lib, handle, with_relay: bool) -> dict:
+    """The collated arrays of a native batch handle (copied), then free it."""
     try:
         sc = [ctypes.c_int64() for _ in range(4)]
         lib.hexo_batch_scalars(handle, *(ctypes.byref(x) for x in sc))
@@ -229,6 +234,39 @@ def build_batch_prefixes(games, ts, threads: int = 0, with_relay: bool = True) -
         return out
     finally:
         lib.hexo_batch_free(handle)
+
+
+def encode_position(moves) -> bytes:
+    """The versioned wire item of the live position after ``moves``
+    (encoder.rs:539-621; the worker side of seam.rs:15)."""
+    mv = np.ascontiguousarray(np.asarray(moves, np.int16).reshape(-1, 2))
+    lib = N.encoder()
+    err = N.errbuf()
+    length = ctypes.c_int64()
+    N.check(lib.hexo_encode_position(len(mv), mv.ctypes.data_as(N.c_i16p), None, 0, ctypes.byref(length), err,
+                                     len(err)), err, "encode_position")
+    buf = (ctypes.c_uint8 * length.value)()
+    N.check(lib.hexo_encode_position(len(mv), mv.ctypes.data_as(N.c_i16p), buf, length.value, ctypes.byref(length),
+                                     err, len(err)), err, "encode_position")
+    return bytes(buf)
+
+
+def decode_batch(items, threads: int = 0, with_relay: bool = True) -> Batch:
+    """Validate wire items and collate them into one Batch
+    (encoder.rs:1632-1639; the batcher side of seam.rs:83).  A malformed item
+    raises ValueError naming the item and the failed check."""
+    items = [bytes(x) for x in items]
+    if not items:
+        raise ValueError("decode_batch needs at least one item")
+    offsets = np.zeros(len(items) + 1, np.int64)
+    offsets[1:] = np.cumsum([len(x) for x in items])
+    blob = np.frombuffer(b"".join(items) or b"\0", dtype=np.uint8)
+    lib = N.encoder()
+    handle = ctypes.c_void_p()
+    err = N.errbuf()
+    N.check(lib.hexo_decode_batch(len(items), blob.ctypes.data, offsets.ctypes.data_as(N.c_i64p), int(threads),
+                                  ctypes.byref(handle), err, len(err)), err, "decode_batch")
+    return _as_batch(_take_arrays(lib, handle, with_relay))
 
 
 def _as_batch(arrays: dict) -> Batch:

@@ -24,6 +24,7 @@ extern "C" {
 #define HEXO_E_TERMINAL 3 /* a terminal position was handed to the builder */
 #define HEXO_E_LIMIT 4    /* a representation limit was exceeded */
 #define HEXO_E_INTERNAL 5 /* an encoder invariant failed */
+#define HEXO_E_WIRE 6     /* a wire item failed validation */
 
 /* Field dtypes reported by hexo_batch_field. */
 #define HEXO_I64 1
@@ -53,6 +54,32 @@ int32_t hexo_build_batch_prefixes(int64_t n_games, const int16_t* moves_qr,
                                   const int64_t* move_offsets, const int64_t* ts,
                                   int32_t n_threads, HexoBatch** out, char* err,
                                   int64_t err_len);
+
+/*
+ * One live position as the versioned worker-to-batcher wire item
+ * (encoder.rs:539-621: magic "MANTIS\0\1", MODEL_REPR_VERSION, the side's
+ * remaining placements, seven u32 counts, then the position's graph arrays,
+ * little-endian).  Replays n_moves placements, builds, and writes the item
+ * into `out` when `cap` holds it; *len always receives the item's length
+ * (call with cap = 0 to size the buffer).  Replaces encoder::encode_position
+ * (used by seam.rs:15).
+ */
+int32_t hexo_encode_position(int64_t n_moves, const int16_t* moves_qr, uint8_t* out, int64_t cap,
+                             int64_t* len, char* err, int64_t err_len);
+
+/*
+ * Validate and collate n_items wire items (item i = bytes[item_offsets[i] ..
+ * item_offsets[i+1])) into one batch, as hexo_build_batch_prefixes does for
+ * replayed games.  Every check of encoder.rs:666-941 runs before collation
+ * (magic, version, remaining placements, reserved bytes, counts capped at the
+ * item length, exact length, every feature's domain and index bound, the
+ * action rows against the decoder incidences, the tactical range and its
+ * nonempty column); the first failure returns HEXO_E_WIRE with the item and
+ * the reason in `err`.  Replaces encoder::decode_batch (encoder.rs:1632-1639,
+ * used by seam.rs:83).
+ */
+int32_t hexo_decode_batch(int64_t n_items, const uint8_t* bytes, const int64_t* item_offsets,
+                          int32_t n_threads, HexoBatch** out, char* err, int64_t err_len);
 
 /* The batch's scalar sizes (builder.py:666-700: n_pos, max_t, max_w, n_cells). */
 int32_t hexo_batch_scalars(const HexoBatch* batch, int64_t* n_pos, int64_t* max_t,
