@@ -171,7 +171,7 @@ __global__ void __launch_bounds__(kThreads) attn_substage_kernel(SubArgs a) {
     }
     float xv[4][8];
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) load8(a.x + rc * a.ldx + 32 * ks + 8 * g, xv[ks]);
+    for (int ks = 0; ks < 4; ++ks) load8_nt(a.x + rc * a.ldx + 32 * ks + 8 * g, xv[ks]);
     int64_t lo[kStages], hi[kStages];
 #pragma unroll
     for (int s = 0; s < kStages; ++s) {
@@ -345,7 +345,7 @@ __global__ void __launch_bounds__(kThreads) attn_substage_kernel(SubArgs a) {
     }
     if (live) {
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) store8(a.x + row * a.ldx + 32 * ks + 8 * g, xv[ks]);
+      for (int ks = 0; ks < 4; ++ks) store8_nt(a.x + row * a.ldx + 32 * ks + 8 * g, xv[ks]);
     }
   }
 }

@@ -83,6 +83,21 @@ __device__ __forceinline__ void load8(const float* p, float (&x)[8]) {
   x[4] = b.x, x[5] = b.y, x[6] = b.z, x[7] = b.w;
 }
 
+// Streaming (non-temporal) forms for rows that are read or written once per
+// pass: they are kept from displacing the gathered rows other lanes reuse in L2.
+typedef float nt_f32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void load8_nt(const float* p, float (&x)[8]) {
+  const nt_f32x4_t a = __builtin_nontemporal_load(reinterpret_cast<const nt_f32x4_t*>(p));
+  const nt_f32x4_t b = __builtin_nontemporal_load(reinterpret_cast<const nt_f32x4_t*>(p) + 1);
+  x[0] = a.x, x[1] = a.y, x[2] = a.z, x[3] = a.w;
+  x[4] = b.x, x[5] = b.y, x[6] = b.z, x[7] = b.w;
+}
+
+__device__ __forceinline__ void store8_nt(float* p, const float (&x)[8]) {
+  __builtin_nontemporal_store(nt_f32x4_t{x[0], x[1], x[2], x[3]}, reinterpret_cast<nt_f32x4_t*>(p));
+  __builtin_nontemporal_store(nt_f32x4_t{x[4], x[5], x[6], x[7]}, reinterpret_cast<nt_f32x4_t*>(p) + 1);
+}
+
 __device__ __forceinline__ void store8(float* p, const float (&x)[8]) {
   reinterpret_cast<float4*>(p)[0] = make_float4(x[0], x[1], x[2], x[3]);
   reinterpret_cast<float4*>(p)[1] = make_float4(x[4], x[5], x[6], x[7]);

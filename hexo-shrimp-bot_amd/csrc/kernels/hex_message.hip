@@ -59,22 +59,26 @@ __global__ void hex_neighbours_kernel(const int32_t* __restrict__ qr,
 //
 // Gather: the wavefront works in row layout — 16 lanes per cell, 8 dims per
 // lane — so every 16-byte load of a neighbour row is part of a 256-byte
-// contiguous row read (4 full rows per load instruction).  All 24 loads of
-// the tile (4 passes x 6 neighbours) are issued before any is consumed;
-// a missing neighbour reads the cell's own row and is masked in the fp32
-// sum.  The sums go to LDS as bf16, where the MFMA B fragments of sum^T are
-// read back (lane = cell l16, dims 32ks + 8g .. +8).
+// contiguous row read (4 full rows per load instruction).  The tile's 96
+// neighbour indices arrive with two coalesced loads and reach their lanes by
+// shuffles; all 24 row loads of the tile (4 passes x 6 neighbours) are
+// issued before any is consumed; a missing neighbour reads the cell's own
+// row and is masked in the fp32 sum.  The sums go to LDS as bf16, where the
+// MFMA B fragments of sum^T are read back (lane = cell l16, dims 32ks + 8g).
 //
 // Product: y^T (16 outs x 16 cells) = W (16 x 128) . sum^T (128 x 16), one
 // per output tile, serves both outputs by linearity:
 //   out_sum = y + b,   out_mean = y / count + b   (0 neighbours: b).
-// LDS rows are padded to 272 bytes so the 16 rows of a fragment read fall in
-// distinct banks.  HBM traffic is the compulsory minimum (x once, the table
-// once, both outputs once); repeated neighbour reads hit L2/MALL.
+// W is staged in LDS once per 4-wavefront workgroup; its loads are issued
+// before the neighbour indices so the two round trips overlap.  LDS rows are
+// padded to 272 bytes so the 16 rows of a fragment read fall in distinct
+// banks.  HBM traffic is the compulsory minimum (x once, the table once,
+// both outputs once); repeated neighbour reads hit L2/MALL.
 constexpr int kPitch = kDim + 8;  // bf16 per staged LDS row
 constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * 64;
 
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(kThreads)
 hex_aggregate_linear_kernel(const uint16_t* __restrict__ x, const int32_t* __restrict__ nbr,
                             int64_t n_cells, const uint16_t* __restrict__ w,
                             const float* __restrict__ bias, uint16_t* __restrict__ out_sum,
@@ -84,16 +88,34 @@ hex_aggregate_linear_kernel(const uint16_t* __restrict__ x, const int32_t* __res
   __shared__ float scount[kWaves][16];
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
   const int64_t c0 = (int64_t(blockIdx.x) * kWaves + wave) * 16;
+  // ---- W: requested first (4 x 16 bytes per thread), stored once it lands
+  uint4 wst[kDim * kDim / 8 / kThreads];
+#pragma unroll
+  for (int u = 0; u < kDim * kDim / 8 / kThreads; ++u)
+    wst[u] = *reinterpret_cast<const uint4*>(w + 8 * (threadIdx.x + u * kThreads));
+  // ---- the tile's 16 x 6 neighbour indices: lanes 0..63 and 0..31 of two loads
+  const int64_t n_idx = 6 * n_cells;
+  const int64_t i0 = 6 * c0 + lane, i1 = 6 * c0 + 64 + lane;
+  const int32_t v0 = i0 < n_idx ? nbr[i0] : -1;
+  const int32_t v1 = (lane < 32 && i1 < n_idx) ? nbr[i1] : -1;
+#pragma unroll
+  for (int u = 0; u < kDim * kDim / 8 / kThreads; ++u) {
+    const int i = threadIdx.x + u * kThreads;
+    const int r = i / (kDim / 8), c = i % (kDim / 8);
+    *reinterpret_cast<uint4*>(sw + r * kPitch + 8 * c) = wst[u];
+  }
   // ---- gather in row layout: pass p covers cells c0 + 4p + lane/16
   {
     const int sub = lane / 16, d8 = (lane % 16) * 8;
     int32_t js[4][6];
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const int64_t cell = c0 + 4 * p + sub;
+    for (int p = 0; p < 4; ++p)
 #pragma unroll
-      for (int s = 0; s < 6; ++s) js[p][s] = cell < n_cells ? nbr[cell * 6 + s] : -1;
-    }
+      for (int s = 0; s < 6; ++s) {
+        const int k = 6 * (4 * p + sub) + s;  // index slot within the tile, 0..95
+        const int32_t a = __shfl(v0, k & 63), b = __shfl(v1, k & 31);
+        js[p][s] = k < 64 ? a : b;
+      }
     uint4 raw[4][6];
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
@@ -131,10 +153,6 @@ hex_aggregate_linear_kernel(const uint16_t* __restrict__ x, const int32_t* __res
       *reinterpret_cast<uint4*>(&sagg[wave][(4 * p + sub) * kPitch + d8]) = packed;
       if (lane % 16 == 0) scount[wave][4 * p + sub] = float(present);
     }
-  }
-  for (int i = threadIdx.x; i < kDim * kDim / 8; i += kWaves * 64) {
-    const int r = i / (kDim / 8), c = i % (kDim / 8);
-    *reinterpret_cast<uint4*>(sw + r * kPitch + 8 * c) = *reinterpret_cast<const uint4*>(w + r * kDim + 8 * c);
   }
   __syncthreads();
   if (c0 >= n_cells) return;
@@ -195,7 +213,7 @@ int32_t mantis_hex_aggregate_linear(const void* x, const int32_t* nbr, int64_t n
   if (!aligned16(x) || !aligned16(w) || !aligned16(b) || !aligned16(out_sum) || !aligned16(out_mean))
     return MANTIS_E_ARG;
   const int64_t blocks = (n_cells + 16 * kWaves - 1) / (16 * kWaves);
-  hex_aggregate_linear_kernel<<<unsigned(blocks), kWaves * 64, 0, as_stream(stream)>>>(
+  hex_aggregate_linear_kernel<<<unsigned(blocks), kThreads, 0, as_stream(stream)>>>(
       static_cast<const uint16_t*>(x), nbr, n_cells, static_cast<const uint16_t*>(w), b,
       static_cast<uint16_t*>(out_sum), static_cast<uint16_t*>(out_mean), err_flag);
   return launched();
