@@ -245,17 +245,39 @@ latent_read_kernel(const Tin* __restrict__ q, const Tin* __restrict__ k,
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[s][i] = 0.f;
   }
-  for (int64_t i = a + group; i < b; i += kGroupsPerBlock) {
-    const int64_t w = order[i];
-    if (w < 0 || w >= n_w) {
-      raise_flag(flag, MANTIS_FLAG_INDEX);
-      continue;
-    }
-    float kv[8], vv[8];
-    load8(k + w * ldk + lane * 8, kv);
-    load8(v + w * ldv + lane * 8, vv);
+  // Four windows per group are in flight at once, and the order entries of
+  // the next four are requested under them (unconditionally, from a clamped
+  // slot, and checked where they are used).
+  constexpr int kLook = 4;
+  int64_t wr[kLook];
+  auto fetch = [&](int64_t base) {
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
+    for (int u = 0; u < kLook; ++u) {
+      const int64_t i = base + int64_t(u) * kGroupsPerBlock;
+      wr[u] = order[i < b ? i : a];
+    }
+  };
+  if (a < b) fetch(a + group);
+  for (int64_t base = a + group; base < b; base += kLook * kGroupsPerBlock) {
+    float kvs[kLook][8], vvs[kLook][8];
+    bool ok[kLook];
+#pragma unroll
+    for (int u = 0; u < kLook; ++u) {
+      const bool in = base + int64_t(u) * kGroupsPerBlock < b;
+      ok[u] = in && wr[u] >= 0 && wr[u] < n_w;
+      if (in && !ok[u]) raise_flag(flag, MANTIS_FLAG_INDEX);
+      const int64_t w = ok[u] ? wr[u] : 0;
+      load8(k + w * ldk + lane * 8, kvs[u]);
+      load8(v + w * ldv + lane * 8, vvs[u]);
+    }
+    if (base + kLook * kGroupsPerBlock < b) fetch(base + kLook * kGroupsPerBlock);
+#pragma unroll
+    for (int u = 0; u < kLook; ++u) {
+      if (!ok[u]) continue;
+      const float (&kv)[8] = kvs[u];
+      const float (&vv)[8] = vvs[u];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
       float dot = 0.f;
 #pragma unroll
       for (int j = 0; j < 8; ++j) dot = fmaf(qv[s][j], kv[j], dot);
@@ -267,6 +289,7 @@ latent_read_kernel(const Tin* __restrict__ q, const Tin* __restrict__ k,
 #pragma unroll
       for (int j = 0; j < 8; ++j) acc[s][j] = fmaf(p, vv[j], acc[s][j] * alpha);
       m[s] = m_new;
+      }
     }
   }
 #pragma unroll

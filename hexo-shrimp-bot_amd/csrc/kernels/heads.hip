@@ -76,21 +76,36 @@ value_read_kernel(const float* __restrict__ token, const float* __restrict__ row
   int64_t a = offsets[p], b = offsets[p + 1];
   a = a < 0 ? 0 : (a > n_rows ? n_rows : a);
   b = b < a ? a : (b > n_rows ? n_rows : b);
-  // index -1 is the position's token row
-  for (int64_t i = a - 1 + grp; i < b; i += 16) {
-    const float* src;
-    if (i < a) {
-      src = token + p * kRow;
-    } else {
-      const int64_t r = order[i];
-      if (r < 0 || r >= n_rows) {
-        raise_flag(flag, MANTIS_FLAG_INDEX);
-        continue;
-      }
-      src = rows + r * kRow;
+  // index -1 is the position's token row.  Four rows per group are in
+  // flight at once and the order entries of the next four are requested
+  // under them (from a clamped slot, checked where they are used).
+  constexpr int kLook = 4;
+  int64_t rr[kLook];
+  auto fetch = [&](int64_t base) {  // only called with windows present (a < b)
+#pragma unroll
+    for (int u = 0; u < kLook; ++u) {
+      const int64_t i = base + 16 * u;
+      rr[u] = order[i < a ? a : (i >= b ? b - 1 : i)];
     }
-    float v[8];
-    load8(src + lane * 8, v);
+  };
+  for (int u = 0; u < kLook; ++u) rr[u] = -1;
+  if (a < b) fetch(a - 1 + grp);
+  for (int64_t base = a - 1 + grp; base < b; base += 16 * kLook) {
+    float vs[kLook][8];
+    bool ok[kLook];
+#pragma unroll
+    for (int u = 0; u < kLook; ++u) {
+      const int64_t i = base + 16 * u;
+      const bool tok = i < a, in = i < b;
+      ok[u] = in && (tok || (rr[u] >= 0 && rr[u] < n_rows));
+      if (in && !ok[u]) raise_flag(flag, MANTIS_FLAG_INDEX);
+      load8((tok || !ok[u] ? token + p * kRow : rows + rr[u] * kRow) + lane * 8, vs[u]);
+    }
+    if (base + 16 * kLook < b) fetch(base + 16 * kLook);  // implies a < b
+#pragma unroll
+    for (int u = 0; u < kLook; ++u) {
+    if (!ok[u]) continue;
+    float (&v)[8] = vs[u];
     float s = 0.f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) s += v[j];
@@ -116,6 +131,7 @@ value_read_kernel(const float* __restrict__ token, const float* __restrict__ row
 #pragma unroll
       for (int j = 0; j < 8; ++j) acc[q][j] = fmaf(pr, v[j], acc[q][j] * al);
       m[q] = mn;
+    }
     }
   }
 #pragma unroll
