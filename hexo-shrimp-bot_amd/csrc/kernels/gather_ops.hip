@@ -53,20 +53,41 @@ run_reduce_kernel(const Tin* __restrict__ values, int64_t n_src, int64_t ld, int
   if (row >= n_dest) return;
   int64_t start, end;
   segment(ptr, row, n_entries, start, end);
-  for (int64_t c0 = int64_t(lane) * 8; c0 < h; c0 += kGroup * 8) {
+  // Up to 16 of the run's source indices at once (one per lane, unconditional
+  // from a clamped slot), shared by shuffles; four source rows in flight.
+  // The sum runs over the entries in order, so it is the same fp32 sum as
+  // one entry at a time.
+  constexpr int kLook = 4;
+  // every lane runs every chunk step (the shuffles need all 16 lanes); a lane
+  // past the row's width only skips its loads and its store
+  for (int64_t cb = 0; cb < h; cb += kGroup * 8) {
+    const int64_t c0 = cb + int64_t(lane) * 8;
+    const bool mine = c0 < h;
     float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int64_t e = start; e < end; ++e) {
-      int64_t s = gather[e];
-      if (s < 0 || s >= n_src) {
-        raise_flag(flag, MANTIS_FLAG_INDEX);
-        continue;
-      }
-      float x[8];
-      load8(values + s * ld + c0, x);
+    for (int64_t base = start; base < end; base += kGroup) {
+      const int cnt = int(end - base < kGroup ? end - base : kGroup);
+      const int64_t my = gather[base + (lane < cnt ? lane : cnt - 1)];
+      const bool mine_ok = my >= 0 && my < n_src;
+      if (lane < cnt && !mine_ok) raise_flag(flag, MANTIS_FLAG_INDEX);
+      const int32_t my32 = mine_ok ? int32_t(my) : -1;  // n_src fits int32 (host check)
+      for (int j = 0; j < cnt; j += kLook) {
+        float x[kLook][8];
+        bool ok[kLook];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i] += x[i];
+        for (int u = 0; u < kLook; ++u) {
+          const int idx = j + u < cnt ? j + u : cnt - 1;
+          const int32_t src = __shfl(my32, idx, kGroup);
+          ok[u] = j + u < cnt && src >= 0;
+          if (mine && ok[u]) load8(values + int64_t(src) * ld + c0, x[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < kLook; ++u)
+          if (mine && ok[u])
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[i] += x[u][i];
+      }
     }
-    store8(out + row * h + c0, acc);
+    if (mine) store8(out + row * h + c0, acc);
   }
 }
 
@@ -485,6 +506,7 @@ int32_t mantis_run_reduce(const void* values, int32_t values_dtype, int64_t n_sr
   if (!values || !ptr || !out || h <= 0 || ld < h || n_dest < 0 || n_src < 0) return MANTIS_E_ARG;
   if (out_dtype < MANTIS_F32 || out_dtype > MANTIS_F16) return MANTIS_E_ARG;
   if (n_entries < 0 || (n_entries > 0 && !gather)) return MANTIS_E_ARG;
+  if (n_src > 2147483647LL) return MANTIS_E_ARG;  // source indices travel as int32
   const bool vec = h % 8 == 0 && ld % 8 == 0 && aligned16(values) && aligned16(out);
   hipStream_t s = as_stream(stream);
   const dim3 grid(grid_rows(n_dest)), block(kBlock);
