@@ -209,6 +209,7 @@ struct Position {
   std::vector<std::array<int, 2>> legal;   // canonical order
   int mover = 0;
   int moves_remaining = 1;
+  int winner = -1;  // set when the last placement completed six (terminal replays only)
 };
 
 inline int mover_after(int64_t ply) { return ply == 0 ? 0 : (((ply - 1) / 2) % 2 == 0 ? 1 : 0); }
@@ -229,7 +230,10 @@ bool completes_six(const Grid<int8_t>& owner, int q, int r, int who) {
 }
 
 // Replay a placement sequence through the rules and return the position.
-Position replay(const int16_t* moves, int64_t n) {
+// A sequence whose last placement completes six is refused unless
+// allow_terminal: then the position is terminal (no legal placements, the
+// winner to move, as the engine freezes it).
+Position replay(const int16_t* moves, int64_t n, bool allow_terminal = false) {
   Position pos;
   int qlo = 0, qhi = 0, rlo = 0, rhi = 0;
   for (int64_t i = 0; i < n; ++i) {
@@ -261,6 +265,15 @@ Position replay(const int16_t* moves, int64_t n) {
     for (int dq = -kRadius; dq <= kRadius; ++dq)
       for (int dr = std::max(-kRadius, -kRadius - dq); dr <= std::min(kRadius, kRadius - dq); ++dr)
         cover.at(q + dq, r + dr) = 1;
+    if (wins && allow_terminal && ply + 1 == n) {
+      pos.winner = who;
+      pos.mover = who;
+      pos.moves_remaining = remaining_after(n);
+      for (int qq = owner.q0; qq < owner.q0 + owner.nq; ++qq)
+        for (int rr = owner.r0; rr < owner.r0 + owner.nr; ++rr)
+          if (owner.at(qq, rr) >= 0) pos.stones.push_back({qq, rr, owner.at(qq, rr)});
+      return pos;
+    }
     if (wins) {
       std::snprintf(msg, sizeof msg, "ply %lld: (%d, %d) ends the game", (long long)ply, q, r);
       fail(ply + 1 == n ? HEXO_E_TERMINAL : HEXO_E_ILLEGAL,
@@ -1171,6 +1184,26 @@ int32_t hexo_decode_batch(int64_t n_items, const uint8_t* bytes, const int64_t* 
       }
     });
     *out = collate(graphs, n_threads);
+  });
+}
+
+int32_t hexo_position_state(int64_t n_moves, const int16_t* moves_qr, int64_t cap, int16_t* legal_qr,
+                            int64_t* n_legal, int32_t* mover, int32_t* moves_remaining, int32_t* winner,
+                            int64_t* n_stones, char* err, int64_t err_len) {
+  return guarded(err, err_len, [&] {
+    if (!n_legal || n_moves < 0 || (n_moves > 0 && !moves_qr) || cap < 0 || (cap > 0 && !legal_qr))
+      fail(HEXO_E_ARG, "null argument or negative size");
+    Position pos = replay(moves_qr, n_moves, true);
+    *n_legal = int64_t(pos.legal.size());
+    if (int64_t(pos.legal.size()) > cap) fail(HEXO_E_ARG, "legal_qr capacity too small");
+    for (size_t i = 0; i < pos.legal.size(); ++i) {
+      legal_qr[2 * i] = int16_t(pos.legal[i][0]);
+      legal_qr[2 * i + 1] = int16_t(pos.legal[i][1]);
+    }
+    if (mover) *mover = pos.mover;
+    if (moves_remaining) *moves_remaining = pos.moves_remaining;
+    if (winner) *winner = pos.winner;
+    if (n_stones) *n_stones = int64_t(pos.stones.size());
   });
 }
 

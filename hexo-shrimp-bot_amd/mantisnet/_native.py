@@ -81,6 +81,9 @@ def encoder() -> ctypes.CDLL:
         lib.hexo_decode_batch.argtypes = [ctypes.c_int64, vp, c_i64p, ctypes.c_int32, ctypes.POINTER(vp),
                                           ctypes.c_char_p, ctypes.c_int64]
         lib.hexo_decode_batch.restype = ctypes.c_int32
+        lib.hexo_position_state.argtypes = [ctypes.c_int64, c_i16p, ctypes.c_int64, c_i16p, c_i64p, c_i32p, c_i32p,
+                                            c_i32p, c_i64p, ctypes.c_char_p, ctypes.c_int64]
+        lib.hexo_position_state.restype = ctypes.c_int32
         _encoder = lib
     return _encoder
 

@@ -56,6 +56,19 @@ int32_t hexo_build_batch_prefixes(int64_t n_games, const int16_t* moves_qr,
                                   int64_t err_len);
 
 /*
+ * The rules state after replaying `n_moves` placements, terminal positions
+ * included (hexo_py.Position, python/hexo-py/src/lib.rs:40-199): the legal
+ * placements in canonical order (none once terminal; up to `cap` pairs
+ * written, the count in *n_legal), the side to move (frozen at the winner
+ * once terminal), the placements it has left this turn, the winner (-1 while
+ * the game runs) and the stone count.  An illegal placement, or one after
+ * the game ended, fails with HEXO_E_ILLEGAL.
+ */
+int32_t hexo_position_state(int64_t n_moves, const int16_t* moves_qr, int64_t cap, int16_t* legal_qr,
+                            int64_t* n_legal, int32_t* mover, int32_t* moves_remaining, int32_t* winner,
+                            int64_t* n_stones, char* err, int64_t err_len);
+
+/*
  * One live position as the versioned worker-to-batcher wire item
  * (encoder.rs:539-621: magic "MANTIS\0\1", MODEL_REPR_VERSION, the side's
  * remaining placements, seven u32 counts, then the position's graph arrays,
