@@ -19,6 +19,11 @@
 // {4g..4g+3, 16+4g..16+4g+3} of each 32-step, matched by the W3 reads).
 // The weights live in LDS for the whole (persistent) workgroup; rows stream
 // from HBM once, the next tile's rows in flight while the current computes.
+// Compensated weights (kSplit): every weight matrix arrives as an fp16 pair
+// [hi; lo] with lo = fp16(W - hi), and every product runs twice (hi, then lo
+// into the same fp32 accumulator), so the weights carry ~22 mantissa bits
+// while the rows stay fp16 operands.  It doubles the weights' LDS and the
+// MFMA work, which row-streaming launches have to spare.
 #include "common.hpp"
 #include "mfma.hpp"
 
@@ -80,12 +85,14 @@ __device__ __forceinline__ void store4(const Args& a, int64_t row, int f, const 
 
 // LDS layout: W1 (N1 rows), W2 (N1 rows, with a second input), W3 (n3 rows
 // of N1 + 8, with a second stage); n3 is a launch parameter.
-template <int N1, bool kStage2, bool kX2>
+// With kSplit each region holds the hi rows, then the lo rows.
+template <int N1, bool kStage2, bool kX2, bool kSplit = false>
 struct Smem {
-  static constexpr int w1 = N1 * kPitch;
-  static constexpr int w2 = kX2 ? N1 * kPitch : 0;
+  static constexpr int kParts = kSplit ? 2 : 1;
+  static constexpr int w1 = kParts * N1 * kPitch;
+  static constexpr int w2 = kX2 ? kParts * N1 * kPitch : 0;
   static constexpr int p3 = N1 + 8;
-  static int bytes(int n3) { return (w1 + w2 + (kStage2 ? n3 * p3 : 0)) * 2; }
+  static int bytes(int n3) { return (w1 + w2 + (kStage2 ? kParts * n3 * p3 : 0)) * 2; }
 };
 
 // Wavefronts sharing one LDS copy of the weights: 8, or 16 for the widest
@@ -94,25 +101,29 @@ struct Smem {
 template <int N1>
 constexpr int threads_for() { return N1 >= 512 ? 1024 : 512; }
 
-template <typename TX, typename TX2, bool kLN, int N1, bool kX2, bool kRelu, bool kStage2, int kMode>
+template <typename TX, typename TX2, bool kLN, int N1, bool kX2, bool kRelu, bool kStage2, int kMode,
+          bool kSplit = false>
 __global__ void __launch_bounds__(threads_for<N1>()) fused_linear_kernel(Args a) {
   constexpr int kTileRows = 16 * (threads_for<N1>() / 64);
+  constexpr int kParts = kSplit ? 2 : 1;
   extern __shared__ __attribute__((aligned(16))) _Float16 smem[];
-  using S = Smem<N1, kStage2, kX2>;
+  using S = Smem<N1, kStage2, kX2, kSplit>;
   _Float16* sw1 = smem;
   _Float16* sw2 = smem + S::w1;
   _Float16* sw3 = smem + S::w1 + S::w2;
   constexpr int NT1 = N1 / 16;
+  // the lo rows of a split matrix follow its hi rows
+  constexpr int kLo1 = N1 * kPitch;
 
-  // Stage the weights (16-byte chunks).
-  for (int i = threadIdx.x; i < N1 * (kK / 8); i += blockDim.x) {
+  // Stage the weights (16-byte chunks; [hi; lo] rows with kSplit).
+  for (int i = threadIdx.x; i < kParts * N1 * (kK / 8); i += blockDim.x) {
     const int r = i / (kK / 8), c = (i % (kK / 8)) * 8;
     *reinterpret_cast<uint4*>(sw1 + r * kPitch + c) = *reinterpret_cast<const uint4*>(a.w1 + r * kK + c);
     if constexpr (kX2)
       *reinterpret_cast<uint4*>(sw2 + r * kPitch + c) = *reinterpret_cast<const uint4*>(a.w2 + r * kK + c);
   }
   if constexpr (kStage2) {
-    for (int i = threadIdx.x; i < a.n3 * (N1 / 8); i += blockDim.x) {
+    for (int i = threadIdx.x; i < kParts * a.n3 * (N1 / 8); i += blockDim.x) {
       const int r = i / (N1 / 8), c = (i % (N1 / 8)) * 8;
       *reinterpret_cast<uint4*>(sw3 + r * S::p3 + c) = *reinterpret_cast<const uint4*>(a.w3 + r * N1 + c);
     }
@@ -217,11 +228,13 @@ __global__ void __launch_bounds__(threads_for<N1>()) fused_linear_kernel(Args a)
       f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
-        const f16x8_t wf = *reinterpret_cast<const f16x8_t*>(sw1 + (16 * nt + l16) * kPitch + 32 * ks + 8 * g);
-        acc = mfma16x16x32(wf, xb[ks], acc);
+        const int off = (16 * nt + l16) * kPitch + 32 * ks + 8 * g;
+        acc = mfma16x16x32(*reinterpret_cast<const f16x8_t*>(sw1 + off), xb[ks], acc);
+        if constexpr (kSplit) acc = mfma16x16x32(*reinterpret_cast<const f16x8_t*>(sw1 + kLo1 + off), xb[ks], acc);
         if constexpr (kX2) {
-          const f16x8_t wf2 = *reinterpret_cast<const f16x8_t*>(sw2 + (16 * nt + l16) * kPitch + 32 * ks + 8 * g);
-          acc = mfma16x16x32(wf2, x2b[ks], acc);
+          acc = mfma16x16x32(*reinterpret_cast<const f16x8_t*>(sw2 + off), x2b[ks], acc);
+          if constexpr (kSplit)
+            acc = mfma16x16x32(*reinterpret_cast<const f16x8_t*>(sw2 + kLo1 + off), x2b[ks], acc);
         }
       }
       const int f = 16 * nt + 4 * g;
@@ -269,13 +282,15 @@ __global__ void __launch_bounds__(threads_for<N1>()) fused_linear_kernel(Args a)
       for (int ot = 0; ot < NT3; ++ot) {
         f32x4_t y = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int ks = 0; ks < N1 / 32; ++ks) {
-          const _Float16* wr = sw3 + (16 * ot + l16) * S::p3 + 32 * ks;
-          const uint2 lo = *reinterpret_cast<const uint2*>(wr + 4 * g);
-          const uint2 hi = *reinterpret_cast<const uint2*>(wr + 16 + 4 * g);
-          const f16x8_t wf = __builtin_bit_cast(f16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
-          y = mfma16x16x32(wf, hb[ks], y);
-        }
+        for (int part = 0; part < kParts; ++part)
+#pragma unroll
+          for (int ks = 0; ks < N1 / 32; ++ks) {
+            const _Float16* wr = sw3 + (part * a.n3 + 16 * ot + l16) * S::p3 + 32 * ks;
+            const uint2 lo = *reinterpret_cast<const uint2*>(wr + 4 * g);
+            const uint2 hi = *reinterpret_cast<const uint2*>(wr + 16 + 4 * g);
+            const f16x8_t wf = __builtin_bit_cast(f16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
+            y = mfma16x16x32(wf, hb[ks], y);
+          }
         if (live) {
           const int f = 16 * ot + 4 * g;
           const float4 bb = a.b3 ? *reinterpret_cast<const float4*>(a.b3 + f) : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -299,10 +314,11 @@ int cu_count() {
   return g_cus;
 }
 
-template <typename TX, typename TX2, bool kLN, int N1, bool kX2, bool kRelu, bool kStage2, int kMode>
+template <typename TX, typename TX2, bool kLN, int N1, bool kX2, bool kRelu, bool kStage2, int kMode,
+          bool kSplit = false>
 int32_t launch(const Args& a, hipStream_t stream) {
-  using S = Smem<N1, kStage2, kX2>;
-  auto kernel = fused_linear_kernel<TX, TX2, kLN, N1, kX2, kRelu, kStage2, kMode>;
+  using S = Smem<N1, kStage2, kX2, kSplit>;
+  auto kernel = fused_linear_kernel<TX, TX2, kLN, N1, kX2, kRelu, kStage2, kMode, kSplit>;
   const int bytes = S::bytes(a.n3);
   if (bytes > kMaxLds) return MANTIS_E_ARG;
   static bool configured = false;
@@ -324,6 +340,17 @@ int32_t launch(const Args& a, hipStream_t stream) {
 }  // namespace mantis
 
 using namespace mantis;
+
+extern "C" int32_t mantis_fused_linear_split(const void* x, int32_t x_dtype, int64_t ldx,
+                                             const int64_t* x_rows, int64_t n_x, int64_t m,
+                                             int32_t layer_norm, const void* x2, int32_t x2_dtype,
+                                             int64_t ldx2, const void* w1, const void* w2,
+                                             const float* b1, int32_t n1, const float* add1,
+                                             int64_t ld_add1, const float* add2,
+                                             const int64_t* add2_rows, int64_t n_add2, int32_t relu,
+                                             const void* w3, const float* b3, int32_t n3,
+                                             int32_t out_mode, void* out, int64_t ldo,
+                                             int32_t* err_flag, void* stream);
 
 extern "C" int32_t mantis_fused_linear(const void* x, int32_t x_dtype, int64_t ldx,
                                        const int64_t* x_rows, int64_t n_x, int64_t m,
@@ -384,5 +411,47 @@ extern "C" int32_t mantis_fused_linear(const void* x, int32_t x_dtype, int64_t l
     if (x_dtype == MANTIS_F32 && ln) return launch<float, float, true, 256, true, true, true, 1>(a, s);
     if (x_dtype == MANTIS_F16 && !ln) return launch<_Float16, float, false, 256, true, true, true, 1>(a, s);
   }
+  return MANTIS_E_ARG;
+}
+
+// The same launches with compensated [hi; lo] weights (w1, w2: 2 x n1 rows
+// of 128; w3: 2 x n3 rows of n1): the combinations whose doubled weights fit
+// the LDS of one workgroup.
+extern "C" int32_t mantis_fused_linear_split(const void* x, int32_t x_dtype, int64_t ldx,
+                                             const int64_t* x_rows, int64_t n_x, int64_t m,
+                                             int32_t layer_norm, const void* x2, int32_t x2_dtype,
+                                             int64_t ldx2, const void* w1, const void* w2,
+                                             const float* b1, int32_t n1, const float* add1,
+                                             int64_t ld_add1, const float* add2,
+                                             const int64_t* add2_rows, int64_t n_add2, int32_t relu,
+                                             const void* w3, const float* b3, int32_t n3,
+                                             int32_t out_mode, void* out, int64_t ldo,
+                                             int32_t* err_flag, void* stream) {
+  if (m == 0) return MANTIS_OK;
+  if (!x || !w1 || !out || m < 0 || n_x < 0) return MANTIS_E_ARG;
+  if ((x2 == nullptr) != (w2 == nullptr) || (w3 == nullptr) != (n3 == 0)) return MANTIS_E_ARG;
+  if (add2 && !add2_rows) return MANTIS_E_ARG;
+  const int width = w3 ? n3 : n1;
+  if (ldx % 8 || (x2 && ldx2 % 8) || ldo % 4 || ldo < width || ldx < kK || (add1 && ld_add1 % 4))
+    return MANTIS_E_ARG;
+  if (!aligned16(x) || !aligned16(w1) || !aligned16(out) || (x2 && (!aligned16(x2) || !aligned16(w2))) ||
+      (w3 && !aligned16(w3)) || (b1 && !aligned16(b1)) || (b3 && !aligned16(b3)) ||
+      (add1 && !aligned16(add1)) || (add2 && !aligned16(add2)))
+    return MANTIS_E_ARG;
+  if (w3 && (n3 % 16 || n3 > 128)) return MANTIS_E_ARG;
+  Args a{x, ldx, x_rows, x_rows ? n_x : m, m, x2, ldx2, static_cast<const _Float16*>(w1),
+         static_cast<const _Float16*>(w2), b1, add1, ld_add1, add2, add2_rows, n_add2,
+         static_cast<const _Float16*>(w3), b3, n3, out, ldo, err_flag};
+  hipStream_t s = as_stream(stream);
+  const bool ln = layer_norm != 0, r = relu != 0, st2 = w3 != nullptr, hx2 = x2 != nullptr;
+  if (n1 != 128 || st2 || x_dtype != MANTIS_F32) return MANTIS_E_ARG;
+  // LN projection (fp16 or fp32 rows out)
+  if (!hx2 && ln && !r && out_mode == 0) return launch<float, float, true, 128, false, false, false, 0, true>(a, s);
+  if (!hx2 && ln && !r && out_mode == 1) return launch<float, float, true, 128, false, false, false, 1, true>(a, s);
+  // residual projection: out += x W^T + b
+  if (!hx2 && !ln && !r && out_mode == 2) return launch<float, float, false, 128, false, false, false, 2, true>(a, s);
+  // first layer of a pair MLP: relu(LN(x) W1^T + x2 W2^T + b1), fp32 out
+  if (hx2 && ln && r && out_mode == 1 && x2_dtype == MANTIS_F16)
+    return launch<float, _Float16, true, 128, true, true, false, 1, true>(a, s);
   return MANTIS_E_ARG;
 }

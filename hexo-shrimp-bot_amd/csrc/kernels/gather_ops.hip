@@ -66,7 +66,8 @@ run_reduce_kernel(const Tin* __restrict__ values, int64_t n_src, int64_t ld, int
     float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     for (int64_t base = start; base < end; base += kGroup) {
       const int cnt = int(end - base < kGroup ? end - base : kGroup);
-      const int64_t my = gather[base + (lane < cnt ? lane : cnt - 1)];
+      const int64_t slot = base + (lane < cnt ? lane : cnt - 1);
+      const int64_t my = gather ? gather[slot] : slot;
       const bool mine_ok = my >= 0 && my < n_src;
       if (lane < cnt && !mine_ok) raise_flag(flag, MANTIS_FLAG_INDEX);
       const int32_t my32 = mine_ok ? int32_t(my) : -1;  // n_src fits int32 (host check)
@@ -106,7 +107,7 @@ run_reduce_scalar_kernel(const Tin* __restrict__ values, int64_t n_src, int64_t 
   for (int64_t c = lane; c < h; c += kGroup) {
     float acc = 0.f;
     for (int64_t e = start; e < end; ++e) {
-      int64_t s = gather[e];
+      const int64_t s = gather ? gather[e] : e;
       if (s < 0 || s >= n_src) {
         raise_flag(flag, MANTIS_FLAG_INDEX);
         continue;
@@ -505,7 +506,7 @@ int32_t mantis_run_reduce(const void* values, int32_t values_dtype, int64_t n_sr
   if (n_dest == 0) return MANTIS_OK;
   if (!values || !ptr || !out || h <= 0 || ld < h || n_dest < 0 || n_src < 0) return MANTIS_E_ARG;
   if (out_dtype < MANTIS_F32 || out_dtype > MANTIS_F16) return MANTIS_E_ARG;
-  if (n_entries < 0 || (n_entries > 0 && !gather)) return MANTIS_E_ARG;
+  if (n_entries < 0) return MANTIS_E_ARG;  // gather NULL: entry e reads source row e
   if (n_src > 2147483647LL) return MANTIS_E_ARG;  // source indices travel as int32
   const bool vec = h % 8 == 0 && ld % 8 == 0 && aligned16(values) && aligned16(out);
   hipStream_t s = as_stream(stream);

@@ -26,6 +26,13 @@ SIGNATURES = {
     "mantis_hip_version": ([], i32),
     "mantis_runs_to_ptr": ([vp, i64, i64, vp, vp, vp], i32),
     "mantis_run_reduce": ([vp, i32, i64, i64, i64, vp, i64, vp, i64, vp, i32, vp, vp], i32),
+    "mantis_class_reduce_workspace": ([i64, i64, i64], i64),
+    "mantis_class_reduce": ([vp, i32, i64, i64, i64, vp, i64, vp, i64, vp, i64, vp, i32, vp, vp], i32),
+    "mantis_cell_pass": ([vp, i32, i64, i64, i64, vp, i32, i64, i64, vp, i64, vp, vp, i64, vp, vp, vp, vp, vp, vp],
+                         i32),
+    "mantis_cell_pass_backward_workspace": ([i64, i64, i64, i64], i64),
+    "mantis_cell_pass_backward": ([vp, i32, i64, i64, i64, vp, i32, i64, i64, vp, i32, i64, vp, i64, vp, vp, i64, vp,
+                                   vp, vp, vp, vp, i64, vp, vp, vp, vp], i32),
     "mantis_cell_attention": (
         [vp, vp, vp, i32, i64, i64, i64, vp, i64, vp, i32, vp, vp, vp, i64, i64, i64, i32, i32, vp, i32, vp, vp, vp, vp],
         i32),
@@ -45,6 +52,8 @@ SIGNATURES = {
     "mantis_stone_attention": ([vp, vp, vp, vp, vp, vp, i32, vp, i64, i32, i64, i32, vp, vp, vp, vp], i32),
     "mantis_fused_linear": ([vp, i32, i64, vp, i64, i64, i32, vp, i32, i64, vp, vp, vp, i32, vp, i64, vp, vp, i64,
                              i32, vp, vp, i32, i32, vp, i64, vp, vp], i32),
+    "mantis_fused_linear_split": ([vp, i32, i64, vp, i64, i64, i32, vp, i32, i64, vp, vp, vp, i32, vp, i64, vp, vp,
+                                   i64, i32, vp, vp, i32, i32, vp, i64, vp, vp], i32),
     "mantis_layer_norm": ([vp, i64, i64, vp, vp, vp, i32, i64, vp], i32),
     "mantis_value_read": ([vp, vp, i64, vp, vp, i64, vp, vp, vp, i32, vp, vp, vp], i32),
     "mantis_compose_q": ([vp, i64, vp, i64, i64, ctypes.c_float, vp, vp, vp], i32),

@@ -34,8 +34,10 @@ cell_tables and cell_node_edge_tables) are derived once per batch on the
 device and shared by the trunk and the heads.
 
 Scope: the production cell-state configuration (``cell_nodes=True``, either
-node scope), H = 128, 4 heads of 32, 4 value queries.  Other knob
-combinations raise ``NotImplementedError``; the forward is inference-only.
+node scope) and the knob-off default (no cell state: the transient cell pass
+of model.py:374-395, and heads over the decoder's window sums), H = 128, 4
+heads of 32, 4 value queries.  Other knob combinations raise
+``NotImplementedError``; the forward is inference-only.
 """
 
 from __future__ import annotations
@@ -58,8 +60,9 @@ ORBIT48 = 48
 
 def _supported(model) -> torch.device:
     cfg = model.cfg
-    if not (cfg.cell_nodes and cfg.uses_cell_state):
-        raise NotImplementedError("the MI355X forward implements the cell-node configuration (cell_nodes=True)")
+    if cfg.cell_latents and not cfg.cell_nodes:
+        raise NotImplementedError("the MI355X forward implements cell_nodes=True or the knob-off cell pass, "
+                                  "not covered-only cell latents")
     if cfg.cell_adjacency or cfg.cell_structure or cfg.action_tactical:
         raise NotImplementedError("cell_adjacency / cell_structure / action_tactical are not implemented")
     if cfg.h != 128 or cfg.heads != 4 or cfg.value_queries != 4 or cfg.ffn_factor != 2 or cfg.policy_hidden != 128:
@@ -123,6 +126,24 @@ def _interleaved(pair):
     return w.index_select(0, idx).contiguous(), b.index_select(0, idx).contiguous()
 
 
+def _prepare_cell_stage(t, put, P, pb):
+    """The three typed-attention sub-stages of one cell-state block.  The
+    sub-stages read k/v and class-value rows head-interleaved: the k/v
+    projections emit that layout (output rows permuted)."""
+    put(pb + "cr_q", _fold(P, pb + "ln_cr_c", [pb + "cr_wq"]))
+    put(pb + "cr_kv", _interleaved(_fold(P, pb + "ln_cr_w", [pb + "cr_wk", pb + "cr_wv"])))
+    put(pb + "cr_o", _fold(P, None, [pb + "cr_wo"]))
+    # class-value rows gathered once per edge: fp16 halves their bytes
+    t[pb + "cr_vcls"] = ops.interleave_heads(P[pb + "cr_vclass.weight"]).to(HALF).contiguous()
+    put(pb + "rad_q", _fold(P, pb + "ln_radius_c", [pb + "radius_wq"]))
+    put(pb + "rad_kv", _interleaved(_fold(P, pb + "ln_radius_s", [pb + "radius_wk", pb + "radius_wv"])))
+    put(pb + "rad_o", _fold(P, None, [pb + "radius_wo"]))
+    t[pb + "rad_vcls"] = ops.interleave_heads(P[pb + "radius_vclass.weight"]).to(HALF).contiguous()
+    put(pb + "wr_q", _fold(P, pb + "ln_wr_w", [pb + "wr_wq"]))
+    put(pb + "wr_kv", _interleaved(_fold(P, pb + "ln_wr_c", [pb + "wr_wk", pb + "wr_wv"])))
+    put(pb + "wr_o", _fold(P, None, [pb + "wr_wo"]))
+
+
 def _prepare(model, P) -> dict[str, Tensor]:
     cfg = model.cfg
     t: dict[str, Tensor] = {}
@@ -139,20 +160,18 @@ def _prepare(model, P) -> dict[str, Tensor]:
         put(pb + "mlp_w3", _fold(P, None, [pb + "mlp_w.out"]))
         # window class term composed with lin_b: counts @ e_ws @ lin_b^T, per pattern
         t[pb + "ws_tab"] = (counts @ (P[pb + "e_ws.weight"] @ P[pb + "mlp_w.lin_b.weight"].t())).contiguous()
-        # the sub-stages read k/v and class-value rows head-interleaved: the
-        # k/v projections emit that layout (output rows permuted)
-        put(pb + "cr_q", _fold(P, pb + "ln_cr_c", [pb + "cr_wq"]))
-        put(pb + "cr_kv", _interleaved(_fold(P, pb + "ln_cr_w", [pb + "cr_wk", pb + "cr_wv"])))
-        put(pb + "cr_o", _fold(P, None, [pb + "cr_wo"]))
-        # class-value rows gathered once per edge: fp16 halves their bytes
-        t[pb + "cr_vcls"] = ops.interleave_heads(P[pb + "cr_vclass.weight"]).to(HALF).contiguous()
-        put(pb + "rad_q", _fold(P, pb + "ln_radius_c", [pb + "radius_wq"]))
-        put(pb + "rad_kv", _interleaved(_fold(P, pb + "ln_radius_s", [pb + "radius_wk", pb + "radius_wv"])))
-        put(pb + "rad_o", _fold(P, None, [pb + "radius_wo"]))
-        t[pb + "rad_vcls"] = ops.interleave_heads(P[pb + "radius_vclass.weight"]).to(HALF).contiguous()
-        put(pb + "wr_q", _fold(P, pb + "ln_wr_w", [pb + "wr_wq"]))
-        put(pb + "wr_kv", _interleaved(_fold(P, pb + "ln_wr_c", [pb + "wr_wk", pb + "wr_wv"])))
-        put(pb + "wr_o", _fold(P, None, [pb + "wr_wo"]))
+        if not cfg.cell_nodes:
+            # knob-off cell pass: u_cp(LN w), the relay, then mlp_cp.  The relay
+            # sums u_cp's output over up to 18 windows per cell and six cells per
+            # window, so a rounding of these weights adds up coherently: they are
+            # compensated [hi; lo] fp16 pairs (~22 mantissa bits)
+            for key, ln, lin in (("cp_u", "ln_cp_in", "u_cp"), ("mlp_cp1", "ln_cp_w", "mlp_cp.lin_a"),
+                                 ("mlp_cp3", None, "mlp_cp.out")):
+                w32, b32 = _fold32(P, pb + ln if ln else None, [pb + lin])
+                t[pb + key + ".w"], t[pb + key + ".b"] = ops.split_weight(w32), b32
+            t[pb + "mlp_cp2.w"] = ops.split_weight(P[pb + "mlp_cp.lin_b.weight"])
+        else:
+            _prepare_cell_stage(t, put, P, pb)
         # the three projections of the same window state (stones <- windows
         # values, latent-read keys/values, latent-broadcast queries) in one
         # 512-wide launch: one read of w instead of three
@@ -242,9 +261,9 @@ class Plan:
     win_ptr: Tensor  # window-major decoder CSR
     edge_wcell: Tensor
     edge_wclass: Tensor
-    radius_ptr: Tensor
-    radius_src: Tensor
-    radius_class: Tensor
+    radius_ptr: Tensor | None  # radius views: cell-node configurations only
+    radius_src: Tensor | None
+    radius_class: Tensor | None
     seq_lens: Tensor
     attn_src: Tensor  # padded attention slot -> row of [s; g] (or -1)
     attn_back: Tensor  # row of [s; g] -> padded attention slot
@@ -311,15 +330,17 @@ def make_plan(model, b: Batch) -> Plan:
     covered = cell_ptr[1:] > cell_ptr[:-1]
     win_ptr = ops.runs_to_ptr(edge_window[worder].contiguous(), n_w)
     # radius edge tables (cell_nodes.py:23-94, model.py:843-859)
-    if cfg.cell_node_scope == "uncovered":
-        keep = ~covered[dst]
-        src, dst, classes = src[keep], dst[keep], classes[keep]
-    if canonical:
-        radius_src, radius_dst, radius_class = src, dst, classes
-    else:
-        rorder = _stable_order(dst)
-        radius_src, radius_dst, radius_class = src[rorder], dst[rorder], classes[rorder]
-    radius_ptr = ops.runs_to_ptr(radius_dst.contiguous(), n_c)
+    radius_ptr = radius_src = radius_class = None
+    if cfg.cell_nodes:
+        if cfg.cell_node_scope == "uncovered":
+            keep = ~covered[dst]
+            src, dst, classes = src[keep], dst[keep], classes[keep]
+        if canonical:
+            radius_src, radius_dst, radius_class = src, dst, classes
+        else:
+            rorder = _stable_order(dst)
+            radius_src, radius_dst, radius_class = src[rorder], dst[rorder], classes[rorder]
+        radius_ptr = ops.runs_to_ptr(radius_dst.contiguous(), n_c)
     # attention rows [latents; stones] per position over the [s; g] buffer
     gslot = (torch.arange(p, device=dev)[:, None] * max_t + torch.arange(GLOBAL_ROWS, device=dev)[None, :]).reshape(-1)
     attn_src = torch.full((p * max_t,), -1, dtype=torch.long, device=dev)
@@ -388,6 +409,24 @@ def _cell_stage(W, P, pb, plan: Plan, s, w, c):
     ops.attention_substages(w, [wr])
 
 
+def _cell_pass(W, P, pb, plan: Plan, b: Batch, w):
+    """The knob-off cell pass (model.py:374-395): w += mlp_cp(LN w, relay of
+    u_cp(LN w) through the empty cells the windows share).  The batch's
+    compact relay views are used when it carries them; the plan's views over
+    all legal cells give the same sums in the same order otherwise."""
+    x = FL(w, W[pb + "cp_u.w"], W[pb + "cp_u.b"], layer_norm=True, split=True)  # (n_w, 128) fp16
+    if getattr(b, "relay_cell_ptr", None) is not None:
+        views = (b.relay_cell_ptr, b.relay_window, b.relay_class, b.relay_win_ptr, b.relay_wcell)
+    else:
+        views = (plan.cell_ptr, plan.edge_window, plan.edge_class, plan.win_ptr, plan.edge_wcell)
+    agg = ops.cell_pass(x, P[pb + "e_cp.weight"], *views)
+    # mlp_cp in two launches (the compensated weights of one launch fit LDS):
+    # the hidden layer in fp32, then out-projection and residual
+    hid = FL(w, W[pb + "mlp_cp1.w"], W[pb + "mlp_cp1.b"], layer_norm=True, x2=agg, w2=W[pb + "mlp_cp2.w"],
+             relu=True, out_dtype=F32, split=True)
+    FL(hid, W[pb + "mlp_cp3.w"], W[pb + "mlp_cp3.b"], out=w, residual=True, split=True)
+
+
 def _latent_cycle(W, P, pb, plan: Plan, w, g2, kv, qb):
     """kv: the windows' latent-read keys|values, qb: their broadcast queries
     (both projected from w with the stones' values, see _block)."""
@@ -413,8 +452,11 @@ def _block(W, P, i: int, plan: Plan, b: Batch, sg, w, c, sw_all, update_stones: 
     FL(w, W[pb + "mlp_w1.w"], W[pb + "mlp_w1.b"], layer_norm=True, x2=agg, w2=W[pb + "mlp_w2.w"],
        add2=W[pb + "ws_tab"], add2_rows=b.window_feat, relu=True, w3=W[pb + "mlp_w3.w"], b3=W[pb + "mlp_w3.b"],
        out=w, residual=True)
-    # §5.1b cell stage
-    _cell_stage(W, P, pb, plan, s, w, c)
+    # §5.1b cell stage, or the knob-off cell pass
+    if c is not None:
+        _cell_stage(W, P, pb, plan, s, w, c)
+    else:
+        _cell_pass(W, P, pb, plan, b, w)
     # §5.2 stones <- windows: s += mlp_s(LN s, agg + class term); w does not
     # change again until the latent broadcast, so its latent-read keys/values
     # and broadcast queries are projected here in the same launch
@@ -472,16 +514,20 @@ def _trunk(model, b: Batch, plan: Plan, raw_cells: bool = False):
     sg[:n_s] = P["stone_table.weight"].index_select(0, b.stone_own)
     sg[n_s:] = (P["latent_base"][None] + P["token_moves.weight"].index_select(0, b.moves_idx)[:, None]).reshape(-1, 128)
     w = P["window_table.weight"].index_select(0, b.window_feat)
-    # covered cells start from cell_base, the others from their nearest-stone
-    # row: one gather from the table [nearest rows; cell_base]
-    table = torch.cat([P["cell_nearest_table.weight"], P["cell_base"][None, :]])
-    c = table.index_select(0, torch.where(plan.covered_mask, table.shape[0] - 1, b.cell_nearest))
+    c = None
+    if cfg.cell_nodes:
+        # covered cells start from cell_base, the others from their nearest-stone
+        # row: one gather from the table [nearest rows; cell_base]
+        table = torch.cat([P["cell_nearest_table.weight"], P["cell_base"][None, :]])
+        c = table.index_select(0, torch.where(plan.covered_mask, table.shape[0] - 1, b.cell_nearest))
     sw_all = ops.run_reduce(W["sw_all"], plan.run_class, plan.inc_stone_ptr, n_s, F32)
     for i in range(cfg.blocks):
         _block(W, P, i, plan, b, sg, w, c, sw_all, i + 1 < cfg.blocks)
     g = sg[n_s:].view(p, GLOBAL_ROWS, 128)
     w_out = ops.layer_norm(w, P["ln_out.weight"], P["ln_out.bias"], F32)
     g_out = F.layer_norm(g, (128,), P["ln_out.weight"], P["ln_out.bias"], 1e-5).mean(dim=1)
+    if c is None:
+        return w_out, g_out, None
     cells = c if raw_cells else ops.layer_norm(c, P["ln_out.weight"], P["ln_out.bias"], HALF)
     return w_out, g_out, cells
 
@@ -505,9 +551,16 @@ def _value_head(model, w: Tensor, g: Tensor, b: Batch, plan: Plan):
 
 def _head_rows(model, w: Tensor, g: Tensor, cells: Tensor, b: Batch, plan: Plan, raw_cells: bool = False) -> Tensor:
     """(N_c, 16) fp32: column 0 the policy logit, 1..3 the critic logits.
-    ``cells`` are ln_out(c) rows, or with raw_cells the fp32 cell state."""
-    if cells is None:
+    ``cells`` are ln_out(c) rows, or with raw_cells the fp32 cell state; with
+    cell state off they are None and each legal cell reads the sum of its
+    decoder windows' ln_out rows (model.py:985-1029)."""
+    if model.cfg.uses_cell_state and cells is None:
         raise ValueError("cell state is on but the trunk's cell rows were not passed to the decoder")
+    if not model.cfg.uses_cell_state:
+        if cells is not None:
+            raise ValueError("cell rows were passed but cell state is off")
+        cells = ops.run_reduce(w, b.dec_window, plan.dec_cell_ptr, plan.n_c, HALF)
+        raw_cells = False
     W = _prepared(model)
     P = dict(model.named_parameters())
     pre = FL(w.float().contiguous(), W["act_proj.w"], W["act_proj.b"])  # act_proj(w), fp16

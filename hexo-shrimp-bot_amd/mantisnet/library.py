@@ -3,8 +3,10 @@
 Every operator keeps the reference's qualified name, argument list and
 output structure, so code written against the reference's ``torch.ops``
 surface runs unchanged.  Each has a fake (meta) implementation for tracing.
-Only the forward is provided: this is the inference path, and asking for a
-gradient raises.
+The run reductions and the cell pass carry their backward (the reference's
+``register_autograd`` pairs, as HIP run reductions); the attention-family and
+latent operators are forward-only here, and asking them for a gradient
+raises.
 
 Differences from the reference, all deliberate:
 
@@ -18,7 +20,9 @@ Differences from the reference, all deliberate:
 Reference registrations (python/mantisnet/mantisnet/...):
 attention.py:719-760, message_passing.py:191-227 and 344-365,
 cell_latents.py:168-208 and 834-952, cell_nodes.py:97-147,
-window_latents.py:38-64, 553-587 and 648-664, row_encoder.py:368-380.
+window_latents.py:38-64, 553-587 and 648-664, row_encoder.py:368-380,
+relay.py:452-574; backward registrations message_passing.py:234-279 and
+373-431.
 """
 
 from __future__ import annotations
@@ -106,6 +110,33 @@ def _(values, inc_stone, inc_window, run_stone, run_window, n_stones):
     return values.new_empty((n_stones, values.shape[1]), dtype=torch.float32)
 
 
+def _setup_incidence(ctx, inputs, output) -> None:
+    values, inc_stone, inc_window, run_stone, run_window, _n_dest = inputs
+    ctx.save_for_backward(inc_stone, inc_window, run_stone, run_window)
+    ctx.n_source = values.shape[0]
+    ctx.values_dtype = values.dtype
+
+
+def _backward_to_windows(ctx, grad_out):
+    # a stone row's gradient: its entries' upstream window rows, the
+    # stone-major run reduction (message_passing.py:242-255)
+    _inc_stone, _inc_window, run_stone, run_window = ctx.saved_tensors
+    grad = _run_sum(grad_out, run_window, run_stone, ctx.n_source, ctx.values_dtype)
+    return grad, None, None, None, None, None
+
+
+def _backward_to_stones(ctx, grad_out):
+    # a window row's gradient: its entries' upstream stone rows, the
+    # window-major run reduction (message_passing.py:258-271)
+    inc_stone, inc_window, _run_stone, _run_window = ctx.saved_tensors
+    grad = _run_sum(grad_out, inc_stone, inc_window, ctx.n_source, ctx.values_dtype)
+    return grad, None, None, None, None, None
+
+
+aggregate_to_windows.register_autograd(_backward_to_windows, setup_context=_setup_incidence)
+aggregate_to_stones.register_autograd(_backward_to_stones, setup_context=_setup_incidence)
+
+
 @torch.library.custom_op(f"{_NS}::class_row_sum", mutates_args=())
 def class_row_sum(weight: Tensor, gather: Tensor, runs: Tensor, n_dest: int, run_len: int) -> Tensor:
     """out[d] = sum of weight[gather[e]] over the ascending run of d, fp32."""
@@ -116,6 +147,27 @@ def class_row_sum(weight: Tensor, gather: Tensor, runs: Tensor, n_dest: int, run
 @class_row_sum.register_fake
 def _(weight, gather, runs, n_dest, run_len):
     return weight.new_empty((n_dest, weight.shape[1]), dtype=torch.float32)
+
+
+def _setup_class(ctx, inputs, output) -> None:
+    weight, gather, runs, _n_dest, _run_len = inputs
+    ctx.save_for_backward(gather, runs)
+    ctx.n_classes = weight.shape[0]
+    ctx.weight_dtype = weight.dtype
+
+
+def _class_row_sum_backward(ctx, grad_out):
+    # the table gradient reduces by class over unbounded runs
+    # (message_passing.py:380-397): the class-major view of the entries, then
+    # the sliced class reduction
+    gather, runs = ctx.saved_tensors
+    order = torch.argsort(gather, stable=True)
+    cls_ptr = ops.runs_to_ptr(gather.index_select(0, order), ctx.n_classes)
+    grad = ops.class_reduce(grad_out, runs.index_select(0, order), cls_ptr, ctx.n_classes, ctx.weight_dtype)
+    return grad, None, None, None, None
+
+
+class_row_sum.register_autograd(_class_row_sum_backward, setup_context=_setup_class)
 
 
 @torch.library.custom_op(f"{_NS}::incidence_row_sum", mutates_args=())
@@ -130,6 +182,67 @@ def incidence_row_sum(values: Tensor, gather: Tensor, runs: Tensor, rev_gather: 
 @incidence_row_sum.register_fake
 def _(values, gather, runs, rev_gather, rev_runs, n_dest, run_len, rev_run_len):
     return values.new_empty((n_dest, values.shape[1]), dtype=torch.float32)
+
+
+def _setup_incidence_rows(ctx, inputs, output) -> None:
+    values, _gather, _runs, rev_gather, rev_runs, _n_dest, _run_len, _rev_run_len = inputs
+    ctx.save_for_backward(rev_gather, rev_runs)
+    ctx.n_source = values.shape[0]
+    ctx.values_dtype = values.dtype
+
+
+def _incidence_row_sum_backward(ctx, grad_out):
+    # a source row's gradient: the reverse ordering's run reduction
+    # (message_passing.py:409-423)
+    rev_gather, rev_runs = ctx.saved_tensors
+    grad = _run_sum(grad_out, rev_gather, rev_runs, ctx.n_source, ctx.values_dtype)
+    return grad, None, None, None, None, None, None, None
+
+
+incidence_row_sum.register_autograd(_incidence_row_sum_backward, setup_context=_setup_incidence_rows)
+
+
+# ----------------------------------------------------------------- the knob-off cell pass
+
+
+@torch.library.custom_op(f"{_NS}::cell_pass", mutates_args=())
+def cell_pass(x: Tensor, emb: Tensor, cell_ptr: Tensor, edge_window: Tensor, edge_class: Tensor, win_ptr: Tensor,
+              edge_wcell: Tensor, cls_ptr: Tensor, edge_ccell: Tensor) -> Tensor:
+    """The (N_w, H) window aggregate of the cell pass over one batch's relay
+    tables (cls_ptr / edge_ccell serve the backward)."""
+    ops._check_cell_pass(x, emb, cell_ptr, edge_window, edge_class, win_ptr, edge_wcell, cls_ptr, edge_ccell)
+    return ops.cell_pass(x, emb, cell_ptr, edge_window, edge_class, win_ptr, edge_wcell)
+
+
+@cell_pass.register_fake
+def _(x, emb, cell_ptr, edge_window, edge_class, win_ptr, edge_wcell, cls_ptr, edge_ccell):
+    return torch.empty_like(x)
+
+
+@torch.library.custom_op(f"{_NS}::cell_pass_backward", mutates_args=())
+def cell_pass_backward(x: Tensor, emb: Tensor, cell_ptr: Tensor, edge_window: Tensor, edge_class: Tensor,
+                       win_ptr: Tensor, edge_wcell: Tensor, cls_ptr: Tensor, edge_ccell: Tensor,
+                       grad_out: Tensor) -> tuple[Tensor, Tensor]:
+    """(dx, d_emb) of the cell pass."""
+    return ops.cell_pass_backward(x, emb, cell_ptr, edge_window, edge_class, win_ptr, edge_wcell, cls_ptr,
+                                  edge_ccell, grad_out)
+
+
+@cell_pass_backward.register_fake
+def _(x, emb, cell_ptr, edge_window, edge_class, win_ptr, edge_wcell, cls_ptr, edge_ccell, grad_out):
+    return torch.empty_like(x), torch.empty_like(emb)
+
+
+def _setup_cell_pass(ctx, inputs, output) -> None:
+    ctx.save_for_backward(*inputs)
+
+
+def _cell_pass_autograd(ctx, grad_out):
+    dx, d_emb = cell_pass_backward(*ctx.saved_tensors, grad_out)
+    return dx, d_emb, None, None, None, None, None, None, None
+
+
+cell_pass.register_autograd(_cell_pass_autograd, setup_context=_setup_cell_pass)
 
 
 # ----------------------------------------------------------------- typed cell attention
@@ -321,8 +434,10 @@ def _(window_pos, positions):
 OPERATORS = (
     "fused_attention", "aggregate_to_windows", "aggregate_to_stones", "class_row_sum", "incidence_row_sum",
     "cell_attention", "cell_attention_plain", "window_latent_read", "window_latent_broadcast",
-    "action_row_encode", "cell_tables", "cell_node_edge_tables", "window_latent_layout",
+    "action_row_encode", "cell_tables", "cell_node_edge_tables", "window_latent_layout", "cell_pass",
+    "cell_pass_backward",
 )
 
-for _name in OPERATORS[:10]:
+for _name in ("fused_attention", "cell_attention", "cell_attention_plain", "window_latent_read",
+              "window_latent_broadcast", "action_row_encode"):
     _register_inference_only(globals()[_name], _name)

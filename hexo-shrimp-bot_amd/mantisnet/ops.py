@@ -237,6 +237,147 @@ def run_reduce(values: Tensor, gather: Tensor, ptr: Tensor, n_dest: int, out_dty
     return out
 
 
+def _workspace(nbytes: int, dev: torch.device) -> Tensor:
+    if nbytes < 0:
+        raise ValueError("negative size")
+    return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=dev)
+
+
+def _row_major(t: Tensor) -> Tensor:
+    """Rows with unit column stride and a row stride of at least the width
+    (an empty or expanded tensor can report strides of 0)."""
+    if t.numel() == 0:
+        return torch.empty(t.shape, dtype=t.dtype, device=t.device)
+    if t.stride(-1) == 1 and (t.ndim < 2 or t.stride(0) >= t.shape[-1]):
+        return t
+    return t.contiguous()
+
+
+def class_reduce(values: Tensor, gather: Tensor, cls_ptr: Tensor, n_classes: int, out_dtype: torch.dtype) -> Tensor:
+    """out[k] = sum of values[gather[e]] over e in [cls_ptr[k], cls_ptr[k+1]):
+    fp32 sums over slices of 64 entries, then each class's slices in order,
+    so unbounded class runs spread over the device (deterministic)."""
+    dev = _on_gpu(values, gather, cls_ptr)
+    if values.ndim != 2:
+        raise ValueError("values must have shape (N, H)")
+    values = _row_major(values)
+    gather = _i64(gather, "gather")
+    cls_ptr = _i64(cls_ptr, "cls_ptr")
+    if cls_ptr.numel() != n_classes + 1:
+        raise ValueError("cls_ptr must have n_classes + 1 entries")
+    h = values.shape[1]
+    out = torch.empty((n_classes, h), dtype=out_dtype, device=dev)
+    if n_classes == 0 or h == 0:
+        return out
+    e = gather.numel()
+    ws = _workspace(_lib().mantis_class_reduce_workspace(e, n_classes, h), dev)
+    nbytes = e * 8 + min(e, values.shape[0]) * h * values.element_size() + n_classes * h * out.element_size()
+    _launch("class_reduce", nbytes, e * h, lambda: _check(
+        _lib().mantis_class_reduce(
+            _ptr(values), _dt(values), values.shape[0], values.stride(0), h, _ptr(gather), e, _ptr(cls_ptr),
+            n_classes, _ptr(ws), ws.numel(), _ptr(out), _dt(out), _ptr(error_flag(dev)), _stream(),
+        ),
+        "class_reduce",
+    ))
+    return out
+
+
+def _check_cell_pass(x, emb, cell_ptr, edge_window, edge_class, win_ptr, edge_wcell, cls_ptr=None,
+                     edge_ccell=None) -> None:
+    """The reference's argument checks (relay.py:268-289), before any device check."""
+    if x.ndim != 2:
+        raise ValueError("x must have shape (N_w, H)")
+    if emb.ndim != 2 or emb.shape[1] != x.shape[1]:
+        raise ValueError("emb must have shape (n_classes, H) matching x")
+    edges = edge_window.shape
+    views = [edge_class, edge_wcell] + ([edge_ccell] if edge_ccell is not None else [])
+    if any(t.shape != edges for t in views):
+        raise ValueError("the three edge views must have one length")
+    if win_ptr.numel() != x.shape[0] + 1:
+        raise ValueError("win_ptr must have one entry per window plus one")
+    if cls_ptr is not None and cls_ptr.numel() != emb.shape[0] + 1:
+        raise ValueError("cls_ptr must have one entry per class plus one")
+    tables = [cell_ptr, edge_window, edge_class, win_ptr, edge_wcell] + [t for t in (cls_ptr, edge_ccell)
+                                                                         if t is not None]
+    if any(t.device != x.device for t in tables) or emb.device != x.device:
+        raise ValueError("all cell-pass inputs must be on one device")
+
+
+def cell_pass(x: Tensor, emb: Tensor, cell_ptr: Tensor, edge_window: Tensor, edge_class: Tensor, win_ptr: Tensor,
+              edge_wcell: Tensor) -> Tensor:
+    """The knob-off cell pass: out[w] = sum over the window's relay cells c of
+    ReLU(sum over c's entries of x[window] + emb[class]), fp32 sums, out in
+    x's dtype (relay.py:1-13)."""
+    _check_cell_pass(x, emb, cell_ptr, edge_window, edge_class, win_ptr, edge_wcell)
+    dev = _on_gpu(x, emb, cell_ptr, edge_window, edge_class, win_ptr, edge_wcell)
+    x, emb = _row_major(x), _row_major(emb)
+    cell_ptr, edge_window, edge_class = _i64(cell_ptr, "cell_ptr"), _i64(edge_window, "edge_window"), \
+        _i64(edge_class, "edge_class")
+    win_ptr, edge_wcell = _i64(win_ptr, "win_ptr"), _i64(edge_wcell, "edge_wcell")
+    n_w, h = x.shape
+    n_relay = cell_ptr.numel() - 1
+    if n_relay < 0:
+        raise ValueError("cell_ptr must have at least one entry")
+    out = torch.empty((n_w, h), dtype=x.dtype, device=dev)
+    if n_w == 0 or h == 0:
+        return out
+    val = torch.empty((max(n_relay, 1), h), dtype=torch.float32, device=dev)
+    e = edge_window.numel()
+    # entries: 3 indices + x and class rows; cells: value row out and back in; windows: out row
+    nbytes = e * 24 + min(e, n_w) * h * x.element_size() + min(e, emb.shape[0]) * h * emb.element_size() \
+        + 2 * n_relay * h * 4 + n_w * (8 + h * out.element_size())
+    _launch(f"cell_pass_{_SHORT[x.dtype]}", nbytes, 3 * e * h, lambda: _check(
+        _lib().mantis_cell_pass(
+            _ptr(x), _dt(x), x.stride(0), n_w, h, _ptr(emb), _dt(emb), emb.stride(0), emb.shape[0], _ptr(cell_ptr),
+            n_relay, _ptr(edge_window), _ptr(edge_class), e, _ptr(win_ptr), _ptr(edge_wcell), _ptr(val), _ptr(out),
+            _ptr(error_flag(dev)), _stream(),
+        ),
+        "cell_pass",
+    ))
+    return out
+
+
+def cell_pass_backward(x: Tensor, emb: Tensor, cell_ptr: Tensor, edge_window: Tensor, edge_class: Tensor,
+                       win_ptr: Tensor, edge_wcell: Tensor, cls_ptr: Tensor, edge_ccell: Tensor,
+                       grad_out: Tensor) -> tuple[Tensor, Tensor]:
+    """(dx in x's dtype, d_emb in emb's dtype) of ``cell_pass`` for grad_out
+    (relay.py:235-265, 385-438): the ReLU mask recomputed per cell, fp32
+    sums in a fixed order (two calls agree bitwise)."""
+    _check_cell_pass(x, emb, cell_ptr, edge_window, edge_class, win_ptr, edge_wcell, cls_ptr, edge_ccell)
+    if grad_out.shape != x.shape:
+        raise ValueError("grad_out must have the shape of x")
+    dev = _on_gpu(x, emb, cell_ptr, edge_window, edge_class, win_ptr, edge_wcell, cls_ptr, edge_ccell, grad_out)
+    x, emb, grad_out = _row_major(x), _row_major(emb), _row_major(grad_out)
+    idx = [_i64(t, n) for t, n in ((cell_ptr, "cell_ptr"), (edge_window, "edge_window"), (edge_class, "edge_class"),
+                                   (win_ptr, "win_ptr"), (edge_wcell, "edge_wcell"), (cls_ptr, "cls_ptr"),
+                                   (edge_ccell, "edge_ccell"))]
+    cell_ptr, edge_window, edge_class, win_ptr, edge_wcell, cls_ptr, edge_ccell = idx
+    n_w, h = x.shape
+    n_cls = emb.shape[0]
+    n_relay = cell_ptr.numel() - 1
+    if n_relay < 0:
+        raise ValueError("cell_ptr must have at least one entry")
+    dx = torch.empty_like(x, memory_format=torch.contiguous_format)
+    d_emb = torch.empty((n_cls, h), dtype=emb.dtype, device=dev)
+    if h == 0 or (n_w == 0 and n_cls == 0):
+        return dx, d_emb
+    e = edge_window.numel()
+    ws = _workspace(_lib().mantis_cell_pass_backward_workspace(n_relay, e, n_cls, h), dev)
+    nbytes = e * 40 + min(e, n_w) * h * (x.element_size() + grad_out.element_size()) \
+        + min(e, n_cls) * h * emb.element_size() + 3 * n_relay * h * 4 + n_w * h * dx.element_size() \
+        + n_cls * h * d_emb.element_size()
+    _launch(f"cell_pass_backward_{_SHORT[x.dtype]}", nbytes, 5 * e * h, lambda: _check(
+        _lib().mantis_cell_pass_backward(
+            _ptr(x), _dt(x), x.stride(0), n_w, h, _ptr(emb), _dt(emb), emb.stride(0), n_cls, _ptr(grad_out),
+            _dt(grad_out), grad_out.stride(0), _ptr(cell_ptr), n_relay, _ptr(edge_window), _ptr(edge_class), e,
+            _ptr(win_ptr), _ptr(edge_wcell), _ptr(cls_ptr), _ptr(edge_ccell), _ptr(ws), ws.numel(), _ptr(dx),
+            _ptr(d_emb), _ptr(error_flag(dev)), _stream(),
+        ),
+        "cell_pass_backward",
+    ))
+    return dx, d_emb
+
+
 # ----------------------------------------------------------------- attention family
 
 
@@ -716,14 +857,22 @@ def fused_linear(x: Tensor, w1: Tensor, b1: Tensor | None = None, *, layer_norm:
                  add1: Tensor | None = None, add2: Tensor | None = None, add2_rows: Tensor | None = None,
                  relu: bool = False, w3: Tensor | None = None, b3: Tensor | None = None,
                  out: Tensor | None = None, out_dtype: torch.dtype = torch.float16,
-                 residual: bool = False) -> Tensor:
+                 residual: bool = False, split: bool = False) -> Tensor:
     """One fused row-GEMM launch (see mantis_fused_linear in
     include/mantis_hip.h).  ``residual=True`` adds into ``out`` (fp32, in
-    place); otherwise a new (m, width) tensor of ``out_dtype`` is returned."""
+    place); otherwise a new (m, width) tensor of ``out_dtype`` is returned.
+    ``split=True``: w1/w2 are compensated [hi; lo] pairs (2 n1 rows, see
+    ``split_weight``), for the launches mantis_fused_linear_split covers."""
     dev = _on_gpu(x, w1, b1, x_rows, x2, w2, add1, add2, add2_rows, w3, b3, out)
     if x.ndim != 2 or x.shape[1] < 128 or x.stride(1) != 1:
         raise ValueError("x must be (n, >=128) rows with unit column stride")
     m = x_rows.numel() if x_rows is not None else x.shape[0]
+    if split:
+        if w1.shape[0] % 2 or w3 is not None:
+            raise ValueError("split weights are [hi; lo] row pairs, single stage")
+        w1_full, w2_full = w1, w2
+        w1 = w1[: w1.shape[0] // 2]
+        w2 = None if w2 is None else w2[: w2.shape[0] // 2]
     n1 = w1.shape[0]
     width = w3.shape[0] if w3 is not None else n1
     for t, name in ((w1, "w1"), (w2, "w2"), (w3, "w3")):
@@ -764,7 +913,12 @@ def fused_linear(x: Tensor, w1: Tensor, b1: Tensor | None = None, *, layer_norm:
     flops = 2 * m * (128 * n1 * (2 if w2 is not None else 1) + (n1 * width if w3 is not None else 0))
     kind = "mlp" if w3 is not None else ("residual" if residual else "proj")
     name = f"fused_linear_{kind}_{_SHORT[x.dtype]}" + (f"_{_SHORT[x2.dtype]}" if x2 is not None else "") + f"_n{n1}"
-    st = _launch(name, nbytes, flops, lambda: _lib().mantis_fused_linear(
+    entry = _lib().mantis_fused_linear
+    if split:
+        name += "_split"
+        entry = _lib().mantis_fused_linear_split
+        w1, w2 = w1_full, w2_full
+    st = _launch(name, nbytes, flops, lambda: entry(
         _ptr(x), _dt(x), x.stride(0), _ptr(x_rows), x.shape[0], m, int(layer_norm),
         _ptr(x2), _dt(x2) if x2 is not None else 0, x2.stride(0) if x2 is not None else 0,
         _ptr(w1), _ptr(w2), _ptr(b1), n1, _ptr(add1), add1.stride(0) if add1 is not None else 0,
@@ -774,6 +928,14 @@ def fused_linear(x: Tensor, w1: Tensor, b1: Tensor | None = None, *, layer_norm:
     ))
     _check(st, "fused_linear")
     return out
+
+
+def split_weight(w: Tensor) -> Tensor:
+    """A weight as the compensated fp16 pair [hi; lo], hi = fp16(w) and
+    lo = fp16(w - hi): hi + lo carries ~22 mantissa bits of w."""
+    w = w.float()
+    hi = w.to(torch.float16)
+    return torch.cat([hi, (w - hi.float()).to(torch.float16)]).contiguous()
 
 
 def layer_norm(x: Tensor, gamma: Tensor, beta: Tensor, out_dtype: torch.dtype = torch.float32) -> Tensor:

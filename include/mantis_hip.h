@@ -54,7 +54,8 @@ int32_t mantis_runs_to_ptr(const int64_t* dest, int64_t n_entries, int64_t n_des
  * Run reduction: out[d, :] = sum over e in [ptr[d], ptr[d+1]) of
  * values[gather[e], :], accumulated in fp32, cast to out_dtype.  Rows with
  * no entries are written as zeros.  values is (n_src, ld) with the first `h`
- * columns read.  Replaces mantisnet::aggregate_to_windows,
+ * columns read; gather may be NULL, in which case entry e reads row e.
+ * Replaces mantisnet::aggregate_to_windows,
  * aggregate_to_stones, class_row_sum and incidence_row_sum
  * (python/mantisnet/mantisnet/message_passing.py:40-99, 191-227, 344-365).
  */
@@ -62,6 +63,72 @@ int32_t mantis_run_reduce(const void* values, int32_t values_dtype, int64_t n_sr
                           int64_t h, const int64_t* gather, int64_t n_entries,
                           const int64_t* ptr, int64_t n_dest, void* out, int32_t out_dtype,
                           int32_t* err_flag, void* stream);
+
+/*
+ * Class-major run reduction for unbounded runs:
+ *   out[k, :] = sum over e in [cls_ptr[k], cls_ptr[k+1]) of values[gather[e], :]
+ * fp32 sums in a fixed order: every run is cut into slices of 64 entries,
+ * each slice summed into a partial row, and each class's partials summed in
+ * slice order, so a class owning most of the entries does not serialise on
+ * one row.  Two calls agree bitwise.  values is (n_src, ld), first `h`
+ * columns read; out (n_classes, h) contiguous in out_dtype; workspace: at
+ * least mantis_class_reduce_workspace(n_entries, n_classes, h) bytes,
+ * 16-byte aligned.  The backward of mantisnet::class_row_sum
+ * (python/mantisnet/mantisnet/message_passing.py:380-397) over the
+ * class-sorted view of its entries, and the class gradient of the cell pass.
+ */
+int64_t mantis_class_reduce_workspace(int64_t n_entries, int64_t n_classes, int64_t h);
+int32_t mantis_class_reduce(const void* values, int32_t values_dtype, int64_t n_src, int64_t ld, int64_t h,
+                            const int64_t* gather, int64_t n_entries, const int64_t* cls_ptr, int64_t n_classes,
+                            void* workspace, int64_t workspace_bytes, void* out, int32_t out_dtype,
+                            int32_t* err_flag, void* stream);
+
+/*
+ * The knob-off cell pass (windows <- windows through shared empty cells):
+ *   val[c] = ReLU(sum over the cell's entries e of x[edge_window[e]] + emb[edge_class[e]])
+ *   out[w] = sum over the window's entries e of val[edge_wcell[e]]
+ * fp32 sums in a fixed order, `out` cast to x_dtype.  x is (n_windows, ldx)
+ * and emb (n_classes, lde), first `h` columns read, fp32/bf16/fp16 each;
+ * cell_ptr (n_relay + 1) indexes the cell-major entries edge_window /
+ * edge_class, win_ptr (n_windows + 1) the window-major entries edge_wcell
+ * (relay cell ids); val is an (n_relay, h) fp32 workspace (it holds the cell
+ * values afterwards); out is (n_windows, h) contiguous.  Out-of-range
+ * entries set MANTIS_FLAG_INDEX and are skipped.  Replaces
+ * mantisnet::cell_pass (python/mantisnet/mantisnet/relay.py:452-486, 577-591).
+ */
+int32_t mantis_cell_pass(const void* x, int32_t x_dtype, int64_t ldx, int64_t n_windows, int64_t h, const void* emb,
+                         int32_t emb_dtype, int64_t lde, int64_t n_classes, const int64_t* cell_ptr, int64_t n_relay,
+                         const int64_t* edge_window, const int64_t* edge_class, int64_t n_edges,
+                         const int64_t* win_ptr, const int64_t* edge_wcell, float* val, void* out,
+                         int32_t* err_flag, void* stream);
+
+/*
+ * Workspace bytes mantis_cell_pass_backward needs for these sizes (-1 on a
+ * negative size).
+ */
+int64_t mantis_cell_pass_backward_workspace(int64_t n_relay, int64_t n_edges, int64_t n_classes, int64_t h);
+
+/*
+ * Backward of mantis_cell_pass for an output gradient grad_out
+ * (n_windows, ldg) in grad_dtype:
+ *   d_pre[c] = (pre[c] > 0) * sum over the cell's entries of grad_out[edge_window[e]]
+ *   dx[w]    = sum over the window's entries of d_pre[edge_wcell[e]]   (x_dtype, contiguous)
+ *   d_emb[k] = sum over the class's entries of d_pre[edge_ccell[e]]     (emb_dtype, contiguous)
+ * with pre recomputed from x and emb; cls_ptr (n_classes + 1) indexes the
+ * class-major entries edge_ccell.  Every sum is fp32 in a fixed order
+ * (class runs in slices of 64 entries, then the slices in order), so two
+ * calls agree bitwise.  workspace: at least
+ * mantis_cell_pass_backward_workspace(...) bytes of device memory, 16-byte
+ * aligned.  Replaces mantisnet::cell_pass_backward
+ * (python/mantisnet/mantisnet/relay.py:503-544, 563-574).
+ */
+int32_t mantis_cell_pass_backward(const void* x, int32_t x_dtype, int64_t ldx, int64_t n_windows, int64_t h,
+                                  const void* emb, int32_t emb_dtype, int64_t lde, int64_t n_classes,
+                                  const void* grad_out, int32_t grad_dtype, int64_t ldg, const int64_t* cell_ptr,
+                                  int64_t n_relay, const int64_t* edge_window, const int64_t* edge_class,
+                                  int64_t n_edges, const int64_t* win_ptr, const int64_t* edge_wcell,
+                                  const int64_t* cls_ptr, const int64_t* edge_ccell, void* workspace,
+                                  int64_t workspace_bytes, void* dx, void* d_emb, int32_t* err_flag, void* stream);
 
 /*
  * Typed segment attention, one query row per CSR segment:
@@ -290,6 +357,26 @@ int32_t mantis_fused_linear(const void* x, int32_t x_dtype, int64_t ldx, const i
                             int32_t relu, const void* w3, const float* b3, int32_t n3,
                             int32_t out_mode, void* out, int64_t ldo, int32_t* err_flag,
                             void* stream);
+
+/*
+ * mantis_fused_linear with compensated weights: w1 and w2 are (2 n1, 128)
+ * fp16, the rows [hi; lo] of W with hi = fp16(W) and lo = fp16(W - hi), and
+ * every product runs on both halves into one fp32 accumulator, so the
+ * weights act with ~22 mantissa bits (the rows remain fp16 operands).
+ * Covered: n1 = 128, single stage, fp32 x: the LayerNorm projection (out_mode
+ * 0 or 1), the residual projection (out_mode 2, no LayerNorm) and a pair
+ * MLP's first layer relu(LN(x) W1^T + x2 W2^T + b1) with fp16 x2 (out_mode
+ * 1).  Used where rounding the weights to fp16 would be summed coherently
+ * (the knob-off cell pass's u_cp and mlp_cp, model.py:374-395).
+ */
+int32_t mantis_fused_linear_split(const void* x, int32_t x_dtype, int64_t ldx, const int64_t* x_rows,
+                                  int64_t n_x, int64_t m, int32_t layer_norm, const void* x2,
+                                  int32_t x2_dtype, int64_t ldx2, const void* w1, const void* w2,
+                                  const float* b1, int32_t n1, const float* add1, int64_t ld_add1,
+                                  const float* add2, const int64_t* add2_rows, int64_t n_add2,
+                                  int32_t relu, const void* w3, const float* b3, int32_t n3,
+                                  int32_t out_mode, void* out, int64_t ldo, int32_t* err_flag,
+                                  void* stream);
 
 /*
  * Row LayerNorm over rows of 128 features (eps 1e-5, biased variance), fp32

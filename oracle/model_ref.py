@@ -10,6 +10,8 @@ What each function follows (python/mantisnet/mantisnet/...):
 
 * ``forward`` / ``trunk`` / ``_block`` ........ model.py:898-1200, 543-692
 * ``_cell_stage`` ............................. model.py:397-490
+* ``cell_pass`` (knob-off relay) .............. relay.py:1-13 (the scatter form,
+  tests/test_relay.py:31-43); ``cell_pass_loops`` is the literal loop form
 * ``_latent_cycle`` ........................... model.py:492-541
 * ``value_head`` / ``cell_head_logits`` ....... model.py:1160-1183, 1111-1139
 * ``_action_contribution`` / ``_cell_scores`` . model.py:1031-1091
@@ -61,6 +63,7 @@ class Cfg:
     policy_hidden: int = 128
     value_hidden: int = 128
     cell_node_scope: str = "all"
+    cell_nodes: bool = True  # False: the knob-off cell pass, heads over decoder window sums
 
 
 # ----------------------------------------------------------------- primitives
@@ -83,6 +86,30 @@ def run_sum(values, gather, dest, n_dest):
     """out[d] = sum of values[gather[e]] over entries with dest[e] == d, fp32."""
     rows = values.float().index_select(0, gather)
     return torch.zeros(n_dest, values.shape[1], dtype=torch.float32).index_add_(0, dest, rows)
+
+
+def cell_pass(x, emb, dec_cell, dec_window, dec_class, n_cells):
+    """The knob-off cell pass over the raw decoder incidence: every cell sums
+    its entries' window rows plus class rows, ReLU, and every window sums its
+    entries' cell values; fp32."""
+    msg = x.float().index_select(0, dec_window) + emb.float().index_select(0, dec_class)
+    cells = torch.zeros(n_cells, x.shape[1], dtype=torch.float32).index_add_(0, dec_cell, msg).relu()
+    return torch.zeros(x.shape[0], x.shape[1], dtype=torch.float32).index_add_(
+        0, dec_window, cells.index_select(0, dec_cell))
+
+
+def cell_pass_loops(x, emb, dec_cell, dec_window, dec_class, n_cells):
+    """``cell_pass`` as literal Python loops (small inputs only)."""
+    h = x.shape[1]
+    pre = [[0.0] * h for _ in range(n_cells)]
+    for c, w, k in zip(dec_cell.tolist(), dec_window.tolist(), dec_class.tolist()):
+        for j in range(h):
+            pre[c][j] += float(x[w, j]) + float(emb[k, j])
+    out = torch.zeros(x.shape[0], h, dtype=torch.float64)
+    for c, w in zip(dec_cell.tolist(), dec_window.tolist()):
+        for j in range(h):
+            out[w, j] += max(pre[c][j], 0.0)
+    return out
 
 
 def incidence_plan(inc_stone, inc_window, inc_class):
@@ -348,8 +375,14 @@ def _block(sd, i, cfg, b, s, w, g, c, seq_lens, plan, layout, ctab, radius, ws_r
     x = lin(ln(s, sd, pre + "ln_ws_s"), sd, pre + "u")
     agg = run_sum(x, b["inc_stone"], b["inc_window"], w.shape[0]) + ws_rows
     w = w + pair_mlp(ln(w, sd, pre + "ln_ws_w"), agg, sd, pre + "mlp_w")
-    # §5.1b cell stage
-    w, c = _cell_stage(sd, pre, cfg, s, w, c, ctab, radius)
+    # §5.1b cell stage, or the knob-off cell pass (model.py:374-395)
+    if cfg.cell_nodes:
+        w, c = _cell_stage(sd, pre, cfg, s, w, c, ctab, radius)
+    else:
+        x = lin(ln(w, sd, pre + "ln_cp_in"), sd, pre + "u_cp")
+        agg = cell_pass(x, sd[pre + "e_cp.weight"], b["dec_cell"], b["dec_window"], b["dec_class"],
+                        b["cell_pos"].shape[0])
+        w = w + pair_mlp(ln(w, sd, pre + "ln_cp_w"), agg, sd, pre + "mlp_cp")
     # §5.2 stones <- windows
     y = lin(ln(w, sd, pre + "ln_sw_w"), sd, pre + "v")
     agg = run_sum(y, run_window, run_stone, s.shape[0]) + sw_rows
@@ -396,12 +429,14 @@ def trunk(sd, cfg, b, pattern_counts):
     plan = incidence_plan(b["inc_stone"], b["inc_window"], b["inc_class"])
     window_pos = b["window_slot"] // b["value_valid"].shape[1]
     offsets, order = window_layout(window_pos, p)
-    ctab = cell_tables(b["dec_cell"], b["dec_window"], b["dec_class"], w.shape[0], n_c)
-    c = sd["cell_nearest_table.weight"][b["cell_nearest"]].clone()
-    c[ctab["covered"]] = sd["cell_base"]
-    classes = b["radius_orbit"] + ORBIT48 * (b["radius_own"] + 2 * b["radius_on_axis"])
-    radius = edge_tables(b["radius_src"], b["radius_dst"], classes, ctab["covered"], n_c,
-                         cfg.cell_node_scope == "uncovered")
+    ctab = c = radius = None
+    if cfg.cell_nodes:
+        ctab = cell_tables(b["dec_cell"], b["dec_window"], b["dec_class"], w.shape[0], n_c)
+        c = sd["cell_nearest_table.weight"][b["cell_nearest"]].clone()
+        c[ctab["covered"]] = sd["cell_base"]
+        classes = b["radius_orbit"] + ORBIT48 * (b["radius_own"] + 2 * b["radius_on_axis"])
+        radius = edge_tables(b["radius_src"], b["radius_dst"], classes, ctab["covered"], n_c,
+                             cfg.cell_node_scope == "uncovered")
     seq_lens = b["attn_valid"].sum(1)
     ws_all = (pattern_counts @ torch.cat([sd[f"blocks.{i}.e_ws.weight"] for i in range(cfg.blocks)], 1))[b["window_feat"]]
     sw_all = run_sum(torch.cat([sd[f"blocks.{i}.e_sw.weight"] for i in range(cfg.blocks)], 1), plan[2], plan[0], s.shape[0])
@@ -409,7 +444,7 @@ def trunk(sd, cfg, b, pattern_counts):
         sl = slice(i * h, (i + 1) * h)
         s, w, g, c = _block(sd, i, cfg, b, s, w, g, c, seq_lens, plan, (window_pos, offsets, order),
                             ctab, radius, ws_all[:, sl], sw_all[:, sl], i + 1 < cfg.blocks)
-    return ln(w, sd, "ln_out"), ln(g, sd, "ln_out").mean(1), ln(c, sd, "ln_out")
+    return ln(w, sd, "ln_out"), ln(g, sd, "ln_out").mean(1), (ln(c, sd, "ln_out") if c is not None else None)
 
 
 def value_head(sd, cfg, b, w, g):
@@ -437,6 +472,8 @@ def action_contribution(sd, b, w, empty_classes):
 def cell_head_logits(sd, cfg, b, w, g, cells, empty_classes):
     acts = action_contribution(sd, b, w, empty_classes)
     n_c = b["cell_pos"].shape[0]
+    if cells is None:  # cell state off: each cell reads its decoder windows' sum (model.py:985-1029)
+        cells = run_sum(w, b["dec_window"], b["dec_cell"], n_c)
     extra = run_sum(torch.cat([sd["e_pw.weight"], sd["e_qw.weight"]], 1), b["dec_class"], b["dec_cell"], n_c)
     outs = []
     for head, proj, ext, mlp, sl in (("p", "p", "p_act", "mlp_p", slice(0, cfg.h)),

@@ -21,7 +21,7 @@ def _declarations(header: str) -> dict[str, int]:
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     text = re.sub(r"//[^\n]*", "", text)
     out = {}
-    for m in re.finditer(r"\b(?:int32_t|void)\s+(\w+)\s*\(([^)]*)\)\s*;", text):
+    for m in re.finditer(r"\b(?:int32_t|int64_t|void)\s+(\w+)\s*\(([^)]*)\)\s*;", text):
         params = m.group(2).strip()
         out[m.group(1)] = 0 if params in ("", "void") else params.count(",") + 1
     return out

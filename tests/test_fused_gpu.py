@@ -335,3 +335,47 @@ def test_latent_mix_matches_the_fp32_formulation(device):
     got = g.to(device)
     ops.latent_mix(got, w.t().contiguous().to(device), b.to(device), wo.t().contiguous().to(device), bo.to(device))
     torch.testing.assert_close(got.cpu(), ref, rtol=1e-5, atol=2e-5)
+
+
+def test_compensated_weights_act_as_fp32(device):
+    """Split [hi; lo] weights: every launch the split entry covers matches
+    fp32 weights (operands: the fp16-rounded rows), far inside the error of
+    fp16-rounded weights."""
+    gen = _g(41)
+    m = 700
+    # rows of +-2 with as many signs of each kind: the mean is exactly 0, so
+    # LN(x) rounds to exactly +-1 in fp16 on both sides and the comparison
+    # sees the weights' precision alone
+    signs = torch.ones(m, 128)
+    signs[:, 64:] = -1
+    x = 2 * torch.gather(signs, 1, torch.argsort(torch.rand(m, 128, generator=gen), dim=1))
+    x2 = _h(3 * torch.randn(m, 128, generator=gen))
+    w1 = torch.randn(128, 128, generator=gen) / math.sqrt(128)
+    w2 = torch.randn(128, 128, generator=gen) / math.sqrt(128)
+    b = 0.1 * torch.randn(128, generator=gen)
+    d = lambda t: t.to(device)  # noqa: E731
+    sw1, sw2 = d(ops.split_weight(w1)), d(ops.split_weight(w2))
+    # hi + lo reproduces the fp32 weight to ~2^-22 relative
+    assert (sw1[:128].float().cpu() + sw1[128:].float().cpu() - w1).abs().max() < 1e-6
+
+    def close(got, exp, fp16_weights_exp):
+        err = (got.float().cpu() - exp).abs().max().item()
+        err16 = (fp16_weights_exp - exp).abs().max().item()
+        assert err <= 2e-5 * max(1.0, exp.abs().max().item()), err
+        assert err < err16 / 8, (err, err16)
+
+    # LayerNorm projection, fp32 out
+    got = ops.fused_linear(d(x), sw1, d(b), layer_norm=True, out_dtype=torch.float32, split=True)
+    xn = _h(_ln(x))
+    close(got, xn @ w1.t() + b, xn @ w1.to(H16).float().t() + b)
+    # pair-MLP first layer: relu(LN(x) W1^T + x2 W2^T + b), fp32 out
+    got = ops.fused_linear(d(x), sw1, d(b), layer_norm=True, x2=d(x2.to(H16)), w2=sw2, relu=True,
+                           out_dtype=torch.float32, split=True)
+    close(got, F.relu(xn @ w1.t() + x2 @ w2.t() + b),
+          F.relu(xn @ w1.to(H16).float().t() + x2 @ w2.to(H16).float().t() + b))
+    # residual projection: out += x W^T + b
+    base = torch.randn(m, 128, generator=gen)
+    out = d(base.clone())
+    ops.fused_linear(d(x), sw1, d(b), out=out, residual=True, split=True)
+    close(out, base + _h(x) @ w1.t() + b, base + _h(x) @ w1.to(H16).float().t() + b)
+    ops.raise_on_device_error(device)

@@ -24,7 +24,8 @@ OPS = torch.ops.mantisnet
 # The reference's operator signatures: argument names in order and the
 # number of outputs (attention.py:719-725, message_passing.py:191-227 and
 # 344-365, cell_latents.py:168-183 and 834-940, cell_nodes.py:97-123,
-# window_latents.py:38-56, 553-560 and 648-651, row_encoder.py:368-380).
+# window_latents.py:38-56, 553-560 and 648-651, row_encoder.py:368-380,
+# relay.py:452-514).
 REFERENCE_SCHEMAS = {
     "fused_attention": (["q", "k", "v", "seq_lens"], 2),
     "aggregate_to_windows": (["values", "inc_stone", "inc_window", "run_stone", "run_window", "n_windows"], 1),
@@ -43,6 +44,11 @@ REFERENCE_SCHEMAS = {
     "cell_node_edge_tables": (["src", "dst", "cls", "covered_destinations", "n_sources", "n_destinations",
                                "n_classes", "uncovered_only"], 12),
     "window_latent_layout": (["window_pos", "positions"], 2),
+    # relay.py:452-462 and 503-514
+    "cell_pass": (["x", "emb", "cell_ptr", "edge_window", "edge_class", "win_ptr", "edge_wcell", "cls_ptr",
+                   "edge_ccell"], 1),
+    "cell_pass_backward": (["x", "emb", "cell_ptr", "edge_window", "edge_class", "win_ptr", "edge_wcell", "cls_ptr",
+                            "edge_ccell", "grad_out"], 2),
 }
 
 
