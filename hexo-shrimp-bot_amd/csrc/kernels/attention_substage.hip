@@ -32,6 +32,11 @@
 // the workgroups of one XCD (dispatch is round-robin over the 8 XCDs) sweep
 // one contiguous eighth of the rows, so the gathered k/v rows of a position
 // stay in that XCD's L2.
+//
+// A tile's entry loop runs as long as its longest row.  An optional row
+// order (a permutation of the rows) groups rows of similar entry counts into
+// tiles; each row's arithmetic is the same in any order, so the results are
+// bitwise those of the natural order.
 #include "common.hpp"
 #include "mfma.hpp"
 
@@ -68,6 +73,7 @@ struct SubArgs {
   float* x;
   int64_t ldx;
   int64_t n_rows;
+  const int32_t* order;  // tile slot -> row, or null for the natural order
   Stage st[2];
   float scale;
   int32_t* flag;
@@ -154,13 +160,25 @@ __global__ void __launch_bounds__(kThreads) attn_substage_kernel(SubArgs a) {
   // their values are used: a check right after the load would make the
   // wavefront wait for it there, and with in-order load counters also for
   // every row load issued before it.
-  for (int64_t tile = t_begin + int64_t(blockIdx.x / kXcds) * kWaves + wave; tile < t_end; tile += waves_here) {
+  // the row of a tile slot (raw: validated where it is used); slots past the
+  // end read entry 0 of the order
+  auto order_at = [&](int64_t t) -> int64_t {
+    const int64_t slot = t * 16 + l16;
+    if (!a.order) return slot;
+    return a.order[slot < a.n_rows ? slot : 0];
+  };
+  const int64_t tile0 = t_begin + int64_t(blockIdx.x / kXcds) * kWaves + wave;
+  int64_t next_row = tile0 < t_end ? order_at(tile0) : 0;
+  for (int64_t tile = tile0; tile < t_end; tile += waves_here) {
     // an offset the compiler cannot see through: keeps the weight-fragment
     // reads inside the loop instead of hoisting all of them into registers
     int lds_off = 0;
     asm volatile("" : "+s"(lds_off));
-    const int64_t row = tile * 16 + l16;
-    const bool live = row < a.n_rows;
+    const int64_t row = next_row;
+    next_row = order_at(tile + waves_here < t_end ? tile + waves_here : tile);  // one tile ahead
+    const bool in_tile = tile * 16 + l16 < a.n_rows;
+    const bool live = in_tile && row >= 0 && row < a.n_rows;
+    if (in_tile && !live) raise_flag(a.flag, MANTIS_FLAG_INDEX);
     const int64_t rc = live ? row : 0;  // dead lanes read a real row and store nothing
     // the entry walk's pointers first (the first entries depend on them), then x
     int64_t pa[kStages], pb[kStages];
@@ -392,19 +410,21 @@ Stage to_stage(const mantis_substage& d) {
 
 using namespace mantis;
 
-extern "C" int32_t mantis_attention_substages(float* x, int64_t ldx, int64_t n_rows, const mantis_substage* stages,
-                                              int32_t n_stages, int32_t* err_flag, void* stream) {
+extern "C" int32_t mantis_attention_substages(float* x, int64_t ldx, int64_t n_rows, const int32_t* row_order,
+                                              const mantis_substage* stages, int32_t n_stages, int32_t* err_flag,
+                                              void* stream) {
   if (n_rows < 0 || !stages || n_stages < 1 || n_stages > 2) return MANTIS_E_ARG;
   if (n_rows == 0) return MANTIS_OK;
   for (int s = 0; s < n_stages; ++s)
     if (!stage_ok(stages[s])) return MANTIS_E_ARG;
   // both stages of a pass carry class values, or neither does
   if (n_stages == 2 && (stages[0].vcls == nullptr) != (stages[1].vcls == nullptr)) return MANTIS_E_ARG;
-  if (!x || ldx < kK || ldx % 4 || !aligned16(x)) return MANTIS_E_ARG;
+  if (!x || ldx < kK || ldx % 4 || !aligned16(x) || n_rows > 2147483647LL) return MANTIS_E_ARG;
   SubArgs a{};
   a.x = x;
   a.ldx = ldx;
   a.n_rows = n_rows;
+  a.order = row_order;
   for (int s = 0; s < n_stages; ++s) a.st[s] = to_stage(stages[s]);
   a.scale = 0.17677669529663687f;  // 1/sqrt(32)
   a.flag = err_flag;
@@ -420,5 +440,5 @@ extern "C" int32_t mantis_attention_substage(float* x, int64_t ldx, int64_t n_ro
                                              int64_t n_entries, const void* wo, const float* bo,
                                              int32_t* err_flag, void* stream) {
   const mantis_substage d{wq, bq, k, v, ldk, ldv, n_src, bias, n_classes, vcls, seg_ptr, src, cls, n_entries, wo, bo};
-  return mantis_attention_substages(x, ldx, n_rows, &d, 1, err_flag, stream);
+  return mantis_attention_substages(x, ldx, n_rows, nullptr, &d, 1, err_flag, stream);
 }

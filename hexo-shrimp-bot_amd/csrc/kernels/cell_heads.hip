@@ -20,7 +20,10 @@
 // tiles are packed to fp16 as the second product's B fragments (K slots
 // {4g..4g+3, 16+4g..16+4g+3} of each 32-step, matched by the W3 reads).
 // W1, W2 and W3 live in LDS for the persistent workgroup (8 wavefronts,
-// one workgroup per CU).
+// one workgroup per CU).  An optional row order (a permutation of the cells)
+// groups cells of similar decoder run lengths into tiles, since a tile's
+// walk runs as long as its longest run; each cell's arithmetic is the same
+// in any order.
 #include "common.hpp"
 #include "mfma.hpp"
 
@@ -64,6 +67,7 @@ struct HeadArgs {
   const int64_t* dec_class;
   int64_t n_entries;
   float* out;                // (n_cells, 16)
+  const int32_t* order;      // tile slot -> cell, or null
   int32_t* flag;
 };
 
@@ -89,7 +93,16 @@ __global__ void __launch_bounds__(kThreads) cell_heads_kernel(HeadArgs a) {
   const int src_m = 16 * aq + ar;                  // MFMA lane of this walk lane's (cell, group)
   const int src_a = 4 * l16 + g;                   // walk lane of this MFMA lane's (cell, group)
   const int64_t n_tiles = (a.n_cells + 15) / 16;
-  for (int64_t tile = int64_t(blockIdx.x) * kWaves + wave; tile < n_tiles; tile += int64_t(gridDim.x) * kWaves) {
+  const int64_t stride = int64_t(gridDim.x) * kWaves;
+  // the cell of a tile slot (raw: validated where it is used), one tile ahead
+  auto order_at = [&](int64_t t) -> int64_t {
+    const int64_t slot = t * 16 + l16;
+    if (!a.order) return slot;
+    return a.order[slot < a.n_cells ? slot : 0];
+  };
+  const int64_t tile0 = int64_t(blockIdx.x) * kWaves + wave;
+  int64_t next_row = tile0 < n_tiles ? order_at(tile0) : 0;
+  for (int64_t tile = tile0; tile < n_tiles; tile += stride) {
     // an offset the compiler cannot see through: keeps the weight-fragment
     // reads inside the loop instead of hoisting them into registers
     int lds_off = 0;
@@ -97,8 +110,11 @@ __global__ void __launch_bounds__(kThreads) cell_heads_kernel(HeadArgs a) {
     const _Float16* w1s = sw1 + lds_off;
     const _Float16* w2s = sw2 + lds_off;
     const _Float16* w3s = sw3 + lds_off;
-    const int64_t row = tile * 16 + l16;
-    const bool live = row < a.n_cells;
+    const int64_t row = next_row;
+    next_row = order_at(tile + stride < n_tiles ? tile + stride : tile);
+    const bool in_tile = tile * 16 + l16 < a.n_cells;
+    const bool live = in_tile && row >= 0 && row < a.n_cells;
+    if (in_tile && !live) raise_flag(a.flag, MANTIS_FLAG_INDEX);
     const int64_t rc = live ? row : 0;  // dead lanes read a real row and store nothing
     // ---- the cell's decoder run and position, then its row
     int64_t st = a.dec_ptr[rc], en = a.dec_ptr[rc + 1];
@@ -202,10 +218,11 @@ __global__ void __launch_bounds__(kThreads) cell_heads_kernel(HeadArgs a) {
         }
       }
     }
-    // EMPTY-class action rows, weighted by the cell's counts
+    // EMPTY-class action rows, weighted by the cell's counts (the walk lane's
+    // cell: the row of MFMA lane src_m; cell indices fit int32, host check)
     {
-      const int64_t arow = tile * 16 + ar;
-      if (arow < a.n_cells) {
+      const int64_t arow = from_lane(src_m, int32_t(rc));
+      if (from_lane(src_m, int32_t(live))) {
 #pragma unroll
         for (int o = 0; o < 3; ++o) {
           const float n = float(a.act_empty[arow * 3 + o]);
@@ -297,7 +314,7 @@ __global__ void __launch_bounds__(kThreads) cell_heads_kernel(HeadArgs a) {
 using namespace mantis;
 
 extern "C" int32_t mantis_cell_heads(const void* c, int32_t c_dtype, int32_t layer_norm, int64_t ldc, int64_t n_cells,
-                                     const void* w1, const float* b1,
+                                     const int32_t* row_order, const void* w1, const float* b1,
                                      const void* w2, const void* w3, const float* b3, const void* pre, int64_t n_w,
                                      const void* act_table, int64_t n_acls, const float* empty_rows,
                                      const int64_t* act_empty, const void* head_tab, int64_t n_dcls,
@@ -314,6 +331,7 @@ extern "C" int32_t mantis_cell_heads(const void* c, int32_t c_dtype, int32_t lay
     return MANTIS_E_ARG;
   // gathered rows use 32-bit element offsets
   if (n_w > 4294967295LL / kK || n_acls > 4294967295LL / kK || n_dcls > 4294967295LL / kN1) return MANTIS_E_ARG;
+  if (n_cells > 2147483647LL) return MANTIS_E_ARG;  // cell indices move between lanes as int32
   for (const void* p : {c, w1, static_cast<const void*>(b1), w2, w3,
                         static_cast<const void*>(b3), act_table,
                         static_cast<const void*>(empty_rows), head_tab,
@@ -324,7 +342,7 @@ extern "C" int32_t mantis_cell_heads(const void* c, int32_t c_dtype, int32_t lay
              static_cast<const _Float16*>(w3), b3, static_cast<const _Float16*>(pre), n_w,
              static_cast<const _Float16*>(act_table), n_acls, empty_rows, act_empty,
              static_cast<const _Float16*>(head_tab), n_dcls, g_half, n_pos, cell_pos, dec_ptr, dec_window, act_class,
-             dec_class, n_entries, out, err_flag};
+             dec_class, n_entries, out, row_order, err_flag};
   int dev = 0, cus = 0;
   if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
                                               hipSuccess || cus <= 0)

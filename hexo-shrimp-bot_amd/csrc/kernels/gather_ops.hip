@@ -41,6 +41,52 @@ __global__ void runs_to_ptr_kernel(const int64_t* __restrict__ dest, int64_t n, 
   for (int64_t d = prev + 1; d <= cur; ++d) ptr[d] = e;
 }
 
+// ------------------------------------------------------------ tile orders
+
+// Within every segment [seg_ptr[s], seg_ptr[s+1]) of the rows, the rows in
+// ascending (run length in ptr_a clamped to 31, run length in ptr_b clamped
+// to 63): one workgroup per segment, a counting sort over the 2048 keys in
+// LDS.  Rows of one key keep no particular order (the consumers' results do
+// not depend on it).
+constexpr int kOrderBuckets = 2048;
+
+__global__ void __launch_bounds__(256)
+segment_order_kernel(const int64_t* __restrict__ seg_ptr, int64_t n_seg, const int64_t* __restrict__ ptr_a,
+                     const int64_t* __restrict__ ptr_b, int64_t n_rows, int32_t* __restrict__ order,
+                     int32_t* flag) {
+  __shared__ int32_t count[kOrderBuckets];
+  // the segments must tile [0, n_rows) in order, or some order slots stay unwritten
+  if (blockIdx.x == 0 && threadIdx.x == 0 && (seg_ptr[0] != 0 || seg_ptr[n_seg] != n_rows))
+    raise_flag(flag, MANTIS_FLAG_ORDER);
+  for (int64_t sg = blockIdx.x; sg < n_seg; sg += gridDim.x) {
+    int64_t lo, hi;
+    segment(seg_ptr, sg, n_rows, lo, hi);
+    if (threadIdx.x == 0 && seg_ptr[sg + 1] < seg_ptr[sg]) raise_flag(flag, MANTIS_FLAG_ORDER);
+    for (int k = threadIdx.x; k < kOrderBuckets; k += blockDim.x) count[k] = 0;
+    __syncthreads();
+    auto key_of = [&](int64_t r) {
+      const int64_t na = ptr_a[r + 1] - ptr_a[r];
+      const int64_t nb = ptr_b ? ptr_b[r + 1] - ptr_b[r] : 0;
+      return int((na < 0 ? 0 : (na > 31 ? 31 : na)) << 6 | (nb < 0 ? 0 : (nb > 63 ? 63 : nb)));
+    };
+    for (int64_t r = lo + threadIdx.x; r < hi; r += blockDim.x) atomicAdd(&count[key_of(r)], 1);
+    __syncthreads();
+    // exclusive prefix sum of the counts (one thread: 2048 adds)
+    if (threadIdx.x == 0) {
+      int32_t run = 0;
+      for (int k = 0; k < kOrderBuckets; ++k) {
+        const int32_t c = count[k];
+        count[k] = run;
+        run += c;
+      }
+    }
+    __syncthreads();
+    for (int64_t r = lo + threadIdx.x; r < hi; r += blockDim.x)
+      order[lo + atomicAdd(&count[key_of(r)], 1)] = int32_t(r);
+    __syncthreads();  // count is reset by the next segment
+  }
+}
+
 // ------------------------------------------------------------ run reduction
 
 template <typename Tin, typename Tout>
@@ -496,6 +542,16 @@ int32_t mantis_runs_to_ptr(const int64_t* dest, int64_t n_entries, int64_t n_des
   const int64_t threads = n_entries + 1;
   runs_to_ptr_kernel<<<unsigned((threads + 255) / 256), 256, 0, as_stream(stream)>>>(
       dest, n_entries, n_dest, ptr, err_flag);
+  return launched();
+}
+
+int32_t mantis_segment_order(const int64_t* seg_ptr, int64_t n_seg, const int64_t* ptr_a, const int64_t* ptr_b,
+                             int64_t n_rows, int32_t* order, int32_t* err_flag, void* stream) {
+  if (n_rows == 0) return MANTIS_OK;
+  if (!seg_ptr || !ptr_a || !order || n_seg <= 0 || n_rows < 0 || n_rows > 2147483647LL) return MANTIS_E_ARG;
+  const int64_t grid = n_seg < 4096 ? n_seg : 4096;
+  segment_order_kernel<<<unsigned(grid), 256, 0, as_stream(stream)>>>(seg_ptr, n_seg, ptr_a, ptr_b, n_rows, order,
+                                                                       err_flag);
   return launched();
 }
 

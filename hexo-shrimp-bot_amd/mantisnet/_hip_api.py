@@ -25,6 +25,7 @@ class MantisSubstage(ctypes.Structure):
 SIGNATURES = {
     "mantis_hip_version": ([], i32),
     "mantis_runs_to_ptr": ([vp, i64, i64, vp, vp, vp], i32),
+    "mantis_segment_order": ([vp, i64, vp, vp, i64, vp, vp, vp], i32),
     "mantis_run_reduce": ([vp, i32, i64, i64, i64, vp, i64, vp, i64, vp, i32, vp, vp], i32),
     "mantis_class_reduce_workspace": ([i64, i64, i64], i64),
     "mantis_class_reduce": ([vp, i32, i64, i64, i64, vp, i64, vp, i64, vp, i64, vp, i32, vp, vp], i32),
@@ -38,9 +39,9 @@ SIGNATURES = {
         i32),
     "mantis_attention_substage": (
         [vp, i64, i64, vp, vp, vp, vp, i64, i64, i64, vp, i64, vp, vp, vp, vp, i64, vp, vp, vp, vp], i32),
-    "mantis_attention_substages": ([vp, i64, i64, vp, i32, vp, vp], i32),
+    "mantis_attention_substages": ([vp, i64, i64, vp, vp, i32, vp, vp], i32),
     "mantis_cell_heads": (
-        [vp, i32, i32, i64, i64, vp, vp, vp, vp, vp, vp, i64, vp, i64, vp, vp, vp, i64, vp, i64, vp, vp, vp, vp, vp,
+        [vp, i32, i32, i64, i64, vp, vp, vp, vp, vp, vp, vp, i64, vp, i64, vp, vp, vp, i64, vp, i64, vp, vp, vp, vp, vp,
          i64, vp, vp, vp], i32),
     "mantis_improve_policy": ([vp, vp, vp, i32, vp, i64, i64, ctypes.c_double, ctypes.c_double, vp, vp, vp, vp, vp, vp],
                               i32),

@@ -261,6 +261,8 @@ class Plan:
     win_ptr: Tensor  # window-major decoder CSR
     edge_wcell: Tensor
     edge_wclass: Tensor
+    cell_order: Tensor | None  # int32 tile order of the cell stages (cell-node configurations)
+    head_order: Tensor  # int32 tile order of the fused heads
     radius_ptr: Tensor | None  # radius views: cell-node configurations only
     radius_src: Tensor | None
     radius_class: Tensor | None
@@ -330,7 +332,7 @@ def make_plan(model, b: Batch) -> Plan:
     covered = cell_ptr[1:] > cell_ptr[:-1]
     win_ptr = ops.runs_to_ptr(edge_window[worder].contiguous(), n_w)
     # radius edge tables (cell_nodes.py:23-94, model.py:843-859)
-    radius_ptr = radius_src = radius_class = None
+    radius_ptr = radius_src = radius_class = cell_order = None
     if cfg.cell_nodes:
         if cfg.cell_node_scope == "uncovered":
             keep = ~covered[dst]
@@ -341,6 +343,11 @@ def make_plan(model, b: Batch) -> Plan:
             rorder = _stable_order(dst)
             radius_src, radius_dst, radius_class = src[rorder], dst[rorder], classes[rorder]
         radius_ptr = ops.runs_to_ptr(radius_dst.contiguous(), n_c)
+        # the fused cell stages run each 16-cell tile as long as its longest
+        # entry run: within each position, visit cells by (decoder entries,
+        # radius entries) so tiles hold cells of like counts (the cells of a
+        # position stay together, and with them the k/v rows they gather)
+        cell_order = ops.segment_order(b.legal_offsets, cell_ptr, radius_ptr, n_c)
     # attention rows [latents; stones] per position over the [s; g] buffer
     gslot = (torch.arange(p, device=dev)[:, None] * max_t + torch.arange(GLOBAL_ROWS, device=dev)[None, :]).reshape(-1)
     attn_src = torch.full((p * max_t,), -1, dtype=torch.long, device=dev)
@@ -355,6 +362,10 @@ def make_plan(model, b: Batch) -> Plan:
         window_pos=window_pos, layout_offsets=offsets, layout_order=lorder,
         covered_mask=covered, cell_ptr=cell_ptr, edge_window=edge_window, edge_class=edge_class,
         win_ptr=win_ptr, edge_wcell=edge_cell[worder], edge_wclass=edge_class[worder],
+        cell_order=cell_order,
+        # the heads walk the same decoder runs (cell_ptr has the batch's run
+        # lengths in any entry order), so the stages' order serves them too
+        head_order=cell_order if cell_order is not None else ops.segment_order(b.legal_offsets, cell_ptr, None, n_c),
         radius_ptr=radius_ptr, radius_src=radius_src, radius_class=radius_class,
         seq_lens=b.attn_valid.sum(dim=1, dtype=torch.int32), attn_src=attn_src, attn_back=attn_back,
         dec_cell_ptr=cell_ptr if canonical else ops.runs_to_ptr(b.dec_cell, n_c),
@@ -403,7 +414,7 @@ def _cell_stage(W, P, pb, plan: Plan, s, w, c):
                    plan.edge_window, plan.edge_class)
     rad = _substage(W, P, pb, "rad", _proj(W, pb + "rad_kv", s), "radius_bias", W[pb + "rad_vcls"],
                     plan.radius_ptr, plan.radius_src, plan.radius_class)
-    ops.attention_substages(c, [cr, rad])
+    ops.attention_substages(c, [cr, rad], row_order=plan.cell_order)
     wr = _substage(W, P, pb, "wr", _proj(W, pb + "wr_kv", c), "wr_bias", None, plan.win_ptr, plan.edge_wcell,
                    plan.edge_wclass)
     ops.attention_substages(w, [wr])
@@ -570,7 +581,8 @@ def _head_rows(model, w: Tensor, g: Tensor, cells: Tensor, b: Batch, plan: Plan,
     key = "head1ln" if raw_cells else "head1"
     return ops.cell_heads(x.contiguous(), W[key + ".w"], W[key + ".b"], W["head2.w"], W["head3.w"], W["head3.b"], pre,
                           P["act_table.weight"], empty_rows, b.act_empty, W["head_tab"], g_half, b.cell_pos,
-                          plan.dec_cell_ptr, b.dec_window, b.act_class, b.dec_class, layer_norm=raw_cells)
+                          plan.dec_cell_ptr, b.dec_window, b.act_class, b.dec_class, layer_norm=raw_cells,
+                          row_order=plan.head_order)
 
 
 @torch.no_grad()

@@ -205,6 +205,24 @@ def runs_to_ptr(dest: Tensor, n_dest: int) -> Tensor:
     return ptr
 
 
+def segment_order(seg_ptr: Tensor, ptr_a: Tensor, ptr_b: Tensor | None, n_rows: int) -> Tensor:
+    """int32 permutation of the rows: within each segment of ``seg_ptr``, rows
+    by ascending (run length in ptr_a up to 31, in ptr_b up to 63) — the
+    tile order of the fused cell kernels."""
+    dev = _on_gpu(seg_ptr, ptr_a, ptr_b)
+    seg_ptr, ptr_a = _i64(seg_ptr, "seg_ptr"), _i64(ptr_a, "ptr_a")
+    ptr_b = None if ptr_b is None else _i64(ptr_b, "ptr_b")
+    if ptr_a.numel() != n_rows + 1 or (ptr_b is not None and ptr_b.numel() != n_rows + 1):
+        raise ValueError("ptr_a / ptr_b must have n_rows + 1 entries")
+    if seg_ptr.numel() < 2:
+        raise ValueError("seg_ptr must hold at least one segment")
+    order = torch.empty(n_rows, dtype=torch.int32, device=dev)
+    _launch("segment_order", 8 * (seg_ptr.numel() + 2 * (n_rows + 1)) + 4 * n_rows, 0, lambda: _check(
+        _lib().mantis_segment_order(_ptr(seg_ptr), seg_ptr.numel() - 1, _ptr(ptr_a), _ptr(ptr_b), n_rows, _ptr(order),
+                                    _ptr(error_flag(dev)), _stream()), "segment_order"))
+    return order
+
+
 # ----------------------------------------------------------------- run reduction
 
 
@@ -519,15 +537,21 @@ def _substage_struct(st: SubStage, n: int):
     return d, (bias, vcls, seg_ptr, src, cls), e
 
 
-def attention_substages(x: Tensor, stages: list[SubStage]) -> Tensor:
+def attention_substages(x: Tensor, stages: list[SubStage], row_order: Tensor | None = None) -> Tensor:
     """In place on the fp32 residual rows x (n, 128), for each stage in order:
     x += fp16(attend(fp16(LN(x) wq^T + bq))) wo^T + bo, the attention typed
     by (bias, vcls) over the stage's CSR entries with k/v the two halves of
     its kv rows.  One launch for one or two stages (x stays on chip between
-    them); both stages carry class values or neither does."""
+    them); both stages carry class values or neither does.  ``row_order``
+    (int32, a permutation of the rows) sets the order rows are grouped into
+    16-row tiles in; the results do not depend on it."""
     if not 1 <= len(stages) <= 2:
         raise ValueError("one or two stages per launch")
-    dev = _on_gpu(x, *[t for st in stages for t in st])
+    dev = _on_gpu(x, row_order, *[t for st in stages for t in st])
+    if row_order is not None:
+        if row_order.dtype != torch.int32 or row_order.shape != (x.shape[0],):
+            raise ValueError("row_order must be an int32 permutation of the rows")
+        row_order = row_order.contiguous()
     n = x.shape[0]
     if x.ndim != 2 or x.shape[1] != 128 or x.dtype != torch.float32 or x.stride(1) != 1:
         raise ValueError("x must be fp32 (n, 128) rows")
@@ -544,8 +568,8 @@ def attention_substages(x: Tensor, stages: list[SubStage]) -> Tensor:
         kind = "vcls" if stages[0].vcls is not None else "plain"
         name = f"attention_substage_{kind}" if len(stages) == 1 else f"attention_substages{len(stages)}_{kind}"
         _launch(name, nbytes, flops, lambda: _check(
-            _lib().mantis_attention_substages(_ptr(x), x.stride(0), n, ctypes.cast(arr, ctypes.c_void_p), len(built),
-                                              _ptr(error_flag(dev)), _stream()),
+            _lib().mantis_attention_substages(_ptr(x), x.stride(0), n, _ptr(row_order), ctypes.cast(arr, ctypes.c_void_p),
+                                              len(built), _ptr(error_flag(dev)), _stream()),
             "attention_substages",
         ))
     return x
@@ -560,12 +584,15 @@ def attention_substage(x: Tensor, wq: Tensor, bq: Tensor, kv: Tensor, bias: Tens
 def cell_heads(c: Tensor, w1: Tensor, b1: Tensor, w2: Tensor, w3: Tensor, b3: Tensor, pre: Tensor,
                act_table: Tensor, empty_rows: Tensor, act_empty: Tensor, head_tab: Tensor, g_half: Tensor,
                cell_pos: Tensor, dec_ptr: Tensor, dec_window: Tensor, act_class: Tensor, dec_class: Tensor,
-               layer_norm: bool) -> Tensor:
+               layer_norm: bool, row_order: Tensor | None = None) -> Tensor:
     """(n_cells, 16) fp32 head rows of every cell in one launch (see
     mantis_cell_heads in include/mantis_hip.h): column 0 the policy logit,
-    1..3 the critic logits."""
+    1..3 the critic logits.  ``row_order`` (int32 permutation of the cells)
+    sets their grouping into tiles; the results do not depend on it."""
     dev = _on_gpu(c, w1, b1, w2, w3, b3, pre, act_table, empty_rows, act_empty, head_tab, g_half, cell_pos, dec_ptr,
-                  dec_window, act_class, dec_class)
+                  dec_window, act_class, dec_class, row_order)
+    if row_order is not None and (row_order.dtype != torch.int32 or row_order.shape != (c.shape[0],)):
+        raise ValueError("row_order must be an int32 permutation of the cells")
     n = c.shape[0]
     if c.ndim != 2 or c.shape[1] != 128 or c.stride(1) != 1 or c.dtype not in (torch.float32, torch.float16):
         raise ValueError("c must be (n_cells, 128) fp32 or fp16 rows")
@@ -602,7 +629,8 @@ def cell_heads(c: Tensor, w1: Tensor, b1: Tensor, w2: Tensor, w3: Tensor, b3: Te
         flops = n * 2 * (2 * 256 * 128 + 16 * 256)
         _launch("cell_heads", nbytes, flops, lambda: _check(
             _lib().mantis_cell_heads(
-                _ptr(c), _dt(c), int(layer_norm), c.stride(0), n, _ptr(w1), _ptr(b1), _ptr(w2), _ptr(w3), _ptr(b3),
+                _ptr(c), _dt(c), int(layer_norm), c.stride(0), n, _ptr(row_order), _ptr(w1), _ptr(b1), _ptr(w2), _ptr(w3),
+                _ptr(b3),
                 _ptr(pre), pre.shape[0], _ptr(act_table), act_table.shape[0], _ptr(empty_rows), _ptr(act_empty),
                 _ptr(head_tab), head_tab.shape[0], _ptr(g_half), g_half.shape[0], _ptr(cell_pos), _ptr(dec_ptr),
                 _ptr(dec_window), _ptr(act_class), _ptr(dec_class), e, _ptr(out), _ptr(error_flag(dev)), _stream(),

@@ -51,6 +51,19 @@ int32_t mantis_runs_to_ptr(const int64_t* dest, int64_t n_entries, int64_t n_des
                            int64_t* ptr, int32_t* err_flag, void* stream);
 
 /*
+ * A tile order for row kernels whose per-tile work follows the tile's
+ * longest entry run (mantis_attention_substages, mantis_cell_heads): within
+ * every segment [seg_ptr[s], seg_ptr[s+1]) of the rows (the segments must
+ * tile [0, n_rows) in order; else MANTIS_FLAG_ORDER), the rows in ascending
+ * (min(ptr_a[r+1] - ptr_a[r], 31), min(ptr_b[r+1] - ptr_b[r], 63)); ptr_b
+ * may be NULL.  order (n_rows int32) receives the permutation.  Rows of one
+ * key come in no particular order.  No counterpart in the reference: the
+ * cells of a position are grouped by their decoder and radius run lengths.
+ */
+int32_t mantis_segment_order(const int64_t* seg_ptr, int64_t n_seg, const int64_t* ptr_a, const int64_t* ptr_b,
+                             int64_t n_rows, int32_t* order, int32_t* err_flag, void* stream);
+
+/*
  * Run reduction: out[d, :] = sum over e in [ptr[d], ptr[d+1]) of
  * values[gather[e], :], accumulated in fp32, cast to out_dtype.  Rows with
  * no entries are written as zeros.  values is (n_src, ld) with the first `h`
@@ -184,6 +197,10 @@ int32_t mantis_attention_substage(float* x, int64_t ldx, int64_t n_rows, const v
  * its own weights, k/v rows, class tables and CSR entries; the stages of one
  * call either all carry class values (vcls) or none does.  The fields of
  * mantis_substage are the per-stage arguments of mantis_attention_substage.
+ * row_order, when not NULL, is a permutation of [0, n_rows) (int32) in which
+ * the rows are visited: 16 consecutive entries form a tile, and a tile's
+ * entry loop runs as long as its longest row, so an order that groups rows
+ * of similar entry counts saves work.  The results do not depend on it.
  * Replaces the two cell sub-stages of the reference's _cell_stage (cells <-
  * windows, then cells <- stones; model.py:397-490, kernels
  * cell_latents.py:213-285, 834-1001).
@@ -207,8 +224,9 @@ typedef struct mantis_substage {
   const float* bo;
 } mantis_substage;
 
-int32_t mantis_attention_substages(float* x, int64_t ldx, int64_t n_rows, const mantis_substage* stages,
-                                   int32_t n_stages, int32_t* err_flag, void* stream);
+int32_t mantis_attention_substages(float* x, int64_t ldx, int64_t n_rows, const int32_t* row_order,
+                                   const mantis_substage* stages, int32_t n_stages, int32_t* err_flag,
+                                   void* stream);
 
 /*
  * Fused cell heads: for every legal cell r (position cell_pos[r]) with
@@ -223,12 +241,15 @@ int32_t mantis_attention_substages(float* x, int64_t ldx, int64_t n_rows, const 
  * fp16 with lane-blocked columns (column 64*q + 4*nt + t holds feature
  * 16*nt + 4*q + t); empty_rows (3, 128), g_half (n_pos, 256) fp32;
  * act_empty (n_cells, 3) and the index arrays int64; out (n_cells, 16) fp32.
+ * row_order, when not NULL, is a permutation of the cells (int32) in which
+ * they are grouped into 16-cell tiles (see mantis_segment_order); the
+ * results do not depend on it.
  * Replaces the reference's _action_contribution / encode_rows / class_row_sum
  * and the first layers of mlp_p and mlp_q (model.py:1031-1091,
  * row_encoder.py:40-112, message_passing.py:331-339).
  */
 int32_t mantis_cell_heads(const void* c, int32_t c_dtype, int32_t layer_norm, int64_t ldc, int64_t n_cells,
-                          const void* w1, const float* b1, const void* w2, const void* w3, const float* b3,
+                          const int32_t* row_order, const void* w1, const float* b1, const void* w2, const void* w3, const float* b3,
                           const void* pre, int64_t n_w, const void* act_table, int64_t n_acls,
                           const float* empty_rows, const int64_t* act_empty, const void* head_tab, int64_t n_dcls,
                           const float* g_half, int64_t n_pos, const int64_t* cell_pos, const int64_t* dec_ptr,

@@ -250,6 +250,36 @@ def test_two_substages_in_one_pass_match_two_launches(device, with_vcls):
     assert not torch.equal(got.cpu(), x)
 
 
+def test_row_order_changes_the_tiles_not_the_results(device):
+    # the rows visited in a random permutation (and in an order sorted by
+    # entry count) give bitwise the natural order's results; an order entry
+    # out of range is flagged and its slot skipped
+    gen = _g(13)
+    n = 1999
+    st1 = _random_stage(gen, n, 301, 726, True, 9)
+    st2 = _random_stage(gen, n, 57, 192, True, 25)
+    dev = lambda st: ops.SubStage(*[None if t is None else t.to(device) for t in st])  # noqa: E731
+    s1, s2 = dev(st1), dev(st2)
+    x = 2 * torch.randn(n, 128, generator=gen) - 0.3
+    ref = x.to(device)
+    ops.attention_substages(ref, [s1, s2])
+    counts = (st1.seg_ptr[1:] - st1.seg_ptr[:-1]) * 64 + (st2.seg_ptr[1:] - st2.seg_ptr[:-1])
+    for order in (torch.randperm(n, generator=gen), torch.argsort(counts)):
+        got = x.to(device)
+        ops.attention_substages(got, [s1, s2], row_order=order.to(torch.int32).to(device))
+        ops.raise_on_device_error(device)
+        assert torch.equal(got.cpu(), ref.cpu())
+    bad = torch.arange(n, dtype=torch.int32)
+    bad[5] = n
+    got = x.to(device)
+    ops.attention_substages(got, [s1, s2], row_order=bad.to(device))
+    with pytest.raises(ValueError):
+        ops.raise_on_device_error(device)
+    keep = torch.ones(n, dtype=torch.bool)
+    keep[5] = False  # row 5 was never visited: unchanged
+    assert torch.equal(got.cpu()[keep], ref.cpu()[keep]) and torch.equal(got.cpu()[5], x[5])
+
+
 def test_substages_reject_mixed_class_values_and_flag_bad_indices(device):
     gen = _g(12)
     n = 64
@@ -312,6 +342,20 @@ def test_cell_heads_match_the_unfused_composition(device, mode):
     # second product; summed in another order than row_encode's, a rare sum
     # lands one fp16 unit (up to 8e-3) apart, a few 1e-4 in the outputs
     torch.testing.assert_close(got.cpu(), ref.cpu(), rtol=1e-4, atol=1e-3)
+    # the cells grouped by run length into tiles (per position, as the
+    # forward does): bitwise the same rows
+    order = ops.segment_order(d(torch.searchsorted(cell_pos, torch.arange(p + 1))), d(ptr), None, n)
+    ops.raise_on_device_error(device)
+    perm = order.cpu().long()
+    assert torch.equal(torch.sort(perm).values, torch.arange(n))
+    lens = (ptr[1:] - ptr[:-1]).clamp(max=31)
+    assert torch.equal(cell_pos[perm], cell_pos) and all(
+        bool((lens[perm][cell_pos == q][1:] >= lens[perm][cell_pos == q][:-1]).all()) for q in range(p))
+    got2 = ops.cell_heads(d(x), d(w1), d(b1), d(w2), d(w3), d(b3), d(pre), d(table), d(empty_rows), d(act_empty),
+                          d(head_tab), d(g_half), d(cell_pos), d(ptr), d(win), d(acl), d(dcl),
+                          layer_norm=mode == "layer_norm", row_order=order)
+    ops.raise_on_device_error(device)
+    assert torch.equal(got2.cpu(), got.cpu())
 
 
 def test_latent_mix_matches_the_fp32_formulation(device):
