@@ -70,7 +70,7 @@ struct Stage {
 };
 
 struct SubArgs {
-  float* x;
+  void* x;  // fp32 or fp16 rows (the kernel's TX)
   int64_t ldx;
   int64_t n_rows;
   const int32_t* order;  // tile slot -> row, or null for the natural order
@@ -128,8 +128,9 @@ __device__ __forceinline__ void load_head(const _Float16* row_g, uint4 (&h)[4]) 
   for (int w = 0; w < 4; ++w) h[w] = *reinterpret_cast<const uint4*>(row_g + 32 * w);
 }
 
-template <int kStages, bool kVcls>
+template <int kStages, bool kVcls, typename TX>
 __global__ void __launch_bounds__(kThreads) attn_substage_kernel(SubArgs a) {
+  TX* const xs = static_cast<TX*>(a.x);
   __shared__ __attribute__((aligned(16))) _Float16 sw[kStages][2][kK * kPitch];  // [stage][q, o]
 #pragma unroll
   for (int s = 0; s < kStages; ++s) {
@@ -189,7 +190,7 @@ __global__ void __launch_bounds__(kThreads) attn_substage_kernel(SubArgs a) {
     }
     float xv[4][8];
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) load8_nt(a.x + rc * a.ldx + 32 * ks + 8 * g, xv[ks]);
+    for (int ks = 0; ks < 4; ++ks) load8_nt(xs + rc * a.ldx + 32 * ks + 8 * g, xv[ks]);
     int64_t lo[kStages], hi[kStages];
 #pragma unroll
     for (int s = 0; s < kStages; ++s) {
@@ -363,12 +364,12 @@ __global__ void __launch_bounds__(kThreads) attn_substage_kernel(SubArgs a) {
     }
     if (live) {
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) store8_nt(a.x + row * a.ldx + 32 * ks + 8 * g, xv[ks]);
+      for (int ks = 0; ks < 4; ++ks) store8_nt(xs + row * a.ldx + 32 * ks + 8 * g, xv[ks]);
     }
   }
 }
 
-template <int kStages, bool kVcls>
+template <int kStages, bool kVcls, typename TX>
 int32_t launch(const SubArgs& a, void* stream) {
   int dev = 0, cus = 0;
   if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
@@ -379,7 +380,7 @@ int32_t launch(const SubArgs& a, void* stream) {
   int64_t grid = ((int64_t(cus) + kXcds - 1) / kXcds) * kXcds;
   const int64_t need = ((tiles + kWaves - 1) / kWaves + kXcds - 1) / kXcds * kXcds;
   if (need < grid) grid = need;
-  attn_substage_kernel<kStages, kVcls><<<dim3(unsigned(grid)), dim3(kThreads), 0, as_stream(stream)>>>(a);
+  attn_substage_kernel<kStages, kVcls, TX><<<dim3(unsigned(grid)), dim3(kThreads), 0, as_stream(stream)>>>(a);
   return launched();
 }
 
@@ -410,16 +411,19 @@ Stage to_stage(const mantis_substage& d) {
 
 using namespace mantis;
 
-extern "C" int32_t mantis_attention_substages(float* x, int64_t ldx, int64_t n_rows, const int32_t* row_order,
-                                              const mantis_substage* stages, int32_t n_stages, int32_t* err_flag,
-                                              void* stream) {
+extern "C" int32_t mantis_attention_substages(void* x, int32_t x_dtype, int64_t ldx, int64_t n_rows,
+                                              const int32_t* row_order, const mantis_substage* stages,
+                                              int32_t n_stages, int32_t* err_flag, void* stream) {
   if (n_rows < 0 || !stages || n_stages < 1 || n_stages > 2) return MANTIS_E_ARG;
   if (n_rows == 0) return MANTIS_OK;
   for (int s = 0; s < n_stages; ++s)
     if (!stage_ok(stages[s])) return MANTIS_E_ARG;
   // both stages of a pass carry class values, or neither does
   if (n_stages == 2 && (stages[0].vcls == nullptr) != (stages[1].vcls == nullptr)) return MANTIS_E_ARG;
-  if (!x || ldx < kK || ldx % 4 || !aligned16(x) || n_rows > 2147483647LL) return MANTIS_E_ARG;
+  if (x_dtype != MANTIS_F32 && x_dtype != MANTIS_F16) return MANTIS_E_ARG;
+  // whole 16-byte chunks: 4 fp32 or 8 fp16 per row-stride unit
+  if (!x || ldx < kK || ldx % (x_dtype == MANTIS_F16 ? 8 : 4) || !aligned16(x) || n_rows > 2147483647LL)
+    return MANTIS_E_ARG;
   SubArgs a{};
   a.x = x;
   a.ldx = ldx;
@@ -429,8 +433,14 @@ extern "C" int32_t mantis_attention_substages(float* x, int64_t ldx, int64_t n_r
   a.scale = 0.17677669529663687f;  // 1/sqrt(32)
   a.flag = err_flag;
   const bool vc = stages[0].vcls != nullptr;
-  if (n_stages == 2) return vc ? launch<2, true>(a, stream) : launch<2, false>(a, stream);
-  return vc ? launch<1, true>(a, stream) : launch<1, false>(a, stream);
+  // instantiated: fp32 rows (windows, one stage, and the cell stages' fp32
+  // form), fp16 rows (the cells' two stages)
+  if (x_dtype == MANTIS_F16) {
+    if (n_stages == 2) return vc ? launch<2, true, _Float16>(a, stream) : launch<2, false, _Float16>(a, stream);
+    return vc ? launch<1, true, _Float16>(a, stream) : launch<1, false, _Float16>(a, stream);
+  }
+  if (n_stages == 2) return vc ? launch<2, true, float>(a, stream) : launch<2, false, float>(a, stream);
+  return vc ? launch<1, true, float>(a, stream) : launch<1, false, float>(a, stream);
 }
 
 extern "C" int32_t mantis_attention_substage(float* x, int64_t ldx, int64_t n_rows, const void* wq, const float* bq,
@@ -440,5 +450,5 @@ extern "C" int32_t mantis_attention_substage(float* x, int64_t ldx, int64_t n_ro
                                              int64_t n_entries, const void* wo, const float* bo,
                                              int32_t* err_flag, void* stream) {
   const mantis_substage d{wq, bq, k, v, ldk, ldv, n_src, bias, n_classes, vcls, seg_ptr, src, cls, n_entries, wo, bo};
-  return mantis_attention_substages(x, ldx, n_rows, nullptr, &d, 1, err_flag, stream);
+  return mantis_attention_substages(x, MANTIS_F32, ldx, n_rows, nullptr, &d, 1, err_flag, stream);
 }

@@ -357,6 +357,8 @@ extern "C" int32_t mantis_cell_heads(const void* c, int32_t c_dtype, int32_t lay
     cell_heads_kernel<float, false><<<gd, bd, 0, s>>>(a);
   else if (c_dtype == MANTIS_F16 && !layer_norm)
     cell_heads_kernel<_Float16, false><<<gd, bd, 0, s>>>(a);
+  else if (c_dtype == MANTIS_F16)
+    cell_heads_kernel<_Float16, true><<<gd, bd, 0, s>>>(a);
   else
     return MANTIS_E_ARG;
   return launched();

@@ -98,6 +98,21 @@ __device__ __forceinline__ void store8_nt(float* p, const float (&x)[8]) {
   __builtin_nontemporal_store(nt_f32x4_t{x[4], x[5], x[6], x[7]}, reinterpret_cast<nt_f32x4_t*>(p) + 1);
 }
 
+typedef _Float16 nt_f16x8_t __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ void load8_nt(const _Float16* p, float (&x)[8]) {
+  const nt_f16x8_t u = __builtin_nontemporal_load(reinterpret_cast<const nt_f16x8_t*>(p));
+#pragma unroll
+  for (int i = 0; i < 8; ++i) x[i] = float(u[i]);
+}
+
+// fp16 rows are rounded to nearest even, saturating at the largest finite fp16
+__device__ __forceinline__ void store8_nt(_Float16* p, const float (&x)[8]) {
+  nt_f16x8_t u;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) u[i] = _Float16(fminf(fmaxf(x[i], -65504.f), 65504.f));
+  __builtin_nontemporal_store(u, reinterpret_cast<nt_f16x8_t*>(p));
+}
+
 __device__ __forceinline__ void store8(float* p, const float (&x)[8]) {
   reinterpret_cast<float4*>(p)[0] = make_float4(x[0], x[1], x[2], x[3]);
   reinterpret_cast<float4*>(p)[1] = make_float4(x[4], x[5], x[6], x[7]);

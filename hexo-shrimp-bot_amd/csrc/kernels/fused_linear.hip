@@ -101,9 +101,16 @@ struct Smem {
 template <int N1>
 constexpr int threads_for() { return N1 >= 512 ? 1024 : 512; }
 
+// kPair (single stage, fp16 out): the W1 rows are staged permuted so that
+// feature tiles 2k and 2k+1 leave lane group g holding the eight consecutive
+// features 32k + 8g .. +7 of its row: one 16-byte store per pair of tiles
+// instead of two 8-byte ones.
+__device__ __forceinline__ int pair_feature(int nt, int g, int t) { return 32 * (nt >> 1) + 8 * g + 4 * (nt & 1) + t; }
+
 template <typename TX, typename TX2, bool kLN, int N1, bool kX2, bool kRelu, bool kStage2, int kMode,
-          bool kSplit = false>
+          bool kSplit = false, bool kPair = false>
 __global__ void __launch_bounds__(threads_for<N1>()) fused_linear_kernel(Args a) {
+  static_assert(!kPair || (!kStage2 && !kX2 && kMode == kStoreF16 && N1 % 32 == 0), "paired stores: fp16 projections");
   constexpr int kTileRows = 16 * (threads_for<N1>() / 64);
   constexpr int kParts = kSplit ? 2 : 1;
   extern __shared__ __attribute__((aligned(16))) _Float16 smem[];
@@ -118,7 +125,9 @@ __global__ void __launch_bounds__(threads_for<N1>()) fused_linear_kernel(Args a)
   // Stage the weights (16-byte chunks; [hi; lo] rows with kSplit).
   for (int i = threadIdx.x; i < kParts * N1 * (kK / 8); i += blockDim.x) {
     const int r = i / (kK / 8), c = (i % (kK / 8)) * 8;
-    *reinterpret_cast<uint4*>(sw1 + r * kPitch + c) = *reinterpret_cast<const uint4*>(a.w1 + r * kK + c);
+    // LDS row r = 16 nt + 4 g + t holds feature pair_feature(nt, g, t) with kPair
+    const int src = kPair ? (r / N1) * N1 + pair_feature((r % N1) >> 4, (r & 15) >> 2, r & 3) : r;
+    *reinterpret_cast<uint4*>(sw1 + r * kPitch + c) = *reinterpret_cast<const uint4*>(a.w1 + src * kK + c);
     if constexpr (kX2)
       *reinterpret_cast<uint4*>(sw2 + r * kPitch + c) = *reinterpret_cast<const uint4*>(a.w2 + r * kK + c);
   }
@@ -237,7 +246,9 @@ __global__ void __launch_bounds__(threads_for<N1>()) fused_linear_kernel(Args a)
             acc = mfma16x16x32(*reinterpret_cast<const f16x8_t*>(sw2 + kLo1 + off), x2b[ks], acc);
         }
       }
-      const int f = 16 * nt + 4 * g;
+      // the tile's four features of this lane: 16 nt + 4 g .. +3, or with
+      // kPair the four at pair_feature(nt, g, 0)
+      const int f = kPair ? pair_feature(nt, g, 0) : 16 * nt + 4 * g;
       float4 add = a.b1 ? *reinterpret_cast<const float4*>(a.b1 + f) : make_float4(0.f, 0.f, 0.f, 0.f);
       if (live && a.add1) {
         const float4 r = *reinterpret_cast<const float4*>(a.add1 + row * a.ld_add1 + f);
@@ -268,6 +279,20 @@ __global__ void __launch_bounds__(threads_for<N1>()) fused_linear_kernel(Args a)
         }
         // keep each step's weight loads next to its products (bounded live range)
         __builtin_amdgcn_sched_barrier(0);
+      }
+    } else if constexpr (kPair) {
+#pragma unroll 2
+      for (int k = 0; k < NT1 / 2; ++k) {
+        const f32x4_t lo = feature_tile(2 * k);
+        const f32x4_t hi = feature_tile(2 * k + 1);
+        if (live) {
+          uint4 w;
+          w.x = pack_f16x2(lo[0], lo[1]);
+          w.y = pack_f16x2(lo[2], lo[3]);
+          w.z = pack_f16x2(hi[0], hi[1]);
+          w.w = pack_f16x2(hi[2], hi[3]);
+          *reinterpret_cast<uint4*>(static_cast<_Float16*>(a.out) + row * a.ldo + 32 * k + 8 * g) = w;
+        }
       }
     } else {
 #pragma unroll 2
@@ -315,10 +340,10 @@ int cu_count() {
 }
 
 template <typename TX, typename TX2, bool kLN, int N1, bool kX2, bool kRelu, bool kStage2, int kMode,
-          bool kSplit = false>
+          bool kSplit = false, bool kPair = false>
 int32_t launch(const Args& a, hipStream_t stream) {
   using S = Smem<N1, kStage2, kX2, kSplit>;
-  auto kernel = fused_linear_kernel<TX, TX2, kLN, N1, kX2, kRelu, kStage2, kMode, kSplit>;
+  auto kernel = fused_linear_kernel<TX, TX2, kLN, N1, kX2, kRelu, kStage2, kMode, kSplit, kPair>;
   const int bytes = S::bytes(a.n3);
   if (bytes > kMaxLds) return MANTIS_E_ARG;
   static bool configured = false;
@@ -383,6 +408,14 @@ extern "C" int32_t mantis_fused_linear(const void* x, int32_t x_dtype, int64_t l
   // The supported combinations: projections, residual projections, and the
   // two-layer MLP residuals of the blocks and heads.
   if (!hx2 && !st2) {
+    // the projections (fp16 out; paired 16-byte stores, except where an
+    // add1/add2 row is read per feature)
+    if (x_dtype == MANTIS_F32 && ln && !r && mode == 0 && !a.add1 && !a.add2) {
+      if (n1 == 128) return launch<float, float, true, 128, false, false, false, 0, false, true>(a, s);
+      if (n1 == 256) return launch<float, float, true, 256, false, false, false, 0, false, true>(a, s);
+      if (n1 == 384) return launch<float, float, true, 384, false, false, false, 0, false, true>(a, s);
+      if (n1 == 512) return launch<float, float, true, 512, false, false, false, 0, false, true>(a, s);
+    }
     if (x_dtype == MANTIS_F32 && ln && !r && mode == 0) {
       if (n1 == 128) return launch<float, float, true, 128, false, false, false, 0>(a, s);
       if (n1 == 256) return launch<float, float, true, 256, false, false, false, 0>(a, s);
@@ -391,6 +424,11 @@ extern "C" int32_t mantis_fused_linear(const void* x, int32_t x_dtype, int64_t l
     }
     if (x_dtype == MANTIS_F32 && ln && !r && mode == 1 && n1 == 128)
       return launch<float, float, true, 128, false, false, false, 1>(a, s);
+    // fp16 rows with a LayerNorm (the cell state's k/v projection)
+    if (x_dtype == MANTIS_F16 && ln && !r && mode == 0 && n1 == 256 && !a.add1 && !a.add2)
+      return launch<_Float16, float, true, 256, false, false, false, 0, false, true>(a, s);
+    if (x_dtype == MANTIS_F16 && ln && !r && mode == 0 && n1 == 256)
+      return launch<_Float16, float, true, 256, false, false, false, 0>(a, s);
     if (!ln && !r && mode == 2 && n1 == 128) {
       if (x_dtype == MANTIS_F32) return launch<float, float, false, 128, false, false, false, 2>(a, s);
       if (x_dtype == MANTIS_F16) return launch<_Float16, float, false, 128, false, false, false, 2>(a, s);

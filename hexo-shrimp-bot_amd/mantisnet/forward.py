@@ -514,7 +514,7 @@ def trunk(model, batch: Batch):
 
 def _trunk(model, b: Batch, plan: Plan, raw_cells: bool = False):
     """(w_out, g_out, cells): cells are ln_out(c) in fp16, or with raw_cells
-    the fp32 cell state itself (the fused heads normalise it on the fly)."""
+    the fp16 cell state itself (the fused heads normalise it on the fly)."""
     W = _prepared(model)
     P = dict(model.named_parameters())
     cfg = model.cfg
@@ -528,8 +528,11 @@ def _trunk(model, b: Batch, plan: Plan, raw_cells: bool = False):
     c = None
     if cfg.cell_nodes:
         # covered cells start from cell_base, the others from their nearest-stone
-        # row: one gather from the table [nearest rows; cell_base]
-        table = torch.cat([P["cell_nearest_table.weight"], P["cell_base"][None, :]])
+        # row: one gather from the table [nearest rows; cell_base].  The cell
+        # state is stored in fp16 (866 MB -> 433 MB per pass at 1.69M cells):
+        # every kernel that updates it keeps the rows in fp32 registers and
+        # rounds once on the store, and its readers feed fp16 MFMA operands
+        table = torch.cat([P["cell_nearest_table.weight"], P["cell_base"][None, :]]).to(HALF)
         c = table.index_select(0, torch.where(plan.covered_mask, table.shape[0] - 1, b.cell_nearest))
     sw_all = ops.run_reduce(W["sw_all"], plan.run_class, plan.inc_stone_ptr, n_s, F32)
     for i in range(cfg.blocks):
@@ -539,7 +542,7 @@ def _trunk(model, b: Batch, plan: Plan, raw_cells: bool = False):
     g_out = F.layer_norm(g, (128,), P["ln_out.weight"], P["ln_out.bias"], 1e-5).mean(dim=1)
     if c is None:
         return w_out, g_out, None
-    cells = c if raw_cells else ops.layer_norm(c, P["ln_out.weight"], P["ln_out.bias"], HALF)
+    cells = c if raw_cells else ops.layer_norm(c.float(), P["ln_out.weight"], P["ln_out.bias"], HALF)
     return w_out, g_out, cells
 
 
@@ -562,7 +565,7 @@ def _value_head(model, w: Tensor, g: Tensor, b: Batch, plan: Plan):
 
 def _head_rows(model, w: Tensor, g: Tensor, cells: Tensor, b: Batch, plan: Plan, raw_cells: bool = False) -> Tensor:
     """(N_c, 16) fp32: column 0 the policy logit, 1..3 the critic logits.
-    ``cells`` are ln_out(c) rows, or with raw_cells the fp32 cell state; with
+    ``cells`` are ln_out(c) rows, or with raw_cells the fp16 cell state; with
     cell state off they are None and each legal cell reads the sum of its
     decoder windows' ln_out rows (model.py:985-1029)."""
     if model.cfg.uses_cell_state and cells is None:

@@ -553,8 +553,8 @@ def attention_substages(x: Tensor, stages: list[SubStage], row_order: Tensor | N
             raise ValueError("row_order must be an int32 permutation of the rows")
         row_order = row_order.contiguous()
     n = x.shape[0]
-    if x.ndim != 2 or x.shape[1] != 128 or x.dtype != torch.float32 or x.stride(1) != 1:
-        raise ValueError("x must be fp32 (n, 128) rows")
+    if x.ndim != 2 or x.shape[1] != 128 or x.dtype not in (torch.float32, torch.float16) or x.stride(1) != 1:
+        raise ValueError("x must be fp32 or fp16 (n, 128) rows")
     if len({st.vcls is None for st in stages}) != 1:
         raise ValueError("the stages of one launch all carry class values or none does")
     built = [_substage_struct(st, n) for st in stages]
@@ -562,14 +562,17 @@ def attention_substages(x: Tensor, stages: list[SubStage], row_order: Tensor | N
         arr = (_hip_api.MantisSubstage * len(built))(*[d for d, _, _ in built])
         # x read and written once; per stage the CSR pointers and entry
         # indices once and each source's k and v rows once
-        nbytes = n * 128 * 4 * 2 + sum(n * 8 + e * 16 + st.kv.shape[0] * 256 * 2 for st, (_, _, e) in
+        nbytes = n * 128 * x.element_size() * 2 + sum(n * 8 + e * 16 + st.kv.shape[0] * 256 * 2 for st, (_, _, e) in
                                        zip(stages, built))
         flops = sum(2 * n * 128 * 128 * 2 + e * 4 * 128 * 2 for _, _, e in built)
         kind = "vcls" if stages[0].vcls is not None else "plain"
         name = f"attention_substage_{kind}" if len(stages) == 1 else f"attention_substages{len(stages)}_{kind}"
+        if x.dtype == torch.float16:
+            name += "_f16"
         _launch(name, nbytes, flops, lambda: _check(
-            _lib().mantis_attention_substages(_ptr(x), x.stride(0), n, _ptr(row_order), ctypes.cast(arr, ctypes.c_void_p),
-                                              len(built), _ptr(error_flag(dev)), _stream()),
+            _lib().mantis_attention_substages(_ptr(x), _dt(x), x.stride(0), n, _ptr(row_order),
+                                              ctypes.cast(arr, ctypes.c_void_p), len(built), _ptr(error_flag(dev)),
+                                              _stream()),
             "attention_substages",
         ))
     return x
@@ -596,8 +599,6 @@ def cell_heads(c: Tensor, w1: Tensor, b1: Tensor, w2: Tensor, w3: Tensor, b3: Te
     n = c.shape[0]
     if c.ndim != 2 or c.shape[1] != 128 or c.stride(1) != 1 or c.dtype not in (torch.float32, torch.float16):
         raise ValueError("c must be (n_cells, 128) fp32 or fp16 rows")
-    if layer_norm and c.dtype != torch.float32:
-        raise ValueError("the fused LayerNorm reads fp32 rows")
     for t, shape, name in ((w1, (256, 128), "w1"), (w2, (256, 128), "w2"), (w3, (16, 256), "w3")):
         if t.shape != shape or t.dtype != torch.float16 or not t.is_contiguous():
             raise ValueError(f"{name} must be a contiguous fp16 {shape} matrix")

@@ -197,8 +197,10 @@ int32_t mantis_attention_substage(float* x, int64_t ldx, int64_t n_rows, const v
  * its own weights, k/v rows, class tables and CSR entries; the stages of one
  * call either all carry class values (vcls) or none does.  The fields of
  * mantis_substage are the per-stage arguments of mantis_attention_substage.
- * row_order, when not NULL, is a permutation of [0, n_rows) (int32) in which
- * the rows are visited: 16 consecutive entries form a tile, and a tile's
+ * x holds fp32 or fp16 rows (x_dtype MANTIS_F32 / MANTIS_F16; fp16 rows
+ * are widened on load and rounded once, to nearest even, on the final
+ * store).  row_order, when not NULL, is a permutation of [0, n_rows) (int32)
+ * in which the rows are visited: 16 consecutive entries form a tile, and a tile's
  * entry loop runs as long as its longest row, so an order that groups rows
  * of similar entry counts saves work.  The results do not depend on it.
  * Replaces the two cell sub-stages of the reference's _cell_stage (cells <-
@@ -224,7 +226,7 @@ typedef struct mantis_substage {
   const float* bo;
 } mantis_substage;
 
-int32_t mantis_attention_substages(float* x, int64_t ldx, int64_t n_rows, const int32_t* row_order,
+int32_t mantis_attention_substages(void* x, int32_t x_dtype, int64_t ldx, int64_t n_rows, const int32_t* row_order,
                                    const mantis_substage* stages, int32_t n_stages, int32_t* err_flag,
                                    void* stream);
 
@@ -235,7 +237,7 @@ int32_t mantis_attention_substages(float* x, int64_t ldx, int64_t n_rows, const 
  *   acts = sum_e relu(pre[dec_window[e]] + act_table[act_class[e]]) + sum_k act_empty[r,k] * empty_rows[k]
  *   h    = relu(w1 x + w2 fp16(acts) + b1 + sum_e head_tab[dec_class[e]] + g_half[cell_pos[r]])
  *   out[r] = w3 fp16(h) + b3
- * c: (n_cells, 128) rows in c_dtype (fp32, or fp16 without layer_norm), row
+ * c: (n_cells, 128) rows in c_dtype (fp32 or fp16), row
  * stride ldc; w1, w2: (256, 128) fp16; b1 (256); w3 (16, 256) fp16; b3 (16);
  * pre (n_w, 128) and act_table (n_acls, 128) fp16; head_tab (n_dcls, 256)
  * fp16 with lane-blocked columns (column 64*q + 4*nt + t holds feature

@@ -39,15 +39,16 @@ def _h(x):
     return x.to(H16).float()
 
 
-@pytest.mark.parametrize("n1", [128, 256, 384])
-def test_projection_with_layer_norm(device, n1):
+@pytest.mark.parametrize("n1,xdt", [(128, torch.float32), (256, torch.float32), (384, torch.float32),
+                                    (512, torch.float32), (256, H16)])
+def test_projection_with_layer_norm(device, n1, xdt):
     gen = _g(n1)
     m = 1000
-    x = 3 * torch.randn(m, 128, generator=gen) + 1
+    x = (3 * torch.randn(m, 128, generator=gen) + 1).to(xdt).float()
     w = _w(n1, 128, gen)
     b = 0.1 * torch.randn(n1, generator=gen)
     rows = torch.randint(-1, m, (777,), generator=gen)
-    out = ops.fused_linear(x.to(device), w.to(device), b.to(device), layer_norm=True, x_rows=rows.to(device))
+    out = ops.fused_linear(x.to(device, xdt), w.to(device), b.to(device), layer_norm=True, x_rows=rows.to(device))
     ops.raise_on_device_error(device)
     xs = torch.where(rows[:, None] >= 0, x[rows.clamp(min=0)], torch.zeros(1, 128))
     exp = _h(_ln(xs)) @ w.float().t() + b
@@ -248,6 +249,15 @@ def test_two_substages_in_one_pass_match_two_launches(device, with_vcls):
     ops.raise_on_device_error(device)
     torch.testing.assert_close(got.cpu(), ref.cpu(), rtol=1e-6, atol=1e-6)
     assert not torch.equal(got.cpu(), x)
+    # fp16 rows: widened on load, rounded once on the store, so bitwise the
+    # fp32 path on the same values rounded to nearest even
+    x16 = x.to(H16)
+    got16 = x16.to(device)
+    ops.attention_substages(got16, [s1, s2])
+    ref32 = x16.float().to(device)
+    ops.attention_substages(ref32, [s1, s2])
+    ops.raise_on_device_error(device)
+    assert got16.dtype == H16 and torch.equal(got16.cpu(), ref32.cpu().to(H16))
 
 
 def test_row_order_changes_the_tiles_not_the_results(device):
@@ -296,7 +306,7 @@ def test_substages_reject_mixed_class_values_and_flag_bad_indices(device):
         ops.raise_on_device_error(device)
 
 
-@pytest.mark.parametrize("mode", ["layer_norm", "fp16_rows", "fp32_rows"])
+@pytest.mark.parametrize("mode", ["layer_norm", "layer_norm_fp16", "fp16_rows", "fp32_rows"])
 def test_cell_heads_match_the_unfused_composition(device, mode):
     # fused heads = row_encode + class_row_sum + the two-layer head GEMM
     gen = _g(10)
@@ -324,10 +334,11 @@ def test_cell_heads_match_the_unfused_composition(device, mode):
     w3 = w3.to(H16)
     b1, b3 = 0.1 * torch.randn(256, generator=gen), 0.1 * torch.randn(16, generator=gen)
     d = lambda t: t.to(device)  # noqa: E731
-    x = {"layer_norm": c, "fp16_rows": c.to(H16), "fp32_rows": c}[mode]
+    x = {"layer_norm": c, "layer_norm_fp16": c.to(H16), "fp16_rows": c.to(H16), "fp32_rows": c}[mode]
+    ln = mode.startswith("layer_norm")
     got = ops.cell_heads(d(x), d(w1), d(b1), d(w2), d(w3), d(b3), d(pre), d(table), d(empty_rows), d(act_empty),
                          d(head_tab), d(g_half), d(cell_pos), d(ptr), d(win), d(acl), d(dcl),
-                         layer_norm=mode == "layer_norm")
+                         layer_norm=ln)
     ops.raise_on_device_error(device)
     # the fused kernel gathers the two class tables in fp16: the reference
     # composition gets the same fp16-rounded tables
@@ -335,7 +346,7 @@ def test_cell_heads_match_the_unfused_composition(device, mode):
     acts = ops.row_encode(d(pre), d(t16), d(win), d(acl), d(ptr), n, d(act_empty), d(empty_rows))
     ext = ops.run_reduce(d(h16), d(dcl), d(ptr), n, torch.float32)
     # (fp32 rows enter the products as fp16, exactly as fp16 rows do)
-    xin = ops.layer_norm(d(c), d(torch.ones(128)), d(torch.zeros(128)), H16) if mode == "layer_norm" else d(c.to(H16))
+    xin = ops.layer_norm(d(x.float()), d(torch.ones(128)), d(torch.zeros(128)), H16) if ln else d(c.to(H16))
     ref = ops.fused_linear(xin, d(w1), d(b1), x2=acts, w2=d(w2), add1=ext, add2=d(g_half), add2_rows=d(cell_pos),
                            relu=True, w3=d(w3), b3=d(b3), out_dtype=torch.float32)
     # the action-row sums (|acts| up to ~10) are rounded to fp16 for the
@@ -353,7 +364,7 @@ def test_cell_heads_match_the_unfused_composition(device, mode):
         bool((lens[perm][cell_pos == q][1:] >= lens[perm][cell_pos == q][:-1]).all()) for q in range(p))
     got2 = ops.cell_heads(d(x), d(w1), d(b1), d(w2), d(w3), d(b3), d(pre), d(table), d(empty_rows), d(act_empty),
                           d(head_tab), d(g_half), d(cell_pos), d(ptr), d(win), d(acl), d(dcl),
-                          layer_norm=mode == "layer_norm", row_order=order)
+                          layer_norm=ln, row_order=order)
     ops.raise_on_device_error(device)
     assert torch.equal(got2.cpu(), got.cpu())
 
