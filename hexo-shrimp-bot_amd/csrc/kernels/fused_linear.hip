@@ -36,7 +36,7 @@ constexpr int kK = 128;
 constexpr int kPitch = kK + 8;  // fp16 elements per LDS weight row (W1/W2)
 constexpr int kMaxLds = 160 * 1024;  // LDS per CU on gfx950
 
-enum OutMode { kStoreF16 = 0, kStoreF32 = 1, kAddF32 = 2 };
+enum OutMode { kStoreF16 = 0, kStoreF32 = 1, kAddF32 = 2, kAddF16 = 3 };
 
 struct Args {
   const void* x;
@@ -75,11 +75,20 @@ __device__ __forceinline__ void store4(const Args& a, int64_t row, int f, const 
     *reinterpret_cast<uint2*>(static_cast<_Float16*>(a.out) + row * a.ldo + f) = w;
   } else if constexpr (kMode == kStoreF32) {
     *reinterpret_cast<float4*>(static_cast<float*>(a.out) + row * a.ldo + f) = make_float4(v[0], v[1], v[2], v[3]);
-  } else {
+  } else if constexpr (kMode == kAddF32) {
     float4* o = reinterpret_cast<float4*>(static_cast<float*>(a.out) + row * a.ldo + f);
     float4 r = *o;
     r.x += v[0], r.y += v[1], r.z += v[2], r.w += v[3];
     *o = r;
+  } else {
+    // fp16 residual rows: widened, added in fp32, rounded once
+    uint2* o = reinterpret_cast<uint2*>(static_cast<_Float16*>(a.out) + row * a.ldo + f);
+    const uint2 r = *o;
+    const f16x2_t r0 = __builtin_bit_cast(f16x2_t, r.x), r1 = __builtin_bit_cast(f16x2_t, r.y);
+    uint2 w;
+    w.x = pack_f16x2(float(r0[0]) + v[0], float(r0[1]) + v[1]);
+    w.y = pack_f16x2(float(r1[0]) + v[2], float(r1[1]) + v[3]);
+    *o = w;
   }
 }
 
@@ -427,6 +436,8 @@ extern "C" int32_t mantis_fused_linear(const void* x, int32_t x_dtype, int64_t l
     // fp16 rows with a LayerNorm (the cell state's k/v projection)
     if (x_dtype == MANTIS_F16 && ln && !r && mode == 0 && n1 == 256 && !a.add1 && !a.add2)
       return launch<_Float16, float, true, 256, false, false, false, 0, false, true>(a, s);
+    if (x_dtype == MANTIS_F16 && ln && !r && mode == 0 && n1 == 512 && !a.add1 && !a.add2)
+      return launch<_Float16, float, true, 512, false, false, false, 0, false, true>(a, s);
     if (x_dtype == MANTIS_F16 && ln && !r && mode == 0 && n1 == 256)
       return launch<_Float16, float, true, 256, false, false, false, 0>(a, s);
     if (!ln && !r && mode == 2 && n1 == 128) {
@@ -438,6 +449,13 @@ extern "C" int32_t mantis_fused_linear(const void* x, int32_t x_dtype, int64_t l
     if (!ln && !r && mode == 0 && n1 == 128 && x_dtype == MANTIS_F32)
       return launch<float, float, false, 128, false, false, false, 0>(a, s);
   }
+  // fp16 residual rows (the window state of the cell-node configuration)
+  if (!hx2 && !st2 && !r && mode == 3 && n1 == 128 && !ln && x_dtype == MANTIS_F16)
+    return launch<_Float16, float, false, 128, false, false, false, 3>(a, s);
+  if (!hx2 && !st2 && !r && mode == 3 && n1 == 128 && !ln && x_dtype == MANTIS_F32)
+    return launch<float, float, false, 128, false, false, false, 3>(a, s);
+  if (st2 && r && mode == 3 && x_dtype == MANTIS_F16 && ln && hx2 && n1 == 128 && x2_dtype == MANTIS_F16)
+    return launch<_Float16, _Float16, true, 128, true, true, true, 3>(a, s);
   if (st2 && r && mode == 2 && x_dtype == MANTIS_F32 && ln) {
     if (hx2 && n1 == 128 && x2_dtype == MANTIS_F32)
       return launch<float, float, true, 128, true, true, true, 2>(a, s);

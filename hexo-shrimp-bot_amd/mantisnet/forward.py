@@ -524,7 +524,12 @@ def _trunk(model, b: Batch, plan: Plan, raw_cells: bool = False):
     sg = torch.empty((n_s + p * GLOBAL_ROWS, 128), dtype=F32, device=b.stone_own.device)
     sg[:n_s] = P["stone_table.weight"].index_select(0, b.stone_own)
     sg[n_s:] = (P["latent_base"][None] + P["token_moves.weight"].index_select(0, b.moves_idx)[:, None]).reshape(-1, 128)
+    # the window state is stored in fp16 in the cell-node configuration, like
+    # the cell state (each update adds in fp32 and rounds once); the knob-off
+    # cell pass keeps it in fp32 for its compensated-weight launches
     w = P["window_table.weight"].index_select(0, b.window_feat)
+    if cfg.cell_nodes:
+        w = w.to(HALF)
     c = None
     if cfg.cell_nodes:
         # covered cells start from cell_base, the others from their nearest-stone
@@ -538,7 +543,7 @@ def _trunk(model, b: Batch, plan: Plan, raw_cells: bool = False):
     for i in range(cfg.blocks):
         _block(W, P, i, plan, b, sg, w, c, sw_all, i + 1 < cfg.blocks)
     g = sg[n_s:].view(p, GLOBAL_ROWS, 128)
-    w_out = ops.layer_norm(w, P["ln_out.weight"], P["ln_out.bias"], F32)
+    w_out = ops.layer_norm(w.float(), P["ln_out.weight"], P["ln_out.bias"], F32)
     g_out = F.layer_norm(g, (128,), P["ln_out.weight"], P["ln_out.bias"], 1e-5).mean(dim=1)
     if c is None:
         return w_out, g_out, None

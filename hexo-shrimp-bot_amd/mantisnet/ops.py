@@ -919,9 +919,9 @@ def fused_linear(x: Tensor, w1: Tensor, b1: Tensor | None = None, *, layer_norm:
     if add2_rows is not None and add2_rows.numel() != m:
         raise ValueError("add2_rows must have one entry per row")
     if residual:
-        if out is None or out.dtype != torch.float32 or out.shape[0] != m or out.stride(1) != 1:
-            raise ValueError("a residual launch needs an fp32 (m, width) out tensor")
-        mode = 2
+        if out is None or out.dtype not in (torch.float32, torch.float16) or out.shape[0] != m or out.stride(1) != 1:
+            raise ValueError("a residual launch needs an fp32 or fp16 (m, width) out tensor")
+        mode = 2 if out.dtype == torch.float32 else 3
     else:
         mode = _MODES[out_dtype]
         if out is None:

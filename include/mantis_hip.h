@@ -363,14 +363,16 @@ int32_t mantis_stone_attention(const void* q, const int64_t* q_strides, const vo
  *   h[i]     = relu(h[i])                      if relu
  *   y[i]     = h[i] W3^T + b3                  if w3 (n3 outputs), else h[i]
  *   out[i]   = y[i] (out_mode 0: fp16 store, 1: fp32 store) or out[i] += y[i]
- *              (out_mode 2: fp32 residual, in place)
+ *              (out_mode 2: fp32 residual, in place; out_mode 3: fp16 residual,
+ *              added in fp32 and rounded once)
  * The LayerNorm affine is folded into W1/b1 by the caller.  x is fp32 or
  * fp16 (rows of stride ldx), x2 fp32 or fp16; W1/W2 (n1, 128), W3 (n3, n1)
  * fp16 row-major; b1/add1/add2 (.., n1) and b3 (n3) fp32.  fp16 MFMA with
  * fp32 accumulation and fp32 LayerNorm statistics.  Supported shapes: the
- * projection (n1 in 128/256/384, fp16 out), the residual projection
- * (n1 = 128, add), the two-layer residual MLPs (n1 = 128 with x2, n1 = 256
- * without) and the two-layer head (n1 = 256 with x2, fp32 out).
+ * projection (n1 in 128/256/384/512 from fp32 rows, 256/512 from fp16 rows,
+ * fp16 out), the residual projection (n1 = 128, fp32 or fp16 residual), the
+ * two-layer residual MLPs (n1 = 128 with x2 into fp32 or fp16 residual rows,
+ * n1 = 256 without) and the two-layer head (n1 = 256 with x2, fp32 out).
  */
 int32_t mantis_fused_linear(const void* x, int32_t x_dtype, int64_t ldx, const int64_t* x_rows,
                             int64_t n_x, int64_t m, int32_t layer_norm, const void* x2,

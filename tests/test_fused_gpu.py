@@ -40,7 +40,7 @@ def _h(x):
 
 
 @pytest.mark.parametrize("n1,xdt", [(128, torch.float32), (256, torch.float32), (384, torch.float32),
-                                    (512, torch.float32), (256, H16)])
+                                    (512, torch.float32), (256, H16), (512, H16)])
 def test_projection_with_layer_norm(device, n1, xdt):
     gen = _g(n1)
     m = 1000
@@ -67,6 +67,12 @@ def test_residual_projection(device, xdt):
     ops.fused_linear(x.to(device), w.to(device), b.to(device), out=out, residual=True)
     exp = r + _h(x.float()) @ w.float().t() + b
     torch.testing.assert_close(out.cpu(), exp, rtol=1e-4, atol=1e-4)
+    # fp16 residual rows: added in fp32, rounded once
+    r16 = r.to(H16)
+    out16 = r16.to(device)
+    ops.fused_linear(x.to(device), w.to(device), b.to(device), out=out16, residual=True)
+    exp16 = (r16.float() + _h(x.float()) @ w.float().t() + b).to(H16).float()
+    torch.testing.assert_close(out16.float().cpu(), exp16, rtol=2e-3, atol=2e-3)
 
 
 @pytest.mark.parametrize("x2dt", [torch.float32, H16])
@@ -87,6 +93,18 @@ def test_pair_mlp_residual(device, x2dt):
     hid = F.relu(_h(_ln(r)) @ w1.float().t() + _h(x2.float()) @ w2.float().t() + b1 + add2[rows])
     exp = r + _h(hid) @ w3.float().t() + b3
     torch.testing.assert_close(out.cpu(), exp, rtol=2e-3, atol=2e-3)
+    if x2dt == H16:
+        # fp16 rows in, LayerNorm, fp16 residual out (the window state)
+        r16 = r.to(H16)
+        out16 = r16.to(device)
+        ops.fused_linear(out16, w1.to(device), b1.to(device), layer_norm=True, x2=x2.to(device), w2=w2.to(device),
+                         add2=add2.to(device), add2_rows=rows.to(device), relu=True, w3=w3.to(device),
+                         b3=b3.to(device), out=out16, residual=True)
+        ops.raise_on_device_error(device)
+        rf = r16.float()
+        hid = F.relu(_h(_ln(rf)) @ w1.float().t() + _h(x2.float()) @ w2.float().t() + b1 + add2[rows])
+        exp16 = (rf + _h(hid) @ w3.float().t() + b3).to(H16).float()
+        torch.testing.assert_close(out16.float().cpu(), exp16, rtol=3e-3, atol=3e-3)
 
 
 def test_ffn_residual_with_add1(device):
