@@ -17,9 +17,9 @@ __device__ __forceinline__ float group16_sum(float x) {
 }
 
 // LayerNorm over rows of 128 (eps 1e-5, biased variance), 16 lanes per row.
-template <typename TO>
+template <typename TI, typename TO>
 __global__ void __launch_bounds__(256)
-layer_norm_kernel(const float* __restrict__ x, int64_t ldx, int64_t m, const float* __restrict__ gamma,
+layer_norm_kernel(const TI* __restrict__ x, int64_t ldx, int64_t m, const float* __restrict__ gamma,
                   const float* __restrict__ beta, TO* __restrict__ out, int64_t ldo) {
   const int64_t row = int64_t(blockIdx.x) * 16 + threadIdx.x / 16;
   const int lane = threadIdx.x % 16;
@@ -197,20 +197,27 @@ using namespace mantis;
 
 extern "C" {
 
-int32_t mantis_layer_norm(const float* x, int64_t ldx, int64_t m, const float* gamma, const float* beta,
-                          void* out, int32_t out_dtype, int64_t ldo, void* stream) {
+int32_t mantis_layer_norm(const void* x, int32_t x_dtype, int64_t ldx, int64_t m, const float* gamma,
+                          const float* beta, void* out, int32_t out_dtype, int64_t ldo, void* stream) {
   if (m == 0) return MANTIS_OK;
   if (!x || !gamma || !beta || !out || m < 0 || ldx < kRow || ldo < kRow || ldx % 8 || ldo % 8)
     return MANTIS_E_ARG;
   if (!aligned16(x) || !aligned16(gamma) || !aligned16(beta) || !aligned16(out)) return MANTIS_E_ARG;
   const unsigned grid = unsigned((m + 15) / 16);
   hipStream_t s = as_stream(stream);
-  if (out_dtype == MANTIS_F32)
-    layer_norm_kernel<float><<<grid, 256, 0, s>>>(x, ldx, m, gamma, beta, static_cast<float*>(out), ldo);
-  else if (out_dtype == MANTIS_F16)
-    layer_norm_kernel<_Float16><<<grid, 256, 0, s>>>(x, ldx, m, gamma, beta, static_cast<_Float16*>(out), ldo);
-  else
-    return MANTIS_E_ARG;
+  auto run = [&](auto ti) {
+    using TI = decltype(ti);
+    const TI* xi = static_cast<const TI*>(x);
+    if (out_dtype == MANTIS_F32)
+      layer_norm_kernel<TI, float><<<grid, 256, 0, s>>>(xi, ldx, m, gamma, beta, static_cast<float*>(out), ldo);
+    else
+      layer_norm_kernel<TI, _Float16><<<grid, 256, 0, s>>>(xi, ldx, m, gamma, beta, static_cast<_Float16*>(out),
+                                                           ldo);
+  };
+  if (out_dtype != MANTIS_F32 && out_dtype != MANTIS_F16) return MANTIS_E_ARG;
+  if (x_dtype == MANTIS_F32) run(float{});
+  else if (x_dtype == MANTIS_F16) run(_Float16{});
+  else return MANTIS_E_ARG;
   return launched();
 }
 

@@ -527,9 +527,8 @@ def _trunk(model, b: Batch, plan: Plan, raw_cells: bool = False):
     # the window state is stored in fp16 in the cell-node configuration, like
     # the cell state (each update adds in fp32 and rounds once); the knob-off
     # cell pass keeps it in fp32 for its compensated-weight launches
-    w = P["window_table.weight"].index_select(0, b.window_feat)
-    if cfg.cell_nodes:
-        w = w.to(HALF)
+    wtab = P["window_table.weight"]
+    w = (wtab.to(HALF) if cfg.cell_nodes else wtab).index_select(0, b.window_feat)
     c = None
     if cfg.cell_nodes:
         # covered cells start from cell_base, the others from their nearest-stone
@@ -543,11 +542,11 @@ def _trunk(model, b: Batch, plan: Plan, raw_cells: bool = False):
     for i in range(cfg.blocks):
         _block(W, P, i, plan, b, sg, w, c, sw_all, i + 1 < cfg.blocks)
     g = sg[n_s:].view(p, GLOBAL_ROWS, 128)
-    w_out = ops.layer_norm(w.float(), P["ln_out.weight"], P["ln_out.bias"], F32)
+    w_out = ops.layer_norm(w, P["ln_out.weight"], P["ln_out.bias"], F32)
     g_out = F.layer_norm(g, (128,), P["ln_out.weight"], P["ln_out.bias"], 1e-5).mean(dim=1)
     if c is None:
         return w_out, g_out, None
-    cells = c if raw_cells else ops.layer_norm(c.float(), P["ln_out.weight"], P["ln_out.bias"], HALF)
+    cells = c if raw_cells else ops.layer_norm(c, P["ln_out.weight"], P["ln_out.bias"], HALF)
     return w_out, g_out, cells
 
 

@@ -969,12 +969,13 @@ def split_weight(w: Tensor) -> Tensor:
 
 def layer_norm(x: Tensor, gamma: Tensor, beta: Tensor, out_dtype: torch.dtype = torch.float32) -> Tensor:
     dev = _on_gpu(x, gamma, beta)
-    if x.ndim != 2 or x.shape[1] != 128 or x.dtype != torch.float32 or x.stride(1) != 1:
-        raise ValueError("layer_norm takes fp32 (n, 128) rows")
+    if x.ndim != 2 or x.shape[1] != 128 or x.dtype not in (torch.float32, torch.float16) or x.stride(1) != 1:
+        raise ValueError("layer_norm takes fp32 or fp16 (n, 128) rows")
     out = torch.empty(x.shape, dtype=out_dtype, device=dev)
     g32, b32 = gamma.float().contiguous(), beta.float().contiguous()
-    _launch(f"layer_norm_{_SHORT[out_dtype]}", x.shape[0] * 128 * (4 + out.element_size()), 0, lambda: _check(
-        _lib().mantis_layer_norm(_ptr(x), x.stride(0), x.shape[0], _ptr(g32), _ptr(b32), _ptr(out),
+    nbytes = x.shape[0] * 128 * (x.element_size() + out.element_size())
+    _launch(f"layer_norm_{_SHORT[out_dtype]}", nbytes, 0, lambda: _check(
+        _lib().mantis_layer_norm(_ptr(x), _dt(x), x.stride(0), x.shape[0], _ptr(g32), _ptr(b32), _ptr(out),
                                  _MODES_LN[out_dtype], 128, _stream()), "layer_norm"))
     return out
 

@@ -405,10 +405,10 @@ int32_t mantis_fused_linear_split(const void* x, int32_t x_dtype, int64_t ldx, c
 
 /*
  * Row LayerNorm over rows of 128 features (eps 1e-5, biased variance), fp32
- * in, fp32 or fp16 out (nn.LayerNorm as the trunk's shared ln_out applies
+ * or fp16 in (x_dtype), fp32 or fp16 out (nn.LayerNorm as the trunk's shared ln_out applies
  * it, python/mantisnet/mantisnet/model.py:973-985).
  */
-int32_t mantis_layer_norm(const float* x, int64_t ldx, int64_t m, const float* gamma,
+int32_t mantis_layer_norm(const void* x, int32_t x_dtype, int64_t ldx, int64_t m, const float* gamma,
                           const float* beta, void* out, int32_t out_dtype, int64_t ldo,
                           void* stream);
 

@@ -151,6 +151,10 @@ def test_layer_norm_rows(device):
     torch.testing.assert_close(out.cpu(), F.layer_norm(x, (128,), g, b, 1e-5), rtol=1e-5, atol=1e-5)
     out16 = ops.layer_norm(x.to(device), g.to(device), b.to(device), H16)
     torch.testing.assert_close(out16.float().cpu(), F.layer_norm(x, (128,), g, b, 1e-5), rtol=2e-3, atol=2e-3)
+    # fp16 rows in: the statistics of the widened rows
+    xh = x.to(H16)
+    out_h = ops.layer_norm(xh.to(device), g.to(device), b.to(device))
+    torch.testing.assert_close(out_h.cpu(), F.layer_norm(xh.float(), (128,), g, b, 1e-5), rtol=1e-5, atol=1e-5)
 
 
 def test_value_read_matches_padded_masked_softmax(device):
