@@ -188,9 +188,21 @@ __global__ void __launch_bounds__(kThreads) attn_substage_kernel(SubArgs a) {
       pa[s] = a.st[s].seg_ptr[rc];
       pb[s] = a.st[s].seg_ptr[rc + 1];
     }
+    // the row state: fp32 rows stay fp32 in registers across the stages;
+    // fp16 rows stay packed (half the registers) and are rounded after each
+    // stage, exactly as a launch per stage would leave them
+    constexpr bool kPacked = sizeof(TX) == 2;
     float xv[4][8];
+    uint4 xh[kPacked ? 4 : 1];
+    if constexpr (kPacked) {
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) load8_nt(xs + rc * a.ldx + 32 * ks + 8 * g, xv[ks]);
+      for (int ks = 0; ks < 4; ++ks)
+        xh[ks] = __builtin_bit_cast(uint4, __builtin_nontemporal_load(
+                                               reinterpret_cast<const nt_f16x8_t*>(xs + rc * a.ldx + 32 * ks + 8 * g)));
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) load8_nt(xs + rc * a.ldx + 32 * ks + 8 * g, xv[ks]);
+    }
     int64_t lo[kStages], hi[kStages];
 #pragma unroll
     for (int s = 0; s < kStages; ++s) {
@@ -230,6 +242,14 @@ __global__ void __launch_bounds__(kThreads) attn_substage_kernel(SubArgs a) {
       // the first batch's entries, requested before the projection
       if (maxc > 0) fetch(0);
       // ---- LayerNorm + Q projection
+      if constexpr (kPacked) {
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          const f16x8_t h = __builtin_bit_cast(f16x8_t, xh[ks]);
+#pragma unroll
+          for (int t = 0; t < 8; ++t) xv[ks][t] = float(h[t]);
+        }
+      }
       uint32_t qh[16];
       {
         float sum = 0.f;
@@ -354,17 +374,32 @@ __global__ void __launch_bounds__(kThreads) attn_substage_kernel(SubArgs a) {
             d = mfma16x16x32(wf, ab[ks], d);
           }
           const float4 b = *reinterpret_cast<const float4*>(S.bo + 32 * (nt >> 1) + 8 * g + 4 * (nt & 1));
-          float* xr = xv[nt >> 1] + 4 * (nt & 1);
-          xr[0] += d[0] + b.x;
-          xr[1] += d[1] + b.y;
-          xr[2] += d[2] + b.z;
-          xr[3] += d[3] + b.w;
+          if constexpr (kPacked) {
+            // widen, add in fp32, round once
+            uint32_t* w = reinterpret_cast<uint32_t*>(&xh[nt >> 1]) + 2 * (nt & 1);
+            const f16x2_t h0 = __builtin_bit_cast(f16x2_t, w[0]), h1 = __builtin_bit_cast(f16x2_t, w[1]);
+            w[0] = pack_f16x2(float(h0[0]) + (d[0] + b.x), float(h0[1]) + (d[1] + b.y));
+            w[1] = pack_f16x2(float(h1[0]) + (d[2] + b.z), float(h1[1]) + (d[3] + b.w));
+          } else {
+            float* xr = xv[nt >> 1] + 4 * (nt & 1);
+            xr[0] += d[0] + b.x;
+            xr[1] += d[1] + b.y;
+            xr[2] += d[2] + b.z;
+            xr[3] += d[3] + b.w;
+          }
         }
       }
     }
     if (live) {
+      if constexpr (kPacked) {
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) store8_nt(xs + row * a.ldx + 32 * ks + 8 * g, xv[ks]);
+        for (int ks = 0; ks < 4; ++ks)
+          __builtin_nontemporal_store(__builtin_bit_cast(nt_f16x8_t, xh[ks]),
+                                      reinterpret_cast<nt_f16x8_t*>(xs + row * a.ldx + 32 * ks + 8 * g));
+      } else {
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) store8_nt(xs + row * a.ldx + 32 * ks + 8 * g, xv[ks]);
+      }
     }
   }
 }

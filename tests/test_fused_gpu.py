@@ -271,15 +271,21 @@ def test_two_substages_in_one_pass_match_two_launches(device, with_vcls):
     ops.raise_on_device_error(device)
     torch.testing.assert_close(got.cpu(), ref.cpu(), rtol=1e-6, atol=1e-6)
     assert not torch.equal(got.cpu(), x)
-    # fp16 rows: widened on load, rounded once on the store, so bitwise the
+    # fp16 rows: widened on load and rounded after each stage, so the pass
+    # is bitwise two single-stage fp16 launches, and each stage bitwise the
     # fp32 path on the same values rounded to nearest even
     x16 = x.to(H16)
     got16 = x16.to(device)
     ops.attention_substages(got16, [s1, s2])
-    ref32 = x16.float().to(device)
-    ops.attention_substages(ref32, [s1, s2])
+    two16 = x16.to(device)
+    ops.attention_substages(two16, [s1])
+    mid32 = x16.float().to(device)
+    ops.attention_substages(mid32, [s1])
     ops.raise_on_device_error(device)
-    assert got16.dtype == H16 and torch.equal(got16.cpu(), ref32.cpu().to(H16))
+    assert torch.equal(two16.cpu(), mid32.cpu().to(H16))
+    ops.attention_substages(two16, [s2])
+    ops.raise_on_device_error(device)
+    assert got16.dtype == H16 and torch.equal(got16.cpu(), two16.cpu())
 
 
 def test_row_order_changes_the_tiles_not_the_results(device):
