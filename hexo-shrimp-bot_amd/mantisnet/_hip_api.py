@@ -31,6 +31,12 @@ SIGNATURES = {
     "mantis_class_reduce": ([vp, i32, i64, i64, i64, vp, i64, vp, i64, vp, i64, vp, i32, vp, vp], i32),
     "mantis_cell_pass": ([vp, i32, i64, i64, i64, vp, i32, i64, i64, vp, i64, vp, vp, i64, vp, vp, vp, vp, vp, vp],
                          i32),
+    "mantis_attention_backward_workspace": ([i64, i64, i64], i64),
+    "mantis_attention_backward": ([vp, vp, vp, i32, i64, i64, i64, i64, i64, vp, i64, vp, i32, vp, i64, vp, vp, vp,
+                                   vp, vp, vp, i64, vp, vp, vp, vp, vp, vp, i64, vp, vp, vp, vp, vp, vp, vp], i32),
+    "mantis_row_encode_backward_workspace": ([i64, i64], i64),
+    "mantis_row_encode_backward": ([vp, i32, i64, i64, vp, i32, i64, vp, i64, vp, vp, vp, i64, vp, vp, vp, vp, vp, i64,
+                                    vp, vp, vp, vp], i32),
     "mantis_cell_pass_backward_workspace": ([i64, i64, i64, i64], i64),
     "mantis_cell_pass_backward": ([vp, i32, i64, i64, i64, vp, i32, i64, i64, vp, i32, i64, vp, i64, vp, vp, i64, vp,
                                    vp, vp, vp, vp, i64, vp, vp, vp, vp], i32),

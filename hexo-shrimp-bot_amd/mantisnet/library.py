@@ -3,10 +3,13 @@
 Every operator keeps the reference's qualified name, argument list and
 output structure, so code written against the reference's ``torch.ops``
 surface runs unchanged.  Each has a fake (meta) implementation for tracing.
-The run reductions and the cell pass carry their backward (the reference's
-``register_autograd`` pairs, as HIP run reductions); the attention-family and
-latent operators are forward-only here, and asking them for a gradient
-raises.
+Every differentiable operator carries the reference's backward
+(``register_autograd`` with the reference's ``*_backward`` operators where it
+registers them): the run reductions and the cell pass as run reductions, the
+attention family and the window latents through one segment-attention
+backward (query-major pass, source-major pass, sliced class sums), the
+action-row encoder through masked run sums.  Every backward sums in a fixed
+order: two calls agree bitwise.
 
 Differences from the reference, all deliberate:
 
@@ -22,7 +25,8 @@ attention.py:719-760, message_passing.py:191-227 and 344-365,
 cell_latents.py:168-208 and 834-952, cell_nodes.py:97-147,
 window_latents.py:38-64, 553-587 and 648-664, row_encoder.py:368-380,
 relay.py:452-574; backward registrations message_passing.py:234-279 and
-373-431.
+373-431, attention.py:775-892, cell_latents.py:869-1001,
+window_latents.py:589-715, row_encoder.py:382-413.
 """
 
 from __future__ import annotations
@@ -33,17 +37,6 @@ from torch import Tensor
 from . import ops, tables
 
 _NS = "mantisnet"
-
-
-def _no_grad(name):
-    def backward(ctx, *grads):
-        raise RuntimeError(f"{_NS}::{name} is inference-only on this build (no backward kernel)")
-
-    return backward
-
-
-def _register_inference_only(op, name: str) -> None:
-    op.register_autograd(_no_grad(name), setup_context=lambda ctx, inputs, output: None)
 
 
 # ----------------------------------------------------------------- stone attention
@@ -61,6 +54,34 @@ def fused_attention(q: Tensor, k: Tensor, v: Tensor, seq_lens: Tensor) -> tuple[
 @fused_attention.register_fake
 def _(q, k, v, seq_lens):
     return torch.empty_like(q), q.new_empty(q.shape[:3], dtype=torch.float32)
+
+
+@torch.library.custom_op(f"{_NS}::fused_attention_backward", mutates_args=())
+def fused_attention_backward(q: Tensor, k: Tensor, v: Tensor, seq_lens: Tensor, out: Tensor, lse: Tensor,
+                             grad_out: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+    """(dq, dk, dv) of fused_attention; pad rows and keys get zero gradients."""
+    dq, dk, dv = ops.stone_attention_backward(q, k, v, seq_lens, lse, grad_out)
+    return dq.contiguous(), dk.contiguous(), dv.contiguous()
+
+
+@fused_attention_backward.register_fake
+def _(q, k, v, seq_lens, out, lse, grad_out):
+    return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+
+
+def _fa_setup(ctx, inputs, output) -> None:
+    q, k, v, seq_lens = inputs
+    out, lse = output
+    ctx.save_for_backward(q, k, v, seq_lens, out, lse)
+    ctx.mark_non_differentiable(lse)
+
+
+def _fa_backward(ctx, grad_out, _grad_lse):
+    dq, dk, dv = fused_attention_backward(*ctx.saved_tensors, grad_out)
+    return dq, dk, dv, None
+
+
+fused_attention.register_autograd(_fa_backward, setup_context=_fa_setup)
 
 
 # ----------------------------------------------------------------- run reductions
@@ -299,6 +320,57 @@ def _(q, k, v, bias, seg_ptr, src, cls, qid, sseg_ptr, sqid, scls, cptr, cedge_q
             q.new_empty((n_q, heads), dtype=torch.float32))
 
 
+@torch.library.custom_op(f"{_NS}::cell_attention_backward", mutates_args=())
+def cell_attention_backward(q: Tensor, k: Tensor, v: Tensor, bias: Tensor, vcls: Tensor, seg_ptr: Tensor,
+                            src: Tensor, cls: Tensor, qid: Tensor, sseg_ptr: Tensor, sqid: Tensor, scls: Tensor,
+                            cptr: Tensor, cedge_q: Tensor, m: Tensor, l: Tensor,
+                            grad_out: Tensor) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """(dq, dk, dv, dbias, dvcls) of cell_attention."""
+    return ops.attention_backward(q, k, v, bias, vcls, grad_out, m, l, seg_ptr, src, cls, qid, sseg_ptr, sqid, scls,
+                                  cptr, cedge_q)
+
+
+@cell_attention_backward.register_fake
+def _(q, k, v, bias, vcls, seg_ptr, src, cls, qid, sseg_ptr, sqid, scls, cptr, cedge_q, m, l, grad_out):
+    return (torch.empty_like(q), torch.empty_like(k), torch.empty_like(v), torch.empty_like(bias),
+            torch.empty_like(vcls))
+
+
+@torch.library.custom_op(f"{_NS}::cell_attention_plain_backward", mutates_args=())
+def cell_attention_plain_backward(q: Tensor, k: Tensor, v: Tensor, bias: Tensor, seg_ptr: Tensor, src: Tensor,
+                                  cls: Tensor, qid: Tensor, sseg_ptr: Tensor, sqid: Tensor, scls: Tensor,
+                                  cptr: Tensor, cedge_q: Tensor, m: Tensor, l: Tensor,
+                                  grad_out: Tensor) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """(dq, dk, dv, dbias) of cell_attention_plain."""
+    dq, dk, dv, dbias, _ = ops.attention_backward(q, k, v, bias, None, grad_out, m, l, seg_ptr, src, cls, qid,
+                                                  sseg_ptr, sqid, scls, cptr, cedge_q)
+    return dq, dk, dv, dbias
+
+
+@cell_attention_plain_backward.register_fake
+def _(q, k, v, bias, seg_ptr, src, cls, qid, sseg_ptr, sqid, scls, cptr, cedge_q, m, l, grad_out):
+    return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v), torch.empty_like(bias)
+
+
+def _ca_setup(ctx, inputs, output) -> None:
+    _out, m, l = output
+    ctx.save_for_backward(*inputs, m, l)
+
+
+def _ca_backward(ctx, grad_out, _gm, _gl):
+    grads = cell_attention_backward(*ctx.saved_tensors, grad_out)
+    return grads + (None,) * 9
+
+
+def _ca_plain_backward(ctx, grad_out, _gm, _gl):
+    grads = cell_attention_plain_backward(*ctx.saved_tensors, grad_out)
+    return grads + (None,) * 9
+
+
+cell_attention.register_autograd(_ca_backward, setup_context=_ca_setup)
+cell_attention_plain.register_autograd(_ca_plain_backward, setup_context=_ca_setup)
+
+
 # ----------------------------------------------------------------- window latents
 
 
@@ -351,6 +423,56 @@ def _(q, k, v, window_pos, offsets, order):
             q.new_empty(q.shape[:-1], dtype=torch.float32))
 
 
+@torch.library.custom_op(f"{_NS}::window_latent_read_backward", mutates_args=())
+def window_latent_read_backward(q: Tensor, k: Tensor, v: Tensor, window_pos: Tensor, offsets: Tensor, order: Tensor,
+                                out: Tensor, m: Tensor, l: Tensor,
+                                grad_out: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+    """(dq, dk, dv) of window_latent_read."""
+    return ops.latent_read_backward(q, k, v, window_pos, offsets, order, m, l, grad_out)
+
+
+@window_latent_read_backward.register_fake
+def _(q, k, v, window_pos, offsets, order, out, m, l, grad_out):
+    return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+
+
+@torch.library.custom_op(f"{_NS}::window_latent_broadcast_backward", mutates_args=())
+def window_latent_broadcast_backward(q: Tensor, k: Tensor, v: Tensor, window_pos: Tensor, offsets: Tensor,
+                                     order: Tensor, m: Tensor, l: Tensor,
+                                     grad_out: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+    """(dq, dk, dv) of window_latent_broadcast."""
+    return ops.latent_broadcast_backward(q, k, v, window_pos, offsets, order, m, l, grad_out)
+
+
+@window_latent_broadcast_backward.register_fake
+def _(q, k, v, window_pos, offsets, order, m, l, grad_out):
+    return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+
+
+def _read_setup(ctx, inputs, output) -> None:
+    out, m, l = output
+    ctx.save_for_backward(*inputs, out, m, l)
+
+
+def _read_backward(ctx, grad_out, _gm, _gl):
+    dq, dk, dv = window_latent_read_backward(*ctx.saved_tensors, grad_out)
+    return dq, dk, dv, None, None, None
+
+
+def _broadcast_setup(ctx, inputs, output) -> None:
+    _out, m, l = output
+    ctx.save_for_backward(*inputs, m, l)
+
+
+def _broadcast_backward(ctx, grad_out, _gm, _gl):
+    dq, dk, dv = window_latent_broadcast_backward(*ctx.saved_tensors, grad_out)
+    return dq, dk, dv, None, None, None
+
+
+window_latent_read.register_autograd(_read_backward, setup_context=_read_setup)
+window_latent_broadcast.register_autograd(_broadcast_backward, setup_context=_broadcast_setup)
+
+
 # ----------------------------------------------------------------- action rows
 
 
@@ -373,6 +495,20 @@ def action_row_encode(pre_w: Tensor, table: Tensor, edge_window: Tensor, edge_cl
 @action_row_encode.register_fake
 def _(pre_w, table, edge_window, edge_class, edge_cell, edge_rev, n_cells):
     return pre_w.new_empty((n_cells, pre_w.shape[1]), dtype=torch.float32)
+
+
+def _rows_setup(ctx, inputs, output) -> None:
+    pre_w, table, edge_window, edge_class, edge_cell, edge_rev, _n_cells = inputs
+    ctx.save_for_backward(pre_w, table, edge_window, edge_class, edge_cell, edge_rev)
+
+
+def _rows_backward(ctx, grad_out):
+    pre_w, table, edge_window, edge_class, edge_cell, edge_rev = ctx.saved_tensors
+    dpre, dtable = ops.row_encode_backward(pre_w, table, edge_window, edge_class, edge_cell, edge_rev, grad_out)
+    return dpre, dtable, None, None, None, None, None
+
+
+action_row_encode.register_autograd(_rows_backward, setup_context=_rows_setup)
 
 
 # ----------------------------------------------------------------- table derivation
@@ -435,9 +571,6 @@ OPERATORS = (
     "fused_attention", "aggregate_to_windows", "aggregate_to_stones", "class_row_sum", "incidence_row_sum",
     "cell_attention", "cell_attention_plain", "window_latent_read", "window_latent_broadcast",
     "action_row_encode", "cell_tables", "cell_node_edge_tables", "window_latent_layout", "cell_pass",
-    "cell_pass_backward",
+    "cell_pass_backward", "fused_attention_backward", "cell_attention_backward", "cell_attention_plain_backward",
+    "window_latent_read_backward", "window_latent_broadcast_backward",
 )
-
-for _name in ("fused_attention", "cell_attention", "cell_attention_plain", "window_latent_read",
-              "window_latent_broadcast", "action_row_encode"):
-    _register_inference_only(globals()[_name], _name)

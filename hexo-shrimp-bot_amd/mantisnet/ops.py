@@ -321,6 +321,166 @@ def _check_cell_pass(x, emb, cell_ptr, edge_window, edge_class, win_ptr, edge_wc
         raise ValueError("all cell-pass inputs must be on one device")
 
 
+def attention_backward(q: Tensor, k: Tensor, v: Tensor, bias: Tensor | None, vcls: Tensor | None, grad_out: Tensor,
+                       m: Tensor, l: Tensor, seg_ptr: Tensor, src: Tensor, cls: Tensor | None, qid: Tensor | None,
+                       sseg_ptr: Tensor, sqid: Tensor, scls: Tensor | None, cptr: Tensor | None,
+                       cedge_q: Tensor | None):
+    """(dq, dk, dv, dbias, dvcls) of the segment attention over query-major
+    entries (seg_ptr, src, cls) with the source-major (sseg_ptr, sqid, scls)
+    and class-major (cptr, cedge_q) views of the same entries; rows of
+    4 heads x 32 (q, k, v shaped (n, 4, 32) or (n, 128)); m / l the
+    forward's softmax statistics.  bias None: untyped entries (dbias and
+    dvcls None)."""
+    dev = _on_gpu(q, k, v, bias, vcls, grad_out, m, l, seg_ptr, src, cls, qid, sseg_ptr, sqid, scls, cptr, cedge_q)
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("q, k and v must share one dtype")
+    n_q, n_k = q.shape[0], k.shape[0]
+    if v.shape[0] != n_k:
+        raise ValueError("k and v must have one row count")
+    q2, ldq = _rows128(q, "q")
+    k2, ldk = _rows128(k, "k")
+    v2, ldv = _rows128(v, "v")
+    go = grad_out.reshape(n_q, 128).float().contiguous()
+    m32 = m.reshape(n_q, 4).float().contiguous()
+    l32 = l.reshape(n_q, 4).float().contiguous()
+    typed = bias is not None
+    n_cls = bias.shape[1] if typed else 0
+    bias32 = bias.float().contiguous() if typed else None
+    if vcls is not None:
+        if not typed or vcls.shape != (n_cls, 128):
+            raise ValueError("vcls must be (classes, 128) with a bias")
+        vcls = vcls.contiguous()
+    ids = {n: (None if t is None else _i64(t, n)) for n, t in (
+        ("seg_ptr", seg_ptr), ("src", src), ("cls", cls), ("qid", qid), ("sseg_ptr", sseg_ptr), ("sqid", sqid),
+        ("scls", scls), ("cptr", cptr), ("cedge_q", cedge_q))}
+    if ids["seg_ptr"].numel() != n_q + 1 or ids["sseg_ptr"].numel() != n_k + 1:
+        raise ValueError("seg_ptr / sseg_ptr must have one entry per row plus one")
+    e = ids["src"].numel()
+    if ids["sqid"].numel() != e or (typed and (ids["cls"] is None or ids["scls"] is None or ids["cptr"] is None
+                                               or ids["cedge_q"] is None)):
+        raise ValueError("typed entries need cls, scls, cptr and cedge_q of one length")
+    dq = torch.empty((n_q, 128), dtype=q.dtype, device=dev)
+    dk = torch.empty((n_k, 128), dtype=q.dtype, device=dev)
+    dv = torch.empty((n_k, 128), dtype=q.dtype, device=dev)
+    dbias_t = torch.empty((n_cls, 4), dtype=torch.float32, device=dev) if typed else None
+    dvcls = torch.empty((n_cls, 128), dtype=vcls.dtype, device=dev) if vcls is not None else None
+    ws = _workspace(_lib().mantis_attention_backward_workspace(n_q, e, n_cls), dev)
+    if n_q or n_k:
+        nbytes = 2 * e * 128 * (3 * q.element_size() + 4) + (n_q + 2 * n_k) * 128 * q.element_size()
+        _launch(f"attention_backward_{_SHORT[q.dtype]}", nbytes, 8 * e * 128, lambda: _check(
+            _lib().mantis_attention_backward(
+                _ptr(q2), _ptr(k2), _ptr(v2), _dt(q), ldq, ldk, ldv, n_q, n_k, _ptr(bias32), n_cls, _ptr(vcls),
+                _dt(vcls) if vcls is not None else 0, _ptr(go), 128, _ptr(m32), _ptr(l32), _ptr(ids["seg_ptr"]),
+                _ptr(ids["src"]), _ptr(ids["cls"]), _ptr(ids["qid"]), e, _ptr(ids["sseg_ptr"]), _ptr(ids["sqid"]),
+                _ptr(ids["scls"]), _ptr(ids["cptr"]), _ptr(ids["cedge_q"]), _ptr(ws), ws.numel(), _ptr(dq),
+                _ptr(dk), _ptr(dv), _ptr(dbias_t), _ptr(dvcls), _ptr(error_flag(dev)), _stream(),
+            ),
+            "attention_backward",
+        ))
+    dbias = dbias_t.t().contiguous().to(bias.dtype) if typed else None
+    return dq.view(q.shape), dk.view(k.shape), dv.view(v.shape), dbias, dvcls
+
+
+def _run_edges(offsets: Tensor, order: Tensor, slots: int):
+    """Row-major edge lists of 'every one of `slots` rows of position p meets
+    every window of p': per row p*slots+s the CSR of order[offsets[p]:offsets[p+1]]."""
+    cnt = (offsets[1:] - offsets[:-1]).repeat_interleave(slots)
+    ptr = torch.zeros(cnt.numel() + 1, dtype=torch.int64, device=offsets.device)
+    torch.cumsum(cnt, 0, out=ptr[1:])
+    rows = torch.repeat_interleave(torch.arange(cnt.numel(), device=offsets.device), cnt)
+    within = torch.arange(rows.numel(), device=offsets.device) - ptr[rows]
+    return ptr, order.index_select(0, offsets.index_select(0, rows // slots) + within)
+
+
+def _slot_edges(window_pos: Tensor, slots: int):
+    """Row-major edge lists of 'window w meets the `slots` latent rows of its position'."""
+    n = window_pos.numel()
+    ptr = torch.arange(0, slots * n + 1, slots, dtype=torch.int64, device=window_pos.device)
+    dst = (window_pos.repeat_interleave(slots) * slots
+           + torch.arange(slots, device=window_pos.device).repeat(n))
+    return ptr, dst
+
+
+def latent_read_backward(q, k, v, window_pos, offsets, order, m, l, grad_out):
+    """(dq, dk, dv) of latent_read: the four slot queries of each position
+    over its windows (window_latents.py:132-163)."""
+    p_ptr, p_src = _run_edges(offsets, order, 4)
+    w_ptr, w_dst = _slot_edges(window_pos, 4)
+    dq, dk, dv, _, _ = attention_backward(q.reshape(-1, 4, 32), k, v, None, None, grad_out, m, l, p_ptr, p_src, None,
+                                          None, w_ptr, w_dst, None, None, None)
+    return dq.view(q.shape), dk, dv
+
+
+def latent_broadcast_backward(q, k, v, window_pos, offsets, order, m, l, grad_out):
+    """(dq, dk, dv) of latent_broadcast: every window over its position's four
+    latent rows (window_latents.py:191-230)."""
+    w_ptr, w_dst = _slot_edges(window_pos, 4)
+    p_ptr, p_src = _run_edges(offsets, order, 4)
+    dq, dk, dv, _, _ = attention_backward(q, k.reshape(-1, 4, 32), v.reshape(-1, 4, 32), None, None, grad_out, m, l,
+                                          w_ptr, w_dst, None, None, p_ptr, p_src, None, None, None)
+    return dq, dk.view(k.shape), dv.view(v.shape)
+
+
+def stone_attention_backward(q, k, v, seq_lens, lse, grad_out):
+    """(dq, dk, dv) of stone_attention: every live query row of a position over
+    its live prefix, heads in blocks of four (the softmax statistics from
+    the forward's natural-log lse)."""
+    p, heads, t, hd = q.shape
+    if hd != 32 or heads % 4:
+        raise ValueError("the attention backward covers head_dim 32 and a multiple of 4 heads")
+    g = heads // 4
+    rows = lambda x: x.permute(0, 2, 1, 3).reshape(p * t * g, 4, 32)  # noqa: E731  (p, t, head block)
+    dev = q.device
+    lens = seq_lens.long().clamp(0, t)
+    # the live (i, j) pairs of every position and head block, row-major by i
+    cnt = torch.where(torch.arange(t, device=dev)[None, :] < lens[:, None], lens[:, None], 0)  # (p, t)
+    cnt = cnt.repeat_interleave(g, dim=1).reshape(-1)  # rows (p, t, g)
+    ptr = torch.zeros(cnt.numel() + 1, dtype=torch.int64, device=dev)
+    torch.cumsum(cnt, 0, out=ptr[1:])
+    r = torch.repeat_interleave(torch.arange(cnt.numel(), device=dev), cnt)
+    j = torch.arange(r.numel(), device=dev) - ptr[r]
+    pos, hb = r // (t * g), r % g
+    other = (pos * t + j) * g + hb  # row (p, j, hb)
+    m = lse.permute(0, 2, 1).reshape(p * t * g, 4)
+    ones = torch.ones_like(m)
+    dq, dk, dv, _, _ = attention_backward(rows(q), rows(k), rows(v), None, None,
+                                          grad_out.permute(0, 2, 1, 3).reshape(p * t * g, 4, 32), m, ones, ptr, other,
+                                          None, None, ptr, other, None, None, None)
+    back = lambda x: x.view(p, t, heads, hd).permute(0, 2, 1, 3)  # noqa: E731
+    return back(dq), back(dk), back(dv)
+
+
+def row_encode_backward(pre: Tensor, table: Tensor, edge_window: Tensor, edge_class: Tensor, edge_cell: Tensor,
+                        edge_rev: Tensor, grad_out: Tensor):
+    """(dpre, dtable) of row_encode (row_encoder.py:300-413): the ReLU mask
+    recomputed per entry, window-major sums for pre, class sums for the table."""
+    dev = _on_gpu(pre, table, edge_window, edge_class, edge_cell, edge_rev, grad_out)
+    if pre.ndim != 2 or pre.shape[1] != 128 or table.ndim != 2 or table.shape[1] != 128:
+        raise ValueError("pre and table must be (n, 128)")
+    pre = _row_major(pre)
+    table = table.contiguous()
+    edge_window, edge_class, edge_cell, edge_rev = (_i64(t, n) for t, n in (
+        (edge_window, "edge_window"), (edge_class, "edge_class"), (edge_cell, "edge_cell"), (edge_rev, "edge_rev")))
+    n_w, n_cls, n_cells = pre.shape[0], table.shape[0], grad_out.shape[0]
+    go = grad_out.reshape(n_cells, 128).float().contiguous()
+    win_ptr = runs_to_ptr(edge_window.index_select(0, edge_rev), n_w)
+    cls_order = torch.argsort(edge_class, stable=True)
+    cls_ptr = runs_to_ptr(edge_class.index_select(0, cls_order), n_cls)
+    e = edge_window.numel()
+    dpre = torch.empty((n_w, 128), dtype=pre.dtype, device=dev)
+    dtable = torch.empty((n_cls, 128), dtype=table.dtype, device=dev)
+    ws = _workspace(_lib().mantis_row_encode_backward_workspace(e, n_cls), dev)
+    _launch("row_encode_backward", e * (32 + 3 * 128 * 4) + (n_w + n_cls) * 128 * 4, 0, lambda: _check(
+        _lib().mantis_row_encode_backward(
+            _ptr(pre), _dt(pre), pre.stride(0), n_w, _ptr(table), _dt(table), n_cls, _ptr(go), n_cells,
+            _ptr(edge_window), _ptr(edge_class), _ptr(edge_cell), e, _ptr(win_ptr), _ptr(edge_rev), _ptr(cls_ptr),
+            _ptr(cls_order), _ptr(ws), ws.numel(), _ptr(dpre), _ptr(dtable), _ptr(error_flag(dev)), _stream(),
+        ),
+        "row_encode_backward",
+    ))
+    return dpre, dtable
+
+
 def cell_pass(x: Tensor, emb: Tensor, cell_ptr: Tensor, edge_window: Tensor, edge_class: Tensor, win_ptr: Tensor,
               edge_wcell: Tensor) -> Tensor:
     """The knob-off cell pass: out[w] = sum over the window's relay cells c of

@@ -97,6 +97,62 @@ int32_t mantis_class_reduce(const void* values, int32_t values_dtype, int64_t n_
                             int32_t* err_flag, void* stream);
 
 /*
+ * Backward of the segment attention (mantis_cell_attention and the
+ * window-latent read / broadcast, which are the same attention over other
+ * edge lists), rows of 4 heads x 32.  For query row i's entries e in
+ * [seg_ptr[i], seg_ptr[i+1]) with source src[e] and class cls[e]:
+ *   alpha_e  = exp(q_i.k_src / sqrt(32) + bias[h, cls] - m[i,h]) / l[i,h]
+ *   dalpha_e = grad_out_i . (v_src + vcls[cls])
+ *   delta_i  = sum_e alpha_e dalpha_e,   dscore_e = alpha_e (dalpha_e - delta_i)
+ *   dq_i = sum_e dscore_e k_src / sqrt(32)          (query-major pass)
+ *   dk_j = sum_e dscore_e q_i / sqrt(32), dv_j = sum_e alpha_e grad_out_i
+ *                                                   (source-major pass over
+ *                                                   sseg_ptr / sqid / scls)
+ *   dbias_t[c, h] = sum_e dscore_e, dvcls[c] = sum_e alpha_e grad_out_qid[e]
+ *                                                   (class-major: cptr / cedge_q,
+ *                                                   sliced, deterministic)
+ * q/k/v in dtype (fp32/bf16/fp16; row strides ldq/ldk/ldv, multiples of 8),
+ * grad_out fp32 (row stride ldgo), m/l (n_q, 4) fp32 as the forward returns
+ * them; dq/dk/dv contiguous in dtype, dbias_t (n_classes, 4) fp32, dvcls
+ * (n_classes, 128) in vcls_dtype.  bias NULL: untyped edges (no cls, scls,
+ * cptr, cedge_q, dbias_t); vcls NULL: no class values.  workspace: at least
+ * mantis_attention_backward_workspace(n_q, n_entries, n_classes or 0) bytes.
+ * Replaces mantisnet::cell_attention_backward / cell_attention_plain_backward
+ * (python/mantisnet/mantisnet/cell_latents.py:570-621, 680-797, 869-1001) and
+ * mantisnet::window_latent_read_backward / window_latent_broadcast_backward
+ * (window_latents.py:132-230, 503-551, 589-712).
+ */
+int64_t mantis_attention_backward_workspace(int64_t n_q, int64_t n_entries, int64_t n_classes);
+int32_t mantis_attention_backward(const void* q, const void* k, const void* v, int32_t dtype, int64_t ldq, int64_t ldk,
+                                  int64_t ldv, int64_t n_q, int64_t n_k, const float* bias, int64_t n_classes,
+                                  const void* vcls, int32_t vcls_dtype, const float* grad_out, int64_t ldgo,
+                                  const float* m, const float* l, const int64_t* seg_ptr, const int64_t* src,
+                                  const int64_t* cls, const int64_t* qid, int64_t n_entries, const int64_t* sseg_ptr,
+                                  const int64_t* sqid, const int64_t* scls, const int64_t* cptr,
+                                  const int64_t* cedge_q, void* workspace, int64_t workspace_bytes, void* dq,
+                                  void* dk, void* dv, float* dbias_t, void* dvcls, int32_t* err_flag, void* stream);
+
+/*
+ * Backward of the action-row encoder: with mask_e = pre[edge_window[e]] +
+ * table[edge_class[e]] > 0 (recomputed),
+ *   dpre[w]   = sum over the window's entries (win_ptr over edge_rev) of mask_e grad_out[edge_cell[e]]
+ *   dtable[c] = sum over the class's entries (cls_ptr over cls_order) of mask_e grad_out[edge_cell[e]]
+ * pre (n_w, ldp) and table (n_cls, 128) in their dtypes, grad_out
+ * (n_cells, 128) fp32; dpre / dtable contiguous in pre's / table's dtype.
+ * workspace: mantis_row_encode_backward_workspace(n_entries, n_cls) bytes.
+ * Replaces the backward of mantisnet::action_row_encode
+ * (python/mantisnet/mantisnet/row_encoder.py:115-413).
+ */
+int64_t mantis_row_encode_backward_workspace(int64_t n_entries, int64_t n_classes);
+int32_t mantis_row_encode_backward(const void* pre, int32_t pre_dtype, int64_t ldp, int64_t n_w, const void* table,
+                                   int32_t table_dtype, int64_t n_cls, const float* grad_out, int64_t n_cells,
+                                   const int64_t* edge_window, const int64_t* edge_class, const int64_t* edge_cell,
+                                   int64_t n_entries, const int64_t* win_ptr, const int64_t* edge_rev,
+                                   const int64_t* cls_ptr, const int64_t* cls_order, void* workspace,
+                                   int64_t workspace_bytes, void* dpre, void* dtable, int32_t* err_flag,
+                                   void* stream);
+
+/*
  * The knob-off cell pass (windows <- windows through shared empty cells):
  *   val[c] = ReLU(sum over the cell's entries e of x[edge_window[e]] + emb[edge_class[e]])
  *   out[w] = sum over the window's entries e of val[edge_wcell[e]]

@@ -49,6 +49,14 @@ REFERENCE_SCHEMAS = {
                    "edge_ccell"], 1),
     "cell_pass_backward": (["x", "emb", "cell_ptr", "edge_window", "edge_class", "win_ptr", "edge_wcell", "cls_ptr",
                             "edge_ccell", "grad_out"], 2),
+    # attention.py:823-832, cell_latents.py:869-889 and 953-972, window_latents.py:589-593 and 666-670
+    "fused_attention_backward": (["q", "k", "v", "seq_lens", "out", "lse", "grad_out"], 3),
+    "cell_attention_backward": (["q", "k", "v", "bias", "vcls", "seg_ptr", "src", "cls", "qid", "sseg_ptr", "sqid",
+                                 "scls", "cptr", "cedge_q", "m", "l", "grad_out"], 5),
+    "cell_attention_plain_backward": (["q", "k", "v", "bias", "seg_ptr", "src", "cls", "qid", "sseg_ptr", "sqid",
+                                       "scls", "cptr", "cedge_q", "m", "l", "grad_out"], 4),
+    "window_latent_read_backward": (["q", "k", "v", "window_pos", "offsets", "order", "out", "m", "l", "grad_out"], 3),
+    "window_latent_broadcast_backward": (["q", "k", "v", "window_pos", "offsets", "order", "m", "l", "grad_out"], 3),
 }
 
 
