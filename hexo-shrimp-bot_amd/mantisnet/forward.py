@@ -255,6 +255,8 @@ class Plan:
     layout_offsets: Tensor
     layout_order: Tensor
     covered_mask: Tensor  # (N_c,) bool
+    cov_rows: Tensor | None  # the covered cells (with decoder entries), ascending (cell-node configurations)
+    edge_wcell_cov: Tensor | None  # edge_wcell as indices into cov_rows
     cell_ptr: Tensor  # cell-major decoder CSR over all legal cells
     edge_window: Tensor
     edge_class: Tensor
@@ -331,6 +333,22 @@ def make_plan(model, b: Batch) -> Plan:
     cell_ptr = ops.runs_to_ptr(edge_cell.contiguous(), n_c)
     covered = cell_ptr[1:] > cell_ptr[:-1]
     win_ptr = ops.runs_to_ptr(edge_window[worder].contiguous(), n_w)
+    edge_wcell = edge_cell[worder]
+    # only the covered cells (those with decoder entries) are read by the
+    # windows: their compact list, for a k/v projection of those rows alone.
+    # The count comes from the batch's relay views (one per covered cell), so
+    # no device read is needed; the list is a scatter of the covered ranks
+    cov_rows = edge_wcell_cov = None
+    if cfg.cell_nodes and getattr(b, "relay_cell_ptr", None) is not None:
+        n_cov = b.relay_cell_ptr.shape[0] - 1
+        rank = torch.cumsum(covered, 0) - 1
+        # (a batch whose relay views disagree with its decoder entries leaves
+        # ranks past n_cov: they go to the spare slot, and the entries that
+        # name them are flagged by the sub-stage)
+        slots = torch.where(covered & (rank < n_cov), rank, n_cov)
+        cov_rows = torch.empty(n_cov + 1, dtype=torch.int64, device=dev).scatter_(
+            0, slots, torch.arange(n_c, device=dev))[:n_cov]
+        edge_wcell_cov = rank.index_select(0, edge_wcell)
     # radius edge tables (cell_nodes.py:23-94, model.py:843-859)
     radius_ptr = radius_src = radius_class = cell_order = None
     if cfg.cell_nodes:
@@ -360,8 +378,9 @@ def make_plan(model, b: Batch) -> Plan:
         run_window=run_window, run_class=run_class,
         inc_stone_ptr=ops.runs_to_ptr(run_stone.contiguous(), n_s),
         window_pos=window_pos, layout_offsets=offsets, layout_order=lorder,
-        covered_mask=covered, cell_ptr=cell_ptr, edge_window=edge_window, edge_class=edge_class,
-        win_ptr=win_ptr, edge_wcell=edge_cell[worder], edge_wclass=edge_class[worder],
+        covered_mask=covered, cov_rows=cov_rows, edge_wcell_cov=edge_wcell_cov, cell_ptr=cell_ptr,
+        edge_window=edge_window, edge_class=edge_class,
+        win_ptr=win_ptr, edge_wcell=edge_wcell, edge_wclass=edge_class[worder],
         cell_order=cell_order,
         # the heads walk the same decoder runs (cell_ptr has the batch's run
         # lengths in any entry order), so the stages' order serves them too
@@ -415,8 +434,12 @@ def _cell_stage(W, P, pb, plan: Plan, s, w, c):
     rad = _substage(W, P, pb, "rad", _proj(W, pb + "rad_kv", s), "radius_bias", W[pb + "rad_vcls"],
                     plan.radius_ptr, plan.radius_src, plan.radius_class)
     ops.attention_substages(c, [cr, rad], row_order=plan.cell_order)
-    wr = _substage(W, P, pb, "wr", _proj(W, pb + "wr_kv", c), "wr_bias", None, plan.win_ptr, plan.edge_wcell,
-                   plan.edge_wclass)
+    if plan.cov_rows is not None:  # k/v of the covered cells only, entries remapped to them
+        wr = _substage(W, P, pb, "wr", _proj(W, pb + "wr_kv", c, x_rows=plan.cov_rows), "wr_bias", None,
+                       plan.win_ptr, plan.edge_wcell_cov, plan.edge_wclass)
+    else:
+        wr = _substage(W, P, pb, "wr", _proj(W, pb + "wr_kv", c), "wr_bias", None, plan.win_ptr, plan.edge_wcell,
+                       plan.edge_wclass)
     ops.attention_substages(w, [wr])
 
 
