@@ -104,11 +104,13 @@ struct Smem {
   static int bytes(int n3) { return (w1 + w2 + (kStage2 ? kParts * n3 * p3 : 0)) * 2; }
 };
 
-// Wavefronts sharing one LDS copy of the weights: 8, or 16 for the widest
+// Wavefronts sharing one LDS copy of the weights: 8; 16 for the widest
 // projection, whose 139 KB of weights leave room for one workgroup per CU
-// (the extra wavefronts keep more rows in flight)
-template <int N1>
-constexpr int threads_for() { return N1 >= 512 ? 1024 : 512; }
+// (the extra wavefronts keep more rows in flight); 12 for the pair MLPs,
+// whose three 128-wide matrices (104 KB) also allow a single workgroup per
+// CU and whose registers allow three wavefronts per SIMD
+template <int N1, bool kX2 = false, bool kStage2 = false>
+constexpr int threads_for() { return N1 >= 512 ? 1024 : (kX2 && kStage2 && N1 == 128 ? 768 : 512); }
 
 // kPair (single stage, fp16 out): the W1 rows are staged permuted so that
 // feature tiles 2k and 2k+1 leave lane group g holding the eight consecutive
@@ -118,9 +120,9 @@ __device__ __forceinline__ int pair_feature(int nt, int g, int t) { return 32 * 
 
 template <typename TX, typename TX2, bool kLN, int N1, bool kX2, bool kRelu, bool kStage2, int kMode,
           bool kSplit = false, bool kPair = false>
-__global__ void __launch_bounds__(threads_for<N1>()) fused_linear_kernel(Args a) {
+__global__ void __launch_bounds__((threads_for<N1, kX2, kStage2>())) fused_linear_kernel(Args a) {
   static_assert(!kPair || (!kStage2 && !kX2 && kMode == kStoreF16 && N1 % 32 == 0), "paired stores: fp16 projections");
-  constexpr int kTileRows = 16 * (threads_for<N1>() / 64);
+  constexpr int kTileRows = 16 * (threads_for<N1, kX2, kStage2>() / 64);
   constexpr int kParts = kSplit ? 2 : 1;
   extern __shared__ __attribute__((aligned(16))) _Float16 smem[];
   using S = Smem<N1, kStage2, kX2, kSplit>;
@@ -362,11 +364,11 @@ int32_t launch(const Args& a, hipStream_t stream) {
       return MANTIS_E_LAUNCH;
     configured = true;
   }
-  constexpr int kTileRows = 16 * (threads_for<N1>() / 64);
+  constexpr int kTileRows = 16 * (threads_for<N1, kX2, kStage2>() / 64);
   const int64_t tiles = (a.m + kTileRows - 1) / kTileRows;
   const int per_cu = std::max(1, std::min(4, kMaxLds / std::max(bytes, 1)));
   const int64_t grid = std::min<int64_t>(tiles, int64_t(cu_count()) * per_cu);
-  kernel<<<unsigned(grid), threads_for<N1>(), bytes, stream>>>(a);
+  kernel<<<unsigned(grid), threads_for<N1, kX2, kStage2>(), bytes, stream>>>(a);
   return launched();
 }
 
