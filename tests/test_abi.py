@@ -55,3 +55,29 @@ def test_substage_struct_matches_header():
 def test_versions_answer_without_a_gpu():
     assert _native.encoder().hexo_repr_version() == 9
     assert _native.hip().mantis_hip_version() > 0
+
+
+def test_every_ops_call_passes_the_declared_argument_count():
+    # each `_lib().mantis_*(...)` call in the ops layer against the header's
+    # parameter list (ctypes would only notice a wrong count at run time)
+    src = (Path(__file__).resolve().parents[1] / "hexo-shrimp-bot_amd" / "mantisnet" / "ops.py").read_text()
+    decls = _declarations("mantis_hip.h")
+    seen = 0
+    for m in re.finditer(r"_lib\(\)\.(mantis_\w+)\(", src):
+        name, k, depth, n, last = m.group(1), m.end(), 1, 1, ""
+        while depth:
+            ch = src[k]
+            if ch in "([":
+                depth += 1
+            elif ch in ")]":
+                depth -= 1
+            elif ch == "," and depth == 1:
+                n += 1
+            if not ch.isspace() and depth:
+                last = ch
+            k += 1
+        if last == ",":
+            n -= 1
+        assert n == decls[name], (name, n, decls[name])
+        seen += 1
+    assert seen >= 20
