@@ -69,6 +69,17 @@ __global__ void hex_neighbours_kernel(const int32_t* __restrict__ qr,
 // Product: y^T (16 outs x 16 cells) = W (16 x 128) . sum^T (128 x 16), one
 // per output tile, serves both outputs by linearity:
 //   out_sum = y + b,   out_mean = y / count + b   (0 neighbours: b).
+// The D fragments (4 consecutive outputs of one cell per lane) go back
+// through the wavefront's LDS rows, so each output leaves as full 256-byte
+// rows, 16 bytes per lane, with non-temporal stores (written once, never
+// re-read by this kernel: they are kept from displacing the neighbour rows
+// in L2).  Scattered 8-byte stores of the fragments cost 40% more time.
+//
+// Blocks are dealt out XCD-contiguously (dispatch is round-robin over the 8
+// XCDs): the tiles one XCD runs are adjacent, so the neighbour rows they
+// share — the cells of the same and the adjacent hex columns — are fetched
+// into that XCD's L2 once.
+//
 // W is staged in LDS once per 4-wavefront workgroup; its loads are issued
 // before the neighbour indices so the two round trips overlap.  LDS rows are
 // padded to 272 bytes so the 16 rows of a fragment read fall in distinct
@@ -77,6 +88,12 @@ __global__ void hex_neighbours_kernel(const int32_t* __restrict__ qr,
 constexpr int kPitch = kDim + 8;  // bf16 per staged LDS row
 constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
+constexpr int kXcds = 8;
+
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void store16_nt(uint16_t* p, uint4 v) {
+  __builtin_nontemporal_store(u32x4_t{v.x, v.y, v.z, v.w}, reinterpret_cast<u32x4_t*>(p));
+}
 
 __global__ void __launch_bounds__(kThreads)
 hex_aggregate_linear_kernel(const uint16_t* __restrict__ x, const int32_t* __restrict__ nbr,
@@ -87,7 +104,11 @@ hex_aggregate_linear_kernel(const uint16_t* __restrict__ x, const int32_t* __res
   __shared__ __align__(16) uint16_t sagg[kWaves][16 * kPitch];
   __shared__ float scount[kWaves][16];
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
-  const int64_t c0 = (int64_t(blockIdx.x) * kWaves + wave) * 16;
+  // XCD-contiguous block order: the grid is a multiple of kXcds, and block
+  // b runs tile-block (b % kXcds) * (grid / kXcds) + b / kXcds (a bijection)
+  const int64_t per_xcd = int64_t(gridDim.x) / kXcds;
+  const int64_t blk = int64_t(blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
+  const int64_t c0 = (blk * kWaves + wave) * 16;
   // ---- W: requested first (4 x 16 bytes per thread), stored once it lands
   uint4 wst[kDim * kDim / 8 / kThreads];
 #pragma unroll
@@ -105,8 +126,8 @@ hex_aggregate_linear_kernel(const uint16_t* __restrict__ x, const int32_t* __res
     *reinterpret_cast<uint4*>(sw + r * kPitch + 8 * c) = wst[u];
   }
   // ---- gather in row layout: pass p covers cells c0 + 4p + lane/16
+  const int sub = lane / 16, d8 = (lane % 16) * 8;
   {
-    const int sub = lane / 16, d8 = (lane % 16) * 8;
     int32_t js[4][6];
 #pragma unroll
     for (int p = 0; p < 4; ++p)
@@ -158,33 +179,52 @@ hex_aggregate_linear_kernel(const uint16_t* __restrict__ x, const int32_t* __res
   if (c0 >= n_cells) return;
   // ---- product in MFMA layout: lane = cell l16, K group g
   const int l16 = lane % 16, g = lane / 16;
-  const int64_t cell = c0 + l16;
-  const bool live = cell < n_cells;
   const float cnt = scount[wave][l16];
   const float inv = cnt > 0.f ? 1.f / cnt : 0.f;
   bf16x8_t fs[4];
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks)
     fs[ks] = as_bf16x8(*reinterpret_cast<const uint4*>(&sagg[wave][l16 * kPitch + 32 * ks + 8 * g]));
+  f32x4_t d[8];
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) {
-    f32x4_t d = {0.f, 0.f, 0.f, 0.f};
+    d[nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       // A fragment: W[16nt + l16][32ks + 8g .. +8]
       const bf16x8_t wf = as_bf16x8(*reinterpret_cast<const uint4*>(sw + (16 * nt + l16) * kPitch + 32 * ks + 8 * g));
-      d = mfma16x16x32(wf, fs[ks], d);
+      d[nt] = mfma16x16x32(wf, fs[ks], d[nt]);
     }
-    if (live) {
+  }
+  // out_sum, then out_mean, through the wavefront's LDS rows (cell l16, outputs
+  // 16nt + 4g .. +3) and out as full rows (cell 4p + sub, dims d8 .. +7).  The
+  // wavefront is the only reader and writer of its rows, and LDS operations of
+  // one wavefront complete in order; the fences keep the compiler from moving
+  // the reads and writes across each other.
+#pragma unroll
+  for (int which = 0; which < 2; ++which) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    const float scale = which ? inv : 1.f;
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
       const int o = 16 * nt + 4 * g;
       const float4 b = *reinterpret_cast<const float4*>(bias + o);
-      uint2 ws, wm;
-      ws.x = pack_bf16x2(d[0] + b.x, d[1] + b.y);
-      ws.y = pack_bf16x2(d[2] + b.z, d[3] + b.w);
-      wm.x = pack_bf16x2(fmaf(d[0], inv, b.x), fmaf(d[1], inv, b.y));
-      wm.y = pack_bf16x2(fmaf(d[2], inv, b.z), fmaf(d[3], inv, b.w));
-      *reinterpret_cast<uint2*>(out_sum + cell * kDim + o) = ws;
-      *reinterpret_cast<uint2*>(out_mean + cell * kDim + o) = wm;
+      uint2 v;
+      v.x = pack_bf16x2(fmaf(d[nt][0], scale, b.x), fmaf(d[nt][1], scale, b.y));
+      v.y = pack_bf16x2(fmaf(d[nt][2], scale, b.z), fmaf(d[nt][3], scale, b.w));
+      *reinterpret_cast<uint2*>(&sagg[wave][l16 * kPitch + o]) = v;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    uint16_t* dst = which ? out_mean : out_sum;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const int64_t c = c0 + 4 * p + sub;
+      const uint4 v = *reinterpret_cast<const uint4*>(&sagg[wave][(4 * p + sub) * kPitch + d8]);
+      if (c < n_cells) store16_nt(dst + c * kDim + d8, v);
     }
   }
 }
@@ -212,7 +252,9 @@ int32_t mantis_hex_aggregate_linear(const void* x, const int32_t* nbr, int64_t n
   if (!x || !nbr || !w || !b || !out_sum || !out_mean || n_cells < 0) return MANTIS_E_ARG;
   if (!aligned16(x) || !aligned16(w) || !aligned16(b) || !aligned16(out_sum) || !aligned16(out_mean))
     return MANTIS_E_ARG;
-  const int64_t blocks = (n_cells + 16 * kWaves - 1) / (16 * kWaves);
+  // rounded up to a multiple of kXcds for the XCD-contiguous block order
+  const int64_t blocks = ((n_cells + 16 * kWaves - 1) / (16 * kWaves) + kXcds - 1) / kXcds * kXcds;
+  if (blocks > 2147483647LL) return MANTIS_E_ARG;
   hex_aggregate_linear_kernel<<<unsigned(blocks), kThreads, 0, as_stream(stream)>>>(
       static_cast<const uint16_t*>(x), nbr, n_cells, static_cast<const uint16_t*>(w), b,
       static_cast<uint16_t*>(out_sum), static_cast<uint16_t*>(out_mean), err_flag);

@@ -225,9 +225,11 @@ def test_hex_neighbours_bit_exact_vs_reference_adjacency(device):
         assert np.array_equal(nbr[gptr[j]:gptr[j + 1]].numpy(), exp)
 
 
-def test_hex_aggregate_linear_closed_form(device):
+@pytest.mark.parametrize("n", [1000, 37, 5003])
+def test_hex_aggregate_linear_closed_form(device, n):
+    # 37 cells: one partial tile and seven empty workgroups of the XCD-rounded
+    # grid; 5003: a ragged last tile in a grid of several XCD rounds
     gen = _g(11)
-    n = 1000
     nbr = torch.randint(-1, n, (n, 6), generator=gen, dtype=torch.int32)
     nbr[:7] = -1  # isolated cells: mean is zero by convention
     x = torch.randn(n, 128, generator=gen).to(BF)
