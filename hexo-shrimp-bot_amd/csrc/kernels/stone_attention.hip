@@ -1,8 +1,8 @@
 // Ragged block-diagonal attention on 16-bit MFMA (bf16 or fp16) for gfx950
 // (replaces the reference's Triton flash kernel, attention.py:44-162).
 //
-// Work split: one workgroup = one (position, head, 128-query tile); each of
-// its four wavefronts owns 32 queries (two 16-query sub-tiles).  The
+// Work split: one workgroup = one item (position, head, 128-query tile); each
+// of its four wavefronts owns 32 queries (two 16-query sub-tiles).  The
 // workgroup streams the position's live keys in 64-key chunks through LDS,
 // double-buffered: while a chunk is consumed the next one is already in
 // registers, and one barrier per chunk separates the buffers.  Per chunk,
@@ -14,14 +14,37 @@
 // stay in registers and the probabilities of a D fragment are the B fragment
 // of the next product (the two 16-key tiles of a 32-key step interleave as
 // K-slots {4g..4g+3, 16+4g..16+4g+3}; V^T is staged in LDS so its A
-// fragment reads the same order).  The online softmax tracks the raw-score
-// maximum and evaluates exp2(s*c - m*c) with c = log2(e)/sqrt(hd): one FMA
-// and one exp2 per score; the row sums come from one more product per
-// 32-key step with an all-ones A operand, so the normaliser sums exactly the
-// rounded probabilities the numerator uses.  Keys at or past seq_len are staged as zeros and
-// masked (only the last chunk can hold them); query rows past seq_len are
-// written as exact zeros.  LDS rows are padded (K 80 B, V^T 144 B) so the
-// 16 rows of a fragment read fall in distinct banks.
+// fragment reads the same order).  The row sums come from one more product
+// per 32-key step with an all-ones A operand, so the normaliser sums exactly
+// the rounded probabilities the numerator uses.  LDS rows are padded (K 80 B,
+// V^T 144 B) so the 16 rows of a fragment read fall in distinct banks.
+//
+// Softmax: p = exp2(s*c - m*c) with c = log2(e)/sqrt(hd), one FMA and one
+// exp2 per score.  The reference point m is raised lazily: only when a
+// chunk's scores exceed it by more than kLazyLog2 (in log2 units) anywhere
+// in the wavefront does the wavefront take the cross-lane maximum and rescale
+// its accumulators; otherwise probabilities up to 2^kLazyLog2 are
+// accumulated as they are (far inside the range of fp16 and bf16, and of the
+// fp32 sums).  The first chunk always sets m.  The final division by the row
+// sum makes the output independent of the reference point up to rounding.
+// Only the last chunk can hold keys at or past seq_len: it alone is masked
+// (a separately compiled copy of the chunk body).  Every global load reads a
+// clamped, in-range row and zeroes the value afterwards: a load under a
+// condition compiles to a flat load, whose completion every LDS wait would
+// then also wait for.  Query rows past seq_len are written as exact zeros.
+//
+// Schedule: items differ in cost by their position's key count (1 to
+// ceil(T/64) chunks), and workgroups are dispatched round-robin over the 8
+// XCDs.  stone_schedule_kernel orders the items by key-chunk count, longest
+// first (items past a position's live prefix, which only write zeros, last),
+// so consecutive workgroups, one per XCD, carry like work and the long items
+// do not trail at the end.  The order within a bucket comes from LDS atomics
+// and varies between runs; every item is computed independently, so the
+// output does not depend on it.  The order depends on seq_lens only, so one
+// schedule serves every attention call over the same lengths.  Without one
+// the items run XCD-contiguously in (position, head, tile) order.
+#include <type_traits>
+
 #include "common.hpp"
 #include "mfma.hpp"
 
@@ -35,6 +58,59 @@ constexpr int kQTile = kWaves * kQPerWave;  // 128
 constexpr int kKChunk = 64;
 constexpr int kKPitch = kHd + 8;        // 16-bit elements per staged K row
 constexpr int kVtPitch = kKChunk + 8;   // 16-bit elements per staged V^T row
+constexpr float kLazyLog2 = 8.f;        // lazy-rescale threshold (probabilities <= 2^8)
+constexpr int kXcds = 8;
+constexpr int kSchedThreads = 1024;
+constexpr int kMaxChunkBuckets = 1024;  // T <= 64 * 1023 when scheduled
+
+// One workgroup: order[i] = item (p * heads + a) * n_qt + qt, live items by
+// key-chunk count descending, then the items past each live prefix.
+__global__ void __launch_bounds__(kSchedThreads)
+stone_schedule_kernel(const int32_t* __restrict__ seq_lens, int64_t n_pos, int heads, int64_t T,
+                      int64_t n_qt, int n_kc, int32_t* __restrict__ order) {
+  __shared__ int64_t cursor[kMaxChunkBuckets + 1];  // items per bucket, then the bucket's next slot
+  __shared__ int64_t dead_cursor;
+  for (int i = threadIdx.x; i <= n_kc; i += kSchedThreads) cursor[i] = 0;
+  __syncthreads();
+  auto span = [&](int64_t p, int64_t& live_qt, int& nk) {
+    int64_t L = seq_lens[p];
+    L = L < 0 ? 0 : (L > T ? T : L);
+    nk = int((L + kKChunk - 1) / kKChunk);
+    live_qt = (L + kQTile - 1) / kQTile;
+  };
+  for (int64_t p = threadIdx.x; p < n_pos; p += kSchedThreads) {
+    int64_t live_qt;
+    int nk;
+    span(p, live_qt, nk);
+    atomicAdd(reinterpret_cast<unsigned long long*>(&cursor[nk]), static_cast<unsigned long long>(heads * live_qt));
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {  // exclusive scan over buckets, most chunks first (n_kc + 1 <= 1024 entries)
+    int64_t run = 0;
+    for (int b = n_kc; b >= 0; --b) {
+      const int64_t c = cursor[b];
+      cursor[b] = run;
+      run += c;
+    }
+    dead_cursor = run;
+  }
+  __syncthreads();
+  for (int64_t p = threadIdx.x; p < n_pos; p += kSchedThreads) {
+    int64_t live_qt;
+    int nk;
+    span(p, live_qt, nk);
+    const int64_t s = int64_t(atomicAdd(reinterpret_cast<unsigned long long*>(&cursor[nk]),
+                                        static_cast<unsigned long long>(heads * live_qt)));
+    const int64_t d = int64_t(atomicAdd(reinterpret_cast<unsigned long long*>(&dead_cursor),
+                                        static_cast<unsigned long long>(heads * (n_qt - live_qt))));
+    for (int64_t a = 0; a < heads; ++a) {
+      const int64_t base = (p * heads + a) * n_qt;
+      for (int64_t qt = 0; qt < live_qt; ++qt) order[s + a * live_qt + qt] = int32_t(base + qt);
+      for (int64_t qt = live_qt; qt < n_qt; ++qt)
+        order[d + a * (n_qt - live_qt) + (qt - live_qt)] = int32_t(base + qt);
+    }
+  }
+}
 
 template <bool kHalf>
 __global__ void __launch_bounds__(256)
@@ -43,14 +119,26 @@ stone_attention_kernel(const uint16_t* __restrict__ q, int64_t qsp, int64_t qsa,
                        const uint16_t* __restrict__ v, int64_t vsp, int64_t vsa, int64_t vst,
                        const int32_t* __restrict__ seq_lens, int heads, int64_t T,
                        uint16_t* __restrict__ out, int64_t osp, int64_t osa, int64_t ost,
-                       float* __restrict__ lse, float c_log2) {
+                       float* __restrict__ lse, float c_log2, int64_t n_items,
+                       const int32_t* __restrict__ schedule) {
   __shared__ __attribute__((aligned(16))) uint16_t sk[2][kKChunk * kKPitch];
   __shared__ __attribute__((aligned(16))) uint16_t svt[2][kHd * kVtPitch];
-  const int64_t pa = blockIdx.y;
+  // item of this workgroup: from the schedule, or XCD-contiguous (the grid is
+  // a multiple of kXcds; block b runs item (b % kXcds) * (grid / kXcds) + b / kXcds)
+  int64_t item;
+  if (schedule) {
+    item = blockIdx.x < n_items ? int64_t(schedule[blockIdx.x]) : n_items;
+  } else {
+    const int64_t per = int64_t(gridDim.x) / kXcds;
+    item = int64_t(blockIdx.x % kXcds) * per + blockIdx.x / kXcds;
+  }
+  if (item < 0 || item >= n_items) return;
+  const int64_t n_qt = (T + kQTile - 1) / kQTile;
+  const int64_t pa = item / n_qt, qt = item % n_qt;
   const int64_t p = pa / heads, a = pa % heads;
   int64_t L = seq_lens[p];
   L = L < 0 ? 0 : (L > T ? T : L);
-  const int64_t q0 = int64_t(blockIdx.x) * kQTile;
+  const int64_t q0 = qt * kQTile;
   const uint16_t* qp = q + p * qsp + a * qsa;
   const uint16_t* kp = k + p * ksp + a * ksa;
   const uint16_t* vp = v + p * vsp + a * vsa;
@@ -73,13 +161,16 @@ stone_attention_kernel(const uint16_t* __restrict__ q, int64_t qsp, int64_t qsa,
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
   const int l16 = lane % 16, g = lane / 16;
   using FR = Frag<kHalf>;
+  const int64_t last = L - 1;  // L >= 1 here: clamp target of out-of-range rows
   typename FR::vec qf[2];
   int64_t qrow[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     qrow[j] = q0 + wave * kQPerWave + 16 * j + l16;
     // B fragment of Q^T: query l16, dims 8g..8g+7
-    qf[j] = FR::cast(qrow[j] < L ? *reinterpret_cast<const uint4*>(qp + qrow[j] * qst + 8 * g) : zero4);
+    const bool live = qrow[j] < L;
+    const uint4 raw = *reinterpret_cast<const uint4*>(qp + (live ? qrow[j] : last) * qst + 8 * g);
+    qf[j] = FR::cast(live ? raw : zero4);
   }
 
   // staging role of this thread: one 16-byte piece of one key's K and V rows
@@ -87,8 +178,12 @@ stone_attention_kernel(const uint16_t* __restrict__ q, int64_t qsp, int64_t qsa,
   uint4 kreg, vreg;
   auto fetch = [&](int64_t kb) {
     const int64_t kk = kb + st_key;
-    kreg = kk < L ? *reinterpret_cast<const uint4*>(kp + kk * kst + st_d) : zero4;
-    vreg = kk < L ? *reinterpret_cast<const uint4*>(vp + kk * vst + st_d) : zero4;
+    const bool live = kk < L;
+    const int64_t row = live ? kk : last;
+    const uint4 kr = *reinterpret_cast<const uint4*>(kp + row * kst + st_d);
+    const uint4 vr = *reinterpret_cast<const uint4*>(vp + row * vst + st_d);
+    kreg = live ? kr : zero4;
+    vreg = live ? vr : zero4;
   };
   auto stage = [&](int buf) {
     *reinterpret_cast<uint4*>(&sk[buf][st_key * kKPitch + st_d]) = kreg;
@@ -101,9 +196,9 @@ stone_attention_kernel(const uint16_t* __restrict__ q, int64_t qsp, int64_t qsa,
     }
   };
 
-  // per sub-tile: running raw-score maximum, O^T accumulators (two 16-dim
-  // tiles) and the row sums, accumulated by an extra product with an
-  // all-ones A operand (every D row holds the sum of the probabilities)
+  // per sub-tile: the reference point of the exponent (raw-score units), O^T
+  // accumulators (two 16-dim tiles) and the row sums, accumulated by an extra
+  // product with an all-ones A operand (every D row holds the sum)
   float m[2] = {-INFINITY, -INFINITY};
   f32x4_t o[2][2], lsum[2];
 #pragma unroll
@@ -115,16 +210,8 @@ stone_attention_kernel(const uint16_t* __restrict__ q, int64_t qsp, int64_t qsa,
   const uint32_t one2 = FR::pack_unit(1.f, 1.f);
   const typename FR::vec ones = FR::cast(make_uint4(one2, one2, one2, one2));
 
-  const int64_t n_chunks = (L + kKChunk - 1) / kKChunk;
-  fetch(0);
-  stage(0);
-  __syncthreads();
-  for (int64_t ch = 0; ch < n_chunks; ++ch) {
-    const int buf = int(ch & 1);
-    const int64_t kb = ch * kKChunk;
-    const bool more = ch + 1 < n_chunks;
+  auto chunk = [&](auto masked, int buf, int64_t kb, bool more) {
     if (more) fetch(kb + kKChunk);
-
     // S^T tiles: keys kb + 16*tt + (4g + t) for query l16 of sub-tile j
     f32x4_t s[2][4];
 #pragma unroll
@@ -133,8 +220,8 @@ stone_attention_kernel(const uint16_t* __restrict__ q, int64_t qsp, int64_t qsa,
 #pragma unroll
       for (int j = 0; j < 2; ++j) s[j][tt] = mfma16x16x32(kf, qf[j], f32x4_t{0.f, 0.f, 0.f, 0.f});
     }
-    const int lim = int(L - kb);  // keys at or past lim are padding
-    if (lim < kKChunk) {           // only the last chunk can hold them
+    if constexpr (decltype(masked)::value) {  // keys at or past lim are padding
+      const int lim = int(L - kb);
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
@@ -147,18 +234,29 @@ stone_attention_kernel(const uint16_t* __restrict__ q, int64_t qsp, int64_t qsa,
     typename FR::vec pf[2][2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      float cmax = m[j];
+      float lmax = s[j][0][0];
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) cmax = fmaxf(cmax, s[j][tt][t]);
-      cmax = fmaxf(cmax, __shfl_xor(cmax, 16));
-      cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
-      // exp2 arguments are <= 0 (or -inf): the raw v_exp_f32 is exact enough
-      // and flushes results below 2^-126 to zero
-      const float alpha = __builtin_amdgcn_exp2f((m[j] - cmax) * c_log2);
-      const float mc = cmax * c_log2;
-      m[j] = cmax;
+        for (int t = 0; t < 4; ++t) lmax = fmaxf(lmax, s[j][tt][t]);
+      // (-inf - -inf is NaN and compares false: a lane that has seen only
+      // padding never asks for a new reference point by itself)
+      if (__builtin_amdgcn_ballot_w64((lmax - m[j]) * c_log2 > kLazyLog2)) {  // wavefront-uniform
+        float cmax = fmaxf(m[j], lmax);
+        cmax = fmaxf(cmax, __shfl_xor(cmax, 16));
+        cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
+        // exp2 arguments are <= 0 (or -inf): the raw v_exp_f32 is exact enough
+        // and flushes results below 2^-126 to zero
+        const float alpha = cmax == -INFINITY ? 1.f : __builtin_amdgcn_exp2f((m[j] - cmax) * c_log2);
+        m[j] = cmax;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          lsum[j][t] *= alpha;
+          o[j][0][t] *= alpha;
+          o[j][1][t] *= alpha;
+        }
+      }
+      const float mc = m[j] * c_log2;
       uint32_t pw[4][2];
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt) {
@@ -167,12 +265,6 @@ stone_attention_kernel(const uint16_t* __restrict__ q, int64_t qsp, int64_t qsa,
         for (int t = 0; t < 4; ++t) pr[t] = __builtin_amdgcn_exp2f(fmaf(s[j][tt][t], c_log2, -mc));
         pw[tt][0] = FR::pack_unit(pr[0], pr[1]);
         pw[tt][1] = FR::pack_unit(pr[2], pr[3]);
-      }
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        lsum[j][t] *= alpha;
-        o[j][0][t] *= alpha;
-        o[j][1][t] *= alpha;
       }
 #pragma unroll
       for (int sc = 0; sc < 2; ++sc)
@@ -195,6 +287,18 @@ stone_attention_kernel(const uint16_t* __restrict__ q, int64_t qsp, int64_t qsa,
     }
     if (more) stage(buf ^ 1);
     __syncthreads();
+  };
+
+  const int64_t n_chunks = (L + kKChunk - 1) / kKChunk;
+  fetch(0);
+  stage(0);
+  __syncthreads();
+  for (int64_t ch = 0; ch + 1 < n_chunks; ++ch)
+    chunk(std::false_type{}, int(ch & 1), ch * kKChunk, true);
+  {
+    const int64_t ch = n_chunks - 1;  // only the last chunk can hold padding keys
+    if (L - ch * kKChunk < kKChunk) chunk(std::true_type{}, int(ch & 1), ch * kKChunk, false);
+    else chunk(std::false_type{}, int(ch & 1), ch * kKChunk, false);
   }
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
@@ -219,11 +323,28 @@ stone_attention_kernel(const uint16_t* __restrict__ q, int64_t qsp, int64_t qsa,
 
 using namespace mantis;
 
+extern "C" int64_t mantis_stone_attention_schedule_len(int64_t n_pos, int32_t heads, int64_t t) {
+  if (n_pos <= 0 || heads <= 0 || t <= 0 || (t + kKChunk - 1) / kKChunk >= kMaxChunkBuckets) return 0;
+  return n_pos * heads * ((t + kQTile - 1) / kQTile);
+}
+
+extern "C" int32_t mantis_stone_attention_schedule(const int32_t* seq_lens, int64_t n_pos, int32_t heads,
+                                                   int64_t t, int32_t* schedule, void* stream) {
+  const int64_t n = mantis_stone_attention_schedule_len(n_pos, heads, t);
+  if (n_pos == 0 || t == 0) return MANTIS_OK;
+  if (!seq_lens || !schedule || n <= 0 || n > 2147483647LL) return MANTIS_E_ARG;
+  const int64_t n_qt = (t + kQTile - 1) / kQTile, n_kc = (t + kKChunk - 1) / kKChunk;
+  stone_schedule_kernel<<<1, kSchedThreads, 0, as_stream(stream)>>>(seq_lens, n_pos, heads, t, n_qt, int(n_kc),
+                                                                   schedule);
+  return launched();
+}
+
 extern "C" int32_t mantis_stone_attention(const void* q, const int64_t* qs, const void* k,
                                           const int64_t* ks, const void* v, const int64_t* vs,
                                           int32_t dtype, const int32_t* seq_lens, int64_t n_pos,
                                           int32_t heads, int64_t t, int32_t hd, void* out,
-                                          const int64_t* os, float* lse, void* stream) {
+                                          const int64_t* os, float* lse, const int32_t* schedule,
+                                          void* stream) {
   if (n_pos == 0 || t == 0) return MANTIS_OK;
   if (!q || !k || !v || !out || !seq_lens || !qs || !ks || !vs || !os) return MANTIS_E_ARG;
   if (hd != kHd || heads <= 0 || n_pos < 0 || t < 0) return MANTIS_E_ARG;
@@ -234,13 +355,16 @@ extern "C" int32_t mantis_stone_attention(const void* q, const int64_t* qs, cons
     if ((st[0] | st[1] | st[2]) % 8) return MANTIS_E_ARG;
   }
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out)) return MANTIS_E_ARG;
-  if (n_pos * heads > 2147483647LL) return MANTIS_E_ARG;
+  const int64_t n_qt = (t + kQTile - 1) / kQTile;
+  const int64_t n_items = n_pos * heads * n_qt;
+  const int64_t grid = (n_items + kXcds - 1) / kXcds * kXcds;
+  if (grid > 2147483647LL) return MANTIS_E_ARG;
+  hipStream_t st = as_stream(stream);
   const float c_log2 = 1.4426950408889634f / sqrtf(float(hd));
-  const dim3 grid(unsigned((t + kQTile - 1) / kQTile), unsigned(n_pos * heads));
   auto kernel = dtype == MANTIS_F16 ? stone_attention_kernel<true> : stone_attention_kernel<false>;
-  kernel<<<grid, 256, 0, as_stream(stream)>>>(
+  kernel<<<unsigned(grid), 256, 0, st>>>(
       static_cast<const uint16_t*>(q), qs[0], qs[1], qs[2], static_cast<const uint16_t*>(k), ks[0],
       ks[1], ks[2], static_cast<const uint16_t*>(v), vs[0], vs[1], vs[2], seq_lens, heads, t,
-      static_cast<uint16_t*>(out), os[0], os[1], os[2], lse, c_log2);
+      static_cast<uint16_t*>(out), os[0], os[1], os[2], lse, c_log2, n_items, schedule);
   return launched();
 }

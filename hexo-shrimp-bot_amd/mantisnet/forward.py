@@ -269,6 +269,7 @@ class Plan:
     radius_src: Tensor | None
     radius_class: Tensor | None
     seq_lens: Tensor
+    stone_schedule: Tensor | None  # longest-first work order of the stone attention (None: one tile each)
     attn_src: Tensor  # padded attention slot -> row of [s; g] (or -1)
     attn_back: Tensor  # row of [s; g] -> padded attention slot
     dec_cell_ptr: Tensor  # CSR of the batch's own decoder order
@@ -372,6 +373,7 @@ def make_plan(model, b: Batch) -> Plan:
     attn_src[b.stone_slot] = torch.arange(n_s, device=dev)
     attn_src[gslot] = n_s + torch.arange(p * GLOBAL_ROWS, device=dev)
     attn_back = torch.cat([b.stone_slot, gslot])
+    seq_lens = b.attn_valid.sum(dim=1, dtype=torch.int32)
     return Plan(
         n_pos=p, max_t=max_t, max_w=max_w, n_s=n_s, n_w=n_w, n_c=n_c,
         inc_win_ptr=ops.runs_to_ptr(b.inc_window, n_w),
@@ -386,7 +388,8 @@ def make_plan(model, b: Batch) -> Plan:
         # lengths in any entry order), so the stages' order serves them too
         head_order=cell_order if cell_order is not None else ops.segment_order(b.legal_offsets, cell_ptr, None, n_c),
         radius_ptr=radius_ptr, radius_src=radius_src, radius_class=radius_class,
-        seq_lens=b.attn_valid.sum(dim=1, dtype=torch.int32), attn_src=attn_src, attn_back=attn_back,
+        seq_lens=seq_lens, stone_schedule=ops.stone_attention_schedule(seq_lens, cfg.heads, max_t),
+        attn_src=attn_src, attn_back=attn_back,
         dec_cell_ptr=cell_ptr if canonical else ops.runs_to_ptr(b.dec_cell, n_c),
     )
 
@@ -507,7 +510,8 @@ def _block(W, P, i: int, plan: Plan, b: Batch, sg, w, c, sw_all, update_stones: 
 
     if update_stones:
         rows = torch.empty((p, max_t, 4, 32), dtype=HALF, device=w.device)
-        ops.stone_attention(view(0), view(1), view(2), plan.seq_lens, out=rows.transpose(1, 2))
+        ops.stone_attention(view(0), view(1), view(2), plan.seq_lens, out=rows.transpose(1, 2),
+                            schedule=plan.stone_schedule)
         _resid(W, pb + "attn_o", rows.view(p * max_t, 128), sg, x_rows=plan.attn_back)
     else:
         # last block: only the four latent rows are read downstream (fp32 read)

@@ -994,8 +994,27 @@ def _strides(t: Tensor):
     return (ctypes.c_int64 * 4)(*t.stride())
 
 
+def stone_attention_schedule(seq_lens: Tensor, heads: int, t: int) -> Tensor | None:
+    """The longest-first work order of stone_attention over these lengths
+    (int32 on the device), or None when every position fits one 128-query
+    tile (then there is little to balance) or t is too long to schedule."""
+    dev = _on_gpu(seq_lens)
+    if seq_lens.ndim != 1 or seq_lens.dtype != torch.int32:
+        raise ValueError("seq_lens must be int32 with shape (P,)")
+    p = seq_lens.shape[0]
+    n = _lib().mantis_stone_attention_schedule_len(p, heads, t) if t > 128 else 0
+    if not n:
+        return None
+    schedule = torch.empty(n, dtype=torch.int32, device=dev)
+    seq_lens = seq_lens.contiguous()
+    _launch("stone_attention_schedule", float(p * 4 + n * 4), 0.0, lambda: _check(
+        _lib().mantis_stone_attention_schedule(_ptr(seq_lens), p, heads, t, _ptr(schedule), _stream()),
+        "stone_attention_schedule"))
+    return schedule
+
+
 def stone_attention(q: Tensor, k: Tensor, v: Tensor, seq_lens: Tensor, want_lse: bool = False,
-                    out: Tensor | None = None):
+                    out: Tensor | None = None, schedule: Tensor | None | bool = True):
     """Ragged attention over each position's live prefix (16-bit MFMA).
     q/k/v (P, A, T, hd) fp16 or bf16 with arbitrary row strides; the output
     has ``empty_like(q)`` strides."""
@@ -1026,10 +1045,20 @@ def stone_attention(q: Tensor, k: Tensor, v: Tensor, seq_lens: Tensor, want_lse:
         # packed live rows of q, k, v, out; 4 L^2 hd flops per head
         nbytes = float(lens.sum()) * heads * hd * q.element_size() * 4
         flops = float((lens.double() ** 2).sum()) * 4 * heads * hd
+    # schedule: True builds the longest-first order here (one small pre-pass),
+    # a tensor from stone_attention_schedule(seq_lens, heads, t) reuses one,
+    # None or False runs the items in natural order
+    if schedule is True:
+        schedule = stone_attention_schedule(seq_lens, heads, t)
+    elif schedule is False:
+        schedule = None
+    elif schedule is not None and (schedule.dtype != torch.int32 or schedule.device != dev or
+                                   schedule.numel() != _lib().mantis_stone_attention_schedule_len(p, heads, t)):
+        raise ValueError("schedule must come from stone_attention_schedule(seq_lens, heads, t)")
     _launch("stone_attention", nbytes, flops, lambda: _check(
         _lib().mantis_stone_attention(
             _ptr(q), qs, _ptr(k), ks, _ptr(v), vs, _dt(q), _ptr(seq_lens), p, heads, t, hd, _ptr(out), os_,
-            _ptr(lse), _stream(),
+            _ptr(lse), _ptr(schedule), _stream(),
         ),
         "stone_attention",
     ))

@@ -399,14 +399,37 @@ int32_t mantis_row_encode(const void* pre, int32_t pre_dtype, int64_t n_w, int64
  * (lse 0).  q/k/v/out share `dtype`, with element strides (sp, sa, st, sd == 1)
  * given per tensor, so the (P, T, A, hd) -> (P, A, T, hd) transposed views
  * the model passes need no copy.  lse (P, heads, T) fp32 or NULL.
- * hd must be 32.  Replaces mantisnet::fused_attention
- * (python/mantisnet/mantisnet/attention.py:44-162, 719-753).
+ * hd must be 32.  `schedule` is NULL (work items in their natural order) or
+ * the order built by mantis_stone_attention_schedule for the same seq_lens,
+ * n_pos, heads and t; the output does not depend on which.  Replaces
+ * mantisnet::fused_attention (python/mantisnet/mantisnet/attention.py:44-162,
+ * 719-753).
  */
 int32_t mantis_stone_attention(const void* q, const int64_t* q_strides, const void* k,
                                const int64_t* k_strides, const void* v, const int64_t* v_strides,
                                int32_t dtype, const int32_t* seq_lens, int64_t n_pos,
                                int32_t heads, int64_t t, int32_t hd, void* out,
-                               const int64_t* out_strides, float* lse, void* stream);
+                               const int64_t* out_strides, float* lse, const int32_t* schedule,
+                               void* stream);
+
+/*
+ * Work order for mantis_stone_attention over these seq_lens: its items
+ * (position, head, 128-query tile) by key-chunk count descending, tiles past
+ * each live prefix last, written to `schedule` (a device array of
+ * mantis_stone_attention_schedule_len(n_pos, heads, t) int32) by one
+ * workgroup on `stream`.  Valid for every attention call over the same
+ * lengths.  Part of the MI355X launch plumbing of mantisnet::fused_attention
+ * (attention.py:719-753 launches its grid in natural order).
+ */
+int32_t mantis_stone_attention_schedule(const int32_t* seq_lens, int64_t n_pos, int32_t heads,
+                                        int64_t t, int32_t* schedule, void* stream);
+
+/*
+ * Entries of a mantis_stone_attention schedule (n_pos * heads * ceil(t / 128)),
+ * or 0 when t is too long to be scheduled (t >= 64 * 1023: pass NULL to the
+ * attention).  Host-side arithmetic only.
+ */
+int64_t mantis_stone_attention_schedule_len(int64_t n_pos, int32_t heads, int64_t t);
 
 /*
  * Fused row GEMM over rows of K = 128 features (LayerNorm -> Linear ->

@@ -190,6 +190,69 @@ def test_stone_attention_pad_keys_get_zero_weight(device):
     assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, BF])
+def test_stone_attention_late_rescale_and_empty_position(device, dtype):
+    # keys of the third 64-key chunk score far above the first chunk (scores
+    # x 12 there: log2-domain jumps well past the lazy-rescale threshold), so
+    # the reference point must be raised after probabilities were accumulated;
+    # position 1 has no live rows at all
+    gen = _g(21)
+    p, t, heads = 3, 300, 4
+    q = torch.randn(p, t, heads, 32, generator=gen).to(dtype).transpose(1, 2)
+    k = torch.randn(p, t, heads, 32, generator=gen)
+    k[:, 128:192] *= 12.0
+    k = k.to(dtype).transpose(1, 2)
+    v = torch.randn(p, t, heads, 32, generator=gen).to(dtype).transpose(1, 2)
+    seq = torch.tensor([300, 0, 190], dtype=torch.int32)
+    out, lse = ops.stone_attention(q.to(device), k.to(device), v.to(device), seq.to(device), want_lse=True)
+    exp = R.stone_attention(q.float(), k.float(), v.float(), seq)
+    tol = 4e-3 if dtype == torch.float16 else 2e-2
+    torch.testing.assert_close(out.float().cpu(), exp, rtol=tol, atol=tol)
+    assert torch.all(out[1].cpu() == 0) and torch.all(lse[1].cpu() == 0)
+    valid = torch.arange(t)[None, :] < seq[:, None]
+    sc = torch.matmul(q.float(), k.float().transpose(-1, -2)) / math.sqrt(32)
+    sc = sc.masked_fill(~valid[:, None, None, :], -torch.inf)
+    exp_lse = torch.logsumexp(sc, -1).masked_fill(~valid[:, None, :], 0.0)
+    torch.testing.assert_close(lse.cpu(), exp_lse, rtol=1e-3, atol=1e-3)
+
+
+def test_stone_attention_schedule_does_not_change_the_output(device):
+    # the longest-first schedule only reorders independent work items: the
+    # scheduled launch equals the unscheduled one bit for bit (C ABI direct)
+    gen = _g(22)
+    p, t, heads = 40, 384, 8
+    q, k, v = (torch.randn(p, t, heads, 32, generator=gen).to(BF).to(device).transpose(1, 2) for _ in range(3))
+    seq = torch.randint(1, t + 1, (p,), generator=gen, dtype=torch.int32).to(device)
+    lib = ops._lib()
+    n = lib.mantis_stone_attention_schedule_len(p, heads, t)
+    assert n == p * heads * 3
+    built = torch.full((n,), -7, dtype=torch.int32, device=device)
+    assert lib.mantis_stone_attention_schedule(seq.data_ptr(), p, heads, t, built.data_ptr(), ops._stream()) == 0
+    outs = []
+    for sched in (None, built):
+        out = torch.empty_like(q)
+        lse = torch.empty((p, heads, t), dtype=torch.float32, device=device)
+        rc = lib.mantis_stone_attention(q.data_ptr(), ops._strides(q), k.data_ptr(), ops._strides(k), v.data_ptr(),
+                                        ops._strides(v), ops._dt(q), seq.data_ptr(), p, heads, t, 32, out.data_ptr(),
+                                        ops._strides(out), lse.data_ptr(), None if sched is None else sched.data_ptr(),
+                                        ops._stream())
+        assert rc == 0
+        torch.cuda.synchronize()
+        outs.append((out.cpu(), lse.cpu(), None if sched is None else sched.cpu()))
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+    order = outs[1][2]
+    assert torch.equal(order.sort().values, torch.arange(n, dtype=torch.int32))  # a permutation of the items
+    # live items (tile start < seq_len) come first, by key-chunk count descending
+    item_pos = order.long() // (heads * 3)
+    item_tile = order.long() % 3
+    lens = seq.cpu().long()[item_pos]
+    live = item_tile * 128 < lens
+    n_live = int(live.sum())
+    assert bool(live[:n_live].all()) and not bool(live[n_live:].any())
+    chunks = (lens[:n_live] + 63) // 64
+    assert bool((chunks[1:] <= chunks[:-1]).all())
+
+
 def _hex_graphs(n_graphs, seed=0):
     from mantisnet import builder as B
     from mantisnet import synthetic as S
