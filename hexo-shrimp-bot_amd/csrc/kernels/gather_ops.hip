@@ -517,6 +517,40 @@ inline bool lds_ok(int64_t a, int64_t b, int64_t c) {
 
 // Calls fn(T{}) with T the element type named by a MANTIS_* dtype code;
 // returns false for an unknown code.
+// Row gather for 128-wide rows (the initial window and cell states):
+//   out[i, :] = table[r(i), :],  r(i) = cover_row when cover_ptr[i + 1] > cover_ptr[i]
+//                                        (cover_ptr given), else idx[i]
+// One thread per 16-byte chunk of an output row, so a row is 16 (fp16) or 32
+// (fp32) adjacent lanes reading one table row and writing 256 or 512
+// contiguous bytes with non-temporal stores (written once, read by a later
+// kernel).  An index outside [0, n_table) writes a zero row and flags
+// MANTIS_FLAG_INDEX.
+template <typename T>
+__global__ void __launch_bounds__(256)
+gather_rows_kernel(const T* __restrict__ table, int64_t ld_table, int64_t n_table, const int64_t* __restrict__ idx,
+                   const int64_t* __restrict__ cover_ptr, int64_t cover_row, int64_t n, T* __restrict__ out,
+                   int64_t ld_out, int32_t* flag) {
+  constexpr int kChunks = 128 * int(sizeof(T)) / 16;
+  constexpr int kPer = 16 / int(sizeof(T));
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  const int64_t total = n * kChunks;
+  for (int64_t t = int64_t(blockIdx.x) * 256 + threadIdx.x; t < total; t += int64_t(gridDim.x) * 256) {
+    const int64_t i = t / kChunks;
+    const int c = int(t % kChunks);
+    int64_t r;
+    if (cover_ptr && cover_ptr[i + 1] > cover_ptr[i]) {
+      r = cover_row;
+    } else {
+      r = idx[i];
+    }
+    const bool ok = r >= 0 && r < n_table;
+    if (!ok && c == 0) raise_flag(flag, MANTIS_FLAG_INDEX);
+    const uint4 v = *reinterpret_cast<const uint4*>(table + (ok ? r : 0) * ld_table + kPer * c);
+    const u32x4 w = ok ? u32x4{v.x, v.y, v.z, v.w} : u32x4{0u, 0u, 0u, 0u};
+    __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(out + i * ld_out + kPer * c));
+  }
+}
+
 template <typename F>
 bool with_type(int32_t dtype, F&& fn) {
   switch (dtype) {
@@ -535,6 +569,33 @@ using namespace mantis;
 extern "C" {
 
 int32_t mantis_hip_version(void) { return 1; }
+
+int32_t mantis_gather_rows(const void* table, int32_t dtype, int64_t ld_table, int64_t n_table, const int64_t* idx,
+                           const int64_t* cover_ptr, int64_t cover_row, int64_t n, void* out, int64_t ld_out,
+                           int32_t* err_flag, void* stream) {
+  if (n == 0) return MANTIS_OK;
+  if (!table || !idx || !out || n < 0 || n_table <= 0) return MANTIS_E_ARG;
+  if (!aligned16(table) || !aligned16(out)) return MANTIS_E_ARG;
+  const int64_t esize = dtype == MANTIS_F32 ? 4 : 2;
+  if ((ld_table * esize) % 16 || (ld_out * esize) % 16 || ld_table < 128 || ld_out < 128) return MANTIS_E_ARG;
+  if (cover_ptr && (cover_row < 0 || cover_row >= n_table)) return MANTIS_E_ARG;
+  const int64_t chunks = n * (128 * esize / 16);
+  int64_t grid = (chunks + 255) / 256;
+  if (grid > 65536) grid = 65536;
+  bool ok = true;
+  if (dtype == MANTIS_F32) {
+    gather_rows_kernel<float><<<unsigned(grid), 256, 0, as_stream(stream)>>>(
+        static_cast<const float*>(table), ld_table, n_table, idx, cover_ptr, cover_row, n, static_cast<float*>(out),
+        ld_out, err_flag);
+  } else if (dtype == MANTIS_F16 || dtype == MANTIS_BF16) {
+    gather_rows_kernel<uint16_t><<<unsigned(grid), 256, 0, as_stream(stream)>>>(
+        static_cast<const uint16_t*>(table), ld_table, n_table, idx, cover_ptr, cover_row, n,
+        static_cast<uint16_t*>(out), ld_out, err_flag);
+  } else {
+    ok = false;
+  }
+  return ok ? launched() : MANTIS_E_ARG;
+}
 
 int32_t mantis_runs_to_ptr(const int64_t* dest, int64_t n_entries, int64_t n_dest, int64_t* ptr,
                            int32_t* err_flag, void* stream) {

@@ -24,6 +24,7 @@ class MantisSubstage(ctypes.Structure):
 
 SIGNATURES = {
     "mantis_hip_version": ([], i32),
+    "mantis_gather_rows": ([vp, i32, i64, i64, vp, vp, i64, i64, vp, i64, vp, vp], i32),
     "mantis_runs_to_ptr": ([vp, i64, i64, vp, vp, vp], i32),
     "mantis_segment_order": ([vp, i64, vp, vp, i64, vp, vp, vp], i32),
     "mantis_run_reduce": ([vp, i32, i64, i64, i64, vp, i64, vp, i64, vp, i32, vp, vp], i32),

@@ -555,16 +555,17 @@ def _trunk(model, b: Batch, plan: Plan, raw_cells: bool = False):
     # the cell state (each update adds in fp32 and rounds once); the knob-off
     # cell pass keeps it in fp32 for its compensated-weight launches
     wtab = P["window_table.weight"]
-    w = (wtab.to(HALF) if cfg.cell_nodes else wtab).index_select(0, b.window_feat)
+    w = ops.gather_rows(wtab.to(HALF) if cfg.cell_nodes else wtab, b.window_feat)
     c = None
     if cfg.cell_nodes:
         # covered cells start from cell_base, the others from their nearest-stone
-        # row: one gather from the table [nearest rows; cell_base].  The cell
-        # state is stored in fp16 (866 MB -> 433 MB per pass at 1.69M cells):
-        # every kernel that updates it keeps the rows in fp32 registers and
-        # rounds once on the store, and its readers feed fp16 MFMA operands
+        # row: one gather from the table [nearest rows; cell_base] (the decoder
+        # CSR tells the covered cells).  The cell state is stored in fp16
+        # (866 MB -> 433 MB per pass at 1.69M cells): every kernel that updates
+        # it keeps the rows in fp32 registers and rounds once on the store, and
+        # its readers feed fp16 MFMA operands
         table = torch.cat([P["cell_nearest_table.weight"], P["cell_base"][None, :]]).to(HALF)
-        c = table.index_select(0, torch.where(plan.covered_mask, table.shape[0] - 1, b.cell_nearest))
+        c = ops.gather_rows(table, b.cell_nearest, cover_ptr=plan.cell_ptr, cover_row=table.shape[0] - 1)
     sw_all = ops.run_reduce(W["sw_all"], plan.run_class, plan.inc_stone_ptr, n_s, F32)
     for i in range(cfg.blocks):
         _block(W, P, i, plan, b, sg, w, c, sw_all, i + 1 < cfg.blocks)

@@ -226,6 +226,34 @@ def segment_order(seg_ptr: Tensor, ptr_a: Tensor, ptr_b: Tensor | None, n_rows: 
 # ----------------------------------------------------------------- run reduction
 
 
+def gather_rows(table: Tensor, idx: Tensor, cover_ptr: Tensor | None = None, cover_row: int = 0) -> Tensor:
+    """out[i] = table[idx[i]] over 128-wide rows, or table[cover_row] where
+    cover_ptr[i + 1] > cover_ptr[i] (a CSR with entries for row i)."""
+    dev = _on_gpu(table, idx, cover_ptr)
+    if table.ndim != 2 or table.shape[1] != 128 or table.stride(1) != 1:
+        raise ValueError("table must be (n, 128) rows")
+    if table.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        raise ValueError("table must be fp32, fp16 or bf16")
+    table = table if table.stride(0) * table.element_size() % 16 == 0 else table.contiguous()
+    idx = _i64(idx, "idx")
+    n = idx.numel()
+    if cover_ptr is not None:
+        cover_ptr = _i64(cover_ptr, "cover_ptr")
+        if cover_ptr.numel() != n + 1:
+            raise ValueError("cover_ptr must have n + 1 entries")
+        if not 0 <= cover_row < table.shape[0]:
+            raise ValueError("cover_row is not a row of the table")
+    out = torch.empty((n, 128), dtype=table.dtype, device=dev)
+    if n:
+        nbytes = n * (8 + 128 * out.element_size()) + table.shape[0] * 128 * table.element_size()
+        _launch(f"gather_rows_{_SHORT[table.dtype]}", nbytes, 0.0, lambda: _check(
+            _lib().mantis_gather_rows(_ptr(table), _dt(table), table.stride(0), table.shape[0], _ptr(idx),
+                                      _ptr(cover_ptr), cover_row, n, _ptr(out), out.stride(0),
+                                      _ptr(error_flag(dev)), _stream()),
+            "gather_rows"))
+    return out
+
+
 def run_reduce(values: Tensor, gather: Tensor, ptr: Tensor, n_dest: int, out_dtype: torch.dtype) -> Tensor:
     """out[d] = sum of values[gather[e]] over e in [ptr[d], ptr[d+1]), fp32 accumulated."""
     dev = _on_gpu(values, gather, ptr)
@@ -645,6 +673,19 @@ def _head_tab_blocked_index() -> Tensor:
 # contiguous columns 64 q .. 64 q + 63
 HEAD_TAB_BLOCKED = _head_tab_blocked_index()
 
+_DEVICE_CONSTS: dict[tuple[int, torch.device], Tensor] = {}
+
+
+def _const_on(t: Tensor, dev: torch.device) -> Tensor:
+    """A device copy of a module-level CPU index constant, made once per
+    device: a copy from pageable host memory on every call would block the
+    host until the stream drains."""
+    key = (id(t), dev)
+    got = _DEVICE_CONSTS.get(key)
+    if got is None:
+        got = _DEVICE_CONSTS[key] = t.to(dev)
+    return got
+
 
 class SubStage(NamedTuple):
     """One typed-attention sub-stage over residual rows: weights (wq, bq, wo,
@@ -772,7 +813,7 @@ def cell_heads(c: Tensor, w1: Tensor, b1: Tensor, w2: Tensor, w3: Tensor, b3: Te
         raise ValueError("act_table must be (n, 128)")
     # the kernel gathers both tables in fp16, the class table lane-blocked
     act_table = act_table.to(torch.float16).contiguous()
-    head_tab = head_tab.index_select(1, HEAD_TAB_BLOCKED.to(head_tab.device)).to(torch.float16).contiguous()
+    head_tab = head_tab.index_select(1, _const_on(HEAD_TAB_BLOCKED, head_tab.device)).to(torch.float16).contiguous()
     act_empty = _i64(act_empty, "act_empty")
     cell_pos, dec_ptr = _i64(cell_pos, "cell_pos"), _i64(dec_ptr, "dec_ptr")
     dec_window, act_class, dec_class = _i64(dec_window, "dec_window"), _i64(act_class, "act_class"), \

@@ -64,6 +64,20 @@ int32_t mantis_segment_order(const int64_t* seg_ptr, int64_t n_seg, const int64_
                              int64_t n_rows, int32_t* order, int32_t* err_flag, void* stream);
 
 /*
+ * Row gather of 128-wide rows: out[i, :] = table[r, :] with r = cover_row
+ * when cover_ptr is given and cover_ptr[i+1] > cover_ptr[i], else idx[i].
+ * table (n_table, ld_table) and out (n, ld_out) share `dtype` (MANTIS_F32,
+ * MANTIS_F16 or MANTIS_BF16), rows 16-byte aligned.  An index outside
+ * [0, n_table) writes a zero row and sets MANTIS_FLAG_INDEX.  Replaces the
+ * initial-state lookups of MantisNet.trunk (python/mantisnet/mantisnet/
+ * model.py:908-935: window_table(window_feat), and cell_base on covered
+ * cells / cell_nearest_table(cell_nearest) elsewhere).
+ */
+int32_t mantis_gather_rows(const void* table, int32_t dtype, int64_t ld_table, int64_t n_table,
+                           const int64_t* idx, const int64_t* cover_ptr, int64_t cover_row, int64_t n,
+                           void* out, int64_t ld_out, int32_t* err_flag, void* stream);
+
+/*
  * Run reduction: out[d, :] = sum over e in [ptr[d], ptr[d+1]) of
  * values[gather[e], :], accumulated in fp32, cast to out_dtype.  Rows with
  * no entries are written as zeros.  values is (n_src, ld) with the first `h`

@@ -253,6 +253,32 @@ def test_stone_attention_schedule_does_not_change_the_output(device):
     assert bool((chunks[1:] <= chunks[:-1]).all())
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32, BF])
+def test_gather_rows_matches_index_select(device, dtype):
+    gen = _g(31)
+    table = torch.randn(11, 128, generator=gen).to(dtype)
+    idx = torch.randint(0, 10, (1037,), generator=gen)
+    got = ops.gather_rows(table.to(device), idx.to(device)).cpu()
+    assert torch.equal(got, table.index_select(0, idx))
+    # covered rows (CSR entries present) take the cover row, as the trunk's
+    # where(covered, cell_base, cell_nearest) lookup
+    counts = torch.randint(0, 3, (1037,), generator=gen)
+    ptr = torch.cat([torch.zeros(1, dtype=torch.long), counts.cumsum(0)])
+    got = ops.gather_rows(table.to(device), idx.to(device), cover_ptr=ptr.to(device), cover_row=10).cpu()
+    exp = table.index_select(0, torch.where(counts > 0, 10, idx))
+    assert torch.equal(got, exp)
+    ops.raise_on_device_error(device)
+
+
+def test_gather_rows_flags_out_of_range_index(device):
+    table = torch.ones(4, 128, dtype=torch.float16, device=device)
+    idx = torch.tensor([0, 3, 4, -1, 2], device=device)
+    got = ops.gather_rows(table, idx).cpu()
+    assert torch.all(got[[0, 1, 4]] == 1) and torch.all(got[[2, 3]] == 0)
+    with pytest.raises(ValueError):
+        ops.raise_on_device_error(device)
+
+
 def _hex_graphs(n_graphs, seed=0):
     from mantisnet import builder as B
     from mantisnet import synthetic as S
