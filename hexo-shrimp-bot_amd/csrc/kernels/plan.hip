@@ -1,0 +1,249 @@
+// Per-batch index plan on the device (the table derivations the reference
+// runs inside every forward: incidence_plan, message_passing.py:495-517; the
+// radius edge classes, model.py:843-859; the attention row maps of the
+// latent/stone sequence, model.py:621-669), each as one or a few launches
+// instead of a chain of generic sorts, gathers and elementwise passes.
+//
+// * plan_check_kernel: whether the batch arrives in the encoder's canonical
+//   orders (dec_cell, radius_dst and window_pos ascending; act_rev exactly the
+//   stable argsort of dec_window, checked as strict lexicographic ascent of
+//   (dec_window[act_rev[i]], act_rev[i]) with act_rev in range).  Any
+//   violation ORs 1 into *bad.  One pass, no host read: the forward reads the
+//   word together with the error flag once at its end.
+// * incidence order (stone-major view of the window-major incidence list,
+//   stable): a counting sort.  Counts per stone (atomics), one workgroup's
+//   exclusive scan into the CSR pointer, a scatter of entry indices into
+//   their stone's slots (atomics: unordered), then each stone's slots sorted
+//   by entry index — a stone lies in at most 18 windows, so the per-stone
+//   insertion sort is short.  The result is the stable order whatever order
+//   the atomics took, and the window and class of every entry are gathered
+//   in the same pass.
+// * radius_class_kernel: orbit + 48 (own + 2 on_axis), one pass.
+// * attention slots: the padded [latents; stones] sequence of each position
+//   (max_t slots, the 4 latent rows first) mapped to rows of the [s; g]
+//   buffer and back.
+#include "common.hpp"
+
+namespace mantis {
+namespace {
+
+constexpr int kScanThreads = 1024;
+
+__device__ __forceinline__ int64_t floordiv(int64_t a, int64_t b) {
+  const int64_t q = a / b;
+  return (a % b != 0 && ((a < 0) != (b < 0))) ? q - 1 : q;
+}
+
+__global__ void plan_check_kernel(const int64_t* __restrict__ dec_cell, const int64_t* __restrict__ dec_window,
+                                  int64_t n_dec, const int64_t* __restrict__ act_rev,
+                                  const int64_t* __restrict__ radius_dst, int64_t n_rad,
+                                  const int64_t* __restrict__ window_slot, int64_t n_w, int64_t max_w,
+                                  int32_t* bad) {
+  int64_t n = n_dec > n_rad ? n_dec : n_rad;
+  n = n > n_w ? n : n_w;
+  bool viol = false;
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x) {
+    if (i + 1 < n_dec && dec_cell[i + 1] < dec_cell[i]) viol = true;
+    if (i + 1 < n_rad && radius_dst[i + 1] < radius_dst[i]) viol = true;
+    if (i + 1 < n_w && floordiv(window_slot[i + 1], max_w) < floordiv(window_slot[i], max_w)) viol = true;
+    if (i < n_dec) {
+      const int64_t r = act_rev[i];
+      if (r < 0 || r >= n_dec) viol = true;
+      if (i + 1 < n_dec) {
+        const int64_t r1 = act_rev[i + 1];
+        const int64_t a = r < 0 ? 0 : (r >= n_dec ? n_dec - 1 : r);
+        const int64_t b = r1 < 0 ? 0 : (r1 >= n_dec ? n_dec - 1 : r1);
+        const int64_t ka = dec_window[a], kb = dec_window[b];
+        if (!(kb > ka || (kb == ka && b > a))) viol = true;
+      }
+    }
+  }
+  if (__builtin_amdgcn_ballot_w64(viol) && (threadIdx.x % 64) == 0) atomicOr(bad, 1);
+}
+
+__global__ void fill_i32_kernel(int32_t* __restrict__ p, int64_t n, int32_t v) {
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x)
+    p[i] = v;
+}
+
+__global__ void count_kernel(const int64_t* __restrict__ key, int64_t n, int64_t n_keys, int32_t* __restrict__ counts,
+                             int32_t* flag) {
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t k = key[i];
+    if (k >= 0 && k < n_keys) atomicAdd(&counts[k], 1);
+    else raise_flag(flag, MANTIS_FLAG_INDEX);
+  }
+}
+
+// ptr[0] = 0, ptr[k + 1] = counts[0] + ... + counts[k]; cursor[k] = ptr[k].
+// One workgroup: thread t sums a contiguous chunk, the chunk totals are
+// scanned in LDS, then each thread writes its chunk's prefix sums.
+__global__ void __launch_bounds__(kScanThreads)
+scan_kernel(const int32_t* __restrict__ counts, int64_t n, int64_t* __restrict__ ptr, int64_t* __restrict__ cursor) {
+  __shared__ int64_t part[kScanThreads];
+  const int64_t per = (n + kScanThreads - 1) / kScanThreads;
+  const int64_t b = int64_t(threadIdx.x) * per;
+  const int64_t e = b + per < n ? b + per : n;
+  int64_t s = 0;
+  for (int64_t i = b; i < e; ++i) s += counts[i];
+  part[threadIdx.x] = s;
+  __syncthreads();
+  for (int off = 1; off < kScanThreads; off <<= 1) {  // inclusive Hillis-Steele scan
+    const int64_t add = threadIdx.x >= off ? part[threadIdx.x - off] : 0;
+    __syncthreads();
+    part[threadIdx.x] += add;
+    __syncthreads();
+  }
+  int64_t run = threadIdx.x ? part[threadIdx.x - 1] : 0;
+  if (threadIdx.x == 0) ptr[0] = 0;
+  for (int64_t i = b; i < e; ++i) {
+    cursor[i] = run;
+    run += counts[i];
+    ptr[i + 1] = run;
+  }
+}
+
+__global__ void scatter_kernel(const int64_t* __restrict__ key, int64_t n, int64_t n_keys,
+                               unsigned long long* __restrict__ cursor, int64_t* __restrict__ perm) {
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t k = key[i];
+    if (k >= 0 && k < n_keys) perm[int64_t(atomicAdd(&cursor[k], 1ull))] = i;
+  }
+}
+
+// each key's run of perm sorted ascending (the stable order), then the
+// entries' second and third columns gathered in that order
+__global__ void segment_sort_gather_kernel(const int64_t* __restrict__ ptr, int64_t n_keys, int64_t* __restrict__ perm,
+                                           const int64_t* __restrict__ col_a, const int64_t* __restrict__ col_b,
+                                           int64_t* __restrict__ out_a, int64_t* __restrict__ out_b) {
+  for (int64_t k = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; k < n_keys; k += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t b = ptr[k], e = ptr[k + 1];
+    for (int64_t i = b + 1; i < e; ++i) {  // insertion sort (runs are short)
+      const int64_t v = perm[i];
+      int64_t j = i - 1;
+      while (j >= b && perm[j] > v) {
+        perm[j + 1] = perm[j];
+        --j;
+      }
+      perm[j + 1] = v;
+    }
+    for (int64_t i = b; i < e; ++i) {
+      const int64_t src = perm[i];
+      out_a[i] = col_a[src];
+      out_b[i] = col_b[src];
+    }
+  }
+}
+
+__global__ void radius_class_kernel(const int64_t* __restrict__ orbit, const int64_t* __restrict__ own,
+                                    const int64_t* __restrict__ on_axis, int64_t n, int64_t* __restrict__ out) {
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x)
+    out[i] = orbit[i] + 48 * (own[i] + 2 * on_axis[i]);
+}
+
+// attn_src over the padded slots: the latent rows of each position (slots
+// 0..3) name rows n_s + 4 p + j, every other slot -1 (stones fill in next)
+__global__ void attn_slots_init_kernel(int64_t n_pos, int64_t max_t, int64_t n_s, int64_t* __restrict__ attn_src) {
+  const int64_t n = n_pos * max_t;
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t p = i / max_t, j = i % max_t;
+    attn_src[i] = j < 4 ? n_s + 4 * p + j : -1;
+  }
+}
+
+// stones into their slots; attn_back = [stone_slot; latent slots]
+__global__ void attn_slots_kernel(const int64_t* __restrict__ stone_slot, int64_t n_s, int64_t n_pos, int64_t max_t,
+                                  int64_t* __restrict__ attn_src, int64_t* __restrict__ attn_back, int32_t* flag) {
+  const int64_t n = n_s + 4 * n_pos;
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x) {
+    if (i < n_s) {
+      const int64_t slot = stone_slot[i];
+      attn_back[i] = slot;
+      if (slot >= 0 && slot < n_pos * max_t && slot % max_t >= 4) attn_src[slot] = i;
+      else raise_flag(flag, MANTIS_FLAG_INDEX);
+    } else {
+      const int64_t j = i - n_s;
+      attn_back[i] = (j / 4) * max_t + j % 4;
+    }
+  }
+}
+
+inline unsigned grid_for(int64_t n, int64_t cap = 16384) {
+  int64_t g = (n + 255) / 256;
+  if (g < 1) g = 1;
+  return unsigned(g > cap ? cap : g);
+}
+
+}  // namespace
+}  // namespace mantis
+
+using namespace mantis;
+
+extern "C" {
+
+int32_t mantis_plan_check(const int64_t* dec_cell, const int64_t* dec_window, int64_t n_dec, const int64_t* act_rev,
+                          const int64_t* radius_dst, int64_t n_rad, const int64_t* window_slot, int64_t n_w,
+                          int64_t max_w, int32_t* bad, void* stream) {
+  if (!bad || n_dec < 0 || n_rad < 0 || n_w < 0 || max_w <= 0) return MANTIS_E_ARG;
+  if ((n_dec && (!dec_cell || !dec_window || !act_rev)) || (n_rad && !radius_dst) || (n_w && !window_slot))
+    return MANTIS_E_ARG;
+  int64_t n = n_dec > n_rad ? n_dec : n_rad;
+  n = n > n_w ? n : n_w;
+  if (n == 0) return MANTIS_OK;
+  plan_check_kernel<<<grid_for(n, 4096), 256, 0, as_stream(stream)>>>(dec_cell, dec_window, n_dec, act_rev,
+                                                                      radius_dst, n_rad, window_slot, n_w, max_w, bad);
+  return launched();
+}
+
+int64_t mantis_stable_key_order_workspace(int64_t n_entries, int64_t n_keys) {
+  if (n_entries < 0 || n_keys < 0) return -1;
+  // counts (int32, padded to 8 bytes), cursors (int64), permutation (int64)
+  return (4 * n_keys + 7) / 8 * 8 + 8 * n_keys + 8 * n_entries;
+}
+
+int32_t mantis_stable_key_order(const int64_t* key, const int64_t* col_a, const int64_t* col_b, int64_t n_entries,
+                                int64_t n_keys, int64_t* ptr, int64_t* out_a, int64_t* out_b, void* workspace,
+                                int32_t* err_flag, void* stream) {
+  if (!ptr || n_entries < 0 || n_keys < 0) return MANTIS_E_ARG;
+  if (n_entries && (!key || !col_a || !col_b || !out_a || !out_b || !workspace)) return MANTIS_E_ARG;
+  if (n_keys && !workspace) return MANTIS_E_ARG;
+  hipStream_t st = as_stream(stream);
+  if (n_keys == 0) {
+    fill_i32_kernel<<<1, 64, 0, st>>>(reinterpret_cast<int32_t*>(ptr), 2, 0);  // ptr[0] = 0 (int64 zero)
+    if (n_entries) count_kernel<<<grid_for(n_entries), 256, 0, st>>>(key, n_entries, 0, nullptr, err_flag);
+    return launched();
+  }
+  int32_t* counts = static_cast<int32_t*>(workspace);
+  int64_t* cursor = reinterpret_cast<int64_t*>(static_cast<char*>(workspace) + ((4 * n_keys + 7) / 8) * 8);
+  int64_t* perm = cursor + n_keys;
+  fill_i32_kernel<<<grid_for(n_keys), 256, 0, st>>>(counts, n_keys, 0);
+  if (n_entries) count_kernel<<<grid_for(n_entries), 256, 0, st>>>(key, n_entries, n_keys, counts, err_flag);
+  scan_kernel<<<1, kScanThreads, 0, st>>>(counts, n_keys, ptr, cursor);
+  if (n_entries) {
+    scatter_kernel<<<grid_for(n_entries), 256, 0, st>>>(key, n_entries, n_keys,
+                                                         reinterpret_cast<unsigned long long*>(cursor), perm);
+    segment_sort_gather_kernel<<<grid_for(n_keys), 256, 0, st>>>(ptr, n_keys, perm, col_a, col_b, out_a, out_b);
+  }
+  return launched();
+}
+
+int32_t mantis_radius_class(const int64_t* orbit, const int64_t* own, const int64_t* on_axis, int64_t n,
+                            int64_t* out, void* stream) {
+  if (n == 0) return MANTIS_OK;
+  if (!orbit || !own || !on_axis || !out || n < 0) return MANTIS_E_ARG;
+  radius_class_kernel<<<grid_for(n), 256, 0, as_stream(stream)>>>(orbit, own, on_axis, n, out);
+  return launched();
+}
+
+int32_t mantis_attention_slots(const int64_t* stone_slot, int64_t n_s, int64_t n_pos, int64_t max_t,
+                               int64_t* attn_src, int64_t* attn_back, int32_t* err_flag, void* stream) {
+  if (n_pos < 0 || n_s < 0 || max_t < 4 || !attn_src || !attn_back || (n_s && !stone_slot)) return MANTIS_E_ARG;
+  if (n_pos == 0 && n_s == 0) return MANTIS_OK;
+  hipStream_t st = as_stream(stream);
+  if (n_pos) attn_slots_init_kernel<<<grid_for(n_pos * max_t), 256, 0, st>>>(n_pos, max_t, n_s, attn_src);
+  attn_slots_kernel<<<grid_for(n_s + 4 * n_pos), 256, 0, st>>>(stone_slot, n_s, n_pos, max_t, attn_src, attn_back,
+                                                               err_flag);
+  return launched();
+}
+
+}  // extern "C"

@@ -24,6 +24,11 @@ class MantisSubstage(ctypes.Structure):
 
 SIGNATURES = {
     "mantis_hip_version": ([], i32),
+    "mantis_plan_check": ([vp, vp, i64, vp, vp, i64, vp, i64, i64, vp, vp], i32),
+    "mantis_stable_key_order_workspace": ([i64, i64], i64),
+    "mantis_stable_key_order": ([vp, vp, vp, i64, i64, vp, vp, vp, vp, vp, vp], i32),
+    "mantis_radius_class": ([vp, vp, vp, i64, vp, vp], i32),
+    "mantis_attention_slots": ([vp, i64, i64, i64, vp, vp, vp, vp], i32),
     "mantis_gather_rows": ([vp, i32, i64, i64, vp, vp, i64, i64, vp, i64, vp, vp], i32),
     "mantis_runs_to_ptr": ([vp, i64, i64, vp, vp, vp], i32),
     "mantis_segment_order": ([vp, i64, vp, vp, i64, vp, vp, vp], i32),

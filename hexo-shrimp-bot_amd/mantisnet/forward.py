@@ -78,19 +78,24 @@ def _supported(model) -> torch.device:
 
 class Prepared:
     """fp16 GEMM operands with folded LayerNorms and composed class tables,
-    rebuilt whenever a parameter changes (tracked by version counters)."""
+    rebuilt whenever a parameter changes (tracked by version counters and
+    storage addresses).  ``params`` is the name -> parameter map."""
 
     def __init__(self, model):
         self.model = model
         self.key = None
         self.t: dict[str, Tensor] = {}
+        self.params: dict[str, Tensor] = dict(model.named_parameters())
+        self._plist = list(self.params.values())
 
     def refresh(self):
-        params = dict(self.model.named_parameters())
-        key = tuple((n, p.data_ptr(), p._version) for n, p in params.items())
+        # the module's parameter set is fixed after construction; what changes
+        # is their storage (load_state_dict, .to) and their version (in-place
+        # optimizer steps)
+        key = tuple((p.data_ptr(), p._version) for p in self._plist)
         if key != self.key:
             with torch.no_grad():
-                self.t = _prepare(self.model, {n: p.detach().float() for n, p in params.items()})
+                self.t = _prepare(self.model, {n: p.detach().float() for n, p in self.params.items()})
             self.key = key
         return self
 
@@ -273,6 +278,7 @@ class Plan:
     attn_src: Tensor  # padded attention slot -> row of [s; g] (or -1)
     attn_back: Tensor  # row of [s; g] -> padded attention slot
     dec_cell_ptr: Tensor  # CSR of the batch's own decoder order
+    noncanonical: Tensor | None = None  # speculative plans: device word, nonzero if the canonical orders failed
 
 
 def _stable_order(key: Tensor) -> Tensor:
@@ -280,7 +286,9 @@ def _stable_order(key: Tensor) -> Tensor:
 
 
 def _canonical_orders(b: Batch, window_pos: Tensor) -> bool:
-    """Whether the batch arrives in the encoder's canonical orders, so the
+    """The canonical-order check as plain tensor arithmetic (the forward runs
+    the same check as one device kernel, ops.plan_check; the two are tested to
+    agree).  Whether the batch arrives in the encoder's canonical orders, so the
     stable sorts of the table derivation are identities (or, for the
     window-major decoder view, equal to the batch's act_rev permutation):
     dec_cell, radius_dst and window_pos ascending, and act_rev exactly the
@@ -304,17 +312,24 @@ def _canonical_orders(b: Batch, window_pos: Tensor) -> bool:
     return bool(torch.stack(flags).all().item())
 
 
-def make_plan(model, b: Batch) -> Plan:
+def make_plan(model, b: Batch, speculative: bool = False) -> Plan:
+    """The per-batch index plan.  The stable sorts of the reference's table
+    derivations are identities on batches in the encoder's canonical orders;
+    a device-side check decides.  speculative=True assumes the canonical
+    orders without reading the check (no host synchronisation) and leaves
+    the check's word in plan.noncanonical for the caller to read once the
+    evaluation is queued; otherwise the check is read here."""
     cfg = model.cfg
     dev = b.stone_own.device
     p, max_t, max_w = b.attn_valid.shape[0], b.attn_valid.shape[1], b.value_valid.shape[1]
     n_s, n_w, n_c = b.stone_own.shape[0], b.window_feat.shape[0], b.cell_pos.shape[0]
     window_pos = torch.div(b.window_slot, max_w, rounding_mode="floor")
-    canonical = _canonical_orders(b, window_pos)
-    # incidence plan (message_passing.py:495-517)
-    order = _stable_order(b.inc_stone.to(torch.int32))
-    run_stone, run_window, run_class = b.inc_stone[order], b.inc_window[order], b.inc_class[order]
-    classes = b.radius_orbit + ORBIT48 * (b.radius_own + 2 * b.radius_on_axis)
+    check = ops.plan_check(b.dec_cell, b.dec_window, b.act_rev, b.radius_dst, b.window_slot, max_w)
+    canonical = True if speculative else not bool(check.item())
+    # incidence plan (message_passing.py:495-517): the stone-major view of the
+    # window-major incidence list, stable, and its CSR
+    inc_stone_ptr, run_window, run_class = ops.stable_key_order(b.inc_stone, b.inc_window, b.inc_class, n_s)
+    classes = ops.radius_class(b.radius_orbit, b.radius_own, b.radius_on_axis)
     src, dst = b.radius_src, b.radius_dst
     if canonical:
         # the sorts below are identities on canonical batches (and act_rev is
@@ -368,17 +383,13 @@ def make_plan(model, b: Batch) -> Plan:
         # position stay together, and with them the k/v rows they gather)
         cell_order = ops.segment_order(b.legal_offsets, cell_ptr, radius_ptr, n_c)
     # attention rows [latents; stones] per position over the [s; g] buffer
-    gslot = (torch.arange(p, device=dev)[:, None] * max_t + torch.arange(GLOBAL_ROWS, device=dev)[None, :]).reshape(-1)
-    attn_src = torch.full((p * max_t,), -1, dtype=torch.long, device=dev)
-    attn_src[b.stone_slot] = torch.arange(n_s, device=dev)
-    attn_src[gslot] = n_s + torch.arange(p * GLOBAL_ROWS, device=dev)
-    attn_back = torch.cat([b.stone_slot, gslot])
+    attn_src, attn_back = ops.attention_slots(b.stone_slot, p, max_t)
     seq_lens = b.attn_valid.sum(dim=1, dtype=torch.int32)
     return Plan(
         n_pos=p, max_t=max_t, max_w=max_w, n_s=n_s, n_w=n_w, n_c=n_c,
         inc_win_ptr=ops.runs_to_ptr(b.inc_window, n_w),
         run_window=run_window, run_class=run_class,
-        inc_stone_ptr=ops.runs_to_ptr(run_stone.contiguous(), n_s),
+        inc_stone_ptr=inc_stone_ptr,
         window_pos=window_pos, layout_offsets=offsets, layout_order=lorder,
         covered_mask=covered, cov_rows=cov_rows, edge_wcell_cov=edge_wcell_cov, cell_ptr=cell_ptr,
         edge_window=edge_window, edge_class=edge_class,
@@ -391,6 +402,7 @@ def make_plan(model, b: Batch) -> Plan:
         seq_lens=seq_lens, stone_schedule=ops.stone_attention_schedule(seq_lens, cfg.heads, max_t),
         attn_src=attn_src, attn_back=attn_back,
         dec_cell_ptr=cell_ptr if canonical else ops.runs_to_ptr(b.dec_cell, n_c),
+        noncanonical=check if speculative else None,
     )
 
 
@@ -539,11 +551,12 @@ def trunk(model, batch: Batch):
     return _trunk(model, b, plan)
 
 
-def _trunk(model, b: Batch, plan: Plan, raw_cells: bool = False):
+def _trunk(model, b: Batch, plan: Plan, raw_cells: bool = False, W: Prepared | None = None):
     """(w_out, g_out, cells): cells are ln_out(c) in fp16, or with raw_cells
-    the fp16 cell state itself (the fused heads normalise it on the fly)."""
-    W = _prepared(model)
-    P = dict(model.named_parameters())
+    the fp16 cell state itself (the fused heads normalise it on the fly).
+    W: the prepared weights when the caller has just refreshed them."""
+    W = W or _prepared(model)
+    P = W.params
     cfg = model.cfg
     n_s, p = plan.n_s, plan.n_pos
     # residual streams: s and g share one buffer so the attention and FFN
@@ -585,8 +598,8 @@ def value_head(model, w: Tensor, g: Tensor, batch: Batch):
     return _value_head(model, w, g, b, plan)
 
 
-def _value_head(model, w: Tensor, g: Tensor, b: Batch, plan: Plan):
-    P = dict(model.named_parameters())
+def _value_head(model, w: Tensor, g: Tensor, b: Batch, plan: Plan, W: Prepared | None = None):
+    P = (W or _prepared(model)).params
     r = ops.value_read(g.float().contiguous(), w.float().contiguous(), plan.layout_offsets, plan.layout_order,
                        P["ln_value.weight"], P["ln_value.bias"], P["value_queries"])
     hidden = F.relu(F.linear(r.reshape(plan.n_pos, -1), P["mlp_v.0.weight"], P["mlp_v.0.bias"]))
@@ -595,7 +608,8 @@ def _value_head(model, w: Tensor, g: Tensor, b: Batch, plan: Plan):
     return dist @ model.bin_centers, dist, logits
 
 
-def _head_rows(model, w: Tensor, g: Tensor, cells: Tensor, b: Batch, plan: Plan, raw_cells: bool = False) -> Tensor:
+def _head_rows(model, w: Tensor, g: Tensor, cells: Tensor, b: Batch, plan: Plan, raw_cells: bool = False,
+               W: Prepared | None = None) -> Tensor:
     """(N_c, 16) fp32: column 0 the policy logit, 1..3 the critic logits.
     ``cells`` are ln_out(c) rows, or with raw_cells the fp16 cell state; with
     cell state off they are None and each legal cell reads the sum of its
@@ -607,8 +621,8 @@ def _head_rows(model, w: Tensor, g: Tensor, cells: Tensor, b: Batch, plan: Plan,
             raise ValueError("cell rows were passed but cell state is off")
         cells = ops.run_reduce(w, b.dec_window, plan.dec_cell_ptr, plan.n_c, HALF)
         raw_cells = False
-    W = _prepared(model)
-    P = dict(model.named_parameters())
+    W = W or _prepared(model)
+    P = W.params
     pre = FL(w.float().contiguous(), W["act_proj.w"], W["act_proj.b"])  # act_proj(w), fp16
     empty_rows = F.relu(P["act_empty_base"] + P["act_table.weight"].index_select(0, model.act_empty_classes))
     g_half = F.linear(g.float(), W["glin_b"]).contiguous()  # (P, 256)
@@ -635,8 +649,9 @@ def cell_heads(model, w: Tensor, g: Tensor, cells: Tensor, batch: Batch, mass_fl
     return _cell_heads(model, w, g, cells, b, plan, mass_floor)
 
 
-def _cell_heads(model, w, g, cells, b: Batch, plan: Plan, mass_floor: float, raw_cells: bool = False):
-    rows = _head_rows(model, w, g, cells, b, plan, raw_cells)
+def _cell_heads(model, w, g, cells, b: Batch, plan: Plan, mass_floor: float, raw_cells: bool = False,
+                W: Prepared | None = None):
+    rows = _head_rows(model, w, g, cells, b, plan, raw_cells, W)
     q_values, q_score = ops.compose_q(rows[:, 1:], b.legal_offsets, mass_floor)
     return rows[:, 0].contiguous(), q_score, q_values
 
@@ -650,8 +665,20 @@ def forward(model, batch: Batch, mass_floor: float):
     _supported(model)
     dev = next(model.parameters()).device
     b = batch if batch.stone_own.device == dev else batch.to(dev)
-    plan = make_plan(model, b)
-    w, g, c = _trunk(model, b, plan, raw_cells=True)
-    value, value_dist, value_logits = _value_head(model, w, g, b, plan)
-    policy, q_score, q_values = _cell_heads(model, w, g, c, b, plan, mass_floor, raw_cells=True)
-    return policy, q_score, q_values, value, value_dist, value_logits
+    W = _prepared(model)  # once per evaluation: trunk and heads share it
+
+    def evaluate(plan):
+        w, g, c = _trunk(model, b, plan, raw_cells=True, W=W)
+        value, value_dist, value_logits = _value_head(model, w, g, b, plan, W)
+        policy, q_score, q_values = _cell_heads(model, w, g, c, b, plan, mass_floor, raw_cells=True, W=W)
+        return policy, q_score, q_values, value, value_dist, value_logits
+
+    # queued on the canonical orders the encoder emits; the order check is read
+    # after everything is queued, and a batch in other orders is evaluated
+    # again over sorted tables (the first pass's results and flags discarded)
+    plan = make_plan(model, b, speculative=True)
+    out = evaluate(plan)
+    if bool(plan.noncanonical.item()):
+        ops.error_flag(dev).zero_()
+        out = evaluate(make_plan(model, b))
+    return out

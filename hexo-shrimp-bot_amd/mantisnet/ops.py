@@ -226,6 +226,74 @@ def segment_order(seg_ptr: Tensor, ptr_a: Tensor, ptr_b: Tensor | None, n_rows: 
 # ----------------------------------------------------------------- run reduction
 
 
+def plan_check(dec_cell: Tensor, dec_window: Tensor, act_rev: Tensor, radius_dst: Tensor, window_slot: Tensor,
+               max_w: int) -> Tensor:
+    """A device int32 word: nonzero unless the batch is in the encoder's
+    canonical orders (see mantis_plan_check).  No host read."""
+    dev = _on_gpu(dec_cell, dec_window, act_rev, radius_dst, window_slot)
+    dec_cell, dec_window, act_rev = _i64(dec_cell, "dec_cell"), _i64(dec_window, "dec_window"), _i64(act_rev, "act_rev")
+    radius_dst, window_slot = _i64(radius_dst, "radius_dst"), _i64(window_slot, "window_slot")
+    bad = torch.zeros(1, dtype=torch.int32, device=dev)
+    if act_rev.numel() != dec_window.numel() or dec_cell.numel() != dec_window.numel():
+        bad.fill_(1)
+        return bad
+    n = max(dec_cell.numel(), radius_dst.numel(), window_slot.numel())
+    _launch("plan_check", 8.0 * (3 * dec_cell.numel() + radius_dst.numel() + window_slot.numel()), 0.0, lambda: _check(
+        _lib().mantis_plan_check(_ptr(dec_cell), _ptr(dec_window), dec_cell.numel(), _ptr(act_rev), _ptr(radius_dst),
+                                 radius_dst.numel(), _ptr(window_slot), window_slot.numel(), max(int(max_w), 1),
+                                 _ptr(bad), _stream()), "plan_check")) if n else None
+    return bad
+
+
+def stable_key_order(key: Tensor, col_a: Tensor, col_b: Tensor, n_keys: int) -> tuple[Tensor, Tensor, Tensor]:
+    """(ptr, a, b): the CSR over keys and col_a / col_b in the stable
+    key-major order of the entries (argsort(key, stable=True) + gathers +
+    searchsorted in one counting sort; key runs must be short)."""
+    dev = _on_gpu(key, col_a, col_b)
+    key, col_a, col_b = _i64(key, "key"), _i64(col_a, "col_a"), _i64(col_b, "col_b")
+    n = key.numel()
+    if col_a.numel() != n or col_b.numel() != n:
+        raise ValueError("key, col_a and col_b must have one length")
+    ptr = torch.empty(n_keys + 1, dtype=torch.int64, device=dev)
+    out_a = torch.empty(n, dtype=torch.int64, device=dev)
+    out_b = torch.empty(n, dtype=torch.int64, device=dev)
+    ws = torch.empty(max(int(_lib().mantis_stable_key_order_workspace(n, n_keys)), 8), dtype=torch.uint8, device=dev)
+    _launch("stable_key_order", 8.0 * (5 * n + 3 * n_keys), 0.0, lambda: _check(
+        _lib().mantis_stable_key_order(_ptr(key), _ptr(col_a), _ptr(col_b), n, n_keys, _ptr(ptr), _ptr(out_a),
+                                       _ptr(out_b), _ptr(ws), _ptr(error_flag(dev)), _stream()),
+        "stable_key_order"))
+    return ptr, out_a, out_b
+
+
+def radius_class(orbit: Tensor, own: Tensor, on_axis: Tensor) -> Tensor:
+    """orbit + 48 (own + 2 on_axis) in one pass (int64)."""
+    dev = _on_gpu(orbit, own, on_axis)
+    orbit, own, on_axis = _i64(orbit, "orbit"), _i64(own, "own"), _i64(on_axis, "on_axis")
+    if not (orbit.shape == own.shape == on_axis.shape) or orbit.ndim != 1:
+        raise ValueError("radius_orbit, radius_own and radius_on_axis must have one length")
+    out = torch.empty_like(orbit)
+    if orbit.numel():
+        _launch("radius_class", 32.0 * orbit.numel(), 0.0, lambda: _check(
+            _lib().mantis_radius_class(_ptr(orbit), _ptr(own), _ptr(on_axis), orbit.numel(), _ptr(out), _stream()),
+            "radius_class"))
+    return out
+
+
+def attention_slots(stone_slot: Tensor, n_pos: int, max_t: int) -> tuple[Tensor, Tensor]:
+    """(attn_src, attn_back) of the padded [latents; stones] sequences: the
+    [s; g] row of every slot (-1 when empty), and the slot of every row."""
+    dev = _on_gpu(stone_slot)
+    stone_slot = _i64(stone_slot, "stone_slot")
+    n_s = stone_slot.numel()
+    attn_src = torch.empty(n_pos * max_t, dtype=torch.int64, device=dev)
+    attn_back = torch.empty(n_s + 4 * n_pos, dtype=torch.int64, device=dev)
+    if n_pos or n_s:
+        _launch("attention_slots", 8.0 * (n_pos * max_t + 2 * n_s + 4 * n_pos), 0.0, lambda: _check(
+            _lib().mantis_attention_slots(_ptr(stone_slot), n_s, n_pos, max_t, _ptr(attn_src), _ptr(attn_back),
+                                          _ptr(error_flag(dev)), _stream()), "attention_slots"))
+    return attn_src, attn_back
+
+
 def gather_rows(table: Tensor, idx: Tensor, cover_ptr: Tensor | None = None, cover_row: int = 0) -> Tensor:
     """out[i] = table[idx[i]] over 128-wide rows, or table[cover_row] where
     cover_ptr[i + 1] > cover_ptr[i] (a CSR with entries for row i)."""

@@ -64,6 +64,54 @@ int32_t mantis_segment_order(const int64_t* seg_ptr, int64_t n_seg, const int64_
                              int64_t n_rows, int32_t* order, int32_t* err_flag, void* stream);
 
 /*
+ * Canonical-order check of a batch (the orders the encoder emits): ORs 1
+ * into *bad (a device int32 the caller zeroes) unless dec_cell, radius_dst and
+ * floor(window_slot / max_w) are ascending and act_rev (n_dec entries) is
+ * exactly the stable argsort of dec_window.  On such a batch the stable sorts
+ * of the table derivation (cell_latents.py:96-165, cell_nodes.py:23-94,
+ * window_latents.py:38-56) are identities or act_rev; no counterpart in the
+ * reference, which always sorts.
+ */
+int32_t mantis_plan_check(const int64_t* dec_cell, const int64_t* dec_window, int64_t n_dec,
+                          const int64_t* act_rev, const int64_t* radius_dst, int64_t n_rad,
+                          const int64_t* window_slot, int64_t n_w, int64_t max_w, int32_t* bad,
+                          void* stream);
+
+/*
+ * Stable key-major view of an entry list with small key runs (the stone-major
+ * incidence view of incidence_plan, message_passing.py:495-517, as
+ * torch.argsort(key, stable=True) + gathers + searchsorted): ptr (n_keys + 1)
+ * the CSR of the keys, out_a / out_b the entries' col_a / col_b in the stable
+ * key-major order.  A counting sort: per-key counts, one scan, an unordered
+ * scatter, then every key's run sorted by entry index (insertion sort: runs
+ * are short, at most 18 for the incidence).  workspace: at least
+ * mantis_stable_key_order_workspace(n_entries, n_keys) bytes, 8-byte aligned.
+ * Keys outside [0, n_keys) set MANTIS_FLAG_INDEX and are dropped.
+ */
+int64_t mantis_stable_key_order_workspace(int64_t n_entries, int64_t n_keys);
+int32_t mantis_stable_key_order(const int64_t* key, const int64_t* col_a, const int64_t* col_b,
+                                int64_t n_entries, int64_t n_keys, int64_t* ptr, int64_t* out_a,
+                                int64_t* out_b, void* workspace, int32_t* err_flag, void* stream);
+
+/*
+ * Radius edge classes: out[e] = orbit[e] + 48 (own[e] + 2 on_axis[e])
+ * (model.py:843-859, the radius_orbit/own/on_axis class index).
+ */
+int32_t mantis_radius_class(const int64_t* orbit, const int64_t* own, const int64_t* on_axis,
+                            int64_t n, int64_t* out, void* stream);
+
+/*
+ * Row maps of the padded per-position [latents; stones] sequence
+ * (model.py:621-669 packs the same rows): attn_src (n_pos * max_t) holds the
+ * [s; g] row of each slot (stone i at stone_slot[i], latent j of position p at
+ * slot p * max_t + j -> row n_s + 4 p + j, empty slots -1); attn_back (n_s +
+ * 4 n_pos) = [stone_slot; latent slots].  A stone slot outside the positions'
+ * stone ranges sets MANTIS_FLAG_INDEX.
+ */
+int32_t mantis_attention_slots(const int64_t* stone_slot, int64_t n_s, int64_t n_pos, int64_t max_t,
+                               int64_t* attn_src, int64_t* attn_back, int32_t* err_flag, void* stream);
+
+/*
  * Row gather of 128-wide rows: out[i, :] = table[r, :] with r = cover_row
  * when cover_ptr is given and cover_ptr[i+1] > cover_ptr[i], else idx[i].
  * table (n_table, ld_table) and out (n, ld_out) share `dtype` (MANTIS_F32,

@@ -279,6 +279,83 @@ def test_gather_rows_flags_out_of_range_index(device):
         ops.raise_on_device_error(device)
 
 
+def _plan_batch():
+    from mantisnet import collate_positions, synthetic
+    return collate_positions(synthetic.random_games(1, 5, start=3))
+
+
+def test_plan_check_agrees_with_the_tensor_check(device):
+    from mantisnet.forward import _canonical_orders
+
+    def both(b):
+        max_w = b.value_valid.shape[1]
+        dev_bad = bool(ops.plan_check(b.dec_cell.to(device), b.dec_window.to(device), b.act_rev.to(device),
+                                      b.radius_dst.to(device), b.window_slot.to(device), max_w).item())
+        return dev_bad, not _canonical_orders(b, b.window_slot // max_w)
+
+    b = _plan_batch()
+    assert both(b) == (False, False)
+    b = _plan_batch()
+    perm = torch.randperm(b.radius_dst.numel(), generator=_g(1))
+    b.radius_dst = b.radius_dst[perm]
+    assert both(b) == (True, True)
+    b = _plan_batch()
+    rev = b.act_rev.clone()
+    w = b.dec_window[rev]
+    i = int(torch.nonzero(w[1:] == w[:-1])[0])
+    rev[i], rev[i + 1] = rev[i + 1].clone(), rev[i].clone()  # window-sorted, no longer stable
+    b.act_rev = rev
+    assert both(b) == (True, True)
+    b = _plan_batch()
+    b.act_rev = b.act_rev.clone()
+    b.act_rev[0] = b.act_rev.numel()  # out of range
+    assert both(b) == (True, True)
+    b = _plan_batch()
+    b.dec_cell = b.dec_cell.flip(0)
+    assert both(b)[0]
+
+
+def test_stable_key_order_matches_stable_argsort(device):
+    b = _plan_batch()
+    n_s = b.stone_own.numel()
+    ptr, win, cls = ops.stable_key_order(b.inc_stone.to(device), b.inc_window.to(device), b.inc_class.to(device), n_s)
+    order = torch.argsort(b.inc_stone, stable=True)
+    assert torch.equal(win.cpu(), b.inc_window[order]) and torch.equal(cls.cpu(), b.inc_class[order])
+    assert torch.equal(ptr.cpu(), torch.searchsorted(b.inc_stone[order], torch.arange(n_s + 1)))
+    # random keys with long runs and empty keys, entries in no particular order
+    gen = _g(5)
+    key = torch.randint(0, 50, (3001,), generator=gen)
+    key[key == 7] = 8  # key 7 has no entries
+    a = torch.arange(3001) * 3
+    c = torch.randint(-5, 5, (3001,), generator=gen)
+    ptr, oa, oc = ops.stable_key_order(key.to(device), a.to(device), c.to(device), 50)
+    order = torch.argsort(key, stable=True)
+    assert torch.equal(oa.cpu(), a[order]) and torch.equal(oc.cpu(), c[order])
+    assert torch.equal(ptr.cpu(), torch.searchsorted(key[order], torch.arange(51)))
+    ops.raise_on_device_error(device)
+    # a key out of range is flagged and dropped
+    ptr, oa, _ = ops.stable_key_order(torch.tensor([0, 3, 1], device=device), torch.tensor([1, 2, 3], device=device),
+                                      torch.tensor([0, 0, 0], device=device), 2)
+    assert ptr.cpu().tolist() == [0, 1, 2]
+    with pytest.raises(ValueError):
+        ops.raise_on_device_error(device)
+
+
+def test_radius_class_and_attention_slots(device):
+    b = _plan_batch()
+    got = ops.radius_class(b.radius_orbit.to(device), b.radius_own.to(device), b.radius_on_axis.to(device)).cpu()
+    assert torch.equal(got, b.radius_orbit + 48 * (b.radius_own + 2 * b.radius_on_axis))
+    p, max_t, n_s = b.attn_valid.shape[0], b.attn_valid.shape[1], b.stone_own.numel()
+    src, back = ops.attention_slots(b.stone_slot.to(device), p, max_t)
+    gslot = (torch.arange(p)[:, None] * max_t + torch.arange(4)[None, :]).reshape(-1)
+    exp_src = torch.full((p * max_t,), -1, dtype=torch.long)
+    exp_src[b.stone_slot] = torch.arange(n_s)
+    exp_src[gslot] = n_s + torch.arange(p * 4)
+    assert torch.equal(src.cpu(), exp_src)
+    assert torch.equal(back.cpu(), torch.cat([b.stone_slot, gslot]))
+    ops.raise_on_device_error(device)
+
+
 def _hex_graphs(n_graphs, seed=0):
     from mantisnet import builder as B
     from mantisnet import synthetic as S
