@@ -11,11 +11,11 @@
 //   violation ORs 1 into *bad.  One pass, no host read: the forward reads the
 //   word together with the error flag once at its end.
 // * incidence order (stone-major view of the window-major incidence list,
-//   stable): a counting sort.  Counts per stone (atomics), one workgroup's
-//   exclusive scan into the CSR pointer, a scatter of entry indices into
-//   their stone's slots (atomics: unordered), then each stone's slots sorted
-//   by entry index — a stone lies in at most 18 windows, so the per-stone
-//   insertion sort is short.  The result is the stable order whatever order
+//   stable): a counting sort.  Counts per stone (atomics), their prefix sums
+//   (the CSR pointer, a library scan between the two launches), a scatter of
+//   entry indices into their stone's run (atomic decrements: unordered), then
+//   each stone's run sorted by entry index in registers — a stone lies in at
+//   most 18 windows.  The result is the stable order whatever order
 //   the atomics took, and the window and class of every entry are gathered
 //   in the same pass.
 // * radius_class_kernel: orbit + 48 (own + 2 on_axis), one pass.
@@ -26,8 +26,6 @@
 
 namespace mantis {
 namespace {
-
-constexpr int kScanThreads = 1024;
 
 __device__ __forceinline__ int64_t floordiv(int64_t a, int64_t b) {
   const int64_t q = a / b;
@@ -75,41 +73,17 @@ __global__ void count_kernel(const int64_t* __restrict__ key, int64_t n, int64_t
   }
 }
 
-// ptr[0] = 0, ptr[k + 1] = counts[0] + ... + counts[k]; cursor[k] = ptr[k].
-// One workgroup: thread t sums a contiguous chunk, the chunk totals are
-// scanned in LDS, then each thread writes its chunk's prefix sums.
-__global__ void __launch_bounds__(kScanThreads)
-scan_kernel(const int32_t* __restrict__ counts, int64_t n, int64_t* __restrict__ ptr, int64_t* __restrict__ cursor) {
-  __shared__ int64_t part[kScanThreads];
-  const int64_t per = (n + kScanThreads - 1) / kScanThreads;
-  const int64_t b = int64_t(threadIdx.x) * per;
-  const int64_t e = b + per < n ? b + per : n;
-  int64_t s = 0;
-  for (int64_t i = b; i < e; ++i) s += counts[i];
-  part[threadIdx.x] = s;
-  __syncthreads();
-  for (int off = 1; off < kScanThreads; off <<= 1) {  // inclusive Hillis-Steele scan
-    const int64_t add = threadIdx.x >= off ? part[threadIdx.x - off] : 0;
-    __syncthreads();
-    part[threadIdx.x] += add;
-    __syncthreads();
-  }
-  int64_t run = threadIdx.x ? part[threadIdx.x - 1] : 0;
-  if (threadIdx.x == 0) ptr[0] = 0;
-  for (int64_t i = b; i < e; ++i) {
-    cursor[i] = run;
-    run += counts[i];
-    ptr[i + 1] = run;
+// entry i into its key's run: slot ptr[k] + (counts[k] after the decrement),
+// so every run is filled (in no particular order) and counts end at zero
+__global__ void scatter_kernel(const int64_t* __restrict__ key, int64_t n, int64_t n_keys, const int64_t* __restrict__ ptr,
+                               int32_t* __restrict__ counts, int64_t* __restrict__ perm) {
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t k = key[i];
+    if (k >= 0 && k < n_keys) perm[ptr[k] + int64_t(atomicSub(&counts[k], 1)) - 1] = i;
   }
 }
 
-__global__ void scatter_kernel(const int64_t* __restrict__ key, int64_t n, int64_t n_keys,
-                               unsigned long long* __restrict__ cursor, int64_t* __restrict__ perm) {
-  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x) {
-    const int64_t k = key[i];
-    if (k >= 0 && k < n_keys) perm[int64_t(atomicAdd(&cursor[k], 1ull))] = i;
-  }
-}
+constexpr int kRegRun = 32;  // runs up to this length are sorted in registers
 
 // each key's run of perm sorted ascending (the stable order), then the
 // entries' second and third columns gathered in that order
@@ -117,20 +91,66 @@ __global__ void segment_sort_gather_kernel(const int64_t* __restrict__ ptr, int6
                                            const int64_t* __restrict__ col_a, const int64_t* __restrict__ col_b,
                                            int64_t* __restrict__ out_a, int64_t* __restrict__ out_b) {
   for (int64_t k = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; k < n_keys; k += int64_t(gridDim.x) * blockDim.x) {
-    const int64_t b = ptr[k], e = ptr[k + 1];
-    for (int64_t i = b + 1; i < e; ++i) {  // insertion sort (runs are short)
-      const int64_t v = perm[i];
+    const int64_t b = ptr[k], e = ptr[k + 1], len = e - b;
+    if (len <= kRegRun) {
+      int64_t v[kRegRun];
+#pragma unroll
+      for (int i = 0; i < kRegRun; ++i) v[i] = i < len ? perm[b + i] : INT64_MAX;
+      // odd-even transposition sort over the fixed register array
+#pragma unroll
+      for (int r = 0; r < kRegRun; ++r)
+#pragma unroll
+        for (int i = r & 1; i + 1 < kRegRun; i += 2) {
+          const int64_t lo = v[i] < v[i + 1] ? v[i] : v[i + 1], hi = v[i] < v[i + 1] ? v[i + 1] : v[i];
+          v[i] = lo;
+          v[i + 1] = hi;
+        }
+#pragma unroll
+      for (int i = 0; i < kRegRun; ++i)
+        if (i < len) {
+          out_a[b + i] = col_a[v[i]];
+          out_b[b + i] = col_b[v[i]];
+        }
+      continue;
+    }
+    for (int64_t i = b + 1; i < e; ++i) {  // long runs (not produced by valid batches): insertion sort in place
+      const int64_t x = perm[i];
       int64_t j = i - 1;
-      while (j >= b && perm[j] > v) {
+      while (j >= b && perm[j] > x) {
         perm[j + 1] = perm[j];
         --j;
       }
-      perm[j + 1] = v;
+      perm[j + 1] = x;
     }
     for (int64_t i = b; i < e; ++i) {
       const int64_t src = perm[i];
       out_a[i] = col_a[src];
       out_b[i] = col_b[src];
+    }
+  }
+}
+
+// the covered cells (cell_ptr[i + 1] > cell_ptr[i]) in ascending order,
+// compacted: cov_rows[rank[i] - 1] = i (rank the inclusive prefix count of
+// covered cells; ranks past n_cov are dropped), and every window-major
+// decoder entry's cell as a covered rank: wcell_cov[e] = rank[wcell[e]] - 1
+__global__ void covered_rows_kernel(const int64_t* __restrict__ cell_ptr, const int64_t* __restrict__ rank, int64_t n_c,
+                                    int64_t n_cov, int64_t* __restrict__ cov_rows, const int64_t* __restrict__ wcell,
+                                    int64_t n_e, int64_t* __restrict__ wcell_cov, int32_t* flag) {
+  const int64_t n = n_c > n_e ? n_c : n_e;
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x) {
+    if (i < n_c && cell_ptr[i + 1] > cell_ptr[i]) {
+      const int64_t r = rank[i] - 1;
+      if (r >= 0 && r < n_cov) cov_rows[r] = i;
+    }
+    if (i < n_e) {
+      const int64_t c = wcell[i];
+      if (c >= 0 && c < n_c) {
+        wcell_cov[i] = rank[c] - 1;
+      } else {
+        wcell_cov[i] = -1;
+        raise_flag(flag, MANTIS_FLAG_INDEX);
+      }
     }
   }
 }
@@ -197,33 +217,44 @@ int32_t mantis_plan_check(const int64_t* dec_cell, const int64_t* dec_window, in
 
 int64_t mantis_stable_key_order_workspace(int64_t n_entries, int64_t n_keys) {
   if (n_entries < 0 || n_keys < 0) return -1;
-  // counts (int32, padded to 8 bytes), cursors (int64), permutation (int64)
-  return (4 * n_keys + 7) / 8 * 8 + 8 * n_keys + 8 * n_entries;
+  // counts (int32, padded to 8 bytes), then the permutation (int64)
+  return (4 * n_keys + 7) / 8 * 8 + 8 * n_entries;
+}
+
+int32_t mantis_stable_key_count(const int64_t* key, int64_t n_entries, int64_t n_keys, void* workspace,
+                                int32_t* err_flag, void* stream) {
+  if (n_entries < 0 || n_keys < 0 || (n_entries && !key) || ((n_keys || n_entries) && !workspace)) return MANTIS_E_ARG;
+  hipStream_t st = as_stream(stream);
+  int32_t* counts = static_cast<int32_t*>(workspace);
+  if (n_keys) fill_i32_kernel<<<grid_for(n_keys), 256, 0, st>>>(counts, n_keys, 0);
+  if (n_entries) count_kernel<<<grid_for(n_entries), 256, 0, st>>>(key, n_entries, n_keys, counts, err_flag);
+  return launched();
 }
 
 int32_t mantis_stable_key_order(const int64_t* key, const int64_t* col_a, const int64_t* col_b, int64_t n_entries,
-                                int64_t n_keys, int64_t* ptr, int64_t* out_a, int64_t* out_b, void* workspace,
-                                int32_t* err_flag, void* stream) {
+                                int64_t n_keys, const int64_t* ptr, int64_t* out_a, int64_t* out_b, void* workspace,
+                                void* stream) {
   if (!ptr || n_entries < 0 || n_keys < 0) return MANTIS_E_ARG;
-  if (n_entries && (!key || !col_a || !col_b || !out_a || !out_b || !workspace)) return MANTIS_E_ARG;
-  if (n_keys && !workspace) return MANTIS_E_ARG;
+  if (n_entries == 0 || n_keys == 0) return MANTIS_OK;
+  if (!key || !col_a || !col_b || !out_a || !out_b || !workspace) return MANTIS_E_ARG;
   hipStream_t st = as_stream(stream);
-  if (n_keys == 0) {
-    fill_i32_kernel<<<1, 64, 0, st>>>(reinterpret_cast<int32_t*>(ptr), 2, 0);  // ptr[0] = 0 (int64 zero)
-    if (n_entries) count_kernel<<<grid_for(n_entries), 256, 0, st>>>(key, n_entries, 0, nullptr, err_flag);
-    return launched();
-  }
   int32_t* counts = static_cast<int32_t*>(workspace);
-  int64_t* cursor = reinterpret_cast<int64_t*>(static_cast<char*>(workspace) + ((4 * n_keys + 7) / 8) * 8);
-  int64_t* perm = cursor + n_keys;
-  fill_i32_kernel<<<grid_for(n_keys), 256, 0, st>>>(counts, n_keys, 0);
-  if (n_entries) count_kernel<<<grid_for(n_entries), 256, 0, st>>>(key, n_entries, n_keys, counts, err_flag);
-  scan_kernel<<<1, kScanThreads, 0, st>>>(counts, n_keys, ptr, cursor);
-  if (n_entries) {
-    scatter_kernel<<<grid_for(n_entries), 256, 0, st>>>(key, n_entries, n_keys,
-                                                         reinterpret_cast<unsigned long long*>(cursor), perm);
-    segment_sort_gather_kernel<<<grid_for(n_keys), 256, 0, st>>>(ptr, n_keys, perm, col_a, col_b, out_a, out_b);
-  }
+  int64_t* perm = reinterpret_cast<int64_t*>(static_cast<char*>(workspace) + (4 * n_keys + 7) / 8 * 8);
+  scatter_kernel<<<grid_for(n_entries), 256, 0, st>>>(key, n_entries, n_keys, ptr, counts, perm);
+  segment_sort_gather_kernel<<<grid_for(n_keys), 256, 0, st>>>(ptr, n_keys, perm, col_a, col_b, out_a, out_b);
+  return launched();
+}
+
+int32_t mantis_covered_rows(const int64_t* cell_ptr, const int64_t* rank, int64_t n_c, int64_t n_cov,
+                            int64_t* cov_rows, const int64_t* wcell, int64_t n_e, int64_t* wcell_cov, int32_t* err_flag,
+                            void* stream) {
+  if (n_c < 0 || n_e < 0 || n_cov < 0 || !cell_ptr || (n_c && !rank) || (n_cov && !cov_rows) ||
+      (n_e && (!wcell || !wcell_cov)))
+    return MANTIS_E_ARG;
+  const int64_t n = n_c > n_e ? n_c : n_e;
+  if (n == 0) return MANTIS_OK;
+  covered_rows_kernel<<<grid_for(n), 256, 0, as_stream(stream)>>>(cell_ptr, rank, n_c, n_cov, cov_rows, wcell, n_e,
+                                                                  wcell_cov, err_flag);
   return launched();
 }
 

@@ -26,7 +26,9 @@ SIGNATURES = {
     "mantis_hip_version": ([], i32),
     "mantis_plan_check": ([vp, vp, i64, vp, vp, i64, vp, i64, i64, vp, vp], i32),
     "mantis_stable_key_order_workspace": ([i64, i64], i64),
-    "mantis_stable_key_order": ([vp, vp, vp, i64, i64, vp, vp, vp, vp, vp, vp], i32),
+    "mantis_stable_key_count": ([vp, i64, i64, vp, vp, vp], i32),
+    "mantis_stable_key_order": ([vp, vp, vp, i64, i64, vp, vp, vp, vp, vp], i32),
+    "mantis_covered_rows": ([vp, vp, i64, i64, vp, vp, i64, vp, vp, vp], i32),
     "mantis_radius_class": ([vp, vp, vp, i64, vp, vp], i32),
     "mantis_attention_slots": ([vp, i64, i64, i64, vp, vp, vp, vp], i32),
     "mantis_gather_rows": ([vp, i32, i64, i64, vp, vp, i64, i64, vp, i64, vp, vp], i32),

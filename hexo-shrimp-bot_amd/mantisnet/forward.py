@@ -259,7 +259,6 @@ class Plan:
     window_pos: Tensor
     layout_offsets: Tensor
     layout_order: Tensor
-    covered_mask: Tensor  # (N_c,) bool
     cov_rows: Tensor | None  # the covered cells (with decoder entries), ascending (cell-node configurations)
     edge_wcell_cov: Tensor | None  # edge_wcell as indices into cov_rows
     cell_ptr: Tensor  # cell-major decoder CSR over all legal cells
@@ -347,7 +346,6 @@ def make_plan(model, b: Batch, speculative: bool = False) -> Plan:
         edge_window, edge_class, edge_cell = b.dec_window[corder], b.dec_class[corder], b.dec_cell[corder]
         worder = _stable_order(edge_window)
     cell_ptr = ops.runs_to_ptr(edge_cell.contiguous(), n_c)
-    covered = cell_ptr[1:] > cell_ptr[:-1]
     win_ptr = ops.runs_to_ptr(edge_window[worder].contiguous(), n_w)
     edge_wcell = edge_cell[worder]
     # only the covered cells (those with decoder entries) are read by the
@@ -357,19 +355,15 @@ def make_plan(model, b: Batch, speculative: bool = False) -> Plan:
     cov_rows = edge_wcell_cov = None
     if cfg.cell_nodes and getattr(b, "relay_cell_ptr", None) is not None:
         n_cov = b.relay_cell_ptr.shape[0] - 1
-        rank = torch.cumsum(covered, 0) - 1
         # (a batch whose relay views disagree with its decoder entries leaves
-        # ranks past n_cov: they go to the spare slot, and the entries that
-        # name them are flagged by the sub-stage)
-        slots = torch.where(covered & (rank < n_cov), rank, n_cov)
-        cov_rows = torch.empty(n_cov + 1, dtype=torch.int64, device=dev).scatter_(
-            0, slots, torch.arange(n_c, device=dev))[:n_cov]
-        edge_wcell_cov = rank.index_select(0, edge_wcell)
+        # covered cells past n_cov out of the list; the entries that name them
+        # are flagged by the sub-stage)
+        cov_rows, edge_wcell_cov = ops.covered_rows(cell_ptr, n_cov, edge_wcell)
     # radius edge tables (cell_nodes.py:23-94, model.py:843-859)
     radius_ptr = radius_src = radius_class = cell_order = None
     if cfg.cell_nodes:
         if cfg.cell_node_scope == "uncovered":
-            keep = ~covered[dst]
+            keep = ~(cell_ptr[1:] > cell_ptr[:-1])[dst]
             src, dst, classes = src[keep], dst[keep], classes[keep]
         if canonical:
             radius_src, radius_dst, radius_class = src, dst, classes
@@ -391,7 +385,7 @@ def make_plan(model, b: Batch, speculative: bool = False) -> Plan:
         run_window=run_window, run_class=run_class,
         inc_stone_ptr=inc_stone_ptr,
         window_pos=window_pos, layout_offsets=offsets, layout_order=lorder,
-        covered_mask=covered, cov_rows=cov_rows, edge_wcell_cov=edge_wcell_cov, cell_ptr=cell_ptr,
+        cov_rows=cov_rows, edge_wcell_cov=edge_wcell_cov, cell_ptr=cell_ptr,
         edge_window=edge_window, edge_class=edge_class,
         win_ptr=win_ptr, edge_wcell=edge_wcell, edge_wclass=edge_class[worder],
         cell_order=cell_order,

@@ -258,11 +258,33 @@ def stable_key_order(key: Tensor, col_a: Tensor, col_b: Tensor, n_keys: int) -> 
     out_a = torch.empty(n, dtype=torch.int64, device=dev)
     out_b = torch.empty(n, dtype=torch.int64, device=dev)
     ws = torch.empty(max(int(_lib().mantis_stable_key_order_workspace(n, n_keys)), 8), dtype=torch.uint8, device=dev)
-    _launch("stable_key_order", 8.0 * (5 * n + 3 * n_keys), 0.0, lambda: _check(
-        _lib().mantis_stable_key_order(_ptr(key), _ptr(col_a), _ptr(col_b), n, n_keys, _ptr(ptr), _ptr(out_a),
-                                       _ptr(out_b), _ptr(ws), _ptr(error_flag(dev)), _stream()),
-        "stable_key_order"))
+    counts = ws[:4 * n_keys].view(torch.int32)
+    _launch("stable_key_order", 8.0 * (5 * n + 3 * n_keys), 0.0, lambda: (
+        _check(_lib().mantis_stable_key_count(_ptr(key), n, n_keys, _ptr(ws), _ptr(error_flag(dev)), _stream()),
+               "stable_key_order"),
+        ptr[:1].zero_(),
+        torch.cumsum(counts, 0, out=ptr[1:]),
+        _check(_lib().mantis_stable_key_order(_ptr(key), _ptr(col_a), _ptr(col_b), n, n_keys, _ptr(ptr), _ptr(out_a),
+                                              _ptr(out_b), _ptr(ws), _stream()), "stable_key_order")))
     return ptr, out_a, out_b
+
+
+def covered_rows(cell_ptr: Tensor, n_cov: int, wcell: Tensor) -> tuple[Tensor, Tensor]:
+    """(cov_rows, wcell_cov): the covered cells (decoder entries present) in
+    ascending order, at most n_cov of them, and each window-major entry's
+    cell as its rank among them (-1 past the compact list)."""
+    dev = _on_gpu(cell_ptr, wcell)
+    cell_ptr, wcell = _i64(cell_ptr, "cell_ptr"), _i64(wcell, "wcell")
+    n_c = cell_ptr.numel() - 1
+    rank = torch.cumsum(cell_ptr[1:] > cell_ptr[:-1], 0)
+    cov_rows = torch.empty(n_cov, dtype=torch.int64, device=dev)
+    wcell_cov = torch.empty_like(wcell)
+    if n_c or wcell.numel():
+        _launch("covered_rows", 8.0 * (3 * n_c + n_cov + 3 * wcell.numel()), 0.0, lambda: _check(
+            _lib().mantis_covered_rows(_ptr(cell_ptr), _ptr(rank), n_c, n_cov, _ptr(cov_rows), _ptr(wcell),
+                                       wcell.numel(), _ptr(wcell_cov), _ptr(error_flag(dev)), _stream()),
+            "covered_rows"))
+    return cov_rows, wcell_cov
 
 
 def radius_class(orbit: Tensor, own: Tensor, on_axis: Tensor) -> Tensor:

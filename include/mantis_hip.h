@@ -78,20 +78,39 @@ int32_t mantis_plan_check(const int64_t* dec_cell, const int64_t* dec_window, in
                           void* stream);
 
 /*
- * Stable key-major view of an entry list with small key runs (the stone-major
+ * Stable key-major view of an entry list with short key runs (the stone-major
  * incidence view of incidence_plan, message_passing.py:495-517, as
- * torch.argsort(key, stable=True) + gathers + searchsorted): ptr (n_keys + 1)
- * the CSR of the keys, out_a / out_b the entries' col_a / col_b in the stable
- * key-major order.  A counting sort: per-key counts, one scan, an unordered
- * scatter, then every key's run sorted by entry index (insertion sort: runs
- * are short, at most 18 for the incidence).  workspace: at least
- * mantis_stable_key_order_workspace(n_entries, n_keys) bytes, 8-byte aligned.
- * Keys outside [0, n_keys) set MANTIS_FLAG_INDEX and are dropped.
+ * torch.argsort(key, stable=True) + gathers + searchsorted), as a counting
+ * sort in two calls around an inclusive prefix sum the caller computes:
+ *   mantis_stable_key_count: counts[k] (int32, at the start of `workspace`)
+ *     = number of entries with key k; keys outside [0, n_keys) set
+ *     MANTIS_FLAG_INDEX and are dropped;
+ *   the caller: ptr[0] = 0, ptr[k + 1] = counts[0] + ... + counts[k] (int64);
+ *   mantis_stable_key_order: out_a / out_b = col_a / col_b in the stable
+ *     key-major order (an unordered scatter into each key's run, then every
+ *     run sorted by entry index; runs up to 32 in registers).
+ * workspace: mantis_stable_key_order_workspace(n_entries, n_keys) bytes,
+ * 8-byte aligned, the same for both calls.
  */
 int64_t mantis_stable_key_order_workspace(int64_t n_entries, int64_t n_keys);
+int32_t mantis_stable_key_count(const int64_t* key, int64_t n_entries, int64_t n_keys, void* workspace,
+                                int32_t* err_flag, void* stream);
 int32_t mantis_stable_key_order(const int64_t* key, const int64_t* col_a, const int64_t* col_b,
-                                int64_t n_entries, int64_t n_keys, int64_t* ptr, int64_t* out_a,
-                                int64_t* out_b, void* workspace, int32_t* err_flag, void* stream);
+                                int64_t n_entries, int64_t n_keys, const int64_t* ptr, int64_t* out_a,
+                                int64_t* out_b, void* workspace, void* stream);
+
+/*
+ * Covered-cell compaction (the cells with decoder entries, whose k/v rows
+ * the windows read): with rank (n_c) the inclusive prefix count of covered
+ * cells (cell_ptr[i + 1] > cell_ptr[i]), cov_rows[rank[i] - 1] = i for the
+ * covered cells of rank <= n_cov, and wcell_cov[e] = rank[wcell[e]] - 1 for
+ * the window-major decoder entries (wcell outside [0, n_c): -1 and
+ * MANTIS_FLAG_INDEX).  The covered-only k/v projection of the cell stage,
+ * no counterpart in the reference (which projects every cell).
+ */
+int32_t mantis_covered_rows(const int64_t* cell_ptr, const int64_t* rank, int64_t n_c, int64_t n_cov,
+                            int64_t* cov_rows, const int64_t* wcell, int64_t n_e, int64_t* wcell_cov,
+                            int32_t* err_flag, void* stream);
 
 /*
  * Radius edge classes: out[e] = orbit[e] + 48 (own[e] + 2 on_axis[e])

@@ -341,6 +341,20 @@ def test_stable_key_order_matches_stable_argsort(device):
         ops.raise_on_device_error(device)
 
 
+def test_covered_rows_matches_the_tensor_formulation(device):
+    gen = _g(41)
+    counts = torch.randint(0, 3, (500,), generator=gen)
+    cell_ptr = torch.cat([torch.zeros(1, dtype=torch.long), counts.cumsum(0)])
+    wcell = torch.randint(0, 500, (900,), generator=gen)
+    covered = counts > 0
+    n_cov = int(covered.sum())
+    cov_rows, wcov = ops.covered_rows(cell_ptr.to(device), n_cov, wcell.to(device))
+    rank = torch.cumsum(covered, 0) - 1
+    assert torch.equal(cov_rows.cpu(), torch.nonzero(covered)[:, 0])
+    assert torch.equal(wcov.cpu(), rank[wcell])
+    ops.raise_on_device_error(device)
+
+
 def test_radius_class_and_attention_slots(device):
     b = _plan_batch()
     got = ops.radius_class(b.radius_orbit.to(device), b.radius_own.to(device), b.radius_on_axis.to(device)).cpu()
