@@ -103,11 +103,15 @@ stone_schedule_kernel(const int32_t* __restrict__ seq_lens, int64_t n_pos, int h
                                         static_cast<unsigned long long>(heads * live_qt)));
     const int64_t d = int64_t(atomicAdd(reinterpret_cast<unsigned long long*>(&dead_cursor),
                                         static_cast<unsigned long long>(heads * (n_qt - live_qt))));
+    // tile-major within the position: the tiles of one head sit `heads` slots
+    // apart, so with 8 heads they run on one XCD (dispatch deals consecutive
+    // workgroups round-robin over the 8 XCDs) and share its L2 copy of the
+    // head's keys and values
     for (int64_t a = 0; a < heads; ++a) {
       const int64_t base = (p * heads + a) * n_qt;
-      for (int64_t qt = 0; qt < live_qt; ++qt) order[s + a * live_qt + qt] = int32_t(base + qt);
+      for (int64_t qt = 0; qt < live_qt; ++qt) order[s + qt * heads + a] = int32_t(base + qt);
       for (int64_t qt = live_qt; qt < n_qt; ++qt)
-        order[d + a * (n_qt - live_qt) + (qt - live_qt)] = int32_t(base + qt);
+        order[d + (qt - live_qt) * heads + a] = int32_t(base + qt);
     }
   }
 }
