@@ -243,7 +243,9 @@ def main() -> int:
         ops.raise_on_device_error(dev)
         _log(f"warm-up done ({args.warmup} steps)")
         traced = ("attention_substage", "cell_attention", "cell_heads", "fused_linear", "stone_attention", "run_reduce",
-                  "runs_to_ptr", "latent_", "row_encode", "layer_norm", "value_read", "compose_q")
+                  "runs_to_ptr", "latent_", "row_encode", "layer_norm", "value_read", "compose_q", "gather_rows",
+                  "plan_check", "stable_key_order", "radius_class", "attention_slots", "covered_rows",
+                  "segment_order")
         per_step = []
         with ops.trace(*traced) as tr:
             torch.cuda.synchronize()
