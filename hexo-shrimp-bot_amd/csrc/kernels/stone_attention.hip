@@ -322,10 +322,109 @@ stone_attention_kernel(const uint16_t* __restrict__ q, int64_t qsp, int64_t qsa,
   }
 }
 
+
+// The last block's latent read (model.py:647-664): for each position, its 4
+// latent rows' queries (4 heads x 32) over every valid key of the padded
+// sequence, in fp32: scores q.k / sqrt(32), masked by attn_valid (a dead key
+// gets -inf), softmax, read = sum p v.  q, k and v are 16-bit columns
+// [0, 128), [128, 256) and [256, 384) of the projected rows (row p * T + t;
+// head a at 32 a).  One workgroup per position: 16 lanes per (head, query)
+// row, each over every 16th key, the scores of the position staged in LDS.
+constexpr int kLatentThreads = 256;
+
+template <bool kHalf>
+__global__ void __launch_bounds__(kLatentThreads)
+latent_attend_kernel(const uint16_t* __restrict__ qkv, int64_t ld, const uint8_t* __restrict__ valid, int64_t T,
+                     float* __restrict__ out) {
+  extern __shared__ float sc[];  // [16][T]
+  const int64_t p = blockIdx.x;
+  const int r = threadIdx.x / 16, s = threadIdx.x % 16;  // row r = 4 * head + query
+  const int a = r / 4, j = r % 4;
+  auto widen = [](uint16_t h) { return kHalf ? float(__builtin_bit_cast(_Float16, h)) : bf2f(h); };
+  const uint16_t* base = qkv + p * T * ld;
+  float q[32];
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const uint4 u = *reinterpret_cast<const uint4*>(base + j * ld + 32 * a + 8 * w);
+    const uint32_t h[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      q[8 * w + 2 * i] = widen(uint16_t(h[i] & 0xffffu));
+      q[8 * w + 2 * i + 1] = widen(uint16_t(h[i] >> 16));
+    }
+  }
+  const float scale = 0.17677669529663687f;  // 1 / sqrt(32)
+  float m = -INFINITY;
+  for (int64_t t = s; t < T; t += 16) {
+    float d = -INFINITY;
+    if (valid[p * T + t]) {
+      d = 0.f;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const uint4 u = *reinterpret_cast<const uint4*>(base + t * ld + 128 + 32 * a + 8 * w);
+        const uint32_t h[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          d = fmaf(q[8 * w + 2 * i], widen(uint16_t(h[i] & 0xffffu)), d);
+          d = fmaf(q[8 * w + 2 * i + 1], widen(uint16_t(h[i] >> 16)), d);
+        }
+      }
+      d *= scale;
+    }
+    sc[r * T + t] = d;
+    m = fmaxf(m, d);
+  }
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+  float l = 0.f;
+  for (int64_t t = s; t < T; t += 16) {
+    const float e = sc[r * T + t] == -INFINITY ? 0.f : expf(sc[r * T + t] - m);
+    sc[r * T + t] = e;
+    l += e;
+  }
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) l += __shfl_xor(l, o);
+  __syncthreads();
+  // dims 2s, 2s + 1 of this row's head
+  float acc0 = 0.f, acc1 = 0.f;
+  for (int64_t t = 0; t < T; ++t) {
+    const float e = sc[r * T + t];
+    const uint32_t h = *reinterpret_cast<const uint32_t*>(base + t * ld + 256 + 32 * a + 2 * s);
+    acc0 = fmaf(e, widen(uint16_t(h & 0xffffu)), acc0);
+    acc1 = fmaf(e, widen(uint16_t(h >> 16)), acc1);
+  }
+  const float inv = 1.f / l;  // a row with no valid key reads NaN, as the reference's softmax does
+  float* o = out + (p * 4 + j) * 128 + 32 * a + 2 * s;
+  o[0] = acc0 * inv;
+  o[1] = acc1 * inv;
+}
+
 }  // namespace
 }  // namespace mantis
 
 using namespace mantis;
+
+extern "C" int32_t mantis_latent_attend(const void* qkv, int32_t dtype, int64_t ld, const uint8_t* attn_valid,
+                                        int64_t n_pos, int64_t t, float* out, void* stream) {
+  if (n_pos == 0) return MANTIS_OK;
+  if (!qkv || !attn_valid || !out || n_pos < 0 || t < 4 || t > 2048 || ld < 384 || ld % 8) return MANTIS_E_ARG;
+  if (dtype != MANTIS_F16 && dtype != MANTIS_BF16) return MANTIS_E_ARG;
+  if (!aligned16(qkv) || n_pos > 2147483647LL) return MANTIS_E_ARG;
+  const size_t lds = size_t(16) * size_t(t) * sizeof(float);
+  auto kernel = dtype == MANTIS_F16 ? latent_attend_kernel<true> : latent_attend_kernel<false>;
+  static bool configured = false;
+  if (!configured) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(latent_attend_kernel<true>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, 16 * 2048 * 4) != hipSuccess ||
+        hipFuncSetAttribute(reinterpret_cast<const void*>(latent_attend_kernel<false>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, 16 * 2048 * 4) != hipSuccess)
+      return MANTIS_E_LAUNCH;
+    configured = true;
+  }
+  kernel<<<unsigned(n_pos), kLatentThreads, lds, as_stream(stream)>>>(static_cast<const uint16_t*>(qkv), ld,
+                                                                      attn_valid, t, out);
+  return launched();
+}
 
 extern "C" int64_t mantis_stone_attention_schedule_len(int64_t n_pos, int32_t heads, int64_t t) {
   if (n_pos <= 0 || heads <= 0 || t <= 0 || (t + kKChunk - 1) / kKChunk >= kMaxChunkBuckets) return 0;

@@ -42,7 +42,6 @@ heads of 32, 4 value queries.  Other knob combinations raise
 
 from __future__ import annotations
 
-import math
 from dataclasses import dataclass
 
 import torch
@@ -520,12 +519,10 @@ def _block(W, P, i: int, plan: Plan, b: Batch, sg, w, c, sw_all, update_stones: 
                             schedule=plan.stone_schedule)
         _resid(W, pb + "attn_o", rows.view(p * max_t, 128), sg, x_rows=plan.attn_back)
     else:
-        # last block: only the four latent rows are read downstream (fp32 read)
-        q = view(0)[:, :, :GLOBAL_ROWS].float()
-        sc = torch.matmul(q, view(1).float().transpose(-1, -2)) / math.sqrt(32)
-        sc = sc.masked_fill(~b.attn_valid[:, None, None, :], -torch.inf)
-        read = torch.matmul(sc.softmax(-1), view(2).float()).transpose(1, 2).reshape(p * GLOBAL_ROWS, 128)
-        _resid(W, pb + "attn_o", read.contiguous(), g2)
+        # last block: only the four latent rows are read downstream (fp32 read,
+        # masked by attn_valid, in one kernel)
+        read = ops.latent_attend(qkv, b.attn_valid, p, max_t)
+        _resid(W, pb + "attn_o", read, g2)
     # §5.4 latent cycle
     _latent_cycle(W, P, pb, plan, w, g2, wp[:, 128:384], wp[:, 384:])
     # FFN over [stones; latents] (latents only in the last block)

@@ -1125,6 +1125,28 @@ def _strides(t: Tensor):
     return (ctypes.c_int64 * 4)(*t.stride())
 
 
+def latent_attend(qkv: Tensor, attn_valid: Tensor, n_pos: int, t: int) -> Tensor:
+    """(4 n_pos, 128) fp32: each position's 4 latent queries (q columns
+    0..127 of its first 4 rows) over its valid keys and values (columns
+    128..383 of all t rows), fp32 scores, softmax and read."""
+    dev = _on_gpu(qkv, attn_valid)
+    if qkv.ndim != 2 or qkv.shape[0] != n_pos * t or qkv.shape[1] < 384 or qkv.stride(1) != 1:
+        raise ValueError("qkv must be (n_pos * t, >= 384) rows")
+    if qkv.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("qkv must be fp16 or bf16")
+    if attn_valid.shape != (n_pos, t) or attn_valid.dtype != torch.bool:
+        raise ValueError("attn_valid must be (n_pos, t) bool")
+    valid = attn_valid.contiguous()
+    out = torch.empty((4 * n_pos, 128), dtype=torch.float32, device=dev)
+    if n_pos:
+        nbytes = n_pos * (t * 256 * qkv.element_size() + 4 * 128 * qkv.element_size() + t + 4 * 128 * 4)
+        flops = n_pos * 16 * t * 32 * 2 * 2
+        _launch("latent_attend", nbytes, flops, lambda: _check(
+            _lib().mantis_latent_attend(_ptr(qkv), _dt(qkv), qkv.stride(0), _ptr(valid), n_pos, t, _ptr(out),
+                                        _stream()), "latent_attend"))
+    return out
+
+
 def stone_attention_schedule(seq_lens: Tensor, heads: int, t: int) -> Tensor | None:
     """The longest-first work order of stone_attention over these lengths
     (int32 on the device), or None when every position fits one 128-query

@@ -506,6 +506,19 @@ int32_t mantis_stone_attention_schedule(const int32_t* seq_lens, int64_t n_pos, 
                                         int64_t t, int32_t* schedule, void* stream);
 
 /*
+ * The last block's latent read (python/mantisnet/mantisnet/model.py:647-664):
+ * for each position p, head a and latent query j < 4,
+ *   out[4 p + j, 32 a + d] = sum_t softmax_t(q_j . k_t / sqrt(32)) v_t[d]
+ * over the keys t < T with attn_valid[p, t] (others weigh 0), all in fp32.
+ * qkv: (n_pos * T, ld) 16-bit rows (`dtype` MANTIS_F16 or MANTIS_BF16) with q,
+ * k, v in columns [0,128), [128,256), [256,384), row p * T + t; attn_valid
+ * (n_pos, T) bytes 0/1; out (4 n_pos, 128) fp32.  4 <= T <= 2048.  A row
+ * with no valid key reads NaN, as the reference's softmax does.
+ */
+int32_t mantis_latent_attend(const void* qkv, int32_t dtype, int64_t ld, const uint8_t* attn_valid,
+                             int64_t n_pos, int64_t t, float* out, void* stream);
+
+/*
  * Entries of a mantis_stone_attention schedule (n_pos * heads * ceil(t / 128)),
  * or 0 when t is too long to be scheduled (t >= 64 * 1023: pass NULL to the
  * attention).  Host-side arithmetic only.

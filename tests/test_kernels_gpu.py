@@ -216,6 +216,26 @@ def test_stone_attention_late_rescale_and_empty_position(device, dtype):
     torch.testing.assert_close(lse.cpu(), exp_lse, rtol=1e-3, atol=1e-3)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, BF])
+def test_latent_attend_matches_the_masked_fp32_read(device, dtype):
+    # the last block's four-query read (model.py:647-664): fp32 scores over
+    # the valid keys (any mask, not only prefixes), softmax, fp32 read
+    gen = _g(51)
+    p, t = 7, 130
+    qkv = (torch.randn(p * t, 384, generator=gen) * 2).to(dtype)
+    valid = torch.rand(p, t, generator=gen) < 0.7
+    valid[:, :4] = True
+    valid[3] = False
+    valid[3, :4] = True  # only the latent rows themselves
+    got = ops.latent_attend(qkv.to(device), valid.to(device), p, t).cpu()
+    view = lambda j: qkv[:, 128 * j:128 * (j + 1)].float().view(p, t, 4, 32).transpose(1, 2)  # noqa: E731
+    q = view(0)[:, :, :4]
+    sc = torch.matmul(q, view(1).transpose(-1, -2)) / math.sqrt(32)
+    sc = sc.masked_fill(~valid[:, None, None, :], -torch.inf)
+    exp = torch.matmul(sc.softmax(-1), view(2)).transpose(1, 2).reshape(p * 4, 128)
+    torch.testing.assert_close(got, exp, rtol=1e-5, atol=1e-5)
+
+
 def test_stone_attention_schedule_does_not_change_the_output(device):
     # the longest-first schedule only reorders independent work items: the
     # scheduled launch equals the unscheduled one bit for bit (C ABI direct)
