@@ -145,7 +145,9 @@ def isolated_message_passing(torch, ops, dev, reps=20):
     n = qr.shape[0]
     gen = torch.Generator(device="cpu").manual_seed(3)
     x = torch.randn(n, 128, generator=gen).to(torch.bfloat16).to(dev)
-    w = (torch.randn(128, 128, generator=gen) / math.sqrt(128)).to(dev)
+    # the layer's weight in the kernel's operand format once, as a model keeps
+    # its parameters: no conversion between the timed launches
+    w = (torch.randn(128, 128, generator=gen) / math.sqrt(128)).to(torch.bfloat16).to(dev)
     bias = (0.02 * torch.randn(128, generator=gen)).to(dev)
     nbr = ops.hex_neighbours(qr, gptr)
     for _ in range(3):
