@@ -267,6 +267,9 @@ def main() -> int:
 
     dom_name, dom = max(kernels.items(), key=lambda kv: kv[1]["total_ms"])
     traffic = _traffic()
+    # the committed counters belong to one workload; other configurations report none
+    if (traffic or {}).get("_workload") != {"config": args.config, "batch": args.batch}:
+        traffic = None
     roofline = {
         "kernel": dom_name,
         "bound": "hbm",
