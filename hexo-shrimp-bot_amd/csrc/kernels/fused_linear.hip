@@ -94,14 +94,19 @@ __device__ __forceinline__ void store4(const Args& a, int64_t row, int f, const 
 
 // LDS layout: W1 (N1 rows), W2 (N1 rows, with a second input), W3 (n3 rows
 // of N1 + 8, with a second stage); n3 is a launch parameter.
-// With kSplit each region holds the hi rows, then the lo rows.
+// With kSplit each region holds the hi rows, then the lo rows.  Then b1
+// (N1 floats) and b3 (n3 floats), zeros where absent: read from LDS, the
+// biases do not add global-load waits to the tile loop (loads and stores
+// share one in-order counter, so such a wait also waits for the next
+// tile's row prefetch and the stores before it).
 template <int N1, bool kStage2, bool kX2, bool kSplit = false>
 struct Smem {
   static constexpr int kParts = kSplit ? 2 : 1;
   static constexpr int w1 = kParts * N1 * kPitch;
   static constexpr int w2 = kX2 ? kParts * N1 * kPitch : 0;
   static constexpr int p3 = N1 + 8;
-  static int bytes(int n3) { return (w1 + w2 + (kStage2 ? kParts * n3 * p3 : 0)) * 2; }
+  __host__ __device__ static int bias_off(int n3) { return w1 + w2 + (kStage2 ? kParts * n3 * p3 : 0); }  // fp16 elements
+  static int bytes(int n3) { return bias_off(n3) * 2 + (N1 + (kStage2 ? n3 : 0)) * 4; }
 };
 
 // Wavefronts sharing one LDS copy of the weights: 8; 16 for the widest
@@ -148,6 +153,11 @@ __global__ void __launch_bounds__((threads_for<N1, kX2, kStage2>())) fused_linea
       *reinterpret_cast<uint4*>(sw3 + r * S::p3 + c) = *reinterpret_cast<const uint4*>(a.w3 + r * N1 + c);
     }
   }
+  float* sb1 = reinterpret_cast<float*>(smem + S::bias_off(a.n3));
+  float* sb3 = sb1 + N1;
+  for (int i = threadIdx.x; i < N1; i += blockDim.x) sb1[i] = a.b1 ? a.b1[i] : 0.f;
+  if constexpr (kStage2)
+    for (int i = threadIdx.x; i < a.n3; i += blockDim.x) sb3[i] = a.b3 ? a.b3[i] : 0.f;
   __syncthreads();
 
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
@@ -260,7 +270,7 @@ __global__ void __launch_bounds__((threads_for<N1, kX2, kStage2>())) fused_linea
       // the tile's four features of this lane: 16 nt + 4 g .. +3, or with
       // kPair the four at pair_feature(nt, g, 0)
       const int f = kPair ? pair_feature(nt, g, 0) : 16 * nt + 4 * g;
-      float4 add = a.b1 ? *reinterpret_cast<const float4*>(a.b1 + f) : make_float4(0.f, 0.f, 0.f, 0.f);
+      float4 add = *reinterpret_cast<const float4*>(sb1 + f);
       if (live && a.add1) {
         const float4 r = *reinterpret_cast<const float4*>(a.add1 + row * a.ld_add1 + f);
         add.x += r.x, add.y += r.y, add.z += r.z, add.w += r.w;
@@ -329,7 +339,7 @@ __global__ void __launch_bounds__((threads_for<N1, kX2, kStage2>())) fused_linea
           }
         if (live) {
           const int f = 16 * ot + 4 * g;
-          const float4 bb = a.b3 ? *reinterpret_cast<const float4*>(a.b3 + f) : make_float4(0.f, 0.f, 0.f, 0.f);
+          const float4 bb = *reinterpret_cast<const float4*>(sb3 + f);
           y[0] += bb.x, y[1] += bb.y, y[2] += bb.z, y[3] += bb.w;
           store4<kMode>(a, row, f, y);
         }
