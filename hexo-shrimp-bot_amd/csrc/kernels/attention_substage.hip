@@ -139,8 +139,16 @@ __global__ void __launch_bounds__(waves_for<kStages>() * 64) attn_substage_kerne
   constexpr int kThreads = kWaves * 64;
   TX* const xs = static_cast<TX*>(a.x);
   __shared__ __attribute__((aligned(16))) _Float16 sw[kStages][2][kK * kPitch];  // [stage][q, o]
+  // the q and o biases: read from LDS, they add no global-load wait to the
+  // tile loop (loads and stores share one in-order counter, so such a wait
+  // would also wait for the look-ahead loads and the stores before it)
+  __shared__ __attribute__((aligned(16))) float sb[kStages][2][kK];
 #pragma unroll
   for (int s = 0; s < kStages; ++s) {
+    for (int i = threadIdx.x; i < kK; i += kThreads) {
+      sb[s][0][i] = a.st[s].bq[i];
+      sb[s][1][i] = a.st[s].bo[i];
+    }
     for (int i = threadIdx.x; i < kK * (kK / 8); i += kThreads) {
       const int r = i / (kK / 8), c = (i % (kK / 8)) * 8;
       *reinterpret_cast<uint4*>(&sw[s][0][r * kPitch + c]) =
@@ -223,6 +231,8 @@ __global__ void __launch_bounds__(waves_for<kStages>() * 64) attn_substage_kerne
       const Stage& S = a.st[s];
       const _Float16* swq = sw[s][0] + lds_off;
       const _Float16* swo = sw[s][1] + lds_off;
+      const float* sbq = sb[s][0];
+      const float* sbo = sb[s][1];
       // entry count of this lane's row, and the wavefront's longest row
       const int cnt = live ? int(hi[s] - lo[s]) : 0;
       int maxc = cnt;
@@ -291,7 +301,7 @@ __global__ void __launch_bounds__(waves_for<kStages>() * 64) attn_substage_kerne
             const f16x8_t wf = *reinterpret_cast<const f16x8_t*>(swq + (16 * nt + l16) * kPitch + 32 * ks + 8 * g);
             d = mfma16x16x32(wf, xb[ks], d);
           }
-          const float4 b = *reinterpret_cast<const float4*>(S.bq + 32 * g + 4 * nt);
+          const float4 b = *reinterpret_cast<const float4*>(sbq + 32 * g + 4 * nt);
           qh[2 * nt] = pack_f16x2(d[0] + b.x, d[1] + b.y);
           qh[2 * nt + 1] = pack_f16x2(d[2] + b.z, d[3] + b.w);
         }
@@ -380,7 +390,7 @@ __global__ void __launch_bounds__(waves_for<kStages>() * 64) attn_substage_kerne
             const f16x8_t wf = *reinterpret_cast<const f16x8_t*>(swo + (16 * nt + l16) * kPitch + 32 * g + 8 * ks);
             d = mfma16x16x32(wf, ab[ks], d);
           }
-          const float4 b = *reinterpret_cast<const float4*>(S.bo + 32 * (nt >> 1) + 8 * g + 4 * (nt & 1));
+          const float4 b = *reinterpret_cast<const float4*>(sbo + 32 * (nt >> 1) + 8 * g + 4 * (nt & 1));
           if constexpr (kPacked) {
             // widen, add in fp32, round once
             uint32_t* w = reinterpret_cast<uint32_t*>(&xh[nt >> 1]) + 2 * (nt & 1);

@@ -76,6 +76,12 @@ __global__ void __launch_bounds__(kThreads) cell_heads_kernel(HeadArgs a) {
   __shared__ __attribute__((aligned(16))) _Float16 sw1[kN1 * kPitch];
   __shared__ __attribute__((aligned(16))) _Float16 sw2[kN1 * kPitch];
   __shared__ __attribute__((aligned(16))) _Float16 sw3[kN3 * kP3];
+  // the biases: read from LDS, they add no global-load wait to the tile loop
+  // (loads and stores share one in-order counter)
+  __shared__ __attribute__((aligned(16))) float sb1[kN1];
+  __shared__ __attribute__((aligned(16))) float sb3[kN3];
+  for (int i = threadIdx.x; i < kN1; i += kThreads) sb1[i] = a.b1[i];
+  for (int i = threadIdx.x; i < kN3; i += kThreads) sb3[i] = a.b3[i];
   for (int i = threadIdx.x; i < kN1 * (kK / 8); i += kThreads) {
     const int r = i / (kK / 8), cc = (i % (kK / 8)) * 8;
     *reinterpret_cast<uint4*>(sw1 + r * kPitch + cc) = *reinterpret_cast<const uint4*>(a.w1 + r * kK + cc);
@@ -271,7 +277,7 @@ __global__ void __launch_bounds__(kThreads) cell_heads_kernel(HeadArgs a) {
           acc = mfma16x16x32(wf2, ab[ks], acc);
         }
         const int f = 16 * nt + 4 * g;
-        float4 add = *reinterpret_cast<const float4*>(a.b1 + f);
+        float4 add = *reinterpret_cast<const float4*>(sb1 + f);
         add.x += ext[nt][0], add.y += ext[nt][1], add.z += ext[nt][2], add.w += ext[nt][3];
         if (pos >= 0) {
           const float4 r = *reinterpret_cast<const float4*>(a.g_half + pos * kN1 + f);
@@ -301,7 +307,7 @@ __global__ void __launch_bounds__(kThreads) cell_heads_kernel(HeadArgs a) {
       y = mfma16x16x32(wf, hb[ks], y);
     }
     if (live) {
-      const float4 bb = *reinterpret_cast<const float4*>(a.b3 + 4 * g);
+      const float4 bb = *reinterpret_cast<const float4*>(sb3 + 4 * g);
       *reinterpret_cast<float4*>(a.out + row * kN3 + 4 * g) =
           make_float4(y[0] + bb.x, y[1] + bb.y, y[2] + bb.z, y[3] + bb.w);
     }
