@@ -196,7 +196,8 @@ def main() -> int:
     if args.gpus != 1:
         print(
             f"bench.py measures one MI355X only; --gpus {args.gpus} is not supported "
-            "(the MantisNet leaf evaluation shards by position with no exchange; see DESIGN.md)",
+            "(the MantisNet leaf evaluation shards by position with no exchange: split the leaf batch "
+            "into per-GPU sub-batches, one process per GPU, outputs concatenated in position order)",
             file=sys.stderr,
         )
         return 2
