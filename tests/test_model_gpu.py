@@ -14,6 +14,7 @@ import torch
 from mantisnet import PRODUCTION, MantisConfig, MantisNet, collate_positions, synthetic
 from mantisnet.klent.train import KlentConfig, network_evaluate
 from oracle.compare import compare_outputs, oracle_forward
+from tests.forward_fixtures import NAMES, Fixture
 
 pytestmark = pytest.mark.gpu
 
@@ -24,10 +25,13 @@ def _model(device, cfg=PRODUCTION, seed=0):
     return net.to(device).eval()
 
 
-@pytest.mark.parametrize("config,count", [(1, 8), (4, 12)])
+@pytest.mark.parametrize("config,count", [(1, 8), (4, 12), (5, 4)])
 def test_forward_matches_oracle(device, config, count):
+    # config 5 is configs[4]: 150-250 stones, up to 254 attention rows, the
+    # longest radius runs
     net = _model(device)
     batch = collate_positions(synthetic.random_games(config, count))
+    print(f"config {config}: {batch.n_pos} positions, {batch.n_cells} cells, max_t {batch.max_t}", flush=True)
     with torch.no_grad():
         out = net(batch.to(device), 0.2)
     from mantisnet import ops
@@ -38,6 +42,23 @@ def test_forward_matches_oracle(device, config, count):
     assert rep["ok"], rep
     assert out.value_dist.dtype == torch.float32
     assert torch.allclose(out.value_dist.sum(-1), torch.ones(batch.n_pos, device=device), atol=1e-5)
+
+
+@pytest.mark.parametrize("name", [n for n in NAMES if n != "tiny_cfg0"])
+def test_forward_matches_reference_fixture(device, name):
+    # the reference's own forward, run on CPU fp32 (tests/golden/forward_*.npz)
+    fx = Fixture(name)
+    batch = fx.batch()
+    print(f"fixture {name}: {batch.n_pos} positions, {batch.n_cells} cells", flush=True)
+    net = fx.model().to(device)
+    with torch.no_grad():
+        out = net(batch.to(device), fx.mass_floor)
+    from mantisnet import ops
+
+    ops.raise_on_device_error(device)
+    rep = compare_outputs(out, fx.expected, batch.legal_offsets)
+    print(rep)
+    assert rep["ok"], rep
 
 
 def test_uncovered_scope_matches_oracle(device):

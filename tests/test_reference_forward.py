@@ -1,0 +1,56 @@
+"""The CPU oracle's composition against the reference's own forward.
+
+``tests/golden/forward_*.npz`` hold the outputs of the reference's
+``MantisNet.forward`` (python/mantisnet/mantisnet/model.py:1185-1200), run on
+CPU fp32 over seeded positions and seeded perturbed weights
+(tests/golden/write_forward_fixtures.py).  The oracle (oracle/model_ref.py)
+must reproduce them to fp32 summation-order noise, which pins its wiring:
+LayerNorm placement, residual order, head folding and the value readout.
+The cases cover the ``_tiny`` widths with the production knobs,
+the production configuration on configs[3] and configs[4] positions, the
+knob-off default configuration, the uncovered cell-node scope and ply-0 /
+single-stone positions.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from tests.forward_fixtures import NAMES, OUTPUTS, Fixture
+from oracle.compare import oracle_forward
+
+# fp32 summation-order noise, scaled by each output's magnitude
+REL = 2e-5
+
+
+def _max_err(a, b):
+    return float((a.float() - b.float()).abs().max()) if a.numel() else 0.0
+
+
+@pytest.mark.parametrize("name", NAMES)
+def test_oracle_matches_reference_forward(name):
+    fx = Fixture(name)
+    batch = fx.batch()
+    assert batch.n_cells == fx.expected["policy_logits"].numel()
+    ref = oracle_forward(fx.model(), batch, fx.mass_floor)
+    for k in OUTPUTS:
+        scale = max(1.0, float(fx.expected[k].abs().max())) if fx.expected[k].numel() else 1.0
+        err = _max_err(ref[k], fx.expected[k])
+        assert err <= REL * scale, (k, err, scale)
+
+
+def test_reference_fixture_detects_a_composition_change():
+    # a mistake planted in the oracle's inputs: the last block's cell-read
+    # LayerNorms swapped between the cell side and the window side (what a
+    # LayerNorm applied to the wrong operand does) must move the outputs far
+    # beyond the tolerance above
+    fx = Fixture("prod_cfg3")
+    net = fx.model()
+    sd = net.state_dict()
+    for leaf in ("weight", "bias"):
+        a, b = f"blocks.3.ln_cr_c.{leaf}", f"blocks.3.ln_cr_w.{leaf}"
+        sd[a], sd[b] = sd[b].clone(), sd[a].clone()
+    net.load_state_dict(sd)
+    ref = oracle_forward(net, fx.batch(), fx.mass_floor)
+    assert _max_err(ref["policy_logits"], fx.expected["policy_logits"]) > 100 * REL
