@@ -13,9 +13,12 @@ The JSON line also carries
 * ``roofline`` — the dominant kernel of the timed steps (largest summed
   duration among the traced kernels), its algorithmic bytes per launch over
   its average HIP-event duration on the launching stream, against 8 TB/s;
+* ``seam`` — the KLENT evaluator seam (trunk + the two cell heads) on the
+  same batch;
 * ``cpu_baseline`` — the CPU fp32 oracle (oracle/model_ref.py, the
   restatement of the reference's CPU formulations) timed on a bounded sample
-  of the same batch on this host;
+  of the same batch on this host's CPU share, plus configs[0] (B=8, smallest
+  widths) with the reference's literal window-latent loops;
 * ``attention`` / ``message_passing`` — the isolated-kernel configurations
   (configs[1] ragged attention, configs[2] hex message passing) with MFMA and
   HBM fractions.
@@ -167,27 +170,121 @@ def isolated_message_passing(torch, ops, dev, reps=20):
     }
 
 
-def cpu_baseline(torch, net, games, sample: int, reps: int):
-    """The CPU fp32 oracle on the first `sample` positions of the batch."""
-    from mantisnet import collate_positions
-    from oracle.compare import oracle_forward
+def seam_timing(torch, net, bd, steps: int) -> dict:
+    """The KLENT evaluator seam (klent/train.py:100-120) on the same
+    device-resident batch: the policy/critic evaluation alone (trunk and the
+    two cell heads, no value readout) and the whole evaluator closure,
+    including both Q compositions and the copy of its three outputs to host
+    memory.  Each is the median of ``steps`` device-synchronised calls."""
+    from mantisnet import forward as fwd
+    from mantisnet.klent.train import KlentConfig, network_evaluate
 
-    threads = min(16, os.cpu_count() or 1)
-    torch.set_num_threads(threads)
-    sub = collate_positions(games[:sample])
-    oracle_forward(net, sub, 0.2)  # warm-up
+    ev = network_evaluate(net, KlentConfig(device="cuda"))
+
+    def timed(fn):
+        for _ in range(2):
+            fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(steps):
+            t0 = time.perf_counter()
+            fn()
+            torch.cuda.synchronize()
+            ts.append(time.perf_counter() - t0)
+        return round(1e3 * statistics.median(ts), 4)
+
+    return {"policy_q_ms": timed(lambda: fwd.policy_q(net, bd)), "evaluator_ms_with_host_copy": timed(lambda: ev(bd)),
+            "steps": steps}
+
+
+def _host_cpus() -> dict:
+    """What the host offers: logical CPUs, this process's affinity, the
+    cgroup CPU quota and the CPU model."""
+    info = {"host_cpus": os.cpu_count(), "affinity_cpus": len(os.sched_getaffinity(0))}
+    try:
+        quota, period = Path("/sys/fs/cgroup/cpu.max").read_text().split()[:2]
+        info["cgroup_cpus"] = None if quota == "max" else math.ceil(int(quota) / int(period))
+    except (OSError, ValueError):
+        info["cgroup_cpus"] = None
+    model = None
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    info["cpu_model"] = model
+    return info
+
+
+def _cpu_threads(info: dict) -> int:
+    """The CPU share this process may use: the affinity set, bounded by the
+    cgroup quota and by OMP_NUM_THREADS when those are set."""
+    n = info["affinity_cpus"]
+    if info["cgroup_cpus"]:
+        n = min(n, info["cgroup_cpus"])
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return max(1, n)
+
+
+def _time_forward(fn, warmup: int, reps: int) -> float:
+    for _ in range(warmup):
+        fn()
     times = []
     for _ in range(reps):
         t0 = time.perf_counter()
-        oracle_forward(net, sub, 0.2)
+        fn()
         times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
+    return statistics.median(times)
+
+
+def cpu_baseline(torch, net, games, sample: int, reps: int):
+    """The CPU fp32 restatement of the reference's CPU path, timed on this
+    host's cores with the reference's method (lab/bench.py:124-142: warm-up
+    forwards, then the median of timed forwards):
+
+    * ``value``: the production configuration on the first ``sample``
+      positions of the benchmark batch, the window-latent cycle
+      vectorised (the reference's literal loops would iterate over ~676k
+      windows per block at B=512);
+    * ``configs0``: BASELINE configs[0] — the smallest model widths with the
+      production knobs, B=8 positions of 10-40 stones — with the window-latent
+      cycle as the reference's literal CPU loops, the formulation that
+      reproduces the reference's own output bit for bit.
+    """
+    from mantisnet import MantisConfig, MantisNet, collate_positions, synthetic
+    from oracle.compare import oracle_forward
+
+    info = _host_cpus()
+    threads = _cpu_threads(info)
+    torch.set_num_threads(threads)
+    sub = collate_positions(games[:sample])
+    med = _time_forward(lambda: oracle_forward(net, sub, 0.2), 1, reps)
+    tiny = MantisNet(MantisConfig(h=16, blocks=1, heads=2, value_queries=2, value_bins=5, policy_hidden=16,
+                                  value_hidden=16, cell_latents=True, cell_nodes=True, cell_node_scope="all"))
+    tiny.load_state_dict(synthetic.perturbed_state_dict(tiny, seed=0))
+    b8 = collate_positions(synthetic.random_games(1, 8))
+    med0 = _time_forward(lambda: oracle_forward(tiny, b8, 0.2, latent_loops=True), 3, 10)
     return {
         "value": round(sample / med, 2),
         "unit": "positions/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"{sample} of the {len(games)} benchmark positions, fp32 oracle forward, median of {reps}",
+        "sample": f"configs[3]: {sample} of the {len(games)} benchmark positions, production configuration, fp32, "
+                  f"window-latent cycle vectorised, median of {reps} forwards after 1 warm-up",
+        "torch_threads": torch.get_num_threads(),
+        **info,
+        "configs0": {
+            "value": round(8 / med0, 2),
+            "unit": "positions/s",
+            "ms_per_forward": round(1e3 * med0, 2),
+            "sample": "configs[0]: B=8 positions of 10-40 stones, h=16 / 1 block / 2 heads with the production "
+                      "knobs, fp32, window-latent cycle as the reference's literal loops, median of 10 after 3 "
+                      "warm-ups",
+        },
     }
 
 
@@ -309,13 +406,15 @@ def main() -> int:
         "roofline": roofline,
         "kernels": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in kernels.items()},
     }
+    line["seam"] = seam_timing(torch, net, bd, min(args.steps, 10))
+    _log(f"seam: {line['seam']}")
     if not args.no_isolated:
         _log("isolated attention (configs[1])")
         line["attention"] = isolated_attention(torch, ops, dev)
         _log("isolated message passing (configs[2])")
         line["message_passing"] = isolated_message_passing(torch, ops, dev)
     if not args.no_cpu_baseline:
-        _log(f"cpu baseline: oracle on {args.cpu_sample} positions x {args.cpu_reps}")
+        _log(f"cpu baseline: oracle on {args.cpu_sample} positions x {args.cpu_reps}, configs[0] B=8")
         line["cpu_baseline"] = cpu_baseline(torch, net, games, args.cpu_sample, args.cpu_reps)
     print(json.dumps(line), flush=True)
     return 0

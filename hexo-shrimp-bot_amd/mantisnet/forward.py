@@ -400,17 +400,13 @@ def make_plan(model, b: Batch, speculative: bool = False) -> Plan:
 
 
 def _plan_for(model, batch: Batch) -> tuple[Batch, Plan]:
-    """The batch on the model's device and its index plan, derived once per
-    batch object (trunk and heads of one evaluation share them).  A batch on
-    another device (the PyO3 seam builds CPU tensors) is moved first."""
-    cache = getattr(model, "_mi355x_plan", None)
-    if cache is not None and cache[0] is batch:
-        return cache[1], cache[2]
+    """The batch on the model's device and its index plan, derived afresh on
+    every call (nothing is kept on the model, so a batch refilled in place
+    never meets a stale plan).  A batch on another device (the PyO3 seam builds
+    CPU tensors) is moved first."""
     dev = next(model.parameters()).device
     b = batch if batch.stone_own.device == dev else batch.to(dev)
-    plan = make_plan(model, b)
-    object.__setattr__(model, "_mi355x_plan", (batch, b, plan))
-    return b, plan
+    return b, make_plan(model, b)
 
 
 # ----------------------------------------------------------------- blocks
@@ -537,9 +533,11 @@ def _block(W, P, i: int, plan: Plan, b: Batch, sg, w, c, sw_all, update_stones: 
 @torch.no_grad()
 def trunk(model, batch: Batch):
     """(ln_out(w) fp32 (N_w, H), mean_j ln_out(g) fp32 (P, H), ln_out(c) fp16 (N_c, H))."""
-    _supported(model)
+    dev = _supported(model)
     b, plan = _plan_for(model, batch)
-    return _trunk(model, b, plan)
+    out = _trunk(model, b, plan)
+    ops.raise_on_device_error(dev)
+    return out
 
 
 def _trunk(model, b: Batch, plan: Plan, raw_cells: bool = False, W: Prepared | None = None):
@@ -584,9 +582,11 @@ def _trunk(model, b: Batch, plan: Plan, raw_cells: bool = False, W: Prepared | N
 
 @torch.no_grad()
 def value_head(model, w: Tensor, g: Tensor, batch: Batch):
-    _supported(model)
+    dev = _supported(model)
     b, plan = _plan_for(model, batch)
-    return _value_head(model, w, g, b, plan)
+    out = _value_head(model, w, g, b, plan)
+    ops.raise_on_device_error(dev)
+    return out
 
 
 def _value_head(model, w: Tensor, g: Tensor, b: Batch, plan: Plan, W: Prepared | None = None):
@@ -627,17 +627,20 @@ def _head_rows(model, w: Tensor, g: Tensor, cells: Tensor, b: Batch, plan: Plan,
 
 @torch.no_grad()
 def cell_head_logits(model, w: Tensor, g: Tensor, cells: Tensor, batch: Batch):
-    _supported(model)
+    dev = _supported(model)
     b, plan = _plan_for(model, batch)
     rows = _head_rows(model, w, g, cells, b, plan)
+    ops.raise_on_device_error(dev)
     return rows[:, 0].contiguous(), rows[:, 1:4]
 
 
 @torch.no_grad()
 def cell_heads(model, w: Tensor, g: Tensor, cells: Tensor, batch: Batch, mass_floor: float):
-    _supported(model)
+    dev = _supported(model)
     b, plan = _plan_for(model, batch)
-    return _cell_heads(model, w, g, cells, b, plan, mass_floor)
+    out = _cell_heads(model, w, g, cells, b, plan, mass_floor)
+    ops.raise_on_device_error(dev)
+    return out
 
 
 def _cell_heads(model, w, g, cells, b: Batch, plan: Plan, mass_floor: float, raw_cells: bool = False,
@@ -647,12 +650,25 @@ def _cell_heads(model, w, g, cells, b: Batch, plan: Plan, mass_floor: float, raw
     return rows[:, 0].contiguous(), q_score, q_values
 
 
+def _speculative(model, b: Batch, evaluate):
+    """Queue ``evaluate(plan)`` on the canonical orders the encoder emits; the
+    order check is read after everything is queued, and a batch in other
+    orders is evaluated again over sorted tables (the first pass's results and
+    flags discarded)."""
+    plan = make_plan(model, b, speculative=True)
+    out = evaluate(plan)
+    if bool(plan.noncanonical.item()):
+        ops.error_flag(b.stone_own.device).zero_()
+        out = evaluate(make_plan(model, b))
+    return out
+
+
 @torch.no_grad()
 def forward(model, batch: Batch, mass_floor: float):
     """Every head of one evaluation (model.py:1185-1200).  The index plan is
     derived inside every call, as the reference derives its tables inside
     every forward; nothing is cached between calls except the prepared
-    weights."""
+    weights.  The caller reads the device error flag."""
     _supported(model)
     dev = next(model.parameters()).device
     b = batch if batch.stone_own.device == dev else batch.to(dev)
@@ -664,12 +680,23 @@ def forward(model, batch: Batch, mass_floor: float):
         policy, q_score, q_values = _cell_heads(model, w, g, c, b, plan, mass_floor, raw_cells=True, W=W)
         return policy, q_score, q_values, value, value_dist, value_logits
 
-    # queued on the canonical orders the encoder emits; the order check is read
-    # after everything is queued, and a batch in other orders is evaluated
-    # again over sorted tables (the first pass's results and flags discarded)
-    plan = make_plan(model, b, speculative=True)
-    out = evaluate(plan)
-    if bool(plan.noncanonical.item()):
-        ops.error_flag(dev).zero_()
-        out = evaluate(make_plan(model, b))
-    return out
+    return _speculative(model, b, evaluate)
+
+
+@torch.no_grad()
+def policy_q(model, batch: Batch):
+    """``cell_head_logits(*trunk(batch), batch)`` as one evaluation: the two
+    heads KLENT trains and collects with (klent/train.py:70-77), without the
+    value readout.  Same plan, fused heads over the raw cell state and device
+    error check as ``forward``: (policy logits (N_c,), critic logits (N_c, 3))."""
+    dev = _supported(model)
+    b = batch if batch.stone_own.device == dev else batch.to(dev)
+    W = _prepared(model)
+
+    def evaluate(plan):
+        w, g, c = _trunk(model, b, plan, raw_cells=True, W=W)
+        return _head_rows(model, w, g, c, b, plan, raw_cells=True, W=W)
+
+    rows = _speculative(model, b, evaluate)
+    ops.raise_on_device_error(dev)
+    return rows[:, 0].contiguous(), rows[:, 1:4]

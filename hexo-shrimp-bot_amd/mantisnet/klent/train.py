@@ -16,7 +16,7 @@ from dataclasses import dataclass
 
 import torch
 
-from ..model import compose_acting_q, compose_q
+from .. import ops
 
 
 @dataclass
@@ -35,9 +35,14 @@ class KlentConfig:
 
 
 def _policy_q(model, batch):
-    """Trunk + the two heads KLENT trains (train.py:70-77)."""
-    w, g, cells = model.trunk(batch)
-    return model.cell_head_logits(w, g, cells, batch)
+    """Trunk + the two heads KLENT trains (train.py:70-77):
+    ``model.cell_head_logits(*model.trunk(batch), batch)``, run as one
+    evaluation (one index plan queued without a host round trip, the heads
+    normalising the raw cell state on the fly, the device error flag read
+    once at the end)."""
+    from .. import forward as fwd
+
+    return fwd.policy_q(model, batch)
 
 
 _gpu_lock = threading.Lock()
@@ -51,10 +56,8 @@ def network_evaluate(model, cfg: KlentConfig):
             b = batch.to(cfg.device)
             with torch.no_grad():
                 policy, critic_logits = _policy_q(model, b)
-            return (
-                policy.float().cpu(),
-                compose_acting_q(critic_logits, b.legal_offsets, cfg.mass_floor).cpu(),
-                compose_q(critic_logits).cpu(),
-            )
+                # both Q roles from one launch: (compose_q, compose_acting_q)
+                q_values, q_score = ops.compose_q(critic_logits.float(), b.legal_offsets, cfg.mass_floor)
+            return policy.float().cpu(), q_score.cpu(), q_values.cpu()
 
     return evaluate

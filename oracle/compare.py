@@ -34,20 +34,22 @@ def batch_dict(batch) -> dict:
     return {k: (v.cpu() if isinstance(v, torch.Tensor) else v) for k, v in vars(batch).items()}
 
 
-def cfg_of(model) -> R.Cfg:
+def cfg_of(model, latent_loops: bool = False) -> R.Cfg:
     c = model.cfg
     if c.cell_latents and not c.cell_nodes:
         raise NotImplementedError("the oracle covers cell_nodes=True and the knob-off cell pass")
     return R.Cfg(h=c.h, blocks=c.blocks, heads=c.heads, ffn_factor=c.ffn_factor,
                  value_queries=c.value_queries, value_bins=c.value_bins,
                  policy_hidden=c.policy_hidden, value_hidden=c.value_hidden,
-                 cell_node_scope=c.cell_node_scope, cell_nodes=c.cell_nodes)
+                 cell_node_scope=c.cell_node_scope, cell_nodes=c.cell_nodes, latent_loops=latent_loops)
 
 
-def oracle_forward(model, batch, mass_floor: float = 0.2) -> dict:
+def oracle_forward(model, batch, mass_floor: float = 0.2, latent_loops: bool = False) -> dict:
+    """The oracle's forward; ``latent_loops`` runs the window-latent cycle as
+    the reference's literal CPU loops."""
     pc, ec = _consts()
     sd = {k: v.detach().float().cpu() for k, v in model.state_dict().items()}
-    return R.forward(sd, cfg_of(model), batch_dict(batch), pc, ec, mass_floor)
+    return R.forward(sd, cfg_of(model, latent_loops), batch_dict(batch), pc, ec, mass_floor)
 
 
 def policy_kl(ref_logits, logits, offsets) -> torch.Tensor:

@@ -64,6 +64,9 @@ class Cfg:
     value_hidden: int = 128
     cell_node_scope: str = "all"
     cell_nodes: bool = True  # False: the knob-off cell pass, heads over decoder window sums
+    # True: the window-latent read and broadcast as the reference's literal
+    # CPU loops (window_latents.py:102-188) instead of the vectorised forms
+    latent_loops: bool = False
 
 
 # ----------------------------------------------------------------- primitives
@@ -347,7 +350,7 @@ def _latent_cycle(sd, pre, cfg, w, g, window_pos, offsets, order):
     rows = ln(w, sd, pre + "latent_ln_read_w")
     k = lin(rows, sd, pre + "latent_wk_read").view(-1, a, hd)
     v = lin(rows, sd, pre + "latent_wv_read").view(-1, a, hd)
-    read = latent_read(q, k, v, offsets, order)
+    read = (latent_read_loops if cfg.latent_loops else latent_read)(q, k, v, offsets, order)
     g = g + lin(read.reshape(p, slots, h), sd, pre + "latent_wo_read")
     z = ln(g, sd, pre + "latent_ln_mix")
     q = lin(z, sd, pre + "latent_wq_mix").view(p, slots, a, hd)
@@ -360,7 +363,7 @@ def _latent_cycle(sd, pre, cfg, w, g, window_pos, offsets, order):
     q = lin(ln(w, sd, pre + "latent_ln_bcast_q"), sd, pre + "latent_wq_bcast").view(-1, a, hd)
     k = lin(lat, sd, pre + "latent_wk_bcast").view(p, slots, a, hd)
     v = lin(lat, sd, pre + "latent_wv_bcast").view(p, slots, a, hd)
-    out = latent_broadcast(q, k, v, window_pos)
+    out = (latent_broadcast_loops if cfg.latent_loops else latent_broadcast)(q, k, v, window_pos)
     w = w + lin(out.reshape(-1, h), sd, pre + "latent_wo_bcast")
     return w, g
 

@@ -112,6 +112,51 @@ def test_network_evaluate_seam(device):
     assert (q_values - ref["q_values"]).abs().max() <= 1e-2
 
 
+def test_network_evaluate_equals_the_forward_heads(device):
+    # the seam's fused evaluation gives bitwise the forward's policy and Q
+    net = _model(device, seed=2)
+    batch = collate_positions(synthetic.random_games(4, 3, start=30))
+    policy, q_score, q_values = network_evaluate(net, KlentConfig(device="cuda"))(batch)
+    with torch.no_grad():
+        out = net(batch.to(device), 0.2)
+    assert torch.equal(policy, out.policy_logits.cpu())
+    assert torch.equal(q_score, out.q_score.cpu()) and torch.equal(q_values, out.q_values.cpu())
+
+
+def test_network_evaluate_raises_on_bad_indices_and_leaves_no_flag(device):
+    # a radius source one past the last stone is skipped and flagged by the
+    # cell pass; the seam raises, and the next valid evaluation is unaffected
+    net = _model(device)
+    games = synthetic.random_games(1, 2, start=40)
+    bad = collate_positions(games)
+    bad.radius_src = bad.radius_src.clone()
+    bad.radius_src[7] = bad.stone_own.numel()
+    with pytest.raises(ValueError):
+        network_evaluate(net, KlentConfig(device="cuda"))(bad)
+    good = collate_positions(games)
+    with torch.no_grad():
+        out = net(good.to(device), 0.2)
+    rep = compare_outputs(out, oracle_forward(net, good, 0.2), good.legal_offsets)
+    assert rep["ok"], rep
+
+
+def test_trunk_and_heads_follow_a_batch_refilled_in_place(device):
+    # trunk / cell_head_logits derive their index plan on every call: a Batch
+    # object refilled with another batch's tensors gives that batch's outputs
+    net = _model(device, seed=8)
+    first = collate_positions(synthetic.random_games(1, 2, start=50)).to(device)
+    second = collate_positions(synthetic.random_games(1, 3, start=60)).to(device)
+    holder = collate_positions(synthetic.random_games(1, 2, start=50)).to(device)
+    with torch.no_grad():
+        net.cell_head_logits(*net.trunk(holder), holder)
+        for k, v in vars(second).items():
+            setattr(holder, k, v)
+        policy, _ = net.cell_head_logits(*net.trunk(holder), holder)
+        want = net(second, 0.2).policy_logits
+    assert first.n_cells != second.n_cells
+    assert (policy - want).abs().max().item() <= 1e-2
+
+
 def test_pyo3_style_single_argument_call_raises_like_the_reference(device):
     # mantisnet_python.rs:105-120 calls model(batch) with one argument; the
     # reference forward has no mass_floor default (model.py:1185), so the

@@ -54,3 +54,19 @@ def test_reference_fixture_detects_a_composition_change():
     net.load_state_dict(sd)
     ref = oracle_forward(net, fx.batch(), fx.mass_floor)
     assert _max_err(ref["policy_logits"], fx.expected["policy_logits"]) > 100 * REL
+
+
+def test_literal_loop_oracle_is_bitwise_the_reference_cpu_path():
+    # with the window-latent cycle as the reference's literal loops
+    # (window_latents.py:102-188), the oracle performs the reference's CPU
+    # operations in the reference's order: configs[0] comes out bit for bit
+    # (same thread count as the writer: the CPU GEMMs' blocking follows it)
+    fx = Fixture("tiny_cfg0")
+    threads = torch.get_num_threads()
+    torch.set_num_threads(8)
+    try:
+        ref = oracle_forward(fx.model(), fx.batch(), fx.mass_floor, latent_loops=True)
+    finally:
+        torch.set_num_threads(threads)
+    for k in OUTPUTS:
+        assert torch.equal(ref[k].float(), fx.expected[k]), k
