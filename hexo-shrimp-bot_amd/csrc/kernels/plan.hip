@@ -22,10 +22,39 @@
 // * attention slots: the padded [latents; stones] sequence of each position
 //   (max_t slots, the 4 latent rows first) mapped to rows of the [s; g]
 //   buffer and back.
+#include <mutex>
+
 #include "common.hpp"
 
 namespace mantis {
 namespace {
+
+// The no-allocation variant of the stable key order keeps its counts and
+// permutation in this file-scope array (one copy per GPU, held until the
+// process ends).  Host code never passes the array's name to a kernel: it
+// reads the array's device address once per device with
+// hipGetSymbolAddress and passes that address.
+static_assert(MANTIS_NOALLOC_SCRATCH_BYTES % 256 == 0, "scratch size");
+__device__ __align__(256) unsigned char scratch[MANTIS_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_addr[kMaxDevices] = {};
+
+// The current device's copy of `scratch` (nullptr if its address cannot be
+// read).  The first call on a device reads the address with that device
+// current; later calls return the kept pointer.
+void* scratch_for_current_device() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_addr[dev]) {
+    void* addr = nullptr;
+    if (hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch)) != hipSuccess || !addr) return nullptr;
+    g_scratch_addr[dev] = addr;
+  }
+  return g_scratch_addr[dev];
+}
 
 __device__ __forceinline__ int64_t floordiv(int64_t a, int64_t b) {
   const int64_t q = a / b;
@@ -80,6 +109,40 @@ __global__ void scatter_kernel(const int64_t* __restrict__ key, int64_t n, int64
   for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x) {
     const int64_t k = key[i];
     if (k >= 0 && k < n_keys) perm[ptr[k] + int64_t(atomicSub(&counts[k], 1)) - 1] = i;
+  }
+}
+
+// ptr[0] = 0, ptr[k + 1] = counts[0] + ... + counts[k]: one workgroup of
+// 1024 threads walks the counts in tiles of 1024 (a wavefront scan by
+// shuffles, then the 16 wavefront totals through LDS), carrying the running
+// total between tiles.  Every thread reads the same totals, so the carry
+// agrees across the workgroup without another exchange.
+__global__ __launch_bounds__(1024) void scan_counts_kernel(const int32_t* __restrict__ counts, int64_t n,
+                                                           int64_t* __restrict__ ptr) {
+  __shared__ int64_t wave_total[16];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (threadIdx.x == 0) ptr[0] = 0;
+  int64_t carry = 0;
+  for (int64_t base = 0; base < n; base += 1024) {
+    const int64_t i = base + threadIdx.x;
+    int64_t v = i < n ? int64_t(counts[i]) : 0;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int64_t u = __shfl_up(v, d, 64);
+      if (lane >= d) v += u;
+    }
+    if (lane == 63) wave_total[wave] = v;
+    __syncthreads();
+    int64_t before = 0, tile = 0;
+#pragma unroll
+    for (int w = 0; w < 16; ++w) {
+      const int64_t t = wave_total[w];
+      before += w < wave ? t : 0;
+      tile += t;
+    }
+    if (i < n) ptr[i + 1] = carry + before + v;
+    carry += tile;
+    __syncthreads();  // wave_total is rewritten by the next tile
   }
 }
 
@@ -242,6 +305,29 @@ int32_t mantis_stable_key_order(const int64_t* key, const int64_t* col_a, const 
   int64_t* perm = reinterpret_cast<int64_t*>(static_cast<char*>(workspace) + (4 * n_keys + 7) / 8 * 8);
   scatter_kernel<<<grid_for(n_entries), 256, 0, st>>>(key, n_entries, n_keys, ptr, counts, perm);
   segment_sort_gather_kernel<<<grid_for(n_keys), 256, 0, st>>>(ptr, n_keys, perm, col_a, col_b, out_a, out_b);
+  return launched();
+}
+
+int32_t mantis_stable_key_order_noalloc(const int64_t* key, const int64_t* col_a, const int64_t* col_b,
+                                        int64_t n_entries, int64_t n_keys, int64_t* ptr, int64_t* out_a,
+                                        int64_t* out_b, int32_t* err_flag, void* stream) {
+  if (!ptr || n_entries < 0 || n_keys < 0) return MANTIS_E_ARG;
+  if (n_entries && (!key || !col_a || !col_b || !out_a || !out_b)) return MANTIS_E_ARG;
+  if (mantis_stable_key_order_workspace(n_entries, n_keys) > MANTIS_NOALLOC_SCRATCH_BYTES) return MANTIS_E_SIZE;
+  void* ws = scratch_for_current_device();
+  if (!ws) return MANTIS_E_LAUNCH;
+  hipStream_t st = as_stream(stream);
+  int32_t* counts = static_cast<int32_t*>(ws);
+  int64_t* perm = reinterpret_cast<int64_t*>(static_cast<char*>(ws) + (4 * n_keys + 7) / 8 * 8);
+  // counts start at zero on every call (the array keeps the last call's
+  // contents); cleared by a kernel, not a memset
+  if (n_keys) fill_i32_kernel<<<grid_for(n_keys), 256, 0, st>>>(counts, n_keys, 0);
+  if (n_entries) count_kernel<<<grid_for(n_entries), 256, 0, st>>>(key, n_entries, n_keys, counts, err_flag);
+  scan_counts_kernel<<<1, 1024, 0, st>>>(counts, n_keys, ptr);
+  if (n_entries && n_keys) {
+    scatter_kernel<<<grid_for(n_entries), 256, 0, st>>>(key, n_entries, n_keys, ptr, counts, perm);
+    segment_sort_gather_kernel<<<grid_for(n_keys), 256, 0, st>>>(ptr, n_keys, perm, col_a, col_b, out_a, out_b);
+  }
   return launched();
 }
 

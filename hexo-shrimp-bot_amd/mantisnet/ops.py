@@ -158,6 +158,9 @@ def raise_on_device_error(device: torch.device | None = None) -> None:
 def _check(status: int, what: str) -> None:
     if status == 1:
         raise ValueError(f"{what}: unsupported shape, dtype, alignment or null input")
+    if status == 3:
+        raise ValueError(f"{what}: the request exceeds the library's fixed device buffer "
+                         f"({_NOALLOC_SCRATCH_BYTES} bytes per GPU)")
     if status != 0:
         raise RuntimeError(f"{what}: HIP launch failed (status {status})")
 
@@ -267,6 +270,31 @@ def stable_key_order(key: Tensor, col_a: Tensor, col_b: Tensor, n_keys: int) -> 
         _check(_lib().mantis_stable_key_order(_ptr(key), _ptr(col_a), _ptr(col_b), n, n_keys, _ptr(ptr), _ptr(out_a),
                                               _ptr(out_b), _ptr(ws), _stream()), "stable_key_order")))
     return ptr, out_a, out_b
+
+
+_NOALLOC_SCRATCH_BYTES = 40 << 20  # MANTIS_NOALLOC_SCRATCH_BYTES
+
+
+def stable_key_order_noalloc(key: Tensor, col_a: Tensor, col_b: Tensor, ptr: Tensor, out_a: Tensor,
+                             out_b: Tensor) -> None:
+    """``stable_key_order`` into caller-owned outputs (ptr: n_keys + 1,
+    out_a / out_b: one per entry, int64) through the entry point that
+    allocates nothing: its counts and permutation live in the library's fixed
+    per-GPU buffer.  Raises ValueError past that buffer's size.  Calls on one
+    GPU share the buffer, so overlapping calls race."""
+    dev = _on_gpu(key, col_a, col_b, ptr, out_a, out_b)
+    for t, name in ((key, "key"), (col_a, "col_a"), (col_b, "col_b"), (ptr, "ptr"), (out_a, "out_a"),
+                    (out_b, "out_b")):
+        if t.dtype != torch.int64 or t.ndim != 1 or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous int64 vector")
+    n, n_keys = key.numel(), ptr.numel() - 1
+    if n_keys < 0 or col_a.numel() != n or col_b.numel() != n or out_a.numel() != n or out_b.numel() != n:
+        raise ValueError("key, col_a, col_b, out_a and out_b must have one length; ptr n_keys + 1")
+    with torch.cuda.device(dev):  # the library reads the current device's buffer address
+        _launch("stable_key_order_noalloc", 8.0 * (5 * n + 3 * n_keys), 0.0, lambda: _check(
+            _lib().mantis_stable_key_order_noalloc(_ptr(key), _ptr(col_a), _ptr(col_b), n, n_keys, _ptr(ptr),
+                                                   _ptr(out_a), _ptr(out_b), _ptr(error_flag(dev)), _stream()),
+            "stable_key_order_noalloc"))
 
 
 def covered_rows(cell_ptr: Tensor, n_cov: int, wcell: Tensor) -> tuple[Tensor, Tensor]:

@@ -34,6 +34,7 @@ extern "C" {
 #define MANTIS_OK 0
 #define MANTIS_E_ARG 1    /* unsupported shape, dtype or null pointer */
 #define MANTIS_E_LAUNCH 2 /* the HIP launch itself failed */
+#define MANTIS_E_SIZE 3   /* the request exceeds a fixed device buffer (the no-allocation entry point) */
 
 #define MANTIS_FLAG_INDEX 1  /* a gather/scatter index was out of range */
 #define MANTIS_FLAG_ORDER 2  /* a CSR/run view was not ascending */
@@ -98,6 +99,28 @@ int32_t mantis_stable_key_count(const int64_t* key, int64_t n_entries, int64_t n
 int32_t mantis_stable_key_order(const int64_t* key, const int64_t* col_a, const int64_t* col_b,
                                 int64_t n_entries, int64_t n_keys, const int64_t* ptr, int64_t* out_a,
                                 int64_t* out_b, void* workspace, void* stream);
+
+/*
+ * The stable key-major view above in one call that allocates nothing: no
+ * counterpart in the reference.  It is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  Same results as mantis_stable_key_count, the
+ * inclusive prefix sum and mantis_stable_key_order, with ptr (n_keys + 1,
+ * int64) written here.  The counts and the permutation live in one
+ * library-owned device array of MANTIS_NOALLOC_SCRATCH_BYTES per GPU (held
+ * until the process ends; its address is read on the first call on each
+ * device, with that device current, and the stream must belong to the
+ * current device).  Requests needing more than that
+ * (mantis_stable_key_order_workspace(n_entries, n_keys) bytes) return
+ * MANTIS_E_SIZE before anything is enqueued.  Every call on a GPU shares that
+ * GPU's array: calls that overlap on one GPU (other streams, other threads)
+ * race and must be serialised by the caller.  Enqueues kernels only (no
+ * memset, no allocation).
+ */
+#define MANTIS_NOALLOC_SCRATCH_BYTES (40ll << 20)
+int32_t mantis_stable_key_order_noalloc(const int64_t* key, const int64_t* col_a, const int64_t* col_b,
+                                        int64_t n_entries, int64_t n_keys, int64_t* ptr, int64_t* out_a,
+                                        int64_t* out_b, int32_t* err_flag, void* stream);
 
 /*
  * Covered-cell compaction (the cells with decoder entries, whose k/v rows
