@@ -23,11 +23,14 @@ arithmetic is regrouped into fused HIP kernels (libmantis_hip.so via
   position row add, and both output layers are one block-diagonal stage 2.
 
 Precision: every GEMM and attention operand is fp16 with fp32 accumulation;
-LayerNorm statistics, softmax, the residual streams (s, w, g, c) and the head
-outputs are fp32.  The reference runs under bf16 autocast
-(klent/train.py:108); fp16 runs at the same MFMA rate with three more
-mantissa bits, which keeps the policy logits within 1e-2 of the fp32
-reference (bf16 operands drift to ~5e-2 over four blocks).
+LayerNorm statistics, softmax and the head outputs are fp32.  The stone and
+latent residual streams (s, g) are stored in fp32.  In the cell-node
+configuration the window and cell streams (w, c) are stored in fp16: every
+kernel that updates them widens the row to fp32, adds in fp32 and rounds
+once on the store (the knob-off configuration keeps w in fp32).  The
+reference runs under bf16 autocast (klent/train.py:108); fp16 runs at the
+same MFMA rate with three more mantissa bits, which keeps the policy logits
+within 1e-2 of the fp32 reference, where bf16 operands do not.
 
 Per-batch index views (the reference's incidence_plan, window_latent_layout,
 cell_tables and cell_node_edge_tables) are derived once per batch on the

@@ -101,16 +101,25 @@ def test_gumbel_search_matches_reference_fixture(device, monkeypatch):
         return real_collate(positions)
 
     traces = []
+    real_sample, real_halve = search._sample, search._halve
 
-    class TracingSearch(search._Search):
-        @property
-        def survivors(self):
-            return self._survivors
+    def tracing_sample(rng, logits, temperature, m):
+        ranks, noise = real_sample(rng, logits, temperature, m)
+        traces.append([int(r) for r in ranks])
+        return ranks, noise
 
-        @survivors.setter
-        def survivors(self, value):
-            self._survivors = list(value)
-            traces.append([int(self.lines[i].root_rank) for i in self._survivors])
+    lines_seen = {}
+
+    def tracing_halve(values, survivors):
+        kept = real_halve(values, survivors)
+        traces.append([int(lines_seen["lines"].rank[i]) for i in kept])
+        return kept
+
+    real_lines = search._Lines
+
+    def recording_lines(*args):
+        lines_seen["lines"] = real_lines(*args)
+        return lines_seen["lines"]
 
     class FixedRootRng:
         def gumbel(self, size):
@@ -153,7 +162,9 @@ def test_gumbel_search_matches_reference_fixture(device, monkeypatch):
         return logits, q, q
 
     monkeypatch.setattr(search, "collate_positions", recording_collate)
-    monkeypatch.setattr(search, "_Search", TracingSearch)
+    monkeypatch.setattr(search, "_sample", tracing_sample)
+    monkeypatch.setattr(search, "_halve", tracing_halve)
+    monkeypatch.setattr(search, "_Lines", recording_lines)
     monkeypatch.setattr(search, "_root_rng", lambda seed: FixedRootRng())
     root = Position.replay(CASE["position_prefix"])
     chooser = search.gumbel_choose(evaluate, tau=cfg["tau"], lam=cfg["lambda"], sims=cfg["sims"])
@@ -163,3 +174,33 @@ def test_gumbel_search_matches_reference_fixture(device, monkeypatch):
     assert traces[1:] == CASE["expected"]["survivor_root_ranks_after_round"]
     assert list(move) == CASE["expected"]["chosen_move"]
     assert root.legal_moves().index(move) == CASE["expected"]["chosen_root_rank"]
+
+
+def _scripted(batch):
+    """A deterministic evaluator: every value depends only on the position
+    (its cell count, each cell's index and nearest-stone distance), so a
+    position gets the same outputs in any batch."""
+    off = batch.legal_offsets.tolist()
+    near = batch.cell_nearest.float()
+    local = torch.cat([torch.arange(off[i + 1] - off[i], dtype=torch.float32) for i in range(len(off) - 1)])
+    n = torch.cat([torch.full((off[i + 1] - off[i],), float(off[i + 1] - off[i])) for i in range(len(off) - 1)])
+    logits = torch.sin(0.37 * local + 0.011 * n) + 0.1 * near
+    q = torch.cos(0.23 * local - 0.007 * n) * 0.8
+    return logits, q, q
+
+
+@pytest.mark.gpu
+def test_batched_and_singleton_calls_choose_alike(device):
+    # one child seed per root (drawn in root order): a batched call and
+    # singleton calls on the same parent stream make the same choices
+    from mantisnet import synthetic
+
+    games = synthetic.random_games(1, 4, start=500)
+    roots = [Position.replay([tuple(m) for m in g.tolist()]) for g in games]
+    chooser = search.gumbel_choose(_scripted, tau=0.1, lam=0.03, sims=24, temperature=1.0)
+    batched = chooser(roots, np.random.default_rng(7))
+    parent = np.random.default_rng(7)
+    single = [chooser([r], parent)[0] for r in roots]
+    assert batched == single
+    for r, mv in zip(roots, batched):
+        assert mv in r.legal_moves()
