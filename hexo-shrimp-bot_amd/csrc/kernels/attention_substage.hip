@@ -33,6 +33,14 @@
 // one contiguous eighth of the rows, so the gathered k/v rows of a position
 // stay in that XCD's L2.
 //
+// The class-bias tables of the stages sit in LDS beside the weights (they
+// are gathered once per entry and head: from LDS they cost no L1 access).
+// A row's entries are read four at a time, lane (r, g) loading entry j + g,
+// validated once and handed to the row's lanes by DPP quad broadcasts.  The
+// online softmax moves its reference point only when a score exceeds it by
+// kTau (e^kTau bounds every weight), so the accumulator is rescaled on the
+// rare entries that do, not on every entry.
+//
 // A tile's entry loop runs as long as its longest row.  An optional row
 // order (a permutation of the rows) groups rows of similar entry counts into
 // tiles; each row's arithmetic is the same in any order, so the results are
@@ -53,7 +61,10 @@ constexpr int kPitch = kK + 8;  // fp16 per staged LDS row (272 bytes: conflict-
 template <int kStages>
 constexpr int waves_for() { return kStages == 2 ? 8 : 12; }
 constexpr int kXcds = 8;
-constexpr int kB = 1;  // entries whose rows are in flight together
+// class-bias tables of all stages in LDS: 4 heads x n_classes fp32 per stage
+// (the two-stage pass leaves 22.5 KB beside its 141 KB of weights)
+constexpr int kBiasPool = 5376;
+constexpr float kTau = 8.f;  // the softmax reference point lags the max by at most this
 
 struct Stage {
   const _Float16* wq;
@@ -80,9 +91,16 @@ struct SubArgs {
   int64_t n_rows;
   const int32_t* order;  // tile slot -> row, or null for the natural order
   Stage st[2];
+  int32_t bias_off[2];   // each stage's table in the LDS bias pool
   float scale;
   int32_t* flag;
 };
+
+// the value v of lane 4 (lane / 4) + u (one DPP quad broadcast)
+template <int u>
+__device__ __forceinline__ int32_t from_quad(int32_t v) {
+  return __builtin_amdgcn_update_dpp(0, v, u * 0x55, 0xF, 0xF, false);
+}
 
 // LDS row r of the staged q weights holds Wq row qrow(r): the accumulator
 // row 16 nt + 4 g + t of lane group g is feature 32 g + 4 nt + t.
@@ -143,12 +161,14 @@ __global__ void __launch_bounds__(waves_for<kStages>() * 64) attn_substage_kerne
   // tile loop (loads and stores share one in-order counter, so such a wait
   // would also wait for the look-ahead loads and the stores before it)
   __shared__ __attribute__((aligned(16))) float sb[kStages][2][kK];
+  __shared__ float sbias[kBiasPool];
 #pragma unroll
   for (int s = 0; s < kStages; ++s) {
     for (int i = threadIdx.x; i < kK; i += kThreads) {
       sb[s][0][i] = a.st[s].bq[i];
       sb[s][1][i] = a.st[s].bo[i];
     }
+    for (int i = threadIdx.x; i < 4 * a.st[s].n_classes; i += kThreads) sbias[a.bias_off[s] + i] = a.st[s].bias[i];
     for (int i = threadIdx.x; i < kK * (kK / 8); i += kThreads) {
       const int r = i / (kK / 8), c = (i % (kK / 8)) * 8;
       *reinterpret_cast<uint4*>(&sw[s][0][r * kPitch + c]) =
@@ -245,18 +265,16 @@ __global__ void __launch_bounds__(waves_for<kStages>() * 64) attn_substage_kerne
       const int acnt = from_lane(src_m, cnt);
       const int64_t alo = int64_t((uint64_t(uint32_t(from_lane(src_m, int32_t(uint64_t(lo[s]) >> 32)))) << 32) |
                                   uint32_t(from_lane(src_m, int32_t(lo[s]))));
-      // raw (source, class) of the batch's entries; a lane past its row's
-      // end reads entry 0 (there is one: some row of the tile has entries)
-      int64_t es[kB], ec[kB];
+      // Entries in groups of four: lane (r, g) holds entry j + g of row r as
+      // validated int32 (source, class), -1 when out of range; a lane past
+      // its row's end reads entry 0 (there is one: some row of the tile has
+      // entries).  The next group's raw indices load under this group's rows.
+      int64_t es = 0, ec = 0;
       auto fetch = [&](int j0) {
-#pragma unroll
-        for (int u = 0; u < kB; ++u) {
-          const int64_t e = j0 + u < acnt ? alo + j0 + u : 0;
-          es[u] = S.src[e];
-          ec[u] = S.cls[e];
-        }
+        const int64_t e = j0 + ag < acnt ? alo + j0 + ag : 0;
+        es = S.src[e];
+        ec = S.cls[e];
       };
-      // the first batch's entries, requested before the projection
       if (maxc > 0) fetch(0);
       // ---- LayerNorm + Q projection
       if constexpr (kPacked) {
@@ -288,11 +306,17 @@ __global__ void __launch_bounds__(waves_for<kStages>() * 64) attn_substage_kerne
         sq += __shfl_xor(sq, 16);
         sq += __shfl_xor(sq, 32);
         const float rstd = rsqrtf(sq * (1.f / kK) + 1e-5f);
+        // normalised values are bounded by sqrt(127): no saturation needed
         f16x8_t xb[4];
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-          for (int t = 0; t < 8; ++t) xb[ks][t] = f2h((xv[ks][t] - mean) * rstd);
+        for (int ks = 0; ks < 4; ++ks) {
+          uint4 w;
+          w.x = pack_f16x2_unit((xv[ks][0] - mean) * rstd, (xv[ks][1] - mean) * rstd);
+          w.y = pack_f16x2_unit((xv[ks][2] - mean) * rstd, (xv[ks][3] - mean) * rstd);
+          w.z = pack_f16x2_unit((xv[ks][4] - mean) * rstd, (xv[ks][5] - mean) * rstd);
+          w.w = pack_f16x2_unit((xv[ks][6] - mean) * rstd, (xv[ks][7] - mean) * rstd);
+          xb[ks] = __builtin_bit_cast(f16x8_t, w);
+        }
 #pragma unroll
         for (int nt = 0; nt < 8; ++nt) {
           f32x4_t d = {0.f, 0.f, 0.f, 0.f};
@@ -314,58 +338,45 @@ __global__ void __launch_bounds__(waves_for<kStages>() * 64) attn_substage_kerne
 #pragma unroll
       for (int i = 0; i < 32; ++i) acc[i] = 0.f;
       float m = -INFINITY, l = 0.f;
-      // Rows are fetched by the lanes whose entry exists only (a short row's
-      // lanes sit out the longer rows' batches without costing the address
-      // unit anything); a lane that sits out keeps the last finite values it
-      // held and weighs them by p = 0.
-      uint4 kr[kB][4], vr[kB][4], cr[kB][4];
-      float bs[kB];
+      const float* sbias_s = sbias + a.bias_off[s] + ag * int32_t(S.n_classes);
+      // Rows are fetched by the lanes whose entry exists only; a lane that
+      // sits out keeps the last finite values it held and weighs them by 0.
+      uint4 kr[4], vr[4], cr[4];
 #pragma unroll
-      for (int u = 0; u < kB; ++u) {
-        bs[u] = 0.f;
-#pragma unroll
-        for (int w = 0; w < 4; ++w) kr[u][w] = vr[u][w] = cr[u][w] = make_uint4(0u, 0u, 0u, 0u);
-      }
-      for (int j = 0; j < maxc; j += kB) {
-        bool ok[kB];
-#pragma unroll
-        for (int u = 0; u < kB; ++u) {
+      for (int w = 0; w < 4; ++w) kr[w] = vr[w] = cr[w] = make_uint4(0u, 0u, 0u, 0u);
+      for (int j = 0; j < maxc; j += 4) {
+        const int32_t s4 = es >= 0 && es < S.n_src ? int32_t(es) : -1;
+        const int32_t c4 = ec >= 0 && ec < S.n_classes ? int32_t(ec) : -1;
+        if (j + 4 < maxc) fetch(j + 4);
+        auto step = [&](int u, int32_t src, int32_t cls) {
           const bool in = j + u < acnt;
-          ok[u] = in && es[u] >= 0 && es[u] < S.n_src && ec[u] >= 0 && ec[u] < S.n_classes;
-          if (in && !ok[u]) raise_flag(a.flag, MANTIS_FLAG_INDEX);
-          if (ok[u]) {
-            const uint32_t sr = uint32_t(es[u]), cc = uint32_t(ec[u]);
-            load_head(S.k + (sr * uint32_t(S.ldk) + uint32_t(8 * ag)), kr[u]);
-            load_head(S.v + (sr * uint32_t(S.ldv) + uint32_t(8 * ag)), vr[u]);
-            if constexpr (kVcls) load_head(S.vcls + (cc * uint32_t(kK) + uint32_t(8 * ag)), cr[u]);
-            bs[u] = S.bias[uint32_t(ag) * uint32_t(S.n_classes) + cc];
+          const bool ok = in && src >= 0 && cls >= 0;
+          if (in && !ok) raise_flag(a.flag, MANTIS_FLAG_INDEX);
+          float bs = 0.f;
+          if (ok) {
+            const uint32_t sr = uint32_t(src), cc = uint32_t(cls);
+            load_head(S.k + (sr * uint32_t(S.ldk) + uint32_t(8 * ag)), kr);
+            load_head(S.v + (sr * uint32_t(S.ldv) + uint32_t(8 * ag)), vr);
+            if constexpr (kVcls) load_head(S.vcls + (cc * uint32_t(kK) + uint32_t(8 * ag)), cr);
+            bs = sbias_s[cls];
           }
-        }
-        if (j + kB < maxc) fetch(j + kB);  // the next batch's entries, under this batch's rows
-        float sc[kB];
-        float m_new = m;
+          const float sc = ok ? fmaf(dot32(qa, kr), a.scale, bs) : -INFINITY;
+          if (sc > m + kTau) {  // a new reference point (always on a row's first entry)
+            const float alpha = __expf(m - sc);
+            l *= alpha;
 #pragma unroll
-        for (int u = 0; u < kB; ++u) {
-          sc[u] = ok[u] ? fmaf(dot32(qa, kr[u]), a.scale, bs[u]) : -INFINITY;
-          m_new = fmaxf(m_new, sc[u]);
-        }
-        const bool any = m_new != -INFINITY;
-        const float alpha = any ? __expf(m - m_new) : 1.f;
-        l *= alpha;
-        float pr[kB];
-#pragma unroll
-        for (int u = 0; u < kB; ++u) {
-          pr[u] = any ? __expf(sc[u] - m_new) : 0.f;
-          l += pr[u];
-        }
-#pragma unroll
-        for (int i = 0; i < 32; ++i) acc[i] *= alpha;
-#pragma unroll
-        for (int u = 0; u < kB; ++u) {
-          axpy32(acc, pr[u], vr[u]);
-          if constexpr (kVcls) axpy32(acc, pr[u], cr[u]);
-        }
-        m = any ? m_new : m;
+            for (int i = 0; i < 32; ++i) acc[i] *= alpha;
+            m = sc;
+          }
+          const float pr = ok ? __expf(sc - m) : 0.f;
+          l += pr;
+          axpy32(acc, pr, vr);
+          if constexpr (kVcls) axpy32(acc, pr, cr);
+        };
+        step(0, from_quad<0>(s4), from_quad<0>(c4));
+        if (j + 1 < maxc) step(1, from_quad<1>(s4), from_quad<1>(c4));
+        if (j + 2 < maxc) step(2, from_quad<2>(s4), from_quad<2>(c4));
+        if (j + 3 < maxc) step(3, from_quad<3>(s4), from_quad<3>(c4));
       }
       // ---- output projection + residual, into the x registers
       {
@@ -373,12 +384,13 @@ __global__ void __launch_bounds__(waves_for<kStages>() * 64) attn_substage_kerne
         f16x8_t ab[4];
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-          // packed on the attention lane, read back by the lane of the MFMA layout
+          // packed on the attention lane (a convex combination of fp16 rows:
+          // in range), read back by the lane of the MFMA layout
           uint4 w;
-          w.x = uint32_t(from_lane(src_a, int32_t(pack_f16x2(acc[8 * ks] * inv, acc[8 * ks + 1] * inv))));
-          w.y = uint32_t(from_lane(src_a, int32_t(pack_f16x2(acc[8 * ks + 2] * inv, acc[8 * ks + 3] * inv))));
-          w.z = uint32_t(from_lane(src_a, int32_t(pack_f16x2(acc[8 * ks + 4] * inv, acc[8 * ks + 5] * inv))));
-          w.w = uint32_t(from_lane(src_a, int32_t(pack_f16x2(acc[8 * ks + 6] * inv, acc[8 * ks + 7] * inv))));
+          w.x = uint32_t(from_lane(src_a, int32_t(pack_f16x2_unit(acc[8 * ks] * inv, acc[8 * ks + 1] * inv))));
+          w.y = uint32_t(from_lane(src_a, int32_t(pack_f16x2_unit(acc[8 * ks + 2] * inv, acc[8 * ks + 3] * inv))));
+          w.z = uint32_t(from_lane(src_a, int32_t(pack_f16x2_unit(acc[8 * ks + 4] * inv, acc[8 * ks + 5] * inv))));
+          w.w = uint32_t(from_lane(src_a, int32_t(pack_f16x2_unit(acc[8 * ks + 6] * inv, acc[8 * ks + 7] * inv))));
           ab[ks] = __builtin_bit_cast(f16x8_t, w);
         }
 #pragma unroll
@@ -482,7 +494,13 @@ extern "C" int32_t mantis_attention_substages(void* x, int32_t x_dtype, int64_t 
   a.ldx = ldx;
   a.n_rows = n_rows;
   a.order = row_order;
-  for (int s = 0; s < n_stages; ++s) a.st[s] = to_stage(stages[s]);
+  int64_t pool = 0;
+  for (int s = 0; s < n_stages; ++s) {
+    a.st[s] = to_stage(stages[s]);
+    a.bias_off[s] = int32_t(pool);
+    pool += 4 * stages[s].n_classes;
+  }
+  if (pool > kBiasPool) return MANTIS_E_ARG;  // the class-bias tables must fit their LDS pool
   a.scale = 0.17677669529663687f;  // 1/sqrt(32)
   a.flag = err_flag;
   const bool vc = stages[0].vcls != nullptr;

@@ -20,7 +20,10 @@
 // tiles are packed to fp16 as the second product's B fragments (K slots
 // {4g..4g+3, 16+4g..16+4g+3} of each 32-step, matched by the W3 reads).
 // W1, W2 and W3 live in LDS for the persistent workgroup (8 wavefronts,
-// one workgroup per CU).  An optional row order (a permutation of the cells)
+// one workgroup per CU).  Tiles are dealt out XCD-contiguously: the
+// workgroups of one XCD (dispatch is round-robin over the 8 XCDs) sweep one
+// contiguous eighth of the tiles, so the action-projection rows a position's
+// cells gather are fetched into one XCD's L2.  An optional row order (a permutation of the cells)
 // groups cells of similar decoder run lengths into tiles, since a tile's
 // walk runs as long as its longest run; each cell's arithmetic is the same
 // in any order.
@@ -40,6 +43,7 @@ constexpr int kPitch = kK + 8;
 constexpr int kP3 = kN1 + 8;
 constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * 64;
+constexpr int kXcds = 8;
 
 struct HeadArgs {
   const void* c;
@@ -56,7 +60,7 @@ struct HeadArgs {
   int64_t n_acls;
   const float* empty_rows;   // (3, 128)
   const int64_t* act_empty;  // (n_cells, 3)
-  const _Float16* head_tab;   // (n_dcls, 256), lane-blocked columns
+  const _Float16* head_tab;   // (n_dcls, 256), quad-chunked columns
   int64_t n_dcls;
   const float* g_half;       // (n_pos, 256)
   int64_t n_pos;
@@ -99,16 +103,18 @@ __global__ void __launch_bounds__(kThreads) cell_heads_kernel(HeadArgs a) {
   const int src_m = 16 * aq + ar;                  // MFMA lane of this walk lane's (cell, group)
   const int src_a = 4 * l16 + g;                   // walk lane of this MFMA lane's (cell, group)
   const int64_t n_tiles = (a.n_cells + 15) / 16;
-  const int64_t stride = int64_t(gridDim.x) * kWaves;
+  const int xcd = int(blockIdx.x % kXcds);
+  const int64_t stride = (int64_t(gridDim.x) - xcd + kXcds - 1) / kXcds * kWaves;  // waves of this XCD
+  const int64_t t_begin = n_tiles * xcd / kXcds, t_end = n_tiles * (xcd + 1) / kXcds;
   // the cell of a tile slot (raw: validated where it is used), one tile ahead
   auto order_at = [&](int64_t t) -> int64_t {
     const int64_t slot = t * 16 + l16;
     if (!a.order) return slot;
     return a.order[slot < a.n_cells ? slot : 0];
   };
-  const int64_t tile0 = int64_t(blockIdx.x) * kWaves + wave;
-  int64_t next_row = tile0 < n_tiles ? order_at(tile0) : 0;
-  for (int64_t tile = tile0; tile < n_tiles; tile += stride) {
+  const int64_t tile0 = t_begin + int64_t(blockIdx.x / kXcds) * kWaves + wave;
+  int64_t next_row = tile0 < t_end ? order_at(tile0) : 0;
+  for (int64_t tile = tile0; tile < t_end; tile += stride) {
     // an offset the compiler cannot see through: keeps the weight-fragment
     // reads inside the loop instead of hoisting them into registers
     int lds_off = 0;
@@ -117,7 +123,7 @@ __global__ void __launch_bounds__(kThreads) cell_heads_kernel(HeadArgs a) {
     const _Float16* w2s = sw2 + lds_off;
     const _Float16* w3s = sw3 + lds_off;
     const int64_t row = next_row;
-    next_row = order_at(tile + stride < n_tiles ? tile + stride : tile);
+    next_row = order_at(tile + stride < t_end ? tile + stride : tile);
     const bool in_tile = tile * 16 + l16 < a.n_cells;
     const bool live = in_tile && row >= 0 && row < a.n_cells;
     if (in_tile && !live) raise_flag(a.flag, MANTIS_FLAG_INDEX);
@@ -187,7 +193,7 @@ __global__ void __launch_bounds__(kThreads) cell_heads_kernel(HeadArgs a) {
       for (int t = 0; t < 8; ++t) xb[ks][t] = f2h(xv[ks][t]);
     // ---- the walk: action rows relu(pre[win] + table[acls]) (features
     // 32 i + 8 aq + t) and class rows head_tab[dcls] (features 16 nt + 4 aq + t,
-    // stored lane-blocked: this lane's 64 values are contiguous)
+    // stored quad-chunked: chunk k of the four lanes is the 64 bytes at 32 k)
     float av[32], ev[64];
 #pragma unroll
     for (int i = 0; i < 32; ++i) av[i] = 0.f;
@@ -206,7 +212,7 @@ __global__ void __launch_bounds__(kThreads) cell_heads_kernel(HeadArgs a) {
         }
 #pragma unroll
         for (int k = 0; k < 8; ++k)
-          ht[k] = *reinterpret_cast<const uint4*>(a.head_tab + (uint32_t(id) * uint32_t(kN1) + uint32_t(64 * aq + 8 * k)));
+          ht[k] = *reinterpret_cast<const uint4*>(a.head_tab + (uint32_t(id) * uint32_t(kN1) + uint32_t(32 * k + 8 * aq)));
       }
       if (j + 1 < maxc) fetch(j + 1);
       if (ok) {
@@ -353,8 +359,11 @@ extern "C" int32_t mantis_cell_heads(const void* c, int32_t c_dtype, int32_t lay
   if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
                                               hipSuccess || cus <= 0)
     cus = 256;
+  // one persistent workgroup per CU, a multiple of the XCD count
   const int64_t tiles = (n_cells + 15) / 16;
-  int64_t grid = std::min<int64_t>(cus, (tiles + kWaves - 1) / kWaves);
+  int64_t grid = ((int64_t(cus) + kXcds - 1) / kXcds) * kXcds;
+  const int64_t need = ((tiles + kWaves - 1) / kWaves + kXcds - 1) / kXcds * kXcds;
+  if (need < grid) grid = need;
   const dim3 gd{unsigned(grid)}, bd{unsigned(kThreads)};
   hipStream_t s = as_stream(stream);
   if (c_dtype == MANTIS_F32 && layer_norm)

@@ -780,16 +780,18 @@ def interleave_heads(t: Tensor) -> Tensor:
     return t.index_select(-1, idx)
 
 
-def _head_tab_blocked_index() -> Tensor:
+def _head_tab_quad_index() -> Tensor:
     j = torch.arange(256)
-    q, nt, t = j // 64, (j // 4) % 16, j % 4
-    return 16 * nt + 4 * q + t
+    k, q, u = j // 32, (j // 8) % 4, j % 8
+    return 16 * (2 * k + u // 4) + 4 * q + u % 4
 
 
-# column j of the cell heads' lane-blocked class table holds natural column
-# HEAD_TAB_BLOCKED[j]: lane group q's 64 features (16 nt + 4 q + t) are the
-# contiguous columns 64 q .. 64 q + 63
-HEAD_TAB_BLOCKED = _head_tab_blocked_index()
+# column j of the cell heads' class table holds natural column
+# HEAD_TAB_QUAD[j]: lane group q's 64 features (16 nt + 4 q + t, in nt-major
+# order) are split into eight 16-byte chunks, and chunk k of the four lane
+# groups is the contiguous 64 bytes at 32 k, so each of the eight loads of a
+# cell's four lanes reads one 64-byte piece of the row
+HEAD_TAB_QUAD = _head_tab_quad_index()
 
 _DEVICE_CONSTS: dict[tuple[int, torch.device], Tensor] = {}
 
@@ -929,9 +931,9 @@ def cell_heads(c: Tensor, w1: Tensor, b1: Tensor, w2: Tensor, w3: Tensor, b3: Te
         raise ValueError("empty_rows (3, 128), head_tab (n, 256) and g_half (P, 256) expected")
     if act_table.ndim != 2 or act_table.shape[1] != 128:
         raise ValueError("act_table must be (n, 128)")
-    # the kernel gathers both tables in fp16, the class table lane-blocked
+    # the kernel gathers both tables in fp16, the class table quad-chunked
     act_table = act_table.to(torch.float16).contiguous()
-    head_tab = head_tab.index_select(1, _const_on(HEAD_TAB_BLOCKED, head_tab.device)).to(torch.float16).contiguous()
+    head_tab = head_tab.index_select(1, _const_on(HEAD_TAB_QUAD, head_tab.device)).to(torch.float16).contiguous()
     act_empty = _i64(act_empty, "act_empty")
     cell_pos, dec_ptr = _i64(cell_pos, "cell_pos"), _i64(dec_ptr, "dec_ptr")
     dec_window, act_class, dec_class = _i64(dec_window, "dec_window"), _i64(act_class, "act_class"), \

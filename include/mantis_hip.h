@@ -363,6 +363,8 @@ int32_t mantis_attention_substage(float* x, int64_t ldx, int64_t n_rows, const v
  * in which the rows are visited: 16 consecutive entries form a tile, and a tile's
  * entry loop runs as long as its longest row, so an order that groups rows
  * of similar entry counts saves work.  The results do not depend on it.
+ * The stages' class-bias tables are staged on chip together: the sum over
+ * stages of n_classes must not exceed 1344 (else MANTIS_E_ARG).
  * Replaces the two cell sub-stages of the reference's _cell_stage (cells <-
  * windows, then cells <- stones; model.py:397-490, kernels
  * cell_latents.py:213-285, 834-1001).
@@ -400,8 +402,8 @@ int32_t mantis_attention_substages(void* x, int32_t x_dtype, int64_t ldx, int64_
  * c: (n_cells, 128) rows in c_dtype (fp32 or fp16), row
  * stride ldc; w1, w2: (256, 128) fp16; b1 (256); w3 (16, 256) fp16; b3 (16);
  * pre (n_w, 128) and act_table (n_acls, 128) fp16; head_tab (n_dcls, 256)
- * fp16 with lane-blocked columns (column 64*q + 4*nt + t holds feature
- * 16*nt + 4*q + t); empty_rows (3, 128), g_half (n_pos, 256) fp32;
+ * fp16 with quad-chunked columns (column 32*k + 8*q + u holds feature
+ * 16*(2*k + u/4) + 4*q + u%4); empty_rows (3, 128), g_half (n_pos, 256) fp32;
  * act_empty (n_cells, 3) and the index arrays int64; out (n_cells, 16) fp32.
  * row_order, when not NULL, is a permutation of the cells (int32) in which
  * they are grouped into 16-cell tiles (see mantis_segment_order); the

@@ -60,12 +60,13 @@ def test_head_interleave_layout():
         ops.interleave_heads(torch.zeros(3, 100))
 
 
-def test_head_tab_blocked_layout():
-    # lane group q's 64 features 16 nt + 4 q + t are columns 64 q .. 64 q + 63
+def test_head_tab_quad_layout():
+    # lane group q's 64 features (16 nt + 4 q + t, nt-major) in eight
+    # 16-byte chunks; chunk k of the four lane groups is columns 32 k .. 32 k + 31
     from mantisnet import ops
-    idx = ops.HEAD_TAB_BLOCKED
+    idx = ops.HEAD_TAB_QUAD
     assert sorted(idx.tolist()) == list(range(256))
     for q in range(4):
-        for nt in range(16):
-            for t in range(4):
-                assert idx[64 * q + 4 * nt + t] == 16 * nt + 4 * q + t
+        for i in range(64):  # the lane's i-th value: nt = i // 4, t = i % 4
+            k, u = i // 8, i % 8
+            assert idx[32 * k + 8 * q + u] == 16 * (i // 4) + 4 * q + i % 4
