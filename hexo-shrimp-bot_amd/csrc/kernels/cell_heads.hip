@@ -75,11 +75,15 @@ struct HeadArgs {
   int32_t* flag;
 };
 
-template <typename Tin, bool kLN>
+// hi + lo fp16 pair of x (lo: the residual of the rounding, unsaturated)
+__device__ __forceinline__ _Float16 f16_lo(float x, _Float16 hi) { return _Float16(x - float(hi)); }
+
+template <typename Tin, bool kLN, bool kComp>
 __global__ void __launch_bounds__(kThreads) cell_heads_kernel(HeadArgs a) {
+  constexpr int kW3Rows = kComp ? 2 * kN3 : kN3;  // W3, or [W3 hi; W3 lo]
   __shared__ __attribute__((aligned(16))) _Float16 sw1[kN1 * kPitch];
   __shared__ __attribute__((aligned(16))) _Float16 sw2[kN1 * kPitch];
-  __shared__ __attribute__((aligned(16))) _Float16 sw3[kN3 * kP3];
+  __shared__ __attribute__((aligned(16))) _Float16 sw3[kW3Rows * kP3];
   // the biases: read from LDS, they add no global-load wait to the tile loop
   // (loads and stores share one in-order counter)
   __shared__ __attribute__((aligned(16))) float sb1[kN1];
@@ -91,7 +95,7 @@ __global__ void __launch_bounds__(kThreads) cell_heads_kernel(HeadArgs a) {
     *reinterpret_cast<uint4*>(sw1 + r * kPitch + cc) = *reinterpret_cast<const uint4*>(a.w1 + r * kK + cc);
     *reinterpret_cast<uint4*>(sw2 + r * kPitch + cc) = *reinterpret_cast<const uint4*>(a.w2 + r * kK + cc);
   }
-  for (int i = threadIdx.x; i < kN3 * (kN1 / 8); i += kThreads) {
+  for (int i = threadIdx.x; i < kW3Rows * (kN1 / 8); i += kThreads) {
     const int r = i / (kN1 / 8), cc = (i % (kN1 / 8)) * 8;
     *reinterpret_cast<uint4*>(sw3 + r * kP3 + cc) = *reinterpret_cast<const uint4*>(a.w3 + r * kN1 + cc);
   }
@@ -186,11 +190,14 @@ __global__ void __launch_bounds__(kThreads) cell_heads_kernel(HeadArgs a) {
 #pragma unroll
         for (int t = 0; t < 8; ++t) xv[ks][t] = (xv[ks][t] - mean) * rstd;
     }
-    f16x8_t xb[4];
+    f16x8_t xb[4], xl[kComp ? 4 : 1];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-      for (int t = 0; t < 8; ++t) xb[ks][t] = f2h(xv[ks][t]);
+      for (int t = 0; t < 8; ++t) {
+        xb[ks][t] = f2h(xv[ks][t]);
+        if constexpr (kComp) xl[ks][t] = f16_lo(xv[ks][t], xb[ks][t]);
+      }
     // ---- the walk: action rows relu(pre[win] + table[acls]) (features
     // 32 i + 8 aq + t) and class rows head_tab[dcls] (features 16 nt + 4 aq + t,
     // stored quad-chunked: chunk k of the four lanes is the 64 bytes at 32 k)
@@ -250,15 +257,31 @@ __global__ void __launch_bounds__(kThreads) cell_heads_kernel(HeadArgs a) {
     }
     // ---- back to the MFMA layout: the action rows as fp16 B fragments, the
     // class sums as the fp32 addends of the hidden tiles
-    f16x8_t ab[4];
+    f16x8_t ab[4], al[kComp ? 4 : 1];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
+      uint32_t hw[4], lw[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        hw[i] = pack_f16x2(av[8 * ks + 2 * i], av[8 * ks + 2 * i + 1]);
+        if constexpr (kComp) {
+          const f16x2_t h = __builtin_bit_cast(f16x2_t, hw[i]);
+          lw[i] = pack_f16x2_unit(av[8 * ks + 2 * i] - float(h[0]), av[8 * ks + 2 * i + 1] - float(h[1]));
+        }
+      }
       uint4 w;
-      w.x = uint32_t(from_lane(src_a, int32_t(pack_f16x2(av[8 * ks], av[8 * ks + 1]))));
-      w.y = uint32_t(from_lane(src_a, int32_t(pack_f16x2(av[8 * ks + 2], av[8 * ks + 3]))));
-      w.z = uint32_t(from_lane(src_a, int32_t(pack_f16x2(av[8 * ks + 4], av[8 * ks + 5]))));
-      w.w = uint32_t(from_lane(src_a, int32_t(pack_f16x2(av[8 * ks + 6], av[8 * ks + 7]))));
+      w.x = uint32_t(from_lane(src_a, int32_t(hw[0])));
+      w.y = uint32_t(from_lane(src_a, int32_t(hw[1])));
+      w.z = uint32_t(from_lane(src_a, int32_t(hw[2])));
+      w.w = uint32_t(from_lane(src_a, int32_t(hw[3])));
       ab[ks] = __builtin_bit_cast(f16x8_t, w);
+      if constexpr (kComp) {
+        w.x = uint32_t(from_lane(src_a, int32_t(lw[0])));
+        w.y = uint32_t(from_lane(src_a, int32_t(lw[1])));
+        w.z = uint32_t(from_lane(src_a, int32_t(lw[2])));
+        w.w = uint32_t(from_lane(src_a, int32_t(lw[3])));
+        al[ks] = __builtin_bit_cast(f16x8_t, w);
+      }
     }
     f32x4_t ext[kN1 / 16];
 #pragma unroll
@@ -266,8 +289,9 @@ __global__ void __launch_bounds__(kThreads) cell_heads_kernel(HeadArgs a) {
 #pragma unroll
       for (int t = 0; t < 4; ++t)
         ext[nt][t] = __int_as_float(from_lane(src_a, __float_as_int(ev[4 * nt + t])));
-    // ---- hidden tiles: h^T = W1 . x^T + W2 . acts^T + b1 + ext + g_half[pos]
-    f16x8_t hb[kN1 / 32];
+    // ---- hidden tiles: h^T = W1 . x^T + W2 . acts^T + b1 + ext + g_half[pos],
+    // each 32-feature slice fed to out^T (16 x 16 cells) += W3 . h^T as it is formed
+    f32x4_t y = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int k = 0; k < kN1 / 32; ++k) {
       f32x4_t hv[2];
@@ -279,8 +303,10 @@ __global__ void __launch_bounds__(kThreads) cell_heads_kernel(HeadArgs a) {
         for (int ks = 0; ks < 4; ++ks) {
           const f16x8_t wf = *reinterpret_cast<const f16x8_t*>(w1s + (16 * nt + l16) * kPitch + 32 * ks + 8 * g);
           acc = mfma16x16x32(wf, xb[ks], acc);
+          if constexpr (kComp) acc = mfma16x16x32(wf, xl[ks], acc);
           const f16x8_t wf2 = *reinterpret_cast<const f16x8_t*>(w2s + (16 * nt + l16) * kPitch + 32 * ks + 8 * g);
           acc = mfma16x16x32(wf2, ab[ks], acc);
+          if constexpr (kComp) acc = mfma16x16x32(wf2, al[ks], acc);
         }
         const int f = 16 * nt + 4 * g;
         float4 add = *reinterpret_cast<const float4*>(sb1 + f);
@@ -295,22 +321,30 @@ __global__ void __launch_bounds__(kThreads) cell_heads_kernel(HeadArgs a) {
         acc[3] = fmaxf(acc[3] + add.w, 0.f);
         hv[half] = acc;
       }
+      f16x8_t hb, hl;
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        hb[k][t] = f2h(hv[0][t]);
-        hb[k][4 + t] = f2h(hv[1][t]);
+        hb[t] = f2h(hv[0][t]);
+        hb[4 + t] = f2h(hv[1][t]);
+        if constexpr (kComp) {
+          hl[t] = f16_lo(hv[0][t], hb[t]);
+          hl[4 + t] = f16_lo(hv[1][t], hb[4 + t]);
+        }
+      }
+      // the W3 columns of this slice: K slots {4g..4g+3, 16+4g..16+4g+3}
+      auto w3frag = [&](int row0) {
+        const _Float16* wr = w3s + (row0 + l16) * kP3 + 32 * k;
+        const uint2 lo = *reinterpret_cast<const uint2*>(wr + 4 * g);
+        const uint2 hi = *reinterpret_cast<const uint2*>(wr + 16 + 4 * g);
+        return __builtin_bit_cast(f16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
+      };
+      const f16x8_t wf3 = w3frag(0);
+      y = mfma16x16x32(wf3, hb, y);
+      if constexpr (kComp) {
+        y = mfma16x16x32(wf3, hl, y);
+        y = mfma16x16x32(w3frag(kN3), hb, y);
       }
       __builtin_amdgcn_sched_barrier(0);
-    }
-    // ---- out^T (16 x 16 cells) = W3 . h^T
-    f32x4_t y = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ks = 0; ks < kN1 / 32; ++ks) {
-      const _Float16* wr = w3s + l16 * kP3 + 32 * ks;
-      const uint2 lo = *reinterpret_cast<const uint2*>(wr + 4 * g);
-      const uint2 hi = *reinterpret_cast<const uint2*>(wr + 16 + 4 * g);
-      const f16x8_t wf = __builtin_bit_cast(f16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
-      y = mfma16x16x32(wf, hb[ks], y);
     }
     if (live) {
       const float4 bb = *reinterpret_cast<const float4*>(sb3 + 4 * g);
@@ -325,7 +359,8 @@ __global__ void __launch_bounds__(kThreads) cell_heads_kernel(HeadArgs a) {
 
 using namespace mantis;
 
-extern "C" int32_t mantis_cell_heads(const void* c, int32_t c_dtype, int32_t layer_norm, int64_t ldc, int64_t n_cells,
+extern "C" int32_t mantis_cell_heads(const void* c, int32_t c_dtype, int32_t layer_norm, int32_t compensated,
+                                     int64_t ldc, int64_t n_cells,
                                      const int32_t* row_order, const void* w1, const float* b1,
                                      const void* w2, const void* w3, const float* b3, const void* pre, int64_t n_w,
                                      const void* act_table, int64_t n_acls, const float* empty_rows,
@@ -366,14 +401,18 @@ extern "C" int32_t mantis_cell_heads(const void* c, int32_t c_dtype, int32_t lay
   if (need < grid) grid = need;
   const dim3 gd{unsigned(grid)}, bd{unsigned(kThreads)};
   hipStream_t s = as_stream(stream);
-  if (c_dtype == MANTIS_F32 && layer_norm)
-    cell_heads_kernel<float, true><<<gd, bd, 0, s>>>(a);
+  if (compensated) {
+    // the knob-off heads: fp32 cell sums, no LayerNorm
+    if (c_dtype != MANTIS_F32 || layer_norm) return MANTIS_E_ARG;
+    cell_heads_kernel<float, false, true><<<gd, bd, 0, s>>>(a);
+  } else if (c_dtype == MANTIS_F32 && layer_norm)
+    cell_heads_kernel<float, true, false><<<gd, bd, 0, s>>>(a);
   else if (c_dtype == MANTIS_F32)
-    cell_heads_kernel<float, false><<<gd, bd, 0, s>>>(a);
+    cell_heads_kernel<float, false, false><<<gd, bd, 0, s>>>(a);
   else if (c_dtype == MANTIS_F16 && !layer_norm)
-    cell_heads_kernel<_Float16, false><<<gd, bd, 0, s>>>(a);
+    cell_heads_kernel<_Float16, false, false><<<gd, bd, 0, s>>>(a);
   else if (c_dtype == MANTIS_F16)
-    cell_heads_kernel<_Float16, true><<<gd, bd, 0, s>>>(a);
+    cell_heads_kernel<_Float16, true, false><<<gd, bd, 0, s>>>(a);
   else
     return MANTIS_E_ARG;
   return launched();

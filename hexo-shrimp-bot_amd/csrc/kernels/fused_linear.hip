@@ -19,11 +19,12 @@
 // {4g..4g+3, 16+4g..16+4g+3} of each 32-step, matched by the W3 reads).
 // The weights live in LDS for the whole (persistent) workgroup; rows stream
 // from HBM once, the next tile's rows in flight while the current computes.
-// Compensated weights (kSplit): every weight matrix arrives as an fp16 pair
-// [hi; lo] with lo = fp16(W - hi), and every product runs twice (hi, then lo
-// into the same fp32 accumulator), so the weights carry ~22 mantissa bits
-// while the rows stay fp16 operands.  It doubles the weights' LDS and the
-// MFMA work, which row-streaming launches have to spare.
+// Compensated products (kSplit): every weight matrix arrives as an fp16 pair
+// [hi; lo] with lo = fp16(W - hi), and the fp32 rows are split the same way
+// (x = x_hi + x_lo); each product runs as W_hi x_hi + W_lo x_hi + W_hi x_lo
+// into one fp32 accumulator (the W_lo x_lo term is below fp32 rounding), so
+// weights and rows both act with ~22 mantissa bits.  It doubles the weights'
+// LDS and triples the MFMA work, which row-streaming launches have to spare.
 #include "common.hpp"
 #include "mfma.hpp"
 
@@ -223,12 +224,15 @@ __global__ void __launch_bounds__((threads_for<N1, kX2, kStage2>())) fused_linea
 #pragma unroll
         for (int t = 0; t < 8; ++t) xv[ks][t] = (xv[ks][t] - mean) * rstd;
     }
-    f16x8_t xb[4];
+    f16x8_t xb[4], xl[kSplit ? 4 : 1];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-      for (int t = 0; t < 8; ++t) xb[ks][t] = f2h(xv[ks][t]);
-    f16x8_t x2b[4];
+      for (int t = 0; t < 8; ++t) {
+        xb[ks][t] = f2h(xv[ks][t]);
+        if constexpr (kSplit) xl[ks][t] = _Float16(xv[ks][t] - float(xb[ks][t]));
+      }
+    f16x8_t x2b[4], x2l[kSplit && kX2 ? 4 : 1];
     if constexpr (kX2) {
       const TX2* x2p = static_cast<const TX2*>(a.x2);
 #pragma unroll
@@ -239,7 +243,10 @@ __global__ void __launch_bounds__((threads_for<N1, kX2, kStage2>())) fused_linea
 #pragma unroll
           for (int t = 0; t < 8; ++t) v2[t] = 0.f;
 #pragma unroll
-        for (int t = 0; t < 8; ++t) x2b[ks][t] = f2h(v2[t]);
+        for (int t = 0; t < 8; ++t) {
+          x2b[ks][t] = f2h(v2[t]);
+          if constexpr (kSplit) x2l[ks][t] = _Float16(v2[t] - float(x2b[ks][t]));
+        }
       }
     }
     // ---- row-group offset of the per-group add (validated once per row)
@@ -259,12 +266,19 @@ __global__ void __launch_bounds__((threads_for<N1, kX2, kStage2>())) fused_linea
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
         const int off = (16 * nt + l16) * kPitch + 32 * ks + 8 * g;
-        acc = mfma16x16x32(*reinterpret_cast<const f16x8_t*>(sw1 + off), xb[ks], acc);
-        if constexpr (kSplit) acc = mfma16x16x32(*reinterpret_cast<const f16x8_t*>(sw1 + kLo1 + off), xb[ks], acc);
+        const f16x8_t w1f = *reinterpret_cast<const f16x8_t*>(sw1 + off);
+        acc = mfma16x16x32(w1f, xb[ks], acc);
+        if constexpr (kSplit) {
+          acc = mfma16x16x32(*reinterpret_cast<const f16x8_t*>(sw1 + kLo1 + off), xb[ks], acc);
+          acc = mfma16x16x32(w1f, xl[ks], acc);
+        }
         if constexpr (kX2) {
-          acc = mfma16x16x32(*reinterpret_cast<const f16x8_t*>(sw2 + off), x2b[ks], acc);
-          if constexpr (kSplit)
+          const f16x8_t w2f = *reinterpret_cast<const f16x8_t*>(sw2 + off);
+          acc = mfma16x16x32(w2f, x2b[ks], acc);
+          if constexpr (kSplit) {
             acc = mfma16x16x32(*reinterpret_cast<const f16x8_t*>(sw2 + kLo1 + off), x2b[ks], acc);
+            acc = mfma16x16x32(w2f, x2l[ks], acc);
+          }
         }
       }
       // the tile's four features of this lane: 16 nt + 4 g .. +3, or with
@@ -521,5 +535,7 @@ extern "C" int32_t mantis_fused_linear_split(const void* x, int32_t x_dtype, int
   // first layer of a pair MLP: relu(LN(x) W1^T + x2 W2^T + b1), fp32 out
   if (hx2 && ln && r && out_mode == 1 && x2_dtype == MANTIS_F16)
     return launch<float, _Float16, true, 128, true, true, false, 1, true>(a, s);
+  if (hx2 && ln && r && out_mode == 1 && x2_dtype == MANTIS_F32)
+    return launch<float, float, true, 128, true, true, false, 1, true>(a, s);
   return MANTIS_E_ARG;
 }

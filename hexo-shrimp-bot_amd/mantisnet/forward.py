@@ -229,6 +229,8 @@ def _prepare(model, P) -> dict[str, Tensor]:
     b3[0] = P["mlp_p.out.bias"][0]
     b3[1:4] = P["mlp_q.out.bias"]
     t["head3.w"], t["head3.b"] = w3.to(HALF).contiguous(), b3
+    # [hi; lo] fp16 pair of the output layer for the compensated heads
+    t["head3c.w"] = ops.split_weight(w3)
     t["glin_b"] = torch.cat([P["mlp_p.lin_b.weight"], P["mlp_q.lin_b.weight"]]).contiguous()  # (256, 128)
     return t
 
@@ -455,7 +457,9 @@ def _cell_pass(W, P, pb, plan: Plan, b: Batch, w):
     u_cp(LN w) through the empty cells the windows share).  The batch's
     compact relay views are used when it carries them; the plan's views over
     all legal cells give the same sums in the same order otherwise."""
-    x = FL(w, W[pb + "cp_u.w"], W[pb + "cp_u.b"], layer_norm=True, split=True)  # (n_w, 128) fp16
+    # u_cp's rows and the relay sums stay fp32: they are summed over up to 18
+    # windows and 6 cells, so their fp16 roundings would add up coherently
+    x = FL(w, W[pb + "cp_u.w"], W[pb + "cp_u.b"], layer_norm=True, split=True, out_dtype=F32)
     if getattr(b, "relay_cell_ptr", None) is not None:
         views = (b.relay_cell_ptr, b.relay_window, b.relay_class, b.relay_win_ptr, b.relay_wcell)
     else:
@@ -610,10 +614,14 @@ def _head_rows(model, w: Tensor, g: Tensor, cells: Tensor, b: Batch, plan: Plan,
     decoder windows' ln_out rows (model.py:985-1029)."""
     if model.cfg.uses_cell_state and cells is None:
         raise ValueError("cell state is on but the trunk's cell rows were not passed to the decoder")
-    if not model.cfg.uses_cell_state:
+    compensated = not model.cfg.uses_cell_state
+    if compensated:
+        # each cell reads the fp32 sum of up to 18 window rows: the heads run
+        # their products on compensated operands (the sums' and the hidden
+        # activations' fp16 roundings would otherwise add up coherently)
         if cells is not None:
             raise ValueError("cell rows were passed but cell state is off")
-        cells = ops.run_reduce(w, b.dec_window, plan.dec_cell_ptr, plan.n_c, HALF)
+        cells = ops.run_reduce(w, b.dec_window, plan.dec_cell_ptr, plan.n_c, F32)
         raw_cells = False
     W = W or _prepared(model)
     P = W.params
@@ -622,10 +630,11 @@ def _head_rows(model, w: Tensor, g: Tensor, cells: Tensor, b: Batch, plan: Plan,
     g_half = F.linear(g.float(), W["glin_b"]).contiguous()  # (P, 256)
     x = cells if cells.dtype in (HALF, F32) else cells.float()
     key = "head1ln" if raw_cells else "head1"
-    return ops.cell_heads(x.contiguous(), W[key + ".w"], W[key + ".b"], W["head2.w"], W["head3.w"], W["head3.b"], pre,
+    return ops.cell_heads(x.contiguous(), W[key + ".w"], W[key + ".b"], W["head2.w"],
+                          W["head3c.w" if compensated else "head3.w"], W["head3.b"], pre,
                           P["act_table.weight"], empty_rows, b.act_empty, W["head_tab"], g_half, b.cell_pos,
                           plan.dec_cell_ptr, b.dec_window, b.act_class, b.dec_class, layer_norm=raw_cells,
-                          row_order=plan.head_order)
+                          row_order=plan.head_order, compensated=compensated)
 
 
 @torch.no_grad()

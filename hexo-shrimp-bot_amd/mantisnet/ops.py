@@ -908,11 +908,13 @@ def attention_substage(x: Tensor, wq: Tensor, bq: Tensor, kv: Tensor, bias: Tens
 def cell_heads(c: Tensor, w1: Tensor, b1: Tensor, w2: Tensor, w3: Tensor, b3: Tensor, pre: Tensor,
                act_table: Tensor, empty_rows: Tensor, act_empty: Tensor, head_tab: Tensor, g_half: Tensor,
                cell_pos: Tensor, dec_ptr: Tensor, dec_window: Tensor, act_class: Tensor, dec_class: Tensor,
-               layer_norm: bool, row_order: Tensor | None = None) -> Tensor:
+               layer_norm: bool, row_order: Tensor | None = None, compensated: bool = False) -> Tensor:
     """(n_cells, 16) fp32 head rows of every cell in one launch (see
     mantis_cell_heads in include/mantis_hip.h): column 0 the policy logit,
     1..3 the critic logits.  ``row_order`` (int32 permutation of the cells)
-    sets their grouping into tiles; the results do not depend on it."""
+    sets their grouping into tiles; the results do not depend on it.
+    ``compensated`` (fp32 rows, no LayerNorm; w3 (32, 256) = [hi; lo]) runs
+    the three products on hi + lo fp16 operand pairs."""
     dev = _on_gpu(c, w1, b1, w2, w3, b3, pre, act_table, empty_rows, act_empty, head_tab, g_half, cell_pos, dec_ptr,
                   dec_window, act_class, dec_class, row_order)
     if row_order is not None and (row_order.dtype != torch.int32 or row_order.shape != (c.shape[0],)):
@@ -920,7 +922,10 @@ def cell_heads(c: Tensor, w1: Tensor, b1: Tensor, w2: Tensor, w3: Tensor, b3: Te
     n = c.shape[0]
     if c.ndim != 2 or c.shape[1] != 128 or c.stride(1) != 1 or c.dtype not in (torch.float32, torch.float16):
         raise ValueError("c must be (n_cells, 128) fp32 or fp16 rows")
-    for t, shape, name in ((w1, (256, 128), "w1"), (w2, (256, 128), "w2"), (w3, (16, 256), "w3")):
+    if compensated and (c.dtype != torch.float32 or layer_norm):
+        raise ValueError("the compensated heads take fp32 rows without LayerNorm")
+    for t, shape, name in ((w1, (256, 128), "w1"), (w2, (256, 128), "w2"),
+                           (w3, (32 if compensated else 16, 256), "w3")):
         if t.shape != shape or t.dtype != torch.float16 or not t.is_contiguous():
             raise ValueError(f"{name} must be a contiguous fp16 {shape} matrix")
     if pre.ndim != 2 or pre.shape[1] != 128 or pre.dtype != torch.float16 or not pre.is_contiguous():
@@ -951,7 +956,8 @@ def cell_heads(c: Tensor, w1: Tensor, b1: Tensor, w2: Tensor, w3: Tensor, b3: Te
         flops = n * 2 * (2 * 256 * 128 + 16 * 256)
         _launch("cell_heads", nbytes, flops, lambda: _check(
             _lib().mantis_cell_heads(
-                _ptr(c), _dt(c), int(layer_norm), c.stride(0), n, _ptr(row_order), _ptr(w1), _ptr(b1), _ptr(w2), _ptr(w3),
+                _ptr(c), _dt(c), int(layer_norm), int(compensated), c.stride(0), n, _ptr(row_order), _ptr(w1), _ptr(b1),
+                _ptr(w2), _ptr(w3),
                 _ptr(b3),
                 _ptr(pre), pre.shape[0], _ptr(act_table), act_table.shape[0], _ptr(empty_rows), _ptr(act_empty),
                 _ptr(head_tab), head_tab.shape[0], _ptr(g_half), g_half.shape[0], _ptr(cell_pos), _ptr(dec_ptr),

@@ -408,11 +408,17 @@ int32_t mantis_attention_substages(void* x, int32_t x_dtype, int64_t ldx, int64_
  * row_order, when not NULL, is a permutation of the cells (int32) in which
  * they are grouped into 16-cell tiles (see mantis_segment_order); the
  * results do not depend on it.
+ * compensated = 1 (fp32 rows, layer_norm = 0 only): x, fp16(acts) and
+ * fp16(h) become hi + lo fp16 pairs and w3 is (32, 256) = [W3 hi; W3 lo]
+ * (lo = the fp32 weight minus its fp16 rounding), so the three products carry
+ * about 22 mantissa bits of x, acts and h (w1 and w2 stay fp16).  For the
+ * knob-off configuration, whose cell rows are sums of up to 18 window rows.
  * Replaces the reference's _action_contribution / encode_rows / class_row_sum
  * and the first layers of mlp_p and mlp_q (model.py:1031-1091,
  * row_encoder.py:40-112, message_passing.py:331-339).
  */
-int32_t mantis_cell_heads(const void* c, int32_t c_dtype, int32_t layer_norm, int64_t ldc, int64_t n_cells,
+int32_t mantis_cell_heads(const void* c, int32_t c_dtype, int32_t layer_norm, int32_t compensated,
+                          int64_t ldc, int64_t n_cells,
                           const int32_t* row_order, const void* w1, const float* b1, const void* w2, const void* w3, const float* b3,
                           const void* pre, int64_t n_w, const void* act_table, int64_t n_acls,
                           const float* empty_rows, const int64_t* act_empty, const void* head_tab, int64_t n_dcls,
@@ -582,14 +588,15 @@ int32_t mantis_fused_linear(const void* x, int32_t x_dtype, int64_t ldx, const i
                             void* stream);
 
 /*
- * mantis_fused_linear with compensated weights: w1 and w2 are (2 n1, 128)
- * fp16, the rows [hi; lo] of W with hi = fp16(W) and lo = fp16(W - hi), and
- * every product runs on both halves into one fp32 accumulator, so the
- * weights act with ~22 mantissa bits (the rows remain fp16 operands).
+ * mantis_fused_linear with compensated products: w1 and w2 are (2 n1, 128)
+ * fp16, the rows [hi; lo] of W with hi = fp16(W) and lo = fp16(W - hi); the
+ * fp32 rows are split the same way, and each product runs as
+ * W_hi x_hi + W_lo x_hi + W_hi x_lo into one fp32 accumulator, so weights
+ * and rows act with ~22 mantissa bits (fp16 rows have x_lo = 0).
  * Covered: n1 = 128, single stage, fp32 x: the LayerNorm projection (out_mode
  * 0 or 1), the residual projection (out_mode 2, no LayerNorm) and a pair
- * MLP's first layer relu(LN(x) W1^T + x2 W2^T + b1) with fp16 x2 (out_mode
- * 1).  Used where rounding the weights to fp16 would be summed coherently
+ * MLP's first layer relu(LN(x) W1^T + x2 W2^T + b1) with fp16 or fp32 x2
+ * (out_mode 1).  Used where rounding the weights to fp16 would be summed coherently
  * (the knob-off cell pass's u_cp and mlp_cp, model.py:374-395).
  */
 int32_t mantis_fused_linear_split(const void* x, int32_t x_dtype, int64_t ldx, const int64_t* x_rows,

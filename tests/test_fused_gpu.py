@@ -397,6 +397,59 @@ def test_cell_heads_match_the_unfused_composition(device, mode):
     assert torch.equal(got2.cpu(), got.cpu())
 
 
+def test_compensated_cell_heads_match_fp32(device):
+    # the knob-off heads: fp32 rows of large magnitude (sums of up to 18
+    # window rows), x / acts / h as hi + lo fp16 pairs and W3 as [hi; lo]:
+    # against an fp32 composition on the CPU with the same fp16 W1 and W2,
+    # the outputs agree to ~1e-5 relative, far closer than the uncompensated
+    # kernel on the same rows
+    gen = _g(21)
+    n, n_w, p, acls, dcls = 1200, 250, 5, 729, 726
+    counts = torch.randint(0, 19, (n,), generator=gen)
+    dest = torch.repeat_interleave(torch.arange(n), counts)
+    e = dest.numel()
+    win = torch.randint(0, n_w, (e,), generator=gen)
+    acl = torch.randint(0, acls, (e,), generator=gen)
+    dcl = torch.randint(0, dcls, (e,), generator=gen)
+    ptr = torch.searchsorted(dest, torch.arange(n + 1))
+    cell_pos = torch.sort(torch.randint(0, p, (n,), generator=gen)).values
+    c = 6 * torch.randn(n, 128, generator=gen) + 1.0
+    pre = torch.randn(n_w, 128, generator=gen).to(H16)
+    table = 0.5 * torch.randn(acls, 128, generator=gen)
+    empty_rows = torch.randn(3, 128, generator=gen).relu()
+    act_empty = torch.randint(0, 6, (n, 3), generator=gen)
+    head_tab = 0.2 * torch.randn(dcls, 256, generator=gen)
+    g_half = torch.randn(p, 256, generator=gen)
+    w1, w2 = _w(256, 128, gen), _w(256, 128, gen)
+    w3 = torch.zeros(16, 256)
+    w3[0, :128] = 0.05 * torch.randn(128, generator=gen)
+    w3[1:4, 128:] = 0.05 * torch.randn(3, 128, generator=gen)
+    b1, b3 = 0.1 * torch.randn(256, generator=gen), 0.1 * torch.randn(16, generator=gen)
+    d = lambda t: t.to(device)  # noqa: E731
+    args = (d(pre), d(table), d(empty_rows), d(act_empty), d(head_tab), d(g_half), d(cell_pos), d(ptr), d(win),
+            d(acl), d(dcl))
+    got = ops.cell_heads(d(c), d(w1), d(b1), d(w2), d(ops.split_weight(w3)), d(b3), *args, layer_norm=False,
+                         compensated=True)
+    plain = ops.cell_heads(d(c), d(w1), d(b1), d(w2), d(w3.to(H16)), d(b3), *args, layer_norm=False)
+    ops.raise_on_device_error(device)
+    # fp32 composition (the class tables in fp16, as the kernel gathers them)
+    t16, h16 = table.to(H16).double(), head_tab.to(H16).double()
+    acts = torch.zeros(n, 128, dtype=torch.float64).index_add_(0, dest, (pre.double()[win] + t16[acl]).relu())
+    acts += (act_empty.double().unsqueeze(-1) * empty_rows.double().unsqueeze(0)).sum(1)
+    ext = torch.zeros(n, 256, dtype=torch.float64).index_add_(0, dest, h16[dcl])
+    h = (c.double() @ w1.double().t() + acts @ w2.double().t() + b1.double() + ext + g_half.double()[cell_pos]).relu()
+    ref = (h @ w3.double().t() + b3.double()).float()
+    scale = float(ref.abs().max())
+    err_c = float((got.cpu() - ref).abs().max())
+    err_p = float((plain.cpu() - ref).abs().max())
+    print({"scale": scale, "compensated": err_c, "plain": err_p})
+    assert err_c <= 2e-5 * scale
+    assert err_p > 10 * err_c
+    with pytest.raises(ValueError):
+        ops.cell_heads(d(c.to(H16)), d(w1), d(b1), d(w2), d(ops.split_weight(w3)), d(b3), *args, layer_norm=False,
+                       compensated=True)
+
+
 def test_latent_mix_matches_the_fp32_formulation(device):
     # the four latents of a position attend to each other (model.py:516-526)
     gen = _g(13)

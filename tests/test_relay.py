@@ -287,7 +287,7 @@ def test_message_passing_backward_matches_autograd(device):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("config,count", [(1, 8), (4, 8)])
+@pytest.mark.parametrize("config,count", [(1, 8), (4, 8), (5, 4)])
 def test_knob_off_forward_matches_oracle(device, config, count):
     net = _perturbed(MantisConfig(), seed=2).to(device).eval()
     batch = collate_positions(synthetic.random_games(config, count, start=20))
@@ -295,18 +295,13 @@ def test_knob_off_forward_matches_oracle(device, config, count):
         out = net(batch.to(device), 0.2)
     rep = compare_outputs(out, oracle_forward(net, batch, 0.2), batch.legal_offsets)
     print(rep)
-    # KL, value and q at the production bars.  Policy max-abs at 1.5e-2, not
-    # 1e-2: the knob-off logits run ~2.8x the production scale (max |logit|
-    # 7.6 vs 2.7 at these seeds), and both the relay and the heads' decoder
-    # rows are sums of many rows through one weight matrix, so fp16 weight
-    # rounding adds up coherently.  The relay block's weights are compensated
-    # (hi + lo) for that reason; the heads' are not (their doubled weights
-    # do not fit LDS), and an oracle run with fp16-rounded head weights alone
-    # is ~0.008 from fp32.  Measured: 0.0068 (configs 1) / 0.0097 (configs 4)
-    # here, 0.0116 at configs 5.
-    assert rep["policy_kl_max"] <= 1e-4 and rep["value_max_abs"] <= 2e-3, rep
-    assert rep["q_values_max_abs"] <= 1e-2 and rep["q_score_max_abs"] <= 1e-2, rep
-    assert rep["policy_max_abs"] <= 1.5e-2, rep
+    # every output at the production bars.  The knob-off logits run ~3x the
+    # production scale and both the relay and the heads' decoder rows are sums
+    # of many rows through one weight matrix, so fp16 roundings there add up
+    # coherently: the relay block runs compensated products on fp32 rows and
+    # the heads compensated operands (measured 0.0077 at configs[3] and 0.0091
+    # at configs[4] positions)
+    assert rep["ok"], rep
 
 
 @pytest.mark.gpu
