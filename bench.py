@@ -66,6 +66,7 @@ def _args():
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-isolated", action="store_true", help="skip the isolated attention/message-passing lines")
+    ap.add_argument("--no-seam", action="store_true", help="skip the evaluator-seam timing")
     ap.add_argument("--isolated-only", action="store_true",
                     help="run only the isolated attention and message-passing lines (for kernel profiling)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -414,8 +415,9 @@ def main() -> int:
         "roofline": roofline,
         "kernels": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in kernels.items()},
     }
-    line["seam"] = seam_timing(torch, net, bd, min(args.steps, 10))
-    _log(f"seam: {line['seam']}")
+    if not args.no_seam:
+        line["seam"] = seam_timing(torch, net, bd, min(args.steps, 10))
+        _log(f"seam: {line['seam']}")
     if not args.no_isolated:
         _log("isolated attention (configs[1])")
         line["attention"] = isolated_attention(torch, ops, dev)

@@ -383,6 +383,8 @@ def make_plan(model, b: Batch, speculative: bool = False) -> Plan:
     # attention rows [latents; stones] per position over the [s; g] buffer
     attn_src, attn_back = ops.attention_slots(b.stone_slot, p, max_t)
     seq_lens = b.attn_valid.sum(dim=1, dtype=torch.int32)
+    if ops.tracing("stone_attention"):
+        ops.register_seq_lens(seq_lens)  # (a trace only: one read, for its accounting)
     return Plan(
         n_pos=p, max_t=max_t, max_w=max_w, n_s=n_s, n_w=n_w, n_c=n_c,
         inc_win_ptr=ops.runs_to_ptr(b.inc_window, n_w),

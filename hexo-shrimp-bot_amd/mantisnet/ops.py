@@ -1154,7 +1154,14 @@ _STONE_LENS: dict[int, Tensor] = {}
 
 
 def register_seq_lens(seq_lens: Tensor) -> None:
+    """The host copy of a lengths tensor, for the trace's byte and flop
+    accounting of the attention launches that take it (one device read)."""
     _STONE_LENS[seq_lens.data_ptr()] = seq_lens.detach().cpu().to(torch.int64)
+
+
+def tracing(name: str) -> bool:
+    """Whether a trace that records ``name`` is active."""
+    return _TRACE is not None and _TRACE.wants(name)
 
 
 def _strides(t: Tensor):
