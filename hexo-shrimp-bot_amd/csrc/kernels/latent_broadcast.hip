@@ -1,0 +1,168 @@
+// Window <- latents broadcast fused with its output projection and residual,
+// for gfx950.  For every window row r of position p = window_pos[r] and each
+// of the 4 heads a (32 dims each):
+//   s_j  = q[r, a] . k[4 p + j, a] / sqrt(32)          j = 0..3, the position's latents
+//   o_a  = fp16( sum_j softmax_j(s) v[4 p + j, a] )      (fp32 softmax and sums)
+//   x[r] += Wo o + bo                                    (fp16 rows: widened, added in fp32, rounded once)
+// It replaces the broadcast attention (window_latents.py:350-381, the
+// window-major read of _window_latent_cycle, model.py:527-541) and the
+// latent_wo_bcast projection that reads its output back: the (n_w, 128)
+// attention output never leaves the chip.
+//
+// Layout: a wavefront owns 16 rows; lane (l16, g) = (row, 8-dim group) holds
+// q[r][32 a + 8 g .. +8] for every head a, which is the B fragment layout of
+// v_mfma_f32_16x16x32_f16 for o^T.  A score is 8 products on the lane and a
+// sum over the four lanes of the row (two shuffles); the latent k and v
+// slices a lane reads are the same 16 bytes for every row of the tile that
+// shares a position, so their loads mostly coalesce into one 64-byte piece.
+// o^T then multiplies Wo (LDS, padded rows) on MFMA, and the D fragment
+// (four consecutive outputs of one row per lane) is added into x in place.
+// Workgroups are persistent (8 wavefronts, Wo and bo staged once).
+#include "common.hpp"
+#include "mfma.hpp"
+
+namespace mantis {
+namespace {
+
+constexpr int kK = 128;
+constexpr int kPitch = kK + 8;  // fp16 per staged LDS row: 16 rows of a fragment read fall in distinct banks
+constexpr int kWaves = 8;
+constexpr int kThreads = kWaves * 64;
+
+struct BcastArgs {
+  const _Float16* q;  // (n_w, >= 128) rows, ldq
+  int64_t ldq;
+  const _Float16* kv;  // (4 n_pos, >= 256): k | v per latent row, ldkv
+  int64_t ldkv;
+  const int64_t* window_pos;
+  int64_t n_pos;
+  int64_t n_w;
+  const _Float16* wo;  // (128, 128)
+  const float* bo;     // (128,)
+  _Float16* x;         // (n_w, 128) fp16 residual rows, ldx
+  int64_t ldx;
+  int32_t* flag;
+};
+
+__global__ void __launch_bounds__(kThreads) latent_broadcast_residual_kernel(BcastArgs a) {
+  __shared__ __attribute__((aligned(16))) _Float16 sw[kK * kPitch];
+  __shared__ __attribute__((aligned(16))) float sb[kK];
+  for (int i = threadIdx.x; i < kK * (kK / 8); i += kThreads) {
+    const int r = i / (kK / 8), c = (i % (kK / 8)) * 8;
+    *reinterpret_cast<uint4*>(sw + r * kPitch + c) = *reinterpret_cast<const uint4*>(a.wo + r * kK + c);
+  }
+  for (int i = threadIdx.x; i < kK; i += kThreads) sb[i] = a.bo[i];
+  __syncthreads();
+
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+  const int l16 = lane % 16, g = lane / 16;
+  const int64_t n_tiles = (a.n_w + 15) / 16;
+  const float scale = 0.17677669529663687f;  // 1 / sqrt(32)
+  for (int64_t tile = int64_t(blockIdx.x) * kWaves + wave; tile < n_tiles; tile += int64_t(gridDim.x) * kWaves) {
+    const int64_t row = tile * 16 + l16;
+    const bool in = row < a.n_w;
+    const int64_t rr = in ? row : a.n_w - 1;  // rows past the end compute on a real row and store nothing
+    const int64_t p = a.window_pos[rr];
+    const bool ok = p >= 0 && p < a.n_pos;
+    if (in && !ok && g == 0) raise_flag(a.flag, MANTIS_FLAG_INDEX);
+    const int64_t pc = ok ? p : 0;
+    // q of this lane: dims 8 g .. 8 g + 7 of each head
+    f16x8_t qv[4];
+#pragma unroll
+    for (int h = 0; h < 4; ++h) qv[h] = *reinterpret_cast<const f16x8_t*>(a.q + rr * a.ldq + 32 * h + 8 * g);
+    // the tile's residual rows, requested now: their latency overlaps the attention
+    uint2 xr[8];
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) xr[nt] = *reinterpret_cast<const uint2*>(a.x + rr * a.ldx + 16 * nt + 4 * g);
+    // one head at a time (a scheduling barrier keeps its eight latent loads
+    // from being hoisted with the other heads': registers for occupancy):
+    // scores as partial dots summed over the row's four lanes, softmax over
+    // the four latents, and the weighted values as o^T's B fragment
+    f16x8_t ob[4];
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      f16x8_t kf[4], vf[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        kf[j] = *reinterpret_cast<const f16x8_t*>(a.kv + (4 * pc + j) * a.ldkv + 32 * h + 8 * g);
+        vf[j] = *reinterpret_cast<const f16x8_t*>(a.kv + (4 * pc + j) * a.ldkv + kK + 32 * h + 8 * g);
+      }
+      float s[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float d = 0.f;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) d = fmaf(float(qv[h][t]), float(kf[j][t]), d);
+        d += __shfl_xor(d, 16);
+        d += __shfl_xor(d, 32);
+        s[j] = d * scale;
+      }
+      const float m = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+      float e[4], den = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        e[j] = __expf(s[j] - m);
+        den += e[j];
+      }
+      const float inv = ok ? 1.f / den : 0.f;  // an out-of-range position reads zero
+      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) acc[t] = fmaf(e[j], float(vf[j][t]), acc[t]);
+      uint4 w;
+      w.x = pack_f16x2_unit(acc[0] * inv, acc[1] * inv);  // convex combinations of fp16 rows: in range
+      w.y = pack_f16x2_unit(acc[2] * inv, acc[3] * inv);
+      w.z = pack_f16x2_unit(acc[4] * inv, acc[5] * inv);
+      w.w = pack_f16x2_unit(acc[6] * inv, acc[7] * inv);
+      ob[h] = __builtin_bit_cast(f16x8_t, w);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // y^T = Wo . o^T, one 16-output tile at a time, added into the fp16 rows
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      f32x4_t d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const f16x8_t wf = *reinterpret_cast<const f16x8_t*>(sw + (16 * nt + l16) * kPitch + 32 * ks + 8 * g);
+        d = mfma16x16x32(wf, ob[ks], d);
+      }
+      if (in) {
+        const int f = 16 * nt + 4 * g;
+        const float4 b = *reinterpret_cast<const float4*>(sb + f);
+        const f16x2_t r0 = __builtin_bit_cast(f16x2_t, xr[nt].x), r1 = __builtin_bit_cast(f16x2_t, xr[nt].y);
+        uint2 w;
+        w.x = pack_f16x2(float(r0[0]) + (d[0] + b.x), float(r0[1]) + (d[1] + b.y));
+        w.y = pack_f16x2(float(r1[0]) + (d[2] + b.z), float(r1[1]) + (d[3] + b.w));
+        *reinterpret_cast<uint2*>(a.x + row * a.ldx + f) = w;
+      }
+    }
+  }
+}
+
+}  // namespace
+}  // namespace mantis
+
+using namespace mantis;
+
+extern "C" int32_t mantis_latent_broadcast_residual(const void* q, int64_t ldq, const void* kv, int64_t ldkv,
+                                                    const int64_t* window_pos, int64_t n_pos, int64_t n_w,
+                                                    const void* wo, const float* bo, void* x, int64_t ldx,
+                                                    int32_t* err_flag, void* stream) {
+  if (n_w == 0) return MANTIS_OK;
+  if (!q || !kv || !window_pos || !wo || !bo || !x || n_w < 0 || n_pos <= 0) return MANTIS_E_ARG;
+  if (ldq < kK || ldq % 8 || ldkv < 2 * kK || ldkv % 8 || ldx < kK || ldx % 8) return MANTIS_E_ARG;
+  if (!aligned16(q) || !aligned16(kv) || !aligned16(wo) || !aligned16(bo) || !aligned16(x)) return MANTIS_E_ARG;
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    cus = 256;
+  const int64_t tiles = (n_w + 15) / 16;
+  int64_t grid = int64_t(cus) * 3;  // three persistent workgroups per CU
+  const int64_t need = (tiles + kWaves - 1) / kWaves;
+  if (need < grid) grid = need;
+  BcastArgs a{static_cast<const _Float16*>(q), ldq, static_cast<const _Float16*>(kv), ldkv, window_pos, n_pos, n_w,
+              static_cast<const _Float16*>(wo), bo, static_cast<_Float16*>(x), ldx, err_flag};
+  latent_broadcast_residual_kernel<<<dim3(unsigned(grid)), dim3(kThreads), 0, as_stream(stream)>>>(a);
+  return launched();
+}

@@ -484,8 +484,12 @@ def _latent_cycle(W, P, pb, plan: Plan, w, g2, kv, qb):
     # 4 x 4 latent self-mix, fp32 (all four slots live; model.py:516-526)
     ops.latent_mix(g2, W[pb + "mix_qkv.wt"], W[pb + "mix_qkv.b"], W[pb + "mix_o.wt"], W[pb + "mix_o.b"])
     kvb = _proj(W, pb + "lkv_bcast", g2)
-    out = ops.latent_broadcast_rows(qb, kvb, plan.window_pos, out_dtype=HALF)
-    _resid(W, pb + "lo_bcast", out.view(plan.n_w, 128), w)
+    if w.dtype == HALF:
+        # broadcast, output projection and residual in one pass over the windows
+        ops.latent_broadcast_residual(qb, kvb, plan.window_pos, W[pb + "lo_bcast.w"], W[pb + "lo_bcast.b"], w)
+    else:
+        out = ops.latent_broadcast_rows(qb, kvb, plan.window_pos, out_dtype=HALF)
+        _resid(W, pb + "lo_bcast", out.view(plan.n_w, 128), w)
 
 
 def _block(W, P, i: int, plan: Plan, b: Batch, sg, w, c, sw_all, update_stones: bool):

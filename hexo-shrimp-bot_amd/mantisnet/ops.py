@@ -968,6 +968,37 @@ def cell_heads(c: Tensor, w1: Tensor, b1: Tensor, w2: Tensor, w3: Tensor, b3: Te
     return out
 
 
+def latent_broadcast_residual(q: Tensor, kv: Tensor, window_pos: Tensor, wo: Tensor, bo: Tensor, x: Tensor) -> Tensor:
+    """x += wo . broadcast(q over the position's 4 latents) + bo, in place on
+    fp16 window rows x (see mantis_latent_broadcast_residual): q (n_w, 128)
+    and kv (4 P, 256) = k | v fp16 rows with unit column stride."""
+    dev = _on_gpu(q, kv, window_pos, wo, bo, x)
+    n_w = x.shape[0]
+    if x.dtype != torch.float16 or x.ndim != 2 or x.shape[1] != 128 or x.stride(1) != 1:
+        raise ValueError("x must be fp16 (n_w, 128) rows")
+    if q.dtype != torch.float16 or q.shape != (n_w, 128) or q.stride(1) != 1:
+        raise ValueError("q must be fp16 (n_w, 128) rows")
+    if kv.dtype != torch.float16 or kv.ndim != 2 or kv.shape[1] != 256 or kv.shape[0] % 4 or kv.stride(1) != 1:
+        raise ValueError("kv must be fp16 (4 P, 256) rows")
+    if wo.dtype != torch.float16 or wo.shape != (128, 128) or not wo.is_contiguous():
+        raise ValueError("wo must be a contiguous fp16 (128, 128) matrix")
+    bo = bo.float().contiguous()
+    window_pos = _i64(window_pos, "window_pos")
+    if window_pos.shape != (n_w,):
+        raise ValueError("window_pos must have one entry per window")
+    if n_w:
+        n_pos = kv.shape[0] // 4
+        # q, x read and x written once per window; the latent k/v once per position
+        nbytes = n_w * (256 + 512 + 8) + n_pos * 4 * 512
+        flops = n_w * (2 * 128 * 128 + 4 * 4 * 32 * 4)
+        _launch("latent_broadcast_residual", nbytes, flops, lambda: _check(
+            _lib().mantis_latent_broadcast_residual(_ptr(q), q.stride(0), _ptr(kv), kv.stride(0), _ptr(window_pos),
+                                                    n_pos, n_w, _ptr(wo), _ptr(bo), _ptr(x), x.stride(0),
+                                                    _ptr(error_flag(dev)), _stream()),
+            "latent_broadcast_residual"))
+    return x
+
+
 def latent_read(q: Tensor, k: Tensor, v: Tensor, offsets: Tensor, order: Tensor, stats: bool = False):
     """Four latent queries per position over its windows; q (P, 4, ...) and
     k/v 128-wide rows; returns fp32 (P, 4, 4, 32) [and m, l]."""

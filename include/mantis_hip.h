@@ -427,6 +427,24 @@ int32_t mantis_cell_heads(const void* c, int32_t c_dtype, int32_t layer_norm, in
                           int64_t n_entries, float* out, int32_t* err_flag, void* stream);
 
 /*
+ * Window <- latents broadcast fused with its output projection and residual,
+ * in place on fp16 window rows x (n_w, 128), row stride ldx: for window r of
+ * position p = window_pos[r] and head a (4 heads of 32 dims),
+ *   o[r, a] = fp16( sum_j softmax_j(q[r, a] . k[4p + j, a] / sqrt(32)) v[4p + j, a] )
+ *   x[r]   += wo o[r] + bo     (widened, added in fp32, rounded once)
+ * q: (n_w, >= 128) fp16 rows, stride ldq (head a at columns 32a..32a+31);
+ * kv: (4 n_pos, >= 256) fp16 rows, stride ldkv, k in columns 0..127 and v in
+ * 128..255; wo (128, 128) fp16 (out x in), bo (128) fp32.  A window whose
+ * position is out of range reads o = 0 and sets MANTIS_FLAG_INDEX.
+ * Replaces the broadcast attention (window_latents.py:350-381, as
+ * mantis_latent_broadcast) and the latent_wo_bcast residual projection that
+ * reads its output back (model.py:527-541).
+ */
+int32_t mantis_latent_broadcast_residual(const void* q, int64_t ldq, const void* kv, int64_t ldkv,
+                                         const int64_t* window_pos, int64_t n_pos, int64_t n_w, const void* wo,
+                                         const float* bo, void* x, int64_t ldx, int32_t* err_flag, void* stream);
+
+/*
  * Latent self-mix, in place on the fp32 latent rows g (n_pos * 4 rows of
  * 128, row stride ldg), per position p in fp32:
  *   z = LN(g_p) (no affine: fold it into wqkv_t / bqkv),

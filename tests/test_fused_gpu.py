@@ -450,6 +450,39 @@ def test_compensated_cell_heads_match_fp32(device):
                        compensated=True)
 
 
+def test_latent_broadcast_residual_matches_the_unfused_composition(device):
+    # broadcast over the 4 latents + output projection + fp16 residual in one
+    # pass = latent_broadcast_rows (fp16 out) then the residual projection
+    gen = _g(31)
+    n_pos, n_w = 37, 3001
+    wide = torch.randn(n_w, 512, generator=gen).to(H16)  # q at columns 384..511, as the forward's view
+    q = wide[:, 384:]
+    kv = torch.randn(4 * n_pos, 256, generator=gen).to(H16)
+    pos = torch.sort(torch.randint(0, n_pos, (n_w,), generator=gen)).values
+    wo = _w(128, 128, gen)
+    bo = 0.05 * torch.randn(128, generator=gen)
+    x0 = (2 * torch.randn(n_w, 128, generator=gen)).to(H16)
+    d = lambda t: t.to(device)  # noqa: E731
+    got = d(x0.clone())
+    ops.latent_broadcast_residual(d(wide)[:, 384:], d(kv), d(pos), d(wo), d(bo), got)
+    ops.raise_on_device_error(device)
+    ref = d(x0.clone())
+    out = ops.latent_broadcast_rows(d(q), d(kv), d(pos), out_dtype=H16)
+    ops.fused_linear(out.view(n_w, 128), d(wo), d(bo), out=ref, residual=True)
+    ops.raise_on_device_error(device)
+    # one fp16 unit of the attention output or of the stored row apart at most
+    torch.testing.assert_close(got.float().cpu(), ref.float().cpu(), rtol=2e-3, atol=2e-3)
+    # an out-of-range position reads zero attention (x += bo) and is flagged
+    bad = pos.clone()
+    bad[5] = n_pos
+    got = d(x0.clone())
+    ops.latent_broadcast_residual(d(wide)[:, 384:], d(kv), d(bad), d(wo), d(bo), got)
+    with pytest.raises(ValueError):
+        ops.raise_on_device_error(device)
+    want5 = (x0[5].float() + bo).to(H16)
+    assert torch.equal(got[5].cpu(), want5)
+
+
 def test_latent_mix_matches_the_fp32_formulation(device):
     # the four latents of a position attend to each other (model.py:516-526)
     gen = _g(13)
