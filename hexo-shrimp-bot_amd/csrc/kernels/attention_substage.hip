@@ -41,6 +41,11 @@
 // kTau (e^kTau bounds every weight), so the accumulator is rescaled on the
 // rare entries that do, not on every entry.
 //
+// A wavefront has the next tile's row and CSR bounds in registers before it
+// starts a tile, and requests both stages' first entry groups at the tile's
+// start, so neither stage begins with a chain of dependent index loads
+// (956 -> 920 us per launch at the production batch).
+//
 // A tile's entry loop runs as long as its longest row.  An optional row
 // order (a permutation of the rows) groups rows of similar entry counts into
 // tiles; each row's arithmetic is the same in any order, so the results are
@@ -191,38 +196,54 @@ __global__ void __launch_bounds__(waves_for<kStages>() * 64) attn_substage_kerne
   const int64_t waves_here = wgs_here * kWaves;
   const int64_t t_begin = n_tiles * xcd / kXcds, t_end = n_tiles * (xcd + 1) / kXcds;
 
-  // The look-ahead loads below (the next batch's entries) are issued
-  // unconditionally from a clamped, valid address and validated only where
-  // their values are used: a check right after the load would make the
-  // wavefront wait for it there, and with in-order load counters also for
-  // every row load issued before it.
-  // the row of a tile slot (raw: validated where it is used); slots past the
-  // end read entry 0 of the order
-  auto order_at = [&](int64_t t) -> int64_t {
+  // The look-ahead loads below (the next tile's row and bounds, the next
+  // group's entries) are issued unconditionally from a clamped, valid
+  // address and validated only where their values are used: a check right
+  // after the load would make the wavefront wait for it there, and with
+  // in-order load counters also for every load issued before it.
+  // The order word of a tile slot (raw, 32-bit: widened where it is used, so
+  // nothing consumes the load until the next tile); slots past the end read
+  // entry 0 of the order (rows fit int32: the host checks n_rows)
+  const int32_t* order = a.order;
+  auto order_at = [&](int64_t t) -> int32_t {
     const int64_t slot = t * 16 + l16;
-    if (!a.order) return slot;
-    return a.order[slot < a.n_rows ? slot : 0];
+    if (!order) return slot < a.n_rows ? int32_t(slot) : 0;
+    return order[slot < a.n_rows ? slot : 0];
   };
   const int64_t tile0 = t_begin + int64_t(blockIdx.x / kXcds) * kWaves + wave;
-  int64_t next_row = tile0 < t_end ? order_at(tile0) : 0;
+  auto clamp_row = [&](int64_t r) -> int64_t { return r >= 0 && r < a.n_rows ? r : 0; };
+  // Look-ahead across tiles: when a tile starts, the order word of its row
+  // and the row's CSR bounds are in registers.  The next tile's order word is
+  // requested at the start of a tile, its bounds after the last stage's entry
+  // loop (the word has arrived by then); each register is consumed before it
+  // is loaded again, so no copy ever waits for a load.
+  int32_t row_n = tile0 < t_end ? order_at(tile0) : 0;
+  int64_t pa_n[kStages], pb_n[kStages];
+  {
+    const int64_t rc = clamp_row(row_n);
+#pragma unroll
+    for (int s = 0; s < kStages; ++s) {
+      pa_n[s] = a.st[s].seg_ptr[rc];
+      pb_n[s] = a.st[s].seg_ptr[rc + 1];
+    }
+  }
   for (int64_t tile = tile0; tile < t_end; tile += waves_here) {
     // an offset the compiler cannot see through: keeps the weight-fragment
     // reads inside the loop instead of hoisting all of them into registers
     int lds_off = 0;
     asm volatile("" : "+s"(lds_off));
-    const int64_t row = next_row;
-    next_row = order_at(tile + waves_here < t_end ? tile + waves_here : tile);  // one tile ahead
+    const int64_t row = row_n;
+    int64_t lo[kStages], hi[kStages];
+#pragma unroll
+    for (int s = 0; s < kStages; ++s) {
+      const int64_t n_e = a.st[s].n_entries;
+      lo[s] = pa_n[s] < 0 ? 0 : (pa_n[s] > n_e ? n_e : pa_n[s]);
+      hi[s] = pb_n[s] < lo[s] ? lo[s] : (pb_n[s] > n_e ? n_e : pb_n[s]);
+    }
     const bool in_tile = tile * 16 + l16 < a.n_rows;
     const bool live = in_tile && row >= 0 && row < a.n_rows;
     if (in_tile && !live) raise_flag(a.flag, MANTIS_FLAG_INDEX);
     const int64_t rc = live ? row : 0;  // dead lanes read a real row and store nothing
-    // the entry walk's pointers first (the first entries depend on them), then x
-    int64_t pa[kStages], pb[kStages];
-#pragma unroll
-    for (int s = 0; s < kStages; ++s) {
-      pa[s] = a.st[s].seg_ptr[rc];
-      pb[s] = a.st[s].seg_ptr[rc + 1];
-    }
     // the row state: fp32 rows stay fp32 in registers across the stages;
     // fp16 rows stay packed (half the registers) and are rounded after each
     // stage, exactly as a launch per stage would leave them
@@ -238,12 +259,33 @@ __global__ void __launch_bounds__(waves_for<kStages>() * 64) attn_substage_kerne
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) load8_nt(xs + rc * a.ldx + 32 * ks + 8 * g, xv[ks]);
     }
-    int64_t lo[kStages], hi[kStages];
+    // Per stage: the entry count of this lane's row and the wavefront's
+    // longest row; the attention runs with lane 4 r + g on (row r, head g)
+    // (the four lanes of a row are adjacent, so each 16-byte gather of a quad
+    // covers 64 contiguous bytes of a head-interleaved row), so the row's
+    // count and first entry move there by lane permutes.  Entries go in
+    // groups of four: lane (r, g) holds entry j + g of row r (raw indices,
+    // validated where they are used); a lane past its row's end reads entry 0
+    // (there is one: some row of the tile has entries).  Both stages' first
+    // groups are requested now.
+    int acnt[kStages], maxc[kStages];
+    int64_t alo[kStages], es[kStages], ec[kStages];
 #pragma unroll
     for (int s = 0; s < kStages; ++s) {
-      const int64_t n_e = a.st[s].n_entries;
-      lo[s] = pa[s] < 0 ? 0 : (pa[s] > n_e ? n_e : pa[s]);
-      hi[s] = pb[s] < lo[s] ? lo[s] : (pb[s] > n_e ? n_e : pb[s]);
+      const int cnt = live ? int(hi[s] - lo[s]) : 0;
+      int mc = cnt;
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) mc = max(mc, __shfl_xor(mc, o));
+      maxc[s] = __builtin_amdgcn_readfirstlane(mc);
+      acnt[s] = from_lane(src_m, cnt);
+      alo[s] = int64_t((uint64_t(uint32_t(from_lane(src_m, int32_t(uint64_t(lo[s]) >> 32)))) << 32) |
+                       uint32_t(from_lane(src_m, int32_t(lo[s]))));
+      es[s] = ec[s] = 0;
+      if (maxc[s] > 0) {
+        const int64_t e = ag < acnt[s] ? alo[s] + ag : 0;
+        es[s] = a.st[s].src[e];
+        ec[s] = a.st[s].cls[e];
+      }
     }
 
 #pragma unroll
@@ -253,29 +295,14 @@ __global__ void __launch_bounds__(waves_for<kStages>() * 64) attn_substage_kerne
       const _Float16* swo = sw[s][1] + lds_off;
       const float* sbq = sb[s][0];
       const float* sbo = sb[s][1];
-      // entry count of this lane's row, and the wavefront's longest row
-      const int cnt = live ? int(hi[s] - lo[s]) : 0;
-      int maxc = cnt;
-#pragma unroll
-      for (int o = 1; o < 16; o <<= 1) maxc = max(maxc, __shfl_xor(maxc, o));
-      // The attention runs with lane 4 r + g on (row r, head g): the four
-      // lanes of a row are adjacent, so each 16-byte gather of a quad covers
-      // 64 contiguous bytes of a head-interleaved row.  q moves there and the
-      // output back by lane permutes.
-      const int acnt = from_lane(src_m, cnt);
-      const int64_t alo = int64_t((uint64_t(uint32_t(from_lane(src_m, int32_t(uint64_t(lo[s]) >> 32)))) << 32) |
-                                  uint32_t(from_lane(src_m, int32_t(lo[s]))));
-      // Entries in groups of four: lane (r, g) holds entry j + g of row r as
-      // validated int32 (source, class), -1 when out of range; a lane past
-      // its row's end reads entry 0 (there is one: some row of the tile has
-      // entries).  The next group's raw indices load under this group's rows.
-      int64_t es = 0, ec = 0;
-      auto fetch = [&](int j0) {
-        const int64_t e = j0 + ag < acnt ? alo + j0 + ag : 0;
-        es = S.src[e];
-        ec = S.cls[e];
-      };
-      if (maxc > 0) fetch(0);
+      const int mc = maxc[s];
+      const int ac = acnt[s];
+      auto valid_src = [&](int64_t v) { return v >= 0 && v < S.n_src ? int32_t(v) : -1; };
+      auto valid_cls = [&](int64_t v) { return v >= 0 && v < S.n_classes ? int32_t(v) : -1; };
+      int32_t s4 = valid_src(es[s]), c4 = valid_cls(ec[s]);
+      // the next tile's order word, after the tile's first loads (the counters
+      // are in order: waiting for those does not wait for it)
+      if (s == 0) row_n = order_at(tile + waves_here < t_end ? tile + waves_here : tile);
       // ---- LayerNorm + Q projection
       if constexpr (kPacked) {
 #pragma unroll
@@ -344,12 +371,18 @@ __global__ void __launch_bounds__(waves_for<kStages>() * 64) attn_substage_kerne
       uint4 kr[4], vr[4], cr[4];
 #pragma unroll
       for (int w = 0; w < 4; ++w) kr[w] = vr[w] = cr[w] = make_uint4(0u, 0u, 0u, 0u);
-      for (int j = 0; j < maxc; j += 4) {
-        const int32_t s4 = es >= 0 && es < S.n_src ? int32_t(es) : -1;
-        const int32_t c4 = ec >= 0 && ec < S.n_classes ? int32_t(ec) : -1;
-        if (j + 4 < maxc) fetch(j + 4);
+      for (int j = 0; j < mc; j += 4) {
+        if (j > 0) {  // this group's indices (loaded under the previous group's rows)
+          s4 = valid_src(es[s]);
+          c4 = valid_cls(ec[s]);
+        }
+        if (j + 4 < mc) {  // the next group's raw indices, under this group's rows
+          const int64_t e = j + 4 + ag < ac ? alo[s] + j + 4 + ag : 0;
+          es[s] = S.src[e];
+          ec[s] = S.cls[e];
+        }
         auto step = [&](int u, int32_t src, int32_t cls) {
-          const bool in = j + u < acnt;
+          const bool in = j + u < ac;
           const bool ok = in && src >= 0 && cls >= 0;
           if (in && !ok) raise_flag(a.flag, MANTIS_FLAG_INDEX);
           float bs = 0.f;
@@ -374,9 +407,17 @@ __global__ void __launch_bounds__(waves_for<kStages>() * 64) attn_substage_kerne
           if constexpr (kVcls) axpy32(acc, pr, cr);
         };
         step(0, from_quad<0>(s4), from_quad<0>(c4));
-        if (j + 1 < maxc) step(1, from_quad<1>(s4), from_quad<1>(c4));
-        if (j + 2 < maxc) step(2, from_quad<2>(s4), from_quad<2>(c4));
-        if (j + 3 < maxc) step(3, from_quad<3>(s4), from_quad<3>(c4));
+        if (j + 1 < mc) step(1, from_quad<1>(s4), from_quad<1>(c4));
+        if (j + 2 < mc) step(2, from_quad<2>(s4), from_quad<2>(c4));
+        if (j + 3 < mc) step(3, from_quad<3>(s4), from_quad<3>(c4));
+      }
+      if (s == kStages - 1) {  // the next tile's bounds
+        const int64_t rcn = clamp_row(row_n);
+#pragma unroll
+        for (int t = 0; t < kStages; ++t) {
+          pa_n[t] = a.st[t].seg_ptr[rcn];
+          pb_n[t] = a.st[t].seg_ptr[rcn + 1];
+        }
       }
       // ---- output projection + residual, into the x registers
       {

@@ -288,6 +288,42 @@ def test_two_substages_in_one_pass_match_two_launches(device, with_vcls):
     assert got16.dtype == H16 and torch.equal(got16.cpu(), two16.cpu())
 
 
+def test_two_substages_with_many_tiles_per_wavefront(device):
+    # more rows than one sweep of the persistent grid (256 CUs x 8 wavefronts
+    # x 16 rows), in a random row order: every wavefront walks several tiles
+    # (with the next tile's row and bounds loaded ahead), checked against each
+    # stage as separate launches of projection, attention and output projection
+    gen = _g(14)
+    n = 70001
+    x = 2 * torch.randn(n, 128, generator=gen) + 0.5
+    ref = x.to(device)
+    stages = []
+    for n_src, classes, max_count in ((301, 726, 6), (57, 192, 12)):
+        counts = torch.randint(0, max_count + 1, (n,), generator=gen)
+        counts[::13] = 0
+        dest = torch.repeat_interleave(torch.arange(n), counts)
+        src = torch.randint(0, n_src, (dest.numel(),), generator=gen).to(device)
+        cls = torch.randint(0, classes, (dest.numel(),), generator=gen).to(device)
+        ptr = torch.searchsorted(dest, torch.arange(n + 1)).to(device)
+        kv = torch.randn(n_src, 256, generator=gen).to(H16).to(device)
+        wq, wo = _w(128, 128, gen).to(device), _w(128, 128, gen).to(device)
+        bq, bo = (0.1 * torch.randn(128, generator=gen)).to(device), (0.1 * torch.randn(128, generator=gen)).to(device)
+        bias = (0.3 * torch.randn(4, classes, generator=gen)).to(device)
+        vcls = (0.1 * torch.randn(classes, 128, generator=gen)).to(H16).to(device)
+        q = ops.fused_linear(ref, wq, bq, layer_norm=True)
+        a = ops.cell_attention(q, kv[:, :128], kv[:, 128:], bias, vcls, ptr, src, cls, out_dtype=H16)
+        ops.fused_linear(a.view(n, 128), wo, bo, out=ref, residual=True)
+        stages.append(ops.SubStage(wq, bq, ops.interleave_heads(kv), bias, ops.interleave_heads(vcls), ptr, src, cls,
+                                   wo, bo))
+    got = x.to(device)
+    order = torch.randperm(n, generator=gen).to(torch.int32).to(device)
+    ops.attention_substages(got, stages, row_order=order)
+    ops.raise_on_device_error(device)
+    # per stage as in the one-stage comparison (an fp16 unit of the attention
+    # output apart at most), and the second stage reads the first's rows
+    torch.testing.assert_close(got.cpu(), ref.cpu(), rtol=1e-5, atol=1.5e-3)
+
+
 def test_row_order_changes_the_tiles_not_the_results(device):
     # the rows visited in a random permutation (and in an order sorted by
     # entry count) give bitwise the natural order's results; an order entry
