@@ -35,6 +35,11 @@ namespace {
 
 // the value v of lane `src` (all lanes active)
 __device__ __forceinline__ int32_t from_lane(int src, int32_t v) { return __builtin_amdgcn_ds_bpermute(src << 2, v); }
+// the value v of lane 4 (lane / 4) + u (one DPP quad broadcast)
+template <int u>
+__device__ __forceinline__ int32_t from_quad(int32_t v) {
+  return __builtin_amdgcn_update_dpp(0, v, u * 0x55, 0xF, 0xF, false);
+}
 
 constexpr int kK = 128;
 constexpr int kN1 = 256;
@@ -88,6 +93,13 @@ __global__ void __launch_bounds__(kThreads) cell_heads_kernel(HeadArgs a) {
   // (loads and stores share one in-order counter)
   __shared__ __attribute__((aligned(16))) float sb1[kN1];
   __shared__ __attribute__((aligned(16))) float sb3[kN3];
+  // the three EMPTY-class action rows, and (but for the compensated heads,
+  // whose doubled W3 leaves no room) one g_half row per wavefront: its
+  // tile's position, loaded with one 16-byte load per lane
+  __shared__ __attribute__((aligned(16))) float sempty[3 * kK];
+  constexpr bool kGLds = !kComp;
+  __shared__ __attribute__((aligned(16))) float sgh[kGLds ? kWaves * kN1 : 4];
+  for (int i = threadIdx.x; i < 3 * kK; i += kThreads) sempty[i] = a.empty_rows[i];
   for (int i = threadIdx.x; i < kN1; i += kThreads) sb1[i] = a.b1[i];
   for (int i = threadIdx.x; i < kN3; i += kThreads) sb3[i] = a.b3[i];
   for (int i = threadIdx.x; i < kN1 * (kK / 8); i += kThreads) {
@@ -145,25 +157,32 @@ __global__ void __launch_bounds__(kThreads) cell_heads_kernel(HeadArgs a) {
 #pragma unroll
     for (int o = 1; o < 16; o <<= 1) maxc = max(maxc, __shfl_xor(maxc, o));
     // The decoder walk runs on the walk layout: the four lanes of a cell are
-    // adjacent, so a quad's 16-byte gathers cover 64 contiguous bytes.  Each
-    // entry's three indices are requested one entry ahead, unconditionally
-    // (entry 0 for a lane past its run) and checked where they are used.
+    // adjacent, so a quad's 16-byte gathers cover 64 contiguous bytes.  The
+    // entries go in groups of four: lane (cell, aq) loads the three indices
+    // of entry j + aq (unconditionally: entry 0 for a lane past its run),
+    // the next group's under this group's rows, and the cell's lanes receive
+    // them by DPP quad broadcasts; indices are checked where they are used.
     const int acnt = from_lane(src_m, cnt);
     const int64_t ast = int64_t((uint64_t(uint32_t(from_lane(src_m, int32_t(uint64_t(st) >> 32)))) << 32) |
                                 uint32_t(from_lane(src_m, int32_t(st))));
+    const int mc = __builtin_amdgcn_readfirstlane(maxc);
     int64_t iw = 0, ia = 0, id = 0;
-    auto fetch = [&](int j) {
-      const int64_t e = j < acnt ? ast + j : 0;
+    auto fetch = [&](int j0) {
+      const int64_t e = j0 + aq < acnt ? ast + j0 + aq : 0;
       iw = a.dec_window[e];
       ia = a.act_class[e];
       id = a.dec_class[e];
     };
-    if (maxc > 0) fetch(0);
+    if (mc > 0) fetch(0);
     int64_t pos = -1;
     if (live) {
       if (pos_raw < 0 || pos_raw >= a.n_pos) raise_flag(a.flag, MANTIS_FLAG_INDEX);
       else pos = pos_raw;
     }
+    // the tile's first cell's position (its g_half row is staged in LDS
+    // after the walk when every cell of the tile is in that position)
+    const int64_t p0 = int64_t((uint64_t(uint32_t(__builtin_amdgcn_readfirstlane(int32_t(uint64_t(pos) >> 32)))) << 32) |
+                               uint32_t(__builtin_amdgcn_readfirstlane(int32_t(pos))));
     // ---- x = LN(c) in B layout
     if constexpr (kLN) {
       float s = 0.f;
@@ -207,35 +226,42 @@ __global__ void __launch_bounds__(kThreads) cell_heads_kernel(HeadArgs a) {
 #pragma unroll
     for (int i = 0; i < 64; ++i) ev[i] = 0.f;
     uint4 pr[4], at[4], ht[8];
-    for (int j = 0; j < maxc; ++j) {
-      const bool in = j < acnt;
-      const bool ok = in && iw >= 0 && iw < a.n_w && ia >= 0 && ia < a.n_acls && id >= 0 && id < a.n_dcls;
-      if (in && !ok) raise_flag(a.flag, MANTIS_FLAG_INDEX);
-      if (ok) {
+    for (int j = 0; j < mc; j += 4) {
+      // this group's indices, validated: all three in range, or -1
+      const bool v4 = iw >= 0 && iw < a.n_w && ia >= 0 && ia < a.n_acls && id >= 0 && id < a.n_dcls;
+      const int32_t w4 = v4 ? int32_t(iw) : -1, a4 = v4 ? int32_t(ia) : -1, d4 = v4 ? int32_t(id) : -1;
+      if (j + 4 < mc) fetch(j + 4);
+      auto step = [&](int u, int32_t w, int32_t ac, int32_t dc) {
+        const bool in = j + u < acnt;
+        const bool ok = in && w >= 0;
+        if (in && !ok) raise_flag(a.flag, MANTIS_FLAG_INDEX);
+        if (ok) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          pr[i] = *reinterpret_cast<const uint4*>(a.pre + (uint32_t(iw) * uint32_t(kK) + uint32_t(32 * i + 8 * aq)));
-          at[i] = *reinterpret_cast<const uint4*>(a.act_table + (uint32_t(ia) * uint32_t(kK) + uint32_t(32 * i + 8 * aq)));
+          for (int i = 0; i < 4; ++i) {
+            pr[i] = *reinterpret_cast<const uint4*>(a.pre + (uint32_t(w) * uint32_t(kK) + uint32_t(32 * i + 8 * aq)));
+            at[i] = *reinterpret_cast<const uint4*>(a.act_table + (uint32_t(ac) * uint32_t(kK) + uint32_t(32 * i + 8 * aq)));
+          }
+#pragma unroll
+          for (int k = 0; k < 8; ++k)
+            ht[k] = *reinterpret_cast<const uint4*>(a.head_tab + (uint32_t(dc) * uint32_t(kN1) + uint32_t(32 * k + 8 * aq)));
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const f16x8_t pv = __builtin_bit_cast(f16x8_t, pr[i]), tv = __builtin_bit_cast(f16x8_t, at[i]);
+#pragma unroll
+            for (int t = 0; t < 8; ++t) av[8 * i + t] += fmaxf(float(pv[t]) + float(tv[t]), 0.f);
+          }
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            const f16x8_t hv = __builtin_bit_cast(f16x8_t, ht[k]);
+#pragma unroll
+            for (int t = 0; t < 8; ++t) ev[8 * k + t] += float(hv[t]);
+          }
         }
-#pragma unroll
-        for (int k = 0; k < 8; ++k)
-          ht[k] = *reinterpret_cast<const uint4*>(a.head_tab + (uint32_t(id) * uint32_t(kN1) + uint32_t(32 * k + 8 * aq)));
-      }
-      if (j + 1 < maxc) fetch(j + 1);
-      if (ok) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const f16x8_t pv = __builtin_bit_cast(f16x8_t, pr[i]), tv = __builtin_bit_cast(f16x8_t, at[i]);
-#pragma unroll
-          for (int t = 0; t < 8; ++t) av[8 * i + t] += fmaxf(float(pv[t]) + float(tv[t]), 0.f);
-        }
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          const f16x8_t hv = __builtin_bit_cast(f16x8_t, ht[k]);
-#pragma unroll
-          for (int t = 0; t < 8; ++t) ev[8 * k + t] += float(hv[t]);
-        }
-      }
+      };
+      step(0, from_quad<0>(w4), from_quad<0>(a4), from_quad<0>(d4));
+      if (j + 1 < mc) step(1, from_quad<1>(w4), from_quad<1>(a4), from_quad<1>(d4));
+      if (j + 2 < mc) step(2, from_quad<2>(w4), from_quad<2>(a4), from_quad<2>(d4));
+      if (j + 3 < mc) step(3, from_quad<3>(w4), from_quad<3>(a4), from_quad<3>(d4));
     }
     // EMPTY-class action rows, weighted by the cell's counts (the walk lane's
     // cell: the row of MFMA lane src_m; cell indices fit int32, host check)
@@ -247,13 +273,23 @@ __global__ void __launch_bounds__(kThreads) cell_heads_kernel(HeadArgs a) {
           const float n = float(a.act_empty[arow * 3 + o]);
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            float r[8];
-            load8(a.empty_rows + o * kK + 32 * i + 8 * aq, r);
+            const float4 r0 = *reinterpret_cast<const float4*>(sempty + o * kK + 32 * i + 8 * aq);
+            const float4 r1 = *reinterpret_cast<const float4*>(sempty + o * kK + 32 * i + 8 * aq + 4);
+            const float r[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
 #pragma unroll
             for (int t = 0; t < 8; ++t) av[8 * i + t] = fmaf(n, r[t], av[8 * i + t]);
           }
         }
       }
+    }
+    // g_half[pos]: from the wavefront's staged row when every cell of the
+    // tile is in the first cell's position, else from memory
+    bool staged = false;
+    if constexpr (kGLds) {
+      staged = p0 >= 0 && __builtin_amdgcn_ballot_w64(pos >= 0 && pos != p0) == 0;
+      if (staged)  // one 16-byte piece per lane
+        *reinterpret_cast<float4*>(sgh + wave * kN1 + 4 * lane) =
+            *reinterpret_cast<const float4*>(a.g_half + p0 * kN1 + 4 * lane);
     }
     // ---- back to the MFMA layout: the action rows as fp16 B fragments, the
     // class sums as the fp32 addends of the hidden tiles
@@ -312,7 +348,8 @@ __global__ void __launch_bounds__(kThreads) cell_heads_kernel(HeadArgs a) {
         float4 add = *reinterpret_cast<const float4*>(sb1 + f);
         add.x += ext[nt][0], add.y += ext[nt][1], add.z += ext[nt][2], add.w += ext[nt][3];
         if (pos >= 0) {
-          const float4 r = *reinterpret_cast<const float4*>(a.g_half + pos * kN1 + f);
+          const float4 r = staged ? *reinterpret_cast<const float4*>(sgh + wave * kN1 + f)
+                                  : *reinterpret_cast<const float4*>(a.g_half + pos * kN1 + f);
           add.x += r.x, add.y += r.y, add.z += r.z, add.w += r.w;
         }
         acc[0] = fmaxf(acc[0] + add.x, 0.f);
@@ -378,7 +415,8 @@ extern "C" int32_t mantis_cell_heads(const void* c, int32_t c_dtype, int32_t lay
     return MANTIS_E_ARG;
   // gathered rows use 32-bit element offsets
   if (n_w > 4294967295LL / kK || n_acls > 4294967295LL / kK || n_dcls > 4294967295LL / kN1) return MANTIS_E_ARG;
-  if (n_cells > 2147483647LL) return MANTIS_E_ARG;  // cell indices move between lanes as int32
+  // cell and position indices move between lanes as int32
+  if (n_cells > 2147483647LL || n_pos > 2147483647LL) return MANTIS_E_ARG;
   for (const void* p : {c, w1, static_cast<const void*>(b1), w2, w3,
                         static_cast<const void*>(b3), act_table,
                         static_cast<const void*>(empty_rows), head_tab,
