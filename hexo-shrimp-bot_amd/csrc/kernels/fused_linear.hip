@@ -112,11 +112,11 @@ struct Smem {
 
 // Wavefronts sharing one LDS copy of the weights: 8; 16 for the widest
 // projection, whose 139 KB of weights leave room for one workgroup per CU
-// (the extra wavefronts keep more rows in flight); 12 for the pair MLPs,
-// whose three 128-wide matrices (104 KB) also allow a single workgroup per
-// CU and whose registers allow three wavefronts per SIMD
+// (the extra wavefronts keep more rows in flight).  The pair MLPs keep the
+// next tile's two rows and this tile's row adds in registers: 8 wavefronts
+// (two per SIMD) leave them the registers for that.
 template <int N1, bool kX2 = false, bool kStage2 = false>
-constexpr int threads_for() { return N1 >= 512 ? 1024 : (kX2 && kStage2 && N1 == 128 ? 768 : 512); }
+constexpr int threads_for() { return N1 >= 512 ? 1024 : 512; }
 
 // kPair (single stage, fp16 out): the W1 rows are staged permuted so that
 // feature tiles 2k and 2k+1 leave lane group g holding the eight consecutive
@@ -166,39 +166,114 @@ __global__ void __launch_bounds__((threads_for<N1, kX2, kStage2>())) fused_linea
   const int64_t n_tiles = (a.m + kTileRows - 1) / kTileRows;
   const TX* xp = static_cast<const TX*>(a.x);
 
-  // This lane's 32 features of its row of tile t (4 chunks of 8), through
-  // the optional row gather.  Software pipeline: the next tile's chunks are
-  // requested before the current tile computes, so its HBM latency overlaps
-  // the LayerNorm, the products and the stores.
-  auto fetch = [&](int64_t t, float (&dst)[4][8]) {
-    const int64_t r = t * kTileRows + wave * 16 + l16;
-    int64_t src = (t < n_tiles && r < a.m) ? r : -1;
-    if (src >= 0 && a.x_rows) {
-      src = a.x_rows[r];
-      if (src >= a.n_x) {
-        raise_flag(a.flag, MANTIS_FLAG_INDEX);
-        src = -1;
-      }
+  // Software pipeline: the rows of tile t + gridDim.x (and, through x_rows,
+  // the gather index of the tile after) are requested before tile t
+  // computes, so their latency overlaps the LayerNorm, the products and the
+  // stores.  Every load goes unconditionally to a clamped, valid row and is
+  // kept raw (16-byte chunks); rows are widened, and dead or invalid ones
+  // zeroed, only where they are used.  A load whose value is consumed inside
+  // a branch would make the wavefront wait there for it and, the counters
+  // being in order, for every load and store issued before it.
+  constexpr int kRX = sizeof(TX) == 2 ? 4 : 8;    // chunks of this lane's 32 features
+  constexpr int kRX2 = sizeof(TX2) == 2 ? 4 : 8;
+  static_assert(sizeof(TX) == 2 || sizeof(TX) == 4, "fp16 or fp32 rows");
+  // the pair MLPs (128 wide) request their tile's row adds with the tile's
+  // rows, ahead of the next tile's; the other shapes read them in the loop
+  constexpr bool kEarlyAdd = kX2 && kStage2 && N1 == 128;
+  const int64_t G = gridDim.x;
+  auto row_of = [&](int64_t t) { return t * kTileRows + wave * 16 + l16; };
+  auto row_ok = [&](int64_t t) { return t < n_tiles && row_of(t) < a.m; };
+  auto idx_at = [&](int64_t t) -> int64_t { return a.x_rows[row_ok(t) ? row_of(t) : 0]; };
+  // the source row of a tile's lane: -1 past the end and for a negative
+  // gather index (a zero row), and for one past the rows (flagged)
+  auto src_of = [&](int64_t t, int64_t idx) -> int64_t {
+    if (!row_ok(t)) return -1;
+    if (!a.x_rows) return row_of(t);
+    if (idx >= a.n_x) {
+      raise_flag(a.flag, MANTIS_FLAG_INDEX);
+      return -1;
     }
+    return idx < 0 ? -1 : idx;
+  };
+  auto load_x = [&](int64_t src, uint4 (&d)[kRX]) {
+    const TX* p = xp + (src >= 0 ? src : 0) * a.ldx + 8 * g;
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      if (src >= 0) load_chunk(xp + src * a.ldx + 32 * ks + 8 * g, dst[ks]);
-      else
+    for (int i = 0; i < kRX; ++i)
+      d[i] = *reinterpret_cast<const uint4*>(p + (kRX == 4 ? 32 * i : 32 * (i >> 1) + 4 * (i & 1)));
+  };
+  auto load_x2 = [&](int64_t t, uint4 (&d)[kRX2]) {
+    const TX2* p = static_cast<const TX2*>(a.x2) + (row_ok(t) ? row_of(t) : 0) * a.ldx2 + 8 * g;
 #pragma unroll
-        for (int t2 = 0; t2 < 8; ++t2) dst[ks][t2] = 0.f;
+    for (int i = 0; i < kRX2; ++i)
+      d[i] = *reinterpret_cast<const uint4*>(p + (kRX2 == 4 ? 32 * i : 32 * (i >> 1) + 4 * (i & 1)));
+  };
+  // chunk ks (8 features 32 ks + 8 g ..) of a raw row, widened; zeros when !ok
+  auto widen = [&](const uint4* d, int n_raw, int ks, bool ok, float (&v)[8]) {
+    if (n_raw == 4) {
+      const f16x8_t h = __builtin_bit_cast(f16x8_t, d[ks]);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) v[t] = ok ? float(h[t]) : 0.f;
+    } else {
+      const float4 lo = __builtin_bit_cast(float4, d[2 * ks]), hi = __builtin_bit_cast(float4, d[2 * ks + 1]);
+      const float u[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+      for (int t = 0; t < 8; ++t) v[t] = ok ? u[t] : 0.f;
     }
   };
-  float xn[4][8];
-  fetch(blockIdx.x, xn);
-  for (int64_t tile = blockIdx.x; tile < n_tiles; tile += gridDim.x) {
-    const int64_t row = tile * kTileRows + wave * 16 + l16;
+  int64_t src_n = src_of(blockIdx.x, a.x_rows ? idx_at(blockIdx.x) : 0);
+  uint4 xr[kRX], x2r[kX2 ? kRX2 : 1];
+  load_x(src_n, xr);
+  if constexpr (kX2) load_x2(blockIdx.x, x2r);
+  int64_t grp_n = a.add2 ? a.add2_rows[row_ok(blockIdx.x) ? row_of(blockIdx.x) : 0] : 0;
+  int64_t idx_n = a.x_rows ? idx_at(blockIdx.x + G) : 0;  // the gather index one tile ahead
+  for (int64_t tile = blockIdx.x; tile < n_tiles; tile += G) {
+    const int64_t row = row_of(tile);
     const bool live = row < a.m;
+    const int64_t src = src_n;
     float xv[4][8];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) widen(xr, kRX, ks, src >= 0, xv[ks]);
+    float x2v[kX2 ? 4 : 1][8];
+    if constexpr (kX2)
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) widen(x2r, kRX2, ks, live, x2v[ks]);
+    // ---- row-group of the per-group add (validated once per row)
+    int64_t grp = -1;
+    if (a.add2) {
+      if (live && (grp_n < 0 || grp_n >= a.n_add2)) raise_flag(a.flag, MANTIS_FLAG_INDEX);
+      else if (live) grp = grp_n;
+    }
+    // ---- this tile's row adds (pair MLPs), before the next tile's rows
+    float4 ea1[kEarlyAdd ? N1 / 16 : 1], ea2[kEarlyAdd ? N1 / 16 : 1];
+    if constexpr (kEarlyAdd) {
+      const int64_t r1 = live ? row : 0, g2 = grp >= 0 ? grp : 0;
+#pragma unroll
+      for (int nt = 0; nt < N1 / 16; ++nt) {
+        const int f = 16 * nt + 4 * g;
+        ea1[nt] = a.add1 ? *reinterpret_cast<const float4*>(a.add1 + r1 * a.ld_add1 + f) : make_float4(0.f, 0.f, 0.f, 0.f);
+        ea2[nt] = a.add2 ? *reinterpret_cast<const float4*>(a.add2 + g2 * N1 + f) : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+    // ---- the next tile's rows (and the gather index of the tile after),
+    // into the registers this tile's rows were widened from: no copy at the
+    // loop's back edge, which would have to wait for the loads.  The widened
+    // values are materialised first (the empty statements take them as
+    // operands; the last one orders the loads after them).
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-      for (int t = 0; t < 8; ++t) xv[ks][t] = xn[ks][t];
-    fetch(tile + gridDim.x, xn);
+      for (int t = 0; t < 8; ++t) asm volatile("" : "+v"(xv[ks][t]));
+    if constexpr (kX2)
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) asm volatile("" : "+v"(x2v[ks][t]));
+    asm volatile("" ::: "memory");
+    src_n = src_of(tile + G, idx_n);
+    load_x(src_n, xr);
+    if constexpr (kX2) load_x2(tile + G, x2r);
+    if (a.add2) grp_n = a.add2_rows[row_ok(tile + G) ? row_of(tile + G) : 0];
+    if (a.x_rows) idx_n = idx_at(tile + 2 * G);
     if constexpr (kLN) {
       float s = 0.f;
 #pragma unroll
@@ -234,29 +309,13 @@ __global__ void __launch_bounds__((threads_for<N1, kX2, kStage2>())) fused_linea
       }
     f16x8_t x2b[4], x2l[kSplit && kX2 ? 4 : 1];
     if constexpr (kX2) {
-      const TX2* x2p = static_cast<const TX2*>(a.x2);
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        float v2[8];
-        if (live) load_chunk(x2p + row * a.ldx2 + 32 * ks + 8 * g, v2);
-        else
-#pragma unroll
-          for (int t = 0; t < 8; ++t) v2[t] = 0.f;
+      for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
-          x2b[ks][t] = f2h(v2[t]);
-          if constexpr (kSplit) x2l[ks][t] = _Float16(v2[t] - float(x2b[ks][t]));
+          x2b[ks][t] = f2h(x2v[ks][t]);
+          if constexpr (kSplit) x2l[ks][t] = _Float16(x2v[ks][t] - float(x2b[ks][t]));
         }
-      }
-    }
-    // ---- row-group offset of the per-group add (validated once per row)
-    int64_t grp = -1;
-    if (live && a.add2) {
-      grp = a.add2_rows[row];
-      if (grp < 0 || grp >= a.n_add2) {
-        raise_flag(a.flag, MANTIS_FLAG_INDEX);
-        grp = -1;
-      }
     }
     // ---- stage 1, one 16-feature tile at a time: h^T = W1 . x-hat^T (+ W2 . x2^T),
     // then bias / row adds / activation; without a second stage the tile is
@@ -285,13 +344,17 @@ __global__ void __launch_bounds__((threads_for<N1, kX2, kStage2>())) fused_linea
       // kPair the four at pair_feature(nt, g, 0)
       const int f = kPair ? pair_feature(nt, g, 0) : 16 * nt + 4 * g;
       float4 add = *reinterpret_cast<const float4*>(sb1 + f);
-      if (live && a.add1) {
-        const float4 r = *reinterpret_cast<const float4*>(a.add1 + row * a.ld_add1 + f);
-        add.x += r.x, add.y += r.y, add.z += r.z, add.w += r.w;
+      if (a.add1) {
+        float4 r;
+        if constexpr (kEarlyAdd) r = ea1[nt];
+        else r = *reinterpret_cast<const float4*>(a.add1 + (live ? row : 0) * a.ld_add1 + f);
+        if (live) add.x += r.x, add.y += r.y, add.z += r.z, add.w += r.w;
       }
-      if (grp >= 0) {
-        const float4 r = *reinterpret_cast<const float4*>(a.add2 + grp * N1 + f);
-        add.x += r.x, add.y += r.y, add.z += r.z, add.w += r.w;
+      if (a.add2) {
+        float4 r;
+        if constexpr (kEarlyAdd) r = ea2[nt];
+        else r = *reinterpret_cast<const float4*>(a.add2 + (grp >= 0 ? grp : 0) * N1 + f);
+        if (grp >= 0) add.x += r.x, add.y += r.y, add.z += r.z, add.w += r.w;
       }
       acc[0] += add.x, acc[1] += add.y, acc[2] += add.z, acc[3] += add.w;
       if constexpr (kRelu)
