@@ -30,8 +30,8 @@
 // Weights live in LDS (permuted while they are staged) for the persistent
 // workgroup, one workgroup per CU (8 or 12 wavefronts, see waves_for).  Tiles are dealt out XCD-contiguously:
 // the workgroups of one XCD (dispatch is round-robin over the 8 XCDs) sweep
-// one contiguous eighth of the rows, so the gathered k/v rows of a position
-// stay in that XCD's L2.
+// one contiguous eighth of the rows, a tile at a time from a counter per
+// XCD, so the gathered k/v rows of a position stay in that XCD's L2.
 //
 // The class-bias tables of the stages sit in LDS beside the weights (they
 // are gathered once per entry and head: from LDS they cost no L1 access).
@@ -52,6 +52,8 @@
 // bitwise those of the natural order.
 #include "common.hpp"
 #include "mfma.hpp"
+
+#include <mutex>
 
 namespace mantis {
 namespace {
@@ -90,6 +92,27 @@ struct Stage {
   const float* bo;
 };
 
+// The library's own tile counters, for callers that pass none (see
+// mantis_attention_substages): calls that overlap on one device share them.
+// Host code reads each device's copy's address once, with that device
+// current, and passes the address.
+__device__ uint32_t g_tile_counters[2 * kXcds * 32];
+constexpr int kMaxDevices = 64;
+std::mutex g_counters_mutex;
+uint32_t* g_counters_addr[kMaxDevices] = {};
+
+uint32_t* counters_for_current_device() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_counters_mutex);
+  if (!g_counters_addr[dev]) {
+    void* addr = nullptr;
+    if (hipGetSymbolAddress(&addr, HIP_SYMBOL(g_tile_counters)) != hipSuccess || !addr) return nullptr;
+    g_counters_addr[dev] = static_cast<uint32_t*>(addr);
+  }
+  return g_counters_addr[dev];
+}
+
 struct SubArgs {
   void* x;  // fp32 or fp16 rows (the kernel's TX)
   int64_t ldx;
@@ -99,6 +122,7 @@ struct SubArgs {
   int32_t bias_off[2];   // each stage's table in the LDS bias pool
   float scale;
   int32_t* flag;
+  uint32_t* counters;  // per XCD (128 bytes apart): next tile, then wavefronts done
 };
 
 // the value v of lane 4 (lane / 4) + u (one DPP quad broadcast)
@@ -210,7 +234,19 @@ __global__ void __launch_bounds__(waves_for<kStages>() * 64) attn_substage_kerne
     if (!order) return slot < a.n_rows ? int32_t(slot) : 0;
     return order[slot < a.n_rows ? slot : 0];
   };
-  const int64_t tile0 = t_begin + int64_t(blockIdx.x / kXcds) * kWaves + wave;
+  // Tiles are handed out one at a time from the XCD's counter, so the
+  // wavefronts of an XCD stay within a narrow window of tiles whatever their
+  // tiles cost, and the gathered rows of that window stay in its L2 (with a
+  // fixed share per wavefront, cheap and costly tiles let the wavefronts
+  // drift apart and the rows were fetched into L2 about twice: 898 -> 787 us)
+  uint32_t* const next_ctr = a.counters + 32 * xcd;
+  uint32_t* const done_ctr = a.counters + 32 * (kXcds + xcd);
+  auto claim = [&]() -> int64_t {
+    uint32_t v = 0;
+    if (lane == 0) v = atomicAdd(next_ctr, 1u);
+    return t_begin + int64_t(__builtin_amdgcn_readfirstlane(v));
+  };
+  const int64_t tile0 = claim();
   auto clamp_row = [&](int64_t r) -> int64_t { return r >= 0 && r < a.n_rows ? r : 0; };
   // Look-ahead across tiles: when a tile starts, the order word of its row
   // and the row's CSR bounds are in registers.  The next tile's order word is
@@ -227,7 +263,9 @@ __global__ void __launch_bounds__(waves_for<kStages>() * 64) attn_substage_kerne
       pb_n[s] = a.st[s].seg_ptr[rc + 1];
     }
   }
-  for (int64_t tile = tile0; tile < t_end; tile += waves_here) {
+  int64_t next = tile0;
+  for (int64_t tile = tile0; tile < t_end; tile = next) {
+    next = claim();  // the tile after this one (its row is loaded ahead)
     // an offset the compiler cannot see through: keeps the weight-fragment
     // reads inside the loop instead of hoisting all of them into registers
     int lds_off = 0;
@@ -302,7 +340,7 @@ __global__ void __launch_bounds__(waves_for<kStages>() * 64) attn_substage_kerne
       int32_t s4 = valid_src(es[s]), c4 = valid_cls(ec[s]);
       // the next tile's order word, after the tile's first loads (the counters
       // are in order: waiting for those does not wait for it)
-      if (s == 0) row_n = order_at(tile + waves_here < t_end ? tile + waves_here : tile);
+      if (s == 0) row_n = order_at(next < t_end ? next : tile);
       // ---- LayerNorm + Q projection
       if constexpr (kPacked) {
 #pragma unroll
@@ -472,6 +510,13 @@ __global__ void __launch_bounds__(waves_for<kStages>() * 64) attn_substage_kerne
       }
     }
   }
+  // Every wavefront has made its last claim (one past the XCD's tiles): the
+  // XCD's last wavefront to get here leaves both counters at zero for the
+  // next launch
+  if (lane == 0 && atomicAdd(done_ctr, 1u) == uint32_t(waves_here) - 1) {
+    *next_ctr = 0u;
+    *done_ctr = 0u;
+  }
 }
 
 template <int kStages, bool kVcls, typename TX>
@@ -519,7 +564,8 @@ using namespace mantis;
 
 extern "C" int32_t mantis_attention_substages(void* x, int32_t x_dtype, int64_t ldx, int64_t n_rows,
                                               const int32_t* row_order, const mantis_substage* stages,
-                                              int32_t n_stages, int32_t* err_flag, void* stream) {
+                                              int32_t n_stages, int32_t* err_flag, uint32_t* tile_counters,
+                                              void* stream) {
   if (n_rows < 0 || !stages || n_stages < 1 || n_stages > 2) return MANTIS_E_ARG;
   if (n_rows == 0) return MANTIS_OK;
   for (int s = 0; s < n_stages; ++s)
@@ -544,6 +590,8 @@ extern "C" int32_t mantis_attention_substages(void* x, int32_t x_dtype, int64_t 
   if (pool > kBiasPool) return MANTIS_E_ARG;  // the class-bias tables must fit their LDS pool
   a.scale = 0.17677669529663687f;  // 1/sqrt(32)
   a.flag = err_flag;
+  a.counters = tile_counters ? tile_counters : counters_for_current_device();
+  if (!a.counters) return MANTIS_E_LAUNCH;
   const bool vc = stages[0].vcls != nullptr;
   // instantiated: fp32 rows (windows, one stage, and the cell stages' fp32
   // form), fp16 rows (the cells' two stages)
@@ -562,5 +610,5 @@ extern "C" int32_t mantis_attention_substage(float* x, int64_t ldx, int64_t n_ro
                                              int64_t n_entries, const void* wo, const float* bo,
                                              int32_t* err_flag, void* stream) {
   const mantis_substage d{wq, bq, k, v, ldk, ldv, n_src, bias, n_classes, vcls, seg_ptr, src, cls, n_entries, wo, bo};
-  return mantis_attention_substages(x, MANTIS_F32, ldx, n_rows, nullptr, &d, 1, err_flag, stream);
+  return mantis_attention_substages(x, MANTIS_F32, ldx, n_rows, nullptr, &d, 1, err_flag, nullptr, stream);
 }

@@ -22,13 +22,16 @@
 // W1, W2 and W3 live in LDS for the persistent workgroup (8 wavefronts,
 // one workgroup per CU).  Tiles are dealt out XCD-contiguously: the
 // workgroups of one XCD (dispatch is round-robin over the 8 XCDs) sweep one
-// contiguous eighth of the tiles, so the action-projection rows a position's
-// cells gather are fetched into one XCD's L2.  An optional row order (a permutation of the cells)
+// contiguous eighth of the tiles, a tile at a time from a counter per XCD,
+// so the action-projection rows a position's cells gather are fetched into
+// one XCD's L2 while its wavefronts work on neighbouring tiles.  An optional row order (a permutation of the cells)
 // groups cells of similar decoder run lengths into tiles, since a tile's
 // walk runs as long as its longest run; each cell's arithmetic is the same
 // in any order.
 #include "common.hpp"
 #include "mfma.hpp"
+
+#include <mutex>
 
 namespace mantis {
 namespace {
@@ -49,6 +52,27 @@ constexpr int kP3 = kN1 + 8;
 constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * 64;
 constexpr int kXcds = 8;
+
+// The library's own tile counters, for callers that pass none (see
+// mantis_cell_heads): calls that overlap on one device share them.  Host
+// code reads each device's copy's address once, with that device current,
+// and passes the address.
+__device__ uint32_t g_head_counters[2 * kXcds * 32];
+constexpr int kMaxDevices = 64;
+std::mutex g_counters_mutex;
+uint32_t* g_counters_addr[kMaxDevices] = {};
+
+uint32_t* counters_for_current_device() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_counters_mutex);
+  if (!g_counters_addr[dev]) {
+    void* addr = nullptr;
+    if (hipGetSymbolAddress(&addr, HIP_SYMBOL(g_head_counters)) != hipSuccess || !addr) return nullptr;
+    g_counters_addr[dev] = static_cast<uint32_t*>(addr);
+  }
+  return g_counters_addr[dev];
+}
 
 struct HeadArgs {
   const void* c;
@@ -78,6 +102,7 @@ struct HeadArgs {
   float* out;                // (n_cells, 16)
   const int32_t* order;      // tile slot -> cell, or null
   int32_t* flag;
+  uint32_t* counters;        // per XCD (128 bytes apart): next tile, then wavefronts done
 };
 
 // hi + lo fp16 pair of x (lo: the residual of the rounding, unsaturated)
@@ -120,7 +145,7 @@ __global__ void __launch_bounds__(kThreads) cell_heads_kernel(HeadArgs a) {
   const int src_a = 4 * l16 + g;                   // walk lane of this MFMA lane's (cell, group)
   const int64_t n_tiles = (a.n_cells + 15) / 16;
   const int xcd = int(blockIdx.x % kXcds);
-  const int64_t stride = (int64_t(gridDim.x) - xcd + kXcds - 1) / kXcds * kWaves;  // waves of this XCD
+  const int64_t waves_here = (int64_t(gridDim.x) - xcd + kXcds - 1) / kXcds * kWaves;  // waves of this XCD
   const int64_t t_begin = n_tiles * xcd / kXcds, t_end = n_tiles * (xcd + 1) / kXcds;
   // the cell of a tile slot (raw: validated where it is used), one tile ahead
   auto order_at = [&](int64_t t) -> int64_t {
@@ -128,9 +153,20 @@ __global__ void __launch_bounds__(kThreads) cell_heads_kernel(HeadArgs a) {
     if (!a.order) return slot;
     return a.order[slot < a.n_cells ? slot : 0];
   };
-  const int64_t tile0 = t_begin + int64_t(blockIdx.x / kXcds) * kWaves + wave;
+  // tiles one at a time from the XCD's counter: the XCD's wavefronts stay
+  // within a narrow window of tiles, whose gathered rows stay in its L2
+  uint32_t* const next_ctr = a.counters + 32 * xcd;
+  uint32_t* const done_ctr = a.counters + 32 * (kXcds + xcd);
+  auto claim = [&]() -> int64_t {
+    uint32_t v = 0;
+    if (lane == 0) v = atomicAdd(next_ctr, 1u);
+    return t_begin + int64_t(__builtin_amdgcn_readfirstlane(v));
+  };
+  const int64_t tile0 = claim();
   int64_t next_row = tile0 < t_end ? order_at(tile0) : 0;
-  for (int64_t tile = tile0; tile < t_end; tile += stride) {
+  int64_t next = tile0;
+  for (int64_t tile = tile0; tile < t_end; tile = next) {
+    next = claim();
     // an offset the compiler cannot see through: keeps the weight-fragment
     // reads inside the loop instead of hoisting them into registers
     int lds_off = 0;
@@ -139,7 +175,7 @@ __global__ void __launch_bounds__(kThreads) cell_heads_kernel(HeadArgs a) {
     const _Float16* w2s = sw2 + lds_off;
     const _Float16* w3s = sw3 + lds_off;
     const int64_t row = next_row;
-    next_row = order_at(tile + stride < t_end ? tile + stride : tile);
+    next_row = order_at(next < t_end ? next : tile);
     const bool in_tile = tile * 16 + l16 < a.n_cells;
     const bool live = in_tile && row >= 0 && row < a.n_cells;
     if (in_tile && !live) raise_flag(a.flag, MANTIS_FLAG_INDEX);
@@ -389,6 +425,12 @@ __global__ void __launch_bounds__(kThreads) cell_heads_kernel(HeadArgs a) {
           make_float4(y[0] + bb.x, y[1] + bb.y, y[2] + bb.z, y[3] + bb.w);
     }
   }
+  // every wavefront has made its last claim: the XCD's last one to get here
+  // leaves both counters at zero for the next launch
+  if (lane == 0 && atomicAdd(done_ctr, 1u) == uint32_t(waves_here) - 1) {
+    *next_ctr = 0u;
+    *done_ctr = 0u;
+  }
 }
 
 }  // namespace
@@ -405,7 +447,7 @@ extern "C" int32_t mantis_cell_heads(const void* c, int32_t c_dtype, int32_t lay
                                      const float* g_half, int64_t n_pos, const int64_t* cell_pos,
                                      const int64_t* dec_ptr, const int64_t* dec_window, const int64_t* act_class,
                                      const int64_t* dec_class, int64_t n_entries, float* out, int32_t* err_flag,
-                                     void* stream) {
+                                     uint32_t* tile_counters, void* stream) {
   if (n_cells == 0) return MANTIS_OK;
   if (!c || !w1 || !b1 || !w2 || !w3 || !b3 || !act_table || !empty_rows || !act_empty || !head_tab || !g_half ||
       !cell_pos || !dec_ptr || !out || n_cells < 0 || n_pos <= 0 || n_acls <= 0 || n_dcls <= 0 || ldc < kK ||
@@ -427,7 +469,9 @@ extern "C" int32_t mantis_cell_heads(const void* c, int32_t c_dtype, int32_t lay
              static_cast<const _Float16*>(w3), b3, static_cast<const _Float16*>(pre), n_w,
              static_cast<const _Float16*>(act_table), n_acls, empty_rows, act_empty,
              static_cast<const _Float16*>(head_tab), n_dcls, g_half, n_pos, cell_pos, dec_ptr, dec_window, act_class,
-             dec_class, n_entries, out, row_order, err_flag};
+             dec_class, n_entries, out, row_order, err_flag,
+             tile_counters ? tile_counters : counters_for_current_device()};
+  if (!a.counters) return MANTIS_E_LAUNCH;
   int dev = 0, cus = 0;
   if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
                                               hipSuccess || cus <= 0)

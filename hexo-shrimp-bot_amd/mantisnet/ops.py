@@ -134,6 +134,24 @@ def _on_gpu(*ts: Tensor) -> torch.device:
     return dev
 
 
+_TILE_COUNTERS = 512  # uint32 per set (MANTIS_TILE_COUNTERS)
+_counters: dict[tuple[int, int], Tensor] = {}
+
+
+def tile_counters(device: torch.device) -> Tensor:
+    """The tile counters of the row kernels that hand out their tiles one at a
+    time (attention_substages, cell_heads): one zeroed set per (device,
+    stream).  Launches on one stream run in order, so no two of them use a set
+    at the same time, and every launch leaves its set at zero."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    key = (idx, torch.cuda.current_stream(torch.device("cuda", idx)).cuda_stream)
+    c = _counters.get(key)
+    if c is None:
+        c = torch.zeros(_TILE_COUNTERS, dtype=torch.int32, device=torch.device("cuda", idx))
+        _counters[key] = c
+    return c
+
+
 def error_flag(device: torch.device) -> Tensor:
     idx = device.index if device.index is not None else torch.cuda.current_device()
     f = _flags.get(idx)
@@ -858,14 +876,18 @@ def _substage_struct(st: SubStage, n: int):
     return d, (bias, vcls, seg_ptr, src, cls), e
 
 
-def attention_substages(x: Tensor, stages: list[SubStage], row_order: Tensor | None = None) -> Tensor:
+def attention_substages(x: Tensor, stages: list[SubStage], row_order: Tensor | None = None,
+                        library_counters: bool = False) -> Tensor:
     """In place on the fp32 residual rows x (n, 128), for each stage in order:
     x += fp16(attend(fp16(LN(x) wq^T + bq))) wo^T + bo, the attention typed
     by (bias, vcls) over the stage's CSR entries with k/v the two halves of
     its kv rows.  One launch for one or two stages (x stays on chip between
     them); both stages carry class values or neither does.  ``row_order``
     (int32, a permutation of the rows) sets the order rows are grouped into
-    16-row tiles in; the results do not depend on it."""
+    16-row tiles in; the results do not depend on it.  The tiles are handed
+    out from the stream's tile counters (tile_counters), or with
+    ``library_counters`` from the library's per-device set, which launches
+    running at the same time on one device would share."""
     if not 1 <= len(stages) <= 2:
         raise ValueError("one or two stages per launch")
     dev = _on_gpu(x, row_order, *[t for st in stages for t in st])
@@ -893,7 +915,7 @@ def attention_substages(x: Tensor, stages: list[SubStage], row_order: Tensor | N
         _launch(name, nbytes, flops, lambda: _check(
             _lib().mantis_attention_substages(_ptr(x), _dt(x), x.stride(0), n, _ptr(row_order),
                                               ctypes.cast(arr, ctypes.c_void_p), len(built), _ptr(error_flag(dev)),
-                                              _stream()),
+                                              None if library_counters else _ptr(tile_counters(dev)), _stream()),
             "attention_substages",
         ))
     return x
@@ -908,13 +930,15 @@ def attention_substage(x: Tensor, wq: Tensor, bq: Tensor, kv: Tensor, bias: Tens
 def cell_heads(c: Tensor, w1: Tensor, b1: Tensor, w2: Tensor, w3: Tensor, b3: Tensor, pre: Tensor,
                act_table: Tensor, empty_rows: Tensor, act_empty: Tensor, head_tab: Tensor, g_half: Tensor,
                cell_pos: Tensor, dec_ptr: Tensor, dec_window: Tensor, act_class: Tensor, dec_class: Tensor,
-               layer_norm: bool, row_order: Tensor | None = None, compensated: bool = False) -> Tensor:
+               layer_norm: bool, row_order: Tensor | None = None, compensated: bool = False,
+               library_counters: bool = False) -> Tensor:
     """(n_cells, 16) fp32 head rows of every cell in one launch (see
     mantis_cell_heads in include/mantis_hip.h): column 0 the policy logit,
     1..3 the critic logits.  ``row_order`` (int32 permutation of the cells)
     sets their grouping into tiles; the results do not depend on it.
     ``compensated`` (fp32 rows, no LayerNorm; w3 (32, 256) = [hi; lo]) runs
-    the three products on hi + lo fp16 operand pairs."""
+    the three products on hi + lo fp16 operand pairs.  Tiles are handed out
+    as in attention_substages (``library_counters`` likewise)."""
     dev = _on_gpu(c, w1, b1, w2, w3, b3, pre, act_table, empty_rows, act_empty, head_tab, g_half, cell_pos, dec_ptr,
                   dec_window, act_class, dec_class, row_order)
     if row_order is not None and (row_order.dtype != torch.int32 or row_order.shape != (c.shape[0],)):
@@ -961,7 +985,8 @@ def cell_heads(c: Tensor, w1: Tensor, b1: Tensor, w2: Tensor, w3: Tensor, b3: Te
                 _ptr(b3),
                 _ptr(pre), pre.shape[0], _ptr(act_table), act_table.shape[0], _ptr(empty_rows), _ptr(act_empty),
                 _ptr(head_tab), head_tab.shape[0], _ptr(g_half), g_half.shape[0], _ptr(cell_pos), _ptr(dec_ptr),
-                _ptr(dec_window), _ptr(act_class), _ptr(dec_class), e, _ptr(out), _ptr(error_flag(dev)), _stream(),
+                _ptr(dec_window), _ptr(act_class), _ptr(dec_class), e, _ptr(out), _ptr(error_flag(dev)),
+                None if library_counters else _ptr(tile_counters(dev)), _stream(),
             ),
             "cell_heads",
         ))

@@ -365,6 +365,12 @@ int32_t mantis_attention_substage(float* x, int64_t ldx, int64_t n_rows, const v
  * of similar entry counts saves work.  The results do not depend on it.
  * The stages' class-bias tables are staged on chip together: the sum over
  * stages of n_classes must not exceed 1344 (else MANTIS_E_ARG).
+ * tile_counters: MANTIS_TILE_COUNTERS uint32 of device memory, all zero
+ * before the first call that uses them; every call leaves them zero again.
+ * The tiles of the rows are handed out from them one at a time, so calls
+ * that run at the same time (on two streams of one device) must not share
+ * them.  NULL: the library's own per-device counters, which such calls would
+ * share.
  * Replaces the two cell sub-stages of the reference's _cell_stage (cells <-
  * windows, then cells <- stones; model.py:397-490, kernels
  * cell_latents.py:213-285, 834-1001).
@@ -388,9 +394,11 @@ typedef struct mantis_substage {
   const float* bo;
 } mantis_substage;
 
+#define MANTIS_TILE_COUNTERS 512
+
 int32_t mantis_attention_substages(void* x, int32_t x_dtype, int64_t ldx, int64_t n_rows, const int32_t* row_order,
                                    const mantis_substage* stages, int32_t n_stages, int32_t* err_flag,
-                                   void* stream);
+                                   uint32_t* tile_counters, void* stream);
 
 /*
  * Fused cell heads: for every legal cell r (position cell_pos[r]) with
@@ -407,7 +415,9 @@ int32_t mantis_attention_substages(void* x, int32_t x_dtype, int64_t ldx, int64_
  * act_empty (n_cells, 3) and the index arrays int64; out (n_cells, 16) fp32.
  * row_order, when not NULL, is a permutation of the cells (int32) in which
  * they are grouped into 16-cell tiles (see mantis_segment_order); the
- * results do not depend on it.
+ * results do not depend on it.  tile_counters: as for
+ * mantis_attention_substages (MANTIS_TILE_COUNTERS zeroed uint32, not
+ * shared by calls that run at the same time; NULL: the library's own).
  * compensated = 1 (fp32 rows, layer_norm = 0 only): x, fp16(acts) and
  * fp16(h) become hi + lo fp16 pairs and w3 is (32, 256) = [W3 hi; W3 lo]
  * (lo = the fp32 weight minus its fp16 rounding), so the three products carry
@@ -424,7 +434,8 @@ int32_t mantis_cell_heads(const void* c, int32_t c_dtype, int32_t layer_norm, in
                           const float* empty_rows, const int64_t* act_empty, const void* head_tab, int64_t n_dcls,
                           const float* g_half, int64_t n_pos, const int64_t* cell_pos, const int64_t* dec_ptr,
                           const int64_t* dec_window, const int64_t* act_class, const int64_t* dec_class,
-                          int64_t n_entries, float* out, int32_t* err_flag, void* stream);
+                          int64_t n_entries, float* out, int32_t* err_flag, uint32_t* tile_counters,
+                          void* stream);
 
 /*
  * Window <- latents broadcast fused with its output projection and residual,
