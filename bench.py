@@ -90,6 +90,23 @@ def _traffic():
     return None
 
 
+COLD_FLUSH_MIB = 512  # more than the 256 MB MALL and the L2s together
+
+
+def _cold(torch, ops, dev, name, launch, reps):
+    """The traced op `name` timed with the caches cold: a 512 MiB fill (not
+    traced) before every launch evicts its inputs from L2 and the MALL."""
+    flush = torch.empty(COLD_FLUSH_MIB * 2**20 // 4, dtype=torch.float32, device=dev)
+    launch()
+    with ops.trace(name) as tr:
+        for _ in range(reps):
+            flush.fill_(1.0)
+            launch()
+        torch.cuda.synchronize()
+    del flush
+    return tr.summary()[name]
+
+
 def isolated_attention(torch, ops, dev, reps=20):
     """B=256 sequences, L ~ U{64..512}, 8 heads, hd 32, N(0,1)."""
     import numpy as np
@@ -118,6 +135,7 @@ def isolated_attention(torch, ops, dev, reps=20):
             for _ in range(reps):
                 ops.stone_attention(*qkv, sl, schedule=sched)
         s = tr.summary()["stone_attention"]
+        c = _cold(torch, ops, dev, "stone_attention", lambda: ops.stone_attention(*qkv, sl, schedule=sched), reps)
         res[name] = {
             "avg_us": round(s["avg_us"], 2),
             "schedule_us": round(trs.summary()["stone_attention_schedule"]["avg_us"], 2),
@@ -126,8 +144,11 @@ def isolated_attention(torch, ops, dev, reps=20):
             "gbps": round(s["gbps"], 1),
             "gflop_per_launch": round(s["flops_per_launch"] / 1e9, 2),
             "mb_per_launch": round(s["bytes_per_launch"] / 1e6, 1),
+            "cold_avg_us": round(c["avg_us"], 2),
+            "cold_mfma_frac": round(c["tflops"] / MFMA_F16_PEAK_TFLOPS, 4),
         }
-    return {"config": "B=256, L~U{64..512}, H=8, hd=32, key-padding mask, no bias (warm L2/MALL)", **res}
+    return {"config": "B=256, L~U{64..512}, H=8, hd=32, key-padding mask, no bias; warm (inputs in L2/MALL) "
+                      f"and cold ({COLD_FLUSH_MIB} MiB written before each launch)", **res}
 
 
 def isolated_message_passing(torch, ops, dev, reps=20):
@@ -161,13 +182,17 @@ def isolated_message_passing(torch, ops, dev, reps=20):
         for _ in range(reps):
             ops.hex_aggregate_linear(x, nbr, w, bias)
     s = tr.summary()["hex_aggregate_linear"]
+    c = _cold(torch, ops, dev, "hex_aggregate_linear", lambda: ops.hex_aggregate_linear(x, nbr, w, bias), reps)
     ops.raise_on_device_error(dev)
     return {
-        "config": f"256 graphs, N={n} cells, 6 axial neighbours, sum+mean then Linear(128,128), bf16",
+        "config": f"256 graphs, N={n} cells, 6 axial neighbours, sum+mean then Linear(128,128), bf16; warm "
+                  f"(inputs in L2/MALL) and cold ({COLD_FLUSH_MIB} MiB written before each launch)",
         "avg_us": round(s["avg_us"], 2),
         "gbps": round(s["gbps"], 1),
         "hbm_frac": round(s["gbps"] / HBM_PEAK_GBPS, 4),
         "mb_per_launch": round(s["bytes_per_launch"] / 1e6, 2),
+        "cold_avg_us": round(c["avg_us"], 2),
+        "cold_hbm_frac": round(c["gbps"] / HBM_PEAK_GBPS, 4),
     }
 
 
