@@ -61,6 +61,7 @@ struct Args {
   void* out;
   int64_t ldo;
   int32_t* flag;
+  int32_t inplace;  // out is x itself (same rows, same stride, no gather)
 };
 
 template <typename T>
@@ -130,6 +131,12 @@ __global__ void __launch_bounds__((threads_for<N1, kX2, kStage2>())) fused_linea
   static_assert(!kPair || (!kStage2 && !kX2 && kMode == kStoreF16 && N1 % 32 == 0), "paired stores: fp16 projections");
   constexpr int kTileRows = 16 * (threads_for<N1, kX2, kStage2>() / 64);
   constexpr int kParts = kSplit ? 2 : 1;
+  // The fp16 in-place residual MLP (the window pair MLP): stage 2's outputs
+  // are staged in pair order (W3 rows permuted), so a lane's two output tiles
+  // 2k, 2k+1 are the eight features of its x chunk k: the residual comes from
+  // the row already in registers when the update is in place, and each pair
+  // leaves as one 16-byte store.  (The host requires n3 = 128 with it.)
+  constexpr bool kResidReg = kStage2 && kMode == kAddF16 && sizeof(TX) == 2 && !kSplit;
   extern __shared__ __attribute__((aligned(16))) _Float16 smem[];
   using S = Smem<N1, kStage2, kX2, kSplit>;
   _Float16* sw1 = smem;
@@ -151,7 +158,9 @@ __global__ void __launch_bounds__((threads_for<N1, kX2, kStage2>())) fused_linea
   if constexpr (kStage2) {
     for (int i = threadIdx.x; i < kParts * a.n3 * (N1 / 8); i += blockDim.x) {
       const int r = i / (N1 / 8), c = (i % (N1 / 8)) * 8;
-      *reinterpret_cast<uint4*>(sw3 + r * S::p3 + c) = *reinterpret_cast<const uint4*>(a.w3 + r * N1 + c);
+      // with kResidReg LDS row r = 16 ot + 4 g + t holds W3 row pair_feature(ot, g, t)
+      const int src = kResidReg ? pair_feature(r >> 4, (r & 15) >> 2, r & 3) : r;
+      *reinterpret_cast<uint4*>(sw3 + r * S::p3 + c) = *reinterpret_cast<const uint4*>(a.w3 + src * N1 + c);
     }
   }
   float* sb1 = reinterpret_cast<float*>(smem + S::bias_off(a.n3));
@@ -233,6 +242,12 @@ __global__ void __launch_bounds__((threads_for<N1, kX2, kStage2>())) fused_linea
     float xv[4][8];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) widen(xr, kRX, ks, src >= 0, xv[ks]);
+    // the raw row itself, kept for the in-place residual (the prefetch below
+    // reuses xr)
+    uint4 xc[kResidReg ? 4 : 1];
+    if constexpr (kResidReg)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) xc[i] = xr[i];
     float x2v[kX2 ? 4 : 1][8];
     if constexpr (kX2)
 #pragma unroll
@@ -399,7 +414,40 @@ __global__ void __launch_bounds__((threads_for<N1, kX2, kStage2>())) fused_linea
         if (live) store4<kMode>(a, row, 16 * nt + 4 * g, acc);
       }
     }
-    if constexpr (kStage2) {
+    if constexpr (kResidReg) {
+      // ---- stage 2 in output-tile pairs (n3 = 128): lane (l16, g) holds
+      // features 32 k + 8 g .. +7 of its row, the layout of its x chunk k
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        f32x4_t y2[2];
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+          const int ot = 2 * k + half;
+          f32x4_t y = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int ks = 0; ks < N1 / 32; ++ks) {
+            const _Float16* wr = sw3 + (16 * ot + l16) * S::p3 + 32 * ks;
+            const uint2 lo = *reinterpret_cast<const uint2*>(wr + 4 * g);
+            const uint2 hi = *reinterpret_cast<const uint2*>(wr + 16 + 4 * g);
+            y = mfma16x16x32(__builtin_bit_cast(f16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y)), hb[ks], y);
+          }
+          y2[half] = y;
+        }
+        if (live) {
+          const int f = 32 * k + 8 * g;
+          const float4 b0 = *reinterpret_cast<const float4*>(sb3 + f), b1 = *reinterpret_cast<const float4*>(sb3 + f + 4);
+          uint4* o = reinterpret_cast<uint4*>(static_cast<_Float16*>(a.out) + row * a.ldo + f);
+          // fp16 residual rows: widened, added in fp32, rounded once
+          const f16x8_t r = __builtin_bit_cast(f16x8_t, a.inplace ? xc[k] : *o);
+          uint4 w;
+          w.x = pack_f16x2(float(r[0]) + (y2[0][0] + b0.x), float(r[1]) + (y2[0][1] + b0.y));
+          w.y = pack_f16x2(float(r[2]) + (y2[0][2] + b0.z), float(r[3]) + (y2[0][3] + b0.w));
+          w.z = pack_f16x2(float(r[4]) + (y2[1][0] + b1.x), float(r[5]) + (y2[1][1] + b1.y));
+          w.w = pack_f16x2(float(r[6]) + (y2[1][2] + b1.z), float(r[7]) + (y2[1][3] + b1.w));
+          *o = w;
+        }
+      }
+    } else if constexpr (kStage2) {
       // ---- stage 2: y^T (n3 x 16) = W3 . h^T
       const int NT3 = a.n3 / 16;
       for (int ot = 0; ot < NT3; ++ot) {
@@ -499,7 +547,8 @@ extern "C" int32_t mantis_fused_linear(const void* x, int32_t x_dtype, int64_t l
   if (w3 && (n3 % 16 || n3 > 128)) return MANTIS_E_ARG;
   Args a{x, ldx, x_rows, x_rows ? n_x : m, m, x2, ldx2, static_cast<const _Float16*>(w1),
          static_cast<const _Float16*>(w2), b1, add1, ld_add1, add2, add2_rows, n_add2,
-         static_cast<const _Float16*>(w3), b3, n3, out, ldo, err_flag};
+         static_cast<const _Float16*>(w3), b3, n3, out, ldo, err_flag,
+         int32_t(out == x && !x_rows && ldo == ldx)};
   hipStream_t s = as_stream(stream);
   const bool ln = layer_norm != 0, r = relu != 0, st2 = w3 != nullptr, hx2 = x2 != nullptr;
   const int mode = out_mode;
@@ -543,7 +592,8 @@ extern "C" int32_t mantis_fused_linear(const void* x, int32_t x_dtype, int64_t l
     return launch<_Float16, float, false, 128, false, false, false, 3>(a, s);
   if (!hx2 && !st2 && !r && mode == 3 && n1 == 128 && !ln && x_dtype == MANTIS_F32)
     return launch<float, float, false, 128, false, false, false, 3>(a, s);
-  if (st2 && r && mode == 3 && x_dtype == MANTIS_F16 && ln && hx2 && n1 == 128 && x2_dtype == MANTIS_F16)
+  if (st2 && r && mode == 3 && x_dtype == MANTIS_F16 && ln && hx2 && n1 == 128 && x2_dtype == MANTIS_F16 &&
+      n3 == 128)  // the pair-ordered second stage is 128 wide
     return launch<_Float16, _Float16, true, 128, true, true, true, 3>(a, s);
   if (st2 && r && mode == 2 && x_dtype == MANTIS_F32 && ln) {
     if (hx2 && n1 == 128 && x2_dtype == MANTIS_F32)

@@ -105,6 +105,14 @@ def test_pair_mlp_residual(device, x2dt):
         hid = F.relu(_h(_ln(rf)) @ w1.float().t() + _h(x2.float()) @ w2.float().t() + b1 + add2[rows])
         exp16 = (rf + _h(hid) @ w3.float().t() + b3).to(H16).float()
         torch.testing.assert_close(out16.float().cpu(), exp16, rtol=3e-3, atol=3e-3)
+        # the same update into a separate copy of the rows (the residual read
+        # back from memory instead of the registers): bitwise the same
+        src16, dst16 = r16.to(device), r16.to(device)
+        ops.fused_linear(src16, w1.to(device), b1.to(device), layer_norm=True, x2=x2.to(device), w2=w2.to(device),
+                         add2=add2.to(device), add2_rows=rows.to(device), relu=True, w3=w3.to(device),
+                         b3=b3.to(device), out=dst16, residual=True)
+        ops.raise_on_device_error(device)
+        assert torch.equal(dst16.cpu(), out16.cpu()) and torch.equal(src16.cpu(), r16)
 
 
 def test_ffn_residual_with_add1(device):
