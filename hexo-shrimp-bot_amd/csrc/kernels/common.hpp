@@ -135,6 +135,47 @@ __device__ __forceinline__ void from_f32(float& d, float x) { d = x; }
 __device__ __forceinline__ void from_f32(_Float16& d, float x) { d = f2h(x); }
 __device__ __forceinline__ void from_f32(uint16_t& d, float x) { d = f2bf(x); }
 
+// Row access through a structured buffer: the descriptor holds the base,
+// the row pitch in bytes (< 16384: a 14-bit field) and the row count; an
+// access names a row index and a byte offset within the row.  A row index at
+// or past the count is out of range: a load returns zeros and a store is
+// dropped, without a memory access.  A lane with no row passes -1, so the
+// instruction needs no branch around it (a branch around a load or store
+// leaves the compiler unable to count the loads and stores in flight after
+// it, and its later waits then wait for all of them).
+typedef int32_t i32x4_t __attribute__((ext_vector_type(4)));
+typedef int32_t i32x2_t __attribute__((ext_vector_type(2)));
+__device__ i32x4_t llvm_struct_buffer_load_x4(i32x4_t rsrc, int32_t vindex, int32_t voffset, int32_t soffset,
+                                              int32_t aux) __asm("llvm.amdgcn.struct.buffer.load.v4i32");
+__device__ i32x2_t llvm_struct_buffer_load_x2(i32x4_t rsrc, int32_t vindex, int32_t voffset, int32_t soffset,
+                                              int32_t aux) __asm("llvm.amdgcn.struct.buffer.load.v2i32");
+__device__ void llvm_struct_buffer_store_x4(i32x4_t data, i32x4_t rsrc, int32_t vindex, int32_t voffset,
+                                            int32_t soffset, int32_t aux) __asm("llvm.amdgcn.struct.buffer.store.v4i32");
+__device__ void llvm_struct_buffer_store_x2(i32x2_t data, i32x4_t rsrc, int32_t vindex, int32_t voffset,
+                                            int32_t soffset, int32_t aux) __asm("llvm.amdgcn.struct.buffer.store.v2i32");
+
+__device__ __forceinline__ i32x4_t rows_rsrc(const void* base, uint32_t pitch_bytes, uint32_t n_rows) {
+  const uint64_t p = reinterpret_cast<uint64_t>(base);
+  i32x4_t r;
+  r.x = int32_t(uint32_t(p));
+  r.y = int32_t((uint32_t(p >> 32) & 0xFFFFu) | (pitch_bytes << 16));
+  r.z = int32_t(n_rows);
+  r.w = 0x00020000;  // 32-bit data format, no swizzle, index from the lane
+  return r;
+}
+__device__ __forceinline__ uint4 row_load16(i32x4_t rsrc, int32_t row, int32_t byte_off) {
+  return __builtin_bit_cast(uint4, llvm_struct_buffer_load_x4(rsrc, row, byte_off, 0, 0));
+}
+__device__ __forceinline__ uint2 row_load8(i32x4_t rsrc, int32_t row, int32_t byte_off) {
+  return __builtin_bit_cast(uint2, llvm_struct_buffer_load_x2(rsrc, row, byte_off, 0, 0));
+}
+__device__ __forceinline__ void row_store16(i32x4_t rsrc, int32_t row, int32_t byte_off, uint4 v) {
+  llvm_struct_buffer_store_x4(__builtin_bit_cast(i32x4_t, v), rsrc, row, byte_off, 0, 0);
+}
+__device__ __forceinline__ void row_store8(i32x4_t rsrc, int32_t row, int32_t byte_off, uint2 v) {
+  llvm_struct_buffer_store_x2(__builtin_bit_cast(i32x2_t, v), rsrc, row, byte_off, 0, 0);
+}
+
 __device__ __forceinline__ void raise_flag(int32_t* flag, int32_t bit) {
   if (flag) atomicOr(flag, bit);
 }

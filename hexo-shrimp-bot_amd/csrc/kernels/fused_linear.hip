@@ -67,30 +67,30 @@ struct Args {
 template <typename T>
 __device__ __forceinline__ void load_chunk(const T* p, float (&v)[8]) { load8(p, v); }
 
-// Four consecutive output features of one row: fp16/fp32 store or fp32 add.
+// Four consecutive output features f .. f+3 of output row `brow` (-1: a
+// lane without a row, whose accesses are dropped): fp16/fp32 store, or an
+// fp32/fp16 residual add, through the output's buffer descriptor.
 template <int kMode>
-__device__ __forceinline__ void store4(const Args& a, int64_t row, int f, const f32x4_t& v) {
+__device__ __forceinline__ void store4(i32x4_t orsrc, int32_t brow, int f, const f32x4_t& v) {
   if constexpr (kMode == kStoreF16) {
     uint2 w;
     w.x = pack_f16x2(v[0], v[1]);
     w.y = pack_f16x2(v[2], v[3]);
-    *reinterpret_cast<uint2*>(static_cast<_Float16*>(a.out) + row * a.ldo + f) = w;
+    row_store8(orsrc, brow, 2 * f, w);
   } else if constexpr (kMode == kStoreF32) {
-    *reinterpret_cast<float4*>(static_cast<float*>(a.out) + row * a.ldo + f) = make_float4(v[0], v[1], v[2], v[3]);
+    row_store16(orsrc, brow, 4 * f, __builtin_bit_cast(uint4, make_float4(v[0], v[1], v[2], v[3])));
   } else if constexpr (kMode == kAddF32) {
-    float4* o = reinterpret_cast<float4*>(static_cast<float*>(a.out) + row * a.ldo + f);
-    float4 r = *o;
+    float4 r = __builtin_bit_cast(float4, row_load16(orsrc, brow, 4 * f));
     r.x += v[0], r.y += v[1], r.z += v[2], r.w += v[3];
-    *o = r;
+    row_store16(orsrc, brow, 4 * f, __builtin_bit_cast(uint4, r));
   } else {
     // fp16 residual rows: widened, added in fp32, rounded once
-    uint2* o = reinterpret_cast<uint2*>(static_cast<_Float16*>(a.out) + row * a.ldo + f);
-    const uint2 r = *o;
+    const uint2 r = row_load8(orsrc, brow, 2 * f);
     const f16x2_t r0 = __builtin_bit_cast(f16x2_t, r.x), r1 = __builtin_bit_cast(f16x2_t, r.y);
     uint2 w;
     w.x = pack_f16x2(float(r0[0]) + v[0], float(r0[1]) + v[1]);
     w.y = pack_f16x2(float(r1[0]) + v[2], float(r1[1]) + v[3]);
-    *o = w;
+    row_store8(orsrc, brow, 2 * f, w);
   }
 }
 
@@ -190,19 +190,31 @@ __global__ void __launch_bounds__((threads_for<N1, kX2, kStage2>())) fused_linea
   // rows, ahead of the next tile's; the other shapes read them in the loop
   constexpr bool kEarlyAdd = kX2 && kStage2 && N1 == 128;
   const int64_t G = gridDim.x;
+  // the output rows (pitch and row count checked on the host)
+  constexpr int kOutBytes = (kMode == kStoreF16 || kMode == kAddF16) ? 2 : 4;
+  const i32x4_t orsrc = rows_rsrc(a.out, uint32_t(a.ldo * kOutBytes), uint32_t(a.m));
+  // a valid address for the index loads a launch does not need (the
+  // weights): the loads stay unconditional and their values unused
+  const int64_t* no_idx = reinterpret_cast<const int64_t*>(a.w1);
   auto row_of = [&](int64_t t) { return t * kTileRows + wave * 16 + l16; };
   auto row_ok = [&](int64_t t) { return t < n_tiles && row_of(t) < a.m; };
-  auto idx_at = [&](int64_t t) -> int64_t { return a.x_rows[row_ok(t) ? row_of(t) : 0]; };
+  auto idx_at = [&](int64_t t) -> int64_t {
+    return a.x_rows ? a.x_rows[row_ok(t) ? row_of(t) : 0] : no_idx[0];
+  };
+  auto grp_at = [&](int64_t t) -> int64_t {
+    return a.add2_rows ? a.add2_rows[row_ok(t) ? row_of(t) : 0] : no_idx[0];
+  };
+  // Bad indices are noted in a register and flagged once after the loop: an
+  // atomic under a branch inside the loop would leave the compiler unable to
+  // count the loads in flight after it.
+  bool bad = false;
   // the source row of a tile's lane: -1 past the end and for a negative
   // gather index (a zero row), and for one past the rows (flagged)
   auto src_of = [&](int64_t t, int64_t idx) -> int64_t {
     if (!row_ok(t)) return -1;
     if (!a.x_rows) return row_of(t);
-    if (idx >= a.n_x) {
-      raise_flag(a.flag, MANTIS_FLAG_INDEX);
-      return -1;
-    }
-    return idx < 0 ? -1 : idx;
+    bad |= idx >= a.n_x;
+    return idx < 0 || idx >= a.n_x ? -1 : idx;
   };
   auto load_x = [&](int64_t src, uint4 (&d)[kRX]) {
     const TX* p = xp + (src >= 0 ? src : 0) * a.ldx + 8 * g;
@@ -233,11 +245,12 @@ __global__ void __launch_bounds__((threads_for<N1, kX2, kStage2>())) fused_linea
   uint4 xr[kRX], x2r[kX2 ? kRX2 : 1];
   load_x(src_n, xr);
   if constexpr (kX2) load_x2(blockIdx.x, x2r);
-  int64_t grp_n = a.add2 ? a.add2_rows[row_ok(blockIdx.x) ? row_of(blockIdx.x) : 0] : 0;
-  int64_t idx_n = a.x_rows ? idx_at(blockIdx.x + G) : 0;  // the gather index one tile ahead
+  int64_t grp_n = grp_at(blockIdx.x);
+  int64_t idx_n = idx_at(blockIdx.x + G);  // the gather index one tile ahead
   for (int64_t tile = blockIdx.x; tile < n_tiles; tile += G) {
     const int64_t row = row_of(tile);
     const bool live = row < a.m;
+    const int32_t brow = live ? int32_t(row) : -1;  // the output row of the buffer accesses
     const int64_t src = src_n;
     float xv[4][8];
 #pragma unroll
@@ -255,8 +268,9 @@ __global__ void __launch_bounds__((threads_for<N1, kX2, kStage2>())) fused_linea
     // ---- row-group of the per-group add (validated once per row)
     int64_t grp = -1;
     if (a.add2) {
-      if (live && (grp_n < 0 || grp_n >= a.n_add2)) raise_flag(a.flag, MANTIS_FLAG_INDEX);
-      else if (live) grp = grp_n;
+      const bool ok = grp_n >= 0 && grp_n < a.n_add2;
+      bad |= live && !ok;
+      grp = live && ok ? grp_n : -1;
     }
     // ---- this tile's row adds (pair MLPs), before the next tile's rows
     float4 ea1[kEarlyAdd ? N1 / 16 : 1], ea2[kEarlyAdd ? N1 / 16 : 1];
@@ -287,8 +301,8 @@ __global__ void __launch_bounds__((threads_for<N1, kX2, kStage2>())) fused_linea
     src_n = src_of(tile + G, idx_n);
     load_x(src_n, xr);
     if constexpr (kX2) load_x2(tile + G, x2r);
-    if (a.add2) grp_n = a.add2_rows[row_ok(tile + G) ? row_of(tile + G) : 0];
-    if (a.x_rows) idx_n = idx_at(tile + 2 * G);
+    grp_n = grp_at(tile + G);
+    idx_n = idx_at(tile + 2 * G);
     if constexpr (kLN) {
       float s = 0.f;
 #pragma unroll
@@ -398,20 +412,18 @@ __global__ void __launch_bounds__((threads_for<N1, kX2, kStage2>())) fused_linea
       for (int k = 0; k < NT1 / 2; ++k) {
         const f32x4_t lo = feature_tile(2 * k);
         const f32x4_t hi = feature_tile(2 * k + 1);
-        if (live) {
-          uint4 w;
-          w.x = pack_f16x2(lo[0], lo[1]);
-          w.y = pack_f16x2(lo[2], lo[3]);
-          w.z = pack_f16x2(hi[0], hi[1]);
-          w.w = pack_f16x2(hi[2], hi[3]);
-          *reinterpret_cast<uint4*>(static_cast<_Float16*>(a.out) + row * a.ldo + 32 * k + 8 * g) = w;
-        }
+        uint4 w;
+        w.x = pack_f16x2(lo[0], lo[1]);
+        w.y = pack_f16x2(lo[2], lo[3]);
+        w.z = pack_f16x2(hi[0], hi[1]);
+        w.w = pack_f16x2(hi[2], hi[3]);
+        row_store16(orsrc, brow, 2 * (32 * k + 8 * g), w);
       }
     } else {
 #pragma unroll 2
       for (int nt = 0; nt < NT1; ++nt) {
         const f32x4_t acc = feature_tile(nt);
-        if (live) store4<kMode>(a, row, 16 * nt + 4 * g, acc);
+        store4<kMode>(orsrc, brow, 16 * nt + 4 * g, acc);
       }
     }
     if constexpr (kResidReg) {
@@ -433,19 +445,16 @@ __global__ void __launch_bounds__((threads_for<N1, kX2, kStage2>())) fused_linea
           }
           y2[half] = y;
         }
-        if (live) {
-          const int f = 32 * k + 8 * g;
-          const float4 b0 = *reinterpret_cast<const float4*>(sb3 + f), b1 = *reinterpret_cast<const float4*>(sb3 + f + 4);
-          uint4* o = reinterpret_cast<uint4*>(static_cast<_Float16*>(a.out) + row * a.ldo + f);
-          // fp16 residual rows: widened, added in fp32, rounded once
-          const f16x8_t r = __builtin_bit_cast(f16x8_t, a.inplace ? xc[k] : *o);
-          uint4 w;
-          w.x = pack_f16x2(float(r[0]) + (y2[0][0] + b0.x), float(r[1]) + (y2[0][1] + b0.y));
-          w.y = pack_f16x2(float(r[2]) + (y2[0][2] + b0.z), float(r[3]) + (y2[0][3] + b0.w));
-          w.z = pack_f16x2(float(r[4]) + (y2[1][0] + b1.x), float(r[5]) + (y2[1][1] + b1.y));
-          w.w = pack_f16x2(float(r[6]) + (y2[1][2] + b1.z), float(r[7]) + (y2[1][3] + b1.w));
-          *o = w;
-        }
+        const int f = 32 * k + 8 * g;
+        const float4 b0 = *reinterpret_cast<const float4*>(sb3 + f), b1 = *reinterpret_cast<const float4*>(sb3 + f + 4);
+        // fp16 residual rows: widened, added in fp32, rounded once
+        const f16x8_t r = __builtin_bit_cast(f16x8_t, a.inplace ? xc[k] : row_load16(orsrc, brow, 2 * f));
+        uint4 w;
+        w.x = pack_f16x2(float(r[0]) + (y2[0][0] + b0.x), float(r[1]) + (y2[0][1] + b0.y));
+        w.y = pack_f16x2(float(r[2]) + (y2[0][2] + b0.z), float(r[3]) + (y2[0][3] + b0.w));
+        w.z = pack_f16x2(float(r[4]) + (y2[1][0] + b1.x), float(r[5]) + (y2[1][1] + b1.y));
+        w.w = pack_f16x2(float(r[6]) + (y2[1][2] + b1.z), float(r[7]) + (y2[1][3] + b1.w));
+        row_store16(orsrc, brow, 2 * f, w);
       }
     } else if constexpr (kStage2) {
       // ---- stage 2: y^T (n3 x 16) = W3 . h^T
@@ -462,15 +471,14 @@ __global__ void __launch_bounds__((threads_for<N1, kX2, kStage2>())) fused_linea
             const f16x8_t wf = __builtin_bit_cast(f16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
             y = mfma16x16x32(wf, hb[ks], y);
           }
-        if (live) {
-          const int f = 16 * ot + 4 * g;
-          const float4 bb = *reinterpret_cast<const float4*>(sb3 + f);
-          y[0] += bb.x, y[1] += bb.y, y[2] += bb.z, y[3] += bb.w;
-          store4<kMode>(a, row, f, y);
-        }
+        const int f = 16 * ot + 4 * g;
+        const float4 bb = *reinterpret_cast<const float4*>(sb3 + f);
+        y[0] += bb.x, y[1] += bb.y, y[2] += bb.z, y[3] += bb.w;
+        store4<kMode>(orsrc, brow, f, y);
       }
     }
   }
+  if (bad) raise_flag(a.flag, MANTIS_FLAG_INDEX);
 }
 
 int g_cus = 0;
@@ -545,6 +553,10 @@ extern "C" int32_t mantis_fused_linear(const void* x, int32_t x_dtype, int64_t l
       (add1 && !aligned16(add1)) || (add2 && !aligned16(add2)))
     return MANTIS_E_ARG;
   if (w3 && (n3 % 16 || n3 > 128)) return MANTIS_E_ARG;
+  // output rows go through a buffer descriptor: a row pitch below 16 KiB,
+  // int32 row indices
+  if (ldo * (out_mode == 1 || out_mode == 2 ? 4 : 2) >= 16384 || m > 2147483647LL) return MANTIS_E_ARG;
+  if (x_rows && n_x == 0) return MANTIS_E_ARG;  // every gathered row would be out of range
   Args a{x, ldx, x_rows, x_rows ? n_x : m, m, x2, ldx2, static_cast<const _Float16*>(w1),
          static_cast<const _Float16*>(w2), b1, add1, ld_add1, add2, add2_rows, n_add2,
          static_cast<const _Float16*>(w3), b3, n3, out, ldo, err_flag,
@@ -634,6 +646,8 @@ extern "C" int32_t mantis_fused_linear_split(const void* x, int32_t x_dtype, int
       (add1 && !aligned16(add1)) || (add2 && !aligned16(add2)))
     return MANTIS_E_ARG;
   if (w3 && (n3 % 16 || n3 > 128)) return MANTIS_E_ARG;
+  if (ldo * (out_mode == 1 || out_mode == 2 ? 4 : 2) >= 16384 || m > 2147483647LL) return MANTIS_E_ARG;
+  if (x_rows && n_x == 0) return MANTIS_E_ARG;
   Args a{x, ldx, x_rows, x_rows ? n_x : m, m, x2, ldx2, static_cast<const _Float16*>(w1),
          static_cast<const _Float16*>(w2), b1, add1, ld_add1, add2, add2_rows, n_add2,
          static_cast<const _Float16*>(w3), b3, n3, out, ldo, err_flag};
