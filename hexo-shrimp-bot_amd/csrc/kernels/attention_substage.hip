@@ -241,6 +241,10 @@ __global__ void __launch_bounds__(waves_for<kStages>() * 64) attn_substage_kerne
   // drift apart and the rows were fetched into L2 about twice: 898 -> 787 us)
   uint32_t* const next_ctr = a.counters + 32 * xcd;
   uint32_t* const done_ctr = a.counters + 32 * (kXcds + xcd);
+  // Bad indices are noted in a register and flagged once at the end: an
+  // atomic under a branch inside the loops would leave the compiler unable
+  // to count the loads in flight after it.
+  bool bad = false;
   auto claim = [&]() -> int64_t {
     uint32_t v = 0;
     if (lane == 0) v = atomicAdd(next_ctr, 1u);
@@ -280,7 +284,7 @@ __global__ void __launch_bounds__(waves_for<kStages>() * 64) attn_substage_kerne
     }
     const bool in_tile = tile * 16 + l16 < a.n_rows;
     const bool live = in_tile && row >= 0 && row < a.n_rows;
-    if (in_tile && !live) raise_flag(a.flag, MANTIS_FLAG_INDEX);
+    bad |= in_tile && !live;
     const int64_t rc = live ? row : 0;  // dead lanes read a real row and store nothing
     // the row state: fp32 rows stay fp32 in registers across the stages;
     // fp16 rows stay packed (half the registers) and are rounded after each
@@ -422,7 +426,7 @@ __global__ void __launch_bounds__(waves_for<kStages>() * 64) attn_substage_kerne
         auto step = [&](int u, int32_t src, int32_t cls) {
           const bool in = j + u < ac;
           const bool ok = in && src >= 0 && cls >= 0;
-          if (in && !ok) raise_flag(a.flag, MANTIS_FLAG_INDEX);
+          bad |= in && !ok;
           float bs = 0.f;
           if (ok) {
             const uint32_t sr = uint32_t(src), cc = uint32_t(cls);
@@ -510,6 +514,7 @@ __global__ void __launch_bounds__(waves_for<kStages>() * 64) attn_substage_kerne
       }
     }
   }
+  if (bad) raise_flag(a.flag, MANTIS_FLAG_INDEX);
   // Every wavefront has made its last claim (one past the XCD's tiles): the
   // XCD's last wavefront to get here leaves both counters at zero for the
   // next launch

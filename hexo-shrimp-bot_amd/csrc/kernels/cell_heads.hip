@@ -157,6 +157,10 @@ __global__ void __launch_bounds__(kThreads) cell_heads_kernel(HeadArgs a) {
   // within a narrow window of tiles, whose gathered rows stay in its L2
   uint32_t* const next_ctr = a.counters + 32 * xcd;
   uint32_t* const done_ctr = a.counters + 32 * (kXcds + xcd);
+  // Bad indices are noted in a register and flagged once at the end: an
+  // atomic under a branch inside the loops would leave the compiler unable
+  // to count the loads in flight after it.
+  bool bad = false;
   auto claim = [&]() -> int64_t {
     uint32_t v = 0;
     if (lane == 0) v = atomicAdd(next_ctr, 1u);
@@ -178,7 +182,7 @@ __global__ void __launch_bounds__(kThreads) cell_heads_kernel(HeadArgs a) {
     next_row = order_at(next < t_end ? next : tile);
     const bool in_tile = tile * 16 + l16 < a.n_cells;
     const bool live = in_tile && row >= 0 && row < a.n_cells;
-    if (in_tile && !live) raise_flag(a.flag, MANTIS_FLAG_INDEX);
+    bad |= in_tile && !live;
     const int64_t rc = live ? row : 0;  // dead lanes read a real row and store nothing
     // ---- the cell's decoder run and position, then its row
     int64_t st = a.dec_ptr[rc], en = a.dec_ptr[rc + 1];
@@ -212,7 +216,7 @@ __global__ void __launch_bounds__(kThreads) cell_heads_kernel(HeadArgs a) {
     if (mc > 0) fetch(0);
     int64_t pos = -1;
     if (live) {
-      if (pos_raw < 0 || pos_raw >= a.n_pos) raise_flag(a.flag, MANTIS_FLAG_INDEX);
+      if (pos_raw < 0 || pos_raw >= a.n_pos) bad = true;
       else pos = pos_raw;
     }
     // the tile's first cell's position (its g_half row is staged in LDS
@@ -270,7 +274,7 @@ __global__ void __launch_bounds__(kThreads) cell_heads_kernel(HeadArgs a) {
       auto step = [&](int u, int32_t w, int32_t ac, int32_t dc) {
         const bool in = j + u < acnt;
         const bool ok = in && w >= 0;
-        if (in && !ok) raise_flag(a.flag, MANTIS_FLAG_INDEX);
+        bad |= in && !ok;
         if (ok) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
@@ -425,6 +429,7 @@ __global__ void __launch_bounds__(kThreads) cell_heads_kernel(HeadArgs a) {
           make_float4(y[0] + bb.x, y[1] + bb.y, y[2] + bb.z, y[3] + bb.w);
     }
   }
+  if (bad) raise_flag(a.flag, MANTIS_FLAG_INDEX);
   // every wavefront has made its last claim: the XCD's last one to get here
   // leaves both counters at zero for the next launch
   if (lane == 0 && atomicAdd(done_ctr, 1u) == uint32_t(waves_here) - 1) {
