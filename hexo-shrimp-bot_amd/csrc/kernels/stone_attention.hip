@@ -25,13 +25,18 @@
 // in the wavefront does the wavefront take the cross-lane maximum and rescale
 // its accumulators; otherwise probabilities up to 2^kLazyLog2 are
 // accumulated as they are (far inside the range of fp16 and bf16, and of the
-// fp32 sums).  The first chunk always sets m.  The final division by the row
-// sum makes the output independent of the reference point up to rounding.
-// Only the last chunk can hold keys at or past seq_len: it alone is masked
-// (a separately compiled copy of the chunk body).  Every global load reads a
-// clamped, in-range row and zeroes the value afterwards: a load under a
-// condition compiles to a flat load, whose completion every LDS wait would
-// then also wait for.  Query rows past seq_len are written as exact zeros.
+// fp32 sums).  The first chunk sets m (a copy of the chunk body without the
+// rescale).  The final division by the row sum makes the output independent
+// of the reference point up to rounding.  Only the last chunk can hold keys
+// at or past seq_len: in its copy the score products start from -inf in the
+// MFMA's C operand for those keys.  A sub-tile whose 16 queries all lie past
+// seq_len does no key work (wavefront-uniform, a copy of the loop per count
+// of live sub-tiles), but its wavefront still stages and meets the barriers.
+// q, k and v rows are read through buffer descriptors over the position's
+// live rows: a row at or past seq_len is out of range and reads zeros with
+// no memory access, so no load needs a clamp, a branch or a zeroing (a load
+// under a branch would also make the compiler's later waits count it).
+// Query rows past seq_len are written as exact zeros.
 //
 // Schedule: items differ in cost by their position's key count (1 to
 // ceil(T/64) chunks), and workgroups are dispatched round-robin over the 8
@@ -165,29 +170,28 @@ stone_attention_kernel(const uint16_t* __restrict__ q, int64_t qsp, int64_t qsa,
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
   const int l16 = lane % 16, g = lane / 16;
   using FR = Frag<kHalf>;
-  const int64_t last = L - 1;  // L >= 1 here: clamp target of out-of-range rows
+  // q, k and v rows of this (position, head) through buffer descriptors over
+  // its live rows: a row at or past L is out of range and reads zeros without
+  // a memory access, so no load needs a clamp, a condition or a zeroing
+  const i32x4_t qrs = rows_rsrc(qp, uint32_t(qst * 2), uint32_t(L));
+  const i32x4_t krs = rows_rsrc(kp, uint32_t(kst * 2), uint32_t(L));
+  const i32x4_t vrs = rows_rsrc(vp, uint32_t(vst * 2), uint32_t(L));
   typename FR::vec qf[2];
   int64_t qrow[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     qrow[j] = q0 + wave * kQPerWave + 16 * j + l16;
     // B fragment of Q^T: query l16, dims 8g..8g+7
-    const bool live = qrow[j] < L;
-    const uint4 raw = *reinterpret_cast<const uint4*>(qp + (live ? qrow[j] : last) * qst + 8 * g);
-    qf[j] = FR::cast(live ? raw : zero4);
+    qf[j] = FR::cast(row_load16(qrs, int32_t(qrow[j]), 16 * g));
   }
 
   // staging role of this thread: one 16-byte piece of one key's K and V rows
   const int st_key = threadIdx.x / 4, st_d = (threadIdx.x % 4) * 8;
   uint4 kreg, vreg;
   auto fetch = [&](int64_t kb) {
-    const int64_t kk = kb + st_key;
-    const bool live = kk < L;
-    const int64_t row = live ? kk : last;
-    const uint4 kr = *reinterpret_cast<const uint4*>(kp + row * kst + st_d);
-    const uint4 vr = *reinterpret_cast<const uint4*>(vp + row * vst + st_d);
-    kreg = live ? kr : zero4;
-    vreg = live ? vr : zero4;
+    const int32_t row = int32_t(kb) + st_key;
+    kreg = row_load16(krs, row, 2 * st_d);
+    vreg = row_load16(vrs, row, 2 * st_d);
   };
   auto stage = [&](int buf) {
     *reinterpret_cast<uint4*>(&sk[buf][st_key * kKPitch + st_d]) = kreg;
@@ -204,6 +208,8 @@ stone_attention_kernel(const uint16_t* __restrict__ q, int64_t qsp, int64_t qsa,
   // accumulators (two 16-dim tiles) and the row sums, accumulated by an extra
   // product with an all-ones A operand (every D row holds the sum)
   float m[2] = {-INFINITY, -INFINITY};
+  float thr[2];  // m + kLazyLog2 / c_log2: a score above it moves the reference point
+  const float lazy_raw = kLazyLog2 / c_log2;
   f32x4_t o[2][2], lsum[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
@@ -214,96 +220,125 @@ stone_attention_kernel(const uint16_t* __restrict__ q, int64_t qsp, int64_t qsa,
   const uint32_t one2 = FR::pack_unit(1.f, 1.f);
   const typename FR::vec ones = FR::cast(make_uint4(one2, one2, one2, one2));
 
-  auto chunk = [&](auto masked, int buf, int64_t kb, bool more) {
+  // One 64-key chunk for the first kNJ sub-tiles of this wavefront (a
+  // sub-tile whose 16 queries are all past L does no key work: its
+  // accumulators stay zero and its rows are written as zeros).  Every
+  // wavefront stages its share of the next chunk and meets the barrier.
+  auto chunk = [&](auto nj, auto first, auto masked, int buf, int64_t kb, bool more) {
+    constexpr int kNJ = decltype(nj)::value;
     if (more) fetch(kb + kKChunk);
-    // S^T tiles: keys kb + 16*tt + (4g + t) for query l16 of sub-tile j
-    f32x4_t s[2][4];
+    if constexpr (kNJ > 0) {
+      // S^T tiles: keys kb + 16*tt + (4g + t) for query l16 of sub-tile j; in
+      // the chunk that holds padding keys the products start from -inf there
+      f32x4_t cb[4];
 #pragma unroll
-    for (int tt = 0; tt < 4; ++tt) {
-      const typename FR::vec kf = FR::cast(*reinterpret_cast<const uint4*>(&sk[buf][(16 * tt + l16) * kKPitch + 8 * g]));
+      for (int tt = 0; tt < 4; ++tt) cb[tt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      if constexpr (decltype(masked)::value) {
+        const int lim = int(L - kb) - 4 * g;
 #pragma unroll
-      for (int j = 0; j < 2; ++j) s[j][tt] = mfma16x16x32(kf, qf[j], f32x4_t{0.f, 0.f, 0.f, 0.f});
-    }
-    if constexpr (decltype(masked)::value) {  // keys at or past lim are padding
-      const int lim = int(L - kb);
+        for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-          if (16 * tt + 4 * g + t >= lim) {
-            s[0][tt][t] = -INFINITY;
-            s[1][tt][t] = -INFINITY;
-          }
-    }
-    typename FR::vec pf[2][2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      float lmax = s[j][0][0];
-#pragma unroll
-      for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-        for (int t = 0; t < 4; ++t) lmax = fmaxf(lmax, s[j][tt][t]);
-      // (-inf - -inf is NaN and compares false: a lane that has seen only
-      // padding never asks for a new reference point by itself)
-      if (__builtin_amdgcn_ballot_w64((lmax - m[j]) * c_log2 > kLazyLog2)) {  // wavefront-uniform
-        float cmax = fmaxf(m[j], lmax);
-        cmax = fmaxf(cmax, __shfl_xor(cmax, 16));
-        cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
-        // exp2 arguments are <= 0 (or -inf): the raw v_exp_f32 is exact enough
-        // and flushes results below 2^-126 to zero
-        const float alpha = cmax == -INFINITY ? 1.f : __builtin_amdgcn_exp2f((m[j] - cmax) * c_log2);
-        m[j] = cmax;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          lsum[j][t] *= alpha;
-          o[j][0][t] *= alpha;
-          o[j][1][t] *= alpha;
-        }
+          for (int t = 0; t < 4; ++t) cb[tt][t] = 16 * tt + t >= lim ? -INFINITY : 0.f;
       }
-      const float mc = m[j] * c_log2;
-      uint32_t pw[4][2];
+      f32x4_t s[kNJ][4];
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt) {
-        float pr[4];
+        const typename FR::vec kf =
+            FR::cast(*reinterpret_cast<const uint4*>(&sk[buf][(16 * tt + l16) * kKPitch + 8 * g]));
 #pragma unroll
-        for (int t = 0; t < 4; ++t) pr[t] = __builtin_amdgcn_exp2f(fmaf(s[j][tt][t], c_log2, -mc));
-        pw[tt][0] = FR::pack_unit(pr[0], pr[1]);
-        pw[tt][1] = FR::pack_unit(pr[2], pr[3]);
+        for (int j = 0; j < kNJ; ++j) s[j][tt] = mfma16x16x32(kf, qf[j], cb[tt]);
       }
+      typename FR::vec pf[kNJ][2];
 #pragma unroll
-      for (int sc = 0; sc < 2; ++sc)
-        pf[j][sc] = FR::cast(make_uint4(pw[2 * sc][0], pw[2 * sc][1], pw[2 * sc + 1][0], pw[2 * sc + 1][1]));
-    }
-    // O^T += V^T . P^T over two 32-key steps; each V^T fragment serves both sub-tiles
+      for (int j = 0; j < kNJ; ++j) {
+        float lmax = s[j][0][0];
 #pragma unroll
-    for (int sc = 0; sc < 2; ++sc) {
+        for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
-      for (int dt = 0; dt < 2; ++dt) {
-        const uint16_t* row = &svt[buf][(16 * dt + l16) * kVtPitch + 32 * sc];
-        const uint2 lo = *reinterpret_cast<const uint2*>(row + 4 * g);
-        const uint2 hi = *reinterpret_cast<const uint2*>(row + 16 + 4 * g);
-        const typename FR::vec vf = FR::cast(make_uint4(lo.x, lo.y, hi.x, hi.y));
+          for (int t = 0; t < 4; ++t) lmax = fmaxf(lmax, s[j][tt][t]);
+        if constexpr (decltype(first)::value) {
+          // the first chunk sets the reference point (key 0 is live, so every
+          // row has a finite score); the accumulators are still zero
+          float cmax = fmaxf(lmax, __shfl_xor(lmax, 16));
+          cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
+          m[j] = cmax;
+          thr[j] = cmax + lazy_raw;
+        } else if (__builtin_amdgcn_ballot_w64(lmax > thr[j])) {  // wavefront-uniform
+          // (a lane that has seen only padding has lmax = -inf and never asks
+          // for a new reference point by itself)
+          float cmax = fmaxf(m[j], lmax);
+          cmax = fmaxf(cmax, __shfl_xor(cmax, 16));
+          cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
+          // exp2 arguments are <= 0 (or -inf): the raw v_exp_f32 is exact enough
+          // and flushes results below 2^-126 to zero
+          const float alpha = cmax == -INFINITY ? 1.f : __builtin_amdgcn_exp2f((m[j] - cmax) * c_log2);
+          m[j] = cmax;
+          thr[j] = cmax + lazy_raw;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) o[j][dt] = mfma16x16x32(vf, pf[j][sc], o[j][dt]);
+          for (int t = 0; t < 4; ++t) {
+            lsum[j][t] *= alpha;
+            o[j][0][t] *= alpha;
+            o[j][1][t] *= alpha;
+          }
+        }
+        const float mc = m[j] * c_log2;
+        uint32_t pw[4][2];
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+          float pr[4];
+#pragma unroll
+          for (int t = 0; t < 4; ++t) pr[t] = __builtin_amdgcn_exp2f(fmaf(s[j][tt][t], c_log2, -mc));
+          pw[tt][0] = FR::pack_unit(pr[0], pr[1]);
+          pw[tt][1] = FR::pack_unit(pr[2], pr[3]);
+        }
+#pragma unroll
+        for (int sc = 0; sc < 2; ++sc)
+          pf[j][sc] = FR::cast(make_uint4(pw[2 * sc][0], pw[2 * sc][1], pw[2 * sc + 1][0], pw[2 * sc + 1][1]));
       }
+      // O^T += V^T . P^T over two 32-key steps; each V^T fragment serves every sub-tile
 #pragma unroll
-      for (int j = 0; j < 2; ++j) lsum[j] = mfma16x16x32(ones, pf[j][sc], lsum[j]);
+      for (int sc = 0; sc < 2; ++sc) {
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt) {
+          const uint16_t* row = &svt[buf][(16 * dt + l16) * kVtPitch + 32 * sc];
+          const uint2 lo = *reinterpret_cast<const uint2*>(row + 4 * g);
+          const uint2 hi = *reinterpret_cast<const uint2*>(row + 16 + 4 * g);
+          const typename FR::vec vf = FR::cast(make_uint4(lo.x, lo.y, hi.x, hi.y));
+#pragma unroll
+          for (int j = 0; j < kNJ; ++j) o[j][dt] = mfma16x16x32(vf, pf[j][sc], o[j][dt]);
+        }
+#pragma unroll
+        for (int j = 0; j < kNJ; ++j) lsum[j] = mfma16x16x32(ones, pf[j][sc], lsum[j]);
+      }
     }
     if (more) stage(buf ^ 1);
     __syncthreads();
   };
 
   const int64_t n_chunks = (L + kKChunk - 1) / kKChunk;
+  auto run = [&](auto nj) {
+    constexpr std::true_type yes{};
+    constexpr std::false_type no{};
+    const int64_t last = n_chunks - 1;  // only the last chunk can hold padding keys
+    const bool pad = L - last * kKChunk < kKChunk;
+    if (last == 0) {
+      if (pad) chunk(nj, yes, yes, 0, 0, false);
+      else chunk(nj, yes, no, 0, 0, false);
+      return;
+    }
+    chunk(nj, yes, no, 0, 0, true);
+    for (int64_t ch = 1; ch < last; ++ch) chunk(nj, no, no, int(ch & 1), ch * kKChunk, true);
+    if (pad) chunk(nj, no, yes, int(last & 1), last * kKChunk, false);
+    else chunk(nj, no, no, int(last & 1), last * kKChunk, false);
+  };
   fetch(0);
   stage(0);
   __syncthreads();
-  for (int64_t ch = 0; ch + 1 < n_chunks; ++ch)
-    chunk(std::false_type{}, int(ch & 1), ch * kKChunk, true);
-  {
-    const int64_t ch = n_chunks - 1;  // only the last chunk can hold padding keys
-    if (L - ch * kKChunk < kKChunk) chunk(std::true_type{}, int(ch & 1), ch * kKChunk, false);
-    else chunk(std::false_type{}, int(ch & 1), ch * kKChunk, false);
-  }
+  // live sub-tiles of this wavefront (wavefront-uniform)
+  const int64_t live_q = L - (q0 + wave * kQPerWave);
+  if (live_q > 16) run(std::integral_constant<int, 2>{});
+  else if (live_q > 0) run(std::integral_constant<int, 1>{});
+  else run(std::integral_constant<int, 0>{});
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const float lt = lsum[j][0];
@@ -457,6 +492,11 @@ extern "C" int32_t mantis_stone_attention(const void* q, const int64_t* qs, cons
     if (st[3] != 1) return MANTIS_E_ARG;
     if ((st[0] | st[1] | st[2]) % 8) return MANTIS_E_ARG;
   }
+  // q, k and v rows are read through buffer descriptors: a row pitch of 32 to
+  // 8,191 elements (the descriptor's stride field) and row indices in int32
+  for (const int64_t* st : {qs, ks, vs})
+    if (st[2] < hd || st[2] >= 8192) return MANTIS_E_ARG;
+  if (t > 2147483647LL) return MANTIS_E_ARG;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out)) return MANTIS_E_ARG;
   const int64_t n_qt = (t + kQTile - 1) / kQTile;
   const int64_t n_items = n_pos * heads * n_qt;

@@ -1280,7 +1280,10 @@ def stone_attention(q: Tensor, k: Tensor, v: Tensor, seq_lens: Tensor, want_lse:
         raise ValueError("stone attention runs 16-bit MFMA: q, k and v must share float16 or bfloat16")
     if hd != 32:
         raise ValueError("stone attention supports head_dim 32")
-    fix = lambda x: x if x.stride(3) == 1 and all(s % 8 == 0 for s in x.stride()[:3]) else x.contiguous()  # noqa: E731
+    # unit dim stride, 16-byte aligned rows, and a row pitch the kernel's
+    # buffer descriptors take (32 to 8,191 elements)
+    fix = lambda x: (x if x.stride(3) == 1 and all(s % 8 == 0 for s in x.stride()[:3])  # noqa: E731
+                     and 32 <= x.stride(2) < 8192 else x.contiguous())
     q, k, v = fix(q), fix(k), fix(v)
     seq_lens = seq_lens.contiguous()
     if out is None:

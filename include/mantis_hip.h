@@ -539,7 +539,9 @@ int32_t mantis_row_encode(const void* pre, int32_t pre_dtype, int64_t n_w, int64
  * for t < seq_lens[p]; rows t >= seq_lens[p] are written as exact zeros
  * (lse 0).  q/k/v/out share `dtype`, with element strides (sp, sa, st, sd == 1)
  * given per tensor, so the (P, T, A, hd) -> (P, A, T, hd) transposed views
- * the model passes need no copy.  lse (P, heads, T) fp32 or NULL.
+ * the model passes need no copy; every stride is a multiple of 8, and the row
+ * strides of q, k and v lie in [hd, 8191] (MANTIS_E_ARG otherwise).  lse
+ * (P, heads, T) fp32 or NULL.
  * hd must be 32.  `schedule` is NULL (work items in their natural order) or
  * the order built by mantis_stone_attention_schedule for the same seq_lens,
  * n_pos, heads and t; the output does not depend on which.  Replaces
