@@ -45,7 +45,7 @@ heads of 32, 4 value queries.  Other knob combinations raise
 
 from __future__ import annotations
 
-from dataclasses import dataclass
+from functools import cached_property
 
 import torch
 import torch.nn.functional as F
@@ -159,6 +159,11 @@ def _prepare(model, P) -> dict[str, Tensor]:
         t[key + ".w"], t[key + ".b"] = pair
 
     counts = model.pattern_counts.float()
+    # the initial-state tables in the stream dtypes: the window table (fp16
+    # in the cell-node configuration) and [nearest-stone rows; cell_base]
+    t["window_table"] = P["window_table.weight"].to(HALF if cfg.cell_nodes else F32).contiguous()
+    if cfg.cell_nodes:
+        t["cell_table"] = torch.cat([P["cell_nearest_table.weight"], P["cell_base"][None, :]]).to(HALF).contiguous()
     for i in range(cfg.blocks):
         pb = f"blocks.{i}."
         put(pb + "u", _fold(P, pb + "ln_ws_s", [pb + "u"]))
@@ -246,42 +251,232 @@ def _prepared(model) -> Prepared:
 # ----------------------------------------------------------------- per-batch plan
 
 
-@dataclass
 class Plan:
-    """Device index views shared by every block of one forward."""
+    """Device index views shared by every block of one forward, each derived
+    on first use.  Every view is a device computation on the batch alone, so
+    deriving it lazily changes only when its small kernels are queued: they
+    interleave with the forward's large launches instead of all running
+    before the first of them, and the host's launch work for the next views
+    overlaps the device's work on the current one.
 
-    n_pos: int
-    max_t: int
-    max_w: int
-    n_s: int
-    n_w: int
-    n_c: int
-    inc_win_ptr: Tensor  # window-major incidence CSR (aggregate_to_windows)
-    run_window: Tensor
-    run_class: Tensor
-    inc_stone_ptr: Tensor  # stone-major incidence CSR (aggregate_to_stones)
-    window_pos: Tensor
-    layout_offsets: Tensor
-    layout_order: Tensor
-    cov_rows: Tensor | None  # the covered cells (with decoder entries), ascending (cell-node configurations)
-    edge_wcell_cov: Tensor | None  # edge_wcell as indices into cov_rows
-    cell_ptr: Tensor  # cell-major decoder CSR over all legal cells
-    edge_window: Tensor
-    edge_class: Tensor
-    win_ptr: Tensor  # window-major decoder CSR
-    edge_wcell: Tensor
-    edge_wclass: Tensor
-    cell_order: Tensor | None  # int32 tile order of the cell stages (cell-node configurations)
-    head_order: Tensor  # int32 tile order of the fused heads
-    radius_ptr: Tensor | None  # radius views: cell-node configurations only
-    radius_src: Tensor | None
-    radius_class: Tensor | None
-    seq_lens: Tensor
-    stone_schedule: Tensor | None  # longest-first work order of the stone attention (None: one tile each)
-    attn_src: Tensor  # padded attention slot -> row of [s; g] (or -1)
-    attn_back: Tensor  # row of [s; g] -> padded attention slot
-    dec_cell_ptr: Tensor  # CSR of the batch's own decoder order
-    noncanonical: Tensor | None = None  # speculative plans: device word, nonzero if the canonical orders failed
+    Scalars: n_pos, max_t, max_w, n_s, n_w, n_c.  Views (all device tensors):
+    inc_win_ptr (window-major incidence CSR), inc_stone_ptr / run_window /
+    run_class (its stone-major view), window_pos, layout_offsets /
+    layout_order (window-latent layout), cell_ptr / edge_window / edge_class
+    (cell-major decoder CSR over all legal cells), win_ptr / edge_wcell /
+    edge_wclass (window-major decoder CSR), cov_rows / edge_wcell_cov (the
+    covered cells and edge_wcell as indices into them; cell-node
+    configurations with relay views, else None), radius_ptr / radius_src /
+    radius_class (cell-node configurations, else None), cell_order (int32
+    tile order of the cell stages, or None), head_order (int32 tile order of
+    the fused heads), seq_lens, stone_schedule (longest-first work order of
+    the stone attention, or None), attn_src / attn_back (padded attention
+    slot <-> row of [s; g]), dec_cell_ptr (CSR of the batch's own decoder
+    order), noncanonical (speculative plans: device word, nonzero if the
+    canonical orders failed; None otherwise).
+    """
+
+    def __init__(self, model, b: Batch, speculative: bool = False):
+        self._b = b
+        self._cfg = model.cfg
+        self._speculative = speculative
+        self.n_pos, self.max_t, self.max_w = b.attn_valid.shape[0], b.attn_valid.shape[1], b.value_valid.shape[1]
+        self.n_s, self.n_w, self.n_c = b.stone_own.shape[0], b.window_feat.shape[0], b.cell_pos.shape[0]
+        if speculative:
+            # the canonical orders are assumed; the check is queued when first
+            # asked for (after the evaluation) and read by the caller
+            self.canonical = True
+        else:
+            self.canonical = not bool(self.noncanonical.item())
+            self.noncanonical = None
+
+    def start(self) -> None:
+        """Queue the order check of a speculative plan: called once the forward
+        has queued its first large launch, so the check runs while the host
+        is still queueing the early, small work rather than at the end."""
+        if self._speculative:
+            self.noncanonical  # noqa: B018 (derives and caches the device word)
+
+    @cached_property
+    def noncanonical(self) -> Tensor:
+        b = self._b
+        return ops.plan_check(b.dec_cell, b.dec_window, b.act_rev, b.radius_dst, b.window_slot, self.max_w)
+
+    @cached_property
+    def window_pos(self) -> Tensor:
+        return torch.div(self._b.window_slot, self.max_w, rounding_mode="floor")
+
+    @cached_property
+    def inc_win_ptr(self) -> Tensor:
+        return ops.runs_to_ptr(self._b.inc_window, self.n_w)
+
+    @cached_property
+    def _incidence(self) -> tuple[Tensor, Tensor, Tensor]:
+        # incidence plan (message_passing.py:495-517): the stone-major view of
+        # the window-major incidence list, stable, and its CSR
+        b = self._b
+        return ops.stable_key_order(b.inc_stone, b.inc_window, b.inc_class, self.n_s)
+
+    @property
+    def inc_stone_ptr(self) -> Tensor:
+        return self._incidence[0]
+
+    @property
+    def run_window(self) -> Tensor:
+        return self._incidence[1]
+
+    @property
+    def run_class(self) -> Tensor:
+        return self._incidence[2]
+
+    @cached_property
+    def _layout(self) -> tuple[Tensor, Tensor]:
+        # window-latent layout (window_latents.py:38-56); the sort is the
+        # identity on canonical batches
+        if self.canonical:
+            return torch.arange(self.n_w, device=self.window_pos.device), ops.runs_to_ptr(self.window_pos, self.n_pos)
+        lorder = _stable_order(self.window_pos.to(torch.int32))
+        return lorder, ops.runs_to_ptr(self.window_pos[lorder].contiguous(), self.n_pos)
+
+    @property
+    def layout_order(self) -> Tensor:
+        return self._layout[0]
+
+    @property
+    def layout_offsets(self) -> Tensor:
+        return self._layout[1]
+
+    @cached_property
+    def _decoder(self) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+        # decoder cell tables over all legal cells (cell_latents.py:96-165):
+        # on canonical batches the stable sorts are identities and act_rev is
+        # the window-major order
+        b = self._b
+        if self.canonical:
+            return b.dec_window, b.dec_class, b.dec_cell, b.act_rev
+        corder = _stable_order(b.dec_cell)
+        edge_window, edge_class, edge_cell = b.dec_window[corder], b.dec_class[corder], b.dec_cell[corder]
+        return edge_window, edge_class, edge_cell, _stable_order(edge_window)
+
+    @property
+    def edge_window(self) -> Tensor:
+        return self._decoder[0]
+
+    @property
+    def edge_class(self) -> Tensor:
+        return self._decoder[1]
+
+    @cached_property
+    def cell_ptr(self) -> Tensor:
+        return ops.runs_to_ptr(self._decoder[2].contiguous(), self.n_c)
+
+    @cached_property
+    def win_ptr(self) -> Tensor:
+        return ops.runs_to_ptr(self.edge_window[self._decoder[3]].contiguous(), self.n_w)
+
+    @cached_property
+    def edge_wcell(self) -> Tensor:
+        return self._decoder[2][self._decoder[3]]
+
+    @cached_property
+    def edge_wclass(self) -> Tensor:
+        return self.edge_class[self._decoder[3]]
+
+    @cached_property
+    def _covered(self) -> tuple[Tensor | None, Tensor | None]:
+        # only the covered cells (those with decoder entries) are read by the
+        # windows: their compact list, for a k/v projection of those rows
+        # alone.  The count comes from the batch's relay views (one per covered
+        # cell), so no device read is needed; the list is a scatter of the
+        # covered ranks.  (A batch whose relay views disagree with its decoder
+        # entries leaves covered cells past n_cov out of the list; the entries
+        # that name them are flagged by the sub-stage.)
+        b = self._b
+        if not (self._cfg.cell_nodes and getattr(b, "relay_cell_ptr", None) is not None):
+            return None, None
+        return ops.covered_rows(self.cell_ptr, b.relay_cell_ptr.shape[0] - 1, self.edge_wcell)
+
+    @property
+    def cov_rows(self) -> Tensor | None:
+        return self._covered[0]
+
+    @property
+    def edge_wcell_cov(self) -> Tensor | None:
+        return self._covered[1]
+
+    @cached_property
+    def _radius(self) -> tuple[Tensor | None, Tensor | None, Tensor | None]:
+        # radius edge tables (cell_nodes.py:23-94, model.py:843-859)
+        if not self._cfg.cell_nodes:
+            return None, None, None
+        b = self._b
+        classes = ops.radius_class(b.radius_orbit, b.radius_own, b.radius_on_axis)
+        src, dst = b.radius_src, b.radius_dst
+        if self._cfg.cell_node_scope == "uncovered":
+            keep = ~(self.cell_ptr[1:] > self.cell_ptr[:-1])[dst]
+            src, dst, classes = src[keep], dst[keep], classes[keep]
+        if not self.canonical:
+            rorder = _stable_order(dst)
+            src, dst, classes = src[rorder], dst[rorder], classes[rorder]
+        return ops.runs_to_ptr(dst.contiguous(), self.n_c), src, classes
+
+    @property
+    def radius_ptr(self) -> Tensor | None:
+        return self._radius[0]
+
+    @property
+    def radius_src(self) -> Tensor | None:
+        return self._radius[1]
+
+    @property
+    def radius_class(self) -> Tensor | None:
+        return self._radius[2]
+
+    @cached_property
+    def cell_order(self) -> Tensor | None:
+        # the fused cell stages run each 16-cell tile as long as its longest
+        # entry run: within each position, visit cells by (decoder entries,
+        # radius entries) so tiles hold cells of like counts (the cells of a
+        # position stay together, and with them the k/v rows they gather)
+        if not self._cfg.cell_nodes:
+            return None
+        return ops.segment_order(self._b.legal_offsets, self.cell_ptr, self.radius_ptr, self.n_c)
+
+    @cached_property
+    def head_order(self) -> Tensor:
+        # the heads walk the same decoder runs (cell_ptr has the batch's run
+        # lengths in any entry order), so the stages' order serves them too
+        if self.cell_order is not None:
+            return self.cell_order
+        return ops.segment_order(self._b.legal_offsets, self.cell_ptr, None, self.n_c)
+
+    @cached_property
+    def _slots(self) -> tuple[Tensor, Tensor]:
+        # attention rows [latents; stones] per position over the [s; g] buffer
+        return ops.attention_slots(self._b.stone_slot, self.n_pos, self.max_t)
+
+    @property
+    def attn_src(self) -> Tensor:
+        return self._slots[0]
+
+    @property
+    def attn_back(self) -> Tensor:
+        return self._slots[1]
+
+    @cached_property
+    def seq_lens(self) -> Tensor:
+        seq_lens = self._b.attn_valid.sum(dim=1, dtype=torch.int32)
+        if ops.tracing("stone_attention"):
+            ops.register_seq_lens(seq_lens)  # (a trace only: one read, for its accounting)
+        return seq_lens
+
+    @cached_property
+    def stone_schedule(self) -> Tensor | None:
+        return ops.stone_attention_schedule(self.seq_lens, self._cfg.heads, self.max_t)
+
+    @cached_property
+    def dec_cell_ptr(self) -> Tensor:
+        return self.cell_ptr if self.canonical else ops.runs_to_ptr(self._b.dec_cell, self.n_c)
 
 
 def _stable_order(key: Tensor) -> Tensor:
@@ -322,88 +517,7 @@ def make_plan(model, b: Batch, speculative: bool = False) -> Plan:
     orders without reading the check (no host synchronisation) and leaves
     the check's word in plan.noncanonical for the caller to read once the
     evaluation is queued; otherwise the check is read here."""
-    cfg = model.cfg
-    dev = b.stone_own.device
-    p, max_t, max_w = b.attn_valid.shape[0], b.attn_valid.shape[1], b.value_valid.shape[1]
-    n_s, n_w, n_c = b.stone_own.shape[0], b.window_feat.shape[0], b.cell_pos.shape[0]
-    window_pos = torch.div(b.window_slot, max_w, rounding_mode="floor")
-    check = ops.plan_check(b.dec_cell, b.dec_window, b.act_rev, b.radius_dst, b.window_slot, max_w)
-    canonical = True if speculative else not bool(check.item())
-    # incidence plan (message_passing.py:495-517): the stone-major view of the
-    # window-major incidence list, stable, and its CSR
-    inc_stone_ptr, run_window, run_class = ops.stable_key_order(b.inc_stone, b.inc_window, b.inc_class, n_s)
-    classes = ops.radius_class(b.radius_orbit, b.radius_own, b.radius_on_axis)
-    src, dst = b.radius_src, b.radius_dst
-    if canonical:
-        # the sorts below are identities on canonical batches (and act_rev is
-        # the window-major one): the same tables without them
-        lorder = torch.arange(n_w, device=dev)
-        offsets = ops.runs_to_ptr(window_pos, p)
-        edge_window, edge_class, edge_cell = b.dec_window, b.dec_class, b.dec_cell
-        worder = b.act_rev
-    else:
-        # window-latent layout (window_latents.py:38-56)
-        lorder = _stable_order(window_pos.to(torch.int32))
-        offsets = ops.runs_to_ptr(window_pos[lorder].contiguous(), p)
-        # decoder cell tables over all legal cells (cell_latents.py:96-165)
-        corder = _stable_order(b.dec_cell)
-        edge_window, edge_class, edge_cell = b.dec_window[corder], b.dec_class[corder], b.dec_cell[corder]
-        worder = _stable_order(edge_window)
-    cell_ptr = ops.runs_to_ptr(edge_cell.contiguous(), n_c)
-    win_ptr = ops.runs_to_ptr(edge_window[worder].contiguous(), n_w)
-    edge_wcell = edge_cell[worder]
-    # only the covered cells (those with decoder entries) are read by the
-    # windows: their compact list, for a k/v projection of those rows alone.
-    # The count comes from the batch's relay views (one per covered cell), so
-    # no device read is needed; the list is a scatter of the covered ranks
-    cov_rows = edge_wcell_cov = None
-    if cfg.cell_nodes and getattr(b, "relay_cell_ptr", None) is not None:
-        n_cov = b.relay_cell_ptr.shape[0] - 1
-        # (a batch whose relay views disagree with its decoder entries leaves
-        # covered cells past n_cov out of the list; the entries that name them
-        # are flagged by the sub-stage)
-        cov_rows, edge_wcell_cov = ops.covered_rows(cell_ptr, n_cov, edge_wcell)
-    # radius edge tables (cell_nodes.py:23-94, model.py:843-859)
-    radius_ptr = radius_src = radius_class = cell_order = None
-    if cfg.cell_nodes:
-        if cfg.cell_node_scope == "uncovered":
-            keep = ~(cell_ptr[1:] > cell_ptr[:-1])[dst]
-            src, dst, classes = src[keep], dst[keep], classes[keep]
-        if canonical:
-            radius_src, radius_dst, radius_class = src, dst, classes
-        else:
-            rorder = _stable_order(dst)
-            radius_src, radius_dst, radius_class = src[rorder], dst[rorder], classes[rorder]
-        radius_ptr = ops.runs_to_ptr(radius_dst.contiguous(), n_c)
-        # the fused cell stages run each 16-cell tile as long as its longest
-        # entry run: within each position, visit cells by (decoder entries,
-        # radius entries) so tiles hold cells of like counts (the cells of a
-        # position stay together, and with them the k/v rows they gather)
-        cell_order = ops.segment_order(b.legal_offsets, cell_ptr, radius_ptr, n_c)
-    # attention rows [latents; stones] per position over the [s; g] buffer
-    attn_src, attn_back = ops.attention_slots(b.stone_slot, p, max_t)
-    seq_lens = b.attn_valid.sum(dim=1, dtype=torch.int32)
-    if ops.tracing("stone_attention"):
-        ops.register_seq_lens(seq_lens)  # (a trace only: one read, for its accounting)
-    return Plan(
-        n_pos=p, max_t=max_t, max_w=max_w, n_s=n_s, n_w=n_w, n_c=n_c,
-        inc_win_ptr=ops.runs_to_ptr(b.inc_window, n_w),
-        run_window=run_window, run_class=run_class,
-        inc_stone_ptr=inc_stone_ptr,
-        window_pos=window_pos, layout_offsets=offsets, layout_order=lorder,
-        cov_rows=cov_rows, edge_wcell_cov=edge_wcell_cov, cell_ptr=cell_ptr,
-        edge_window=edge_window, edge_class=edge_class,
-        win_ptr=win_ptr, edge_wcell=edge_wcell, edge_wclass=edge_class[worder],
-        cell_order=cell_order,
-        # the heads walk the same decoder runs (cell_ptr has the batch's run
-        # lengths in any entry order), so the stages' order serves them too
-        head_order=cell_order if cell_order is not None else ops.segment_order(b.legal_offsets, cell_ptr, None, n_c),
-        radius_ptr=radius_ptr, radius_src=radius_src, radius_class=radius_class,
-        seq_lens=seq_lens, stone_schedule=ops.stone_attention_schedule(seq_lens, cfg.heads, max_t),
-        attn_src=attn_src, attn_back=attn_back,
-        dec_cell_ptr=cell_ptr if canonical else ops.runs_to_ptr(b.dec_cell, n_c),
-        noncanonical=check if speculative else None,
-    )
+    return Plan(model, b, speculative)
 
 
 def _plan_for(model, batch: Batch) -> tuple[Batch, Plan]:
@@ -561,16 +675,18 @@ def _trunk(model, b: Batch, plan: Plan, raw_cells: bool = False, W: Prepared | N
     P = W.params
     cfg = model.cfg
     n_s, p = plan.n_s, plan.n_pos
+    # the window state is stored in fp16 in the cell-node configuration, like
+    # the cell state (each update adds in fp32 and rounds once); the knob-off
+    # cell pass keeps it in fp32 for its compensated-weight launches.  Its
+    # gather is the forward's first large launch: the plan's small kernels
+    # and the host's work to queue them follow it
+    w = ops.gather_rows(W["window_table"], b.window_feat)
+    plan.start()
     # residual streams: s and g share one buffer so the attention and FFN
     # launches cover both with one row range
     sg = torch.empty((n_s + p * GLOBAL_ROWS, 128), dtype=F32, device=b.stone_own.device)
     sg[:n_s] = P["stone_table.weight"].index_select(0, b.stone_own)
     sg[n_s:] = (P["latent_base"][None] + P["token_moves.weight"].index_select(0, b.moves_idx)[:, None]).reshape(-1, 128)
-    # the window state is stored in fp16 in the cell-node configuration, like
-    # the cell state (each update adds in fp32 and rounds once); the knob-off
-    # cell pass keeps it in fp32 for its compensated-weight launches
-    wtab = P["window_table.weight"]
-    w = ops.gather_rows(wtab.to(HALF) if cfg.cell_nodes else wtab, b.window_feat)
     c = None
     if cfg.cell_nodes:
         # covered cells start from cell_base, the others from their nearest-stone
@@ -579,7 +695,7 @@ def _trunk(model, b: Batch, plan: Plan, raw_cells: bool = False, W: Prepared | N
         # (866 MB -> 433 MB per pass at 1.69M cells): every kernel that updates
         # it keeps the rows in fp32 registers and rounds once on the store, and
         # its readers feed fp16 MFMA operands
-        table = torch.cat([P["cell_nearest_table.weight"], P["cell_base"][None, :]]).to(HALF)
+        table = W["cell_table"]
         c = ops.gather_rows(table, b.cell_nearest, cover_ptr=plan.cell_ptr, cover_row=table.shape[0] - 1)
     sw_all = ops.run_reduce(W["sw_all"], plan.run_class, plan.inc_stone_ptr, n_s, F32)
     for i in range(cfg.blocks):
