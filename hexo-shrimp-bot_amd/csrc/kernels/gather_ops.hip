@@ -281,37 +281,49 @@ cell_attention_kernel(const Tin* __restrict__ q, const Tin* __restrict__ k,
 
 // ------------------------------------------------------------ window latents
 
-// One workgroup per position: kThreadsLR / 16 lane-groups stride over the
-// position's windows, each keeping an online softmax for the 4 slots of its
-// head chunk, kLookLR windows in flight; the partial states merge through LDS
-// in a fixed order.  A large workgroup per position (one per CU, 64
-// lane-groups with two windows each in flight): 129 -> 120 us per launch at
-// the production batch against 16 lane-groups with four.
-constexpr int kThreadsLR = 1024;
+// Each position's windows are split over kSplitLR workgroups (window ranges
+// of equal length): kThreadsLR / 16 lane-groups of a workgroup stride over
+// its range, each keeping an online softmax for the 4 slots of its head
+// chunk, kLookLR windows in flight; the groups' states merge through LDS in a
+// fixed order into the workgroup's partial state (the maxima, the sums and
+// the unnormalised accumulators), and latent_read_merge_kernel combines a
+// position's kSplitLR partial states in split order.  With one workgroup per
+// position the launch ended with the CUs that drew the positions with the
+// most windows (120 us per launch at the production batch); split, the
+// workgroups are short and balance over the CUs (111 us, merge included;
+// 107 us with the packed queries, the lazily moved reference point and no
+// order indirection for canonical batches).
+constexpr int kThreadsLR = 256;
 constexpr int kGroupsLR = kThreadsLR / kGroup;
 constexpr int kLookLR = 2;
+constexpr int kSplitLR = 8;
+constexpr int kPartLR = 4 * 4 * 2 + 4 * kRow;  // m[4][4], l[4][4], acc[4][128]
+constexpr float kTauLR = 8.f;  // the softmax reference point lags the maximum by at most this
 
-template <typename Tin>
+template <typename Tin, bool kOrder>
 __global__ void __launch_bounds__(kThreadsLR)
 latent_read_kernel(const Tin* __restrict__ q, const Tin* __restrict__ k,
                    const Tin* __restrict__ v, int64_t ldq, int64_t ldk, int64_t ldv,
                    const int64_t* __restrict__ offsets,
                    const int64_t* __restrict__ order, int64_t n_pos, int64_t n_w, float scale,
-                   float* __restrict__ out, float* __restrict__ m_out, float* __restrict__ l_out,
-                   int32_t* flag) {
+                   float* __restrict__ part, int32_t* flag) {
   __shared__ float s_m[kGroupsLR][4][4];         // [group][slot][head]
   __shared__ float s_l[kGroupsLR][4][4];
   __shared__ float s_acc[kGroupsLR][4][kRow];    // [group][slot][dim]
-  const int64_t pos = blockIdx.x;
+  const int64_t pos = blockIdx.x / kSplitLR;
+  const int split = blockIdx.x % kSplitLR;
   const int group = threadIdx.x / kGroup;
   const int lane = threadIdx.x % kGroup;
   const int head = lane >> 2;
-  float qv[4][8];
+  // the four slot queries in their storage format (16-bit pairs feed v_dot2)
+  Chunk8<Tin> qc[4];
 #pragma unroll
-  for (int s = 0; s < 4; ++s) load8(q + (pos * 4 + s) * ldq + lane * 8, qv[s]);
-  int64_t a = offsets[pos], b = offsets[pos + 1];
-  a = a < 0 ? 0 : (a > n_w ? n_w : a);
-  b = b < a ? a : (b > n_w ? n_w : b);
+  for (int s = 0; s < 4; ++s) qc[s].load(q + (pos * 4 + s) * ldq + lane * 8);
+  int64_t a0 = offsets[pos], b0 = offsets[pos + 1];
+  a0 = a0 < 0 ? 0 : (a0 > n_w ? n_w : a0);
+  b0 = b0 < a0 ? a0 : (b0 > n_w ? n_w : b0);
+  // this workgroup's share of the position's windows
+  const int64_t a = a0 + (b0 - a0) * split / kSplitLR, b = a0 + (b0 - a0) * (split + 1) / kSplitLR;
   float m[4], l[4], acc[4][8];
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
@@ -320,21 +332,23 @@ latent_read_kernel(const Tin* __restrict__ q, const Tin* __restrict__ k,
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[s][i] = 0.f;
   }
-  // Four windows per group are in flight at once, and the order entries of
-  // the next four are requested under them (unconditionally, from a clamped
-  // slot, and checked where they are used).
+  // kLook windows per group are in flight at once, and the order entries of
+  // the next kLook are requested under them (unconditionally, from a clamped
+  // slot, and checked where they are used).  Without an order (the identity:
+  // the windows of a position are contiguous) no index load precedes the
+  // row loads.
   constexpr int kLook = kLookLR;
   int64_t wr[kLook];
   auto fetch = [&](int64_t base) {
 #pragma unroll
     for (int u = 0; u < kLook; ++u) {
       const int64_t i = base + int64_t(u) * kGroupsLR;
-      wr[u] = order[i < b ? i : a];
+      wr[u] = kOrder ? order[i < b ? i : a] : i;
     }
   };
   if (a < b) fetch(a + group);
   for (int64_t base = a + group; base < b; base += kLook * kGroupsLR) {
-    float kvs[kLook][8], vvs[kLook][8];
+    Chunk8<Tin> kc[kLook], vc[kLook];
     bool ok[kLook];
 #pragma unroll
     for (int u = 0; u < kLook; ++u) {
@@ -342,28 +356,28 @@ latent_read_kernel(const Tin* __restrict__ q, const Tin* __restrict__ k,
       ok[u] = in && wr[u] >= 0 && wr[u] < n_w;
       if (in && !ok[u]) raise_flag(flag, MANTIS_FLAG_INDEX);
       const int64_t w = ok[u] ? wr[u] : 0;
-      load8(k + w * ldk + lane * 8, kvs[u]);
-      load8(v + w * ldv + lane * 8, vvs[u]);
+      kc[u].load(k + w * ldk + lane * 8);
+      vc[u].load(v + w * ldv + lane * 8);
     }
     if (base + kLook * kGroupsLR < b) fetch(base + kLook * kGroupsLR);
 #pragma unroll
     for (int u = 0; u < kLook; ++u) {
       if (!ok[u]) continue;
-      const float (&kv)[8] = kvs[u];
-      const float (&vv)[8] = vvs[u];
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-      float dot = 0.f;
+        const float score = head_sum(chunk_dot(qc[s], kc[u])) * scale;
+        // the reference point moves only when a score exceeds it by kTauLR
+        // (every weight stays below e^kTauLR); the first window sets it
+        if (score > m[s] + kTauLR) {
+          const float alpha = __expf(m[s] - score);
+          l[s] *= alpha;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) dot = fmaf(qv[s][j], kv[j], dot);
-      const float score = head_sum(dot) * scale;
-      const float m_new = fmaxf(m[s], score);
-      const float alpha = __expf(m[s] - m_new);
-      const float p = __expf(score - m_new);
-      l[s] = l[s] * alpha + p;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) acc[s][j] = fmaf(p, vv[j], acc[s][j] * alpha);
-      m[s] = m_new;
+          for (int j = 0; j < 8; ++j) acc[s][j] *= alpha;
+          m[s] = score;
+        }
+        const float p = __expf(score - m[s]);
+        l[s] += p;
+        chunk_axpy<false>(acc[s], p, vc[u], vc[u]);
       }
     }
   }
@@ -377,7 +391,9 @@ latent_read_kernel(const Tin* __restrict__ q, const Tin* __restrict__ k,
     for (int j = 0; j < 8; ++j) s_acc[group][s][lane * 8 + j] = acc[s][j];
   }
   __syncthreads();
-  // 4 slots x 128 dims = 512 outputs over 256 threads.
+  // the workgroup's partial state: per slot and head the maximum and the sum,
+  // per slot and dim the accumulator, both relative to that maximum
+  float* out = part + int64_t(blockIdx.x) * kPartLR;
   for (int o = threadIdx.x; o < 4 * kRow; o += kThreadsLR) {
     const int s = o / kRow, d = o % kRow, hh = d / 32;
     float mx = -INFINITY;
@@ -390,11 +406,38 @@ latent_read_kernel(const Tin* __restrict__ q, const Tin* __restrict__ k,
         at = fmaf(s_acc[g][s][d], f, at);
       }
     }
-    out[(pos * 4 + s) * kRow + d] = lt > 0.f ? at / lt : 0.f;
+    out[32 + s * kRow + d] = at;
     if ((d & 31) == 0) {
-      if (m_out) m_out[(pos * 4 + s) * 4 + hh] = mx;
-      if (l_out) l_out[(pos * 4 + s) * 4 + hh] = lt;
+      out[s * 4 + hh] = mx;
+      out[16 + s * 4 + hh] = lt;
     }
+  }
+}
+
+// A position's kSplitLR partial states, combined in split order: per slot
+// and dim the normalised read, per slot and head the final maximum and sum.
+__global__ void __launch_bounds__(4 * kRow)
+latent_read_merge_kernel(const float* __restrict__ part, int64_t n_pos, float* __restrict__ out,
+                         float* __restrict__ m_out, float* __restrict__ l_out) {
+  const int64_t pos = blockIdx.x;
+  const int o = threadIdx.x, s = o / kRow, d = o % kRow, hh = d / 32;
+  const float* pp = part + pos * kSplitLR * kPartLR;
+  float mx = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < kSplitLR; ++k) mx = fmaxf(mx, pp[k * kPartLR + s * 4 + hh]);
+  float lt = 0.f, at = 0.f;
+  if (mx > -INFINITY) {
+#pragma unroll
+    for (int k = 0; k < kSplitLR; ++k) {
+      const float f = __expf(pp[k * kPartLR + s * 4 + hh] - mx);
+      lt = fmaf(pp[k * kPartLR + 16 + s * 4 + hh], f, lt);
+      at = fmaf(pp[k * kPartLR + 32 + s * kRow + d], f, at);
+    }
+  }
+  out[(pos * 4 + s) * kRow + d] = lt > 0.f ? at / lt : 0.f;
+  if ((d & 31) == 0) {
+    if (m_out) m_out[(pos * 4 + s) * 4 + hh] = mx;
+    if (l_out) l_out[(pos * 4 + s) * 4 + hh] = lt;
   }
 }
 
@@ -707,24 +750,31 @@ int32_t mantis_cell_attention(const void* q, const void* k, const void* v, int32
   return launched();
 }
 
+int64_t mantis_latent_read_workspace(int64_t n_pos) {
+  return n_pos <= 0 ? 0 : n_pos * kSplitLR * kPartLR * int64_t(sizeof(float));
+}
+
 int32_t mantis_latent_read(const void* q, const void* k, const void* v, int32_t dtype,
                            int64_t ldq, int64_t ldk, int64_t ldv, const int64_t* offsets, const int64_t* order, int64_t n_pos,
                            int64_t n_w, int32_t heads, int32_t hd, float* out, float* m, float* l,
-                           int32_t* err_flag, void* stream) {
+                           float* workspace, int32_t* err_flag, void* stream) {
   if (n_pos == 0) return MANTIS_OK;
-  if (!q || !offsets || !out || heads != 4 || hd != 32 || n_pos < 0 || n_w < 0) return MANTIS_E_ARG;
+  if (!q || !offsets || !out || !workspace || heads != 4 || hd != 32 || n_pos < 0 || n_w < 0) return MANTIS_E_ARG;
+  if (n_pos > 2147483647LL / kSplitLR) return MANTIS_E_ARG;
   if (!lds_ok(ldq, ldk, ldv) || !aligned16(q) || (n_w > 0 && (!aligned16(k) || !aligned16(v))))
     return MANTIS_E_ARG;
-  if (n_w > 0 && (!k || !v || !order)) return MANTIS_E_ARG;
+  if (n_w > 0 && (!k || !v)) return MANTIS_E_ARG;
   const float scale = 1.0f / sqrtf(float(hd));
   hipStream_t s = as_stream(stream);
   const bool ok = with_type(dtype, [&](auto tv) {
     using T = decltype(tv);
-    latent_read_kernel<T><<<unsigned(n_pos), kThreadsLR, 0, s>>>(
+    auto kernel = order ? latent_read_kernel<T, true> : latent_read_kernel<T, false>;
+    kernel<<<unsigned(n_pos * kSplitLR), kThreadsLR, 0, s>>>(
         static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v), ldq, ldk, ldv,
-        offsets, order, n_pos, n_w, scale, out, m, l, err_flag);
+        offsets, order, n_pos, n_w, scale, workspace, err_flag);
   });
   if (!ok) return MANTIS_E_ARG;
+  latent_read_merge_kernel<<<unsigned(n_pos), 4 * kRow, 0, s>>>(workspace, n_pos, out, m, l);
   return launched();
 }
 

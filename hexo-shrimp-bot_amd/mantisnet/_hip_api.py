@@ -62,7 +62,8 @@ SIGNATURES = {
     "mantis_improve_policy": ([vp, vp, vp, i32, vp, i64, i64, ctypes.c_double, ctypes.c_double, vp, vp, vp, vp, vp, vp],
                               i32),
     "mantis_latent_mix": ([vp, i64, i64, vp, vp, vp, vp, vp], i32),
-    "mantis_latent_read": ([vp, vp, vp, i32, i64, i64, i64, vp, vp, i64, i64, i32, i32, vp, vp, vp, vp, vp], i32),
+    "mantis_latent_read": ([vp, vp, vp, i32, i64, i64, i64, vp, vp, i64, i64, i32, i32, vp, vp, vp, vp, vp, vp], i32),
+    "mantis_latent_read_workspace": ([i64], i64),
     "mantis_latent_broadcast": ([vp, vp, vp, i32, i64, i64, i64, vp, i64, i64, i32, i32, vp, i32, vp, vp, vp, vp],
                                 i32),
     "mantis_row_encode": ([vp, i32, i64, i64, vp, i64, vp, vp, i64, vp, i64, vp, vp, vp, vp, vp], i32),

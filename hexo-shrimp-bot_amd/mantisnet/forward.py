@@ -593,7 +593,9 @@ def _latent_cycle(W, P, pb, plan: Plan, w, g2, kv, qb):
     (both projected from w with the stones' values, see _block)."""
     p = plan.n_pos
     q = _proj(W, pb + "lq_read", g2)
-    read = ops.latent_read(q.view(p, 4, 4, 32), kv[:, :128], kv[:, 128:], plan.layout_offsets, plan.layout_order)
+    # (canonical batches: each position's windows are contiguous, no order)
+    read = ops.latent_read(q.view(p, 4, 4, 32), kv[:, :128], kv[:, 128:], plan.layout_offsets,
+                           None if plan.canonical else plan.layout_order)
     _resid(W, pb + "lo_read", read.view(p * 4, 128), g2)
     # 4 x 4 latent self-mix, fp32 (all four slots live; model.py:516-526)
     ops.latent_mix(g2, W[pb + "mix_qkv.wt"], W[pb + "mix_qkv.b"], W[pb + "mix_o.wt"], W[pb + "mix_o.b"])

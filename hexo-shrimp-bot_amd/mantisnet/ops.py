@@ -1024,32 +1024,36 @@ def latent_broadcast_residual(q: Tensor, kv: Tensor, window_pos: Tensor, wo: Ten
     return x
 
 
-def latent_read(q: Tensor, k: Tensor, v: Tensor, offsets: Tensor, order: Tensor, stats: bool = False):
+def latent_read(q: Tensor, k: Tensor, v: Tensor, offsets: Tensor, order: Tensor | None, stats: bool = False):
     """Four latent queries per position over its windows; q (P, 4, ...) and
-    k/v 128-wide rows; returns fp32 (P, 4, 4, 32) [and m, l]."""
-    dev = _on_gpu(q, k, v, offsets, order)
+    k/v 128-wide rows; returns fp32 (P, 4, 4, 32) [and m, l].  order None:
+    the windows of position p are rows offsets[p]..offsets[p+1]-1."""
+    dev = _on_gpu(q, k, v, offsets, *([] if order is None else [order]))
     p = q.shape[0]
     if q.numel() != p * 4 * 128:
         raise ValueError("read q must have shape (P, 4, heads, head_dim) with heads x head_dim = 128")
     if k.shape != v.shape:
         raise ValueError("read k and v must share one shape")
     n_w = k.shape[0]
-    if offsets.numel() != p + 1 or order.numel() != n_w:
+    if offsets.numel() != p + 1 or (order is not None and order.numel() != n_w):
         raise ValueError("offsets must be (P + 1,) and order (N_w,)")
     q2, ldq = _rows128(q.reshape(p * 4, -1) if q.is_contiguous() else q.contiguous().view(p * 4, -1), "q")
     k, ldk = _rows128(k, "k")
     v, ldv = _rows128(v, "v")
-    offsets, order = _i64(offsets, "offsets"), _i64(order, "order")
+    offsets = _i64(offsets, "offsets")
+    order = None if order is None else _i64(order, "order")
     out = torch.empty((p, 4, 4, 32), dtype=torch.float32, device=dev)
     m = torch.empty((p, 4, 4), dtype=torch.float32, device=dev) if stats else None
     l = torch.empty((p, 4, 4), dtype=torch.float32, device=dev) if stats else None
     if p:
+        # the partial softmax states of each position's window ranges
+        ws = torch.empty(_lib().mantis_latent_read_workspace(p) // 4, dtype=torch.float32, device=dev)
         # queries and outputs once, each window's k, v rows and order entry once
         nbytes = p * 4 * 128 * (q2.element_size() + 4) + n_w * (256 * k.element_size() + 8) + 8 * (p + 1)
         _launch("latent_read", nbytes, n_w * 4 * 4 * 128 * 2, lambda: _check(
             _lib().mantis_latent_read(
                 _ptr(q2), _ptr(k), _ptr(v), _dt(q2), ldq, ldk, ldv, _ptr(offsets), _ptr(order), p, n_w,
-                4, 32, _ptr(out), _ptr(m), _ptr(l), _ptr(error_flag(dev)), _stream(),
+                4, 32, _ptr(out), _ptr(m), _ptr(l), _ptr(ws), _ptr(error_flag(dev)), _stream(),
             ),
             "latent_read",
         ))

@@ -490,16 +490,27 @@ int32_t mantis_improve_policy(const void* policy_logits, const void* q_score, co
 
 /*
  * Window-latent read: four latent queries per position attend over the
- * position's windows (rows order[offsets[p]:offsets[p+1]] of k/v).  q is
+ * position's windows (rows order[offsets[p]:offsets[p+1]] of k/v; with
+ * order NULL, rows offsets[p]..offsets[p+1]-1 themselves).  q is
  * (P*4, heads*hd), k/v (n_w, heads*hd) rows in `dtype` with row strides
  * ldq/ldk/ldv; out (P, 4, heads, hd)
  * fp32; m/l (P, 4, heads) or NULL.  An empty position reads zero.
+ * `workspace`: device memory of mantis_latent_read_workspace(n_pos) bytes
+ * (16-byte aligned) for the partial softmax states of the position's window
+ * ranges, which the call combines before it returns to the stream; calls
+ * that share a workspace must be ordered on one stream.
  * Replaces mantisnet::window_latent_read (window_latents.py:224-268, 553-577).
  */
 int32_t mantis_latent_read(const void* q, const void* k, const void* v, int32_t dtype,
                            int64_t ldq, int64_t ldk, int64_t ldv, const int64_t* offsets, const int64_t* order, int64_t n_pos,
                            int64_t n_w, int32_t heads, int32_t hd, float* out, float* m, float* l,
-                           int32_t* err_flag, void* stream);
+                           float* workspace, int32_t* err_flag, void* stream);
+
+/*
+ * Bytes of the workspace mantis_latent_read needs for n_pos positions (no
+ * counterpart in the reference: the size of a buffer the caller provides).
+ */
+int64_t mantis_latent_read_workspace(int64_t n_pos);
 
 /*
  * Window-latent broadcast: every window attends over its position's four

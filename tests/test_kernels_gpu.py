@@ -118,6 +118,11 @@ def test_latent_read_and_broadcast_match_literal_loops(device, dt):
     exp = R.latent_read_loops(q.float(), k.float(), v.float(), offsets, order)
     torch.testing.assert_close(out.cpu(), exp, rtol=1e-4, atol=1e-5)
     assert torch.all(out.cpu()[0] == 0) and torch.all(out.cpu()[5] == 0)
+    # without an order the windows of a position are the rows offsets[p]..:
+    # the same read over the rows stored in layout order
+    kl, vl = k[order], v[order]
+    out_id = ops.latent_read(q.to(device), kl.to(device), vl.to(device), offsets.to(device), None)
+    torch.testing.assert_close(out_id.cpu(), exp, rtol=1e-4, atol=1e-5)
     qb = torch.randn(n_w, 4, 32, generator=gen).to(dt)
     kb = torch.randn(p, 4, 4, 32, generator=gen).to(dt)
     vb = torch.randn(p, 4, 4, 32, generator=gen).to(dt)
