@@ -176,6 +176,28 @@ __device__ __forceinline__ void row_store8(i32x4_t rsrc, int32_t row, int32_t by
   llvm_struct_buffer_store_x2(__builtin_bit_cast(i32x2_t, v), rsrc, row, byte_off, 0, 0);
 }
 
+// Sums over groups of 4 and 16 consecutive lanes by DPP (a VALU operand
+// modifier, no LDS round trip as a lane shuffle takes): the lanes of a quad
+// exchange with their xor-1 and xor-2 partners; a 16-lane row then adds its
+// mirrored half-rows and halves.  Every lane of the group ends with the same
+// sum, bitwise that of the xor butterfly (each step adds two operands that
+// are the same in both orders).
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f32(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), kCtrl, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float quad_sum(float x) {
+  x += dpp_f32<0xB1>(x);  // quad_perm [1, 0, 3, 2]: lane ^ 1
+  x += dpp_f32<0x4E>(x);  // quad_perm [2, 3, 0, 1]: lane ^ 2
+  return x;
+}
+__device__ __forceinline__ float row16_sum(float x) {
+  x = quad_sum(x);
+  x += dpp_f32<0x141>(x);  // row_half_mirror: the other quad of the 8-lane half
+  x += dpp_f32<0x140>(x);  // row_mirror: the other half of the 16-lane row
+  return x;
+}
+
 __device__ __forceinline__ void raise_flag(int32_t* flag, int32_t bit) {
   if (flag) atomicOr(flag, bit);
 }

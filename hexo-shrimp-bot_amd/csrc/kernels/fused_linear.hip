@@ -583,7 +583,10 @@ extern "C" int32_t mantis_fused_linear(const void* x, int32_t x_dtype, int64_t l
     }
     if (x_dtype == MANTIS_F32 && ln && !r && mode == 1 && n1 == 128)
       return launch<float, float, true, 128, false, false, false, 1>(a, s);
-    // fp16 rows with a LayerNorm (the cell state's k/v projection)
+    // fp16 rows with a LayerNorm (the cell state's k/v projection; the
+    // heads' action projection of the raw window state)
+    if (x_dtype == MANTIS_F16 && ln && !r && mode == 0 && n1 == 128 && !a.add1 && !a.add2)
+      return launch<_Float16, float, true, 128, false, false, false, 0, false, true>(a, s);
     if (x_dtype == MANTIS_F16 && ln && !r && mode == 0 && n1 == 256 && !a.add1 && !a.add2)
       return launch<_Float16, float, true, 256, false, false, false, 0, false, true>(a, s);
     if (x_dtype == MANTIS_F16 && ln && !r && mode == 0 && n1 == 512 && !a.add1 && !a.add2)

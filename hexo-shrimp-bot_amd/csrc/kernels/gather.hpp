@@ -8,11 +8,7 @@
 namespace mantis {
 
 // per-head sum of a lane partial: the head's 4 consecutive lanes
-__device__ __forceinline__ float head_sum(float x) {
-  x += __shfl_xor(x, 1);
-  x += __shfl_xor(x, 2);
-  return x;
-}
+__device__ __forceinline__ float head_sum(float x) { return quad_sum(x); }
 
 // An 8-element row chunk held in its storage format until the math needs
 // it, so a batch of rows can be requested before any is converted.

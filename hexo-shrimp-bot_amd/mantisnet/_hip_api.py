@@ -76,7 +76,8 @@ SIGNATURES = {
     "mantis_fused_linear_split": ([vp, i32, i64, vp, i64, i64, i32, vp, i32, i64, vp, vp, vp, i32, vp, i64, vp, vp,
                                    i64, i32, vp, vp, i32, i32, vp, i64, vp, vp], i32),
     "mantis_layer_norm": ([vp, i32, i64, i64, vp, vp, vp, i32, i64, vp], i32),
-    "mantis_value_read": ([vp, vp, i64, vp, vp, i64, vp, vp, vp, i32, vp, vp, vp], i32),
+    "mantis_value_read": ([vp, vp, i32, i64, vp, vp, i64, vp, vp, vp, vp, vp, i32, vp, vp, vp, vp], i32),
+    "mantis_value_read_workspace": ([i64], i64),
     "mantis_compose_q": ([vp, i64, vp, i64, i64, ctypes.c_float, vp, vp, vp], i32),
     "mantis_hex_neighbours": ([vp, vp, i64, i64, vp, vp, vp], i32),
     "mantis_hex_aggregate_linear": ([vp, vp, i64, vp, vp, vp, vp, vp, vp], i32),

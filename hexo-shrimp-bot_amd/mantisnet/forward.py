@@ -210,8 +210,10 @@ def _prepare(model, P) -> dict[str, Tensor]:
         put(pb + "ffn1", _fold(P, pb + "ln_ffn", [pb + "ffn.0"]))
         put(pb + "ffn2", _fold(P, None, [pb + "ffn.2"]))
     t["sw_all"] = torch.cat([t[f"blocks.{i}.sw_tab"] for i in range(cfg.blocks)], 1).contiguous()
-    # heads: act_proj reads ln_out(w)
+    # heads: act_proj reads ln_out(w) (the fused paths: the raw fp16 window
+    # state, with ln_out folded in)
     put("act_proj", _fold(P, None, ["act_proj"]))
+    put("act_proj_ln", _fold(P, "ln_out", ["act_proj"]))
     h1, h2, hb, tabs = [], [], [], []
     for proj, ext, mlp, emb in (("p", "p_act", "mlp_p", "e_pw"), ("q", "q_act", "mlp_q", "e_qw")):
         la = P[mlp + ".lin_a.weight"]
@@ -669,10 +671,14 @@ def trunk(model, batch: Batch):
     return out
 
 
-def _trunk(model, b: Batch, plan: Plan, raw_cells: bool = False, W: Prepared | None = None):
+def _trunk(model, b: Batch, plan: Plan, raw_cells: bool = False, W: Prepared | None = None,
+           raw_windows: bool = False):
     """(w_out, g_out, cells): cells are ln_out(c) in fp16, or with raw_cells
-    the fp16 cell state itself (the fused heads normalise it on the fly).
-    W: the prepared weights when the caller has just refreshed them."""
+    the fp16 cell state itself (the fused heads normalise it on the fly);
+    with raw_windows, in the cell-node configuration, w_out is the fp16
+    window state itself (the value read and the action projection apply
+    ln_out on the fly).  W: the prepared weights when the caller has just
+    refreshed them."""
     W = W or _prepared(model)
     P = W.params
     cfg = model.cfg
@@ -703,7 +709,7 @@ def _trunk(model, b: Batch, plan: Plan, raw_cells: bool = False, W: Prepared | N
     for i in range(cfg.blocks):
         _block(W, P, i, plan, b, sg, w, c, sw_all, i + 1 < cfg.blocks)
     g = sg[n_s:].view(p, GLOBAL_ROWS, 128)
-    w_out = ops.layer_norm(w, P["ln_out.weight"], P["ln_out.bias"], F32)
+    w_out = w if raw_windows and w.dtype == HALF else ops.layer_norm(w, P["ln_out.weight"], P["ln_out.bias"], F32)
     g_out = F.layer_norm(g, (128,), P["ln_out.weight"], P["ln_out.bias"], 1e-5).mean(dim=1)
     if c is None:
         return w_out, g_out, None
@@ -721,9 +727,16 @@ def value_head(model, w: Tensor, g: Tensor, batch: Batch):
 
 
 def _value_head(model, w: Tensor, g: Tensor, b: Batch, plan: Plan, W: Prepared | None = None):
+    """w: ln_out(w) fp32 rows, or the raw fp16 window state (ln_out applied
+    in the read)."""
     P = (W or _prepared(model)).params
-    r = ops.value_read(g.float().contiguous(), w.float().contiguous(), plan.layout_offsets, plan.layout_order,
-                       P["ln_value.weight"], P["ln_value.bias"], P["value_queries"])
+    if w.dtype == HALF:
+        r = ops.value_read(g.float().contiguous(), w.contiguous(), plan.layout_offsets, plan.layout_order,
+                           P["ln_value.weight"], P["ln_value.bias"], P["value_queries"],
+                           pre_gamma=P["ln_out.weight"], pre_beta=P["ln_out.bias"])
+    else:
+        r = ops.value_read(g.float().contiguous(), w.float().contiguous(), plan.layout_offsets, plan.layout_order,
+                           P["ln_value.weight"], P["ln_value.bias"], P["value_queries"])
     hidden = F.relu(F.linear(r.reshape(plan.n_pos, -1), P["mlp_v.0.weight"], P["mlp_v.0.bias"]))
     logits = F.linear(hidden, P["mlp_v.2.weight"], P["mlp_v.2.bias"])
     dist = logits.softmax(-1)
@@ -749,7 +762,10 @@ def _head_rows(model, w: Tensor, g: Tensor, cells: Tensor, b: Batch, plan: Plan,
         raw_cells = False
     W = W or _prepared(model)
     P = W.params
-    pre = FL(w.float().contiguous(), W["act_proj.w"], W["act_proj.b"])  # act_proj(w), fp16
+    if w.dtype == HALF:  # the raw window state: act_proj(ln_out(w)) with ln_out folded
+        pre = FL(w.contiguous(), W["act_proj_ln.w"], W["act_proj_ln.b"], layer_norm=True)
+    else:
+        pre = FL(w.float().contiguous(), W["act_proj.w"], W["act_proj.b"])  # act_proj(w), fp16
     empty_rows = F.relu(P["act_empty_base"] + P["act_table.weight"].index_select(0, model.act_empty_classes))
     g_half = F.linear(g.float(), W["glin_b"]).contiguous()  # (P, 256)
     x = cells if cells.dtype in (HALF, F32) else cells.float()
@@ -811,7 +827,7 @@ def forward(model, batch: Batch, mass_floor: float):
     W = _prepared(model)  # once per evaluation: trunk and heads share it
 
     def evaluate(plan):
-        w, g, c = _trunk(model, b, plan, raw_cells=True, W=W)
+        w, g, c = _trunk(model, b, plan, raw_cells=True, W=W, raw_windows=True)
         value, value_dist, value_logits = _value_head(model, w, g, b, plan, W)
         policy, q_score, q_values = _cell_heads(model, w, g, c, b, plan, mass_floor, raw_cells=True, W=W)
         return policy, q_score, q_values, value, value_dist, value_logits
@@ -830,7 +846,7 @@ def policy_q(model, batch: Batch):
     W = _prepared(model)
 
     def evaluate(plan):
-        w, g, c = _trunk(model, b, plan, raw_cells=True, W=W)
+        w, g, c = _trunk(model, b, plan, raw_cells=True, W=W, raw_windows=True)
         return _head_rows(model, w, g, c, b, plan, raw_cells=True, W=W)
 
     rows = _speculative(model, b, evaluate)

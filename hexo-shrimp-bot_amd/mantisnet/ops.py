@@ -1432,21 +1432,33 @@ _MODES_LN = {torch.float32: 0, torch.float16: 2}
 
 
 def value_read(token: Tensor, rows: Tensor, offsets: Tensor, order: Tensor, gamma: Tensor, beta: Tensor,
-               queries: Tensor) -> Tensor:
+               queries: Tensor, pre_gamma: Tensor | None = None, pre_beta: Tensor | None = None) -> Tensor:
+    """The value head's readout over [token; rows of each position], rows
+    normalised by (gamma, beta) on the fly; with pre_gamma/pre_beta the rows
+    (fp32 or fp16) first pass a LayerNorm with them (the trunk's ln_out of
+    the raw window state)."""
     dev = _on_gpu(token, rows, offsets, order, gamma, beta, queries)
     p = token.shape[0]
-    for t in (token, rows):
-        if t.dtype != torch.float32 or not t.is_contiguous() or t.shape[-1] != 128:
-            raise ValueError("value_read takes contiguous fp32 rows of 128")
+    if token.dtype != torch.float32 or not token.is_contiguous() or token.shape[-1] != 128:
+        raise ValueError("value_read takes a contiguous fp32 token row of 128 per position")
+    if rows.dtype not in (torch.float32, torch.float16) or not rows.is_contiguous() or rows.shape[-1] != 128:
+        raise ValueError("value_read takes contiguous fp32 or fp16 rows of 128")
+    if (pre_gamma is None) != (pre_beta is None):
+        raise ValueError("pre_gamma and pre_beta go together")
     if queries.shape != (4, 128):
         raise ValueError("value_read takes four 128-wide queries")
     out = torch.empty((p, 4, 128), dtype=torch.float32, device=dev)
     offsets, order = _i64(offsets, "offsets"), _i64(order, "order")
     g32, b32, q32 = gamma.float().contiguous(), beta.float().contiguous(), queries.float().contiguous()
-    nbytes = (rows.shape[0] + p) * (512 + 8) + p * 4 * 512
+    pg = None if pre_gamma is None else pre_gamma.float().contiguous()
+    pb = None if pre_beta is None else pre_beta.float().contiguous()
+    # the partial softmax states of each position's row ranges
+    ws = torch.empty(max(1, _lib().mantis_value_read_workspace(p) // 4), dtype=torch.float32, device=dev)
+    nbytes = rows.shape[0] * (128 * rows.element_size() + 8) + p * (512 + 8) + p * 4 * 512
     _launch("value_read", nbytes, 0, lambda: _check(
-        _lib().mantis_value_read(_ptr(token), _ptr(rows), rows.shape[0], _ptr(offsets), _ptr(order), p, _ptr(g32),
-                                 _ptr(b32), _ptr(q32), 4, _ptr(out), _ptr(error_flag(dev)), _stream()),
+        _lib().mantis_value_read(_ptr(token), _ptr(rows), _dt(rows), rows.shape[0], _ptr(offsets), _ptr(order), p,
+                                 _ptr(pg), _ptr(pb), _ptr(g32), _ptr(b32), _ptr(q32), 4, _ptr(out), _ptr(ws),
+                                 _ptr(error_flag(dev)), _stream()),
         "value_read"))
     return out
 

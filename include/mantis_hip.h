@@ -664,12 +664,25 @@ int32_t mantis_layer_norm(const void* x, int32_t x_dtype, int64_t ldx, int64_t m
  * learned 128-wide queries attend with scale 1/sqrt(128) over
  * [LN(token[p]); LN(rows[order[offsets[p]:offsets[p+1]]])], LN with
  * gamma/beta computed on the fly; out (n_pos, 4, 128) fp32 holds the
- * softmax-weighted sums.  fp32 throughout.
+ * softmax-weighted sums.  rows are fp32 or fp16 (rows_dtype); with
+ * pre_gamma/pre_beta (both or neither) a first LayerNorm with them is
+ * applied to each window row before LN (the trunk's ln_out, model.py:973-985,
+ * so the raw window state can be passed; the token row is taken as given).
+ * fp32 arithmetic throughout.
  */
-int32_t mantis_value_read(const float* token, const float* rows, int64_t n_rows,
-                          const int64_t* offsets, const int64_t* order, int64_t n_pos,
-                          const float* gamma, const float* beta, const float* queries,
-                          int32_t n_queries, float* out, int32_t* err_flag, void* stream);
+int32_t mantis_value_read(const float* token, const void* rows, int32_t rows_dtype, int64_t n_rows,
+                          const int64_t* offsets, const int64_t* order, int64_t n_pos, const float* pre_gamma,
+                          const float* pre_beta, const float* gamma, const float* beta, const float* queries,
+                          int32_t n_queries, float* out, float* workspace, int32_t* err_flag, void* stream);
+
+/*
+ * Bytes of the workspace mantis_value_read needs for n_pos positions: the
+ * partial softmax states of each position's row ranges, combined by the
+ * call before it returns to the stream (no counterpart in the reference:
+ * the size of a buffer the caller provides; calls sharing one must be
+ * ordered on one stream).
+ */
+int64_t mantis_value_read_workspace(int64_t n_pos);
 
 /*
  * Critic composition (model.py:177-220, segments.py:24-31): for the critic

@@ -191,6 +191,33 @@ def test_value_read_matches_padded_masked_softmax(device):
     sc = sc.masked_fill(~valid[:, None, :], torch.finfo(torch.float32).min)
     exp = torch.einsum("pqt,pth->pqh", sc.softmax(-1), pad)
     torch.testing.assert_close(out.cpu(), exp, rtol=1e-4, atol=1e-5)
+    # the raw fp16 window state with the trunk's ln_out applied in the read
+    # (the fused forward's path): value_read(token, LN_out(rows16)) in fp32
+    g0, b0 = 1 + 0.2 * torch.randn(128, generator=gen), 0.1 * torch.randn(128, generator=gen)
+    rows16 = (3 * torch.randn(rows.shape[0], 128, generator=gen) + 1).to(H16)
+    out16 = ops.value_read(token.to(device), rows16.to(device), offsets.to(device), order.to(device), g.to(device),
+                           b.to(device), queries.to(device), pre_gamma=g0.to(device), pre_beta=b0.to(device))
+    ops.raise_on_device_error(device)
+    normed = F.layer_norm(rows16.float(), (128,), g0, b0, 1e-5)
+    ref16 = ops.value_read(token.to(device), normed.to(device), offsets.to(device), order.to(device), g.to(device),
+                           b.to(device), queries.to(device))
+    torch.testing.assert_close(out16.cpu(), ref16.cpu(), rtol=1e-4, atol=1e-5)
+
+
+def test_action_projection_of_the_raw_window_state(device):
+    # act_proj(ln_out(w)) from fp16 rows with ln_out folded into the weights
+    # (the fused heads' path) against the fp32 LayerNorm then the projection
+    gen = _g(71)
+    m = 1000
+    w16 = (2 * torch.randn(m, 128, generator=gen) + 0.5).to(H16)
+    wt, bt = _w(128, 128, gen), 0.1 * torch.randn(128, generator=gen)
+    g0, b0 = 1 + 0.2 * torch.randn(128, generator=gen), 0.1 * torch.randn(128, generator=gen)
+    wf = (wt.float() * g0[None, :]).to(H16)
+    bf = bt + wt.float() @ b0
+    out = ops.fused_linear(w16.to(device), wf.to(device), bf.to(device), layer_norm=True)
+    ops.raise_on_device_error(device)
+    exp = _h(_ln(w16.float())) @ wf.float().t() + bf
+    torch.testing.assert_close(out.float().cpu(), exp, rtol=3e-3, atol=3e-3)
 
 
 def test_compose_q_matches_reference_formula(device):
