@@ -377,12 +377,11 @@ class MantisNet(nn.Module):
     def forward(self, batch: Batch, mass_floor: float) -> ModelOutput:
         """Every head (model.py:1185-1200).  Index errors the kernels flagged
         (out-of-range or unsorted tables) raise ValueError here, as the
-        reference's input validation does; checking costs one 4-byte read."""
+        reference's input validation does; the flag is read in the same
+        8-byte copy as the forward's order check."""
         from . import forward as fwd
-        from . import ops
 
         policy_logits, q_score, q_values, value, value_dist, value_logits = fwd.forward(self, batch, mass_floor)
-        ops.raise_on_device_error(policy_logits.device)
         return ModelOutput(
             policy_logits=policy_logits,
             q_score=q_score,

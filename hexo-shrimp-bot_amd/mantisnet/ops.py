@@ -152,25 +152,47 @@ def tile_counters(device: torch.device) -> Tensor:
     return c
 
 
-def error_flag(device: torch.device) -> Tensor:
+def _flag_words(device: torch.device) -> Tensor:
+    """The device's two int32 words: [0] the error flag, [1] a word that a
+    caller can have a kernel write and then read with the flag in one copy."""
     idx = device.index if device.index is not None else torch.cuda.current_device()
     f = _flags.get(idx)
     if f is None:
-        f = torch.zeros(1, dtype=torch.int32, device=device)
+        f = torch.zeros(2, dtype=torch.int32, device=device)
         _flags[idx] = f
     return f
+
+
+def error_flag(device: torch.device) -> Tensor:
+    return _flag_words(device)[:1]
+
+
+def flag_and_word(device: torch.device) -> tuple[Tensor, Tensor]:
+    """(error flag, spare word) of the device, both 1-element views."""
+    f = _flag_words(device)
+    return f[:1], f[1:]
+
+
+def read_flag_and_word(device: torch.device) -> tuple[int, int]:
+    """Both words in one device-to-host copy (one synchronisation)."""
+    bits, word = _flag_words(device).tolist()
+    return int(bits), int(word)
+
+
+def raise_on_bits(device: torch.device, bits: int) -> None:
+    """Clear the device's error flag and raise if ``bits`` (a value read from
+    it) names an error."""
+    if bits:
+        error_flag(device).zero_()
+        what = "; ".join(v for k, v in _FLAG_NAMES.items() if bits & k)
+        raise ValueError(f"MantisNet kernel input error on {device}: {what}")
 
 
 def raise_on_device_error(device: torch.device | None = None) -> None:
     """Raise if any kernel since the last check flagged bad indices."""
     devs = [device] if device is not None else [torch.device("cuda", i) for i in list(_flags)]
     for d in devs:
-        f = error_flag(d)
-        bits = int(f.item())
-        if bits:
-            f.zero_()
-            what = "; ".join(v for k, v in _FLAG_NAMES.items() if bits & k)
-            raise ValueError(f"MantisNet kernel input error on {d}: {what}")
+        raise_on_bits(d, int(error_flag(d).item()))
 
 
 def _check(status: int, what: str) -> None:
@@ -248,13 +270,19 @@ def segment_order(seg_ptr: Tensor, ptr_a: Tensor, ptr_b: Tensor | None, n_rows: 
 
 
 def plan_check(dec_cell: Tensor, dec_window: Tensor, act_rev: Tensor, radius_dst: Tensor, window_slot: Tensor,
-               max_w: int) -> Tensor:
+               max_w: int, out: Tensor | None = None) -> Tensor:
     """A device int32 word: nonzero unless the batch is in the encoder's
-    canonical orders (see mantis_plan_check).  No host read."""
+    canonical orders (see mantis_plan_check).  No host read.  ``out``: a
+    1-element int32 device tensor to write the word into (cleared first)."""
     dev = _on_gpu(dec_cell, dec_window, act_rev, radius_dst, window_slot)
     dec_cell, dec_window, act_rev = _i64(dec_cell, "dec_cell"), _i64(dec_window, "dec_window"), _i64(act_rev, "act_rev")
     radius_dst, window_slot = _i64(radius_dst, "radius_dst"), _i64(window_slot, "window_slot")
-    bad = torch.zeros(1, dtype=torch.int32, device=dev)
+    if out is None:
+        bad = torch.zeros(1, dtype=torch.int32, device=dev)
+    else:
+        if out.dtype != torch.int32 or out.numel() != 1 or out.device != dev:
+            raise ValueError("plan_check: out must be one int32 word on the inputs' device")
+        bad = out.zero_()
     if act_rev.numel() != dec_window.numel() or dec_cell.numel() != dec_window.numel():
         bad.fill_(1)
         return bad

@@ -262,3 +262,36 @@ def test_non_canonical_edge_order_takes_the_sorting_path(device):
     # the GPU path's summation order differs, so hold it to the tolerances
     rep = compare_outputs(out, oracle_forward(net, batch, 0.2), batch.legal_offsets)
     assert rep["ok"], rep
+
+
+def _same_outputs(a, b):
+    return all(torch.equal(getattr(a, k), getattr(b, k))
+               for k in ("policy_logits", "q_score", "q_values", "value", "value_dist", "value_logits"))
+
+
+def test_weights_changed_between_evaluations_are_used(device):
+    # once two evaluations have found the parameters unchanged, the next one
+    # runs on the last prepared operands and checks the parameters after it
+    # is queued; a change found then is evaluated again on rebuilt operands.
+    # Each result must be bitwise that of a fresh model holding the same
+    # weights, for an in-place change (optimizer-style) and a reload.
+    net = _model(device, seed=3)
+    batch = collate_positions(synthetic.random_games(1, 3, start=35)).to(device)
+    with torch.no_grad():
+        for _ in range(3):
+            net(batch, 0.2)
+        p = dict(net.named_parameters())
+        p["blocks.0.mlp_w.lin_a.weight"].mul_(1.25)
+        p["ln_out.weight"].add_(0.5)
+        got = net(batch, 0.2)
+        fresh = MantisNet(PRODUCTION)
+        fresh.load_state_dict(net.state_dict())
+        want = fresh.to(device).eval()(batch, 0.2)
+        assert _same_outputs(got, want)
+        # unchanged again: the evaluations after the change keep the new weights
+        assert _same_outputs(net(batch, 0.2), want) and _same_outputs(net(batch, 0.2), want)
+        other = synthetic.perturbed_state_dict(net, seed=9)
+        net.load_state_dict(other)
+        got = net(batch, 0.2)
+        fresh.load_state_dict(other)
+        assert _same_outputs(got, fresh(batch, 0.2))
