@@ -384,7 +384,7 @@ def main() -> int:
         ops.raise_on_device_error(dev)
         traced = ("attention_substage", "cell_attention", "cell_heads", "fused_linear", "stone_attention", "run_reduce",
                   "runs_to_ptr", "latent_", "row_encode", "layer_norm", "value_read", "compose_q", "gather_rows",
-                  "plan_check", "stable_key_order", "radius_class", "attention_slots", "covered_rows",
+                  "plan_check", "stable_key_order", "radius_class", "attention_slots", "covered_rows", "window_view",
                   "segment_order")
         with ops.trace(*traced) as tr:
             for _ in range(args.steps):

@@ -14,8 +14,9 @@
 //   stable): a counting sort.  Counts per stone (atomics), their prefix sums
 //   (the CSR pointer, a library scan between the two launches), a scatter of
 //   entry indices into their stone's run (atomic decrements: unordered), then
-//   each stone's run sorted by entry index in registers — a stone lies in at
-//   most 18 windows.  The result is the stable order whatever order
+//   each stone's run ordered by entry index across the lanes of half a
+//   wavefront (an entry's place is the count of the run's entries below it)
+//   — a stone lies in at most 18 windows.  The result is the stable order whatever order
 //   the atomics took, and the window and class of every entry are gathered
 //   in the same pass.
 // * radius_class_kernel: orbit + 48 (own + 2 on_axis), one pass.
@@ -146,49 +147,49 @@ __global__ __launch_bounds__(1024) void scan_counts_kernel(const int32_t* __rest
   }
 }
 
-constexpr int kRegRun = 32;  // runs up to this length are sorted in registers
+constexpr int kRunLanes = 32;  // runs up to this length are ordered across the lanes of a half-wavefront
 
-// each key's run of perm sorted ascending (the stable order), then the
-// entries' second and third columns gathered in that order
-__global__ void segment_sort_gather_kernel(const int64_t* __restrict__ ptr, int64_t n_keys, int64_t* __restrict__ perm,
-                                           const int64_t* __restrict__ col_a, const int64_t* __restrict__ col_b,
-                                           int64_t* __restrict__ out_a, int64_t* __restrict__ out_b) {
-  for (int64_t k = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; k < n_keys; k += int64_t(gridDim.x) * blockDim.x) {
-    const int64_t b = ptr[k], e = ptr[k + 1], len = e - b;
-    if (len <= kRegRun) {
-      int64_t v[kRegRun];
-#pragma unroll
-      for (int i = 0; i < kRegRun; ++i) v[i] = i < len ? perm[b + i] : INT64_MAX;
-      // odd-even transposition sort over the fixed register array
-#pragma unroll
-      for (int r = 0; r < kRegRun; ++r)
-#pragma unroll
-        for (int i = r & 1; i + 1 < kRegRun; i += 2) {
-          const int64_t lo = v[i] < v[i + 1] ? v[i] : v[i + 1], hi = v[i] < v[i + 1] ? v[i + 1] : v[i];
-          v[i] = lo;
-          v[i + 1] = hi;
-        }
-#pragma unroll
-      for (int i = 0; i < kRegRun; ++i)
-        if (i < len) {
-          out_a[b + i] = col_a[v[i]];
-          out_b[b + i] = col_b[v[i]];
-        }
-      continue;
+// each key's run of perm in ascending order (the stable order), and the
+// entries' second and third columns gathered in that order.  Half a
+// wavefront per key: lane j holds the run's entry j, and its place in the
+// order is the number of the run's entries below it (the entries of a run
+// are distinct).  Longer runs (no valid batch has them: a stone lies in at
+// most 18 windows) are sorted in place by one lane.
+__global__ void __launch_bounds__(256)
+segment_sort_gather_kernel(const int64_t* __restrict__ ptr, int64_t n_keys, int64_t* __restrict__ perm,
+                           const int64_t* __restrict__ col_a, const int64_t* __restrict__ col_b,
+                           int64_t* __restrict__ out_a, int64_t* __restrict__ out_b) {
+  const int lane = threadIdx.x % 64, sub = lane % kRunLanes, half = lane / kRunLanes;
+  const int64_t waves = int64_t(gridDim.x) * (blockDim.x / 64);
+  // the loop is uniform over the wavefront (the lane exchanges need every lane)
+  for (int64_t pair = int64_t(blockIdx.x) * (blockDim.x / 64) + threadIdx.x / 64; 2 * pair < n_keys;
+       pair += waves) {
+    const int64_t k = 2 * pair + half;
+    const int64_t b = k < n_keys ? ptr[k] : 0, e = k < n_keys ? ptr[k + 1] : 0, len = e - b;
+    const bool short_run = len <= kRunLanes;
+    const int64_t v = short_run && sub < len ? perm[b + sub] : INT64_MAX;
+    int rank = 0;
+#pragma unroll 8
+    for (int j = 0; j < kRunLanes; ++j) rank += __shfl(v, half * kRunLanes + j, 64) < v ? 1 : 0;
+    if (short_run && sub < len) {
+      out_a[b + rank] = col_a[v];
+      out_b[b + rank] = col_b[v];
     }
-    for (int64_t i = b + 1; i < e; ++i) {  // long runs (not produced by valid batches): insertion sort in place
-      const int64_t x = perm[i];
-      int64_t j = i - 1;
-      while (j >= b && perm[j] > x) {
-        perm[j + 1] = perm[j];
-        --j;
+    if (!short_run && sub == 0) {
+      for (int64_t i = b + 1; i < e; ++i) {
+        const int64_t x = perm[i];
+        int64_t j = i - 1;
+        while (j >= b && perm[j] > x) {
+          perm[j + 1] = perm[j];
+          --j;
+        }
+        perm[j + 1] = x;
       }
-      perm[j + 1] = x;
-    }
-    for (int64_t i = b; i < e; ++i) {
-      const int64_t src = perm[i];
-      out_a[i] = col_a[src];
-      out_b[i] = col_b[src];
+      for (int64_t i = b; i < e; ++i) {
+        const int64_t src = perm[i];
+        out_a[i] = col_a[src];
+        out_b[i] = col_b[src];
+      }
     }
   }
 }
@@ -215,6 +216,65 @@ __global__ void covered_rows_kernel(const int64_t* __restrict__ cell_ptr, const 
         raise_flag(flag, MANTIS_FLAG_INDEX);
       }
     }
+  }
+}
+
+// The window-major decoder view in one pass: entry i of the view is
+// cell-major entry perm[i]; its window, class and cell are gathered, the
+// windows' CSR pointer is derived from the gathered windows (as
+// runs_to_ptr_kernel does: ascending, in [0, n_w)), and the cell is written
+// as its covered rank (rank[c] - 1) when rank is given, else as is.  With
+// rank, cov_rows is filled as in covered_rows_kernel.  A permutation entry
+// out of range writes -1 to the entry's outputs and flags the index.
+__global__ void window_view_kernel(const int64_t* __restrict__ perm, const int64_t* __restrict__ dec_cell,
+                                   const int64_t* __restrict__ dec_class, const int64_t* __restrict__ dec_window,
+                                   int64_t n_e, int64_t n_w, int64_t n_c, const int64_t* __restrict__ cell_ptr,
+                                   const int64_t* __restrict__ rank, int64_t n_cov, int64_t* __restrict__ cov_rows,
+                                   int64_t* __restrict__ wcell, int64_t* __restrict__ wclass,
+                                   int64_t* __restrict__ win_ptr, int32_t* flag) {
+  const int64_t n = n_e + 1 > n_c ? n_e + 1 : n_c;
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x) {
+    if (rank && i < n_c && cell_ptr[i + 1] > cell_ptr[i]) {
+      const int64_t r = rank[i] - 1;
+      if (r >= 0 && r < n_cov) cov_rows[r] = i;
+    }
+    if (i > n_e) continue;
+    // the window of view entry i (n_w past the end) and of entry i - 1
+    // (-1 before the start); an entry out of range is reported by its owner
+    auto window_of = [&](int64_t v, bool own) -> int64_t {
+      const int64_t j = perm[v];
+      if (j < 0 || j >= n_e) {
+        if (own) {
+          raise_flag(flag, MANTIS_FLAG_INDEX);
+          wcell[v] = wclass[v] = -1;
+        }
+        return -2;
+      }
+      const int64_t w = dec_window[j];
+      if (own) {
+        const int64_t c = dec_cell[j];
+        wclass[v] = dec_class[j];
+        if (!rank) {
+          wcell[v] = c;
+        } else if (c >= 0 && c < n_c) {
+          wcell[v] = rank[c] - 1;
+        } else {
+          wcell[v] = -1;
+          raise_flag(flag, MANTIS_FLAG_INDEX);
+        }
+        if (w < 0 || w >= n_w) raise_flag(flag, MANTIS_FLAG_INDEX);
+      }
+      return w;
+    };
+    int64_t cur = i < n_e ? window_of(i, true) : n_w;
+    int64_t prev = i > 0 ? window_of(i - 1, false) : -1;
+    if (cur == -2 || (i < n_e && (cur < 0 || cur >= n_w))) continue;  // flagged above
+    if (i > 0 && (prev < 0 || prev >= n_w)) prev = cur;               // reported by the owner of i - 1
+    if (cur < prev) {
+      raise_flag(flag, MANTIS_FLAG_ORDER);
+      continue;
+    }
+    for (int64_t d = prev + 1; d <= cur; ++d) win_ptr[d] = i;
   }
 }
 
@@ -304,7 +364,8 @@ int32_t mantis_stable_key_order(const int64_t* key, const int64_t* col_a, const 
   int32_t* counts = static_cast<int32_t*>(workspace);
   int64_t* perm = reinterpret_cast<int64_t*>(static_cast<char*>(workspace) + (4 * n_keys + 7) / 8 * 8);
   scatter_kernel<<<grid_for(n_entries), 256, 0, st>>>(key, n_entries, n_keys, ptr, counts, perm);
-  segment_sort_gather_kernel<<<grid_for(n_keys), 256, 0, st>>>(ptr, n_keys, perm, col_a, col_b, out_a, out_b);
+  segment_sort_gather_kernel<<<grid_for((n_keys + 1) / 2 * 64), 256, 0, st>>>(ptr, n_keys, perm, col_a, col_b, out_a,
+                                                                              out_b);
   return launched();
 }
 
@@ -326,7 +387,8 @@ int32_t mantis_stable_key_order_noalloc(const int64_t* key, const int64_t* col_a
   scan_counts_kernel<<<1, 1024, 0, st>>>(counts, n_keys, ptr);
   if (n_entries && n_keys) {
     scatter_kernel<<<grid_for(n_entries), 256, 0, st>>>(key, n_entries, n_keys, ptr, counts, perm);
-    segment_sort_gather_kernel<<<grid_for(n_keys), 256, 0, st>>>(ptr, n_keys, perm, col_a, col_b, out_a, out_b);
+    segment_sort_gather_kernel<<<grid_for((n_keys + 1) / 2 * 64), 256, 0, st>>>(ptr, n_keys, perm, col_a, col_b, out_a,
+                                                                              out_b);
   }
   return launched();
 }
@@ -341,6 +403,20 @@ int32_t mantis_covered_rows(const int64_t* cell_ptr, const int64_t* rank, int64_
   if (n == 0) return MANTIS_OK;
   covered_rows_kernel<<<grid_for(n), 256, 0, as_stream(stream)>>>(cell_ptr, rank, n_c, n_cov, cov_rows, wcell, n_e,
                                                                   wcell_cov, err_flag);
+  return launched();
+}
+
+int32_t mantis_window_view(const int64_t* perm, const int64_t* dec_cell, const int64_t* dec_class,
+                           const int64_t* dec_window, int64_t n_e, int64_t n_w, int64_t n_c, const int64_t* cell_ptr,
+                           const int64_t* rank, int64_t n_cov, int64_t* cov_rows, int64_t* wcell, int64_t* wclass,
+                           int64_t* win_ptr, int32_t* err_flag, void* stream) {
+  if (n_e < 0 || n_w < 0 || n_c < 0 || n_cov < 0 || !win_ptr) return MANTIS_E_ARG;
+  if (n_e && (!perm || !dec_cell || !dec_class || !dec_window || !wcell || !wclass)) return MANTIS_E_ARG;
+  if (rank && (!cell_ptr || (n_cov && !cov_rows))) return MANTIS_E_ARG;
+  const int64_t n = n_e + 1 > n_c ? n_e + 1 : n_c;
+  window_view_kernel<<<grid_for(n), 256, 0, as_stream(stream)>>>(perm, dec_cell, dec_class, dec_window, n_e, n_w,
+                                                                 rank ? n_c : 0, cell_ptr, rank, n_cov, cov_rows,
+                                                                 wcell, wclass, win_ptr, err_flag);
   return launched();
 }
 

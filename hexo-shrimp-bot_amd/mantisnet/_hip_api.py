@@ -31,6 +31,7 @@ SIGNATURES = {
     "mantis_stable_key_order_noalloc": ([vp, vp, vp, i64, i64, vp, vp, vp, vp, vp], i32),
     "mantis_latent_broadcast_residual": ([vp, i64, vp, i64, vp, i64, i64, vp, vp, vp, i64, vp, vp], i32),
     "mantis_covered_rows": ([vp, vp, i64, i64, vp, vp, i64, vp, vp, vp], i32),
+    "mantis_window_view": ([vp, vp, vp, vp, i64, i64, i64, vp, vp, i64, vp, vp, vp, vp, vp, vp], i32),
     "mantis_radius_class": ([vp, vp, vp, i64, vp, vp], i32),
     "mantis_attention_slots": ([vp, i64, i64, i64, vp, vp, vp, vp], i32),
     "mantis_gather_rows": ([vp, i32, i64, i64, vp, vp, i64, i64, vp, i64, vp, vp], i32),

@@ -398,38 +398,46 @@ class Plan:
         return ops.runs_to_ptr(self._decoder[2].contiguous(), self.n_c)
 
     @cached_property
+    def _window_major(self) -> tuple[Tensor, Tensor, Tensor, Tensor | None]:
+        # the window-major decoder view (win_ptr, cell or covered rank, class,
+        # covered-cell list) in one launch.  Only the covered cells (those with
+        # decoder entries) are read by the windows: their compact list is for
+        # a k/v projection of those rows alone.  The count comes from the
+        # batch's relay views (one per covered cell), so no device read is
+        # needed.  (A batch whose relay views disagree with its decoder entries
+        # leaves covered cells past n_cov out of the list; the entries that
+        # name them are flagged by the sub-stage.)
+        b = self._b
+        cell, cls, window, perm = self._decoder[2], self._decoder[1], self._decoder[0], self._decoder[3]
+        if self._covers:
+            return ops.window_view(perm, cell, cls, window, self.n_w, self.cell_ptr, b.relay_cell_ptr.shape[0] - 1)
+        return ops.window_view(perm, cell, cls, window, self.n_w)
+
+    @property
+    def _covers(self) -> bool:
+        return bool(self._cfg.cell_nodes and getattr(self._b, "relay_cell_ptr", None) is not None)
+
+    @property
     def win_ptr(self) -> Tensor:
-        return ops.runs_to_ptr(self.edge_window[self._decoder[3]].contiguous(), self.n_w)
+        return self._window_major[0]
 
     @cached_property
     def edge_wcell(self) -> Tensor:
-        return self._decoder[2][self._decoder[3]]
+        if self._covers:  # the view holds covered ranks: the cells by a gather
+            return self._decoder[2][self._decoder[3]]
+        return self._window_major[1]
 
-    @cached_property
+    @property
     def edge_wclass(self) -> Tensor:
-        return self.edge_class[self._decoder[3]]
-
-    @cached_property
-    def _covered(self) -> tuple[Tensor | None, Tensor | None]:
-        # only the covered cells (those with decoder entries) are read by the
-        # windows: their compact list, for a k/v projection of those rows
-        # alone.  The count comes from the batch's relay views (one per covered
-        # cell), so no device read is needed; the list is a scatter of the
-        # covered ranks.  (A batch whose relay views disagree with its decoder
-        # entries leaves covered cells past n_cov out of the list; the entries
-        # that name them are flagged by the sub-stage.)
-        b = self._b
-        if not (self._cfg.cell_nodes and getattr(b, "relay_cell_ptr", None) is not None):
-            return None, None
-        return ops.covered_rows(self.cell_ptr, b.relay_cell_ptr.shape[0] - 1, self.edge_wcell)
+        return self._window_major[2]
 
     @property
     def cov_rows(self) -> Tensor | None:
-        return self._covered[0]
+        return self._window_major[3]
 
     @property
     def edge_wcell_cov(self) -> Tensor | None:
-        return self._covered[1]
+        return self._window_major[1] if self._covers else None
 
     @cached_property
     def _radius(self) -> tuple[Tensor | None, Tensor | None, Tensor | None]:

@@ -361,6 +361,36 @@ def covered_rows(cell_ptr: Tensor, n_cov: int, wcell: Tensor) -> tuple[Tensor, T
     return cov_rows, wcell_cov
 
 
+def window_view(perm: Tensor, dec_cell: Tensor, dec_class: Tensor, dec_window: Tensor, n_w: int,
+                cell_ptr: Tensor | None = None, n_cov: int = 0) -> tuple[Tensor, Tensor, Tensor, Tensor | None]:
+    """(win_ptr, wcell, wclass, cov_rows): the window-major view of the
+    cell-major decoder entries in one launch — dec_window[perm] as its CSR
+    pointer, dec_class[perm], and dec_cell[perm], or with cell_ptr the
+    covered rank of that cell plus the covered-cell list (as covered_rows)."""
+    dev = _on_gpu(perm, dec_cell, dec_class, dec_window, cell_ptr)
+    perm, dec_cell = _i64(perm, "perm"), _i64(dec_cell, "dec_cell")
+    dec_class, dec_window = _i64(dec_class, "dec_class"), _i64(dec_window, "dec_window")
+    n_e = perm.numel()
+    if not (dec_cell.numel() == dec_class.numel() == dec_window.numel() == n_e):
+        raise ValueError("perm, dec_cell, dec_class and dec_window must have one length")
+    rank = cov_rows = None
+    n_c = 0
+    if cell_ptr is not None:
+        cell_ptr = _i64(cell_ptr, "cell_ptr")
+        n_c = cell_ptr.numel() - 1
+        rank = torch.cumsum(cell_ptr[1:] > cell_ptr[:-1], 0)
+        cov_rows = torch.empty(n_cov, dtype=torch.int64, device=dev)
+    win_ptr = torch.empty(n_w + 1, dtype=torch.int64, device=dev)
+    wcell, wclass = torch.empty_like(perm), torch.empty_like(perm)
+    _launch("window_view", 8.0 * (7 * n_e + n_w + (3 * n_c + n_cov if rank is not None else 0)), 0.0,
+            lambda: _check(_lib().mantis_window_view(
+                _ptr(perm), _ptr(dec_cell), _ptr(dec_class), _ptr(dec_window), n_e, n_w, n_c,
+                _ptr(cell_ptr) if rank is not None else None, _ptr(rank) if rank is not None else None, n_cov,
+                _ptr(cov_rows) if rank is not None else None, _ptr(wcell), _ptr(wclass), _ptr(win_ptr),
+                _ptr(error_flag(dev)), _stream()), "window_view"))
+    return win_ptr, wcell, wclass, cov_rows
+
+
 def radius_class(orbit: Tensor, own: Tensor, on_axis: Tensor) -> Tensor:
     """orbit + 48 (own + 2 on_axis) in one pass (int64)."""
     dev = _on_gpu(orbit, own, on_axis)

@@ -136,6 +136,23 @@ int32_t mantis_covered_rows(const int64_t* cell_ptr, const int64_t* rank, int64_
                             int32_t* err_flag, void* stream);
 
 /*
+ * The window-major view of the cell-major decoder entries, in one pass
+ * (replaces the gathers edge_cell[order], edge_class[order],
+ * edge_window[order] and the runs_to_ptr of the last, cell_latents.py:96-165):
+ * view entry i is entry perm[i]; wclass[i] = dec_class[perm[i]]; win_ptr
+ * (n_w + 1) is the CSR pointer of the gathered windows (ascending, in
+ * [0, n_w), else MANTIS_FLAG_ORDER / MANTIS_FLAG_INDEX); wcell[i] is the
+ * cell dec_cell[perm[i]], or with rank (NULL allowed) its covered rank as in
+ * mantis_covered_rows, which also fills cov_rows (n_cov) from cell_ptr
+ * (n_c + 1) and rank (n_c).  perm outside [0, n_e): that entry's outputs -1
+ * and MANTIS_FLAG_INDEX.
+ */
+int32_t mantis_window_view(const int64_t* perm, const int64_t* dec_cell, const int64_t* dec_class,
+                           const int64_t* dec_window, int64_t n_e, int64_t n_w, int64_t n_c, const int64_t* cell_ptr,
+                           const int64_t* rank, int64_t n_cov, int64_t* cov_rows, int64_t* wcell, int64_t* wclass,
+                           int64_t* win_ptr, int32_t* err_flag, void* stream);
+
+/*
  * Radius edge classes: out[e] = orbit[e] + 48 (own[e] + 2 on_axis[e])
  * (model.py:843-859, the radius_orbit/own/on_axis class index).
  */

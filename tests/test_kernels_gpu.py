@@ -380,6 +380,52 @@ def test_covered_rows_matches_the_tensor_formulation(device):
     ops.raise_on_device_error(device)
 
 
+def test_window_view_matches_gathers_runs_and_covered_rows(device):
+    # the one-launch window-major decoder view against the separate steps it
+    # replaces: three gathers through the permutation, the windows' CSR and
+    # the covered-cell compaction; on a real batch (act_rev) and on a random
+    # cell-major table with its stable window order
+    def check(perm, cell, cls, window, n_w, n_c, cell_ptr=None):
+        n_cov = 0 if cell_ptr is None else int((cell_ptr[1:] > cell_ptr[:-1]).sum())
+        args = [t.to(device) for t in (perm, cell, cls, window)]
+        win_ptr, wcell, wclass, cov_rows = ops.window_view(
+            *args, n_w, None if cell_ptr is None else cell_ptr.to(device), n_cov)
+        ops.raise_on_device_error(device)
+        assert torch.equal(wclass.cpu(), cls[perm])
+        assert torch.equal(win_ptr.cpu(), torch.searchsorted(window[perm], torch.arange(n_w + 1)))
+        if cell_ptr is None:
+            assert cov_rows is None and torch.equal(wcell.cpu(), cell[perm])
+        else:
+            covered = cell_ptr[1:] > cell_ptr[:-1]
+            assert torch.equal(cov_rows.cpu(), torch.nonzero(covered)[:, 0])
+            assert torch.equal(wcell.cpu(), (torch.cumsum(covered, 0) - 1)[cell[perm]])
+
+    b = _plan_batch()
+    n_w, n_c = b.window_feat.shape[0], b.cell_pos.shape[0]
+    cell_ptr = torch.searchsorted(b.dec_cell, torch.arange(n_c + 1))
+    for ptr in (None, cell_ptr):
+        check(b.act_rev, b.dec_cell, b.dec_class, b.dec_window, n_w, n_c, ptr)
+    gen = _g(43)
+    n_c, n_w, n_e = 300, 120, 700
+    cell = torch.sort(torch.randint(0, n_c, (n_e,), generator=gen)).values
+    window = torch.randint(0, n_w, (n_e,), generator=gen)
+    window[window == 5] = 6  # window 5 has no entries
+    cls = torch.randint(0, 40, (n_e,), generator=gen)
+    perm = torch.argsort(window, stable=True)
+    for ptr in (None, torch.searchsorted(cell, torch.arange(n_c + 1))):
+        check(perm, cell, cls, window, n_w, n_c, ptr)
+    check(perm[:0], cell[:0], cls[:0], window[:0], n_w, n_c)  # no entries: every window's run empty
+    # a permutation entry out of range, and windows out of order, are flagged
+    bad = perm.clone()
+    bad[3] = n_e
+    ops.window_view(*(t.to(device) for t in (bad, cell, cls, window)), n_w)
+    with pytest.raises(ValueError):
+        ops.raise_on_device_error(device)
+    ops.window_view(*(t.to(device) for t in (perm.flip(0), cell, cls, window)), n_w)
+    with pytest.raises(ValueError):
+        ops.raise_on_device_error(device)
+
+
 def test_radius_class_and_attention_slots(device):
     b = _plan_batch()
     got = ops.radius_class(b.radius_orbit.to(device), b.radius_own.to(device), b.radius_on_axis.to(device)).cpu()
