@@ -589,6 +589,8 @@ extern "C" int32_t mantis_fused_linear(const void* x, int32_t x_dtype, int64_t l
       return launch<_Float16, float, true, 128, false, false, false, 0, false, true>(a, s);
     if (x_dtype == MANTIS_F16 && ln && !r && mode == 0 && n1 == 256 && !a.add1 && !a.add2)
       return launch<_Float16, float, true, 256, false, false, false, 0, false, true>(a, s);
+    if (x_dtype == MANTIS_F16 && ln && !r && mode == 0 && n1 == 384 && !a.add1 && !a.add2)
+      return launch<_Float16, float, true, 384, false, false, false, 0, false, true>(a, s);
     if (x_dtype == MANTIS_F16 && ln && !r && mode == 0 && n1 == 512 && !a.add1 && !a.add2)
       return launch<_Float16, float, true, 512, false, false, false, 0, false, true>(a, s);
     if (x_dtype == MANTIS_F16 && ln && !r && mode == 0 && n1 == 256)

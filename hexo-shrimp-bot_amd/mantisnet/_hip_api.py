@@ -30,6 +30,7 @@ SIGNATURES = {
     "mantis_stable_key_order": ([vp, vp, vp, i64, i64, vp, vp, vp, vp, vp], i32),
     "mantis_stable_key_order_noalloc": ([vp, vp, vp, i64, i64, vp, vp, vp, vp, vp], i32),
     "mantis_latent_broadcast_residual": ([vp, i64, vp, i64, vp, i64, i64, vp, vp, vp, i64, vp, vp], i32),
+    "mantis_latent_broadcast_project_residual": ([vp, vp, vp, i64, vp, i64, i64, vp, vp, vp, i64, vp, vp], i32),
     "mantis_covered_rows": ([vp, vp, i64, i64, vp, vp, i64, vp, vp, vp], i32),
     "mantis_window_view": ([vp, vp, vp, vp, i64, i64, i64, vp, vp, i64, vp, vp, vp, vp, vp, vp], i32),
     "mantis_radius_class": ([vp, vp, vp, i64, vp, vp], i32),

@@ -202,8 +202,15 @@ def _prepare(model, P) -> dict[str, Tensor]:
         wv_, bv_ = _fold(P, pb + "ln_sw_w", [pb + "v"])
         wr_, br_ = _fold(P, pb + "latent_ln_read_w", [pb + "latent_wk_read", pb + "latent_wv_read"])
         wb_, bb_ = _fold(P, pb + "latent_ln_bcast_q", [pb + "latent_wq_bcast"])
-        t[pb + "wproj.w"] = torch.cat([wv_, wr_, wb_]).contiguous()
-        t[pb + "wproj.b"] = torch.cat([bv_, br_, bb_]).contiguous()
+        if cfg.cell_nodes:
+            # fp16 window state: the broadcast projects its queries itself
+            # from the rows it updates, so this launch is 384 wide
+            t[pb + "wproj.w"] = torch.cat([wv_, wr_]).contiguous()
+            t[pb + "wproj.b"] = torch.cat([bv_, br_]).contiguous()
+            t[pb + "bcast_q.w"], t[pb + "bcast_q.b"] = wb_, bb_
+        else:
+            t[pb + "wproj.w"] = torch.cat([wv_, wr_, wb_]).contiguous()
+            t[pb + "wproj.b"] = torch.cat([bv_, br_, bb_]).contiguous()
         put(pb + "mlp_s1", _fold(P, pb + "ln_sw_s", [pb + "mlp_s.lin_a"]))
         t[pb + "mlp_s2.w"] = P[pb + "mlp_s.lin_b.weight"].to(HALF).contiguous()
         put(pb + "mlp_s3", _fold(P, None, [pb + "mlp_s.out"]))
@@ -625,7 +632,8 @@ def _cell_pass(W, P, pb, plan: Plan, b: Batch, w):
 
 def _latent_cycle(W, P, pb, plan: Plan, w, g2, kv, qb):
     """kv: the windows' latent-read keys|values, qb: their broadcast queries
-    (both projected from w with the stones' values, see _block)."""
+    (both projected from w with the stones' values, see _block); qb is None
+    for the fp16 window state, whose broadcast projects the queries itself."""
     p = plan.n_pos
     q = _proj(W, pb + "lq_read", g2)
     # (canonical batches: each position's windows are contiguous, no order)
@@ -636,8 +644,10 @@ def _latent_cycle(W, P, pb, plan: Plan, w, g2, kv, qb):
     ops.latent_mix(g2, W[pb + "mix_qkv.wt"], W[pb + "mix_qkv.b"], W[pb + "mix_o.wt"], W[pb + "mix_o.b"])
     kvb = _proj(W, pb + "lkv_bcast", g2)
     if w.dtype == HALF:
-        # broadcast, output projection and residual in one pass over the windows
-        ops.latent_broadcast_residual(qb, kvb, plan.window_pos, W[pb + "lo_bcast.w"], W[pb + "lo_bcast.b"], w)
+        # query projection, broadcast, output projection and residual in one
+        # pass over the windows
+        ops.latent_broadcast_residual(None, kvb, plan.window_pos, W[pb + "lo_bcast.w"], W[pb + "lo_bcast.b"], w,
+                                      wq=W[pb + "bcast_q.w"], bq=W[pb + "bcast_q.b"])
     else:
         out = ops.latent_broadcast_rows(qb, kvb, plan.window_pos, out_dtype=HALF)
         _resid(W, pb + "lo_bcast", out.view(plan.n_w, 128), w)
@@ -662,7 +672,7 @@ def _block(W, P, i: int, plan: Plan, b: Batch, sg, w, c, sw_all, update_stones: 
     # §5.2 stones <- windows: s += mlp_s(LN s, agg + class term); w does not
     # change again until the latent broadcast, so its latent-read keys/values
     # and broadcast queries are projected here in the same launch
-    wp = _proj(W, pb + "wproj", w)  # (n_w, 512): v | latent k | latent v | broadcast q
+    wp = _proj(W, pb + "wproj", w)  # (n_w, 384 or 512): v | latent k | latent v [| broadcast q]
     agg = ops.run_reduce(wp[:, :128], plan.run_window, plan.inc_stone_ptr, n_s, F32)
     FL(s, W[pb + "mlp_s1.w"], W[pb + "mlp_s1.b"], layer_norm=True, x2=agg, w2=W[pb + "mlp_s2.w"],
        add1=sw_all[:, 128 * i:128 * (i + 1)], relu=True, w3=W[pb + "mlp_s3.w"], b3=W[pb + "mlp_s3.b"],
@@ -684,7 +694,7 @@ def _block(W, P, i: int, plan: Plan, b: Batch, sg, w, c, sw_all, update_stones: 
         read = ops.latent_attend(qkv, b.attn_valid, p, max_t)
         _resid(W, pb + "attn_o", read, g2)
     # §5.4 latent cycle
-    _latent_cycle(W, P, pb, plan, w, g2, wp[:, 128:384], wp[:, 384:])
+    _latent_cycle(W, P, pb, plan, w, g2, wp[:, 128:384], wp[:, 384:] if wp.shape[1] > 384 else None)
     # FFN over [stones; latents] (latents only in the last block)
     tgt = sg if update_stones else g2
     FL(tgt, W[pb + "ffn1.w"], W[pb + "ffn1.b"], layer_norm=True, relu=True, w3=W[pb + "ffn2.w"],

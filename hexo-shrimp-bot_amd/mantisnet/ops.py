@@ -1051,15 +1051,27 @@ def cell_heads(c: Tensor, w1: Tensor, b1: Tensor, w2: Tensor, w3: Tensor, b3: Te
     return out
 
 
-def latent_broadcast_residual(q: Tensor, kv: Tensor, window_pos: Tensor, wo: Tensor, bo: Tensor, x: Tensor) -> Tensor:
+def latent_broadcast_residual(q: Tensor | None, kv: Tensor, window_pos: Tensor, wo: Tensor, bo: Tensor, x: Tensor,
+                              wq: Tensor | None = None, bq: Tensor | None = None) -> Tensor:
     """x += wo . broadcast(q over the position's 4 latents) + bo, in place on
     fp16 window rows x (see mantis_latent_broadcast_residual): q (n_w, 128)
-    and kv (4 P, 256) = k | v fp16 rows with unit column stride."""
-    dev = _on_gpu(q, kv, window_pos, wo, bo, x)
+    and kv (4 P, 256) = k | v fp16 rows with unit column stride.  With q None
+    the queries are fp16(LN(x) wq^T + bq), projected in the same launch from
+    the rows it updates (wq fp16 (128, 128) with the LayerNorm affine folded
+    in, bq (128,); mantis_latent_broadcast_project_residual)."""
+    dev = _on_gpu(q, kv, window_pos, wo, bo, x, wq)
     n_w = x.shape[0]
     if x.dtype != torch.float16 or x.ndim != 2 or x.shape[1] != 128 or x.stride(1) != 1:
         raise ValueError("x must be fp16 (n_w, 128) rows")
-    if q.dtype != torch.float16 or q.shape != (n_w, 128) or q.stride(1) != 1:
+    if q is None:
+        if wq is None or bq is None:
+            raise ValueError("without q rows, wq and bq are needed")
+        if wq.dtype != torch.float16 or wq.shape != (128, 128) or not wq.is_contiguous():
+            raise ValueError("wq must be a contiguous fp16 (128, 128) matrix")
+        if bq.shape != (128,):
+            raise ValueError("bq must have 128 entries")
+        bq = bq.float().contiguous()
+    elif q.dtype != torch.float16 or q.shape != (n_w, 128) or q.stride(1) != 1:
         raise ValueError("q must be fp16 (n_w, 128) rows")
     if kv.dtype != torch.float16 or kv.ndim != 2 or kv.shape[1] != 256 or kv.shape[0] % 4 or kv.stride(1) != 1:
         raise ValueError("kv must be fp16 (4 P, 256) rows")
@@ -1071,14 +1083,22 @@ def latent_broadcast_residual(q: Tensor, kv: Tensor, window_pos: Tensor, wo: Ten
         raise ValueError("window_pos must have one entry per window")
     if n_w:
         n_pos = kv.shape[0] // 4
-        # q, x read and x written once per window; the latent k/v once per position
-        nbytes = n_w * (256 + 512 + 8) + n_pos * 4 * 512
-        flops = n_w * (2 * 128 * 128 + 4 * 4 * 32 * 4)
-        _launch("latent_broadcast_residual", nbytes, flops, lambda: _check(
-            _lib().mantis_latent_broadcast_residual(_ptr(q), q.stride(0), _ptr(kv), kv.stride(0), _ptr(window_pos),
-                                                    n_pos, n_w, _ptr(wo), _ptr(bo), _ptr(x), x.stride(0),
-                                                    _ptr(error_flag(dev)), _stream()),
-            "latent_broadcast_residual"))
+        # q (or none), x read and x written once per window; the latent k/v once per position
+        nbytes = n_w * ((256 if q is not None else 0) + 512 + 8) + n_pos * 4 * 512
+        flops = n_w * ((2 if q is not None else 4) * 128 * 128 + 4 * 4 * 32 * 4)
+        if q is not None:
+            _launch("latent_broadcast_residual", nbytes, flops, lambda: _check(
+                _lib().mantis_latent_broadcast_residual(_ptr(q), q.stride(0), _ptr(kv), kv.stride(0),
+                                                        _ptr(window_pos), n_pos, n_w, _ptr(wo), _ptr(bo), _ptr(x),
+                                                        x.stride(0), _ptr(error_flag(dev)), _stream()),
+                "latent_broadcast_residual"))
+        else:
+            _launch("latent_broadcast_project_residual", nbytes, flops, lambda: _check(
+                _lib().mantis_latent_broadcast_project_residual(_ptr(wq), _ptr(bq), _ptr(kv), kv.stride(0),
+                                                                _ptr(window_pos), n_pos, n_w, _ptr(wo), _ptr(bo),
+                                                                _ptr(x), x.stride(0), _ptr(error_flag(dev)),
+                                                                _stream()),
+                "latent_broadcast_project_residual"))
     return x
 
 

@@ -473,6 +473,19 @@ int32_t mantis_latent_broadcast_residual(const void* q, int64_t ldq, const void*
                                          const float* bo, void* x, int64_t ldx, int32_t* err_flag, void* stream);
 
 /*
+ * mantis_latent_broadcast_residual with the queries projected from the
+ * window rows themselves: q[r] = fp16( LN(x[r]) wq^T + bq ), wq (128, 128)
+ * fp16 (out x in) and bq (128) fp32 with the LayerNorm affine folded in
+ * (the latent_ln_bcast_q LayerNorm and latent_wq_bcast projection,
+ * window_latents.py:350-381, model.py:527-541).  x is read once for both
+ * the query and the residual, and no query rows are written or read.
+ */
+int32_t mantis_latent_broadcast_project_residual(const void* wq, const float* bq, const void* kv, int64_t ldkv,
+                                                 const int64_t* window_pos, int64_t n_pos, int64_t n_w,
+                                                 const void* wo, const float* bo, void* x, int64_t ldx,
+                                                 int32_t* err_flag, void* stream);
+
+/*
  * Latent self-mix, in place on the fp32 latent rows g (n_pos * 4 rows of
  * 128, row stride ldg), per position p in fp32:
  *   z = LN(g_p) (no affine: fold it into wqkv_t / bqkv),

@@ -589,6 +589,49 @@ def test_latent_broadcast_residual_matches_the_unfused_composition(device):
     assert torch.equal(got[5].cpu(), want5)
 
 
+def test_latent_broadcast_projecting_its_queries_matches_the_separate_projection(device):
+    # the form that projects q = fp16(LN(x) wq^T + bq) from the rows it
+    # updates = the fp16 LayerNorm projection of x, then the form that reads q
+    gen = _g(33)
+    n_pos, n_w = 41, 5003
+    kv = torch.randn(4 * n_pos, 256, generator=gen).to(H16)
+    pos = torch.sort(torch.randint(0, n_pos, (n_w,), generator=gen)).values
+    wq, wo = _w(128, 128, gen), _w(128, 128, gen)
+    bq, bo = 0.1 * torch.randn(128, generator=gen), 0.05 * torch.randn(128, generator=gen)
+    x0 = (0.3 + 2 * torch.randn(n_w, 128, generator=gen)).to(H16)
+    d = lambda t: t.to(device)  # noqa: E731
+    got = d(x0.clone())
+    ops.latent_broadcast_residual(None, d(kv), d(pos), d(wo), d(bo), got, wq=d(wq), bq=d(bq))
+    ops.raise_on_device_error(device)
+    q = ops.fused_linear(d(x0), d(wq), d(bq), layer_norm=True)
+    ref = d(x0.clone())
+    ops.latent_broadcast_residual(q, d(kv), d(pos), d(wo), d(bo), ref)
+    ops.raise_on_device_error(device)
+    # the two products sum the same terms in other orders: a query may round
+    # to the neighbouring fp16 value, which moves the output by about that much
+    torch.testing.assert_close(got.float().cpu(), ref.float().cpu(), rtol=2e-3, atol=2e-3)
+    assert (got != ref).float().mean().item() < 0.01
+    # and against an fp64 composition of the whole step
+    xd = x0.double()
+    z = (xd - xd.mean(1, keepdim=True)) / torch.sqrt(xd.var(1, unbiased=False, keepdim=True) + 1e-5)
+    qd = (z @ wq.double().t() + bq.double()).view(n_w, 4, 32)
+    k = kv.double()[:, :128].view(n_pos, 4, 4, 32)[pos]  # (n_w, latent, head, dim)
+    v = kv.double()[:, 128:].view(n_pos, 4, 4, 32)[pos]
+    prob = torch.softmax(torch.einsum("whd,wjhd->whj", qd, k) / 32 ** 0.5, dim=-1)
+    o = torch.einsum("whj,wjhd->whd", prob, v).reshape(n_w, 128)
+    want = xd + o @ wo.double().t() + bo.double()
+    err = (got.double().cpu() - want).abs().max().item()
+    assert err <= 2e-2 * max(1.0, want.abs().max().item()), err
+    # an out-of-range position reads zero attention and is flagged
+    bad = pos.clone()
+    bad[7] = n_pos
+    got = d(x0.clone())
+    ops.latent_broadcast_residual(None, d(kv), d(bad), d(wo), d(bo), got, wq=d(wq), bq=d(bq))
+    with pytest.raises(ValueError):
+        ops.raise_on_device_error(device)
+    assert torch.equal(got[7].cpu(), (x0[7].float() + bo).to(H16))
+
+
 def test_latent_mix_matches_the_fp32_formulation(device):
     # the four latents of a position attend to each other (model.py:516-526)
     gen = _g(13)
