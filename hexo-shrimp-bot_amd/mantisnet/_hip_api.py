@@ -29,6 +29,8 @@ SIGNATURES = {
     "mantis_stable_key_count": ([vp, i64, i64, vp, vp, vp], i32),
     "mantis_stable_key_order": ([vp, vp, vp, i64, i64, vp, vp, vp, vp, vp], i32),
     "mantis_stable_key_order_noalloc": ([vp, vp, vp, i64, i64, vp, vp, vp, vp, vp], i32),
+    "mantis_latent_read_x_workspace": ([i64], i64),
+    "mantis_latent_read_x": ([vp, i64, vp, i64, vp, vp, i64, i64, vp, vp, vp, vp, vp, vp], i32),
     "mantis_latent_broadcast_residual": ([vp, i64, vp, i64, vp, i64, i64, vp, vp, vp, i64, vp, vp], i32),
     "mantis_latent_broadcast_project_residual": ([vp, vp, vp, i64, vp, i64, i64, vp, vp, vp, i64, vp, vp], i32),
     "mantis_covered_rows": ([vp, vp, i64, i64, vp, vp, i64, vp, vp, vp], i32),

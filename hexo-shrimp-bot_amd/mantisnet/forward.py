@@ -203,11 +203,22 @@ def _prepare(model, P) -> dict[str, Tensor]:
         wr_, br_ = _fold(P, pb + "latent_ln_read_w", [pb + "latent_wk_read", pb + "latent_wv_read"])
         wb_, bb_ = _fold(P, pb + "latent_ln_bcast_q", [pb + "latent_wq_bcast"])
         if cfg.cell_nodes:
-            # fp16 window state: the broadcast projects its queries itself
-            # from the rows it updates, so this launch is 384 wide
-            t[pb + "wproj.w"] = torch.cat([wv_, wr_]).contiguous()
-            t[pb + "wproj.b"] = torch.cat([bv_, br_]).contiguous()
+            # fp16 window state: the latent read takes the window rows
+            # themselves (its keys and values folded into composed queries and
+            # a value projection after the sum) and the broadcast projects its
+            # queries from the rows it updates, so this launch is 128 wide
+            t[pb + "wproj.w"], t[pb + "wproj.b"] = wv_, bv_
             t[pb + "bcast_q.w"], t[pb + "bcast_q.b"] = wb_, bb_
+            t[pb + "lread_v.w"], t[pb + "lread_v.b"] = wr_[128:].contiguous(), br_[128:].contiguous()
+            # composed queries: head a's Wk_a^T (Wq_a LN(g) + bq_a) / sqrt(32),
+            # Wk with the window LayerNorm's gain folded in (its bias term
+            # q . bk_a is the same for all of a position's windows)
+            wq32, bq32 = _fold32(P, pb + "latent_ln_read_q", [pb + "latent_wq_read"])
+            wk32 = _fold32(P, pb + "latent_ln_read_w", [pb + "latent_wk_read"])[0]
+            hd = 32
+            sl = [slice(hd * a, hd * (a + 1)) for a in range(128 // hd)]
+            t[pb + "lq_read_x.w"] = (torch.cat([wk32[h].t() @ wq32[h] for h in sl]) / hd ** 0.5).to(HALF).contiguous()
+            t[pb + "lq_read_x.b"] = (torch.cat([wk32[h].t() @ bq32[h] for h in sl]) / hd ** 0.5).contiguous()
         else:
             t[pb + "wproj.w"] = torch.cat([wv_, wr_, wb_]).contiguous()
             t[pb + "wproj.b"] = torch.cat([bv_, br_, bb_]).contiguous()
@@ -632,13 +643,18 @@ def _cell_pass(W, P, pb, plan: Plan, b: Batch, w):
 
 def _latent_cycle(W, P, pb, plan: Plan, w, g2, kv, qb):
     """kv: the windows' latent-read keys|values, qb: their broadcast queries
-    (both projected from w with the stones' values, see _block); qb is None
-    for the fp16 window state, whose broadcast projects the queries itself."""
+    (both projected from w with the stones' values, see _block); both are
+    None for the fp16 window state, whose read and broadcast take the window
+    rows themselves."""
     p = plan.n_pos
-    q = _proj(W, pb + "lq_read", g2)
     # (canonical batches: each position's windows are contiguous, no order)
-    read = ops.latent_read(q.view(p, 4, 4, 32), kv[:, :128], kv[:, 128:], plan.layout_offsets,
-                           None if plan.canonical else plan.layout_order)
+    order = None if plan.canonical else plan.layout_order
+    if kv is None:  # the fp16 window state: the read takes the rows themselves
+        qx = _proj(W, pb + "lq_read_x", g2)
+        read = ops.latent_read_x(qx, w, plan.layout_offsets, order, W[pb + "lread_v.w"], W[pb + "lread_v.b"])
+    else:
+        q = _proj(W, pb + "lq_read", g2)
+        read = ops.latent_read(q.view(p, 4, 4, 32), kv[:, :128], kv[:, 128:], plan.layout_offsets, order)
     _resid(W, pb + "lo_read", read.view(p * 4, 128), g2)
     # 4 x 4 latent self-mix, fp32 (all four slots live; model.py:516-526)
     ops.latent_mix(g2, W[pb + "mix_qkv.wt"], W[pb + "mix_qkv.b"], W[pb + "mix_o.wt"], W[pb + "mix_o.b"])
@@ -672,7 +688,7 @@ def _block(W, P, i: int, plan: Plan, b: Batch, sg, w, c, sw_all, update_stones: 
     # §5.2 stones <- windows: s += mlp_s(LN s, agg + class term); w does not
     # change again until the latent broadcast, so its latent-read keys/values
     # and broadcast queries are projected here in the same launch
-    wp = _proj(W, pb + "wproj", w)  # (n_w, 384 or 512): v | latent k | latent v [| broadcast q]
+    wp = _proj(W, pb + "wproj", w)  # (n_w, 128 or 512): v [| latent k | latent v | broadcast q]
     agg = ops.run_reduce(wp[:, :128], plan.run_window, plan.inc_stone_ptr, n_s, F32)
     FL(s, W[pb + "mlp_s1.w"], W[pb + "mlp_s1.b"], layer_norm=True, x2=agg, w2=W[pb + "mlp_s2.w"],
        add1=sw_all[:, 128 * i:128 * (i + 1)], relu=True, w3=W[pb + "mlp_s3.w"], b3=W[pb + "mlp_s3.b"],
@@ -694,7 +710,8 @@ def _block(W, P, i: int, plan: Plan, b: Batch, sg, w, c, sw_all, update_stones: 
         read = ops.latent_attend(qkv, b.attn_valid, p, max_t)
         _resid(W, pb + "attn_o", read, g2)
     # §5.4 latent cycle
-    _latent_cycle(W, P, pb, plan, w, g2, wp[:, 128:384], wp[:, 384:] if wp.shape[1] > 384 else None)
+    wide = wp.shape[1] > 128
+    _latent_cycle(W, P, pb, plan, w, g2, wp[:, 128:384] if wide else None, wp[:, 384:] if wide else None)
     # FFN over [stones; latents] (latents only in the last block)
     tgt = sg if update_stones else g2
     FL(tgt, W[pb + "ffn1.w"], W[pb + "ffn1.b"], layer_norm=True, relu=True, w3=W[pb + "ffn2.w"],

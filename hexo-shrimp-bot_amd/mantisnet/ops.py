@@ -1138,6 +1138,39 @@ def latent_read(q: Tensor, k: Tensor, v: Tensor, offsets: Tensor, order: Tensor 
     return (out, m, l) if stats else out
 
 
+def latent_read_x(qp: Tensor, x: Tensor, offsets: Tensor, order: Tensor | None, wv: Tensor, bv: Tensor) -> Tensor:
+    """The latent read from the fp16 window rows x (n_w, 128) themselves:
+    qp (4 P, 512) fp16 composed queries (head a's Wk_a^T q / sqrt(32) at
+    columns 128 a ..), wv (128, 128) fp16 / bv (128,) the value projection
+    (LayerNorm affine folded in); returns fp32 (P, 4, 128), see
+    mantis_latent_read_x.  order None: the windows of position p are rows
+    offsets[p] .. offsets[p+1]-1."""
+    dev = _on_gpu(qp, x, offsets, order, wv, bv)
+    if qp.dtype != torch.float16 or qp.ndim != 2 or qp.shape[1] != 512 or qp.shape[0] % 4 or qp.stride(1) != 1:
+        raise ValueError("qp must be fp16 (4 P, 512) rows")
+    if x.dtype != torch.float16 or x.ndim != 2 or x.shape[1] != 128 or x.stride(1) != 1:
+        raise ValueError("x must be fp16 (n_w, 128) rows")
+    if wv.dtype != torch.float16 or wv.shape != (128, 128) or not wv.is_contiguous() or bv.shape != (128,):
+        raise ValueError("wv must be a contiguous fp16 (128, 128) matrix and bv (128,)")
+    p, n_w = qp.shape[0] // 4, x.shape[0]
+    if offsets.numel() != p + 1 or (order is not None and order.numel() != n_w):
+        raise ValueError("offsets must be (P + 1,) and order (N_w,)")
+    offsets = _i64(offsets, "offsets")
+    order = None if order is None else _i64(order, "order")
+    bv = bv.float().contiguous()
+    out = torch.empty((p, 4, 128), dtype=torch.float32, device=dev)
+    if p:
+        ws = torch.empty(_lib().mantis_latent_read_x_workspace(p) // 4, dtype=torch.float32, device=dev)
+        # queries and outputs once, each window row and order entry once, the partial states twice
+        nbytes = p * 4 * (512 * 2 + 128 * 4) + n_w * (256 + (8 if order is not None else 0)) + 8 * (p + 1)
+        _launch("latent_read_x", nbytes, n_w * 16 * 128 * 2 * 2, lambda: _check(
+            _lib().mantis_latent_read_x(_ptr(qp), qp.stride(0), _ptr(x), x.stride(0), _ptr(offsets), _ptr(order), p,
+                                        n_w, _ptr(wv), _ptr(bv), _ptr(out), _ptr(ws), _ptr(error_flag(dev)),
+                                        _stream()),
+            "latent_read_x"))
+    return out
+
+
 def latent_broadcast(q: Tensor, k: Tensor, v: Tensor, window_pos: Tensor, stats: bool = False,
                      out_dtype: torch.dtype = torch.float32):
     """Every window attends over its position's four latents; q 128-wide

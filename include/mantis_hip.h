@@ -455,6 +455,29 @@ int32_t mantis_cell_heads(const void* c, int32_t c_dtype, int32_t layer_norm, in
                           void* stream);
 
 /*
+ * Latent read from the fp16 window rows themselves (the read of
+ * window_latents.py:295-349 in _window_latent_cycle, model.py:527-541, with
+ * its k and v projections folded): for position p, slot s and head a, over
+ * the windows w of p (rows offsets[p] .. offsets[p+1]-1 of x, or those rows
+ * of order when order is not NULL),
+ *   z_w    = (x_w - mean) / sqrt(var + 1e-5)           (fp32 statistics, fp16 z)
+ *   p_w    = softmax_w( qp[4p + s, 128a .. 128a+127] . z_w )
+ *   out[4p + s, 32a + d] = (sum_w p_w z_w) . wv[32a + d] + bv[32a + d]
+ * and 0 for a position without windows.  qp: (4 n_pos, >= 512) fp16 rows,
+ * stride ldq, the composed queries Wk_a^T q[s, a] / sqrt(32) of each head
+ * (Wk with the window LayerNorm's gain folded in; its bias term is the same
+ * for every window and cancels); x: (n_w, >= 128) fp16 rows, stride ldx; wv
+ * (128, 128) fp16 and bv (128) fp32 the value projection with the LayerNorm
+ * affine folded in; out (4 n_pos, 128) fp32.  workspace: at least
+ * mantis_latent_read_x_workspace(n_pos) bytes, 4-byte aligned.  order
+ * entries outside [0, n_w) read row 0 and set MANTIS_FLAG_INDEX.
+ */
+int64_t mantis_latent_read_x_workspace(int64_t n_pos);
+int32_t mantis_latent_read_x(const void* qp, int64_t ldq, const void* x, int64_t ldx, const int64_t* offsets,
+                             const int64_t* order, int64_t n_pos, int64_t n_w, const void* wv, const float* bv,
+                             float* out, float* workspace, int32_t* err_flag, void* stream);
+
+/*
  * Window <- latents broadcast fused with its output projection and residual,
  * in place on fp16 window rows x (n_w, 128), row stride ldx: for window r of
  * position p = window_pos[r] and head a (4 heads of 32 dims),

@@ -632,6 +632,63 @@ def test_latent_broadcast_projecting_its_queries_matches_the_separate_projection
     assert torch.equal(got[7].cpu(), (x0[7].float() + bo).to(H16))
 
 
+def test_latent_read_from_the_window_rows_matches_the_projected_read(device):
+    # keys and values folded: the read over LN(x) rows with composed queries
+    # and the value projection after the sum = the read over the projected
+    # k/v rows (fp64 formulation of the reference's steps), with and without
+    # a window order, positions without windows reading zero
+    gen = _g(35)
+    n_pos = 29
+    counts = torch.randint(0, 90, (n_pos,), generator=gen)
+    counts[[3, 17]] = 0
+    offsets = torch.cat([torch.zeros(1, dtype=torch.long), counts.cumsum(0)])
+    n_w = int(offsets[-1])
+    x = (0.4 + 2 * torch.randn(n_w, 128, generator=gen)).to(H16)
+    g_rows = torch.randn(4 * n_pos, 128, generator=gen)
+    wq, wk, wv = (torch.randn(128, 128, generator=gen) / math.sqrt(128) for _ in range(3))
+    bq, bk, bv = (0.1 * torch.randn(128, generator=gen) for _ in range(3))
+    gam, bet = 1 + 0.1 * torch.randn(128, generator=gen), 0.1 * torch.randn(128, generator=gen)
+    wk_f, wv_f = wk * gam, wv * gam  # the window LayerNorm's affine folded
+    bv_f = bv + wv @ bet
+    qd = (g_rows.double() - g_rows.double().mean(1, keepdim=True)) / torch.sqrt(
+        g_rows.double().var(1, unbiased=False, keepdim=True) + 1e-5)
+    q = qd @ wq.double().t() + bq.double()  # (4 P, 128): slot rows, head a at 32 a ..
+    hs = [slice(32 * a, 32 * (a + 1)) for a in range(4)]
+    qp = torch.cat([(q[:, h] @ wk_f.double()[h]) / 32 ** 0.5 for h in hs], 1)  # (4 P, 512)
+    z = (x.double() - x.double().mean(1, keepdim=True)) / torch.sqrt(x.double().var(1, unbiased=False, keepdim=True)
+                                                                    + 1e-5)
+    k = z @ wk_f.double().t() + (bk + wk @ bet).double()
+    v = z @ wv_f.double().t() + bv_f.double()
+    want = torch.zeros(n_pos, 4, 128, dtype=torch.float64)
+    for p in range(n_pos):
+        lo, hi = int(offsets[p]), int(offsets[p + 1])
+        if hi == lo:
+            continue
+        for a, h in enumerate(hs):
+            sc = q[4 * p:4 * p + 4, h] @ k[lo:hi, h].t() / 32 ** 0.5
+            want[p, :, h] = torch.softmax(sc, 1) @ v[lo:hi, h]
+    d = lambda t: t.to(device)  # noqa: E731
+    args = (d(wv_f.to(H16)), d(bv_f))
+    got = ops.latent_read_x(d(qp.to(H16)), d(x), d(offsets), None, *args)
+    ops.raise_on_device_error(device)
+    err = (got.double().cpu() - want).abs().max().item()
+    print({"err": err, "scale": want.abs().max().item()})
+    assert err <= 1e-2 * max(1.0, want.abs().max().item())
+    assert torch.equal(got[3].cpu(), torch.zeros(4, 128)) and torch.equal(got[17].cpu(), torch.zeros(4, 128))
+    # the same windows stored in another order, read through the order
+    perm = torch.randperm(n_w, generator=gen)
+    x2 = torch.empty_like(x)
+    x2[perm] = x
+    got2 = ops.latent_read_x(d(qp.to(H16)), d(x2), d(offsets), d(perm), *args)
+    ops.raise_on_device_error(device)
+    assert torch.equal(got2.cpu(), got.cpu())
+    bad = perm.clone()
+    bad[5] = n_w
+    ops.latent_read_x(d(qp.to(H16)), d(x2), d(offsets), d(bad), *args)
+    with pytest.raises(ValueError):
+        ops.raise_on_device_error(device)
+
+
 def test_latent_mix_matches_the_fp32_formulation(device):
     # the four latents of a position attend to each other (model.py:516-526)
     gen = _g(13)
