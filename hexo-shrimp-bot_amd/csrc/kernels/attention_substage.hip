@@ -345,113 +345,121 @@ __global__ void __launch_bounds__(waves_for<kStages>() * 64) attn_substage_kerne
       // the next tile's order word, after the tile's first loads (the counters
       // are in order: waiting for those does not wait for it)
       if (s == 0) row_n = order_at(next < t_end ? next : tile);
-      // ---- LayerNorm + Q projection
-      if constexpr (kPacked) {
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          const f16x8_t h = __builtin_bit_cast(f16x8_t, xh[ks]);
-#pragma unroll
-          for (int t = 0; t < 8; ++t) xv[ks][t] = float(h[t]);
-        }
-      }
-      uint32_t qh[16];
-      {
-        float sum = 0.f;
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-          for (int t = 0; t < 8; ++t) sum += xv[ks][t];
-        sum += __shfl_xor(sum, 16);
-        sum += __shfl_xor(sum, 32);
-        const float mean = sum * (1.f / kK);
-        float sq = 0.f;
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-          for (int t = 0; t < 8; ++t) {
-            const float d = xv[ks][t] - mean;
-            sq += d * d;
-          }
-        sq += __shfl_xor(sq, 16);
-        sq += __shfl_xor(sq, 32);
-        const float rstd = rsqrtf(sq * (1.f / kK) + 1e-5f);
-        // normalised values are bounded by sqrt(127): no saturation needed
-        f16x8_t xb[4];
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          uint4 w;
-          w.x = pack_f16x2_unit((xv[ks][0] - mean) * rstd, (xv[ks][1] - mean) * rstd);
-          w.y = pack_f16x2_unit((xv[ks][2] - mean) * rstd, (xv[ks][3] - mean) * rstd);
-          w.z = pack_f16x2_unit((xv[ks][4] - mean) * rstd, (xv[ks][5] - mean) * rstd);
-          w.w = pack_f16x2_unit((xv[ks][6] - mean) * rstd, (xv[ks][7] - mean) * rstd);
-          xb[ks] = __builtin_bit_cast(f16x8_t, w);
-        }
-#pragma unroll
-        for (int nt = 0; nt < 8; ++nt) {
-          f32x4_t d = {0.f, 0.f, 0.f, 0.f};
+      // A stage for which none of the tile's rows has entries adds only the
+      // output bias (its attention output is zero, so the products add
+      // exactly 0): the LayerNorm, both products and the lane exchanges are
+      // skipped, bitwise the same result.  Tiles of cells without decoder
+      // entries (about half of the cells) take this path in the first stage.
+      float acc[32];
+      float l = 0.f;
+      if (mc > 0) {
+        // ---- LayerNorm + Q projection
+        if constexpr (kPacked) {
 #pragma unroll
           for (int ks = 0; ks < 4; ++ks) {
-            const f16x8_t wf = *reinterpret_cast<const f16x8_t*>(swq + (16 * nt + l16) * kPitch + 32 * ks + 8 * g);
-            d = mfma16x16x32(wf, xb[ks], d);
+            const f16x8_t h = __builtin_bit_cast(f16x8_t, xh[ks]);
+#pragma unroll
+            for (int t = 0; t < 8; ++t) xv[ks][t] = float(h[t]);
           }
-          const float4 b = *reinterpret_cast<const float4*>(sbq + 32 * g + 4 * nt);
-          qh[2 * nt] = pack_f16x2(d[0] + b.x, d[1] + b.y);
-          qh[2 * nt + 1] = pack_f16x2(d[2] + b.z, d[3] + b.w);
         }
-      }
-      // ---- typed attention of head ag over row ar's entries
-      uint32_t qa[16];
+        uint32_t qh[16];
+        {
+          float sum = 0.f;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) qa[i] = uint32_t(from_lane(src_m, int32_t(qh[i])));
-      float acc[32];
+          for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-      for (int i = 0; i < 32; ++i) acc[i] = 0.f;
-      float m = -INFINITY, l = 0.f;
-      const float* sbias_s = sbias + a.bias_off[s] + ag * int32_t(S.n_classes);
-      // Rows are fetched by the lanes whose entry exists only; a lane that
-      // sits out keeps the last finite values it held and weighs them by 0.
-      uint4 kr[4], vr[4], cr[4];
+            for (int t = 0; t < 8; ++t) sum += xv[ks][t];
+          sum += __shfl_xor(sum, 16);
+          sum += __shfl_xor(sum, 32);
+          const float mean = sum * (1.f / kK);
+          float sq = 0.f;
 #pragma unroll
-      for (int w = 0; w < 4; ++w) kr[w] = vr[w] = cr[w] = make_uint4(0u, 0u, 0u, 0u);
-      for (int j = 0; j < mc; j += 4) {
-        if (j > 0) {  // this group's indices (loaded under the previous group's rows)
-          s4 = valid_src(es[s]);
-          c4 = valid_cls(ec[s]);
-        }
-        if (j + 4 < mc) {  // the next group's raw indices, under this group's rows
-          const int64_t e = j + 4 + ag < ac ? alo[s] + j + 4 + ag : 0;
-          es[s] = S.src[e];
-          ec[s] = S.cls[e];
-        }
-        auto step = [&](int u, int32_t src, int32_t cls) {
-          const bool in = j + u < ac;
-          const bool ok = in && src >= 0 && cls >= 0;
-          bad |= in && !ok;
-          float bs = 0.f;
-          if (ok) {
-            const uint32_t sr = uint32_t(src), cc = uint32_t(cls);
-            load_head(S.k + (sr * uint32_t(S.ldk) + uint32_t(8 * ag)), kr);
-            load_head(S.v + (sr * uint32_t(S.ldv) + uint32_t(8 * ag)), vr);
-            if constexpr (kVcls) load_head(S.vcls + (cc * uint32_t(kK) + uint32_t(8 * ag)), cr);
-            bs = sbias_s[cls];
+          for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+              const float d = xv[ks][t] - mean;
+              sq += d * d;
+            }
+          sq += __shfl_xor(sq, 16);
+          sq += __shfl_xor(sq, 32);
+          const float rstd = rsqrtf(sq * (1.f / kK) + 1e-5f);
+          // normalised values are bounded by sqrt(127): no saturation needed
+          f16x8_t xb[4];
+#pragma unroll
+          for (int ks = 0; ks < 4; ++ks) {
+            uint4 w;
+            w.x = pack_f16x2_unit((xv[ks][0] - mean) * rstd, (xv[ks][1] - mean) * rstd);
+            w.y = pack_f16x2_unit((xv[ks][2] - mean) * rstd, (xv[ks][3] - mean) * rstd);
+            w.z = pack_f16x2_unit((xv[ks][4] - mean) * rstd, (xv[ks][5] - mean) * rstd);
+            w.w = pack_f16x2_unit((xv[ks][6] - mean) * rstd, (xv[ks][7] - mean) * rstd);
+            xb[ks] = __builtin_bit_cast(f16x8_t, w);
           }
-          const float sc = ok ? fmaf(dot32(qa, kr), a.scale, bs) : -INFINITY;
-          if (sc > m + kTau) {  // a new reference point (always on a row's first entry)
-            const float alpha = __expf(m - sc);
-            l *= alpha;
 #pragma unroll
-            for (int i = 0; i < 32; ++i) acc[i] *= alpha;
-            m = sc;
+          for (int nt = 0; nt < 8; ++nt) {
+            f32x4_t d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+              const f16x8_t wf = *reinterpret_cast<const f16x8_t*>(swq + (16 * nt + l16) * kPitch + 32 * ks + 8 * g);
+              d = mfma16x16x32(wf, xb[ks], d);
+            }
+            const float4 b = *reinterpret_cast<const float4*>(sbq + 32 * g + 4 * nt);
+            qh[2 * nt] = pack_f16x2(d[0] + b.x, d[1] + b.y);
+            qh[2 * nt + 1] = pack_f16x2(d[2] + b.z, d[3] + b.w);
           }
-          const float pr = ok ? __expf(sc - m) : 0.f;
-          l += pr;
-          axpy32(acc, pr, vr);
-          if constexpr (kVcls) axpy32(acc, pr, cr);
-        };
-        step(0, from_quad<0>(s4), from_quad<0>(c4));
-        if (j + 1 < mc) step(1, from_quad<1>(s4), from_quad<1>(c4));
-        if (j + 2 < mc) step(2, from_quad<2>(s4), from_quad<2>(c4));
-        if (j + 3 < mc) step(3, from_quad<3>(s4), from_quad<3>(c4));
+        }
+        // ---- typed attention of head ag over row ar's entries
+        uint32_t qa[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) qa[i] = uint32_t(from_lane(src_m, int32_t(qh[i])));
+#pragma unroll
+        for (int i = 0; i < 32; ++i) acc[i] = 0.f;
+        float m = -INFINITY;
+        const float* sbias_s = sbias + a.bias_off[s] + ag * int32_t(S.n_classes);
+        // Rows are fetched by the lanes whose entry exists only; a lane that
+        // sits out keeps the last finite values it held and weighs them by 0.
+        uint4 kr[4], vr[4], cr[4];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) kr[w] = vr[w] = cr[w] = make_uint4(0u, 0u, 0u, 0u);
+        for (int j = 0; j < mc; j += 4) {
+          if (j > 0) {  // this group's indices (loaded under the previous group's rows)
+            s4 = valid_src(es[s]);
+            c4 = valid_cls(ec[s]);
+          }
+          if (j + 4 < mc) {  // the next group's raw indices, under this group's rows
+            const int64_t e = j + 4 + ag < ac ? alo[s] + j + 4 + ag : 0;
+            es[s] = S.src[e];
+            ec[s] = S.cls[e];
+          }
+          auto step = [&](int u, int32_t src, int32_t cls) {
+            const bool in = j + u < ac;
+            const bool ok = in && src >= 0 && cls >= 0;
+            bad |= in && !ok;
+            float bs = 0.f;
+            if (ok) {
+              const uint32_t sr = uint32_t(src), cc = uint32_t(cls);
+              load_head(S.k + (sr * uint32_t(S.ldk) + uint32_t(8 * ag)), kr);
+              load_head(S.v + (sr * uint32_t(S.ldv) + uint32_t(8 * ag)), vr);
+              if constexpr (kVcls) load_head(S.vcls + (cc * uint32_t(kK) + uint32_t(8 * ag)), cr);
+              bs = sbias_s[cls];
+            }
+            const float sc = ok ? fmaf(dot32(qa, kr), a.scale, bs) : -INFINITY;
+            if (sc > m + kTau) {  // a new reference point (always on a row's first entry)
+              const float alpha = __expf(m - sc);
+              l *= alpha;
+#pragma unroll
+              for (int i = 0; i < 32; ++i) acc[i] *= alpha;
+              m = sc;
+            }
+            const float pr = ok ? __expf(sc - m) : 0.f;
+            l += pr;
+            axpy32(acc, pr, vr);
+            if constexpr (kVcls) axpy32(acc, pr, cr);
+          };
+          step(0, from_quad<0>(s4), from_quad<0>(c4));
+          if (j + 1 < mc) step(1, from_quad<1>(s4), from_quad<1>(c4));
+          if (j + 2 < mc) step(2, from_quad<2>(s4), from_quad<2>(c4));
+          if (j + 3 < mc) step(3, from_quad<3>(s4), from_quad<3>(c4));
+        }
       }
       if (s == kStages - 1) {  // the next tile's bounds
         const int64_t rcn = clamp_row(row_n);
@@ -462,7 +470,24 @@ __global__ void __launch_bounds__(waves_for<kStages>() * 64) attn_substage_kerne
         }
       }
       // ---- output projection + residual, into the x registers
-      {
+      if (mc == 0) {
+#pragma unroll
+        for (int nt = 0; nt < 8; ++nt) {
+          const float4 b = *reinterpret_cast<const float4*>(sbo + 32 * (nt >> 1) + 8 * g + 4 * (nt & 1));
+          if constexpr (kPacked) {
+            uint32_t* w = reinterpret_cast<uint32_t*>(&xh[nt >> 1]) + 2 * (nt & 1);
+            const f16x2_t h0 = __builtin_bit_cast(f16x2_t, w[0]), h1 = __builtin_bit_cast(f16x2_t, w[1]);
+            w[0] = pack_f16x2(float(h0[0]) + (0.f + b.x), float(h0[1]) + (0.f + b.y));
+            w[1] = pack_f16x2(float(h1[0]) + (0.f + b.z), float(h1[1]) + (0.f + b.w));
+          } else {
+            float* xr = xv[nt >> 1] + 4 * (nt & 1);
+            xr[0] += 0.f + b.x;
+            xr[1] += 0.f + b.y;
+            xr[2] += 0.f + b.z;
+            xr[3] += 0.f + b.w;
+          }
+        }
+      } else {
         const float inv = l > 0.f ? 1.f / l : 1.f;
         f16x8_t ab[4];
 #pragma unroll
