@@ -123,6 +123,14 @@ struct SubArgs {
   float scale;
   int32_t* flag;
   uint32_t* counters;  // per XCD (128 bytes apart): next tile, then wavefronts done
+  // the rows' initial state, when not null: row r starts from x_init row
+  // init_cover if the first stage's run of r is non-empty, else from x_init
+  // row init_idx[r] (out of [0, n_init): a zero row, flagged); x is written only
+  const void* x_init;
+  int64_t ld_init;
+  int64_t n_init;
+  const int64_t* init_idx;
+  int64_t init_cover;
 };
 
 // the value v of lane 4 (lane / 4) + u (one DPP quad broadcast)
@@ -259,6 +267,9 @@ __global__ void __launch_bounds__(waves_for<kStages>() * 64) attn_substage_kerne
   // is loaded again, so no copy ever waits for a load.
   int32_t row_n = tile0 < t_end ? order_at(tile0) : 0;
   int64_t pa_n[kStages], pb_n[kStages];
+  // the row's initial-state index (with x_init), loaded with its bounds
+  const int64_t* init_idx = a.init_idx ? a.init_idx : a.st[0].seg_ptr;
+  int64_t ii_n;
   {
     const int64_t rc = clamp_row(row_n);
 #pragma unroll
@@ -266,6 +277,7 @@ __global__ void __launch_bounds__(waves_for<kStages>() * 64) attn_substage_kerne
       pa_n[s] = a.st[s].seg_ptr[rc];
       pb_n[s] = a.st[s].seg_ptr[rc + 1];
     }
+    ii_n = init_idx[rc];
   }
   int64_t next = tile0;
   for (int64_t tile = tile0; tile < t_end; tile = next) {
@@ -288,18 +300,36 @@ __global__ void __launch_bounds__(waves_for<kStages>() * 64) attn_substage_kerne
     const int64_t rc = live ? row : 0;  // dead lanes read a real row and store nothing
     // the row state: fp32 rows stay fp32 in registers across the stages;
     // fp16 rows stay packed (half the registers) and are rounded after each
-    // stage, exactly as a launch per stage would leave them
+    // stage, exactly as a launch per stage would leave them.  With x_init the
+    // state starts from a row of that table instead (a zero row for an index
+    // out of range)
+    const TX* xsrc = xs + rc * a.ldx;
+    bool init_zero = false;
+    if (a.x_init) {
+      const int64_t ir = hi[0] > lo[0] ? a.init_cover : ii_n;
+      const bool ok = ir >= 0 && ir < a.n_init;
+      bad |= live && !ok;
+      init_zero = !ok;
+      xsrc = static_cast<const TX*>(a.x_init) + (ok ? ir : 0) * a.ld_init;
+    }
     constexpr bool kPacked = sizeof(TX) == 2;
     float xv[4][8];
     uint4 xh[kPacked ? 4 : 1];
     if constexpr (kPacked) {
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
+      for (int ks = 0; ks < 4; ++ks) {
         xh[ks] = __builtin_bit_cast(uint4, __builtin_nontemporal_load(
-                                               reinterpret_cast<const nt_f16x8_t*>(xs + rc * a.ldx + 32 * ks + 8 * g)));
+                                               reinterpret_cast<const nt_f16x8_t*>(xsrc + 32 * ks + 8 * g)));
+        if (init_zero) xh[ks] = make_uint4(0u, 0u, 0u, 0u);
+      }
     } else {
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) load8_nt(xs + rc * a.ldx + 32 * ks + 8 * g, xv[ks]);
+      for (int ks = 0; ks < 4; ++ks) {
+        load8_nt(xsrc + 32 * ks + 8 * g, xv[ks]);
+        if (init_zero)
+#pragma unroll
+          for (int t = 0; t < 8; ++t) xv[ks][t] = 0.f;
+      }
     }
     // Per stage: the entry count of this lane's row and the wavefront's
     // longest row; the attention runs with lane 4 r + g on (row r, head g)
@@ -468,6 +498,7 @@ __global__ void __launch_bounds__(waves_for<kStages>() * 64) attn_substage_kerne
           pa_n[t] = a.st[t].seg_ptr[rcn];
           pb_n[t] = a.st[t].seg_ptr[rcn + 1];
         }
+        ii_n = init_idx[rcn];
       }
       // ---- output projection + residual, into the x registers
       if (mc == 0) {
@@ -592,10 +623,19 @@ Stage to_stage(const mantis_substage& d) {
 
 using namespace mantis;
 
-extern "C" int32_t mantis_attention_substages(void* x, int32_t x_dtype, int64_t ldx, int64_t n_rows,
-                                              const int32_t* row_order, const mantis_substage* stages,
-                                              int32_t n_stages, int32_t* err_flag, uint32_t* tile_counters,
-                                              void* stream) {
+namespace {
+
+struct InitRows {
+  const void* x;
+  int64_t ld;
+  int64_t n;
+  const int64_t* idx;
+  int64_t cover_row;
+};
+
+int32_t substages(void* x, int32_t x_dtype, int64_t ldx, int64_t n_rows, const int32_t* row_order,
+                  const mantis_substage* stages, int32_t n_stages, const InitRows* init, int32_t* err_flag,
+                  uint32_t* tile_counters, void* stream) {
   if (n_rows < 0 || !stages || n_stages < 1 || n_stages > 2) return MANTIS_E_ARG;
   if (n_rows == 0) return MANTIS_OK;
   for (int s = 0; s < n_stages; ++s)
@@ -611,6 +651,11 @@ extern "C" int32_t mantis_attention_substages(void* x, int32_t x_dtype, int64_t 
   a.ldx = ldx;
   a.n_rows = n_rows;
   a.order = row_order;
+  a.x_init = init ? init->x : nullptr;
+  a.ld_init = init ? init->ld : 0;
+  a.n_init = init ? init->n : 0;
+  a.init_idx = init ? init->idx : nullptr;
+  a.init_cover = init ? init->cover_row : 0;
   int64_t pool = 0;
   for (int s = 0; s < n_stages; ++s) {
     a.st[s] = to_stage(stages[s]);
@@ -631,6 +676,27 @@ extern "C" int32_t mantis_attention_substages(void* x, int32_t x_dtype, int64_t 
   }
   if (n_stages == 2) return vc ? launch<2, true, float>(a, stream) : launch<2, false, float>(a, stream);
   return vc ? launch<1, true, float>(a, stream) : launch<1, false, float>(a, stream);
+}
+
+}  // namespace
+
+extern "C" int32_t mantis_attention_substages(void* x, int32_t x_dtype, int64_t ldx, int64_t n_rows,
+                                              const int32_t* row_order, const mantis_substage* stages,
+                                              int32_t n_stages, int32_t* err_flag, uint32_t* tile_counters,
+                                              void* stream) {
+  return substages(x, x_dtype, ldx, n_rows, row_order, stages, n_stages, nullptr, err_flag, tile_counters, stream);
+}
+
+extern "C" int32_t mantis_attention_substages_init(void* x, int32_t x_dtype, int64_t ldx, int64_t n_rows,
+                                                   const int32_t* row_order, const mantis_substage* stages,
+                                                   int32_t n_stages, const void* x_init, int64_t ld_init,
+                                                   int64_t n_init, const int64_t* init_idx, int64_t init_cover,
+                                                   int32_t* err_flag, uint32_t* tile_counters, void* stream) {
+  if (!x_init || !init_idx || n_init <= 0 || init_cover < 0 || init_cover >= n_init || !aligned16(x_init) ||
+      ld_init < kK || ld_init % (x_dtype == MANTIS_F16 ? 8 : 4) || x_init == x)
+    return MANTIS_E_ARG;
+  const InitRows init{x_init, ld_init, n_init, init_idx, init_cover};
+  return substages(x, x_dtype, ldx, n_rows, row_order, stages, n_stages, &init, err_flag, tile_counters, stream);
 }
 
 extern "C" int32_t mantis_attention_substage(float* x, int64_t ldx, int64_t n_rows, const void* wq, const float* bq,

@@ -60,6 +60,7 @@ SIGNATURES = {
     "mantis_attention_substage": (
         [vp, i64, i64, vp, vp, vp, vp, i64, i64, i64, vp, i64, vp, vp, vp, vp, i64, vp, vp, vp, vp], i32),
     "mantis_attention_substages": ([vp, i32, i64, i64, vp, vp, i32, vp, vp, vp], i32),
+    "mantis_attention_substages_init": ([vp, i32, i64, i64, vp, vp, i32, vp, i64, i64, vp, i64, vp, vp, vp], i32),
     "mantis_cell_heads": (
         [vp, i32, i32, i32, i64, i64, vp, vp, vp, vp, vp, vp, vp, i64, vp, i64, vp, vp, vp, i64, vp, i64, vp, vp, vp, vp, vp,
          i64, vp, vp, vp, vp], i32),

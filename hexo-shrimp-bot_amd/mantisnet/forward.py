@@ -602,7 +602,7 @@ def _substage(W, P, pb, key, kv, bias, vcls, ptr, src, cls) -> ops.SubStage:
                         W[pb + key + "_o.w"], W[pb + key + "_o.b"])
 
 
-def _cell_stage(W, P, pb, plan: Plan, s, w, c):
+def _cell_stage(W, P, pb, plan: Plan, s, w, c, c_init=None):
     # cells <- windows (decoder classes, class values) then cells <- stones
     # (radius classes, class values): one fused pass over the cell rows, the
     # rows staying on chip between the two sub-stages; then windows <- cells
@@ -611,7 +611,9 @@ def _cell_stage(W, P, pb, plan: Plan, s, w, c):
                    plan.edge_window, plan.edge_class)
     rad = _substage(W, P, pb, "rad", _proj(W, pb + "rad_kv", s), "radius_bias", W[pb + "rad_vcls"],
                     plan.radius_ptr, plan.radius_src, plan.radius_class)
-    ops.attention_substages(c, [cr, rad], row_order=plan.cell_order)
+    # c_init: (table, index, cover row) of the cells' initial state, read by
+    # the first pass in place of c (which it then writes)
+    ops.attention_substages(c, [cr, rad], row_order=plan.cell_order, init=c_init)
     if plan.cov_rows is not None:  # k/v of the covered cells only, entries remapped to them
         wr = _substage(W, P, pb, "wr", _proj(W, pb + "wr_kv", c, x_rows=plan.cov_rows), "wr_bias", None,
                        plan.win_ptr, plan.edge_wcell_cov, plan.edge_wclass)
@@ -669,7 +671,7 @@ def _latent_cycle(W, P, pb, plan: Plan, w, g2, kv, qb):
         _resid(W, pb + "lo_bcast", out.view(plan.n_w, 128), w)
 
 
-def _block(W, P, i: int, plan: Plan, b: Batch, sg, w, c, sw_all, update_stones: bool):
+def _block(W, P, i: int, plan: Plan, b: Batch, sg, w, c, sw_all, update_stones: bool, c_init=None):
     pb = f"blocks.{i}."
     p, max_t, n_s = plan.n_pos, plan.max_t, plan.n_s
     s = sg[:n_s]
@@ -682,7 +684,7 @@ def _block(W, P, i: int, plan: Plan, b: Batch, sg, w, c, sw_all, update_stones: 
        out=w, residual=True)
     # §5.1b cell stage, or the knob-off cell pass
     if c is not None:
-        _cell_stage(W, P, pb, plan, s, w, c)
+        _cell_stage(W, P, pb, plan, s, w, c, c_init)
     else:
         _cell_pass(W, P, pb, plan, b, w)
     # §5.2 stones <- windows: s += mlp_s(LN s, agg + class term); w does not
@@ -749,18 +751,23 @@ def _trunk(model, b: Batch, plan: Plan, raw_cells: bool = False, W: Prepared | N
     # gather is the forward's first large launch: the plan's small kernels
     # and the host's work to queue them follow it
     w = ops.gather_rows(W["window_table"], b.window_feat)
-    c = None
+    c = c_init = None
     if cfg.cell_nodes:
         # covered cells start from cell_base, the others from their nearest-stone
-        # row: one gather from the table [nearest rows; cell_base] (the decoder
-        # CSR tells the covered cells).  The cell state is stored in fp16
-        # (866 MB -> 433 MB per pass at 1.69M cells): every kernel that updates
-        # it keeps the rows in fp32 registers and rounds once on the store, and
-        # its readers feed fp16 MFMA operands.  Queued second: with the two
-        # gathers in the queue, the device has work while the host queues the
-        # small launches below
+        # row of the table [nearest rows; cell_base] (the decoder CSR tells the
+        # covered cells).  The cell state is stored in fp16 (866 MB -> 433 MB
+        # per pass at 1.69M cells): every kernel that updates it keeps the rows
+        # in fp32 registers and rounds once on the store, and its readers feed
+        # fp16 MFMA operands
         table = W["cell_table"]
-        c = ops.gather_rows(table, b.cell_nearest, cover_ptr=plan.cell_ptr, cover_row=table.shape[0] - 1)
+        if cfg.blocks:
+            # the first cell pass reads its rows' initial state from the table
+            # (a few KB, cached) instead of a gathered copy: the state's first
+            # write is that pass's
+            c = torch.empty((plan.n_c, 128), dtype=table.dtype, device=table.device)
+            c_init = (table, b.cell_nearest, table.shape[0] - 1)
+        else:
+            c = ops.gather_rows(table, b.cell_nearest, cover_ptr=plan.cell_ptr, cover_row=table.shape[0] - 1)
     plan.start()
     # residual streams: s and g share one buffer so the attention and FFN
     # launches cover both with one row range
@@ -770,7 +777,7 @@ def _trunk(model, b: Batch, plan: Plan, raw_cells: bool = False, W: Prepared | N
               out=sg[n_s:].view(p, GLOBAL_ROWS, 128))
     sw_all = ops.run_reduce(W["sw_all"], plan.run_class, plan.inc_stone_ptr, n_s, F32)
     for i in range(cfg.blocks):
-        _block(W, P, i, plan, b, sg, w, c, sw_all, i + 1 < cfg.blocks)
+        _block(W, P, i, plan, b, sg, w, c, sw_all, i + 1 < cfg.blocks, c_init if i == 0 else None)
     g = sg[n_s:].view(p, GLOBAL_ROWS, 128)
     w_out = w if raw_windows and w.dtype == HALF else ops.layer_norm(w, P["ln_out.weight"], P["ln_out.bias"], F32)
     g_out = F.layer_norm(g, (128,), P["ln_out.weight"], P["ln_out.bias"], 1e-5).mean(dim=1)

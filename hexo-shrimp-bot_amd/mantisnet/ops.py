@@ -935,7 +935,7 @@ def _substage_struct(st: SubStage, n: int):
 
 
 def attention_substages(x: Tensor, stages: list[SubStage], row_order: Tensor | None = None,
-                        library_counters: bool = False) -> Tensor:
+                        library_counters: bool = False, init: tuple[Tensor, Tensor, int] | None = None) -> Tensor:
     """In place on the fp32 residual rows x (n, 128), for each stage in order:
     x += fp16(attend(fp16(LN(x) wq^T + bq))) wo^T + bo, the attention typed
     by (bias, vcls) over the stage's CSR entries with k/v the two halves of
@@ -945,10 +945,24 @@ def attention_substages(x: Tensor, stages: list[SubStage], row_order: Tensor | N
     16-row tiles in; the results do not depend on it.  The tiles are handed
     out from the stream's tile counters (tile_counters), or with
     ``library_counters`` from the library's per-device set, which launches
-    running at the same time on one device would share."""
+    running at the same time on one device would share.  ``init`` =
+    (table, idx, cover_row): the rows start from table[cover_row] where the
+    first stage's run is non-empty, else from table[idx[r]] (x is only
+    written; see mantis_attention_substages_init)."""
     if not 1 <= len(stages) <= 2:
         raise ValueError("one or two stages per launch")
-    dev = _on_gpu(x, row_order, *[t for st in stages for t in st])
+    dev = _on_gpu(x, row_order, *[t for st in stages for t in st], *(init[:2] if init is not None else ()))
+    if init is not None:
+        table, idx, cover_row = init
+        if table.dtype != x.dtype or table.ndim != 2 or table.shape[1] != 128 or table.stride(1) != 1:
+            raise ValueError("the initial-state table must be (n, 128) rows of x's dtype")
+        if not 0 <= cover_row < table.shape[0]:
+            raise ValueError("cover_row is not a row of the initial-state table")
+        idx = _i64(idx, "init idx")
+        if idx.shape != (x.shape[0],):
+            raise ValueError("the initial-state index must have one entry per row")
+        if table.data_ptr() == x.data_ptr():
+            raise ValueError("the initial-state table must not be x")
     if row_order is not None:
         if row_order.dtype != torch.int32 or row_order.shape != (x.shape[0],):
             raise ValueError("row_order must be an int32 permutation of the rows")
@@ -963,19 +977,29 @@ def attention_substages(x: Tensor, stages: list[SubStage], row_order: Tensor | N
         arr = (_hip_api.MantisSubstage * len(built))(*[d for d, _, _ in built])
         # x read and written once; per stage the CSR pointers and entry
         # indices once and each source's k and v rows once
-        nbytes = n * 128 * x.element_size() * 2 + sum(n * 8 + e * 16 + st.kv.shape[0] * 256 * 2 for st, (_, _, e) in
-                                       zip(stages, built))
+        x_bytes = n * 128 * x.element_size() * (2 if init is None else 1) + (n * 8 if init is not None else 0)
+        nbytes = x_bytes + sum(n * 8 + e * 16 + st.kv.shape[0] * 256 * 2 for st, (_, _, e) in zip(stages, built))
         flops = sum(2 * n * 128 * 128 * 2 + e * 4 * 128 * 2 for _, _, e in built)
         kind = "vcls" if stages[0].vcls is not None else "plain"
         name = f"attention_substage_{kind}" if len(stages) == 1 else f"attention_substages{len(stages)}_{kind}"
         if x.dtype == torch.float16:
             name += "_f16"
-        _launch(name, nbytes, flops, lambda: _check(
-            _lib().mantis_attention_substages(_ptr(x), _dt(x), x.stride(0), n, _ptr(row_order),
-                                              ctypes.cast(arr, ctypes.c_void_p), len(built), _ptr(error_flag(dev)),
-                                              None if library_counters else _ptr(tile_counters(dev)), _stream()),
-            "attention_substages",
-        ))
+        counters = None if library_counters else _ptr(tile_counters(dev))
+        if init is None:
+            _launch(name, nbytes, flops, lambda: _check(
+                _lib().mantis_attention_substages(_ptr(x), _dt(x), x.stride(0), n, _ptr(row_order),
+                                                  ctypes.cast(arr, ctypes.c_void_p), len(built),
+                                                  _ptr(error_flag(dev)), counters, _stream()),
+                "attention_substages",
+            ))
+        else:
+            _launch(name, nbytes, flops, lambda: _check(
+                _lib().mantis_attention_substages_init(_ptr(x), _dt(x), x.stride(0), n, _ptr(row_order),
+                                                       ctypes.cast(arr, ctypes.c_void_p), len(built), _ptr(table),
+                                                       table.stride(0), table.shape[0], _ptr(idx), cover_row,
+                                                       _ptr(error_flag(dev)), counters, _stream()),
+                "attention_substages_init",
+            ))
     return x
 
 

@@ -418,6 +418,23 @@ int32_t mantis_attention_substages(void* x, int32_t x_dtype, int64_t ldx, int64_
                                    uint32_t* tile_counters, void* stream);
 
 /*
+ * mantis_attention_substages with the rows' initial state taken from a
+ * table instead of x: row r starts from x_init row init_cover when the first
+ * stage's run of r is non-empty (seg_ptr[r + 1] > seg_ptr[r]), else from
+ * x_init row init_idx[r] (an index outside [0, n_init) starts from a zero row
+ * and sets MANTIS_FLAG_INDEX); x (n_rows rows) is only written.  x_init has
+ * x's dtype, row stride ld_init, and must not be x.  The first cell stage of
+ * the forward starts from the initial cell state this way (the gather
+ * [cell_nearest rows; cell_base][...] of model.py:843-859, which
+ * mantis_gather_rows with cover_ptr also forms) without writing it first.
+ */
+int32_t mantis_attention_substages_init(void* x, int32_t x_dtype, int64_t ldx, int64_t n_rows,
+                                        const int32_t* row_order, const mantis_substage* stages, int32_t n_stages,
+                                        const void* x_init, int64_t ld_init, int64_t n_init, const int64_t* init_idx,
+                                        int64_t init_cover, int32_t* err_flag, uint32_t* tile_counters,
+                                        void* stream);
+
+/*
  * Fused cell heads: for every legal cell r (position cell_pos[r]) with
  * decoder entries e in [dec_ptr[r], dec_ptr[r+1]):
  *   x    = fp16(LN(c[r])) if layer_norm (no affine: fold it into w1/b1), else fp16(c[r])

@@ -383,6 +383,40 @@ def test_tile_counters_are_left_zero_and_the_library_set_gives_the_same_rows(dev
     assert int(torch.count_nonzero(ops.tile_counters(device))) == 0
 
 
+def test_substages_starting_from_an_initial_state_table(device):
+    # rows that start from a table row (cover row where the first stage's run
+    # is non-empty, else the row's index) give bitwise the pass over the
+    # gathered rows, fp16 and fp32 rows, in a row order; x is only written.
+    # An index out of range starts from a zero row and is flagged.
+    gen = _g(17)
+    n = 30011
+    st1 = _random_stage(gen, n, 301, 726, True, 7)
+    st2 = _random_stage(gen, n, 57, 192, True, 11)
+    dev = lambda st: ops.SubStage(*[None if t is None else t.to(device) for t in st])  # noqa: E731
+    s1, s2 = dev(st1), dev(st2)
+    order = torch.randperm(n, generator=gen).to(torch.int32).to(device)
+    idx = torch.randint(0, 9, (n,), generator=gen)
+    for dtype in (H16, torch.float32):
+        table = (2 * torch.randn(10, 128, generator=gen) - 0.3).to(dtype).to(device)
+        ref = ops.gather_rows(table, idx.to(device), cover_ptr=s1.seg_ptr, cover_row=9)
+        ops.attention_substages(ref, [s1, s2], row_order=order)
+        got = torch.full((n, 128), float("nan"), dtype=dtype, device=device)
+        ops.attention_substages(got, [s1, s2], row_order=order, init=(table, idx.to(device), 9))
+        ops.raise_on_device_error(device)
+        assert torch.equal(got.cpu(), ref.cpu())
+    bad = idx.clone()
+    uncovered = torch.nonzero(st1.seg_ptr[1:] == st1.seg_ptr[:-1])[0, 0].item()
+    bad[uncovered] = 10
+    got = torch.empty((n, 128), dtype=torch.float32, device=device)
+    ops.attention_substages(got, [s1, s2], init=(table, bad.to(device), 9))
+    with pytest.raises(ValueError):
+        ops.raise_on_device_error(device)
+    zero = torch.zeros((n, 128), dtype=torch.float32, device=device)
+    ops.attention_substages(zero, [s1, s2])
+    ops.raise_on_device_error(device)
+    assert torch.equal(got[uncovered].cpu(), zero[uncovered].cpu())
+
+
 def test_row_order_changes_the_tiles_not_the_results(device):
     # the rows visited in a random permutation (and in an order sorted by
     # entry count) give bitwise the natural order's results; an order entry
