@@ -545,6 +545,13 @@ extern "C" int32_t mantis_fused_linear(const void* x, int32_t x_dtype, int64_t l
   if (!x || !w1 || !out || m < 0 || n_x < 0) return MANTIS_E_ARG;
   if ((x2 == nullptr) != (w2 == nullptr) || (w3 == nullptr) != (n3 == 0)) return MANTIS_E_ARG;
   if (add2 && !add2_rows) return MANTIS_E_ARG;
+  // mode 4: mode 3 with the rows added to taken from x (the row each output
+  // row reads, x[x_rows[r]] or x[r]) instead of out; the fp16 pair MLP only
+  const bool seed = out_mode == 4;
+  if (seed) {
+    if (x == out || x_dtype != MANTIS_F16 || !w3 || !x2) return MANTIS_E_ARG;
+    out_mode = 3;
+  }
   const int width = w3 ? n3 : n1;
   if (ldx % 8 || (x2 && ldx2 % 8) || ldo % 4 || ldo < width || ldx < kK || (add1 && ld_add1 % 4))
     return MANTIS_E_ARG;
@@ -560,7 +567,7 @@ extern "C" int32_t mantis_fused_linear(const void* x, int32_t x_dtype, int64_t l
   Args a{x, ldx, x_rows, x_rows ? n_x : m, m, x2, ldx2, static_cast<const _Float16*>(w1),
          static_cast<const _Float16*>(w2), b1, add1, ld_add1, add2, add2_rows, n_add2,
          static_cast<const _Float16*>(w3), b3, n3, out, ldo, err_flag,
-         int32_t(out == x && !x_rows && ldo == ldx)};
+         int32_t(seed || (out == x && !x_rows && ldo == ldx))};
   hipStream_t s = as_stream(stream);
   const bool ln = layer_norm != 0, r = relu != 0, st2 = w3 != nullptr, hx2 = x2 != nullptr;
   const int mode = out_mode;

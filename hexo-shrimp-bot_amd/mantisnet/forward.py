@@ -671,7 +671,7 @@ def _latent_cycle(W, P, pb, plan: Plan, w, g2, kv, qb):
         _resid(W, pb + "lo_bcast", out.view(plan.n_w, 128), w)
 
 
-def _block(W, P, i: int, plan: Plan, b: Batch, sg, w, c, sw_all, update_stones: bool, c_init=None):
+def _block(W, P, i: int, plan: Plan, b: Batch, sg, w, c, sw_all, update_stones: bool, c_init=None, w_init=None):
     pb = f"blocks.{i}."
     p, max_t, n_s = plan.n_pos, plan.max_t, plan.n_s
     s = sg[:n_s]
@@ -679,9 +679,12 @@ def _block(W, P, i: int, plan: Plan, b: Batch, sg, w, c, sw_all, update_stones: 
     # §5.1 windows <- stones: w += mlp_w(LN w, agg + class term)
     x = _proj(W, pb + "u", s)
     agg = ops.run_reduce(x, b.inc_stone, plan.inc_win_ptr, plan.n_w, HALF)
-    FL(w, W[pb + "mlp_w1.w"], W[pb + "mlp_w1.b"], layer_norm=True, x2=agg, w2=W[pb + "mlp_w2.w"],
+    # w_init: (table, rows) of the windows' initial state, read by the first
+    # block's MLP in place of w (which it then writes)
+    src, rows = (w, None) if w_init is None else w_init
+    FL(src, W[pb + "mlp_w1.w"], W[pb + "mlp_w1.b"], layer_norm=True, x_rows=rows, x2=agg, w2=W[pb + "mlp_w2.w"],
        add2=W[pb + "ws_tab"], add2_rows=b.window_feat, relu=True, w3=W[pb + "mlp_w3.w"], b3=W[pb + "mlp_w3.b"],
-       out=w, residual=True)
+       out=w, residual=True, residual_from_x=w_init is not None)
     # §5.1b cell stage, or the knob-off cell pass
     if c is not None:
         _cell_stage(W, P, pb, plan, s, w, c, c_init)
@@ -747,10 +750,17 @@ def _trunk(model, b: Batch, plan: Plan, raw_cells: bool = False, W: Prepared | N
     n_s, p = plan.n_s, plan.n_pos
     # the window state is stored in fp16 in the cell-node configuration, like
     # the cell state (each update adds in fp32 and rounds once); the knob-off
-    # cell pass keeps it in fp32 for its compensated-weight launches.  Its
-    # gather is the forward's first large launch: the plan's small kernels
-    # and the host's work to queue them follow it
-    w = ops.gather_rows(W["window_table"], b.window_feat)
+    # cell pass keeps it in fp32 for its compensated-weight launches.  (The
+    # MLP's group add reads the same window_feat entries and flags any out of
+    # range, as the gather did.)
+    w_init = None
+    if cfg.cell_nodes and cfg.blocks:
+        # the fp16 window state: the first block's pair MLP reads the rows'
+        # initial state from the table (cached) and writes w
+        w = torch.empty((plan.n_w, 128), dtype=HALF, device=b.stone_own.device)
+        w_init = (W["window_table"], b.window_feat)
+    else:
+        w = ops.gather_rows(W["window_table"], b.window_feat)
     c = c_init = None
     if cfg.cell_nodes:
         # covered cells start from cell_base, the others from their nearest-stone
@@ -777,7 +787,8 @@ def _trunk(model, b: Batch, plan: Plan, raw_cells: bool = False, W: Prepared | N
               out=sg[n_s:].view(p, GLOBAL_ROWS, 128))
     sw_all = ops.run_reduce(W["sw_all"], plan.run_class, plan.inc_stone_ptr, n_s, F32)
     for i in range(cfg.blocks):
-        _block(W, P, i, plan, b, sg, w, c, sw_all, i + 1 < cfg.blocks, c_init if i == 0 else None)
+        _block(W, P, i, plan, b, sg, w, c, sw_all, i + 1 < cfg.blocks, c_init if i == 0 else None,
+               w_init if i == 0 else None)
     g = sg[n_s:].view(p, GLOBAL_ROWS, 128)
     w_out = w if raw_windows and w.dtype == HALF else ops.layer_norm(w, P["ln_out.weight"], P["ln_out.bias"], F32)
     g_out = F.layer_norm(g, (128,), P["ln_out.weight"], P["ln_out.bias"], 1e-5).mean(dim=1)

@@ -1469,12 +1469,15 @@ def fused_linear(x: Tensor, w1: Tensor, b1: Tensor | None = None, *, layer_norm:
                  add1: Tensor | None = None, add2: Tensor | None = None, add2_rows: Tensor | None = None,
                  relu: bool = False, w3: Tensor | None = None, b3: Tensor | None = None,
                  out: Tensor | None = None, out_dtype: torch.dtype = torch.float16,
-                 residual: bool = False, split: bool = False) -> Tensor:
+                 residual: bool = False, split: bool = False, residual_from_x: bool = False) -> Tensor:
     """One fused row-GEMM launch (see mantis_fused_linear in
     include/mantis_hip.h).  ``residual=True`` adds into ``out`` (fp32, in
     place); otherwise a new (m, width) tensor of ``out_dtype`` is returned.
     ``split=True``: w1/w2 are compensated [hi; lo] pairs (2 n1 rows, see
-    ``split_weight``), for the launches mantis_fused_linear_split covers."""
+    ``split_weight``), for the launches mantis_fused_linear_split covers.
+    ``residual_from_x=True`` (fp16 pair MLP, residual into fp16 ``out``):
+    out = x[x_rows] + y, the residual rows starting from the rows read
+    rather than from ``out`` (out_mode 4)."""
     dev = _on_gpu(x, w1, b1, x_rows, x2, w2, add1, add2, add2_rows, w3, b3, out)
     if x.ndim != 2 or x.shape[1] < 128 or x.stride(1) != 1:
         raise ValueError("x must be (n, >=128) rows with unit column stride")
@@ -1505,6 +1508,12 @@ def fused_linear(x: Tensor, w1: Tensor, b1: Tensor | None = None, *, layer_norm:
         if out is None or out.dtype not in (torch.float32, torch.float16) or out.shape[0] != m or out.stride(1) != 1:
             raise ValueError("a residual launch needs an fp32 or fp16 (m, width) out tensor")
         mode = 2 if out.dtype == torch.float32 else 3
+        if residual_from_x:
+            if mode != 3 or x.dtype != torch.float16 or x.data_ptr() == out.data_ptr():
+                raise ValueError("residual_from_x: fp16 rows x into another fp16 out")
+            mode = 4
+    elif residual_from_x:
+        raise ValueError("residual_from_x needs residual=True")
     else:
         mode = _MODES[out_dtype]
         if out is None:

@@ -680,13 +680,15 @@ int64_t mantis_stone_attention_schedule_len(int64_t n_pos, int32_t heads, int64_
  *   y[i]     = h[i] W3^T + b3                  if w3 (n3 outputs), else h[i]
  *   out[i]   = y[i] (out_mode 0: fp16 store, 1: fp32 store) or out[i] += y[i]
  *              (out_mode 2: fp32 residual, in place; out_mode 3: fp16 residual,
- *              added in fp32 and rounded once)
+ *              added in fp32 and rounded once); out_mode 4 (the fp16 pair MLP
+ *              with x2 and W3): out[i] = x[x_rows[i]] + y[i] (x[i] without
+ *              x_rows), x not out: the residual rows start from gathered rows
  * The LayerNorm affine is folded into W1/b1 by the caller.  x is fp32 or
  * fp16 (rows of stride ldx), x2 fp32 or fp16; W1/W2 (n1, 128), W3 (n3, n1)
  * fp16 row-major; b1/add1/add2 (.., n1) and b3 (n3) fp32.  fp16 MFMA with
  * fp32 accumulation and fp32 LayerNorm statistics.  Supported shapes: the
- * projection (n1 in 128/256/384/512 from fp32 rows, 256/512 from fp16 rows,
- * fp16 out), the residual projection (n1 = 128, fp32 or fp16 residual), the
+ * projection (n1 in 128/256/384/512 from fp32 rows, 128/256/384/512 from fp16
+ * rows, fp16 out), the residual projection (n1 = 128, fp32 or fp16 residual), the
  * two-layer residual MLPs (n1 = 128 with x2 into fp32 or fp16 residual rows,
  * n1 = 256 without) and the two-layer head (n1 = 256 with x2, fp32 out).
  */

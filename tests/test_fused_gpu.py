@@ -113,6 +113,21 @@ def test_pair_mlp_residual(device, x2dt):
                          b3=b3.to(device), out=dst16, residual=True)
         ops.raise_on_device_error(device)
         assert torch.equal(dst16.cpu(), out16.cpu()) and torch.equal(src16.cpu(), r16)
+        # rows that start from gathered table rows (out = x[x_rows] + y): bitwise
+        # the gather followed by the in-place update; x is left alone and out
+        # is only written
+        table = torch.randn(groups, 128, generator=gen).to(H16)
+        gathered = table[rows].to(device)
+        ops.fused_linear(gathered, w1.to(device), b1.to(device), layer_norm=True, x2=x2.to(device),
+                         w2=w2.to(device), add2=add2.to(device), add2_rows=rows.to(device), relu=True,
+                         w3=w3.to(device), b3=b3.to(device), out=gathered, residual=True)
+        seeded = torch.full((m, 128), float("nan"), dtype=H16, device=device)
+        tab = table.to(device)
+        ops.fused_linear(tab, w1.to(device), b1.to(device), layer_norm=True, x_rows=rows.to(device), x2=x2.to(device),
+                         w2=w2.to(device), add2=add2.to(device), add2_rows=rows.to(device), relu=True,
+                         w3=w3.to(device), b3=b3.to(device), out=seeded, residual=True, residual_from_x=True)
+        ops.raise_on_device_error(device)
+        assert torch.equal(seeded.cpu(), gathered.cpu()) and torch.equal(tab.cpu(), table)
 
 
 def test_ffn_residual_with_add1(device):
