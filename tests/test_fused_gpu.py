@@ -432,6 +432,40 @@ def test_substages_starting_from_an_initial_state_table(device):
     assert torch.equal(got[uncovered].cpu(), zero[uncovered].cpu())
 
 
+def test_tiles_without_entries_add_only_the_output_bias(device):
+    # a stage whose tile has no entries at all skips its products and adds
+    # only its output bias: rows without entries come out as x + bo exactly
+    # (fp32 rows; fp16 rows rounded once), in both stages of a pass and in a
+    # one-stage pass, next to tiles that do have entries
+    gen = _g(21)
+    n = 4099
+    st1 = _random_stage(gen, n, 301, 726, True, 7)
+    st2 = _random_stage(gen, n, 57, 192, True, 11)
+    empty = torch.zeros(n, dtype=torch.bool)
+    empty[1000:2600] = True  # whole 16-row tiles without entries in either stage
+    def strip(st):
+        counts = st.seg_ptr[1:] - st.seg_ptr[:-1]
+        keep = ~torch.repeat_interleave(empty, counts)
+        counts = torch.where(empty, torch.zeros_like(counts), counts)
+        ptr = torch.cat([torch.zeros(1, dtype=torch.long), counts.cumsum(0)])
+        return st._replace(seg_ptr=ptr, src=st.src[keep], cls=st.cls[keep])
+    st1, st2 = strip(st1), strip(st2)
+    dev = lambda st: ops.SubStage(*[None if t is None else t.to(device) for t in st])  # noqa: E731
+    s1, s2 = dev(st1), dev(st2)
+    x = 2 * torch.randn(n, 128, generator=gen) - 0.3
+    got = x.to(device)
+    ops.attention_substages(got, [s1])
+    ops.raise_on_device_error(device)
+    assert torch.equal(got.cpu()[empty], x[empty] + st1.bo)
+    assert not torch.equal(got.cpu()[~empty], x[~empty] + st1.bo)
+    x16 = x.to(H16)
+    got = x16.to(device)
+    ops.attention_substages(got, [s1, s2])
+    ops.raise_on_device_error(device)
+    want = ((x16[empty].float() + st1.bo).to(H16).float() + st2.bo).to(H16)
+    assert torch.equal(got.cpu()[empty], want)
+
+
 def test_row_order_changes_the_tiles_not_the_results(device):
     # the rows visited in a random permutation (and in an order sorted by
     # entry count) give bitwise the natural order's results; an order entry
