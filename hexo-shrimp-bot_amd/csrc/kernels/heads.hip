@@ -245,7 +245,7 @@ value_read_merge_kernel(const float* __restrict__ part, float* __restrict__ out)
 __global__ void __launch_bounds__(256)
 compose_q_kernel(const float* __restrict__ critic, int64_t ld, const int64_t* __restrict__ offsets,
                  int64_t n_cells, float mass_floor, float* __restrict__ q_values,
-                 float* __restrict__ q_score) {
+                 float* __restrict__ q_score, const float* __restrict__ col0, float* __restrict__ col0_out) {
   __shared__ float s_max[256];
   const int64_t p = blockIdx.x;
   int64_t a = offsets[p], b = offsets[p + 1];
@@ -260,6 +260,7 @@ compose_q_kernel(const float* __restrict__ critic, int64_t ld, const int64_t* __
     const float pp = e0 * inv, pn = e1 * inv;
     q_values[i] = pp - pn;
     mx = fmaxf(mx, pp + pn);
+    if (col0_out) col0_out[i] = col0[i * ld];  // the rows' first column, contiguous (the policy logits)
   }
   s_max[threadIdx.x] = mx;
   __syncthreads();
@@ -345,7 +346,18 @@ int32_t mantis_compose_q(const float* critic, int64_t ld, const int64_t* offsets
   if (n_pos == 0) return MANTIS_OK;
   if (!critic || !offsets || !q_values || !q_score || ld < 3 || n_pos < 0 || n_cells < 0) return MANTIS_E_ARG;
   compose_q_kernel<<<unsigned(n_pos), 256, 0, as_stream(stream)>>>(critic, ld, offsets, n_cells, mass_floor,
-                                                                   q_values, q_score);
+                                                                   q_values, q_score, nullptr, nullptr);
+  return launched();
+}
+
+int32_t mantis_compose_q_rows(const float* rows, int64_t ld, const int64_t* offsets, int64_t n_pos,
+                              int64_t n_cells, float mass_floor, float* policy, float* q_values, float* q_score,
+                              void* stream) {
+  if (n_pos == 0) return MANTIS_OK;
+  if (!rows || !offsets || !policy || !q_values || !q_score || ld < 4 || n_pos < 0 || n_cells < 0)
+    return MANTIS_E_ARG;
+  compose_q_kernel<<<unsigned(n_pos), 256, 0, as_stream(stream)>>>(rows + 1, ld, offsets, n_cells, mass_floor,
+                                                                   q_values, q_score, rows, policy);
   return launched();
 }
 

@@ -84,6 +84,7 @@ SIGNATURES = {
     "mantis_value_read": ([vp, vp, i32, i64, vp, vp, i64, vp, vp, vp, vp, vp, i32, vp, vp, vp, vp], i32),
     "mantis_value_read_workspace": ([i64], i64),
     "mantis_compose_q": ([vp, i64, vp, i64, i64, ctypes.c_float, vp, vp, vp], i32),
+    "mantis_compose_q_rows": ([vp, i64, vp, i64, i64, ctypes.c_float, vp, vp, vp, vp], i32),
     "mantis_hex_neighbours": ([vp, vp, i64, i64, vp, vp, vp], i32),
     "mantis_hex_aggregate_linear": ([vp, vp, i64, vp, vp, vp, vp, vp, vp], i32),
 }

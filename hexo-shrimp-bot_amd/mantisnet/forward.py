@@ -879,8 +879,10 @@ def cell_heads(model, w: Tensor, g: Tensor, cells: Tensor, batch: Batch, mass_fl
 def _cell_heads(model, w, g, cells, b: Batch, plan: Plan, mass_floor: float, raw_cells: bool = False,
                 W: Prepared | None = None):
     rows = _head_rows(model, w, g, cells, b, plan, raw_cells, W)
-    q_values, q_score = ops.compose_q(rows[:, 1:], b.legal_offsets, mass_floor)
-    return rows[:, 0].contiguous(), q_score, q_values
+    # the policy column leaves in the same pass (legal_offsets tile the cells:
+    # the cell order's segment check flags them otherwise)
+    policy, q_values, q_score = ops.compose_q_rows(rows, b.legal_offsets, mass_floor)
+    return policy, q_score, q_values
 
 
 def _speculative(model, b: Batch, evaluate):

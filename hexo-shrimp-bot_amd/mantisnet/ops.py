@@ -1622,6 +1622,23 @@ def compose_q(critic: Tensor, offsets: Tensor, mass_floor: float) -> tuple[Tenso
     return qv, qs
 
 
+def compose_q_rows(rows: Tensor, offsets: Tensor, mass_floor: float) -> tuple[Tensor, Tensor, Tensor]:
+    """(policy, q_values, q_score) from the fused heads' fp32 rows (n, >=4):
+    column 0 copied out contiguous, columns 1..3 composed as compose_q."""
+    dev = _on_gpu(rows, offsets)
+    if rows.dtype != torch.float32 or rows.stride(1) != 1 or rows.ndim != 2 or rows.shape[1] < 4:
+        raise ValueError("head rows must be fp32 rows of at least 4")
+    n = rows.shape[0]
+    pol = torch.empty(n, dtype=torch.float32, device=dev)
+    qv = torch.empty(n, dtype=torch.float32, device=dev)
+    qs = torch.empty(n, dtype=torch.float32, device=dev)
+    offsets = _i64(offsets, "offsets")
+    _launch("compose_q", n * (16 + 12), 0, lambda: _check(
+        _lib().mantis_compose_q_rows(_ptr(rows), rows.stride(0), _ptr(offsets), offsets.numel() - 1, n,
+                                     float(mass_floor), _ptr(pol), _ptr(qv), _ptr(qs), _stream()), "compose_q"))
+    return pol, qv, qs
+
+
 # ----------------------------------------------------------------- hex message passing
 
 

@@ -767,6 +767,15 @@ int32_t mantis_compose_q(const float* critic, int64_t ld, const int64_t* offsets
                          void* stream);
 
 /*
+ * mantis_compose_q over the fused heads' rows (n_cells, >= 4) at row stride
+ * ld: columns 1..3 are the critic logits, and column 0 (the policy logit)
+ * is also copied to the contiguous policy (n_cells) in the same pass.
+ */
+int32_t mantis_compose_q_rows(const float* rows, int64_t ld, const int64_t* offsets, int64_t n_pos,
+                              int64_t n_cells, float mass_floor, float* policy, float* q_values, float* q_score,
+                              void* stream);
+
+/*
  * Six-neighbour table of ragged cell graphs: graph j's cells are
  * cells[graph_ptr[j]:graph_ptr[j+1]] given as (q, r) int32 pairs in ascending
  * (q, r) order; nbr[i, s] is the global index of the cell at offset s of

@@ -247,6 +247,10 @@ def test_compose_q_matches_reference_formula(device):
     mass = torch.zeros(4).index_reduce_(0, seg, pr[:, 0] + pr[:, 1], "amax", include_self=False)
     torch.testing.assert_close(qv.cpu(), q, rtol=1e-5, atol=1e-6)
     torch.testing.assert_close(qs.cpu(), q / mass.clamp(min=0.2)[seg], rtol=1e-5, atol=1e-6)
+    # over the whole head rows: the same values, and column 0 copied out
+    pol, qv2, qs2 = ops.compose_q_rows(logits.to(device), offsets.to(device), 0.2)
+    assert torch.equal(qv2.cpu(), qv.cpu()) and torch.equal(qs2.cpu(), qs.cpu())
+    assert torch.equal(pol.cpu(), logits[:, 0])
 
 
 @pytest.mark.parametrize("with_vcls", [True, False])
