@@ -259,6 +259,12 @@ def _prepare(model, P) -> dict[str, Tensor]:
     t["head2.w"] = torch.cat(h2).to(HALF).contiguous()
     t["head1.b"] = torch.cat(hb).contiguous()
     t["head_tab"] = torch.cat(tabs, 1).contiguous()  # (726, 256)
+    # the forms the fused heads gather (fp16, the class table quad-chunked)
+    # and the EMPTY-class action rows, all functions of the parameters alone
+    t["head_tab_k"] = ops.head_table_for_kernel(t["head_tab"])
+    t["act_table16"] = P["act_table.weight"].to(HALF).contiguous()
+    t["empty_rows"] = F.relu(P["act_empty_base"] + P["act_table.weight"].index_select(
+        0, model.act_empty_classes.to(P["act_table.weight"].device))).float().contiguous()
     w3 = torch.zeros(16, 256, device=la.device)
     w3[0, :128] = P["mlp_p.out.weight"][0]
     w3[1:4, 128:] = P["mlp_q.out.weight"]
@@ -847,15 +853,14 @@ def _head_rows(model, w: Tensor, g: Tensor, cells: Tensor, b: Batch, plan: Plan,
         pre = FL(w.contiguous(), W["act_proj_ln.w"], W["act_proj_ln.b"], layer_norm=True)
     else:
         pre = FL(w.float().contiguous(), W["act_proj.w"], W["act_proj.b"])  # act_proj(w), fp16
-    empty_rows = F.relu(P["act_empty_base"] + P["act_table.weight"].index_select(0, model.act_empty_classes))
     g_half = F.linear(g.float(), W["glin_b"]).contiguous()  # (P, 256)
     x = cells if cells.dtype in (HALF, F32) else cells.float()
     key = "head1ln" if raw_cells else "head1"
     return ops.cell_heads(x.contiguous(), W[key + ".w"], W[key + ".b"], W["head2.w"],
                           W["head3c.w" if compensated else "head3.w"], W["head3.b"], pre,
-                          P["act_table.weight"], empty_rows, b.act_empty, W["head_tab"], g_half, b.cell_pos,
+                          W["act_table16"], W["empty_rows"], b.act_empty, W["head_tab_k"], g_half, b.cell_pos,
                           plan.dec_cell_ptr, b.dec_window, b.act_class, b.dec_class, layer_norm=raw_cells,
-                          row_order=plan.head_order, compensated=compensated)
+                          row_order=plan.head_order, compensated=compensated, tables_ready=True)
 
 
 @torch.no_grad()

@@ -869,6 +869,12 @@ def _head_tab_quad_index() -> Tensor:
 # cell's four lanes reads one 64-byte piece of the row
 HEAD_TAB_QUAD = _head_tab_quad_index()
 
+
+def head_table_for_kernel(head_tab: Tensor) -> Tensor:
+    """The (n, 256) class table as mantis_cell_heads gathers it: fp16 with
+    quad-chunked columns."""
+    return head_tab.index_select(1, _const_on(HEAD_TAB_QUAD, head_tab.device)).to(torch.float16).contiguous()
+
 _DEVICE_CONSTS: dict[tuple[int, torch.device], Tensor] = {}
 
 
@@ -1013,14 +1019,17 @@ def cell_heads(c: Tensor, w1: Tensor, b1: Tensor, w2: Tensor, w3: Tensor, b3: Te
                act_table: Tensor, empty_rows: Tensor, act_empty: Tensor, head_tab: Tensor, g_half: Tensor,
                cell_pos: Tensor, dec_ptr: Tensor, dec_window: Tensor, act_class: Tensor, dec_class: Tensor,
                layer_norm: bool, row_order: Tensor | None = None, compensated: bool = False,
-               library_counters: bool = False) -> Tensor:
+               library_counters: bool = False, tables_ready: bool = False) -> Tensor:
     """(n_cells, 16) fp32 head rows of every cell in one launch (see
     mantis_cell_heads in include/mantis_hip.h): column 0 the policy logit,
     1..3 the critic logits.  ``row_order`` (int32 permutation of the cells)
     sets their grouping into tiles; the results do not depend on it.
     ``compensated`` (fp32 rows, no LayerNorm; w3 (32, 256) = [hi; lo]) runs
     the three products on hi + lo fp16 operand pairs.  Tiles are handed out
-    as in attention_substages (``library_counters`` likewise)."""
+    as in attention_substages (``library_counters`` likewise).
+    ``tables_ready``: act_table is already fp16 and head_tab already the
+    kernel's fp16 quad-chunked table (``head_table_for_kernel``), as a caller
+    that prepares them once passes them."""
     dev = _on_gpu(c, w1, b1, w2, w3, b3, pre, act_table, empty_rows, act_empty, head_tab, g_half, cell_pos, dec_ptr,
                   dec_window, act_class, dec_class, row_order)
     if row_order is not None and (row_order.dtype != torch.int32 or row_order.shape != (c.shape[0],)):
@@ -1043,8 +1052,13 @@ def cell_heads(c: Tensor, w1: Tensor, b1: Tensor, w2: Tensor, w3: Tensor, b3: Te
     if act_table.ndim != 2 or act_table.shape[1] != 128:
         raise ValueError("act_table must be (n, 128)")
     # the kernel gathers both tables in fp16, the class table quad-chunked
-    act_table = act_table.to(torch.float16).contiguous()
-    head_tab = head_tab.index_select(1, _const_on(HEAD_TAB_QUAD, head_tab.device)).to(torch.float16).contiguous()
+    if tables_ready:
+        if act_table.dtype != torch.float16 or head_tab.dtype != torch.float16 or not (
+                act_table.is_contiguous() and head_tab.is_contiguous()):
+            raise ValueError("prepared tables must be contiguous fp16")
+    else:
+        act_table = act_table.to(torch.float16).contiguous()
+        head_tab = head_table_for_kernel(head_tab)
     act_empty = _i64(act_empty, "act_empty")
     cell_pos, dec_ptr = _i64(cell_pos, "cell_pos"), _i64(dec_ptr, "dec_ptr")
     dec_window, act_class, dec_class = _i64(dec_window, "dec_window"), _i64(act_class, "act_class"), \
