@@ -20,7 +20,14 @@ arithmetic is regrouped into fused HIP kernels (libmantis_hip.so via
 * the two cell heads run as one two-layer launch: ``lin_a`` is composed into
   the projection, extension and class tables (lin_a(p x + p_act a + sum e) =
   (lin_a p) x + (lin_a p_act) a + sum (e lin_a^T)), the g half is a per-
-  position row add, and both output layers are one block-diagonal stage 2.
+  position row add, and both output layers are one block-diagonal stage 2;
+* over the fp16 window state, the latent read takes the window rows
+  themselves (its key projection composed into the queries, q' = Wk^T q per
+  head, its value projection applied after the weighted sum of LN(w)), and
+  the broadcast projects its queries from the rows it updates: no per-window
+  k, v or q rows are materialised for the latent cycle;
+* the first cell pass and the first window pair MLP read the rows' initial
+  state from the (cached) tables instead of gathered copies.
 
 Precision: every GEMM and attention operand is fp16 with fp32 accumulation;
 LayerNorm statistics, softmax and the head outputs are fp32.  The stone and
