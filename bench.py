@@ -385,7 +385,7 @@ def main() -> int:
         traced = ("attention_substage", "cell_attention", "cell_heads", "fused_linear", "stone_attention", "run_reduce",
                   "runs_to_ptr", "latent_", "row_encode", "layer_norm", "value_read", "compose_q", "gather_rows",
                   "plan_check", "stable_key_order", "radius_class", "attention_slots", "covered_rows", "window_view",
-                  "segment_order")
+                  "segment_order", "radius_", "pack_entries")
         with ops.trace(*traced) as tr:
             for _ in range(args.steps):
                 net(bd, 0.2)

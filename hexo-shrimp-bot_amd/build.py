@@ -22,7 +22,7 @@ CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 HIP_SOURCES = ["gather_ops.hip", "stone_attention.hip", "hex_message.hip", "fused_linear.hip", "heads.hip",
                "attention_substage.hip", "cell_heads.hip", "latent_mix.hip", "improve.hip", "relay.hip", "attn_backward.hip", "plan.hip", "latent_broadcast.hip",
-               "latent_read.hip"]
+               "latent_read.hip", "radius_stage.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 HIP_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",

@@ -52,14 +52,15 @@
 // bitwise those of the natural order.
 #include "common.hpp"
 #include "mfma.hpp"
+#include "substage.hpp"
 
 #include <mutex>
 
 namespace mantis {
 namespace {
 
-constexpr int kK = 128;
-constexpr int kPitch = kK + 8;  // fp16 per staged LDS row (272 bytes: conflict-free fragment reads)
+using namespace substage;
+
 // Wavefronts per workgroup (one workgroup per CU: the weights fill LDS).  A
 // single stage runs 12 (three per SIMD at <= 168 VGPRs); two stages keep
 // more state live across the pass and run 8 (two per SIMD), which leaves
@@ -67,11 +68,9 @@ constexpr int kPitch = kK + 8;  // fp16 per staged LDS row (272 bytes: conflict-
 // production batch, against 12 wavefronts with 17 spilled registers.
 template <int kStages>
 constexpr int waves_for() { return kStages == 2 ? 8 : 12; }
-constexpr int kXcds = 8;
 // class-bias tables of all stages in LDS: 4 heads x n_classes fp32 per stage
 // (the two-stage pass leaves 22.5 KB beside its 141 KB of weights)
 constexpr int kBiasPool = 5376;
-constexpr float kTau = 8.f;  // the softmax reference point lags the max by at most this
 
 struct Stage {
   const _Float16* wq;
@@ -131,62 +130,10 @@ struct SubArgs {
   int64_t n_init;
   const int64_t* init_idx;
   int64_t init_cover;
+  // when set, rows whose first stage's run is empty are neither read nor
+  // written (a later launch adds that stage's output bias to them)
+  int32_t skip_empty;
 };
-
-// the value v of lane 4 (lane / 4) + u (one DPP quad broadcast)
-template <int u>
-__device__ __forceinline__ int32_t from_quad(int32_t v) {
-  return __builtin_amdgcn_update_dpp(0, v, u * 0x55, 0xF, 0xF, false);
-}
-
-// LDS row r of the staged q weights holds Wq row qrow(r): the accumulator
-// row 16 nt + 4 g + t of lane group g is feature 32 g + 4 nt + t.
-__device__ __forceinline__ int qrow(int r) {
-  const int nt = r >> 4, j = r & 15;
-  return 32 * (j >> 2) + 4 * nt + (j & 3);
-}
-// LDS row r of the staged o weights holds Wo row orow(r): the accumulator
-// row 16 nt + 4 g + t is feature 32 (nt/2) + 8 g + 4 (nt%2) + t, the
-// lane's x register [nt/2][4 (nt%2) + t].
-__device__ __forceinline__ int orow(int r) {
-  const int nt = r >> 4, j = r & 15;
-  return 32 * (nt >> 1) + 8 * (j >> 2) + 4 * (nt & 1) + (j & 3);
-}
-
-__device__ __forceinline__ float dot32(const uint32_t (&q)[16], const uint4 (&k)[4]) {
-  float d0 = 0.f, d1 = 0.f;
-#pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    d0 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, q[4 * w]), __builtin_bit_cast(f16x2_t, k[w].x), d0, false);
-    d1 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, q[4 * w + 1]), __builtin_bit_cast(f16x2_t, k[w].y), d1, false);
-    d0 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, q[4 * w + 2]), __builtin_bit_cast(f16x2_t, k[w].z), d0, false);
-    d1 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, q[4 * w + 3]), __builtin_bit_cast(f16x2_t, k[w].w), d1, false);
-  }
-  return d0 + d1;
-}
-
-// acc[i] += p * h[i] for the 32 fp16 values of four 16-byte chunks (v_fma_mix)
-__device__ __forceinline__ void axpy32(float (&acc)[32], float p, const uint4 (&h)[4]) {
-#pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    const uint32_t u[4] = {h[w].x, h[w].y, h[w].z, h[w].w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const f16x2_t v = __builtin_bit_cast(f16x2_t, u[i]);
-      acc[8 * w + 2 * i] = fmaf(p, float(v[0]), acc[8 * w + 2 * i]);
-      acc[8 * w + 2 * i + 1] = fmaf(p, float(v[1]), acc[8 * w + 2 * i + 1]);
-    }
-  }
-}
-
-// the value v of lane `src` (all lanes active)
-__device__ __forceinline__ int32_t from_lane(int src, int32_t v) { return __builtin_amdgcn_ds_bpermute(src << 2, v); }
-
-// head g's 32 values of a head-interleaved row: chunk w sits at 32 w + 8 g
-__device__ __forceinline__ void load_head(const _Float16* row_g, uint4 (&h)[4]) {
-#pragma unroll
-  for (int w = 0; w < 4; ++w) h[w] = *reinterpret_cast<const uint4*>(row_g + 32 * w);
-}
 
 template <int kStages, bool kVcls, typename TX>
 __global__ void __launch_bounds__(waves_for<kStages>() * 64) attn_substage_kernel(SubArgs a) {
@@ -295,8 +242,9 @@ __global__ void __launch_bounds__(waves_for<kStages>() * 64) attn_substage_kerne
       hi[s] = pb_n[s] < lo[s] ? lo[s] : (pb_n[s] > n_e ? n_e : pb_n[s]);
     }
     const bool in_tile = tile * 16 + l16 < a.n_rows;
-    const bool live = in_tile && row >= 0 && row < a.n_rows;
-    bad |= in_tile && !live;
+    const bool valid = in_tile && row >= 0 && row < a.n_rows;
+    bad |= in_tile && !valid;
+    const bool live = valid && (!a.skip_empty || hi[0] > lo[0]);
     const int64_t rc = live ? row : 0;  // dead lanes read a real row and store nothing
     // the row state: fp32 rows stay fp32 in registers across the stages;
     // fp16 rows stay packed (half the registers) and are rounded after each
@@ -635,7 +583,7 @@ struct InitRows {
 
 int32_t substages(void* x, int32_t x_dtype, int64_t ldx, int64_t n_rows, const int32_t* row_order,
                   const mantis_substage* stages, int32_t n_stages, const InitRows* init, int32_t* err_flag,
-                  uint32_t* tile_counters, void* stream) {
+                  uint32_t* tile_counters, void* stream, bool skip_empty = false) {
   if (n_rows < 0 || !stages || n_stages < 1 || n_stages > 2) return MANTIS_E_ARG;
   if (n_rows == 0) return MANTIS_OK;
   for (int s = 0; s < n_stages; ++s)
@@ -656,6 +604,7 @@ int32_t substages(void* x, int32_t x_dtype, int64_t ldx, int64_t n_rows, const i
   a.n_init = init ? init->n : 0;
   a.init_idx = init ? init->idx : nullptr;
   a.init_cover = init ? init->cover_row : 0;
+  a.skip_empty = skip_empty ? 1 : 0;
   int64_t pool = 0;
   for (int s = 0; s < n_stages; ++s) {
     a.st[s] = to_stage(stages[s]);
@@ -697,6 +646,21 @@ extern "C" int32_t mantis_attention_substages_init(void* x, int32_t x_dtype, int
     return MANTIS_E_ARG;
   const InitRows init{x_init, ld_init, n_init, init_idx, init_cover};
   return substages(x, x_dtype, ldx, n_rows, row_order, stages, n_stages, &init, err_flag, tile_counters, stream);
+}
+
+extern "C" int32_t mantis_attention_substages_covered(void* x, int32_t x_dtype, int64_t ldx, int64_t n_rows,
+                                                      const int32_t* row_order, const mantis_substage* stage,
+                                                      const void* x_init, int64_t ld_init, int64_t n_init,
+                                                      const int64_t* init_idx, int64_t init_cover, int32_t* err_flag,
+                                                      uint32_t* tile_counters, void* stream) {
+  // every row this call updates starts from row init_cover (init_idx may be
+  // NULL: it is read only for rows that are skipped)
+  if (x_init && (n_init <= 0 || init_cover < 0 || init_cover >= n_init || !aligned16(x_init) || ld_init < kK ||
+                 ld_init % (x_dtype == MANTIS_F16 ? 8 : 4) || x_init == x))
+    return MANTIS_E_ARG;
+  const InitRows init{x_init, ld_init, n_init, init_idx, init_cover};
+  return substages(x, x_dtype, ldx, n_rows, row_order, stage, 1, x_init ? &init : nullptr, err_flag, tile_counters,
+                   stream, true);
 }
 
 extern "C" int32_t mantis_attention_substage(float* x, int64_t ldx, int64_t n_rows, const void* wq, const float* bq,

@@ -30,7 +30,7 @@
 // its columns in that order (the K slots 32 ks + 8 g + t of the B fragment
 // are features 32 ks + 4 g + t and 32 ks + 16 + 4 g + t - 4) and its rows in
 // the order whose D fragment is the lane's q dims 8 g .. 8 g + 7 of each
-// head.  Wq' takes another 34 KB of LDS: one workgroup of 16 wavefronts per
+// head.  Wq' takes another 34 KB of LDS: one workgroup of 12 wavefronts per
 // CU.
 #include <type_traits>
 
@@ -295,7 +295,7 @@ int32_t launch_broadcast(const BcastArgs& a, hipStream_t stream) {
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
     cus = 256;
   const int64_t tiles = (a.n_w + 15) / 16;
-  // persistent workgroups: three per CU, or one (of 16 wavefronts) when Wq'
+  // persistent workgroups: three per CU, or one (of 12 wavefronts) when Wq'
   // takes its share of the LDS
   int64_t grid = int64_t(cus) * (kQ ? 1 : 3);
   const int64_t need = (tiles + kWaves - 1) / kWaves;

@@ -71,6 +71,9 @@ latent_read_x_kernel(const _Float16* __restrict__ qp, int64_t ldq, const _Float1
     for (int ks = 0; ks < 4; ++ks) qb[ks] = *reinterpret_cast<const f16x8_t*>(qrow + 32 * ks);
   }
   int64_t a0 = offsets[pos], b0 = offsets[pos + 1];
+  // offsets outside [0, n_w] or decreasing are a malformed layout: the range
+  // is clamped (so every access stays in bounds) and the error flag raised
+  bool bad = a0 < 0 || a0 > n_w || b0 < a0 || b0 > n_w;
   a0 = a0 < 0 ? 0 : (a0 > n_w ? n_w : a0);
   b0 = b0 < a0 ? a0 : (b0 > n_w ? n_w : b0);
   const int64_t a = a0 + (b0 - a0) * split / kSplitRX, b = a0 + (b0 - a0) * (split + 1) / kSplitRX;
@@ -81,7 +84,6 @@ latent_read_x_kernel(const _Float16* __restrict__ qp, int64_t ldq, const _Float1
   for (int nt = 0; nt < 8; ++nt) y[nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   _Float16* zt = reinterpret_cast<_Float16*>(s_buf) + wave * kK * kPitchT;
   const int slot = 8 * (l16 >> 2) + (l16 & 3);  // LDS slot of window l16 (+ 4 for window 16 + l16)
-  bool bad = false;
   for (int64_t base = a + int64_t(kChunk) * wave; base < b; base += int64_t(kChunk) * kWavesRX) {
     // the chunk's rows: window base + 16 u + l16, features 32 ks + 8 g ..; a
     // window past the range reads row a and is masked out of the softmax

@@ -340,6 +340,8 @@ int32_t mantis_plan_check(const int64_t* dec_cell, const int64_t* dec_window, in
 
 int64_t mantis_stable_key_order_workspace(int64_t n_entries, int64_t n_keys) {
   if (n_entries < 0 || n_keys < 0) return -1;
+  // counts past these bounds would overflow the byte count below
+  if (n_keys > (INT64_MAX / 8) || n_entries > (INT64_MAX / 16)) return -1;
   // counts (int32, padded to 8 bytes), then the permutation (int64)
   return (4 * n_keys + 7) / 8 * 8 + 8 * n_entries;
 }
@@ -374,7 +376,10 @@ int32_t mantis_stable_key_order_noalloc(const int64_t* key, const int64_t* col_a
                                         int64_t* out_b, int32_t* err_flag, void* stream) {
   if (!ptr || n_entries < 0 || n_keys < 0) return MANTIS_E_ARG;
   if (n_entries && (!key || !col_a || !col_b || !out_a || !out_b)) return MANTIS_E_ARG;
-  if (mantis_stable_key_order_workspace(n_entries, n_keys) > MANTIS_NOALLOC_SCRATCH_BYTES) return MANTIS_E_SIZE;
+  // each count alone bounded first, so the byte count cannot overflow
+  if (n_keys > MANTIS_NOALLOC_SCRATCH_BYTES / 4 || n_entries > MANTIS_NOALLOC_SCRATCH_BYTES / 8 ||
+      mantis_stable_key_order_workspace(n_entries, n_keys) > MANTIS_NOALLOC_SCRATCH_BYTES)
+    return MANTIS_E_SIZE;
   void* ws = scratch_for_current_device();
   if (!ws) return MANTIS_E_LAUNCH;
   hipStream_t st = as_stream(stream);

@@ -60,6 +60,7 @@ from torch import Tensor
 
 from . import ops
 from .builder import Batch
+from .model import NEAREST_BUCKETS, RADIUS_CLASSES
 
 HALF = torch.float16
 F32 = torch.float32
@@ -509,6 +510,31 @@ class Plan:
         return ops.segment_order(self._b.legal_offsets, self.cell_ptr, self.radius_ptr, self.n_c)
 
     @cached_property
+    def radius(self) -> ops.RadiusPlan | None:
+        # the radius stage's tables: chunks of 512 consecutive cells of a
+        # position, each with the stones its cells see, its cells sorted into
+        # tiles and its entries packed; the decoder runs (whose empty ones get
+        # the first sub-stage's bias there) and the cells' initial-state rows
+        # ride in the same per-cell records
+        if not self._cfg.cell_nodes:
+            return None
+        b = self._b
+        return ops.radius_plan(b.legal_offsets, self.seq_lens, self.radius_ptr, self.radius_src, self.radius_class,
+                               self.n_s, RADIUS_CLASSES, pre_ptr=self.cell_ptr, pre_entries=self.edge_window.numel(),
+                               init_idx=b.cell_nearest, n_init=self._n_init, extra=GLOBAL_ROWS)
+
+    @property
+    def _n_init(self) -> int:
+        # rows of the cells' initial-state table [nearest-stone rows; cell_base]
+        return NEAREST_BUCKETS + 1
+
+    @property
+    def n_cov(self) -> int | None:
+        # the number of cells with decoder entries, when the batch's relay
+        # views tell it (trace accounting only)
+        return self._b.relay_cell_ptr.shape[0] - 1 if self._covers else None
+
+    @cached_property
     def head_order(self) -> Tensor:
         # the heads walk the same decoder runs (cell_ptr has the batch's run
         # lengths in any entry order), so the stages' order serves them too
@@ -615,18 +641,42 @@ def _substage(W, P, pb, key, kv, bias, vcls, ptr, src, cls) -> ops.SubStage:
                         W[pb + key + "_o.w"], W[pb + key + "_o.b"])
 
 
+# The cell stage's two cell sub-stages run as one fused launch over every
+# cell, each entry's k/v and class-value rows gathered (False, the default), or
+# as two launches (True): cells <- windows over the cells with decoder
+# entries, then cells <- stones over 512-cell chunks of each position with the
+# chunk's stone k/v rows and the class values staged on chip (radius_stage).
+# Both give bitwise the same rows.  Measured on one MI355X at configs[3], the
+# two launches take 331 + 546 us per block against 745 us fused: the radius
+# launch no longer waits on the texture path, but it re-reads and re-writes
+# the rows the first launch updated and keeps the per-entry VALU work (64
+# v_fma_mix per entry and lane for the value and class-value sums), which
+# bounds it with its wavefronts idle half the time between chunk barriers.
+SPLIT_CELL_STAGES = False
+
+
 def _cell_stage(W, P, pb, plan: Plan, s, w, c, c_init=None):
     # cells <- windows (decoder classes, class values) then cells <- stones
-    # (radius classes, class values): one fused pass over the cell rows, the
-    # rows staying on chip between the two sub-stages; then windows <- cells
-    # (decoder classes). Each sub-stage is LN -> q -> attention -> o -> residual.
+    # (radius classes, class values); then windows <- cells (decoder classes).
+    # Each sub-stage is LN -> q -> attention -> o -> residual.
     cr = _substage(W, P, pb, "cr", _proj(W, pb + "cr_kv", w), "cr_bias", W[pb + "cr_vcls"], plan.cell_ptr,
                    plan.edge_window, plan.edge_class)
-    rad = _substage(W, P, pb, "rad", _proj(W, pb + "rad_kv", s), "radius_bias", W[pb + "rad_vcls"],
-                    plan.radius_ptr, plan.radius_src, plan.radius_class)
+    rad_kv = _proj(W, pb + "rad_kv", s)
     # c_init: (table, index, cover row) of the cells' initial state, read by
     # the first pass in place of c (which it then writes)
-    ops.attention_substages(c, [cr, rad], row_order=plan.cell_order, init=c_init)
+    if SPLIT_CELL_STAGES:
+        # the cells <- windows sub-stage touches only the cells with decoder
+        # entries; the radius launch adds its output bias to the others (all
+        # the sub-stage does to them) and starts them from their table rows
+        ops.attention_substages_covered(c, cr, row_order=plan.cell_order,
+                                        init=None if c_init is None else (c_init[0], c_init[2]), n_cov=plan.n_cov)
+        ops.radius_stage(c, plan.radius, W[pb + "rad_q.w"], W[pb + "rad_q.b"], rad_kv, P[pb + "radius_bias"],
+                         W[pb + "rad_vcls"], W[pb + "rad_o.w"], W[pb + "rad_o.b"], pre_bias=W[pb + "cr_o.b"],
+                         init_table=None if c_init is None else c_init[0])
+    else:
+        rad = _substage(W, P, pb, "rad", rad_kv, "radius_bias", W[pb + "rad_vcls"], plan.radius_ptr,
+                        plan.radius_src, plan.radius_class)
+        ops.attention_substages(c, [cr, rad], row_order=plan.cell_order, init=c_init)
     if plan.cov_rows is not None:  # k/v of the covered cells only, entries remapped to them
         wr = _substage(W, P, pb, "wr", _proj(W, pb + "wr_kv", c, x_rows=plan.cov_rows), "wr_bias", None,
                        plan.win_ptr, plan.edge_wcell_cov, plan.edge_wclass)

@@ -1015,6 +1015,169 @@ def attention_substage(x: Tensor, wq: Tensor, bq: Tensor, kv: Tensor, bias: Tens
     return attention_substages(x, [SubStage(wq, bq, kv, bias, vcls, seg_ptr, src, cls, wo, bo)])
 
 
+def attention_substages_covered(x: Tensor, stage: SubStage, row_order: Tensor | None = None,
+                                init: tuple[Tensor, int] | None = None, n_cov: int | None = None) -> Tensor:
+    """One sub-stage (as attention_substages) over the fp16 rows of x whose run
+    of the stage is non-empty; the other rows are neither read nor written
+    (radius_stage with ``pre`` = this stage's (bo, seg_ptr) adds the stage's
+    output bias to them).  ``init`` = (table, cover_row): the rows it updates
+    start from table[cover_row] (x is then only written).  ``n_cov``: the
+    number of rows with entries, when the caller knows it (trace accounting
+    only)."""
+    dev = _on_gpu(x, row_order, *stage)
+    n = x.shape[0]
+    if x.ndim != 2 or x.shape[1] != 128 or x.dtype != torch.float16 or x.stride(1) != 1:
+        raise ValueError("x must be fp16 (n, 128) rows")
+    if row_order is not None:
+        if row_order.dtype != torch.int32 or row_order.shape != (n,):
+            raise ValueError("row_order must be an int32 permutation of the rows")
+        row_order = row_order.contiguous()
+    table = None
+    if init is not None:
+        table, cover_row = init
+        _on_gpu(table)
+        if table.dtype != x.dtype or table.ndim != 2 or table.shape[1] != 128 or table.stride(1) != 1:
+            raise ValueError("the initial-state table must be (n, 128) rows of x's dtype")
+        if not 0 <= cover_row < table.shape[0]:
+            raise ValueError("cover_row is not a row of the initial-state table")
+        if table.data_ptr() == x.data_ptr():
+            raise ValueError("the initial-state table must not be x")
+    d, keep, e = _substage_struct(stage, n)
+    if n:
+        rows = n if n_cov is None else n_cov
+        nbytes = rows * 256 * (1 if init is not None else 2) + 8 * (n + 1) + 4 * n + e * 16 + stage.kv.shape[0] * 512
+        flops = 2 * rows * 128 * 128 * 2 + e * 4 * 128 * 2
+        name = "attention_substage_covered_" + ("vcls" if stage.vcls is not None else "plain") + "_f16"
+        _launch(name, nbytes, flops, lambda: _check(
+            _lib().mantis_attention_substages_covered(
+                _ptr(x), _dt(x), x.stride(0), n, _ptr(row_order), ctypes.byref(d), _ptr(table),
+                table.stride(0) if table is not None else 0, table.shape[0] if table is not None else 0, None,
+                init[1] if init is not None else 0, _ptr(error_flag(dev)), _ptr(tile_counters(dev)), _stream()),
+            "attention_substages_covered"))
+    return x
+
+
+class RadiusPlan(NamedTuple):
+    """The per-batch tables of radius_stage (mantis_radius_chunks +
+    mantis_radius_prep): chunks (capacity, 4) int32 with their device count
+    n_chunks, one 16-byte record per slot, the packed entries and each
+    chunk's stone list."""
+
+    chunks: Tensor
+    n_chunks: Tensor
+    slots: Tensor
+    packed: Tensor
+    lists: Tensor
+    n_src: int
+
+
+def radius_plan(cell_off: Tensor, seq_lens: Tensor, seg_ptr: Tensor, src: Tensor, cls: Tensor, n_src: int,
+                n_classes: int, pre_ptr: Tensor | None = None, pre_entries: int = 0, init_idx: Tensor | None = None,
+                n_init: int = 0, extra: int = 4) -> RadiusPlan:
+    """Chunks of up to 512 consecutive rows of each position (the rows of
+    position p are cell_off[p] .. cell_off[p+1]-1, each position's stones
+    seq_lens[p] - extra), and per chunk its stones, its rows sorted into
+    16-row tiles and its entries packed (seg_ptr: the CSR of the entries
+    (src, cls) over the rows).  pre_ptr / pre_entries: the previous stage's
+    CSR (its empty runs are flagged in the records); init_idx / n_init: each
+    row's initial-state row.  No host read."""
+    dev = _on_gpu(cell_off, seq_lens, seg_ptr, src, cls, pre_ptr, init_idx)
+    cell_off, seg_ptr = _i64(cell_off, "cell_off"), _i64(seg_ptr, "seg_ptr")
+    src, cls = _i64(src, "src"), _i64(cls, "cls")
+    n_pos, n = cell_off.numel() - 1, seg_ptr.numel() - 1
+    if seq_lens.dtype != torch.int32 or seq_lens.shape != (n_pos,):
+        raise ValueError("seq_lens must be int32 with one entry per position")
+    if src.shape != cls.shape or src.ndim != 1:
+        raise ValueError("src and cls must be one-dimensional and of one length")
+    if not 0 <= n_src < (1 << 22) or not 0 < n_classes <= 256:
+        raise ValueError("radius_plan needs n_src < 2^22 and 0 < n_classes <= 256")
+    if pre_ptr is not None:
+        pre_ptr = _i64(pre_ptr, "pre_ptr")
+        if pre_ptr.numel() != n + 1:
+            raise ValueError("pre_ptr must have one entry per row plus one")
+    if init_idx is not None:
+        init_idx = _i64(init_idx, "init_idx")
+        if init_idx.shape != (n,):
+            raise ValueError("init_idx must have one entry per row")
+    cap = int(_lib().mantis_radius_chunks_capacity(n, n_pos))
+    chunks = torch.empty((cap, 4), dtype=torch.int32, device=dev)
+    n_chunks = torch.zeros(1, dtype=torch.int32, device=dev)
+    slots = torch.empty((n, 4), dtype=torch.int32, device=dev)
+    packed = torch.empty(src.numel(), dtype=torch.int32, device=dev)
+    lists = torch.empty((cap, 64), dtype=torch.int32, device=dev)
+    seq_lens = seq_lens.contiguous()
+    e = src.numel()
+    _launch("radius_chunks", 12 * (n_pos + 1) + 16 * cap, 0, lambda: _check(
+        _lib().mantis_radius_chunks(_ptr(cell_off), _ptr(seq_lens), extra, n_pos, n, n_src, _ptr(chunks), cap,
+                                    _ptr(n_chunks), _ptr(error_flag(dev)), _stream()), "radius_chunks"))
+    # per row: its bounds (twice), the previous stage's bounds, its initial
+    # row and its record; per entry: stone and class in, packed out (the
+    # stones read twice)
+    _launch("radius_prep", 8 * n * (2 + (2 if pre_ptr is not None else 0) + (1 if init_idx is not None else 0))
+            + 16 * n + 28 * e, 0, lambda: _check(
+        _lib().mantis_radius_prep(_ptr(chunks), _ptr(n_chunks), cap, _ptr(seg_ptr), n, _ptr(src), _ptr(cls), e, n_src,
+                                  n_classes, _ptr(pre_ptr), pre_entries, _ptr(init_idx), n_init, _ptr(slots),
+                                  _ptr(packed), _ptr(lists), _ptr(error_flag(dev)), _stream()), "radius_prep"))
+    return RadiusPlan(chunks, n_chunks, slots, packed, lists, n_src)
+
+
+def radius_stage(x: Tensor, plan: RadiusPlan, wq: Tensor, bq: Tensor, kv: Tensor, bias: Tensor, vcls: Tensor,
+                 wo: Tensor, bo: Tensor, pre_bias: Tensor | None = None, init_table: Tensor | None = None) -> Tensor:
+    """In place on fp16 rows x (n, 128): the cells <- stones sub-stage over
+    the plan's chunks with their stones staged on chip (mantis_radius_stage).
+    kv (n_src, 256) fp16 head-interleaved k|v, bias (4, classes), vcls
+    (classes, 128) fp16 head-interleaved.  pre_bias: added first to the rows
+    the plan flags (their previous-stage run is empty); init_table: such rows
+    start from init_table[their initial row] (x is then not read for them)."""
+    dev = _on_gpu(x, plan.chunks, wq, bq, kv, bias, vcls, wo, bo, pre_bias, init_table)
+    n = x.shape[0]
+    if x.ndim != 2 or x.shape[1] != 128 or x.dtype != torch.float16 or x.stride(1) != 1:
+        raise ValueError("x must be fp16 (n, 128) rows")
+    if plan.slots.shape != (n, 4):
+        raise ValueError("the plan was made for another number of rows")
+    for t, name in ((wq, "wq"), (wo, "wo")):
+        if t.shape != (128, 128) or t.dtype != torch.float16 or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous fp16 (128, 128) matrix")
+    for t, name in ((bq, "bq"), (bo, "bo")):
+        if t.shape != (128,) or t.dtype != torch.float32 or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous fp32 vector of 128")
+    if kv.ndim != 2 or kv.shape[1] != 256 or kv.dtype != torch.float16 or kv.stride(1) != 1:
+        raise ValueError("kv must be fp16 (n_src, 256) rows")
+    if kv.shape[0] != plan.n_src:
+        raise ValueError("kv must have the plan's stone count of rows")
+    if bias.ndim != 2 or bias.shape[0] != 4:
+        raise ValueError("bias must have shape (4, classes)")
+    bias = bias.float().contiguous()
+    if vcls.shape != (bias.shape[1], 128):
+        raise ValueError("vcls must have shape (classes, 128)")
+    vcls = vcls.to(torch.float16).contiguous()
+    if pre_bias is not None and (pre_bias.shape != (128,) or pre_bias.dtype != torch.float32):
+        raise ValueError("pre_bias must be fp32 (128,)")
+    if init_table is not None:
+        if init_table.dtype != x.dtype or init_table.ndim != 2 or init_table.shape[1] != 128 or init_table.stride(1) != 1:
+            raise ValueError("the initial-state table must be (n, 128) rows of x's dtype")
+        if init_table.data_ptr() == x.data_ptr():
+            raise ValueError("the initial-state table must not be x")
+    e = plan.packed.numel()
+    if n:
+        # x read and written once (pre-empty rows of the first pass read a
+        # cached table row instead); per row its record, per entry its packed
+        # word; each stone's k|v row once
+        nbytes = n * 256 * (2 if init_table is None else 1) + 16 * n + 4 * e + kv.shape[0] * 512
+        flops = 2 * n * 128 * 128 * 2 + e * 4 * 128 * 2
+        _launch("radius_stage_f16", nbytes, flops, lambda: _check(
+            _lib().mantis_radius_stage(
+                _ptr(x), x.stride(0), n, _ptr(plan.slots), _ptr(plan.chunks), _ptr(plan.n_chunks),
+                plan.chunks.shape[0], _ptr(plan.lists), _ptr(wq), _ptr(bq), _ptr(kv), kv.stride(0), kv.shape[0],
+                _ptr(bias), bias.shape[1], _ptr(vcls), _ptr(plan.packed), e, _ptr(wo), _ptr(bo),
+                _ptr(None if pre_bias is None else pre_bias.contiguous()), _ptr(init_table),
+                init_table.stride(0) if init_table is not None else 0,
+                init_table.shape[0] if init_table is not None else 0,
+                _ptr(error_flag(dev)), _ptr(tile_counters(dev)), _stream()),
+            "radius_stage"))
+    return x
+
+
 def cell_heads(c: Tensor, w1: Tensor, b1: Tensor, w2: Tensor, w3: Tensor, b3: Tensor, pre: Tensor,
                act_table: Tensor, empty_rows: Tensor, act_empty: Tensor, head_tab: Tensor, g_half: Tensor,
                cell_pos: Tensor, dec_ptr: Tensor, dec_window: Tensor, act_class: Tensor, dec_class: Tensor,

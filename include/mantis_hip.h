@@ -435,6 +435,87 @@ int32_t mantis_attention_substages_init(void* x, int32_t x_dtype, int64_t ldx, i
                                         void* stream);
 
 /*
+ * One sub-stage (as mantis_attention_substages) over the rows of x whose run
+ * of the stage is non-empty; the other rows are neither read nor written (a
+ * later mantis_radius_stage with pre_bias = this stage's bo adds the stage's
+ * output bias to them, which is all the stage does to such a row).  With
+ * x_init (may be NULL), the rows it updates start from x_init row init_cover
+ * (init_idx may then be NULL: only skipped rows would read it).
+ * The first half of the cell-state pass (cells <- windows over the cells with
+ * decoder entries; model.py:397-490, cell_latents.py:213-285, 834-1001).
+ */
+int32_t mantis_attention_substages_covered(void* x, int32_t x_dtype, int64_t ldx, int64_t n_rows,
+                                           const int32_t* row_order, const mantis_substage* stage,
+                                           const void* x_init, int64_t ld_init, int64_t n_init,
+                                           const int64_t* init_idx, int64_t init_cover, int32_t* err_flag,
+                                           uint32_t* tile_counters, void* stream);
+
+/*
+ * The cells <- stones sub-stage with each chunk's stones staged on chip
+ * (replaces the second half of the reference's _cell_stage, model.py:397-490,
+ * over the radius edges of cell_nodes.py:23-94; kernel cell_latents.py:213-285).
+ * Three calls:
+ *   mantis_radius_chunks   position p's rows [cell_off[p], cell_off[p + 1])
+ *                          (cell_off must tile [0, n_rows); else
+ *                          MANTIS_FLAG_ORDER) cut into chunks of up to 512
+ *                          consecutive rows, each with the position's first
+ *                          stone (the stones of the positions before it,
+ *                          seq_lens[q] - extra each); chunks: max_chunks x 4
+ *                          int32, max_chunks >= mantis_radius_chunks_capacity;
+ *                          *n_chunks (device int32) receives the count.  One
+ *                          workgroup, no host synchronisation.
+ *   mantis_radius_prep     per chunk: its stones (up to 64, listed in
+ *                          list[chunk * 64 ..]), one 16-byte record per slot
+ *                          (slots: n_rows x 4 int32: row, first entry, entry
+ *                          count | 1 << 30 when pre_ptr's run of the row is
+ *                          empty, init_idx[row] or -1), the chunk's rows
+ *                          sorted by entry count into its slots, and every
+ *                          entry packed (int32: the stone's place in the
+ *                          chunk's list, or 1 << 30 | the global stone index,
+ *                          then << 8 | class; -1 and MANTIS_FLAG_INDEX for a
+ *                          stone or class out of range).  seg_ptr: the CSR of
+ *                          the entries (src, cls) over the rows; n_src <
+ *                          2^22, n_classes <= 256.  The plan of one batch,
+ *                          shared by every block.
+ *   mantis_radius_stage    per fp16 row r of x (n_rows, row stride ldx):
+ *                            x[r] += pre_bias     when its record says pre_ptr's
+ *                                                 run is empty (pre_bias may be
+ *                                                 NULL); with x_init such a row
+ *                                                 starts from x_init[init_idx[r]]
+ *                                                 (out of [0, n_init): from zero,
+ *                                                 MANTIS_FLAG_INDEX)
+ *                            x[r] += attend(LN(x[r]) wq^T + bq, ...) wo^T + bo
+ *                          over its entries, k/v the two 128-wide halves of the
+ *                          fp16 kv rows (head-interleaved, row stride ldkv),
+ *                          bias (4, n_classes) fp32, vcls (n_classes, 128)
+ *                          fp16 head-interleaved, n_classes <= 192.  Each
+ *                          row's arithmetic is that of
+ *                          mantis_attention_substages, so this call after
+ *                          mantis_attention_substages_covered gives bitwise the
+ *                          rows of the two-stage pass.  An entry whose stone
+ *                          is not in its chunk's list reads k and v from global
+ *                          memory: the results do not depend on the lists.
+ *                          tile_counters as for mantis_attention_substages
+ *                          (required).
+ */
+int64_t mantis_radius_chunks_capacity(int64_t n_rows, int64_t n_pos);
+int32_t mantis_radius_chunks(const int64_t* cell_off, const int32_t* seq_lens, int32_t extra, int64_t n_pos,
+                             int64_t n_rows, int64_t n_src, int32_t* chunks, int64_t max_chunks, int32_t* n_chunks,
+                             int32_t* err_flag, void* stream);
+int32_t mantis_radius_prep(int32_t* chunks, const int32_t* n_chunks, int64_t max_chunks, const int64_t* seg_ptr,
+                           int64_t n_rows, const int64_t* src, const int64_t* cls, int64_t n_entries, int64_t n_src,
+                           int64_t n_classes, const int64_t* pre_ptr, int64_t n_pre, const int64_t* init_idx,
+                           int64_t n_init, int32_t* slots, int32_t* packed, int32_t* list, int32_t* err_flag,
+                           void* stream);
+int32_t mantis_radius_stage(void* x, int64_t ldx, int64_t n_rows, const int32_t* slots, const int32_t* chunks,
+                            const int32_t* n_chunks, int64_t max_chunks, const int32_t* list, const void* wq,
+                            const float* bq, const void* kv, int64_t ldkv, int64_t n_src, const float* bias,
+                            int64_t n_classes, const void* vcls, const int32_t* packed, int64_t n_entries,
+                            const void* wo, const float* bo, const float* pre_bias, const void* x_init,
+                            int64_t ld_init, int64_t n_init, int32_t* err_flag, uint32_t* tile_counters,
+                            void* stream);
+
+/*
  * Fused cell heads: for every legal cell r (position cell_pos[r]) with
  * decoder entries e in [dec_ptr[r], dec_ptr[r+1]):
  *   x    = fp16(LN(c[r])) if layer_norm (no affine: fold it into w1/b1), else fp16(c[r])

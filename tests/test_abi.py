@@ -81,3 +81,20 @@ def test_every_ops_call_passes_the_declared_argument_count():
         assert n == decls[name], (name, n, decls[name])
         seen += 1
     assert seen >= 20
+
+
+def test_noalloc_size_guard_holds_at_int64_scale_counts():
+    # the workspace size and the no-allocation entry point's guard with counts
+    # whose byte products would overflow int64: the guard answers
+    # MANTIS_E_SIZE before any device call (none is made: the pointers are
+    # never dereferenced, so stand-in addresses serve), and the size query -1
+    hip = _native.hip()
+    assert hip.mantis_stable_key_order_workspace(10, 3) == 16 + 80
+    for n_entries, n_keys in ((0, 2 ** 62), (2 ** 61, 1), (2 ** 63 - 1, 2 ** 63 - 1), (2 ** 60 + 1, 2 ** 61)):
+        assert hip.mantis_stable_key_order_workspace(n_entries, n_keys) == -1
+    fake = ctypes.c_void_p(0x1000)
+    limit = 40 << 20
+    for n_entries, n_keys in ((0, 2 ** 62), (2 ** 61, 1), (2 ** 63 - 1, 2 ** 63 - 1), (limit // 8 + 1, 1),
+                              (0, limit // 4 + 1)):
+        rc = hip.mantis_stable_key_order_noalloc(fake, fake, fake, n_entries, n_keys, fake, fake, fake, None, None)
+        assert rc == 3, (n_entries, n_keys, rc)

@@ -774,6 +774,16 @@ def test_latent_read_from_the_window_rows_matches_the_projected_read(device):
     ops.latent_read_x(d(qp.to(H16)), d(x2), d(offsets), d(bad), *args)
     with pytest.raises(ValueError):
         ops.raise_on_device_error(device)
+    # a malformed layout (offsets decreasing, or past n_w) is flagged, not
+    # read quietly from a clamped range
+    for i, value in ((6, int(offsets[5]) - 1), (n_pos, n_w + 3)):
+        bad_off = offsets.clone()
+        bad_off[i] = value
+        ops.latent_read_x(d(qp.to(H16)), d(x), d(bad_off), None, *args)
+        with pytest.raises(ValueError):
+            ops.raise_on_device_error(device)
+    ops.latent_read_x(d(qp.to(H16)), d(x), d(offsets), None, *args)
+    ops.raise_on_device_error(device)
 
 
 def test_latent_mix_matches_the_fp32_formulation(device):
