@@ -71,11 +71,30 @@ def _args():
                     help="run only the isolated attention and message-passing lines (for kernel profiling)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only copy MIB mebibytes device-to-device once and exit (HBM counter calibration)")
+    ap.add_argument("--split-cell-stages", action="store_true",
+                    help="run the cell pass as two launches (the decoder sub-stage over the covered cells, then the "
+                         "radius sub-stage with each chunk's stones staged on chip) instead of the fused launch")
+    ap.add_argument("--no-late-game", action="store_true",
+                    help="skip the configs[4] sub-line (B=1024 positions of 150-250 stones)")
+    ap.add_argument("--late-steps", type=int, default=5, help="timed steps of the configs[4] sub-line")
     return ap.parse_args()
 
 
 def _log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def _counters():
+    """The committed rocprofv3 PMC breakdown of the forward's large kernels
+    (texture address/data units, L1 stalls, L2->L1 requests, VALU and MFMA
+    busy), per bench.py trace name."""
+    f = ROOT / "profiles" / "counters.json"
+    if f.exists():
+        try:
+            return json.loads(f.read_text())
+        except ValueError:
+            return None
+    return None
 
 
 def _traffic():
@@ -107,17 +126,57 @@ def _cold(torch, ops, dev, name, launch, reps):
     return tr.summary()[name]
 
 
-def isolated_attention(torch, ops, dev, reps=20):
-    """configs[1]: B=256 sequences, L ~ U{64..512}, 8 heads, hd 32, N(0,1)."""
+def configs1_inputs(torch, dev):
+    """The configs[1] instance: seeded lengths L ~ U{64..512} of B=256
+    sequences (int32), and for fp16 then bf16 the N(0,1) q, k, v in the
+    model's layout ((B, T, 8, 32) storage viewed as (B, 8, T, 32))."""
     import numpy as np
 
     rng = np.random.default_rng([2, 0])
     b, h, t = 256, 8, 512
     lens = torch.from_numpy(rng.integers(64, 513, b).astype(np.int32))
     gen = torch.Generator(device="cpu").manual_seed(2)
+    qkv = {}
+    for dtype in (torch.float16, torch.bfloat16):
+        qkv[dtype] = [torch.randn(b, t, h, 32, generator=gen).to(dtype).to(dev).transpose(1, 2) for _ in range(3)]
+    return lens, qkv
+
+
+def configs2_inputs(torch, dev):
+    """The configs[2] instance: 256 graphs, graph j the first N_j ~
+    U{64..512} legal cells (engine order) of a seeded 40-120-stone position;
+    (cells_qr int32 (N, 2), graph_ptr int64 (257,), x bf16 (N, 128), w bf16
+    (128, 128), bias fp32 (128,)), all on dev."""
+    import numpy as np
+
+    from mantisnet import builder, synthetic
+
+    games = synthetic.random_games(3, 256)
+    cells, sizes = [], []
+    for j, g in enumerate(games):
+        legal, _, _ = builder.legal_moves(g)
+        n = int(np.random.default_rng([3, j, 1]).integers(64, 513))
+        cells.append(legal[:n])
+        sizes.append(min(n, len(legal)))
+    qr = torch.from_numpy(np.concatenate(cells).astype(np.int32)).to(dev)
+    gptr = torch.from_numpy(np.concatenate([[0], np.cumsum(sizes)]).astype(np.int64)).to(dev)
+    n = qr.shape[0]
+    gen = torch.Generator(device="cpu").manual_seed(3)
+    x = torch.randn(n, 128, generator=gen).to(torch.bfloat16).to(dev)
+    # the layer's weight in the kernel's operand format once, as a model keeps
+    # its parameters: no conversion between the timed launches
+    w = (torch.randn(128, 128, generator=gen) / math.sqrt(128)).to(torch.bfloat16).to(dev)
+    bias = (0.02 * torch.randn(128, generator=gen)).to(dev)
+    return qr, gptr, x, w, bias
+
+
+def isolated_attention(torch, ops, dev, reps=20):
+    """configs[1]: B=256 sequences, L ~ U{64..512}, 8 heads, hd 32, N(0,1)."""
+    lens, qkv_all = configs1_inputs(torch, dev)
+    h, t = 8, 512
     res = {}
     for dtype, name in ((torch.float16, "fp16"), (torch.bfloat16, "bf16")):
-        qkv = [torch.randn(b, t, h, 32, generator=gen).to(dtype).to(dev).transpose(1, 2) for _ in range(3)]
+        qkv = qkv_all[dtype]
         sl = lens.to(dev)
         ops.register_seq_lens(sl)
         # the longest-first work order depends on the lengths only: built once,
@@ -154,26 +213,8 @@ def isolated_attention(torch, ops, dev, reps=20):
 def isolated_message_passing(torch, ops, dev, reps=20):
     """256 graphs = first N_j ~ U{64..512} legal cells of seeded
     40-120-stone positions; 6-neighbour sum and mean, Linear(128,128), bf16."""
-    import numpy as np
-
-    from mantisnet import builder, synthetic
-
-    games = synthetic.random_games(3, 256)
-    cells, sizes = [], []
-    for j, g in enumerate(games):
-        legal, _, _ = builder.legal_moves(g)
-        n = int(np.random.default_rng([3, j, 1]).integers(64, 513))
-        cells.append(legal[:n])
-        sizes.append(min(n, len(legal)))
-    qr = torch.from_numpy(np.concatenate(cells).astype(np.int32)).to(dev)
-    gptr = torch.from_numpy(np.concatenate([[0], np.cumsum(sizes)]).astype(np.int64)).to(dev)
+    qr, gptr, x, w, bias = configs2_inputs(torch, dev)
     n = qr.shape[0]
-    gen = torch.Generator(device="cpu").manual_seed(3)
-    x = torch.randn(n, 128, generator=gen).to(torch.bfloat16).to(dev)
-    # the layer's weight in the kernel's operand format once, as a model keeps
-    # its parameters: no conversion between the timed launches
-    w = (torch.randn(128, 128, generator=gen) / math.sqrt(128)).to(torch.bfloat16).to(dev)
-    bias = (0.02 * torch.randn(128, generator=gen)).to(dev)
     nbr = ops.hex_neighbours(qr, gptr)
     for _ in range(3):
         ops.hex_aggregate_linear(x, nbr, w, bias)
@@ -314,6 +355,62 @@ def cpu_baseline(torch, net, games, sample: int, reps: int):
     }
 
 
+TRACED = ("attention_substage", "cell_attention", "cell_heads", "fused_linear", "stone_attention", "run_reduce",
+          "runs_to_ptr", "latent_", "row_encode", "layer_norm", "value_read", "compose_q", "gather_rows", "plan_check",
+          "stable_key_order", "radius_class", "attention_slots", "covered_rows", "window_view", "segment_order",
+          "radius_")
+
+
+def time_workload(torch, ops, net, dev, config: int, batch_size: int, steps: int, warmup: int) -> dict:
+    """One workload: seeded positions of BASELINE config ``config`` (4:
+    40-120 stones, 5: 150-250), encoded and copied to the device, then
+    ``warmup`` forwards, ``steps`` device-synchronised timed forwards
+    (untraced: the tracer's per-launch HIP events cost host time between
+    launches) and a traced pass of the same length for the per-kernel figures."""
+    from mantisnet import collate_positions, synthetic
+
+    t0 = time.perf_counter()
+    games = synthetic.random_games(config, batch_size)
+    t_gen = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    batch = collate_positions(games)
+    t_enc = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    bd = batch.to(dev)
+    torch.cuda.synchronize()
+    t_h2d = time.perf_counter() - t0
+    _log(f"config {config}: B={batch_size} cells={batch.n_cells} windows={batch.window_feat.numel()} "
+         f"stones={batch.stone_own.numel()} (generate {t_gen:.2f}s, encode {t_enc:.2f}s, h2d {t_h2d:.3f}s)")
+    with torch.no_grad():
+        for _ in range(warmup):
+            net(bd, 0.2)
+        torch.cuda.synchronize()
+        ops.raise_on_device_error(dev)
+        _log(f"warm-up done ({warmup} steps)")
+        per_step = []
+        torch.cuda.synchronize()
+        t_start = time.perf_counter()
+        for _ in range(steps):
+            s0 = time.perf_counter()
+            net(bd, 0.2)
+            torch.cuda.synchronize()
+            per_step.append(time.perf_counter() - s0)
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t_start
+        ops.raise_on_device_error(dev)
+        with ops.trace(*TRACED) as tr:
+            for _ in range(steps):
+                net(bd, 0.2)
+            torch.cuda.synchronize()
+        kernels = tr.summary()
+        ops.raise_on_device_error(dev)
+    ms = 1e3 * elapsed / steps
+    value = batch_size * steps / elapsed
+    _log(f"config {config}: timed {steps} steps: {ms:.3f} ms/step, {value:.1f} positions/s")
+    return {"games": games, "batch": batch, "bd": bd, "kernels": kernels, "ms": ms, "value": value,
+            "per_step": per_step, "encode_s": t_enc, "h2d_s": t_h2d}
+
+
 def main() -> int:
     args = _args()
     if args.gpus != 1:
@@ -344,63 +441,29 @@ def main() -> int:
                           "message_passing": isolated_message_passing(torch, ops, dev)}), flush=True)
         return 0
 
+    if args.split_cell_stages:
+        from mantisnet import forward as fwd
+
+        fwd.SPLIT_CELL_STAGES = True
+
     torch.manual_seed(0)
     net = MantisNet(PRODUCTION)
     net.load_state_dict(synthetic.perturbed_state_dict(net, seed=0))
     net = net.to(dev).eval()
 
-    t0 = time.perf_counter()
-    games = synthetic.random_games(args.config, args.batch)
-    t_gen = time.perf_counter() - t0
-    t0 = time.perf_counter()
-    batch = collate_positions(games)
-    t_enc = time.perf_counter() - t0
-    t0 = time.perf_counter()
-    bd = batch.to(dev)
-    torch.cuda.synchronize()
-    t_h2d = time.perf_counter() - t0
-    _log(f"config {args.config}: B={args.batch} cells={batch.n_cells} windows={batch.window_feat.numel()} "
-         f"stones={batch.stone_own.numel()} (generate {t_gen:.2f}s, encode {t_enc:.2f}s, h2d {t_h2d:.3f}s)")
-
-    with torch.no_grad():
-        for _ in range(args.warmup):
-            net(bd, 0.2)
-        torch.cuda.synchronize()
-        ops.raise_on_device_error(dev)
-        _log(f"warm-up done ({args.warmup} steps)")
-        # the timed steps run untraced: the per-launch HIP events of the
-        # tracer cost host time between launches, so the per-kernel figures
-        # come from a separate traced pass over the same number of steps
-        per_step = []
-        torch.cuda.synchronize()
-        t_start = time.perf_counter()
-        for _ in range(args.steps):
-            s0 = time.perf_counter()
-            net(bd, 0.2)
-            torch.cuda.synchronize()
-            per_step.append(time.perf_counter() - s0)
-        torch.cuda.synchronize()
-        elapsed = time.perf_counter() - t_start
-        ops.raise_on_device_error(dev)
-        traced = ("attention_substage", "cell_attention", "cell_heads", "fused_linear", "stone_attention", "run_reduce",
-                  "runs_to_ptr", "latent_", "row_encode", "layer_norm", "value_read", "compose_q", "gather_rows",
-                  "plan_check", "stable_key_order", "radius_class", "attention_slots", "covered_rows", "window_view",
-                  "segment_order", "radius_", "pack_entries")
-        with ops.trace(*traced) as tr:
-            for _ in range(args.steps):
-                net(bd, 0.2)
-            torch.cuda.synchronize()
-        kernels = tr.summary()
-        ops.raise_on_device_error(dev)
-    ms = 1e3 * elapsed / args.steps
-    value = args.batch * args.steps / elapsed
-    _log(f"timed {args.steps} steps: {ms:.3f} ms/step, {value:.1f} positions/s")
+    run = time_workload(torch, ops, net, dev, args.config, args.batch, args.steps, args.warmup)
+    games, batch, bd, kernels = run["games"], run["batch"], run["bd"], run["kernels"]
+    ms, value, per_step = run["ms"], run["value"], run["per_step"]
+    t_enc, t_h2d = run["encode_s"], run["h2d_s"]
 
     dom_name, dom = max(kernels.items(), key=lambda kv: kv[1]["total_ms"])
     traffic = _traffic()
+    counters = _counters()
     # the committed counters belong to one workload; other configurations report none
     if (traffic or {}).get("_workload") != {"config": args.config, "batch": args.batch}:
         traffic = None
+    if (counters or {}).get("_workload") != {"config": args.config, "batch": args.batch}:
+        counters = None
     roofline = {
         "kernel": dom_name,
         "bound": "hbm",
@@ -414,6 +477,11 @@ def main() -> int:
         "share_of_step": round(dom["total_ms"] / args.steps / ms, 4),
         "traced_pass": f"{args.steps} further steps with HIP events around each traced launch",
     }
+    if counters and dom_name in counters:
+        # what actually binds the dominant kernel: its committed PMC breakdown
+        # (the algorithmic-bytes fraction above is against HBM; the kernel is
+        # bound by its gathers' path through the texture units and L1)
+        roofline["limiter"] = counters[dom_name]
     line = {
         "metric": "positions evaluated/sec (MantisNet fwd, B=512)",
         "value": round(value, 2),
@@ -436,10 +504,37 @@ def main() -> int:
             "windows": int(batch.window_feat.numel()),
             "encode_s": round(t_enc, 3),
             "h2d_s": round(t_h2d, 4),
+            "cell_pass": "split (decoder launch + radius launch, stones on chip)" if args.split_cell_stages
+            else "fused (both cell sub-stages in one launch)",
         },
         "roofline": roofline,
         "kernels": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in kernels.items()},
     }
+    if not args.no_late_game and args.config == 4:
+        # the late-game stress batch, timed the same way (its own
+        # warm-up, plain timed steps, a traced pass for the per-kernel figures)
+        late = time_workload(torch, ops, net, dev, 5, 1024, args.late_steps, 2)
+        kl = late["kernels"]
+        ld_name, ld = max(kl.items(), key=lambda kv: kv[1]["total_ms"])
+        line["configs4"] = {
+            "metric": "positions evaluated/sec (MantisNet fwd, B=1024, 150-250 stones)",
+            "value": round(late["value"], 2),
+            "unit": "positions/s",
+            "steps": args.late_steps,
+            "warmup": 2,
+            "ms_per_step": round(late["ms"], 4),
+            "median_ms_per_step": round(1e3 * statistics.median(late["per_step"]), 4),
+            "cells": int(late["batch"].n_cells),
+            "windows": int(late["batch"].window_feat.numel()),
+            "stones": int(late["batch"].stone_own.numel()),
+            "dominant_kernel": {"kernel": ld_name, "avg_us": round(ld["avg_us"], 2),
+                                "launches_per_step": ld["launches"] // args.late_steps,
+                                "share_of_step": round(ld["total_ms"] / args.late_steps / late["ms"], 4),
+                                "achieved_gbps": round(ld["gbps"], 1),
+                                "frac_of_hbm": round(ld["gbps"] / HBM_PEAK_GBPS, 4)},
+        }
+        _log(f"configs[4]: {line['configs4']}")
+        del late
     if not args.no_seam:
         line["seam"] = seam_timing(torch, net, bd, min(args.steps, 10))
         _log(f"seam: {line['seam']}")

@@ -322,7 +322,6 @@ class MantisNet(nn.Module):
             "bin_centers", torch.linspace(-1.0, 1.0, cfg.value_bins), persistent=False
         )
         self._init_weights()
-        self._plan_cache = None
 
     def _init_weights(self) -> None:
         """The reference's initialisation (model.py:775-812): embeddings and
