@@ -89,6 +89,7 @@ struct HeadArgs {
   int64_t n_acls;
   const float* empty_rows;   // (3, 128)
   const int64_t* act_empty;  // (n_cells, 3)
+  const float* acts_add;     // (n_cells, 128) added to the action sums, or null
   const _Float16* head_tab;   // (n_dcls, 256), quad-chunked columns
   int64_t n_dcls;
   const float* g_half;       // (n_pos, 256)
@@ -320,6 +321,18 @@ __global__ void __launch_bounds__(kThreads) cell_heads_kernel(HeadArgs a) {
             for (int t = 0; t < 8; ++t) av[8 * i + t] = fmaf(n, r[t], av[8 * i + t]);
           }
         }
+        // a per-cell row joining the same fp32 sums last (the tactical
+        // scalars' MLP output, model.py:1058-1062)
+        if (a.acts_add) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float4 r0 = *reinterpret_cast<const float4*>(a.acts_add + arow * kK + 32 * i + 8 * aq);
+            const float4 r1 = *reinterpret_cast<const float4*>(a.acts_add + arow * kK + 32 * i + 8 * aq + 4);
+            const float r[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
+#pragma unroll
+            for (int t = 0; t < 8; ++t) av[8 * i + t] += r[t];
+          }
+        }
       }
     }
     // g_half[pos]: from the wavefront's staged row when every cell of the
@@ -448,7 +461,8 @@ extern "C" int32_t mantis_cell_heads(const void* c, int32_t c_dtype, int32_t lay
                                      const int32_t* row_order, const void* w1, const float* b1,
                                      const void* w2, const void* w3, const float* b3, const void* pre, int64_t n_w,
                                      const void* act_table, int64_t n_acls, const float* empty_rows,
-                                     const int64_t* act_empty, const void* head_tab, int64_t n_dcls,
+                                     const int64_t* act_empty, const float* acts_add, const void* head_tab,
+                                     int64_t n_dcls,
                                      const float* g_half, int64_t n_pos, const int64_t* cell_pos,
                                      const int64_t* dec_ptr, const int64_t* dec_window, const int64_t* act_class,
                                      const int64_t* dec_class, int64_t n_entries, float* out, int32_t* err_flag,
@@ -469,10 +483,10 @@ extern "C" int32_t mantis_cell_heads(const void* c, int32_t c_dtype, int32_t lay
                         static_cast<const void*>(empty_rows), head_tab,
                         static_cast<const void*>(g_half), static_cast<const void*>(out)})
     if (!aligned16(p)) return MANTIS_E_ARG;
-  if (pre && !aligned16(pre)) return MANTIS_E_ARG;
+  if ((pre && !aligned16(pre)) || (acts_add && !aligned16(acts_add))) return MANTIS_E_ARG;
   HeadArgs a{c, ldc, n_cells, static_cast<const _Float16*>(w1), b1, static_cast<const _Float16*>(w2),
              static_cast<const _Float16*>(w3), b3, static_cast<const _Float16*>(pre), n_w,
-             static_cast<const _Float16*>(act_table), n_acls, empty_rows, act_empty,
+             static_cast<const _Float16*>(act_table), n_acls, empty_rows, act_empty, acts_add,
              static_cast<const _Float16*>(head_tab), n_dcls, g_half, n_pos, cell_pos, dec_ptr, dec_window, act_class,
              dec_class, n_entries, out, row_order, err_flag,
              tile_counters ? tile_counters : counters_for_current_device()};

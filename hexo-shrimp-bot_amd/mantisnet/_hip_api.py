@@ -68,8 +68,8 @@ SIGNATURES = {
     "mantis_radius_stage": ([vp, i64, i64, vp, vp, vp, i64, vp, vp, vp, vp, i64, i64, vp, i64, vp, vp, i64, vp, vp,
                              vp, vp, i64, i64, vp, vp, vp], i32),
     "mantis_cell_heads": (
-        [vp, i32, i32, i32, i64, i64, vp, vp, vp, vp, vp, vp, vp, i64, vp, i64, vp, vp, vp, i64, vp, i64, vp, vp, vp, vp, vp,
-         i64, vp, vp, vp, vp], i32),
+        [vp, i32, i32, i32, i64, i64, vp, vp, vp, vp, vp, vp, vp, i64, vp, i64, vp, vp, vp, vp, i64, vp, i64, vp, vp, vp,
+         vp, vp, i64, vp, vp, vp, vp], i32),
     "mantis_improve_policy": ([vp, vp, vp, i32, vp, i64, i64, ctypes.c_double, ctypes.c_double, vp, vp, vp, vp, vp, vp],
                               i32),
     "mantis_latent_mix": ([vp, i64, i64, vp, vp, vp, vp, vp], i32),

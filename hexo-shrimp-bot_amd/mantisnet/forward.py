@@ -44,10 +44,13 @@ cell_tables and cell_node_edge_tables) are derived once per batch on the
 device and shared by the trunk and the heads.
 
 Scope: the production cell-state configuration (``cell_nodes=True``, either
-node scope) and the knob-off default (no cell state: the transient cell pass
-of model.py:374-395, and heads over the decoder's window sums), H = 128, 4
-heads of 32, 4 value queries.  Other knob combinations raise
-``NotImplementedError``; the forward is inference-only.
+node scope, with or without the six-neighbour cell stage ``cell_adjacency``),
+covered-only cell latents (``cell_latents`` without cell nodes) and the
+knob-off default (no cell state: the transient cell pass of
+model.py:374-395, and heads over the decoder's window sums), either with the
+tactical action scalars (``action_tactical``); H = 128, 4 heads of 32, 4
+value queries.  Other knob combinations raise ``NotImplementedError``; the
+forward is inference-only.
 """
 
 from __future__ import annotations
@@ -70,11 +73,8 @@ ORBIT48 = 48
 
 def _supported(model) -> torch.device:
     cfg = model.cfg
-    if cfg.cell_latents and not cfg.cell_nodes:
-        raise NotImplementedError("the MI355X forward implements cell_nodes=True or the knob-off cell pass, "
-                                  "not covered-only cell latents")
-    if cfg.cell_adjacency or cfg.cell_structure or cfg.action_tactical:
-        raise NotImplementedError("cell_adjacency / cell_structure / action_tactical are not implemented")
+    if cfg.cell_structure:
+        raise NotImplementedError("cell_structure is not implemented in the MI355X forward")
     if cfg.h != 128 or cfg.heads != 4 or cfg.value_queries != 4 or cfg.ffn_factor != 2 or cfg.policy_hidden != 128:
         raise NotImplementedError("the MI355X kernels are built for H=128, 4 heads, FFN 256, 4 value queries")
     dev = next(model.parameters()).device
@@ -162,10 +162,18 @@ def _prepare_cell_stage(t, put, P, pb):
     put(pb + "cr_o", _fold(P, None, [pb + "cr_wo"]))
     # class-value rows gathered once per edge: fp16 halves their bytes
     t[pb + "cr_vcls"] = ops.interleave_heads(P[pb + "cr_vclass.weight"]).to(HALF).contiguous()
-    put(pb + "rad_q", _fold(P, pb + "ln_radius_c", [pb + "radius_wq"]))
-    put(pb + "rad_kv", _interleaved(_fold(P, pb + "ln_radius_s", [pb + "radius_wk", pb + "radius_wv"])))
-    put(pb + "rad_o", _fold(P, None, [pb + "radius_wo"]))
-    t[pb + "rad_vcls"] = ops.interleave_heads(P[pb + "radius_vclass.weight"]).to(HALF).contiguous()
+    if pb + "radius_wq.weight" in P:  # cell nodes: the radius stage
+        put(pb + "rad_q", _fold(P, pb + "ln_radius_c", [pb + "radius_wq"]))
+        put(pb + "rad_kv", _interleaved(_fold(P, pb + "ln_radius_s", [pb + "radius_wk", pb + "radius_wv"])))
+        put(pb + "rad_o", _fold(P, None, [pb + "radius_wo"]))
+        t[pb + "rad_vcls"] = ops.interleave_heads(P[pb + "radius_vclass.weight"]).to(HALF).contiguous()
+    if pb + "adj_wq.weight" in P:
+        # the six-neighbour cell stage (cell_adjacency): k/v projected from the
+        # cells themselves
+        put(pb + "adj_q", _fold(P, pb + "ln_adj_q", [pb + "adj_wq"]))
+        put(pb + "adj_kv", _interleaved(_fold(P, pb + "ln_adj_k", [pb + "adj_wk", pb + "adj_wv"])))
+        put(pb + "adj_o", _fold(P, None, [pb + "adj_wo"]))
+        t[pb + "adj_vcls"] = ops.interleave_heads(P[pb + "adj_vclass.weight"]).to(HALF).contiguous()
     put(pb + "wr_q", _fold(P, pb + "ln_wr_w", [pb + "wr_wq"]))
     put(pb + "wr_kv", _interleaved(_fold(P, pb + "ln_wr_c", [pb + "wr_wk", pb + "wr_wv"])))
     put(pb + "wr_o", _fold(P, None, [pb + "wr_wo"]))
@@ -180,10 +188,13 @@ def _prepare(model, P) -> dict[str, Tensor]:
 
     counts = model.pattern_counts.float()
     # the initial-state tables in the stream dtypes: the window table (fp16
-    # in the cell-node configuration) and [nearest-stone rows; cell_base]
-    t["window_table"] = P["window_table.weight"].to(HALF if cfg.cell_nodes else F32).contiguous()
+    # in the cell-state configurations) and [nearest-stone rows; cell_base]
+    # (cell nodes) or cell_base alone (covered-only cell latents)
+    t["window_table"] = P["window_table.weight"].to(HALF if cfg.uses_cell_state else F32).contiguous()
     if cfg.cell_nodes:
         t["cell_table"] = torch.cat([P["cell_nearest_table.weight"], P["cell_base"][None, :]]).to(HALF).contiguous()
+    elif cfg.uses_cell_state:
+        t["cell_base16"] = P["cell_base"][None, :].to(HALF).contiguous()
     for i in range(cfg.blocks):
         pb = f"blocks.{i}."
         put(pb + "u", _fold(P, pb + "ln_ws_s", [pb + "u"]))
@@ -192,7 +203,7 @@ def _prepare(model, P) -> dict[str, Tensor]:
         put(pb + "mlp_w3", _fold(P, None, [pb + "mlp_w.out"]))
         # window class term composed with lin_b: counts @ e_ws @ lin_b^T, per pattern
         t[pb + "ws_tab"] = (counts @ (P[pb + "e_ws.weight"] @ P[pb + "mlp_w.lin_b.weight"].t())).contiguous()
-        if not cfg.cell_nodes:
+        if not cfg.uses_cell_state:
             # knob-off cell pass: u_cp(LN w), the relay, then mlp_cp.  The relay
             # sums u_cp's output over up to 18 windows per cell and six cells per
             # window, so a rounding of these weights adds up coherently: they are
@@ -210,7 +221,7 @@ def _prepare(model, P) -> dict[str, Tensor]:
         wv_, bv_ = _fold(P, pb + "ln_sw_w", [pb + "v"])
         wr_, br_ = _fold(P, pb + "latent_ln_read_w", [pb + "latent_wk_read", pb + "latent_wv_read"])
         wb_, bb_ = _fold(P, pb + "latent_ln_bcast_q", [pb + "latent_wq_bcast"])
-        if cfg.cell_nodes:
+        if cfg.uses_cell_state:
             # fp16 window state: the latent read takes the window rows
             # themselves (its keys and values folded into composed queries and
             # a value projection after the sum) and the broadcast projects its
@@ -442,12 +453,42 @@ class Plan:
         b = self._b
         cell, cls, window, perm = self._decoder[2], self._decoder[1], self._decoder[0], self._decoder[3]
         if self._covers:
-            return ops.window_view(perm, cell, cls, window, self.n_w, self.cell_ptr, b.relay_cell_ptr.shape[0] - 1)
+            return ops.window_view(perm, cell, cls, window, self.n_w, self.cell_ptr, self.n_cov)
         return ops.window_view(perm, cell, cls, window, self.n_w)
 
     @property
     def _covers(self) -> bool:
-        return bool(self._cfg.cell_nodes and getattr(self._b, "relay_cell_ptr", None) is not None)
+        # the covered-cell compaction: for cell nodes when the batch's relay
+        # views give the covered count, always for covered-only cell latents
+        if not self._cfg.uses_cell_state:
+            return False
+        return not self._cfg.cell_nodes or getattr(self._b, "relay_cell_ptr", None) is not None
+
+    @cached_property
+    def n_cov(self) -> int | None:
+        # the number of cells with decoder entries: from the batch's relay views
+        # (one per covered cell), else (covered-only latents) one device read
+        if not self._covers:
+            return None
+        if getattr(self._b, "relay_cell_ptr", None) is not None:
+            return self._b.relay_cell_ptr.shape[0] - 1
+        return int((self.cell_ptr[1:] > self.cell_ptr[:-1]).sum().item())
+
+    @cached_property
+    def cov_ptr(self) -> Tensor | None:
+        # covered-only latents: the cell-major decoder CSR over the covered
+        # cells in compact (ascending) order
+        if not self._covers or self._cfg.cell_nodes:
+            return None
+        return torch.cat([self.cell_ptr.index_select(0, self.cov_rows), self.cell_ptr[-1:]]).contiguous()
+
+    @cached_property
+    def cov_order(self) -> Tensor | None:
+        # the compact cells' tile order: within each position by decoder entries
+        if self.cov_ptr is None:
+            return None
+        seg = torch.searchsorted(self.cov_rows, self._b.legal_offsets).contiguous()
+        return ops.segment_order(seg, self.cov_ptr, None, self.n_cov)
 
     @property
     def win_ptr(self) -> Tensor:
@@ -486,6 +527,22 @@ class Plan:
             rorder = _stable_order(dst)
             src, dst, classes = src[rorder], dst[rorder], classes[rorder]
         return ops.runs_to_ptr(dst.contiguous(), self.n_c), src, classes
+
+    @cached_property
+    def _adjacency(self) -> tuple[Tensor, Tensor, Tensor] | None:
+        # the six-neighbour tables of cell_adjacency (model.py:881-896): one
+        # relation class for all three axes, destination-major (stably sorted:
+        # the batch's order check does not cover these entries)
+        if not (self._cfg.cell_nodes and self._cfg.cell_adjacency):
+            return None
+        b = self._b
+        src, dst = b.adjacency_src, b.adjacency_dst
+        if self._cfg.cell_node_scope == "uncovered":
+            keep = ~(self.cell_ptr[1:] > self.cell_ptr[:-1])[dst]
+            src, dst = src[keep], dst[keep]
+        order = _stable_order(dst)
+        src, dst = src[order].contiguous(), dst[order].contiguous()
+        return ops.runs_to_ptr(dst, self.n_c), src, torch.zeros_like(src)
 
     @property
     def radius_ptr(self) -> Tensor | None:
@@ -527,12 +584,6 @@ class Plan:
     def _n_init(self) -> int:
         # rows of the cells' initial-state table [nearest-stone rows; cell_base]
         return NEAREST_BUCKETS + 1
-
-    @property
-    def n_cov(self) -> int | None:
-        # the number of cells with decoder entries, when the batch's relay
-        # views tell it (trace accounting only)
-        return self._b.relay_cell_ptr.shape[0] - 1 if self._covers else None
 
     @cached_property
     def head_order(self) -> Tensor:
@@ -659,6 +710,16 @@ def _cell_stage(W, P, pb, plan: Plan, s, w, c, c_init=None):
     # cells <- windows (decoder classes, class values) then cells <- stones
     # (radius classes, class values); then windows <- cells (decoder classes).
     # Each sub-stage is LN -> q -> attention -> o -> residual.
+    if not plan._cfg.cell_nodes:
+        # covered-only cell latents: the rows are the covered cells alone, in
+        # compact order; no radius stage
+        cr = _substage(W, P, pb, "cr", _proj(W, pb + "cr_kv", w), "cr_bias", W[pb + "cr_vcls"], plan.cov_ptr,
+                       plan.edge_window, plan.edge_class)
+        ops.attention_substages(c, [cr], row_order=plan.cov_order)
+        wr = _substage(W, P, pb, "wr", _proj(W, pb + "wr_kv", c), "wr_bias", None, plan.win_ptr,
+                       plan.edge_wcell_cov, plan.edge_wclass)
+        ops.attention_substages(w, [wr])
+        return
     cr = _substage(W, P, pb, "cr", _proj(W, pb + "cr_kv", w), "cr_bias", W[pb + "cr_vcls"], plan.cell_ptr,
                    plan.edge_window, plan.edge_class)
     rad_kv = _proj(W, pb + "rad_kv", s)
@@ -677,6 +738,13 @@ def _cell_stage(W, P, pb, plan: Plan, s, w, c, c_init=None):
         rad = _substage(W, P, pb, "rad", rad_kv, "radius_bias", W[pb + "rad_vcls"], plan.radius_ptr,
                         plan.radius_src, plan.radius_class)
         ops.attention_substages(c, [cr, rad], row_order=plan.cell_order, init=c_init)
+    if plan._adjacency is not None:
+        # cells <- their axial neighbours (model.py:463-476), k/v from the
+        # cells after the two sub-stages above
+        adj_ptr, adj_src, adj_cls = plan._adjacency
+        adj = _substage(W, P, pb, "adj", _proj(W, pb + "adj_kv", c), "adj_bias", W[pb + "adj_vcls"], adj_ptr,
+                        adj_src, adj_cls)
+        ops.attention_substages(c, [adj])
     if plan.cov_rows is not None:  # k/v of the covered cells only, entries remapped to them
         wr = _substage(W, P, pb, "wr", _proj(W, pb + "wr_kv", c, x_rows=plan.cov_rows), "wr_bias", None,
                        plan.win_ptr, plan.edge_wcell_cov, plan.edge_wclass)
@@ -817,7 +885,7 @@ def _trunk(model, b: Batch, plan: Plan, raw_cells: bool = False, W: Prepared | N
     # MLP's group add reads the same window_feat entries and flags any out of
     # range, as the gather did.)
     w_init = None
-    if cfg.cell_nodes and cfg.blocks:
+    if cfg.uses_cell_state and cfg.blocks:
         # the fp16 window state: the first block's pair MLP reads the rows'
         # initial state from the table (cached) and writes w
         w = torch.empty((plan.n_w, 128), dtype=HALF, device=b.stone_own.device)
@@ -841,6 +909,9 @@ def _trunk(model, b: Batch, plan: Plan, raw_cells: bool = False, W: Prepared | N
             c_init = (table, b.cell_nearest, table.shape[0] - 1)
         else:
             c = ops.gather_rows(table, b.cell_nearest, cover_ptr=plan.cell_ptr, cover_row=table.shape[0] - 1)
+    elif cfg.uses_cell_state:
+        # covered-only cell latents: the covered cells start from cell_base
+        c = W["cell_base16"].expand(plan.n_cov, 128).contiguous()
     plan.start()
     # residual streams: s and g share one buffer so the attention and FFN
     # launches cover both with one row range
@@ -857,6 +928,12 @@ def _trunk(model, b: Batch, plan: Plan, raw_cells: bool = False, W: Prepared | N
     g_out = F.layer_norm(g, (128,), P["ln_out.weight"], P["ln_out.bias"], 1e-5).mean(dim=1)
     if c is None:
         return w_out, g_out, None
+    if not cfg.cell_nodes:
+        # covered-only latents: every legal cell, the uncovered ones carrying
+        # the base row (model.py:975-983)
+        full = W["cell_base16"].expand(plan.n_c, 128).contiguous()
+        full.index_copy_(0, plan.cov_rows, c)
+        c = full
     cells = c if raw_cells else ops.layer_norm(c, P["ln_out.weight"], P["ln_out.bias"], HALF)
     return w_out, g_out, cells
 
@@ -913,11 +990,18 @@ def _head_rows(model, w: Tensor, g: Tensor, cells: Tensor, b: Batch, plan: Plan,
     g_half = F.linear(g.float(), W["glin_b"]).contiguous()  # (P, 256)
     x = cells if cells.dtype in (HALF, F32) else cells.float()
     key = "head1ln" if raw_cells else "head1"
+    tactical = None
+    if model.cfg.action_tactical:
+        # the tactical scalars' MLP (model.py:1058-1062), fp32, joining the
+        # action sums in the heads kernel: two small library GEMMs over the
+        # (N_c, 11) scalars
+        tactical = F.linear(F.relu(F.linear(b.act_tactical.float(), P["tactical_a.weight"], P["tactical_a.bias"])),
+                            P["tactical_out.weight"], P["tactical_out.bias"]).contiguous()
     return ops.cell_heads(x.contiguous(), W[key + ".w"], W[key + ".b"], W["head2.w"],
                           W["head3c.w" if compensated else "head3.w"], W["head3.b"], pre,
                           W["act_table16"], W["empty_rows"], b.act_empty, W["head_tab_k"], g_half, b.cell_pos,
                           plan.dec_cell_ptr, b.dec_window, b.act_class, b.dec_class, layer_norm=raw_cells,
-                          row_order=plan.head_order, compensated=compensated, tables_ready=True)
+                          row_order=plan.head_order, compensated=compensated, tables_ready=True, acts_add=tactical)
 
 
 @torch.no_grad()

@@ -1182,7 +1182,7 @@ def cell_heads(c: Tensor, w1: Tensor, b1: Tensor, w2: Tensor, w3: Tensor, b3: Te
                act_table: Tensor, empty_rows: Tensor, act_empty: Tensor, head_tab: Tensor, g_half: Tensor,
                cell_pos: Tensor, dec_ptr: Tensor, dec_window: Tensor, act_class: Tensor, dec_class: Tensor,
                layer_norm: bool, row_order: Tensor | None = None, compensated: bool = False,
-               library_counters: bool = False, tables_ready: bool = False) -> Tensor:
+               library_counters: bool = False, tables_ready: bool = False, acts_add: Tensor | None = None) -> Tensor:
     """(n_cells, 16) fp32 head rows of every cell in one launch (see
     mantis_cell_heads in include/mantis_hip.h): column 0 the policy logit,
     1..3 the critic logits.  ``row_order`` (int32 permutation of the cells)
@@ -1192,9 +1192,11 @@ def cell_heads(c: Tensor, w1: Tensor, b1: Tensor, w2: Tensor, w3: Tensor, b3: Te
     as in attention_substages (``library_counters`` likewise).
     ``tables_ready``: act_table is already fp16 and head_tab already the
     kernel's fp16 quad-chunked table (``head_table_for_kernel``), as a caller
-    that prepares them once passes them."""
+    that prepares them once passes them.  ``acts_add`` (n_cells, 128) fp32:
+    a per-cell row joining the action sums last (the tactical scalars' MLP
+    output, model.py:1058-1062)."""
     dev = _on_gpu(c, w1, b1, w2, w3, b3, pre, act_table, empty_rows, act_empty, head_tab, g_half, cell_pos, dec_ptr,
-                  dec_window, act_class, dec_class, row_order)
+                  dec_window, act_class, dec_class, row_order, acts_add)
     if row_order is not None and (row_order.dtype != torch.int32 or row_order.shape != (c.shape[0],)):
         raise ValueError("row_order must be an int32 permutation of the cells")
     n = c.shape[0]
@@ -1230,12 +1232,17 @@ def cell_heads(c: Tensor, w1: Tensor, b1: Tensor, w2: Tensor, w3: Tensor, b3: Te
         raise ValueError("act_empty (n, 3), cell_pos (n,) and dec_ptr (n + 1,) expected")
     if not (dec_window.shape == act_class.shape == dec_class.shape) or dec_window.ndim != 1:
         raise ValueError("the decoder entry views must have one length")
+    if acts_add is not None:
+        if acts_add.shape != (n, 128) or acts_add.dtype != torch.float32:
+            raise ValueError("acts_add must be fp32 (n_cells, 128) rows")
+        acts_add = acts_add.contiguous()
     out = torch.empty((n, 16), dtype=torch.float32, device=dev)
     if n:
         e = dec_window.numel()
         # the cell rows once, the output rows once, per entry its three
         # indices, each action-projection row once
-        nbytes = n * (128 * c.element_size() + 64 + 16 + 24) + e * 24 + pre.shape[0] * 256
+        nbytes = n * (128 * c.element_size() + 64 + 16 + 24 + (512 if acts_add is not None else 0)) + e * 24 + \
+            pre.shape[0] * 256
         flops = n * 2 * (2 * 256 * 128 + 16 * 256)
         _launch("cell_heads", nbytes, flops, lambda: _check(
             _lib().mantis_cell_heads(
@@ -1243,7 +1250,7 @@ def cell_heads(c: Tensor, w1: Tensor, b1: Tensor, w2: Tensor, w3: Tensor, b3: Te
                 _ptr(w2), _ptr(w3),
                 _ptr(b3),
                 _ptr(pre), pre.shape[0], _ptr(act_table), act_table.shape[0], _ptr(empty_rows), _ptr(act_empty),
-                _ptr(head_tab), head_tab.shape[0], _ptr(g_half), g_half.shape[0], _ptr(cell_pos), _ptr(dec_ptr),
+                _ptr(acts_add), _ptr(head_tab), head_tab.shape[0], _ptr(g_half), g_half.shape[0], _ptr(cell_pos), _ptr(dec_ptr),
                 _ptr(dec_window), _ptr(act_class), _ptr(dec_class), e, _ptr(out), _ptr(error_flag(dev)),
                 None if library_counters else _ptr(tile_counters(dev)), _stream(),
             ),

@@ -520,6 +520,7 @@ int32_t mantis_radius_stage(void* x, int64_t ldx, int64_t n_rows, const int32_t*
  * decoder entries e in [dec_ptr[r], dec_ptr[r+1]):
  *   x    = fp16(LN(c[r])) if layer_norm (no affine: fold it into w1/b1), else fp16(c[r])
  *   acts = sum_e relu(pre[dec_window[e]] + act_table[act_class[e]]) + sum_k act_empty[r,k] * empty_rows[k]
+ *          [+ acts_add[r]]
  *   h    = relu(w1 x + w2 fp16(acts) + b1 + sum_e head_tab[dec_class[e]] + g_half[cell_pos[r]])
  *   out[r] = w3 fp16(h) + b3
  * c: (n_cells, 128) rows in c_dtype (fp32 or fp16), row
@@ -527,8 +528,10 @@ int32_t mantis_radius_stage(void* x, int64_t ldx, int64_t n_rows, const int32_t*
  * pre (n_w, 128) and act_table (n_acls, 128) fp16; head_tab (n_dcls, 256)
  * fp16 with quad-chunked columns (column 32*k + 8*q + u holds feature
  * 16*(2*k + u/4) + 4*q + u%4); empty_rows (3, 128), g_half (n_pos, 256) fp32;
- * act_empty (n_cells, 3) and the index arrays int64; out (n_cells, 16) fp32.
- * row_order, when not NULL, is a permutation of the cells (int32) in which
+ * act_empty (n_cells, 3) and the index arrays int64; out (n_cells, 16) fp32;
+ * acts_add (n_cells, 128) fp32 or NULL: a per-cell row joining the fp32
+ * action sums last (the tactical scalars' MLP output of the action_tactical
+ * configuration, model.py:1058-1062).  row_order, when not NULL, is a permutation of the cells (int32) in which
  * they are grouped into 16-cell tiles (see mantis_segment_order); the
  * results do not depend on it.  tile_counters: as for
  * mantis_attention_substages (MANTIS_TILE_COUNTERS zeroed uint32, not
@@ -546,8 +549,8 @@ int32_t mantis_cell_heads(const void* c, int32_t c_dtype, int32_t layer_norm, in
                           int64_t ldc, int64_t n_cells,
                           const int32_t* row_order, const void* w1, const float* b1, const void* w2, const void* w3, const float* b3,
                           const void* pre, int64_t n_w, const void* act_table, int64_t n_acls,
-                          const float* empty_rows, const int64_t* act_empty, const void* head_tab, int64_t n_dcls,
-                          const float* g_half, int64_t n_pos, const int64_t* cell_pos, const int64_t* dec_ptr,
+                          const float* empty_rows, const int64_t* act_empty, const float* acts_add,
+                          const void* head_tab, int64_t n_dcls, const float* g_half, int64_t n_pos, const int64_t* cell_pos, const int64_t* dec_ptr,
                           const int64_t* dec_window, const int64_t* act_class, const int64_t* dec_class,
                           int64_t n_entries, float* out, int32_t* err_flag, uint32_t* tile_counters,
                           void* stream);

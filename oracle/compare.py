@@ -36,12 +36,12 @@ def batch_dict(batch) -> dict:
 
 def cfg_of(model, latent_loops: bool = False) -> R.Cfg:
     c = model.cfg
-    if c.cell_latents and not c.cell_nodes:
-        raise NotImplementedError("the oracle covers cell_nodes=True and the knob-off cell pass")
     return R.Cfg(h=c.h, blocks=c.blocks, heads=c.heads, ffn_factor=c.ffn_factor,
                  value_queries=c.value_queries, value_bins=c.value_bins,
                  policy_hidden=c.policy_hidden, value_hidden=c.value_hidden,
-                 cell_node_scope=c.cell_node_scope, cell_nodes=c.cell_nodes, latent_loops=latent_loops)
+                 cell_node_scope=c.cell_node_scope, cell_nodes=c.cell_nodes, cell_latents=c.cell_latents,
+                 cell_adjacency=c.cell_adjacency, cell_structure=c.cell_structure,
+                 action_tactical=c.action_tactical, latent_loops=latent_loops)
 
 
 def oracle_forward(model, batch, mass_floor: float = 0.2, latent_loops: bool = False) -> dict:

@@ -30,12 +30,14 @@ What each function follows (python/mantisnet/mantisnet/...):
 
 Parity status: every kernel-level formulation above is pinned by closed
 forms and brute force in tests/test_oracle_model.py.  The composition (the
-order of LayerNorms, residuals and head folding) is pinned only by the
-reference's invariants — parameter count, exact D6 invariance, batching
-equivalence, fresh-init exact zeros, value_dist normalisation — because the
-reference model cannot be imported here (its package imports the Rust
-``hexo_py`` extension, which this image cannot build): composition parity
-unpinned beyond those invariants.
+order of LayerNorms, residuals and head folding) is pinned by the
+reference's own ``MantisNet.forward``: tests/golden/forward_*.npz hold its
+outputs on seeded positions and weights, for the production configuration,
+the knob-off default, the uncovered scope and the non-production knobs
+(``cell_adjacency``, ``cell_structure``, ``action_tactical``, covered-only
+cell latents), written in the build container by
+tests/golden/write_forward_fixtures.py; tests/test_reference_forward.py holds
+the oracle to them and shows a mistake planted in each knob's term fails.
 """
 
 from __future__ import annotations
@@ -63,10 +65,20 @@ class Cfg:
     policy_hidden: int = 128
     value_hidden: int = 128
     cell_node_scope: str = "all"
-    cell_nodes: bool = True  # False: the knob-off cell pass, heads over decoder window sums
+    cell_nodes: bool = True  # cell state over every legal cell, with the radius stage
+    # cell state over the covered cells only (cell_nodes False); both False:
+    # the knob-off cell pass, heads over decoder window sums
+    cell_latents: bool = True
+    cell_adjacency: bool = False  # the six-neighbour cell stage (model.py:463-476)
+    cell_structure: bool = False  # structure MLP and coverage encodings (model.py:458-461, 827-862)
+    action_tactical: bool = False  # the tactical action scalars (model.py:769-774, 1058-1062)
     # True: the window-latent read and broadcast as the reference's literal
     # CPU loops (window_latents.py:102-188) instead of the vectorised forms
     latent_loops: bool = False
+
+    @property
+    def uses_cell_state(self) -> bool:
+        return self.cell_latents or self.cell_nodes
 
 
 # ----------------------------------------------------------------- primitives
@@ -128,10 +140,14 @@ def window_layout(window_pos, positions):
 
 def cell_tables(dec_cell, dec_window, dec_class, n_windows, n_cells):
     """Cell-major and window-major views of the decoder incidence, with
-    destinations over all legal cells."""
+    destinations over all legal cells, or (n_cells < 0) over the covered cells
+    relabelled compactly in ascending order (cell_latents.py:123-138)."""
     order = torch.argsort(dec_cell, stable=True)
     edge_window, edge_class, edge_cell = dec_window[order], dec_class[order], dec_cell[order]
-    covered = torch.unique_consecutive(edge_cell)
+    covered, counts = torch.unique_consecutive(edge_cell, return_counts=True)
+    if n_cells < 0:
+        edge_cell = torch.repeat_interleave(torch.arange(counts.numel()), counts)
+        n_cells = counts.numel()
     cell_ptr = torch.searchsorted(edge_cell, torch.arange(n_cells + 1))
     worder = torch.argsort(edge_window, stable=True)
     win_ptr = torch.searchsorted(edge_window[worder], torch.arange(n_windows + 1))
@@ -316,23 +332,38 @@ def compose_acting_q(critic, offsets, mass_floor):
 # ----------------------------------------------------------------- model
 
 
-def _cell_stage(sd, pre, cfg, s, w, c, ctab, radius):
+def _cell_stage(sd, pre, cfg, s, w, c, ctab, radius, adjacency=None):
     a, hd = cfg.heads, cfg.h // cfg.heads
     n_c, n_w, n_s = c.shape[0], w.shape[0], s.shape[0]
+    state = c  # the block's incoming cell state (the structure MLP reads it)
     zc, zw = ln(c, sd, pre + "ln_cr_c"), ln(w, sd, pre + "ln_cr_w")
     read = cell_attention(
         lin(zc, sd, pre + "cr_wq").view(n_c, a, hd), lin(zw, sd, pre + "cr_wk").view(n_w, a, hd),
         lin(zw, sd, pre + "cr_wv").view(n_w, a, hd), sd[pre + "cr_bias"], sd[pre + "cr_vclass.weight"],
         ctab["edge_window"], ctab["edge_class"], ctab["edge_cell"],
     )
-    c = c + lin(read.reshape(n_c, cfg.h), sd, pre + "cr_wo")
-    zc, zs = ln(c, sd, pre + "ln_radius_c"), ln(s, sd, pre + "ln_radius_s")
-    read = cell_attention(
-        lin(zc, sd, pre + "radius_wq").view(n_c, a, hd), lin(zs, sd, pre + "radius_wk").view(n_s, a, hd),
-        lin(zs, sd, pre + "radius_wv").view(n_s, a, hd), sd[pre + "radius_bias"],
-        sd[pre + "radius_vclass.weight"], radius["edge_src"], radius["edge_class"], radius["edge_dst"],
-    )
-    c = c + lin(read.reshape(n_c, cfg.h), sd, pre + "radius_wo")
+    reads = lin(read.reshape(n_c, cfg.h), sd, pre + "cr_wo")
+    c = c + reads
+    if cfg.cell_nodes:
+        zc, zs = ln(c, sd, pre + "ln_radius_c"), ln(s, sd, pre + "ln_radius_s")
+        read = cell_attention(
+            lin(zc, sd, pre + "radius_wq").view(n_c, a, hd), lin(zs, sd, pre + "radius_wk").view(n_s, a, hd),
+            lin(zs, sd, pre + "radius_wv").view(n_s, a, hd), sd[pre + "radius_bias"],
+            sd[pre + "radius_vclass.weight"], radius["edge_src"], radius["edge_class"], radius["edge_dst"],
+        )
+        stone = lin(read.reshape(n_c, cfg.h), sd, pre + "radius_wo")
+        c = c + stone
+        reads = reads + stone
+    if cfg.cell_structure:  # model.py:458-461: a second residual over the incoming state and the reads
+        c = c + pair_mlp(ln(state, sd, pre + "ln_c"), reads, sd, pre + "mlp_c")
+    if cfg.cell_adjacency:  # model.py:463-476: cells <- their axial neighbours
+        zq, zk = ln(c, sd, pre + "ln_adj_q"), ln(c, sd, pre + "ln_adj_k")
+        read = cell_attention(
+            lin(zq, sd, pre + "adj_wq").view(n_c, a, hd), lin(zk, sd, pre + "adj_wk").view(n_c, a, hd),
+            lin(zk, sd, pre + "adj_wv").view(n_c, a, hd), sd[pre + "adj_bias"], sd[pre + "adj_vclass.weight"],
+            adjacency["edge_src"], adjacency["edge_class"], adjacency["edge_dst"],
+        )
+        c = c + lin(read.reshape(n_c, cfg.h), sd, pre + "adj_wo")
     zw, zc = ln(w, sd, pre + "ln_wr_w"), ln(c, sd, pre + "ln_wr_c")
     back = cell_attention(
         lin(zw, sd, pre + "wr_wq").view(n_w, a, hd), lin(zc, sd, pre + "wr_wk").view(n_c, a, hd),
@@ -368,7 +399,8 @@ def _latent_cycle(sd, pre, cfg, w, g, window_pos, offsets, order):
     return w, g
 
 
-def _block(sd, i, cfg, b, s, w, g, c, seq_lens, plan, layout, ctab, radius, ws_rows, sw_rows, update_stones):
+def _block(sd, i, cfg, b, s, w, g, c, seq_lens, plan, layout, ctab, radius, ws_rows, sw_rows, update_stones,
+           adjacency=None):
     pre = f"blocks.{i}."
     h, a = cfg.h, cfg.heads
     hd = h // a
@@ -379,8 +411,8 @@ def _block(sd, i, cfg, b, s, w, g, c, seq_lens, plan, layout, ctab, radius, ws_r
     agg = run_sum(x, b["inc_stone"], b["inc_window"], w.shape[0]) + ws_rows
     w = w + pair_mlp(ln(w, sd, pre + "ln_ws_w"), agg, sd, pre + "mlp_w")
     # §5.1b cell stage, or the knob-off cell pass (model.py:374-395)
-    if cfg.cell_nodes:
-        w, c = _cell_stage(sd, pre, cfg, s, w, c, ctab, radius)
+    if cfg.uses_cell_state:
+        w, c = _cell_stage(sd, pre, cfg, s, w, c, ctab, radius, adjacency)
     else:
         x = lin(ln(w, sd, pre + "ln_cp_in"), sd, pre + "u_cp")
         agg = cell_pass(x, sd[pre + "e_cp.weight"], b["dec_cell"], b["dec_window"], b["dec_class"],
@@ -432,22 +464,57 @@ def trunk(sd, cfg, b, pattern_counts):
     plan = incidence_plan(b["inc_stone"], b["inc_window"], b["inc_class"])
     window_pos = b["window_slot"] // b["value_valid"].shape[1]
     offsets, order = window_layout(window_pos, p)
-    ctab = c = radius = None
-    if cfg.cell_nodes:
-        ctab = cell_tables(b["dec_cell"], b["dec_window"], b["dec_class"], w.shape[0], n_c)
-        c = sd["cell_nearest_table.weight"][b["cell_nearest"]].clone()
-        c[ctab["covered"]] = sd["cell_base"]
-        classes = b["radius_orbit"] + ORBIT48 * (b["radius_own"] + 2 * b["radius_on_axis"])
-        radius = edge_tables(b["radius_src"], b["radius_dst"], classes, ctab["covered"], n_c,
-                             cfg.cell_node_scope == "uncovered")
+    ctab = c = radius = adjacency = None
+    if cfg.uses_cell_state:
+        ctab = cell_tables(b["dec_cell"], b["dec_window"], b["dec_class"], w.shape[0],
+                           n_c if cfg.cell_nodes else -1)
+        cov = covered_init(sd, cfg, b, ctab)
+        if cfg.cell_nodes:
+            c = sd["cell_nearest_table.weight"][b["cell_nearest"]].clone()
+            c[ctab["covered"]] = cov
+            classes = b["radius_orbit"] + ORBIT48 * (b["radius_own"] + 2 * b["radius_on_axis"])
+            radius = edge_tables(b["radius_src"], b["radius_dst"], classes, ctab["covered"], n_c,
+                                 cfg.cell_node_scope == "uncovered")
+            if cfg.cell_adjacency:
+                # one relation class for all three axes (model.py:881-896)
+                adjacency = edge_tables(b["adjacency_src"], b["adjacency_dst"], torch.zeros_like(b["adjacency_axis"]),
+                                        ctab["covered"], n_c, cfg.cell_node_scope == "uncovered")
+        else:
+            c = cov
     seq_lens = b["attn_valid"].sum(1)
     ws_all = (pattern_counts @ torch.cat([sd[f"blocks.{i}.e_ws.weight"] for i in range(cfg.blocks)], 1))[b["window_feat"]]
     sw_all = run_sum(torch.cat([sd[f"blocks.{i}.e_sw.weight"] for i in range(cfg.blocks)], 1), plan[2], plan[0], s.shape[0])
     for i in range(cfg.blocks):
         sl = slice(i * h, (i + 1) * h)
         s, w, g, c = _block(sd, i, cfg, b, s, w, g, c, seq_lens, plan, (window_pos, offsets, order),
-                            ctab, radius, ws_all[:, sl], sw_all[:, sl], i + 1 < cfg.blocks)
-    return ln(w, sd, "ln_out"), ln(g, sd, "ln_out").mean(1), (ln(c, sd, "ln_out") if c is not None else None)
+                            ctab, radius, ws_all[:, sl], sw_all[:, sl], i + 1 < cfg.blocks, adjacency)
+    cells = None
+    if cfg.cell_nodes:
+        cells = ln(c, sd, "ln_out")
+    elif cfg.uses_cell_state:
+        # covered-only latents: uncovered legal cells carry the base row (model.py:975-983)
+        cells = ln(sd["cell_base"], sd, "ln_out").expand(n_c, h).clone()
+        cells[ctab["covered"]] = ln(c, sd, "ln_out")
+    return ln(w, sd, "ln_out"), ln(g, sd, "ln_out").mean(1), cells
+
+
+COVERAGE_BUCKET_OF = (0, 0, 1, 2, 3, 4, 4, 5, 5, 5, 6, 6, 6, 6, 7, 7, 7, 7, 7)
+
+
+def covered_init(sd, cfg, b, ctab):
+    """The covered cells' initial state (model.py:827-862): the shared base
+    row, and with cell_structure also the sum of the cell's decoder class rows,
+    its nearest-stone row and its bucketed coverage count."""
+    cov = ctab["covered"]
+    base = sd["cell_base"].expand(cov.shape[0], cfg.h)
+    if not cfg.cell_structure:
+        return base.clone()
+    n_c = b["cell_pos"].shape[0]
+    classes = run_sum(sd["cell_class_table.weight"], b["dec_class"], b["dec_cell"], n_c)[cov]
+    degree = torch.zeros(n_c, dtype=torch.long).index_add_(0, b["dec_cell"], torch.ones_like(b["dec_cell"]))
+    bucket = torch.tensor(COVERAGE_BUCKET_OF, dtype=torch.long)[degree[cov]]
+    return base + classes + sd["cell_nearest_table.weight"][b["cell_nearest"][cov]] + \
+        sd["cell_coverage_table.weight"][bucket]
 
 
 def value_head(sd, cfg, b, w, g):
@@ -465,15 +532,18 @@ def value_head(sd, cfg, b, w, g):
     return dist @ bins, dist, logits
 
 
-def action_contribution(sd, b, w, empty_classes):
+def action_contribution(sd, b, w, empty_classes, tactical=False):
     pre = lin(w, sd, "act_proj")
     acts = encode_rows(pre, sd["act_table.weight"], b["dec_window"], b["act_class"], b["dec_cell"], b["cell_pos"].shape[0])
     empty = F.relu(sd["act_empty_base"] + sd["act_table.weight"][list(empty_classes)])
-    return acts + (b["act_empty"].float().unsqueeze(-1) * empty.unsqueeze(0)).sum(1)
+    acts = acts + (b["act_empty"].float().unsqueeze(-1) * empty.unsqueeze(0)).sum(1)
+    if tactical:  # model.py:1058-1062: the tactical scalars through one small MLP
+        acts = acts + lin(F.relu(lin(b["act_tactical"].float(), sd, "tactical_a")), sd, "tactical_out")
+    return acts
 
 
 def cell_head_logits(sd, cfg, b, w, g, cells, empty_classes):
-    acts = action_contribution(sd, b, w, empty_classes)
+    acts = action_contribution(sd, b, w, empty_classes, cfg.action_tactical)
     n_c = b["cell_pos"].shape[0]
     if cells is None:  # cell state off: each cell reads its decoder windows' sum (model.py:985-1029)
         cells = run_sum(w, b["dec_window"], b["dec_cell"], n_c)

@@ -12,7 +12,8 @@ import numpy as np
 import torch
 
 GOLDEN = Path(__file__).resolve().parent / "golden"
-NAMES = ("tiny_cfg0", "prod_cfg3", "prod_cfg4", "knoboff_cfg3", "uncovered_cfg0", "prod_edges")
+NAMES = ("tiny_cfg0", "prod_cfg3", "prod_cfg4", "knoboff_cfg3", "uncovered_cfg0", "prod_edges",
+         "adjacency_cfg3", "tactical_cfg3", "adjtac_cfg0", "structure_cfg3", "covered_cfg3")
 OUTPUTS = ("policy_logits", "q_score", "q_values", "value", "value_dist", "value_logits")
 
 

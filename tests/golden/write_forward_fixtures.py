@@ -53,6 +53,15 @@ CASES = {
 }
 EDGE_GAMES = [[], [(0, 0)], [(0, 0), (1, 0), (2, 0)]]
 CASES["prod_edges"] = (PROD_KNOBS, None, len(EDGE_GAMES), 0, 4)
+# the non-production knobs: the six-neighbour cell stage, the tactical action
+# scalars, the structure MLP and covered-only cell latents
+CASES.update({
+    "adjacency_cfg3": (dict(PROD_KNOBS, cell_adjacency=True), 4, 4, 40, 5),
+    "tactical_cfg3": (dict(PROD_KNOBS, action_tactical=True), 4, 4, 60, 6),
+    "adjtac_cfg0": (dict(TINY, **PROD_KNOBS, cell_adjacency=True, action_tactical=True), 1, 6, 200, 7),
+    "structure_cfg3": (dict(PROD_KNOBS, cell_structure=True), 4, 3, 80, 8),
+    "covered_cfg3": (dict(cell_latents=True, cell_nodes=False), 4, 3, 120, 9),
+})
 
 
 def fixture_path(name: str) -> Path:

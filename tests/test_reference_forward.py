@@ -8,8 +8,10 @@ must reproduce them to fp32 summation-order noise, which pins its wiring:
 LayerNorm placement, residual order, head folding and the value readout.
 The cases cover the ``_tiny`` widths with the production knobs,
 the production configuration on configs[3] and configs[4] positions, the
-knob-off default configuration, the uncovered cell-node scope and ply-0 /
-single-stone positions.
+knob-off default configuration, the uncovered cell-node scope, ply-0 /
+single-stone positions, and the non-production knobs: the six-neighbour cell
+stage, the tactical action scalars (both also at the ``_tiny`` widths), the
+structure MLP with its coverage encodings, and covered-only cell latents.
 """
 
 from __future__ import annotations
@@ -51,6 +53,34 @@ def test_reference_fixture_detects_a_composition_change():
     for leaf in ("weight", "bias"):
         a, b = f"blocks.3.ln_cr_c.{leaf}", f"blocks.3.ln_cr_w.{leaf}"
         sd[a], sd[b] = sd[b].clone(), sd[a].clone()
+    net.load_state_dict(sd)
+    ref = oracle_forward(net, fx.batch(), fx.mass_floor)
+    assert _max_err(ref["policy_logits"], fx.expected["policy_logits"]) > 100 * REL
+
+
+@pytest.mark.parametrize("name,a,b", [
+    # the adjacency stage's query and key LayerNorms swapped
+    ("adjacency_cfg3", "blocks.2.ln_adj_q", "blocks.2.ln_adj_k"),
+    # the tactical MLP's hidden layer fed the wrong way round: its weight
+    # rows reversed (a transposed or permuted operand)
+    ("tactical_cfg3", "tactical_a", None),
+    # the structure MLP's state LayerNorm swapped with the cell read's
+    ("structure_cfg3", "blocks.1.ln_c", "blocks.1.ln_cr_c"),
+    # covered-only latents: the window read-back's LayerNorms swapped
+    ("covered_cfg3", "blocks.3.ln_wr_w", "blocks.3.ln_wr_c"),
+])
+def test_knob_fixtures_detect_a_wiring_change(name, a, b):
+    # each non-production knob's fixture catches a mistake planted in its own
+    # term, far beyond the tolerance the oracle meets
+    fx = Fixture(name)
+    net = fx.model()
+    sd = net.state_dict()
+    if b is None:
+        sd[f"{a}.weight"] = sd[f"{a}.weight"].flip(0).clone()
+    else:
+        for leaf in ("weight", "bias"):
+            x, y = f"{a}.{leaf}", f"{b}.{leaf}"
+            sd[x], sd[y] = sd[y].clone(), sd[x].clone()
     net.load_state_dict(sd)
     ref = oracle_forward(net, fx.batch(), fx.mass_floor)
     assert _max_err(ref["policy_logits"], fx.expected["policy_logits"]) > 100 * REL
