@@ -619,6 +619,14 @@ extern "C" int32_t mantis_fused_linear(const void* x, int32_t x_dtype, int64_t l
   if (st2 && r && mode == 3 && x_dtype == MANTIS_F16 && ln && hx2 && n1 == 128 && x2_dtype == MANTIS_F16 &&
       n3 == 128)  // the pair-ordered second stage is 128 wide
     return launch<_Float16, _Float16, true, 128, true, true, true, 3>(a, s);
+  // the cell structure MLP of the fp16 cell state: its hidden layer's part
+  // from the incoming rows (LN(x) W1^T + x2 W2^T + b1, fp32 out, x2 the same
+  // raw rows), then its completion from the updated rows (relu(x W1^T + add1)
+  // W3^T + b3 added in place)
+  if (!st2 && !r && mode == 1 && x_dtype == MANTIS_F16 && ln && hx2 && n1 == 128 && x2_dtype == MANTIS_F16)
+    return launch<_Float16, _Float16, true, 128, true, false, false, 1>(a, s);
+  if (st2 && r && mode == 3 && x_dtype == MANTIS_F16 && !ln && !hx2 && n1 == 128 && n3 == 128)
+    return launch<_Float16, float, false, 128, false, true, true, 3>(a, s);
   if (st2 && r && mode == 2 && x_dtype == MANTIS_F32 && ln) {
     if (hx2 && n1 == 128 && x2_dtype == MANTIS_F32)
       return launch<float, float, true, 128, true, true, true, 2>(a, s);

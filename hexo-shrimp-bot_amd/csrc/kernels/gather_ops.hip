@@ -661,6 +661,77 @@ gather_rows_kernel(const T* __restrict__ table, int64_t ld_table, int64_t n_tabl
   }
 }
 
+// The cells' initial state under cell_structure (model.py:827-862), fp16
+// rows of 128: for out row i and its cell r = rows[i] (or i),
+//   covered (a non-empty decoder run [cell_ptr[r], cell_ptr[r+1])):
+//     base + sum_e class_table[entry_class[e]] + nearest_table[cell_nearest[r]]
+//          + degree_table[cell_ptr[r+1] - cell_ptr[r]]
+//   otherwise: nearest_table[cell_nearest[r]]
+// summed in fp32 in that order (the class rows in entry order) and rounded
+// once.  degree_table holds the coverage row of each decoder degree (the
+// coverage table composed with the degree -> bucket map).  16 lanes per row,
+// 8 features per lane; any index out of range contributes a zero row and
+// flags MANTIS_FLAG_INDEX.
+__global__ void __launch_bounds__(256)
+structure_init_kernel(const float* __restrict__ base, const float* __restrict__ class_table, int64_t n_classes,
+                      const float* __restrict__ nearest_table, int64_t n_nearest,
+                      const float* __restrict__ degree_table, int64_t n_degrees, const int64_t* __restrict__ cell_ptr,
+                      const int64_t* __restrict__ entry_class, int64_t n_entries,
+                      const int64_t* __restrict__ cell_nearest, int64_t n_cells, const int64_t* __restrict__ rows,
+                      int64_t n_out, _Float16* __restrict__ out, int64_t ld_out, int32_t* flag) {
+  const int sub = threadIdx.x % 16, f = 8 * sub;
+  bool bad = false;
+  for (int64_t i = (int64_t(blockIdx.x) * 256 + threadIdx.x) / 16; i < n_out; i += int64_t(gridDim.x) * 16) {
+    const int64_t r = rows ? rows[i] : i;
+    const bool r_ok = r >= 0 && r < n_cells;
+    bad |= !r_ok;
+    float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    int64_t lo = 0, hi = 0, near = -1;
+    if (r_ok) {
+      lo = cell_ptr[r];
+      hi = cell_ptr[r + 1];
+      near = cell_nearest[r];
+    }
+    const bool run_ok = lo >= 0 && hi >= lo && hi <= n_entries;
+    bad |= r_ok && !run_ok;
+    if (!run_ok) lo = hi = 0;
+    if (hi > lo) {
+      for (int64_t e = lo; e < hi; ++e) {
+        const int64_t k = entry_class[e];
+        const bool ok = k >= 0 && k < n_classes;
+        bad |= !ok;
+        float t[8];
+        load8(class_table + (ok ? k : 0) * 128 + f, t);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] += ok ? t[j] : 0.f;
+      }
+      float b[8];
+      load8(base + f, b);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = b[j] + v[j];
+    }
+    if (r_ok) {
+      const bool ok = near >= 0 && near < n_nearest;
+      bad |= !ok;
+      float t[8];
+      load8(nearest_table + (ok ? near : 0) * 128 + f, t);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] += ok ? t[j] : 0.f;
+    }
+    if (hi > lo) {
+      const int64_t d = hi - lo;
+      const bool ok = d < n_degrees;
+      bad |= !ok;
+      float t[8];
+      load8(degree_table + (ok ? d : 0) * 128 + f, t);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] += ok ? t[j] : 0.f;
+    }
+    store8(out + i * ld_out + f, v);
+  }
+  if (bad) raise_flag(flag, MANTIS_FLAG_INDEX);
+}
+
 template <typename F>
 bool with_type(int32_t dtype, F&& fn) {
   switch (dtype) {
@@ -705,6 +776,28 @@ int32_t mantis_gather_rows(const void* table, int32_t dtype, int64_t ld_table, i
     ok = false;
   }
   return ok ? launched() : MANTIS_E_ARG;
+}
+
+int32_t mantis_structure_init(const float* base, const float* class_table, int64_t n_classes,
+                              const float* nearest_table, int64_t n_nearest, const float* degree_table,
+                              int64_t n_degrees, const int64_t* cell_ptr, const int64_t* entry_class,
+                              int64_t n_entries, const int64_t* cell_nearest, int64_t n_cells, const int64_t* rows,
+                              int64_t n_out, void* out, int64_t ld_out, int32_t* err_flag, void* stream) {
+  if (n_out == 0) return MANTIS_OK;
+  if (!base || !class_table || !nearest_table || !degree_table || !cell_ptr || !cell_nearest || !out || n_out < 0 ||
+      n_cells < 0 || n_entries < 0 || (n_entries > 0 && !entry_class) || n_classes <= 0 || n_nearest <= 0 ||
+      n_degrees <= 0 || ld_out < 128 || ld_out % 8)
+    return MANTIS_E_ARG;
+  if (!rows && n_out > n_cells) return MANTIS_E_ARG;
+  if (!aligned16(base) || !aligned16(class_table) || !aligned16(nearest_table) || !aligned16(degree_table) ||
+      !aligned16(out))
+    return MANTIS_E_ARG;
+  int64_t grid = (n_out + 15) / 16;
+  if (grid > 65536) grid = 65536;
+  structure_init_kernel<<<unsigned(grid), 256, 0, as_stream(stream)>>>(
+      base, class_table, n_classes, nearest_table, n_nearest, degree_table, n_degrees, cell_ptr, entry_class,
+      n_entries, cell_nearest, n_cells, rows, n_out, static_cast<_Float16*>(out), ld_out, err_flag);
+  return launched();
 }
 
 int32_t mantis_runs_to_ptr(const int64_t* dest, int64_t n_entries, int64_t n_dest, int64_t* ptr,

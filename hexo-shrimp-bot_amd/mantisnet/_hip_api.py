@@ -39,6 +39,7 @@ SIGNATURES = {
     "mantis_attention_slots": ([vp, i64, i64, i64, vp, vp, vp, vp], i32),
     "mantis_gather_rows": ([vp, i32, i64, i64, vp, vp, i64, i64, vp, i64, vp, vp], i32),
     "mantis_runs_to_ptr": ([vp, i64, i64, vp, vp, vp], i32),
+    "mantis_structure_init": ([vp, vp, i64, vp, i64, vp, i64, vp, vp, i64, vp, i64, vp, i64, vp, i64, vp, vp], i32),
     "mantis_segment_order": ([vp, i64, vp, vp, i64, vp, vp, vp], i32),
     "mantis_run_reduce": ([vp, i32, i64, i64, i64, vp, i64, vp, i64, vp, i32, vp, vp], i32),
     "mantis_class_reduce_workspace": ([i64, i64, i64], i64),

@@ -43,13 +43,15 @@ Per-batch index views (the reference's incidence_plan, window_latent_layout,
 cell_tables and cell_node_edge_tables) are derived once per batch on the
 device and shared by the trunk and the heads.
 
-Scope: the production cell-state configuration (``cell_nodes=True``, either
-node scope, with or without the six-neighbour cell stage ``cell_adjacency``),
-covered-only cell latents (``cell_latents`` without cell nodes) and the
-knob-off default (no cell state: the transient cell pass of
-model.py:374-395, and heads over the decoder's window sums), either with the
-tactical action scalars (``action_tactical``); H = 128, 4 heads of 32, 4
-value queries.  Other knob combinations raise ``NotImplementedError``; the
+Scope: every knob combination ``MantisConfig`` accepts at H = 128, 4 heads
+of 32, 4 value queries: the production cell-state configuration
+(``cell_nodes=True``, either node scope), covered-only cell latents
+(``cell_latents`` without cell nodes), each with or without the structure
+MLP and the cells' static encodings (``cell_structure``), the six-neighbour
+cell stage (``cell_adjacency``, with cell nodes), and the knob-off default
+(no cell state: the transient cell pass of model.py:374-395, and heads over
+the decoder's window sums); any of them with the tactical action scalars
+(``action_tactical``).  Other widths raise ``NotImplementedError``; the
 forward is inference-only.
 """
 
@@ -73,8 +75,6 @@ ORBIT48 = 48
 
 def _supported(model) -> torch.device:
     cfg = model.cfg
-    if cfg.cell_structure:
-        raise NotImplementedError("cell_structure is not implemented in the MI355X forward")
     if cfg.h != 128 or cfg.heads != 4 or cfg.value_queries != 4 or cfg.ffn_factor != 2 or cfg.policy_hidden != 128:
         raise NotImplementedError("the MI355X kernels are built for H=128, 4 heads, FFN 256, 4 value queries")
     dev = next(model.parameters()).device
@@ -174,6 +174,18 @@ def _prepare_cell_stage(t, put, P, pb):
         put(pb + "adj_kv", _interleaved(_fold(P, pb + "ln_adj_k", [pb + "adj_wk", pb + "adj_wv"])))
         put(pb + "adj_o", _fold(P, None, [pb + "adj_wo"]))
         t[pb + "adj_vcls"] = ops.interleave_heads(P[pb + "adj_vclass.weight"]).to(HALF).contiguous()
+    if pb + "mlp_c.out.weight" in P:
+        # the structure MLP (cell_structure), out(relu(lin_a(ln_c(state)) +
+        # lin_b(reads))) with reads = the updated rows - the incoming rows:
+        # its hidden layer's part from the incoming rows, ln_c folded into
+        # lin_a, -lin_b (no bias) on the raw rows, then lin_b on the updated
+        # rows (the same fp16 lin_b, negated exactly, so the two products of
+        # an unchanged feature cancel)
+        wa, ba = _fold(P, pb + "ln_c", [pb + "mlp_c.lin_a"])
+        wb = P[pb + "mlp_c.lin_b.weight"].to(HALF).contiguous()
+        t[pb + "struct_u.w"], t[pb + "struct_u.b"] = wa, ba
+        t[pb + "struct_nb.w"], t[pb + "struct_b.w"] = (-wb).contiguous(), wb
+        put(pb + "struct_o", _fold(P, None, [pb + "mlp_c.out"]))
     put(pb + "wr_q", _fold(P, pb + "ln_wr_w", [pb + "wr_wq"]))
     put(pb + "wr_kv", _interleaved(_fold(P, pb + "ln_wr_c", [pb + "wr_wk", pb + "wr_wv"])))
     put(pb + "wr_o", _fold(P, None, [pb + "wr_wo"]))
@@ -195,6 +207,10 @@ def _prepare(model, P) -> dict[str, Tensor]:
         t["cell_table"] = torch.cat([P["cell_nearest_table.weight"], P["cell_base"][None, :]]).to(HALF).contiguous()
     elif cfg.uses_cell_state:
         t["cell_base16"] = P["cell_base"][None, :].to(HALF).contiguous()
+    if cfg.cell_structure:
+        # the coverage row of each decoder degree (the bucket map composed in)
+        t["structure_degree"] = P["cell_coverage_table.weight"].index_select(
+            0, model.coverage_bucket.to(P["cell_coverage_table.weight"].device)).contiguous()
     for i in range(cfg.blocks):
         pb = f"blocks.{i}."
         put(pb + "u", _fold(P, pb + "ln_ws_s", [pb + "u"]))
@@ -710,12 +726,15 @@ def _cell_stage(W, P, pb, plan: Plan, s, w, c, c_init=None):
     # cells <- windows (decoder classes, class values) then cells <- stones
     # (radius classes, class values); then windows <- cells (decoder classes).
     # Each sub-stage is LN -> q -> attention -> o -> residual.
+    # cell_structure: the structure MLP's part from the incoming rows
+    u = _structure_in(W, pb, c)
     if not plan._cfg.cell_nodes:
         # covered-only cell latents: the rows are the covered cells alone, in
         # compact order; no radius stage
         cr = _substage(W, P, pb, "cr", _proj(W, pb + "cr_kv", w), "cr_bias", W[pb + "cr_vcls"], plan.cov_ptr,
                        plan.edge_window, plan.edge_class)
         ops.attention_substages(c, [cr], row_order=plan.cov_order)
+        _structure_out(W, pb, c, u)
         wr = _substage(W, P, pb, "wr", _proj(W, pb + "wr_kv", c), "wr_bias", None, plan.win_ptr,
                        plan.edge_wcell_cov, plan.edge_wclass)
         ops.attention_substages(w, [wr])
@@ -738,6 +757,7 @@ def _cell_stage(W, P, pb, plan: Plan, s, w, c, c_init=None):
         rad = _substage(W, P, pb, "rad", rad_kv, "radius_bias", W[pb + "rad_vcls"], plan.radius_ptr,
                         plan.radius_src, plan.radius_class)
         ops.attention_substages(c, [cr, rad], row_order=plan.cell_order, init=c_init)
+    _structure_out(W, pb, c, u)
     if plan._adjacency is not None:
         # cells <- their axial neighbours (model.py:463-476), k/v from the
         # cells after the two sub-stages above
@@ -752,6 +772,24 @@ def _cell_stage(W, P, pb, plan: Plan, s, w, c, c_init=None):
         wr = _substage(W, P, pb, "wr", _proj(W, pb + "wr_kv", c), "wr_bias", None, plan.win_ptr, plan.edge_wcell,
                        plan.edge_wclass)
     ops.attention_substages(w, [wr])
+
+
+def _structure_in(W, pb, c):
+    """cell_structure (model.py:458-461): the structure MLP's hidden layer
+    before its activation, lin_a(ln_c(c)) - lin_b(c) + both biases, from the
+    rows the cell sub-stages are about to update (fp32); None off the knob."""
+    if pb + "struct_u.w" not in W.t:
+        return None
+    return FL(c, W[pb + "struct_u.w"], W[pb + "struct_u.b"], layer_norm=True, x2=c, w2=W[pb + "struct_nb.w"],
+              out_dtype=F32)
+
+
+def _structure_out(W, pb, c, u):
+    """c += out(relu(u + lin_b(c))): with u from the incoming rows, lin_b
+    acts on reads = the updated rows - the incoming rows."""
+    if u is not None:
+        FL(c, W[pb + "struct_b.w"], None, add1=u, relu=True, w3=W[pb + "struct_o.w"], b3=W[pb + "struct_o.b"],
+           out=c, residual=True)
 
 
 def _cell_pass(W, P, pb, plan: Plan, b: Batch, w):
@@ -893,7 +931,13 @@ def _trunk(model, b: Batch, plan: Plan, raw_cells: bool = False, W: Prepared | N
     else:
         w = ops.gather_rows(W["window_table"], b.window_feat)
     c = c_init = None
-    if cfg.cell_nodes:
+    if cfg.cell_structure:
+        # the cells' own static encodings join the initial state of the covered
+        # cells (per cell, so the first pass reads a materialised state)
+        c = ops.structure_init(P["cell_base"], P["cell_class_table.weight"], P["cell_nearest_table.weight"],
+                               W["structure_degree"], plan.cell_ptr, plan.edge_class, b.cell_nearest,
+                               rows=None if cfg.cell_nodes else plan.cov_rows)
+    elif cfg.cell_nodes:
         # covered cells start from cell_base, the others from their nearest-stone
         # row of the table [nearest rows; cell_base] (the decoder CSR tells the
         # covered cells).  The cell state is stored in fp16 (866 MB -> 433 MB

@@ -448,6 +448,36 @@ def gather_rows(table: Tensor, idx: Tensor, cover_ptr: Tensor | None = None, cov
     return out
 
 
+def structure_init(base: Tensor, class_table: Tensor, nearest_table: Tensor, degree_table: Tensor,
+                   cell_ptr: Tensor, entry_class: Tensor, cell_nearest: Tensor, rows: Tensor | None = None) -> Tensor:
+    """The cells' initial state under cell_structure, fp16 (n, 128): for
+    cell r (rows[i], or every cell), base + the sum of its decoder entries'
+    class rows + its nearest-stone row + the coverage row of its decoder
+    degree when its run [cell_ptr[r], cell_ptr[r+1]) is non-empty, else its
+    nearest-stone row alone (model.py:827-862).  degree_table: the coverage
+    table composed with the degree -> bucket map, one row per degree."""
+    dev = _on_gpu(base, class_table, nearest_table, degree_table, cell_ptr, entry_class, cell_nearest, rows)
+    tabs = [t.float().contiguous() for t in (base, class_table, nearest_table, degree_table)]
+    if tabs[0].numel() != 128 or any(t.ndim != 2 or t.shape[1] != 128 for t in tabs[1:]):
+        raise ValueError("base is 128 wide and the tables are (n, 128)")
+    cell_ptr, entry_class, cell_nearest = (_i64(t, n) for t, n in ((cell_ptr, "cell_ptr"),
+                                                                    (entry_class, "entry_class"),
+                                                                    (cell_nearest, "cell_nearest")))
+    n_cells = cell_nearest.numel()
+    if cell_ptr.numel() != n_cells + 1:
+        raise ValueError("cell_ptr must have one entry per cell plus one")
+    rows = None if rows is None else _i64(rows, "rows")
+    n = n_cells if rows is None else rows.numel()
+    out = torch.empty((n, 128), dtype=torch.float16, device=dev)
+    if n:
+        nbytes = n * (256 + 8 * 3) + entry_class.numel() * 8
+        _launch("structure_init", nbytes, 0.0, lambda: _check(_lib().mantis_structure_init(
+            _ptr(tabs[0]), _ptr(tabs[1]), tabs[1].shape[0], _ptr(tabs[2]), tabs[2].shape[0], _ptr(tabs[3]),
+            tabs[3].shape[0], _ptr(cell_ptr), _ptr(entry_class), entry_class.numel(), _ptr(cell_nearest), n_cells,
+            _ptr(rows), n, _ptr(out), out.stride(0), _ptr(error_flag(dev)), _stream()), "structure_init"))
+    return out
+
+
 def run_reduce(values: Tensor, gather: Tensor, ptr: Tensor, n_dest: int, out_dtype: torch.dtype) -> Tensor:
     """out[d] = sum of values[gather[e]] over e in [ptr[d], ptr[d+1]), fp32 accumulated."""
     dev = _on_gpu(values, gather, ptr)

@@ -185,6 +185,27 @@ int32_t mantis_gather_rows(const void* table, int32_t dtype, int64_t ld_table, i
                            void* out, int64_t ld_out, int32_t* err_flag, void* stream);
 
 /*
+ * The cells' initial state under cell_structure, fp16 rows out (n_out,
+ * ld_out).  Out row i is cell r = rows[i] (rows NULL: r = i, n_out <=
+ * n_cells).  A cell with a non-empty decoder run [cell_ptr[r],
+ * cell_ptr[r+1]) of entry_class (the cell-major decoder classes) starts from
+ *   base + sum_e class_table[entry_class[e]] + nearest_table[cell_nearest[r]]
+ *        + degree_table[cell_ptr[r+1] - cell_ptr[r]]
+ * summed in fp32 in that order; any other cell from
+ * nearest_table[cell_nearest[r]].  All tables are fp32 rows of 128, 16-byte
+ * aligned; degree_table is the coverage table composed with the degree ->
+ * bucket map (one row per degree).  An index out of range contributes a
+ * zero row and sets MANTIS_FLAG_INDEX.  Replaces MantisNet._covered_init
+ * on cell_structure and the trunk's initial cell state around it
+ * (python/mantisnet/mantisnet/model.py:827-862, :908-935).
+ */
+int32_t mantis_structure_init(const float* base, const float* class_table, int64_t n_classes,
+                              const float* nearest_table, int64_t n_nearest, const float* degree_table,
+                              int64_t n_degrees, const int64_t* cell_ptr, const int64_t* entry_class,
+                              int64_t n_entries, const int64_t* cell_nearest, int64_t n_cells, const int64_t* rows,
+                              int64_t n_out, void* out, int64_t ld_out, int32_t* err_flag, void* stream);
+
+/*
  * Run reduction: out[d, :] = sum over e in [ptr[d], ptr[d+1]) of
  * values[gather[e], :], accumulated in fp32, cast to out_dtype.  Rows with
  * no entries are written as zeros.  values is (n_src, ld) with the first `h`

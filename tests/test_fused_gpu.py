@@ -130,6 +130,81 @@ def test_pair_mlp_residual(device, x2dt):
         assert torch.equal(seeded.cpu(), gathered.cpu()) and torch.equal(tab.cpu(), table)
 
 
+def test_structure_mlp_in_two_launches_matches_the_pair_mlp_of_the_reads(device):
+    # cell_structure's out(relu(lin_a(ln_c(state)) + lin_b(reads))) added to
+    # the updated fp16 rows, as the forward runs it: the hidden layer's part
+    # from the incoming rows (LN(x) W_a^T - x W_b^T + b, fp32), then
+    # relu(that + x' W_b^T) W_o^T + b_o added to the updated rows x' in place;
+    # reads = x' - x
+    gen = _g(17)
+    m = 900
+    state = (2.0 * torch.randn(m, 128, generator=gen)).to(H16)
+    reads = (0.5 * torch.randn(m, 128, generator=gen))
+    upd = (state.float() + reads).to(H16)  # the fp16 rows after the sub-stages
+    wa, wb, wo = _w(128, 128, gen), _w(128, 128, gen), _w(128, 128, gen)
+    b, bo = 0.1 * torch.randn(128, generator=gen), 0.1 * torch.randn(128, generator=gen)
+    x = state.to(device)
+    u = ops.fused_linear(x, wa.to(device), b.to(device), layer_norm=True, x2=x, w2=(-wb).to(device),
+                         out_dtype=torch.float32)
+    out = upd.to(device)
+    ops.fused_linear(out, wb.to(device), None, add1=u, relu=True, w3=wo.to(device), b3=bo.to(device), out=out,
+                     residual=True)
+    ops.raise_on_device_error(device)
+    sf, uf = state.float(), upd.float()
+    u_exp = _h(_ln(sf)) @ wa.float().t() - sf @ wb.float().t() + b
+    torch.testing.assert_close(u.cpu(), u_exp, rtol=1e-4, atol=1e-3)
+    # the reads the pair MLP sees are the rows' actual change
+    hid = F.relu(_h(_ln(sf)) @ wa.float().t() + (uf - sf) @ wb.float().t() + b)
+    exp = (uf + _h(hid) @ wo.float().t() + bo).to(H16).float()
+    torch.testing.assert_close(out.float().cpu(), exp, rtol=3e-3, atol=3e-3)
+
+
+def test_structure_init_matches_the_covered_cell_encodings(device):
+    # base + class rows of the cell's decoder entries + nearest row + coverage
+    # row of its degree on covered cells, the nearest row elsewhere, against
+    # the oracle's formulation over a real batch (and a compact covered-only
+    # row set); a bad class index is flagged
+    import numpy as np
+
+    from mantisnet import collate_positions, synthetic
+    from mantisnet.model import COVERAGE_BUCKET_OF
+
+    batch = collate_positions(synthetic.random_games(4, 6, start=50))
+    gen = _g(21)
+    n_dec = int(batch.dec_class.max()) + 1
+    base = 0.3 * torch.randn(128, generator=gen)
+    cls_t = torch.randn(n_dec, 128, generator=gen)
+    near_t = torch.randn(int(batch.cell_nearest.max()) + 1, 128, generator=gen)
+    cov_t = torch.randn(8, 128, generator=gen)
+    deg_t = cov_t[torch.tensor(COVERAGE_BUCKET_OF)]
+    n_c = batch.cell_pos.shape[0]
+    order = torch.from_numpy(np.argsort(batch.dec_cell.numpy(), kind="stable"))
+    cell_ptr = torch.zeros(n_c + 1, dtype=torch.long)
+    cell_ptr[1:] = torch.bincount(batch.dec_cell, minlength=n_c).cumsum(0)
+    ecls = batch.dec_class[order]
+    deg = cell_ptr[1:] - cell_ptr[:-1]
+    covered = deg > 0
+    classes = torch.zeros(n_c, 128).index_add_(0, batch.dec_cell, cls_t[batch.dec_class])
+    exp = near_t[batch.cell_nearest].clone()
+    exp[covered] = (base + classes[covered] + near_t[batch.cell_nearest[covered]] +
+                    deg_t[deg[covered]])
+    d = lambda t: t.to(device)
+    got = ops.structure_init(d(base), d(cls_t), d(near_t), d(deg_t), d(cell_ptr), d(ecls), d(batch.cell_nearest))
+    ops.raise_on_device_error(device)
+    torch.testing.assert_close(got.float().cpu(), exp.to(H16).float(), rtol=2e-3, atol=2e-3)
+    # the compact covered rows (covered-only cell latents) are those rows
+    rows = torch.nonzero(covered).squeeze(1)
+    got_cov = ops.structure_init(d(base), d(cls_t), d(near_t), d(deg_t), d(cell_ptr), d(ecls),
+                                 d(batch.cell_nearest), rows=d(rows))
+    ops.raise_on_device_error(device)
+    assert torch.equal(got_cov.cpu(), got.cpu()[rows])
+    bad = ecls.clone()
+    bad[0] = n_dec
+    ops.structure_init(d(base), d(cls_t), d(near_t), d(deg_t), d(cell_ptr), d(bad), d(batch.cell_nearest))
+    with pytest.raises(ValueError):
+        ops.raise_on_device_error(device)
+
+
 def test_ffn_residual_with_add1(device):
     gen = _g(4)
     m = 300

@@ -47,10 +47,9 @@ def test_forward_matches_oracle(device, config, count):
 # fixtures whose configuration the MI355X forward does not implement: the
 # smallest widths (its kernels are built for H = 128, 4 heads of 32; those
 # widths run on the CPU oracle, which tests/test_reference_forward.py holds to
-# the same fixtures) and the structure MLP
+# the same fixtures)
 _GPU_UNSUPPORTED = {"tiny_cfg0": "H = 16 widths: the kernels are built for H = 128",
-                    "adjtac_cfg0": "H = 16 widths: the kernels are built for H = 128",
-                    "structure_cfg3": "cell_structure is not implemented in the MI355X forward"}
+                    "adjtac_cfg0": "H = 16 widths: the kernels are built for H = 128"}
 
 
 @pytest.mark.parametrize("name", [pytest.param(n, marks=pytest.mark.skip(reason=_GPU_UNSUPPORTED[n]))
@@ -314,10 +313,14 @@ def test_weights_changed_between_evaluations_are_used(device):
     (dict(cell_latents=True, cell_nodes=True, cell_node_scope="uncovered", cell_adjacency=True), 4, 6),
     (dict(cell_latents=True, cell_nodes=False), 4, 10),
     (dict(action_tactical=True), 4, 8),
+    (dict(cell_latents=True, cell_nodes=True, cell_structure=True), 4, 10),
+    (dict(cell_latents=True, cell_nodes=False, cell_structure=True), 4, 8),
+    (dict(cell_latents=True, cell_nodes=True, cell_structure=True, cell_adjacency=True, action_tactical=True), 5, 3),
 ])
 def test_non_production_knobs_match_oracle(device, knobs, config, count):
-    # the six-neighbour cell stage, the tactical action scalars and
-    # covered-only cell latents on configs[3] / configs[4] positions, against
+    # the six-neighbour cell stage, the tactical action scalars, covered-only
+    # cell latents and the structure MLP with the cells' own static encodings,
+    # on configs[3] / configs[4] positions, against
     # the oracle (pinned to the reference's own forward for each knob by the
     # fixtures of tests/test_reference_forward.py)
     net = _model(device, MantisConfig(**knobs), seed=11)
