@@ -56,12 +56,10 @@
 namespace mantis {
 namespace {
 
-constexpr int kHd = 32;
 constexpr int kWaves = 4;
 constexpr int kQPerWave = 32;
 constexpr int kQTile = kWaves * kQPerWave;  // 128
 constexpr int kKChunk = 64;
-constexpr int kKPitch = kHd + 8;        // 16-bit elements per staged K row
 constexpr int kVtPitch = kKChunk + 8;   // 16-bit elements per staged V^T row
 constexpr float kLazyLog2 = 8.f;        // lazy-rescale threshold (probabilities <= 2^8)
 constexpr int kXcds = 8;
@@ -121,7 +119,11 @@ stone_schedule_kernel(const int32_t* __restrict__ seq_lens, int64_t n_pos, int h
   }
 }
 
-template <bool kHalf>
+// HD: the head dim, 16, 32 or 64.  The score product runs HD / 32 MFMA K
+// steps (one for HD = 16, whose upper K slots hold zeros in the Q fragment),
+// the value product HD / 16 output tiles; a chunk's K and V rows are staged
+// in HD / 8 16-byte pieces per key.
+template <bool kHalf, int HD>
 __global__ void __launch_bounds__(256)
 stone_attention_kernel(const uint16_t* __restrict__ q, int64_t qsp, int64_t qsa, int64_t qst,
                        const uint16_t* __restrict__ k, int64_t ksp, int64_t ksa, int64_t kst,
@@ -130,8 +132,14 @@ stone_attention_kernel(const uint16_t* __restrict__ q, int64_t qsp, int64_t qsa,
                        uint16_t* __restrict__ out, int64_t osp, int64_t osa, int64_t ost,
                        float* __restrict__ lse, float c_log2, int64_t n_items,
                        const int32_t* __restrict__ schedule) {
+  static_assert(HD == 16 || HD == 32 || HD == 64, "head dims 16, 32 and 64");
+  constexpr int kKPitch = HD + 8;                // 16-bit elements per staged K row
+  constexpr int kKs = HD < 32 ? 1 : HD / 32;     // K steps of the score product
+  constexpr int kDt = HD / 16;                   // 16-dim output tiles
+  constexpr int kPieces = kKChunk * HD / 8;      // 16-byte pieces of a chunk's K (or V) rows
+  constexpr int kPer = kPieces < 256 ? 1 : kPieces / 256;
   __shared__ __attribute__((aligned(16))) uint16_t sk[2][kKChunk * kKPitch];
-  __shared__ __attribute__((aligned(16))) uint16_t svt[2][kHd * kVtPitch];
+  __shared__ __attribute__((aligned(16))) uint16_t svt[2][HD * kVtPitch];
   // item of this workgroup: from the schedule, or XCD-contiguous (the grid is
   // a multiple of kXcds; block b runs item (b % kXcds) * (grid / kXcds) + b / kXcds)
   int64_t item;
@@ -156,9 +164,9 @@ stone_attention_kernel(const uint16_t* __restrict__ q, int64_t qsp, int64_t qsa,
   const uint4 zero4 = make_uint4(0, 0, 0, 0);
 
   if (q0 >= L) {  // a tile past the live prefix does no key work
-    for (int i = threadIdx.x; i < kQTile * 4; i += 256) {
-      const int64_t row = q0 + i / 4;
-      const int c = (i % 4) * 8;
+    for (int i = threadIdx.x; i < kQTile * (HD / 8); i += 256) {
+      const int64_t row = q0 + i / (HD / 8);
+      const int c = (i % (HD / 8)) * 8;
       if (row < T) {
         *reinterpret_cast<uint4*>(op + row * ost + c) = zero4;
         if (lp && c == 0) lp[row] = 0.f;
@@ -176,46 +184,67 @@ stone_attention_kernel(const uint16_t* __restrict__ q, int64_t qsp, int64_t qsa,
   const i32x4_t qrs = rows_rsrc(qp, uint32_t(qst * 2), uint32_t(L));
   const i32x4_t krs = rows_rsrc(kp, uint32_t(kst * 2), uint32_t(L));
   const i32x4_t vrs = rows_rsrc(vp, uint32_t(vst * 2), uint32_t(L));
-  typename FR::vec qf[2];
+  // the K slots of a score step: dims 32 ks + 8 g .. +7 (HD = 16: lanes
+  // g >= 2 hold zeros in the Q fragment, and read real K dims 8 (g & 1) .. so
+  // every product term they add is an exact zero)
+  auto kdim = [&](int ks) { return HD < 32 ? 8 * (g & 1) : 32 * ks + 8 * g; };
+  typename FR::vec qf[2][kKs];
   int64_t qrow[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     qrow[j] = q0 + wave * kQPerWave + 16 * j + l16;
-    // B fragment of Q^T: query l16, dims 8g..8g+7
-    qf[j] = FR::cast(row_load16(qrs, int32_t(qrow[j]), 16 * g));
+    // B fragment of Q^T: query l16, its dims of each K step
+#pragma unroll
+    for (int ks = 0; ks < kKs; ++ks) {
+      uint4 u = row_load16(qrs, int32_t(qrow[j]), 2 * kdim(ks));
+      if (HD < 32 && g >= 2) u = make_uint4(0u, 0u, 0u, 0u);
+      qf[j][ks] = FR::cast(u);
+    }
   }
 
-  // staging role of this thread: one 16-byte piece of one key's K and V rows
-  const int st_key = threadIdx.x / 4, st_d = (threadIdx.x % 4) * 8;
-  uint4 kreg, vreg;
+  // staging role of this thread: kPer 16-byte pieces of the chunk's K and V
+  // rows (piece i: key i / (HD / 8), dims 8 (i % (HD / 8)) ..); with HD = 16
+  // the upper half of the workgroup stages nothing
+  const bool stager = int(threadIdx.x) < kPieces;
+  uint4 kreg[kPer], vreg[kPer];
   auto fetch = [&](int64_t kb) {
-    const int32_t row = int32_t(kb) + st_key;
-    kreg = row_load16(krs, row, 2 * st_d);
-    vreg = row_load16(vrs, row, 2 * st_d);
+#pragma unroll
+    for (int r = 0; r < kPer; ++r) {
+      const int i = int(threadIdx.x) + 256 * r;
+      const int32_t row = stager ? int32_t(kb) + i / (HD / 8) : -1;
+      kreg[r] = row_load16(krs, row, 16 * (i % (HD / 8)));
+      vreg[r] = row_load16(vrs, row, 16 * (i % (HD / 8)));
+    }
   };
   auto stage = [&](int buf) {
-    *reinterpret_cast<uint4*>(&sk[buf][st_key * kKPitch + st_d]) = kreg;
-    const uint32_t w[4] = {vreg.x, vreg.y, vreg.z, vreg.w};
-    uint16_t* col = &svt[buf][st_d * kVtPitch + st_key];
+    if (!stager) return;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      col[(2 * i) * kVtPitch] = uint16_t(w[i] & 0xffffu);
-      col[(2 * i + 1) * kVtPitch] = uint16_t(w[i] >> 16);
+    for (int r = 0; r < kPer; ++r) {
+      const int i = int(threadIdx.x) + 256 * r;
+      const int st_key = i / (HD / 8), st_d = 8 * (i % (HD / 8));
+      *reinterpret_cast<uint4*>(&sk[buf][st_key * kKPitch + st_d]) = kreg[r];
+      const uint32_t w[4] = {vreg[r].x, vreg[r].y, vreg[r].z, vreg[r].w};
+      uint16_t* col = &svt[buf][st_d * kVtPitch + st_key];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        col[(2 * e) * kVtPitch] = uint16_t(w[e] & 0xffffu);
+        col[(2 * e + 1) * kVtPitch] = uint16_t(w[e] >> 16);
+      }
     }
   };
 
   // per sub-tile: the reference point of the exponent (raw-score units), O^T
-  // accumulators (two 16-dim tiles) and the row sums, accumulated by an extra
+  // accumulators (HD / 16 tiles of 16 dims) and the row sums, accumulated by an extra
   // product with an all-ones A operand (every D row holds the sum)
   float m[2] = {-INFINITY, -INFINITY};
   float thr[2];  // m + kLazyLog2 / c_log2: a score above it moves the reference point
   const float lazy_raw = kLazyLog2 / c_log2;
-  f32x4_t o[2][2], lsum[2];
+  f32x4_t o[2][kDt], lsum[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     lsum[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int dt = 0; dt < 2; ++dt) o[j][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int dt = 0; dt < kDt; ++dt) o[j][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
   const uint32_t one2 = FR::pack_unit(1.f, 1.f);
   const typename FR::vec ones = FR::cast(make_uint4(one2, one2, one2, one2));
@@ -243,10 +272,13 @@ stone_attention_kernel(const uint16_t* __restrict__ q, int64_t qsp, int64_t qsa,
       f32x4_t s[kNJ][4];
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt) {
-        const typename FR::vec kf =
-            FR::cast(*reinterpret_cast<const uint4*>(&sk[buf][(16 * tt + l16) * kKPitch + 8 * g]));
 #pragma unroll
-        for (int j = 0; j < kNJ; ++j) s[j][tt] = mfma16x16x32(kf, qf[j], cb[tt]);
+        for (int ks = 0; ks < kKs; ++ks) {
+          const typename FR::vec kf =
+              FR::cast(*reinterpret_cast<const uint4*>(&sk[buf][(16 * tt + l16) * kKPitch + kdim(ks)]));
+#pragma unroll
+          for (int j = 0; j < kNJ; ++j) s[j][tt] = mfma16x16x32(kf, qf[j][ks], ks == 0 ? cb[tt] : s[j][tt]);
+        }
       }
       typename FR::vec pf[kNJ][2];
 #pragma unroll
@@ -277,8 +309,8 @@ stone_attention_kernel(const uint16_t* __restrict__ q, int64_t qsp, int64_t qsa,
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
             lsum[j][t] *= alpha;
-            o[j][0][t] *= alpha;
-            o[j][1][t] *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < kDt; ++dt) o[j][dt][t] *= alpha;
           }
         }
         const float mc = m[j] * c_log2;
@@ -299,7 +331,7 @@ stone_attention_kernel(const uint16_t* __restrict__ q, int64_t qsp, int64_t qsa,
 #pragma unroll
       for (int sc = 0; sc < 2; ++sc) {
 #pragma unroll
-        for (int dt = 0; dt < 2; ++dt) {
+        for (int dt = 0; dt < kDt; ++dt) {
           const uint16_t* row = &svt[buf][(16 * dt + l16) * kVtPitch + 32 * sc];
           const uint2 lo = *reinterpret_cast<const uint2*>(row + 4 * g);
           const uint2 hi = *reinterpret_cast<const uint2*>(row + 16 + 4 * g);
@@ -345,13 +377,13 @@ stone_attention_kernel(const uint16_t* __restrict__ q, int64_t qsp, int64_t qsa,
     if (qrow[j] < T) {
       const bool live = qrow[j] < L;
       const float inv = (live && lt > 0.f) ? 1.f / lt : 0.f;
-      uint2 w0, w1;
-      w0.x = FR::pack_unit(o[j][0][0] * inv, o[j][0][1] * inv);
-      w0.y = FR::pack_unit(o[j][0][2] * inv, o[j][0][3] * inv);
-      w1.x = FR::pack_unit(o[j][1][0] * inv, o[j][1][1] * inv);
-      w1.y = FR::pack_unit(o[j][1][2] * inv, o[j][1][3] * inv);
-      *reinterpret_cast<uint2*>(op + qrow[j] * ost + 4 * g) = w0;
-      *reinterpret_cast<uint2*>(op + qrow[j] * ost + 16 + 4 * g) = w1;
+#pragma unroll
+      for (int dt = 0; dt < kDt; ++dt) {
+        uint2 w;
+        w.x = FR::pack_unit(o[j][dt][0] * inv, o[j][dt][1] * inv);
+        w.y = FR::pack_unit(o[j][dt][2] * inv, o[j][dt][3] * inv);
+        *reinterpret_cast<uint2*>(op + qrow[j] * ost + 16 * dt + 4 * g) = w;
+      }
       if (lp && g == 0) lp[qrow[j]] = live ? (m[j] * c_log2 + log2f(lt)) * 0.6931471805599453f : 0.f;
     }
   }
@@ -365,6 +397,226 @@ stone_attention_kernel(const uint16_t* __restrict__ q, int64_t qsp, int64_t qsa,
 // [0, 128), [128, 256) and [256, 384) of the projected rows (row p * T + t;
 // head a at 32 a).  One workgroup per position: 16 lanes per (head, query)
 // row, each over every 16th key, the scores of the position staged in LDS.
+// Backward of the ragged attention (the reference's flash backward,
+// attention.py:166-560, with its row statistic delta = sum(out * grad_out)).
+// With a_ij = exp(scale q_i . k_j - lse_i) over the live keys j < L of the
+// live rows i < L, dp_ij = go_i . v_j and ds_ij = a_ij (dp_ij - delta_i):
+//   dq_i = scale sum_j ds_ij k_j,  dk_j = scale sum_i ds_ij q_i,  dv_j = sum_i a_ij go_i.
+// Two passes, each with a row per lane (two adjacent lanes per row for
+// HD = 64, each holding half of its dims): the query-major pass forms delta
+// and dq over the position's keys, the key-major pass dk and dv over its
+// queries; the other side's rows are staged in LDS in 64-row chunks, as fp32.
+// Every sum is fp32 in a fixed order (no atomics): two calls agree bitwise.
+// Rows and keys at or past L get zero gradients.
+template <int HD>
+struct BwdGeom {
+  static constexpr int kSplit = HD == 64 ? 2 : 1;  // lanes per row
+  static constexpr int kDims = HD / kSplit;         // dims per lane
+  static constexpr int kRows = 256 / kSplit;        // rows per workgroup
+};
+constexpr int kBwdChunk = 64;
+
+template <bool kHalf>
+__device__ __forceinline__ float bits_to_f32(uint16_t u) {
+  if constexpr (kHalf) return float(__builtin_bit_cast(_Float16, u));
+  else return bf2f(u);
+}
+
+// n (a multiple of 8) 16-bit values from p (16-byte aligned) into fp32
+template <bool kHalf, int N>
+__device__ __forceinline__ void load_bits(const uint16_t* p, float* x) {
+#pragma unroll
+  for (int c = 0; c < N; c += 8) {
+    const uint4 u = *reinterpret_cast<const uint4*>(p + c);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[c + 2 * e] = bits_to_f32<kHalf>(uint16_t(w[e] & 0xffffu));
+      x[c + 2 * e + 1] = bits_to_f32<kHalf>(uint16_t(w[e] >> 16));
+    }
+  }
+}
+
+template <bool kHalf, int N>
+__device__ __forceinline__ void store_bits(uint16_t* p, const float* x) {
+  using FR = Frag<kHalf>;
+#pragma unroll
+  for (int c = 0; c < N; c += 8) {
+    uint4 u;
+    u.x = FR::pack(x[c], x[c + 1]);
+    u.y = FR::pack(x[c + 2], x[c + 3]);
+    u.z = FR::pack(x[c + 4], x[c + 5]);
+    u.w = FR::pack(x[c + 6], x[c + 7]);
+    *reinterpret_cast<uint4*>(p + c) = u;
+  }
+}
+
+struct BwdRows {  // one (P, A, T, HD) operand: base and element strides
+  const uint16_t* p;
+  int64_t sp, sa, st;
+  __device__ const uint16_t* row(int64_t pos, int64_t a, int64_t t) const { return p + pos * sp + a * sa + t * st; }
+};
+struct BwdOut {
+  uint16_t* p;
+  int64_t sp, sa, st;
+  __device__ uint16_t* row(int64_t pos, int64_t a, int64_t t) const { return p + pos * sp + a * sa + t * st; }
+};
+
+// Stage rows kb .. kb+63 of two operands (zeros at or past L) as fp32.
+template <bool kHalf, int HD>
+__device__ __forceinline__ void stage_pair(const BwdRows& x, const BwdRows& y, int64_t pos, int64_t a, int64_t kb,
+                                           int64_t L, float (*sx)[HD], float (*sy)[HD]) {
+  for (int i = threadIdx.x; i < kBwdChunk * HD / 8; i += 256) {
+    const int r = i / (HD / 8), c = 8 * (i % (HD / 8));
+    float vx[8], vy[8];
+    if (kb + r < L) {
+      load_bits<kHalf, 8>(x.row(pos, a, kb + r) + c, vx);
+      load_bits<kHalf, 8>(y.row(pos, a, kb + r) + c, vy);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) vx[e] = vy[e] = 0.f;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      sx[r][c + e] = vx[e];
+      sy[r][c + e] = vy[e];
+    }
+  }
+}
+
+template <bool kHalf, int HD>
+__global__ void __launch_bounds__(256)
+stone_attention_bwd_q_kernel(BwdRows q, BwdRows k, BwdRows v, BwdRows o, BwdRows go, const int32_t* __restrict__ seq_lens,
+                             int heads, int64_t T, const float* __restrict__ lse, float scale,
+                             float* __restrict__ delta, BwdOut dq) {
+  using G = BwdGeom<HD>;
+  __shared__ float sk[kBwdChunk][HD], sv[kBwdChunk][HD];
+  const int64_t n_tiles = (T + G::kRows - 1) / G::kRows;
+  const int64_t pa = blockIdx.x / n_tiles, tile = blockIdx.x % n_tiles;
+  const int64_t pos = pa / heads, a = pa % heads;
+  int64_t L = seq_lens[pos];
+  L = L < 0 ? 0 : (L > T ? T : L);
+  const int64_t i = tile * G::kRows + threadIdx.x / G::kSplit;
+  const int off = (threadIdx.x % G::kSplit) * G::kDims;
+  const bool live = i < L;
+  float qv[G::kDims], gv[G::kDims], acc[G::kDims];
+  float dl = 0.f, li = 0.f;
+  if (live) {
+    float ov[G::kDims];
+    load_bits<kHalf, G::kDims>(q.row(pos, a, i) + off, qv);
+    load_bits<kHalf, G::kDims>(go.row(pos, a, i) + off, gv);
+    load_bits<kHalf, G::kDims>(o.row(pos, a, i) + off, ov);
+#pragma unroll
+    for (int d = 0; d < G::kDims; ++d) dl = fmaf(ov[d], gv[d], dl);
+    li = lse[pa * T + i];
+  } else {
+#pragma unroll
+    for (int d = 0; d < G::kDims; ++d) qv[d] = gv[d] = 0.f;
+  }
+  if constexpr (G::kSplit == 2) dl += __shfl_xor(dl, 1);
+#pragma unroll
+  for (int d = 0; d < G::kDims; ++d) acc[d] = 0.f;
+  if (tile * G::kRows < L) {  // workgroup-uniform: some row of the tile is live
+    for (int64_t kb = 0; kb < L; kb += kBwdChunk) {
+      __syncthreads();
+      stage_pair<kHalf, HD>(k, v, pos, a, kb, L, sk, sv);
+      __syncthreads();
+      const int n = int(L - kb < kBwdChunk ? L - kb : kBwdChunk);
+      for (int j = 0; j < n; ++j) {
+        float sc = 0.f, dp = 0.f;
+#pragma unroll
+        for (int d = 0; d < G::kDims; ++d) {
+          sc = fmaf(qv[d], sk[j][off + d], sc);
+          dp = fmaf(gv[d], sv[j][off + d], dp);
+        }
+        if constexpr (G::kSplit == 2) {
+          sc += __shfl_xor(sc, 1);
+          dp += __shfl_xor(dp, 1);
+        }
+        const float al = live ? expf(fmaf(sc, scale, -li)) : 0.f;
+        const float ds = al * (dp - dl);
+#pragma unroll
+        for (int d = 0; d < G::kDims; ++d) acc[d] = fmaf(ds, sk[j][off + d], acc[d]);
+      }
+    }
+  }
+  if (i < T) {
+#pragma unroll
+    for (int d = 0; d < G::kDims; ++d) acc[d] = live ? acc[d] * scale : 0.f;
+    store_bits<kHalf, G::kDims>(dq.row(pos, a, i) + off, acc);
+    if (off == 0) delta[pa * T + i] = live ? dl : 0.f;
+  }
+}
+
+template <bool kHalf, int HD>
+__global__ void __launch_bounds__(256)
+stone_attention_bwd_kv_kernel(BwdRows q, BwdRows k, BwdRows v, BwdRows go, const int32_t* __restrict__ seq_lens,
+                              int heads, int64_t T, const float* __restrict__ lse, float scale,
+                              const float* __restrict__ delta, BwdOut dk, BwdOut dv) {
+  using G = BwdGeom<HD>;
+  __shared__ float sq[kBwdChunk][HD], sg[kBwdChunk][HD];
+  __shared__ float sl[kBwdChunk], sd[kBwdChunk];
+  const int64_t n_tiles = (T + G::kRows - 1) / G::kRows;
+  const int64_t pa = blockIdx.x / n_tiles, tile = blockIdx.x % n_tiles;
+  const int64_t pos = pa / heads, a = pa % heads;
+  int64_t L = seq_lens[pos];
+  L = L < 0 ? 0 : (L > T ? T : L);
+  const int64_t j = tile * G::kRows + threadIdx.x / G::kSplit;
+  const int off = (threadIdx.x % G::kSplit) * G::kDims;
+  const bool live = j < L;
+  float kv[G::kDims], vv[G::kDims], ak[G::kDims], av[G::kDims];
+  if (live) {
+    load_bits<kHalf, G::kDims>(k.row(pos, a, j) + off, kv);
+    load_bits<kHalf, G::kDims>(v.row(pos, a, j) + off, vv);
+  } else {
+#pragma unroll
+    for (int d = 0; d < G::kDims; ++d) kv[d] = vv[d] = 0.f;
+  }
+#pragma unroll
+  for (int d = 0; d < G::kDims; ++d) ak[d] = av[d] = 0.f;
+  if (tile * G::kRows < L) {  // workgroup-uniform
+    for (int64_t qb = 0; qb < L; qb += kBwdChunk) {
+      __syncthreads();
+      stage_pair<kHalf, HD>(q, go, pos, a, qb, L, sq, sg);
+      for (int r = threadIdx.x; r < kBwdChunk; r += 256) {
+        const bool ok = qb + r < L;
+        sl[r] = ok ? lse[pa * T + qb + r] : 0.f;
+        sd[r] = ok ? delta[pa * T + qb + r] : 0.f;
+      }
+      __syncthreads();
+      const int n = int(L - qb < kBwdChunk ? L - qb : kBwdChunk);
+      for (int r = 0; r < n; ++r) {
+        float sc = 0.f, dp = 0.f;
+#pragma unroll
+        for (int d = 0; d < G::kDims; ++d) {
+          sc = fmaf(sq[r][off + d], kv[d], sc);
+          dp = fmaf(sg[r][off + d], vv[d], dp);
+        }
+        if constexpr (G::kSplit == 2) {
+          sc += __shfl_xor(sc, 1);
+          dp += __shfl_xor(dp, 1);
+        }
+        const float al = live ? expf(fmaf(sc, scale, -sl[r])) : 0.f;
+        const float ds = al * (dp - sd[r]);
+#pragma unroll
+        for (int d = 0; d < G::kDims; ++d) {
+          av[d] = fmaf(al, sg[r][off + d], av[d]);
+          ak[d] = fmaf(ds, sq[r][off + d], ak[d]);
+        }
+      }
+    }
+  }
+  if (j < T) {
+#pragma unroll
+    for (int d = 0; d < G::kDims; ++d) {
+      ak[d] = live ? ak[d] * scale : 0.f;
+      av[d] = live ? av[d] : 0.f;
+    }
+    store_bits<kHalf, G::kDims>(dk.row(pos, a, j) + off, ak);
+    store_bits<kHalf, G::kDims>(dv.row(pos, a, j) + off, av);
+  }
+}
+
 constexpr int kLatentThreads = 256;
 
 template <bool kHalf>
@@ -485,14 +737,14 @@ extern "C" int32_t mantis_stone_attention(const void* q, const int64_t* qs, cons
                                           void* stream) {
   if (n_pos == 0 || t == 0) return MANTIS_OK;
   if (!q || !k || !v || !out || !seq_lens || !qs || !ks || !vs || !os) return MANTIS_E_ARG;
-  if (hd != kHd || heads <= 0 || n_pos < 0 || t < 0) return MANTIS_E_ARG;
+  if ((hd != 16 && hd != 32 && hd != 64) || heads <= 0 || n_pos < 0 || t < 0) return MANTIS_E_ARG;
   if (dtype != MANTIS_BF16 && dtype != MANTIS_F16) return MANTIS_E_ARG;
   // The innermost (dim) stride must be 1 and every row start 16-byte aligned.
   for (const int64_t* st : {qs, ks, vs, os}) {
     if (st[3] != 1) return MANTIS_E_ARG;
     if ((st[0] | st[1] | st[2]) % 8) return MANTIS_E_ARG;
   }
-  // q, k and v rows are read through buffer descriptors: a row pitch of 32 to
+  // q, k and v rows are read through buffer descriptors: a row pitch of hd to
   // 8,191 elements (the descriptor's stride field) and row indices in int32
   for (const int64_t* st : {qs, ks, vs})
     if (st[2] < hd || st[2] >= 8192) return MANTIS_E_ARG;
@@ -504,10 +756,74 @@ extern "C" int32_t mantis_stone_attention(const void* q, const int64_t* qs, cons
   if (grid > 2147483647LL) return MANTIS_E_ARG;
   hipStream_t st = as_stream(stream);
   const float c_log2 = 1.4426950408889634f / sqrtf(float(hd));
-  auto kernel = dtype == MANTIS_F16 ? stone_attention_kernel<true> : stone_attention_kernel<false>;
+  const bool f16 = dtype == MANTIS_F16;
+  auto kernel = hd == 16   ? (f16 ? stone_attention_kernel<true, 16> : stone_attention_kernel<false, 16>)
+                : hd == 32 ? (f16 ? stone_attention_kernel<true, 32> : stone_attention_kernel<false, 32>)
+                           : (f16 ? stone_attention_kernel<true, 64> : stone_attention_kernel<false, 64>);
   kernel<<<unsigned(grid), 256, 0, st>>>(
       static_cast<const uint16_t*>(q), qs[0], qs[1], qs[2], static_cast<const uint16_t*>(k), ks[0],
       ks[1], ks[2], static_cast<const uint16_t*>(v), vs[0], vs[1], vs[2], seq_lens, heads, t,
       static_cast<uint16_t*>(out), os[0], os[1], os[2], lse, c_log2, n_items, schedule);
   return launched();
+}
+
+namespace {
+template <bool kHalf, int HD>
+int32_t launch_attention_backward(const BwdRows& q, const BwdRows& k, const BwdRows& v, const BwdRows& o,
+                                  const BwdRows& go, const int32_t* seq_lens, int64_t n_pos, int heads, int64_t t,
+                                  const float* lse, float* delta, const BwdOut& dq, const BwdOut& dk,
+                                  const BwdOut& dv, hipStream_t st) {
+  using G = BwdGeom<HD>;
+  const int64_t grid = n_pos * heads * ((t + G::kRows - 1) / G::kRows);
+  if (grid > 2147483647LL) return MANTIS_E_ARG;
+  const float scale = 1.f / sqrtf(float(HD));
+  stone_attention_bwd_q_kernel<kHalf, HD><<<unsigned(grid), 256, 0, st>>>(q, k, v, o, go, seq_lens, heads, t, lse,
+                                                                          scale, delta, dq);
+  stone_attention_bwd_kv_kernel<kHalf, HD><<<unsigned(grid), 256, 0, st>>>(q, k, v, go, seq_lens, heads, t, lse,
+                                                                           scale, delta, dk, dv);
+  return launched();
+}
+}  // namespace
+
+extern "C" int32_t mantis_stone_attention_backward(const void* q, const int64_t* qs, const void* k,
+                                                   const int64_t* ks, const void* v, const int64_t* vs,
+                                                   const void* out, const int64_t* os, const void* grad_out,
+                                                   const int64_t* gs, const float* lse, int32_t dtype,
+                                                   const int32_t* seq_lens, int64_t n_pos, int32_t heads, int64_t t,
+                                                   int32_t hd, float* delta, void* dq, const int64_t* dqs, void* dk,
+                                                   const int64_t* dks, void* dv, const int64_t* dvs, void* stream) {
+  if (n_pos == 0 || t == 0) return MANTIS_OK;
+  if (!q || !k || !v || !out || !grad_out || !lse || !seq_lens || !delta || !dq || !dk || !dv) return MANTIS_E_ARG;
+  if (!qs || !ks || !vs || !os || !gs || !dqs || !dks || !dvs) return MANTIS_E_ARG;
+  if ((hd != 16 && hd != 32 && hd != 64) || heads <= 0 || n_pos < 0 || t < 0) return MANTIS_E_ARG;
+  if (dtype != MANTIS_BF16 && dtype != MANTIS_F16) return MANTIS_E_ARG;
+  // unit dim stride and 16-byte aligned rows everywhere
+  for (const int64_t* st : {qs, ks, vs, os, gs, dqs, dks, dvs}) {
+    if (st[3] != 1) return MANTIS_E_ARG;
+    if ((st[0] | st[1] | st[2]) % 8) return MANTIS_E_ARG;
+  }
+  for (const void* ptr : {q, k, v, out, grad_out, static_cast<const void*>(dq), static_cast<const void*>(dk),
+                          static_cast<const void*>(dv)})
+    if (!aligned16(ptr)) return MANTIS_E_ARG;
+  auto rows = [](const void* ptr, const int64_t* st) {
+    return BwdRows{static_cast<const uint16_t*>(ptr), st[0], st[1], st[2]};
+  };
+  auto outs = [](void* ptr, const int64_t* st) { return BwdOut{static_cast<uint16_t*>(ptr), st[0], st[1], st[2]}; };
+  const BwdRows Q = rows(q, qs), K = rows(k, ks), V = rows(v, vs), O = rows(out, os), GO = rows(grad_out, gs);
+  const BwdOut DQ = outs(dq, dqs), DK = outs(dk, dks), DV = outs(dv, dvs);
+  hipStream_t st = as_stream(stream);
+  const bool f16 = dtype == MANTIS_F16;
+#define MANTIS_BWD(H, HD_)                                                                                    \
+  return launch_attention_backward<H, HD_>(Q, K, V, O, GO, seq_lens, n_pos, heads, t, lse, delta, DQ, DK, DV, st)
+  if (hd == 16) {
+    if (f16) MANTIS_BWD(true, 16);
+    MANTIS_BWD(false, 16);
+  }
+  if (hd == 32) {
+    if (f16) MANTIS_BWD(true, 32);
+    MANTIS_BWD(false, 32);
+  }
+  if (f16) MANTIS_BWD(true, 64);
+  MANTIS_BWD(false, 64);
+#undef MANTIS_BWD
 }

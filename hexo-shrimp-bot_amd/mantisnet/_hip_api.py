@@ -80,6 +80,8 @@ SIGNATURES = {
                                 i32),
     "mantis_row_encode": ([vp, i32, i64, i64, vp, i64, vp, vp, i64, vp, i64, vp, vp, vp, vp, vp], i32),
     "mantis_stone_attention": ([vp, vp, vp, vp, vp, vp, i32, vp, i64, i32, i64, i32, vp, vp, vp, vp, vp], i32),
+    "mantis_stone_attention_backward": ([vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, vp, i64, i32, i64, i32, vp,
+                                         vp, vp, vp, vp, vp, vp, vp], i32),
     "mantis_latent_attend": ([vp, i32, i64, vp, i64, i64, vp, vp], i32),
     "mantis_stone_attention_schedule_len": ([i64, i32, i64], i64),
     "mantis_stone_attention_schedule": ([vp, i64, i32, i64, vp, vp], i32),

@@ -15,8 +15,10 @@ Differences from the reference, all deliberate:
 
 * no fallback: a CPU tensor, a dtype or shape the kernels do not cover
   raises instead of silently composing torch ops;
-* the attention-family kernels are specialised to the model's geometry —
-  4 heads x 32 dims (128-wide rows); ``fused_attention`` takes head_dim 32;
+* the segment-attention kernels are specialised to the model's geometry —
+  4 heads x 32 dims (128-wide rows); ``fused_attention`` takes the head dims
+  of the reference's kernel (16, 32, 64) in fp16 or bf16 and raises for
+  others, where the reference falls back to SDPA;
 * ``aggregate_to_windows`` writes zero rows for windows without entries
   (the reference leaves them uninitialised; windows are never empty).
 
@@ -45,8 +47,9 @@ _NS = "mantisnet"
 @torch.library.custom_op(f"{_NS}::fused_attention", mutates_args=())
 def fused_attention(q: Tensor, k: Tensor, v: Tensor, seq_lens: Tensor) -> tuple[Tensor, Tensor]:
     """Ragged attention over each position's live prefix; pad query rows are
-    exactly zero.  q/k/v (P, A, T, 32) fp16/bf16; returns (out like q, lse
-    (P, A, T) fp32 — natural-log softmax normaliser of each live row)."""
+    exactly zero.  q/k/v (P, A, T, D) fp16/bf16 with D in {16, 32, 64} (the
+    reference kernel's head dims, attention.py:727-735); returns (out like q,
+    lse (P, A, T) fp32 — natural-log softmax normaliser of each live row)."""
     out, lse = ops.stone_attention(q, k, v, seq_lens, want_lse=True)
     return out, lse
 
@@ -60,7 +63,7 @@ def _(q, k, v, seq_lens):
 def fused_attention_backward(q: Tensor, k: Tensor, v: Tensor, seq_lens: Tensor, out: Tensor, lse: Tensor,
                              grad_out: Tensor) -> tuple[Tensor, Tensor, Tensor]:
     """(dq, dk, dv) of fused_attention; pad rows and keys get zero gradients."""
-    dq, dk, dv = ops.stone_attention_backward(q, k, v, seq_lens, lse, grad_out)
+    dq, dk, dv = ops.stone_attention_backward(q, k, v, seq_lens, out, lse, grad_out)
     return dq.contiguous(), dk.contiguous(), dv.contiguous()
 
 

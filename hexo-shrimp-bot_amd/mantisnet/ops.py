@@ -673,33 +673,42 @@ def latent_broadcast_backward(q, k, v, window_pos, offsets, order, m, l, grad_ou
     return dq, dk.view(k.shape), dv.view(v.shape)
 
 
-def stone_attention_backward(q, k, v, seq_lens, lse, grad_out):
-    """(dq, dk, dv) of stone_attention: every live query row of a position over
-    its live prefix, heads in blocks of four (the softmax statistics from
-    the forward's natural-log lse)."""
+def stone_attention_backward(q, k, v, seq_lens, out, lse, grad_out):
+    """(dq, dk, dv) of stone_attention, in q's dtype and layout: the flash
+    backward over each position's live prefix with delta = sum(out * grad_out)
+    per row (mantis_stone_attention_backward); pad rows and keys get zero
+    gradients.  lse: the forward's natural-log normaliser, (P, A, T) fp32."""
+    dev = _on_gpu(q, k, v, seq_lens, out, lse, grad_out)
+    if q.ndim != 4 or any(x.shape != q.shape for x in (k, v, out, grad_out)):
+        raise ValueError("q, k, v, out and grad_out must have one (P, A, T, D) shape")
     p, heads, t, hd = q.shape
-    if hd != 32 or heads % 4:
-        raise ValueError("the attention backward covers head_dim 32 and a multiple of 4 heads")
-    g = heads // 4
-    rows = lambda x: x.permute(0, 2, 1, 3).reshape(p * t * g, 4, 32)  # noqa: E731  (p, t, head block)
-    dev = q.device
-    lens = seq_lens.long().clamp(0, t)
-    # the live (i, j) pairs of every position and head block, row-major by i
-    cnt = torch.where(torch.arange(t, device=dev)[None, :] < lens[:, None], lens[:, None], 0)  # (p, t)
-    cnt = cnt.repeat_interleave(g, dim=1).reshape(-1)  # rows (p, t, g)
-    ptr = torch.zeros(cnt.numel() + 1, dtype=torch.int64, device=dev)
-    torch.cumsum(cnt, 0, out=ptr[1:])
-    r = torch.repeat_interleave(torch.arange(cnt.numel(), device=dev), cnt)
-    j = torch.arange(r.numel(), device=dev) - ptr[r]
-    pos, hb = r // (t * g), r % g
-    other = (pos * t + j) * g + hb  # row (p, j, hb)
-    m = lse.permute(0, 2, 1).reshape(p * t * g, 4)
-    ones = torch.ones_like(m)
-    dq, dk, dv, _, _ = attention_backward(rows(q), rows(k), rows(v), None, None,
-                                          grad_out.permute(0, 2, 1, 3).reshape(p * t * g, 4, 32), m, ones, ptr, other,
-                                          None, None, ptr, other, None, None, None)
-    back = lambda x: x.view(p, t, heads, hd).permute(0, 2, 1, 3)  # noqa: E731
-    return back(dq), back(dk), back(dv)
+    if hd not in (16, 32, 64):
+        raise ValueError("the attention backward supports head_dim 16, 32 and 64")
+    if q.dtype not in (torch.float16, torch.bfloat16) or any(x.dtype != q.dtype for x in (k, v, out)):
+        raise ValueError("q, k, v and out must share float16 or bfloat16")
+    if seq_lens.shape != (p,) or seq_lens.dtype != torch.int32:
+        raise ValueError("seq_lens must be int32 with shape (P,)")
+    if lse.shape != (p, heads, t) or lse.dtype != torch.float32:
+        raise ValueError("lse must be the forward's (P, A, T) fp32 normaliser")
+    aligned = lambda x: x.stride(3) == 1 and all(s % 8 == 0 for s in x.stride()[:3])  # noqa: E731
+    fix = lambda x: x if aligned(x) else x.contiguous()  # noqa: E731
+    q, k, v, out = fix(q), fix(k), fix(v), fix(out)
+    grad_out = fix(grad_out.to(q.dtype))
+    lse, seq_lens = lse.contiguous(), seq_lens.contiguous()
+
+    def like(x):
+        y = torch.empty_like(x)
+        return y if aligned(y) else torch.empty(x.shape, dtype=x.dtype, device=dev)
+
+    dq, dk, dv = like(q), like(k), like(v)
+    delta = torch.empty((p, heads, t), dtype=torch.float32, device=dev)
+    _launch("stone_attention_backward", 0.0, 0.0, lambda: _check(
+        _lib().mantis_stone_attention_backward(
+            _ptr(q), _strides(q), _ptr(k), _strides(k), _ptr(v), _strides(v), _ptr(out), _strides(out),
+            _ptr(grad_out), _strides(grad_out), _ptr(lse), _dt(q), _ptr(seq_lens), p, heads, t, hd, _ptr(delta),
+            _ptr(dq), _strides(dq), _ptr(dk), _strides(dk), _ptr(dv), _strides(dv), _stream()),
+        "stone_attention_backward"))
+    return dq, dk, dv
 
 
 def row_encode_backward(pre: Tensor, table: Tensor, edge_window: Tensor, edge_class: Tensor, edge_cell: Tensor,
@@ -1631,12 +1640,12 @@ def stone_attention(q: Tensor, k: Tensor, v: Tensor, seq_lens: Tensor, want_lse:
         raise ValueError("seq_lens must be int32 with shape (P,)")
     if q.dtype not in (torch.float16, torch.bfloat16) or k.dtype != q.dtype or v.dtype != q.dtype:
         raise ValueError("stone attention runs 16-bit MFMA: q, k and v must share float16 or bfloat16")
-    if hd != 32:
-        raise ValueError("stone attention supports head_dim 32")
+    if hd not in (16, 32, 64):
+        raise ValueError("stone attention supports head_dim 16, 32 and 64")
     # unit dim stride, 16-byte aligned rows, and a row pitch the kernel's
-    # buffer descriptors take (32 to 8,191 elements)
+    # buffer descriptors take (hd to 8,191 elements)
     fix = lambda x: (x if x.stride(3) == 1 and all(s % 8 == 0 for s in x.stride()[:3])  # noqa: E731
-                     and 32 <= x.stride(2) < 8192 else x.contiguous())
+                     and hd <= x.stride(2) < 8192 else x.contiguous())
     q, k, v = fix(q), fix(k), fix(v)
     seq_lens = seq_lens.contiguous()
     if out is None:

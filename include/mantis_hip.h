@@ -728,7 +728,7 @@ int32_t mantis_row_encode(const void* pre, int32_t pre_dtype, int64_t n_w, int64
  * the model passes need no copy; every stride is a multiple of 8, and the row
  * strides of q, k and v lie in [hd, 8191] (MANTIS_E_ARG otherwise).  lse
  * (P, heads, T) fp32 or NULL.
- * hd must be 32.  `schedule` is NULL (work items in their natural order) or
+ * hd is 16, 32 or 64 (the reference kernel's head dims).  `schedule` is NULL (work items in their natural order) or
  * the order built by mantis_stone_attention_schedule for the same seq_lens,
  * n_pos, heads and t; the output does not depend on which.  Replaces
  * mantisnet::fused_attention (python/mantisnet/mantisnet/attention.py:44-162,
@@ -740,6 +740,30 @@ int32_t mantis_stone_attention(const void* q, const int64_t* q_strides, const vo
                                int32_t heads, int64_t t, int32_t hd, void* out,
                                const int64_t* out_strides, float* lse, const int32_t* schedule,
                                void* stream);
+
+/*
+ * Backward of mantis_stone_attention for the same q, k, v, seq_lens, hd and
+ * dtype, given its output `out`, its lse (P, heads, T) fp32 and grad_out
+ * (same dtype and shape as q; each tensor with its own element strides
+ * (sp, sa, st, sd == 1), every stride a multiple of 8, rows 16-byte aligned).
+ * With a = exp(q_i . k_j / sqrt(hd) - lse_i) over live rows and keys,
+ * delta_i = out_i . grad_out_i and ds = a (grad_out_i . v_j - delta_i):
+ *   dq_i = sum_j ds k_j / sqrt(hd),  dk_j = sum_i ds q_i / sqrt(hd),
+ *   dv_j = sum_i a grad_out_i,
+ * fp32 sums in a fixed order (two calls agree bitwise), written in `dtype`;
+ * rows and keys at or past seq_lens[p] get zero gradients.  delta is a
+ * (P, heads, T) fp32 workspace (written).  Replaces
+ * mantisnet::fused_attention_backward (python/mantisnet/mantisnet/
+ * attention.py:166-560, 826-904).
+ */
+int32_t mantis_stone_attention_backward(const void* q, const int64_t* q_strides, const void* k,
+                                        const int64_t* k_strides, const void* v, const int64_t* v_strides,
+                                        const void* out, const int64_t* out_strides, const void* grad_out,
+                                        const int64_t* grad_out_strides, const float* lse, int32_t dtype,
+                                        const int32_t* seq_lens, int64_t n_pos, int32_t heads, int64_t t,
+                                        int32_t hd, float* delta, void* dq, const int64_t* dq_strides, void* dk,
+                                        const int64_t* dk_strides, void* dv, const int64_t* dv_strides,
+                                        void* stream);
 
 /*
  * Work order for mantis_stone_attention over these seq_lens: its items

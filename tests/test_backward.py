@@ -127,22 +127,29 @@ def test_action_row_encode_backward(device, batch):
     mantisnet.ops.raise_on_device_error(device)
 
 
-@pytest.mark.parametrize("heads", [4, 8])
-def test_fused_attention_backward(device, heads):
-    gen = torch.Generator().manual_seed(24)
-    p, t = 5, 70
-    lens = torch.tensor([70, 4, 33, 64, 1], dtype=torch.int32)
-    q, k, v = (torch.randn(p, t, heads, 32, generator=gen).to(torch.float16).transpose(1, 2) for _ in range(3))
-    seed = torch.randn(p, heads, t, 32, generator=gen)
+@pytest.mark.parametrize("heads,hd,dt", [(4, 32, torch.float16), (8, 32, torch.float16), (4, 32, torch.bfloat16),
+                                         (3, 16, torch.float16), (4, 16, torch.bfloat16), (2, 64, torch.float16),
+                                         (4, 64, torch.bfloat16)])
+def test_fused_attention_backward(device, heads, hd, dt):
+    gen = torch.Generator().manual_seed(24 + hd)
+    p, t = 5, 140
+    lens = torch.tensor([140, 4, 65, 64, 0], dtype=torch.int32)
+    q, k, v = (torch.randn(p, t, heads, hd, generator=gen).to(dt).transpose(1, 2) for _ in range(3))
+    seed = torch.randn(p, heads, t, hd, generator=gen)
     valid = torch.arange(t)[None, :] < lens[:, None]
     seed = seed.masked_fill(~valid[:, None, :, None], 0.0)  # pad rows carry no gradient in either form
     ld = lens.to(device)
     got = _grads(lambda a, c, d: OPS.fused_attention(a, c, d, ld)[0], [x.to(device) for x in (q, k, v)],
-                 seed.to(device, torch.float16))
+                 seed.to(device, dt))
     mantisnet.ops.raise_on_device_error(device)
     exp = _grads(lambda a, c, d: R.stone_attention(a, c, d, lens), [x.float() for x in (q, k, v)],
-                 seed.to(torch.float16).float())
-    _close(got, exp, torch.float16)
+                 seed.to(dt).float())
+    _close(got, exp, dt)
+    assert all(g.dtype == dt for g in got)
     # pad keys and rows: zero gradients
     for g in got:
         assert torch.count_nonzero(g.cpu().float().masked_fill(valid[:, None, :, None], 0.0)) == 0
+    # two backward passes agree bitwise
+    again = _grads(lambda a, c, d: OPS.fused_attention(a, c, d, ld)[0], [x.to(device) for x in (q, k, v)],
+                   seed.to(device, dt))
+    assert all(torch.equal(a.cpu(), b.cpu()) for a, b in zip(got, again))

@@ -180,6 +180,35 @@ def test_stone_attention_matches_masked_sdpa(device, p, t, heads, dtype):
     torch.testing.assert_close(lse.cpu(), exp_lse, rtol=1e-3, atol=1e-3)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, BF])
+@pytest.mark.parametrize("hd", [16, 64])
+@pytest.mark.parametrize("p,t,heads", [(3, 31, 4), (5, 200, 8), (2, 513, 4)])
+def test_stone_attention_other_head_dims(device, hd, p, t, heads, dtype):
+    # the reference kernel's other head dims (attention.py:727-735): scores
+    # scaled by 1/sqrt(hd), in the model's (P, T, A, hd) storage; the third
+    # 64-key chunk's keys score far above the first (a late rescale)
+    gen = _g(hd * 100 + t)
+    q = torch.randn(p, t, heads, hd, generator=gen).to(dtype).transpose(1, 2)
+    k = torch.randn(p, t, heads, hd, generator=gen)
+    if t > 192:
+        k[:, 128:192] *= 6.0
+    k = k.to(dtype).transpose(1, 2)
+    v = torch.randn(p, t, heads, hd, generator=gen).to(dtype).transpose(1, 2)
+    seq = torch.randint(1, t + 1, (p,), generator=gen, dtype=torch.int32)
+    seq[0] = t
+    seq[-1] = 0  # a position with no live rows
+    out, lse = ops.stone_attention(q.to(device), k.to(device), v.to(device), seq.to(device), want_lse=True)
+    exp = R.stone_attention(q.float(), k.float(), v.float(), seq)
+    tol = 4e-3 if dtype == torch.float16 else 2e-2
+    torch.testing.assert_close(out.float().cpu(), exp, rtol=tol, atol=tol)
+    valid = torch.arange(t)[None, :] < seq[:, None]
+    assert torch.all(out.float().cpu().transpose(1, 2)[~valid] == 0)
+    sc = torch.matmul(q.float(), k.float().transpose(-1, -2)) / math.sqrt(hd)
+    sc = sc.masked_fill(~valid[:, None, None, :], -torch.inf)
+    exp_lse = torch.logsumexp(sc, -1).masked_fill(~valid[:, None, :], 0.0)
+    torch.testing.assert_close(lse.cpu(), exp_lse, rtol=1e-3, atol=1e-3)
+
+
 def test_stone_attention_pad_keys_get_zero_weight(device):
     # garbage (huge) values past seq_len must not leak into live rows
     gen = _g(9)

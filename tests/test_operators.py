@@ -237,16 +237,22 @@ def test_action_row_encode_operator(device, batch):
 
 
 @pytest.mark.gpu
-def test_fused_attention_operator(device):
+@pytest.mark.parametrize("hd", [16, 32, 64])
+def test_fused_attention_operator(device, hd):
+    # the reference kernel's head dims (attention.py:727-735); others raise
     gen = torch.Generator().manual_seed(5)
     p, a, t = 5, 4, 70
     lens = torch.tensor([70, 4, 33, 64, 1], dtype=torch.int32)
-    q, k, v = (torch.randn(p, t, a, 32, generator=gen).to(torch.float16).transpose(1, 2) for _ in range(3))
+    q, k, v = (torch.randn(p, t, a, hd, generator=gen).to(torch.float16).transpose(1, 2) for _ in range(3))
     out, lse = OPS.fused_attention(*_d(device, q, k, v, lens))
     assert out.stride() == torch.empty_like(q).stride()
     exp = R.stone_attention(q, k, v, lens)
     torch.testing.assert_close(out.cpu().float(), exp, rtol=4e-3, atol=4e-3)
-    sc = torch.matmul(q.float(), k.float().transpose(-1, -2)) / math.sqrt(32)
+    if hd == 32:
+        bad = torch.zeros(p, a, t, 48, dtype=torch.float16, device=device)
+        with pytest.raises(ValueError):
+            OPS.fused_attention(bad, bad, bad, lens.to(device))
+    sc = torch.matmul(q.float(), k.float().transpose(-1, -2)) / math.sqrt(hd)
     valid = torch.arange(t)[None, :] < lens[:, None]
     e_lse = sc.masked_fill(~valid[:, None, None, :], -torch.inf).logsumexp(-1)
     live = valid[:, None, :].expand(p, a, t)
