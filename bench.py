@@ -225,6 +225,22 @@ def isolated_message_passing(torch, ops, dev, reps=20):
     s = tr.summary()["hex_aggregate_linear"]
     c = _cold(torch, ops, dev, "hex_aggregate_linear", lambda: ops.hex_aggregate_linear(x, nbr, w, bias), reps)
     ops.raise_on_device_error(dev)
+    # the practical ceiling at this size: a device copy moving the same bytes
+    # (half read, half written), warm, timed the same way
+    half = int(s["bytes_per_launch"] // 4)
+    src = torch.empty(half, dtype=torch.float16, device=dev).normal_()
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    copy_us = e0.elapsed_time(e1) * 1000.0 / reps
+    del src, dst
     return {
         "config": f"256 graphs, N={n} cells, 6 axial neighbours, sum+mean then Linear(128,128), bf16; warm "
                   f"(inputs in L2/MALL) and cold ({COLD_FLUSH_MIB} MiB written before each launch)",
@@ -234,6 +250,8 @@ def isolated_message_passing(torch, ops, dev, reps=20):
         "mb_per_launch": round(s["bytes_per_launch"] / 1e6, 2),
         "cold_avg_us": round(c["avg_us"], 2),
         "cold_hbm_frac": round(c["gbps"] / HBM_PEAK_GBPS, 4),
+        "copy_same_bytes_us": round(copy_us, 2),
+        "copy_same_bytes_hbm_frac": round(s["bytes_per_launch"] / (copy_us * 1e3) / HBM_PEAK_GBPS, 4),
     }
 
 

@@ -95,7 +95,7 @@ __device__ __forceinline__ void store16_nt(uint16_t* p, uint4 v) {
   __builtin_nontemporal_store(u32x4_t{v.x, v.y, v.z, v.w}, reinterpret_cast<u32x4_t*>(p));
 }
 
-__global__ void __launch_bounds__(kThreads)
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3)))
 hex_aggregate_linear_kernel(const uint16_t* __restrict__ x, const int32_t* __restrict__ nbr,
                             int64_t n_cells, const uint16_t* __restrict__ w,
                             const float* __restrict__ bias, uint16_t* __restrict__ out_sum,
@@ -127,56 +127,59 @@ hex_aggregate_linear_kernel(const uint16_t* __restrict__ x, const int32_t* __res
   }
   // ---- gather in row layout: pass p covers cells c0 + 4p + lane/16
   const int sub = lane / 16, d8 = (lane % 16) * 8;
-  {
-    int32_t js[4][6];
+  int32_t js[4][6];
 #pragma unroll
-    for (int p = 0; p < 4; ++p)
+  for (int p = 0; p < 4; ++p)
 #pragma unroll
-      for (int s = 0; s < 6; ++s) {
-        const int k = 6 * (4 * p + sub) + s;  // index slot within the tile, 0..95
-        const int32_t a = __shfl(v0, k & 63), b = __shfl(v1, k & 31);
-        js[p][s] = k < 64 ? a : b;
-      }
-    uint4 raw[4][6];
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const int64_t cell = c0 + 4 * p + sub;
-      const int64_t self = cell < n_cells ? cell : 0;
-#pragma unroll
-      for (int s = 0; s < 6; ++s) {
-        const bool ok = js[p][s] >= 0 && js[p][s] < n_cells;
-        raw[p][s] = *reinterpret_cast<const uint4*>(x + (ok ? int64_t(js[p][s]) : self) * kDim + d8);
-      }
+    for (int s = 0; s < 6; ++s) {
+      const int k = 6 * (4 * p + sub) + s;  // index slot within the tile, 0..95
+      const int32_t a = __shfl(v0, k & 63), b = __shfl(v1, k & 31);
+      js[p][s] = k < 64 ? a : b;
     }
+  uint4 raw[4][6];
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-      int present = 0;
+  for (int p = 0; p < 4; ++p) {
+    const int64_t cell = c0 + 4 * p + sub;
+    const int64_t self = cell < n_cells ? cell : 0;
 #pragma unroll
-      for (int s = 0; s < 6; ++s) {
-        const int32_t j = js[p][s];
-        const bool ok = j >= 0 && j < n_cells;
-        if (j >= n_cells && (lane % 16) == 0) raise_flag(flag, MANTIS_FLAG_INDEX);
-        present += ok ? 1 : 0;
-        const float mk = ok ? 1.f : 0.f;
-        const uint32_t w4[4] = {raw[p][s].x, raw[p][s].y, raw[p][s].z, raw[p][s].w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          acc[2 * i] = fmaf(__uint_as_float(w4[i] << 16), mk, acc[2 * i]);
-          acc[2 * i + 1] = fmaf(__uint_as_float(w4[i] & 0xffff0000u), mk, acc[2 * i + 1]);
-        }
-      }
-      uint4 packed;
-      packed.x = pack_bf16x2(acc[0], acc[1]);
-      packed.y = pack_bf16x2(acc[2], acc[3]);
-      packed.z = pack_bf16x2(acc[4], acc[5]);
-      packed.w = pack_bf16x2(acc[6], acc[7]);
-      *reinterpret_cast<uint4*>(&sagg[wave][(4 * p + sub) * kPitch + d8]) = packed;
-      if (lane % 16 == 0) scount[wave][4 * p + sub] = float(present);
+    for (int s = 0; s < 6; ++s) {
+      const bool ok = js[p][s] >= 0 && js[p][s] < n_cells;
+      raw[p][s] = *reinterpret_cast<const uint4*>(x + (ok ? int64_t(js[p][s]) : self) * kDim + d8);
     }
   }
-  __syncthreads();
-  if (c0 >= n_cells) return;
+  __syncthreads();  // W staged; the rows are in flight
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int present = 0;
+#pragma unroll
+    for (int s = 0; s < 6; ++s) {
+      const int32_t j = js[p][s];
+      const bool ok = j >= 0 && j < n_cells;
+      if (j >= n_cells && (lane % 16) == 0) raise_flag(flag, MANTIS_FLAG_INDEX);
+      present += ok ? 1 : 0;
+      const float mk = ok ? 1.f : 0.f;
+      const uint32_t w4[4] = {raw[p][s].x, raw[p][s].y, raw[p][s].z, raw[p][s].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[2 * i] = fmaf(__uint_as_float(w4[i] << 16), mk, acc[2 * i]);
+        acc[2 * i + 1] = fmaf(__uint_as_float(w4[i] & 0xffff0000u), mk, acc[2 * i + 1]);
+      }
+    }
+    uint4 packed;
+    packed.x = pack_bf16x2(acc[0], acc[1]);
+    packed.y = pack_bf16x2(acc[2], acc[3]);
+    packed.z = pack_bf16x2(acc[4], acc[5]);
+    packed.w = pack_bf16x2(acc[6], acc[7]);
+    *reinterpret_cast<uint4*>(&sagg[wave][(4 * p + sub) * kPitch + d8]) = packed;
+    if (lane % 16 == 0) scount[wave][4 * p + sub] = float(present);
+  }
+  // the sums and counts were written by this wavefront's own lanes: a
+  // wavefront barrier between fences orders them before the fragment reads
+  // (a tile past the last cell computes zeros and stores nothing)
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
   // ---- product in MFMA layout: lane = cell l16, K group g
   const int l16 = lane % 16, g = lane / 16;
   const float cnt = scount[wave][l16];
