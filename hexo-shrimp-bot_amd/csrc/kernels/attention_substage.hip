@@ -152,14 +152,20 @@ __global__ void __launch_bounds__(waves_for<kStages>() * 64) attn_substage_kerne
       sb[s][0][i] = a.st[s].bq[i];
       sb[s][1][i] = a.st[s].bo[i];
     }
-    for (int i = threadIdx.x; i < 4 * a.st[s].n_classes; i += kThreads) sbias[a.bias_off[s] + i] = a.st[s].bias[i];
-    for (int i = threadIdx.x; i < kK * (kK / 8); i += kThreads) {
-      const int r = i / (kK / 8), c = (i % (kK / 8)) * 8;
-      *reinterpret_cast<uint4*>(&sw[s][0][r * kPitch + c]) =
-          *reinterpret_cast<const uint4*>(a.st[s].wq + qrow(r) * kK + c);
-      *reinterpret_cast<uint4*>(&sw[s][1][r * kPitch + c]) =
-          *reinterpret_cast<const uint4*>(a.st[s].wo + orow(r) * kK + c);
-    }
+    staged_copy_f32<kThreads, 8>(4 * int(a.st[s].n_classes), a.st[s].bias, sbias + a.bias_off[s]);
+    // Wq then Wo, each 128 rows of 16 chunks, permuted as staged
+    constexpr int kChunks = kK * (kK / 8);
+    staged_copy<kThreads, (2 * kChunks + kThreads - 1) / kThreads>(
+        2 * kChunks,
+        [&](int i) {
+          const int m = i / kChunks, j = i % kChunks, r = j / (kK / 8), c = (j % (kK / 8)) * 8;
+          const _Float16* src = m == 0 ? a.st[s].wq + qrow(r) * kK + c : a.st[s].wo + orow(r) * kK + c;
+          return *reinterpret_cast<const chunk16_t*>(src);
+        },
+        [&](int i, chunk16_t v) {
+          const int m = i / kChunks, j = i % kChunks, r = j / (kK / 8), c = (j % (kK / 8)) * 8;
+          *reinterpret_cast<chunk16_t*>(&sw[s][m][r * kPitch + c]) = v;
+        });
   }
   __syncthreads();
 

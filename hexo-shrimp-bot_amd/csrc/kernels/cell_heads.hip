@@ -128,14 +128,33 @@ __global__ void __launch_bounds__(kThreads) cell_heads_kernel(HeadArgs a) {
   for (int i = threadIdx.x; i < 3 * kK; i += kThreads) sempty[i] = a.empty_rows[i];
   for (int i = threadIdx.x; i < kN1; i += kThreads) sb1[i] = a.b1[i];
   for (int i = threadIdx.x; i < kN3; i += kThreads) sb3[i] = a.b3[i];
-  for (int i = threadIdx.x; i < kN1 * (kK / 8); i += kThreads) {
-    const int r = i / (kK / 8), cc = (i % (kK / 8)) * 8;
-    *reinterpret_cast<uint4*>(sw1 + r * kPitch + cc) = *reinterpret_cast<const uint4*>(a.w1 + r * kK + cc);
-    *reinterpret_cast<uint4*>(sw2 + r * kPitch + cc) = *reinterpret_cast<const uint4*>(a.w2 + r * kK + cc);
-  }
-  for (int i = threadIdx.x; i < kW3Rows * (kN1 / 8); i += kThreads) {
-    const int r = i / (kN1 / 8), cc = (i % (kN1 / 8)) * 8;
-    *reinterpret_cast<uint4*>(sw3 + r * kP3 + cc) = *reinterpret_cast<const uint4*>(a.w3 + r * kN1 + cc);
+  {
+    // W1, W2 (kN1 rows of 16 chunks each), then W3 (kW3Rows rows of kN1 / 8)
+    constexpr int k12 = kN1 * (kK / 8), k3 = kW3Rows * (kN1 / 8);
+    staged_copy<kThreads, 8>(
+        2 * k12 + k3,
+        [&](int i) {
+          const _Float16* src;
+          if (i < 2 * k12) {
+            const int j = i % k12, r = j / (kK / 8), cc = (j % (kK / 8)) * 8;
+            src = (i < k12 ? a.w1 : a.w2) + r * kK + cc;
+          } else {
+            const int j = i - 2 * k12, r = j / (kN1 / 8), cc = (j % (kN1 / 8)) * 8;
+            src = a.w3 + r * kN1 + cc;
+          }
+          return *reinterpret_cast<const chunk16_t*>(src);
+        },
+        [&](int i, chunk16_t v) {
+          _Float16* dst;
+          if (i < 2 * k12) {
+            const int j = i % k12, r = j / (kK / 8), cc = (j % (kK / 8)) * 8;
+            dst = (i < k12 ? sw1 : sw2) + r * kPitch + cc;
+          } else {
+            const int j = i - 2 * k12, r = j / (kN1 / 8), cc = (j % (kN1 / 8)) * 8;
+            dst = sw3 + r * kP3 + cc;
+          }
+          *reinterpret_cast<chunk16_t*>(dst) = v;
+        });
   }
   __syncthreads();
 

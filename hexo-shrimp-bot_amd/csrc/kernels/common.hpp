@@ -215,6 +215,46 @@ __device__ __forceinline__ void segment(const int64_t* ptr, int64_t row, int64_t
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
+// Staging copies for kT threads (a workgroup's set-up): chunk i of n, as
+// src(i) -> 16 bytes and store(i, chunk), with up to kMax chunks of a thread
+// requested before any is stored.  One chunk at a time would chain the
+// thread's round trips to L2, which for a launch over few rows is most of
+// its time.  The batch is held in native vectors, which stay in registers.
+typedef uint32_t chunk16_t __attribute__((ext_vector_type(4)));
+template <int kT, int kMax, typename Src, typename Store>
+__device__ __forceinline__ void staged_copy(int n, Src src, Store store) {
+  for (int base = 0; base < n; base += kT * kMax) {
+    chunk16_t v[kMax];
+#pragma unroll
+    for (int u = 0; u < kMax; ++u) {
+      const int i = base + int(threadIdx.x) + u * kT;
+      v[u] = src(i < n ? i : 0);
+    }
+#pragma unroll
+    for (int u = 0; u < kMax; ++u) {
+      const int i = base + int(threadIdx.x) + u * kT;
+      if (i < n) store(i, v[u]);
+    }
+  }
+}
+// the same for n 4-byte values, src -> dst
+template <int kT, int kMax>
+__device__ __forceinline__ void staged_copy_f32(int n, const float* __restrict__ src, float* dst) {
+  for (int base = 0; base < n; base += kT * kMax) {
+    float v[kMax];
+#pragma unroll
+    for (int u = 0; u < kMax; ++u) {
+      const int i = base + int(threadIdx.x) + u * kT;
+      v[u] = src[i < n ? i : 0];
+    }
+#pragma unroll
+    for (int u = 0; u < kMax; ++u) {
+      const int i = base + int(threadIdx.x) + u * kT;
+      if (i < n) dst[i] = v[u];
+    }
+  }
+}
+
 inline int32_t launched() { return hipGetLastError() == hipSuccess ? MANTIS_OK : MANTIS_E_LAUNCH; }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }

@@ -80,16 +80,25 @@ __global__ void __launch_bounds__(waves_for<kQ>() * 64) latent_broadcast_residua
   __shared__ __attribute__((aligned(16))) float sbq[kQ ? kK : 4];
   // per wavefront: the tile's position's four latent k | v rows (4 x 256 fp16)
   __shared__ __attribute__((aligned(16))) _Float16 slat[kWaves][4 * 2 * kK];
-  for (int i = threadIdx.x; i < kK * (kK / 8); i += kThreads) {
-    const int r = i / (kK / 8), c = (i % (kK / 8)) * 8;
-    *reinterpret_cast<uint4*>(sw + r * kPitch + c) = *reinterpret_cast<const uint4*>(a.wo + r * kK + c);
-    if constexpr (kQ) {
-      // K slots c .. c + 7 = 32 ks + 8 g .. : features 32 ks + 4 g .. +3 and 32 ks + 16 + 4 g .. +3
-      const int ks = c / 32, gg = (c % 32) / 8;
-      const _Float16* src = a.wq + qrow(r) * kK + 32 * ks + 4 * gg;
-      const uint2 lo = *reinterpret_cast<const uint2*>(src), hi = *reinterpret_cast<const uint2*>(src + 16);
-      *reinterpret_cast<uint4*>(swq + r * kPitch + c) = make_uint4(lo.x, lo.y, hi.x, hi.y);
-    }
+  {
+    // Wo, then (kQ) Wq: K slots c .. c + 7 = 32 ks + 8 g .. of its row are
+    // features 32 ks + 4 g .. +3 and 32 ks + 16 + 4 g .. +3
+    constexpr int kChunks = kK * (kK / 8);
+    constexpr int kN = (kQ ? 2 : 1) * kChunks;
+    staged_copy<kThreads, (kN + kThreads - 1) / kThreads>(
+        kN,
+        [&](int i) {
+          const int j = i % kChunks, r = j / (kK / 8), c = (j % (kK / 8)) * 8;
+          if (i < kChunks) return *reinterpret_cast<const chunk16_t*>(a.wo + r * kK + c);
+          const int ks = c / 32, gg = (c % 32) / 8;
+          const _Float16* src = a.wq + qrow(r) * kK + 32 * ks + 4 * gg;
+          const uint2 lo = *reinterpret_cast<const uint2*>(src), hi = *reinterpret_cast<const uint2*>(src + 16);
+          return chunk16_t{lo.x, lo.y, hi.x, hi.y};
+        },
+        [&](int i, chunk16_t v) {
+          const int j = i % kChunks, r = j / (kK / 8), c = (j % (kK / 8)) * 8;
+          *reinterpret_cast<chunk16_t*>((i < kChunks ? sw : swq) + r * kPitch + c) = v;
+        });
   }
   for (int i = threadIdx.x; i < kK; i += kThreads) {
     sb[i] = a.bo[i];
