@@ -109,8 +109,15 @@ def _dt(t: Tensor) -> int:
     raise ValueError(f"unsupported dtype {t.dtype}; expected float16, bfloat16 or float32")
 
 
+# the current device's current stream as a raw handle, from torch's C
+# accessors (torch.cuda.current_stream() builds a Stream object per call,
+# several microseconds of host time on every launch)
+_raw_stream = torch._C._cuda_getCurrentRawStream
+_cur_device = torch._C._cuda_getDevice
+
+
 def _stream() -> int:
-    return torch.cuda.current_stream().cuda_stream
+    return _raw_stream(_cur_device())
 
 
 def _ptr(t: Tensor | None) -> int | None:
@@ -118,7 +125,8 @@ def _ptr(t: Tensor | None) -> int | None:
 
 
 def _on_gpu(*ts: Tensor) -> torch.device:
-    dev = None
+    first = None
+    idx = -1
     for t in ts:
         if t is None:
             continue
@@ -127,11 +135,11 @@ def _on_gpu(*ts: Tensor) -> torch.device:
                 "the MantisNet kernels run on the MI355X only (got a CPU tensor); "
                 "there is no CPU path"
             )
-        if dev is None:
-            dev = t.device
-        elif t.device != dev:
+        if first is None:
+            first, idx = t, t.get_device()
+        elif t.get_device() != idx:
             raise ValueError("all inputs must be on one device")
-    return dev
+    return None if first is None else first.device
 
 
 _TILE_COUNTERS = 512  # uint32 per set (MANTIS_TILE_COUNTERS)
@@ -144,7 +152,7 @@ def tile_counters(device: torch.device) -> Tensor:
     stream).  Launches on one stream run in order, so no two of them use a set
     at the same time, and every launch leaves its set at zero."""
     idx = device.index if device.index is not None else torch.cuda.current_device()
-    key = (idx, torch.cuda.current_stream(torch.device("cuda", idx)).cuda_stream)
+    key = (idx, _raw_stream(idx))
     c = _counters.get(key)
     if c is None:
         c = torch.zeros(_TILE_COUNTERS, dtype=torch.int32, device=torch.device("cuda", idx))
@@ -163,8 +171,16 @@ def _flag_words(device: torch.device) -> Tensor:
     return f
 
 
+_flag_views: dict[int, Tensor] = {}
+
+
 def error_flag(device: torch.device) -> Tensor:
-    return _flag_words(device)[:1]
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    v = _flag_views.get(idx)
+    if v is None:
+        v = _flag_words(device)[:1]
+        _flag_views[idx] = v
+    return v
 
 
 def flag_and_word(device: torch.device) -> tuple[Tensor, Tensor]:
