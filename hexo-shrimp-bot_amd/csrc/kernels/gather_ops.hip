@@ -71,13 +71,35 @@ segment_order_kernel(const int64_t* __restrict__ seg_ptr, int64_t n_seg, const i
     };
     for (int64_t r = lo + threadIdx.x; r < hi; r += blockDim.x) atomicAdd(&count[key_of(r)], 1);
     __syncthreads();
-    // exclusive prefix sum of the counts (one thread: 2048 adds)
-    if (threadIdx.x == 0) {
-      int32_t run = 0;
-      for (int k = 0; k < kOrderBuckets; ++k) {
-        const int32_t c = count[k];
-        count[k] = run;
-        run += c;
+    // exclusive prefix sum of the counts: thread t owns buckets 8t .. 8t+7
+    // (a scan of one thread over the 2048 buckets was a chain of dependent
+    // LDS round trips, most of the kernel's time)
+    {
+      static_assert(kOrderBuckets == 8 * 256, "eight buckets per thread of 256");
+      const int t = threadIdx.x, lane = t % 64, w = t / 64;
+      int32_t c[8], own = 0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        c[j] = count[8 * t + j];
+        own += c[j];
+      }
+      // inclusive scan of the threads' totals within the wavefront, then the
+      // wavefronts' totals
+      int32_t inc = own;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int32_t v = __shfl_up(inc, o);
+        if (lane >= o) inc += v;
+      }
+      __shared__ int32_t wave_total[4];
+      if (lane == 63) wave_total[w] = inc;
+      __syncthreads();
+      int32_t run = inc - own;
+      for (int k = 0; k < w; ++k) run += wave_total[k];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        count[8 * t + j] = run;
+        run += c[j];
       }
     }
     __syncthreads();

@@ -47,7 +47,10 @@ latent_mix_kernel(float* __restrict__ g, int64_t ldg, int64_t n_pos, const float
     // q | k | v: column c of the four rows
     for (int c = t; c < 3 * kH; c += kThreads) {
       float acc[kSlots] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 8
+      // unrolled by 32: a weight column is read in four batches of 32 loads
+      // in flight (by 8 it was a chain of 16 dependent L2 round trips, the
+      // whole of the kernel's time)
+#pragma unroll 32
       for (int k = 0; k < kH; ++k) {
         const float w = wqkv_t[k * 3 * kH + c];
 #pragma unroll
@@ -86,7 +89,7 @@ latent_mix_kernel(float* __restrict__ g, int64_t ldg, int64_t n_pos, const float
     {
       const int c = t % kH, r0 = t / kH;
       float a0 = 0.f, a1 = 0.f;
-#pragma unroll 8
+#pragma unroll 32
       for (int k = 0; k < kH; ++k) {
         const float w = wo_t[k * kH + c];
         a0 = fmaf(mixed[r0][k], w, a0);
