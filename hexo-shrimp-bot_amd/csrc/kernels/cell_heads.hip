@@ -4,7 +4,7 @@
 //   acts = sum_e relu(pre[win_e] + act_table[acls_e]) + sum_k empty[r,k] * empty_rows[k]
 //   ext  = sum_e head_tab[dcls_e]                     (entries e of the cell's decoder run)
 //   h    = relu( W1 x + W2 fp16(acts) + b1 + ext + g_half[p] )     (256 wide)
-//   out  = W3 fp16(h) + b3                            (16 wide: policy, 3 critic logits, pad)
+//   out  = (W3 fp16(h) + b3)[0:4]                     (W3 16 rows: policy, 3 critic logits, pad)
 // in one pass over the cells (replaces the reference's _action_contribution,
 // encode_rows and _cell_scores, model.py:1031-1091 with row_encoder.py:40-112,
 // the class_row_sum of e_pw/e_qw, and the two head MLPs' first layer).  The
@@ -46,7 +46,8 @@ __device__ __forceinline__ int32_t from_quad(int32_t v) {
 
 constexpr int kK = 128;
 constexpr int kN1 = 256;
-constexpr int kN3 = 16;
+constexpr int kN3 = 16;   // the second layer's MFMA tile: W3 has 16 rows
+constexpr int kOut = 4;   // of which the first four are stored
 constexpr int kPitch = kK + 8;
 constexpr int kP3 = kN1 + 8;
 constexpr int kWaves = 8;
@@ -100,7 +101,7 @@ struct HeadArgs {
   const int64_t* act_class;
   const int64_t* dec_class;
   int64_t n_entries;
-  float* out;                // (n_cells, 16)
+  float* out;                // (n_cells, 4)
   const int32_t* order;      // tile slot -> cell, or null
   int32_t* flag;
   uint32_t* counters;        // per XCD (128 bytes apart): next tile, then wavefronts done
@@ -455,10 +456,11 @@ __global__ void __launch_bounds__(kThreads) cell_heads_kernel(HeadArgs a) {
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-    if (live) {
-      const float4 bb = *reinterpret_cast<const float4*>(sb3 + 4 * g);
-      *reinterpret_cast<float4*>(a.out + row * kN3 + 4 * g) =
-          make_float4(y[0] + bb.x, y[1] + bb.y, y[2] + bb.z, y[3] + bb.w);
+    // the heads' four outputs (policy, three critic logits) are the lanes
+    // of group 0; the other twelve rows of the output tile are padding
+    if (live && g == 0) {
+      const float4 bb = *reinterpret_cast<const float4*>(sb3);
+      *reinterpret_cast<float4*>(a.out + row * kOut) = make_float4(y[0] + bb.x, y[1] + bb.y, y[2] + bb.z, y[3] + bb.w);
     }
   }
   if (bad) raise_flag(a.flag, MANTIS_FLAG_INDEX);

@@ -1238,7 +1238,8 @@ def cell_heads(c: Tensor, w1: Tensor, b1: Tensor, w2: Tensor, w3: Tensor, b3: Te
                cell_pos: Tensor, dec_ptr: Tensor, dec_window: Tensor, act_class: Tensor, dec_class: Tensor,
                layer_norm: bool, row_order: Tensor | None = None, compensated: bool = False,
                library_counters: bool = False, tables_ready: bool = False, acts_add: Tensor | None = None) -> Tensor:
-    """(n_cells, 16) fp32 head rows of every cell in one launch (see
+    """(n_cells, 4) fp32 head rows (policy, three critic logits) of every
+    cell in one launch (see
     mantis_cell_heads in include/mantis_hip.h): column 0 the policy logit,
     1..3 the critic logits.  ``row_order`` (int32 permutation of the cells)
     sets their grouping into tiles; the results do not depend on it.
@@ -1291,12 +1292,12 @@ def cell_heads(c: Tensor, w1: Tensor, b1: Tensor, w2: Tensor, w3: Tensor, b3: Te
         if acts_add.shape != (n, 128) or acts_add.dtype != torch.float32:
             raise ValueError("acts_add must be fp32 (n_cells, 128) rows")
         acts_add = acts_add.contiguous()
-    out = torch.empty((n, 16), dtype=torch.float32, device=dev)
+    out = torch.empty((n, 4), dtype=torch.float32, device=dev)
     if n:
         e = dec_window.numel()
         # the cell rows once, the output rows once, per entry its three
         # indices, each action-projection row once
-        nbytes = n * (128 * c.element_size() + 64 + 16 + 24 + (512 if acts_add is not None else 0)) + e * 24 + \
+        nbytes = n * (128 * c.element_size() + 16 + 16 + 24 + (512 if acts_add is not None else 0)) + e * 24 + \
             pre.shape[0] * 256
         flops = n * 2 * (2 * 256 * 128 + 16 * 256)
         _launch("cell_heads", nbytes, flops, lambda: _check(

@@ -549,7 +549,9 @@ int32_t mantis_radius_stage(void* x, int64_t ldx, int64_t n_rows, const int32_t*
  * pre (n_w, 128) and act_table (n_acls, 128) fp16; head_tab (n_dcls, 256)
  * fp16 with quad-chunked columns (column 32*k + 8*q + u holds feature
  * 16*(2*k + u/4) + 4*q + u%4); empty_rows (3, 128), g_half (n_pos, 256) fp32;
- * act_empty (n_cells, 3) and the index arrays int64; out (n_cells, 16) fp32;
+ * act_empty (n_cells, 3) and the index arrays int64; out (n_cells, 4) fp32
+ * (the first four rows of w3's 16-row tile: policy and the three critic
+ * logits);
  * acts_add (n_cells, 128) fp32 or NULL: a per-cell row joining the fp32
  * action sums last (the tactical scalars' MLP output of the action_tactical
  * configuration, model.py:1058-1062).  row_order, when not NULL, is a permutation of the cells (int32) in which

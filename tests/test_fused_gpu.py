@@ -634,8 +634,11 @@ def test_cell_heads_match_the_unfused_composition(device, mode, n):
     ext = ops.run_reduce(d(h16), d(dcl), d(ptr), n, torch.float32)
     # (fp32 rows enter the products as fp16, exactly as fp16 rows do)
     xin = ops.layer_norm(d(x.float()), d(torch.ones(128)), d(torch.zeros(128)), H16) if ln else d(c.to(H16))
+    # (the kernel stores the first four of the 16-row output tile: policy and
+    # the three critic logits)
     ref = ops.fused_linear(xin, d(w1), d(b1), x2=acts, w2=d(w2), add1=ext, add2=d(g_half), add2_rows=d(cell_pos),
-                           relu=True, w3=d(w3), b3=d(b3), out_dtype=torch.float32)
+                           relu=True, w3=d(w3), b3=d(b3), out_dtype=torch.float32)[:, :4]
+    assert got.shape == (n, 4)
     # the action-row sums (|acts| up to ~10) are rounded to fp16 for the
     # second product; summed in another order than row_encode's, a rare sum
     # lands one fp16 unit (up to 8e-3) apart, a few 1e-4 in the outputs (up to
@@ -706,7 +709,7 @@ def test_compensated_cell_heads_match_fp32(device):
     acts += (act_empty.double().unsqueeze(-1) * empty_rows.double().unsqueeze(0)).sum(1)
     ext = torch.zeros(n, 256, dtype=torch.float64).index_add_(0, dest, h16[dcl])
     h = (c.double() @ w1.double().t() + acts @ w2.double().t() + b1.double() + ext + g_half.double()[cell_pos]).relu()
-    ref = (h @ w3.double().t() + b3.double()).float()
+    ref = (h @ w3.double().t() + b3.double()).float()[:, :4]
     scale = float(ref.abs().max())
     err_c = float((got.cpu() - ref).abs().max())
     err_p = float((plain.cpu() - ref).abs().max())
