@@ -353,8 +353,7 @@ __global__ void __launch_bounds__(waves_for<kStages>() * 64) attn_substage_kerne
           for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
             for (int t = 0; t < 8; ++t) sum += xv[ks][t];
-          sum += __shfl_xor(sum, 16);
-          sum += __shfl_xor(sum, 32);
+          sum = sum_xor32(sum_xor16(sum));
           const float mean = sum * (1.f / kK);
           float sq = 0.f;
 #pragma unroll
@@ -364,8 +363,7 @@ __global__ void __launch_bounds__(waves_for<kStages>() * 64) attn_substage_kerne
               const float d = xv[ks][t] - mean;
               sq += d * d;
             }
-          sq += __shfl_xor(sq, 16);
-          sq += __shfl_xor(sq, 32);
+          sq = sum_xor32(sum_xor16(sq));
           const float rstd = rsqrtf(sq * (1.f / kK) + 1e-5f);
           // normalised values are bounded by sqrt(127): no saturation needed
           f16x8_t xb[4];

@@ -251,8 +251,7 @@ __global__ void __launch_bounds__(kThreads) cell_heads_kernel(HeadArgs a) {
       for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
         for (int t = 0; t < 8; ++t) s += xv[ks][t];
-      s += __shfl_xor(s, 16);
-      s += __shfl_xor(s, 32);
+      s = sum_xor32(sum_xor16(s));
       const float mean = s * (1.f / kK);
       float q = 0.f;
 #pragma unroll
@@ -262,8 +261,7 @@ __global__ void __launch_bounds__(kThreads) cell_heads_kernel(HeadArgs a) {
           const float d = xv[ks][t] - mean;
           q += d * d;
         }
-      q += __shfl_xor(q, 16);
-      q += __shfl_xor(q, 32);
+      q = sum_xor32(sum_xor16(q));
       const float rstd = rsqrtf(q * (1.f / kK) + 1e-5f);
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks)

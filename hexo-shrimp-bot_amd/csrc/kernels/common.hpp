@@ -215,6 +215,29 @@ __device__ __forceinline__ void segment(const int64_t* ptr, int64_t row, int64_t
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
+// x + (x of lane ^ 16) and x + (x of lane ^ 32) by the VALU lane swaps of
+// gfx950 (v_permlane16_swap / v_permlane32_swap) instead of LDS-crossbar
+// permutes: each lane adds its own value and its partner's, in whichever
+// order, which is the same fp32 sum as x + __shfl_xor(x, 16 / 32).
+__device__ __forceinline__ float sum_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// the same swaps for the maximum over lanes l, l ^ 16 (and l ^ 32)
+__device__ __forceinline__ float max_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 // Staging copies for kT threads (a workgroup's set-up): chunk i of n, as
 // src(i) -> 16 bytes and store(i, chunk), with up to kMax chunks of a thread
 // requested before any is stored.  One chunk at a time would chain the

@@ -11,8 +11,8 @@
 //
 // Layout: a wavefront owns 16 rows; lane (l16, g) = (row, 8-dim group) holds
 // q[r][32 a + 8 g .. +8] for every head a, which is the B fragment layout of
-// v_mfma_f32_16x16x32_f16 for o^T.  A score is 8 products on the lane and a
-// sum over the four lanes of the row (two shuffles).  The 16 rows of a tile
+// v_mfma_f32_16x16x32_f16 for o^T.  A score is 8 products on the lane (four
+// v_dot2) and a sum over the four lanes of the row (two VALU lane swaps).  The 16 rows of a tile
 // nearly always belong to one position: its four latent k | v rows (2 KB)
 // are then staged once in the wavefront's LDS slot and every lane reads its
 // slices from there (159 -> 134 us per launch at the production batch: the
@@ -169,8 +169,7 @@ __global__ void __launch_bounds__(waves_for<kQ>() * 64) latent_broadcast_residua
       for (int nt = 0; nt < 8; ++nt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) sum += xval(nt, i);
-      sum += __shfl_xor(sum, 16);
-      sum += __shfl_xor(sum, 32);
+      sum = sum_xor32(sum_xor16(sum));
       const float mean = sum * (1.f / kK);
       float sq = 0.f;
 #pragma unroll
@@ -180,8 +179,7 @@ __global__ void __launch_bounds__(waves_for<kQ>() * 64) latent_broadcast_residua
           const float d = xval(nt, i) - mean;
           sq += d * d;
         }
-      sq += __shfl_xor(sq, 16);
-      sq += __shfl_xor(sq, 32);
+      sq = sum_xor32(sum_xor16(sq));
       const float rstd = rsqrtf(sq * (1.f / kK) + 1e-5f);
       f16x8_t xb[4];
 #pragma unroll
@@ -236,12 +234,13 @@ __global__ void __launch_bounds__(waves_for<kQ>() * 64) latent_broadcast_residua
         float s[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          float d = 0.f;
-#pragma unroll
-          for (int t = 0; t < 8; ++t) d = fmaf(float(qv[h][t]), float(kf[j][t]), d);
-          d += __shfl_xor(d, 16);
-          d += __shfl_xor(d, 32);
-          s[j] = d * scale;
+          // packed fp16 products with fp32 sums (v_dot2), two chains
+          const uint4 qw = __builtin_bit_cast(uint4, qv[h]), kw = __builtin_bit_cast(uint4, kf[j]);
+          float d0 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, qw.x), __builtin_bit_cast(f16x2_t, kw.x), 0.f, false);
+          float d1 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, qw.y), __builtin_bit_cast(f16x2_t, kw.y), 0.f, false);
+          d0 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, qw.z), __builtin_bit_cast(f16x2_t, kw.z), d0, false);
+          d1 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, qw.w), __builtin_bit_cast(f16x2_t, kw.w), d1, false);
+          s[j] = sum_xor32(sum_xor16(d0 + d1)) * scale;
         }
         const float m = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
         float e[4], den = 0.f;

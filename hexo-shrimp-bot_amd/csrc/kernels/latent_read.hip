@@ -114,8 +114,7 @@ latent_read_x_kernel(const _Float16* __restrict__ qp, int64_t ldq, const _Float1
       for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
         for (int t = 0; t < 8; ++t) sum += val(ks, t);
-      sum += __shfl_xor(sum, 16);
-      sum += __shfl_xor(sum, 32);
+      sum = sum_xor32(sum_xor16(sum));
       const float mean = sum * (1.f / kK);
       float sq = 0.f;
 #pragma unroll
@@ -125,8 +124,7 @@ latent_read_x_kernel(const _Float16* __restrict__ qp, int64_t ldq, const _Float1
           const float d = val(ks, t) - mean;
           sq += d * d;
         }
-      sq += __shfl_xor(sq, 16);
-      sq += __shfl_xor(sq, 32);
+      sq = sum_xor32(sum_xor16(sq));
       const float rstd = rsqrtf(sq * (1.f / kK) + 1e-5f);
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {  // normalised values are bounded by sqrt(127)
@@ -159,8 +157,7 @@ latent_read_x_kernel(const _Float16* __restrict__ qp, int64_t ldq, const _Float1
     float cm = sc[0];
 #pragma unroll
     for (int t = 1; t < 8; ++t) cm = fmaxf(cm, sc[t]);
-    cm = fmaxf(cm, __shfl_xor(cm, 16));
-    cm = fmaxf(cm, __shfl_xor(cm, 32));
+    cm = max_xor32(max_xor16(cm));
     if (cm > m + kTauRX) {  // a new reference point (always on the first chunk)
       const float alpha = __expf(m - cm);
       lsum *= alpha;
@@ -191,8 +188,7 @@ latent_read_x_kernel(const _Float16* __restrict__ qp, int64_t ldq, const _Float1
     __builtin_amdgcn_wave_barrier();
   }
   if (bad) raise_flag(flag, MANTIS_FLAG_INDEX);
-  lsum += __shfl_xor(lsum, 16);
-  lsum += __shfl_xor(lsum, 32);
+  lsum = sum_xor32(sum_xor16(lsum));
   if (g == 0) {
     s_m[wave][l16] = m;
     s_l[wave][l16] = lsum;

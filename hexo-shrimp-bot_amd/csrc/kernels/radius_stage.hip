@@ -523,8 +523,7 @@ __global__ void __launch_bounds__(kThreadsR) radius_stage_kernel(StageArgs a) {
           for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
             for (int tt = 0; tt < 8; ++tt) sum += xv[ks][tt];
-          sum += __shfl_xor(sum, 16);
-          sum += __shfl_xor(sum, 32);
+          sum = sum_xor32(sum_xor16(sum));
           const float mean = sum * (1.f / kK);
           float sq = 0.f;
 #pragma unroll
@@ -534,8 +533,7 @@ __global__ void __launch_bounds__(kThreadsR) radius_stage_kernel(StageArgs a) {
               const float d = xv[ks][tt] - mean;
               sq += d * d;
             }
-          sq += __shfl_xor(sq, 16);
-          sq += __shfl_xor(sq, 32);
+          sq = sum_xor32(sum_xor16(sq));
           const float rstd = rsqrtf(sq * (1.f / kK) + 1e-5f);
           f16x8_t xb[4];
 #pragma unroll
