@@ -133,10 +133,22 @@ struct SubArgs {
   // when set, rows whose first stage's run is empty are neither read nor
   // written (a later launch adds that stage's output bias to them)
   int32_t skip_empty;
+  // the row projection of the updated rows (kProj): pout[r] = fp16( LN(x[r])
+  // wp^T + bp ), x[r] as stored (fp16), the LayerNorm affine folded into wp/bp
+  const _Float16* wp;
+  const float* bp;
+  _Float16* pout;
+  int64_t ldp;
 };
 
-template <int kStages, bool kVcls, typename TX>
+// Features of lane group g in output tiles 2k and 2k+1 of the row projection
+// when its weight rows are staged in this order: 32 k + 8 g .. +7, one
+// 16-byte store per pair of tiles
+__device__ __forceinline__ int pair_feature(int nt, int g, int t) { return 32 * (nt >> 1) + 8 * g + 4 * (nt & 1) + t; }
+
+template <int kStages, bool kVcls, typename TX, bool kProj = false>
 __global__ void __launch_bounds__(waves_for<kStages>() * 64) attn_substage_kernel(SubArgs a) {
+  static_assert(!kProj || (kStages == 1 && sizeof(TX) == 2), "the row projection follows one stage over fp16 rows");
   constexpr int kWaves = waves_for<kStages>();
   constexpr int kThreads = kWaves * 64;
   TX* const xs = static_cast<TX*>(a.x);
@@ -146,6 +158,24 @@ __global__ void __launch_bounds__(waves_for<kStages>() * 64) attn_substage_kerne
   // would also wait for the look-ahead loads and the stores before it)
   __shared__ __attribute__((aligned(16))) float sb[kStages][2][kK];
   __shared__ float sbias[kBiasPool];
+  // the row projection's weights, rows in pair_feature order, and its bias
+  __shared__ __attribute__((aligned(16))) _Float16 swp[kProj ? kK * kPitch : 8];
+  __shared__ __attribute__((aligned(16))) float sbp[kProj ? kK : 4];
+  if constexpr (kProj) {
+    constexpr int kChunks = kK * (kK / 8);
+    staged_copy<kThreads, (kChunks + kThreads - 1) / kThreads>(
+        kChunks,
+        [&](int i) {
+          const int r = i / (kK / 8), c = (i % (kK / 8)) * 8;
+          const int src = pair_feature(r >> 4, (r & 15) >> 2, r & 3);
+          return *reinterpret_cast<const chunk16_t*>(a.wp + src * kK + c);
+        },
+        [&](int i, chunk16_t v) {
+          const int r = i / (kK / 8), c = (i % (kK / 8)) * 8;
+          *reinterpret_cast<chunk16_t*>(swp + r * kPitch + c) = v;
+        });
+    for (int i = threadIdx.x; i < kK; i += kThreads) sbp[i] = a.bp[i];
+  }
 #pragma unroll
   for (int s = 0; s < kStages; ++s) {
     for (int i = threadIdx.x; i < kK; i += kThreads) {
@@ -510,6 +540,65 @@ __global__ void __launch_bounds__(waves_for<kStages>() * 64) attn_substage_kerne
         }
       }
     }
+    if constexpr (kProj) {
+      // ---- the row projection of the rows as stored: LayerNorm (the same
+      // fp32 statistics and roundings as a projection launch over the stored
+      // rows), then LN(x) wp^T + bp, eight consecutive features per lane and
+      // pair of output tiles
+      float pv[4][8];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const f16x8_t h = __builtin_bit_cast(f16x8_t, xh[ks]);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) pv[ks][t] = float(h[t]);
+      }
+      float sum = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) sum += pv[ks][t];
+      sum = sum_xor32(sum_xor16(sum));
+      const float mean = sum * (1.f / kK);
+      float sq = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          const float d = pv[ks][t] - mean;
+          sq += d * d;
+        }
+      sq = sum_xor32(sum_xor16(sq));
+      const float rstd = rsqrtf(sq * (1.f / kK) + 1e-5f);
+      f16x8_t pb[4];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) pb[ks][t] = f2h((pv[ks][t] - mean) * rstd);
+#pragma unroll
+      for (int k2 = 0; k2 < 4; ++k2) {
+        f32x4_t d[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int nt = 2 * k2 + u;
+          d[u] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int ks = 0; ks < 4; ++ks) {
+            const f16x8_t wf = *reinterpret_cast<const f16x8_t*>(swp + (16 * nt + l16) * kPitch + 32 * ks + 8 * g);
+            d[u] = mfma16x16x32(wf, pb[ks], d[u]);
+          }
+          const float4 b = *reinterpret_cast<const float4*>(sbp + pair_feature(nt, g, 0));
+          d[u][0] += b.x, d[u][1] += b.y, d[u][2] += b.z, d[u][3] += b.w;
+        }
+        if (live) {
+          uint4 w;
+          w.x = pack_f16x2(d[0][0], d[0][1]);
+          w.y = pack_f16x2(d[0][2], d[0][3]);
+          w.z = pack_f16x2(d[1][0], d[1][1]);
+          w.w = pack_f16x2(d[1][2], d[1][3]);
+          *reinterpret_cast<uint4*>(a.pout + row * a.ldp + 32 * k2 + 8 * g) = w;
+        }
+      }
+    }
     if (live) {
       if constexpr (kPacked) {
 #pragma unroll
@@ -532,7 +621,7 @@ __global__ void __launch_bounds__(waves_for<kStages>() * 64) attn_substage_kerne
   }
 }
 
-template <int kStages, bool kVcls, typename TX>
+template <int kStages, bool kVcls, typename TX, bool kProj = false>
 int32_t launch(const SubArgs& a, void* stream) {
   int dev = 0, cus = 0;
   if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
@@ -544,7 +633,7 @@ int32_t launch(const SubArgs& a, void* stream) {
   constexpr int kWaves = waves_for<kStages>();
   const int64_t need = ((tiles + kWaves - 1) / kWaves + kXcds - 1) / kXcds * kXcds;
   if (need < grid) grid = need;
-  attn_substage_kernel<kStages, kVcls, TX><<<dim3(unsigned(grid)), dim3(kWaves * 64), 0, as_stream(stream)>>>(a);
+  attn_substage_kernel<kStages, kVcls, TX, kProj><<<dim3(unsigned(grid)), dim3(kWaves * 64), 0, as_stream(stream)>>>(a);
   return launched();
 }
 
@@ -585,9 +674,16 @@ struct InitRows {
   int64_t cover_row;
 };
 
+struct ProjRows {
+  const void* w;
+  const float* b;
+  void* out;
+  int64_t ld;
+};
+
 int32_t substages(void* x, int32_t x_dtype, int64_t ldx, int64_t n_rows, const int32_t* row_order,
                   const mantis_substage* stages, int32_t n_stages, const InitRows* init, int32_t* err_flag,
-                  uint32_t* tile_counters, void* stream, bool skip_empty = false) {
+                  uint32_t* tile_counters, void* stream, bool skip_empty = false, const ProjRows* proj = nullptr) {
   if (n_rows < 0 || !stages || n_stages < 1 || n_stages > 2) return MANTIS_E_ARG;
   if (n_rows == 0) return MANTIS_OK;
   for (int s = 0; s < n_stages; ++s)
@@ -621,6 +717,19 @@ int32_t substages(void* x, int32_t x_dtype, int64_t ldx, int64_t n_rows, const i
   a.counters = tile_counters ? tile_counters : counters_for_current_device();
   if (!a.counters) return MANTIS_E_LAUNCH;
   const bool vc = stages[0].vcls != nullptr;
+  if (proj) {
+    // one stage without class values over fp16 rows (the windows <- cells
+    // stage), then the row projection
+    if (x_dtype != MANTIS_F16 || n_stages != 1 || vc || init || skip_empty) return MANTIS_E_ARG;
+    if (!proj->w || !proj->b || !proj->out || proj->ld < kK || proj->ld % 8 || !aligned16(proj->w) ||
+        !aligned16(proj->b) || !aligned16(proj->out) || proj->out == x)
+      return MANTIS_E_ARG;
+    a.wp = static_cast<const _Float16*>(proj->w);
+    a.bp = proj->b;
+    a.pout = static_cast<_Float16*>(proj->out);
+    a.ldp = proj->ld;
+    return launch<1, false, _Float16, true>(a, stream);
+  }
   // instantiated: fp32 rows (windows, one stage, and the cell stages' fp32
   // form), fp16 rows (the cells' two stages)
   if (x_dtype == MANTIS_F16) {
@@ -665,6 +774,15 @@ extern "C" int32_t mantis_attention_substages_covered(void* x, int32_t x_dtype, 
   const InitRows init{x_init, ld_init, n_init, init_idx, init_cover};
   return substages(x, x_dtype, ldx, n_rows, row_order, stage, 1, x_init ? &init : nullptr, err_flag, tile_counters,
                    stream, true);
+}
+
+extern "C" int32_t mantis_attention_substage_project(void* x, int32_t x_dtype, int64_t ldx, int64_t n_rows,
+                                                     const int32_t* row_order, const mantis_substage* stage,
+                                                     const void* wp, const float* bp, void* pout, int64_t ldp,
+                                                     int32_t* err_flag, uint32_t* tile_counters, void* stream) {
+  const ProjRows proj{wp, bp, pout, ldp};
+  return substages(x, x_dtype, ldx, n_rows, row_order, stage, 1, nullptr, err_flag, tile_counters, stream, false,
+                   &proj);
 }
 
 extern "C" int32_t mantis_attention_substage(float* x, int64_t ldx, int64_t n_rows, const void* wq, const float* bq,

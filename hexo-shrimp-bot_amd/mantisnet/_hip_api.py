@@ -63,6 +63,7 @@ SIGNATURES = {
     "mantis_attention_substages": ([vp, i32, i64, i64, vp, vp, i32, vp, vp, vp], i32),
     "mantis_attention_substages_init": ([vp, i32, i64, i64, vp, vp, i32, vp, i64, i64, vp, i64, vp, vp, vp], i32),
     "mantis_attention_substages_covered": ([vp, i32, i64, i64, vp, vp, vp, i64, i64, vp, i64, vp, vp, vp], i32),
+    "mantis_attention_substage_project": ([vp, i32, i64, i64, vp, vp, vp, vp, vp, i64, vp, vp, vp], i32),
     "mantis_radius_chunks_capacity": ([i64, i64], i64),
     "mantis_radius_chunks": ([vp, vp, i32, i64, i64, i64, vp, i64, vp, vp, vp], i32),
     "mantis_radius_prep": ([vp, vp, i64, vp, i64, vp, vp, i64, i64, i64, vp, i64, vp, i64, vp, vp, vp, vp, vp], i32),

@@ -721,8 +721,24 @@ def _substage(W, P, pb, key, kv, bias, vcls, ptr, src, cls) -> ops.SubStage:
 # bounds it with its wavefronts idle half the time between chunk barriers.
 SPLIT_CELL_STAGES = False
 
+# The windows <- cells sub-stage also writes the stones <- windows value
+# projection v(ln_sw_w(w)) of the rows it updates (True, the default), or the
+# projection is a launch of its own after it (False); bitwise the same.
+FUSE_WINDOW_PROJECTION = True
+
+
+def _windows_from_cells(W, pb, w, wr):
+    """The windows <- cells sub-stage in place on w; returns the value
+    projection of the updated w when the launch forms it, else None."""
+    if FUSE_WINDOW_PROJECTION and w.dtype == HALF and W[pb + "wproj.w"].shape[0] == 128:
+        return ops.attention_substage_project(w, wr, W[pb + "wproj.w"], W[pb + "wproj.b"])
+    ops.attention_substages(w, [wr])
+    return None
+
 
 def _cell_stage(W, P, pb, plan: Plan, s, w, c, c_init=None):
+    """Returns the windows' value projection when the last sub-stage formed
+    it (see _windows_from_cells), else None."""
     # cells <- windows (decoder classes, class values) then cells <- stones
     # (radius classes, class values); then windows <- cells (decoder classes).
     # Each sub-stage is LN -> q -> attention -> o -> residual.
@@ -737,8 +753,7 @@ def _cell_stage(W, P, pb, plan: Plan, s, w, c, c_init=None):
         _structure_out(W, pb, c, u)
         wr = _substage(W, P, pb, "wr", _proj(W, pb + "wr_kv", c), "wr_bias", None, plan.win_ptr,
                        plan.edge_wcell_cov, plan.edge_wclass)
-        ops.attention_substages(w, [wr])
-        return
+        return _windows_from_cells(W, pb, w, wr)
     cr = _substage(W, P, pb, "cr", _proj(W, pb + "cr_kv", w), "cr_bias", W[pb + "cr_vcls"], plan.cell_ptr,
                    plan.edge_window, plan.edge_class)
     rad_kv = _proj(W, pb + "rad_kv", s)
@@ -771,7 +786,7 @@ def _cell_stage(W, P, pb, plan: Plan, s, w, c, c_init=None):
     else:
         wr = _substage(W, P, pb, "wr", _proj(W, pb + "wr_kv", c), "wr_bias", None, plan.win_ptr, plan.edge_wcell,
                        plan.edge_wclass)
-    ops.attention_substages(w, [wr])
+    return _windows_from_cells(W, pb, w, wr)
 
 
 def _structure_in(W, pb, c):
@@ -855,14 +870,16 @@ def _block(W, P, i: int, plan: Plan, b: Batch, sg, w, c, sw_all, update_stones: 
        add2=W[pb + "ws_tab"], add2_rows=b.window_feat, relu=True, w3=W[pb + "mlp_w3.w"], b3=W[pb + "mlp_w3.b"],
        out=w, residual=True, residual_from_x=w_init is not None)
     # §5.1b cell stage, or the knob-off cell pass
+    wp = None
     if c is not None:
-        _cell_stage(W, P, pb, plan, s, w, c, c_init)
+        wp = _cell_stage(W, P, pb, plan, s, w, c, c_init)
     else:
         _cell_pass(W, P, pb, plan, b, w)
     # §5.2 stones <- windows: s += mlp_s(LN s, agg + class term); w does not
     # change again until the latent broadcast, so its latent-read keys/values
     # and broadcast queries are projected here in the same launch
-    wp = _proj(W, pb + "wproj", w)  # (n_w, 128 or 512): v [| latent k | latent v | broadcast q]
+    if wp is None:
+        wp = _proj(W, pb + "wproj", w)  # (n_w, 128 or 512): v [| latent k | latent v | broadcast q]
     agg = ops.run_reduce(wp[:, :128], plan.run_window, plan.inc_stone_ptr, n_s, F32)
     FL(s, W[pb + "mlp_s1.w"], W[pb + "mlp_s1.b"], layer_norm=True, x2=agg, w2=W[pb + "mlp_s2.w"],
        add1=sw_all[:, 128 * i:128 * (i + 1)], relu=True, w3=W[pb + "mlp_s3.w"], b3=W[pb + "mlp_s3.b"],

@@ -1064,6 +1064,50 @@ def attention_substages(x: Tensor, stages: list[SubStage], row_order: Tensor | N
     return x
 
 
+def attention_substage_project(x: Tensor, stage: SubStage, wp: Tensor, bp: Tensor,
+                               row_order: Tensor | None = None, out: Tensor | None = None) -> Tensor:
+    """One sub-stage without class values (see attention_substages) in place
+    on the fp16 rows x (n, 128), then in the same launch the projection of
+    the updated rows fp16(LN(x) wp^T + bp) (wp (128, 128) fp16 with the
+    LayerNorm's gain folded in, bp (128,) fp32) into ``out`` (n, 128) fp16,
+    returned: bitwise attention_substages then fused_linear(x, wp, bp,
+    layer_norm=True)."""
+    dev = _on_gpu(x, row_order, wp, bp, *[t for t in stage])
+    if x.ndim != 2 or x.shape[1] != 128 or x.dtype != torch.float16 or x.stride(1) != 1:
+        raise ValueError("x must be fp16 (n, 128) rows")
+    if stage.vcls is not None:
+        raise ValueError("the projecting sub-stage carries no class values")
+    if wp.dtype != torch.float16 or wp.shape != (128, 128) or not wp.is_contiguous():
+        raise ValueError("wp must be a contiguous fp16 (128, 128) weight")
+    if bp.dtype != torch.float32 or bp.shape != (128,) or not bp.is_contiguous():
+        raise ValueError("bp must be a contiguous fp32 (128,) bias")
+    if row_order is not None:
+        if row_order.dtype != torch.int32 or row_order.shape != (x.shape[0],):
+            raise ValueError("row_order must be an int32 permutation of the rows")
+        row_order = row_order.contiguous()
+    n = x.shape[0]
+    if out is None:
+        out = torch.empty((n, 128), dtype=torch.float16, device=x.device)
+    elif (out.dtype != torch.float16 or out.shape != (n, 128) or out.stride(1) != 1 or out.stride(0) % 8
+          or out.data_ptr() % 16):
+        raise ValueError("out must be fp16 (n, 128) rows, 16-byte aligned, row stride a multiple of 8")
+    if out.data_ptr() == x.data_ptr():
+        raise ValueError("out must not be x")
+    d, keep, e = _substage_struct(stage, n)  # keep: the tensors d points into
+    if n:
+        arr = (_hip_api.MantisSubstage * 1)(d)
+        nbytes = n * 128 * 2 * 3 + n * 8 + e * 16 + stage.kv.shape[0] * 256 * 2
+        flops = 2 * n * 128 * 128 * 3 + e * 4 * 128 * 2
+        _launch("attention_substage_project_f16", nbytes, flops, lambda: _check(
+            _lib().mantis_attention_substage_project(_ptr(x), _dt(x), x.stride(0), n, _ptr(row_order),
+                                                     ctypes.cast(arr, ctypes.c_void_p), _ptr(wp), _ptr(bp),
+                                                     _ptr(out), out.stride(0), _ptr(error_flag(dev)),
+                                                     _ptr(tile_counters(dev)), _stream()),
+            "attention_substage_project",
+        ))
+    return out
+
+
 def attention_substage(x: Tensor, wq: Tensor, bq: Tensor, kv: Tensor, bias: Tensor, vcls: Tensor | None,
                        seg_ptr: Tensor, src: Tensor, cls: Tensor, wo: Tensor, bo: Tensor) -> Tensor:
     """One sub-stage (see attention_substages), in place on x."""

@@ -456,6 +456,23 @@ int32_t mantis_attention_substages_init(void* x, int32_t x_dtype, int64_t ldx, i
                                         void* stream);
 
 /*
+ * One sub-stage without class values (as mantis_attention_substages, one
+ * stage) over fp16 rows, followed in the same launch by the LayerNorm'd row
+ * projection of each updated row as stored: pout[r] = fp16(LN(x[r]) wp^T +
+ * bp), wp (128, 128) fp16 with the LayerNorm's gain folded in, bp 128 fp32,
+ * pout (n_rows, 128) fp16 with row stride ldp (a multiple of 8, not x).
+ * Bitwise the rows of mantis_attention_substages followed by
+ * mantis_fused_linear(x, wp, bp, layer_norm).  The windows <- cells
+ * sub-stage and the stones <- windows value projection y = v(ln_sw_w(w))
+ * that follows it (model.py:397-490, 609), one read of the window rows
+ * instead of two.  x_dtype must be MANTIS_F16.
+ */
+int32_t mantis_attention_substage_project(void* x, int32_t x_dtype, int64_t ldx, int64_t n_rows,
+                                          const int32_t* row_order, const mantis_substage* stage, const void* wp,
+                                          const float* bp, void* pout, int64_t ldp, int32_t* err_flag,
+                                          uint32_t* tile_counters, void* stream);
+
+/*
  * One sub-stage (as mantis_attention_substages) over the rows of x whose run
  * of the stage is non-empty; the other rows are neither read nor written (a
  * later mantis_radius_stage with pre_bias = this stage's bo adds the stage's

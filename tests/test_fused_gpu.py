@@ -417,6 +417,40 @@ def test_two_substages_in_one_pass_match_two_launches(device, with_vcls):
     assert got16.dtype == H16 and torch.equal(got16.cpu(), two16.cpu())
 
 
+@pytest.mark.parametrize("n", [1, 37, 2011])
+def test_substage_with_the_row_projection_matches_the_projection_launch(device, n):
+    # windows <- cells and the stones <- windows value projection of the
+    # updated rows in one launch: bitwise the sub-stage launch followed by the
+    # LayerNorm'd projection launch, in the natural and a permuted row order,
+    # into a fresh and into a strided output
+    gen = _g(19)
+    st = _random_stage(gen, n, 301, 192, False, 9)
+    s1 = ops.SubStage(*[None if t is None else t.to(device) for t in st])
+    wp = _w(128, 128, gen).to(device)
+    bp = (0.1 * torch.randn(128, generator=gen)).to(device)
+    x16 = (2 * torch.randn(n, 128, generator=gen) - 0.3).to(H16)
+    ref = x16.to(device)
+    ops.attention_substages(ref, [s1])
+    want = ops.fused_linear(ref, wp, bp, layer_norm=True)
+    ops.raise_on_device_error(device)
+    for order in (None, torch.randperm(n, generator=gen).to(torch.int32).to(device)):
+        got = x16.to(device)
+        proj = ops.attention_substage_project(got, s1, wp, bp, row_order=order)
+        ops.raise_on_device_error(device)
+        assert torch.equal(got.cpu(), ref.cpu())
+        assert proj.shape == (n, 128) and proj.dtype == H16 and torch.equal(proj.cpu(), want.cpu())
+    buf = torch.full((n, 192), 7.0, dtype=H16, device=device)
+    got = x16.to(device)
+    ops.attention_substage_project(got, s1, wp, bp, out=buf[:, 32:160])
+    ops.raise_on_device_error(device)
+    assert torch.equal(buf[:, 32:160].cpu(), want.cpu())
+    assert bool((buf[:, :32] == 7).all()) and bool((buf[:, 160:] == 7).all())
+    with pytest.raises(ValueError):
+        ops.attention_substage_project(x16.float().to(device), s1, wp, bp)
+    with pytest.raises(ValueError):
+        ops.attention_substage_project(got, s1, wp, bp, out=got)
+
+
 def test_two_substages_with_many_tiles_per_wavefront(device):
     # more rows than one sweep of the persistent grid (256 CUs x 8 wavefronts
     # x 16 rows), in a random row order: every wavefront walks several tiles

@@ -306,6 +306,31 @@ def test_weights_changed_between_evaluations_are_used(device):
         assert _same_outputs(got, fresh(batch, 0.2))
 
 
+@pytest.mark.parametrize("knobs", [dict(), dict(cell_latents=True, cell_nodes=False)])
+def test_fused_window_projection_is_bitwise_the_separate_launch(device, knobs):
+    # the windows <- cells sub-stage forming the stones <- windows value
+    # projection in the same launch, against the projection as a launch of its
+    # own after it: the production forward and covered-only cell latents
+    from mantisnet import forward, ops
+
+    net = _model(device, MantisConfig(**knobs) if knobs else PRODUCTION, seed=5)
+    batch = collate_positions(synthetic.random_games(4, 10, start=500)).to(device)
+    print(f"knobs {knobs}: {batch.n_pos} positions, {batch.n_cells} cells", flush=True)
+    saved = forward.FUSE_WINDOW_PROJECTION
+    try:
+        outs = []
+        for fuse in (True, False):
+            forward.FUSE_WINDOW_PROJECTION = fuse
+            with torch.no_grad():
+                outs.append(net(batch, 0.2))
+            ops.raise_on_device_error(device)
+    finally:
+        forward.FUSE_WINDOW_PROJECTION = saved
+    a, b = outs
+    for name in ("policy_logits", "q_values", "value", "value_dist"):
+        assert torch.equal(getattr(a, name), getattr(b, name)), name
+
+
 @pytest.mark.parametrize("knobs,config,count", [
     (dict(cell_latents=True, cell_nodes=True, cell_adjacency=True), 4, 10),
     (dict(cell_latents=True, cell_nodes=True, action_tactical=True), 4, 10),
