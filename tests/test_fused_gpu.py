@@ -55,6 +55,31 @@ def test_projection_with_layer_norm(device, n1, xdt):
     torch.testing.assert_close(out.float().cpu(), exp, rtol=2e-3, atol=2e-3)
 
 
+@pytest.mark.parametrize("n1", [128, 256])
+@pytest.mark.parametrize("m", [1, 255, 256, 257, 20011])
+def test_fp16_row_projection_is_bitwise_the_fp32_row_projection(device, n1, m):
+    # the fp16-row LayerNorm projection against the fp32-row launch on the
+    # same values: the same LayerNorm and product arithmetic, so bitwise the
+    # same rows, with and without a gather (negative indices give zero rows),
+    # at row counts around the 128-row workgroup tile
+    gen = _g(n1 + m)
+    x16 = (3 * torch.randn(m, 128, generator=gen) + 1).to(H16).to(device)
+    w = _w(n1, 128, gen).to(device)
+    b = (0.1 * torch.randn(n1, generator=gen)).to(device)
+    for rows in (None, torch.randint(-1, m, (m + 37,), generator=gen).to(device)):
+        got = ops.fused_linear(x16, w, b, layer_norm=True, x_rows=rows)
+        want = ops.fused_linear(x16.float(), w, b, layer_norm=True, x_rows=rows)
+        ops.raise_on_device_error(device)
+        assert got.dtype == H16 and got.shape == want.shape and torch.equal(got, want)
+    # an index past the rows: a zero row, flagged
+    bad = torch.arange(m, device=device)
+    bad[m // 2] = m
+    got = ops.fused_linear(x16, w, b, layer_norm=True, x_rows=bad)
+    with pytest.raises(ValueError):
+        ops.raise_on_device_error(device)
+    assert torch.equal(got[m // 2].float(), b.to(H16).float())
+
+
 @pytest.mark.parametrize("xdt", [torch.float32, H16])
 def test_residual_projection(device, xdt):
     gen = _g(2)
