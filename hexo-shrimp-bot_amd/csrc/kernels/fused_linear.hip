@@ -146,73 +146,10 @@ __global__ void __launch_bounds__((threads_for<N1, kX2, kStage2>())) fused_linea
   // the lo rows of a split matrix follow its hi rows
   constexpr int kLo1 = N1 * kPitch;
 
-  // Stage the weights (16-byte chunks; [hi; lo] rows with kSplit), every
-  // chunk of a thread requested before any is stored: a launch over few rows
-  // is as long as its staging, and one chunk at a time would make that a
-  // chain of dependent L2 round trips.
-  constexpr int kT = threads_for<N1, kX2, kStage2>();
-  // (native vector elements: an array of them stays in registers)
-  typedef uint32_t w4_t __attribute__((ext_vector_type(4)));
-  {
-    constexpr int n = kParts * N1 * (kK / 8);
-    static_assert(n % kT == 0, "whole chunks per thread");
-    constexpr int kPer = n / kT;
-    w4_t v1[kPer], v2[kX2 ? kPer : 1];
-#pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-      const int i = int(threadIdx.x) + u * kT;
-      const int r = i / (kK / 8), c = (i % (kK / 8)) * 8;
-      // LDS row r = 16 nt + 4 g + t holds feature pair_feature(nt, g, t) with kPair
-      const int src = kPair ? (r / N1) * N1 + pair_feature((r % N1) >> 4, (r & 15) >> 2, r & 3) : r;
-      v1[u] = *reinterpret_cast<const w4_t*>(a.w1 + src * kK + c);
-      if constexpr (kX2) v2[u] = *reinterpret_cast<const w4_t*>(a.w2 + r * kK + c);
-    }
-#pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-      const int i = int(threadIdx.x) + u * kT;
-      const int r = i / (kK / 8), c = (i % (kK / 8)) * 8;
-      *reinterpret_cast<w4_t*>(sw1 + r * kPitch + c) = v1[u];
-      if constexpr (kX2) *reinterpret_cast<w4_t*>(sw2 + r * kPitch + c) = v2[u];
-    }
-  }
-  if constexpr (kStage2) {
-    // W3 rows (with kResidReg LDS row r = 16 ot + 4 g + t holds W3 row
-    // pair_feature(ot, g, t)); the 128-row form in one batch
-    constexpr int kFull = kParts * 128 * (N1 / 8);
-    auto w3_chunk = [&](int i, int& r, int& c) -> w4_t {
-      r = i / (N1 / 8), c = (i % (N1 / 8)) * 8;
-      const int src = kResidReg ? pair_feature(r >> 4, (r & 15) >> 2, r & 3) : r;
-      return *reinterpret_cast<const w4_t*>(a.w3 + src * N1 + c);
-    };
-    if (a.n3 == 128 && kFull % kT == 0) {
-      constexpr int kPer = kFull / kT;
-      w4_t v3[kPer];
-#pragma unroll
-      for (int u = 0; u < kPer; ++u) {
-        int r, c;
-        v3[u] = w3_chunk(int(threadIdx.x) + u * kT, r, c);
-      }
-#pragma unroll
-      for (int u = 0; u < kPer; ++u) {
-        const int i = int(threadIdx.x) + u * kT;
-        const int r = i / (N1 / 8), c = (i % (N1 / 8)) * 8;
-        *reinterpret_cast<w4_t*>(sw3 + r * S::p3 + c) = v3[u];
-      }
-    } else {
-      for (int i = threadIdx.x; i < kParts * a.n3 * (N1 / 8); i += kT) {
-        int r, c;
-        const w4_t v = w3_chunk(i, r, c);
-        *reinterpret_cast<w4_t*>(sw3 + r * S::p3 + c) = v;
-      }
-    }
-  }
-  float* sb1 = reinterpret_cast<float*>(smem + S::bias_off(a.n3));
-  float* sb3 = sb1 + N1;
-  for (int i = threadIdx.x; i < N1; i += blockDim.x) sb1[i] = a.b1 ? a.b1[i] : 0.f;
-  if constexpr (kStage2)
-    for (int i = threadIdx.x; i < a.n3; i += blockDim.x) sb3[i] = a.b3 ? a.b3[i] : 0.f;
-  __syncthreads();
-
+  // The first tile's rows (and the gather indices ahead of them) are
+  // requested before the weights are staged: a launch with one or two tiles
+  // per wavefront (the stones, the latents) then waits for both latencies at
+  // once instead of one after the other.
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
   const int l16 = lane % 16, g = lane / 16;
   const int64_t n_tiles = (a.m + kTileRows - 1) / kTileRows;
@@ -290,6 +227,74 @@ __global__ void __launch_bounds__((threads_for<N1, kX2, kStage2>())) fused_linea
   if constexpr (kX2) load_x2(blockIdx.x, x2r);
   int64_t grp_n = grp_at(blockIdx.x);
   int64_t idx_n = idx_at(blockIdx.x + G);  // the gather index one tile ahead
+
+  // Stage the weights (16-byte chunks; [hi; lo] rows with kSplit), every
+  // chunk of a thread requested before any is stored: a launch over few rows
+  // is as long as its staging, and one chunk at a time would make that a
+  // chain of dependent L2 round trips.
+  constexpr int kT = threads_for<N1, kX2, kStage2>();
+  // (native vector elements: an array of them stays in registers)
+  typedef uint32_t w4_t __attribute__((ext_vector_type(4)));
+  {
+    constexpr int n = kParts * N1 * (kK / 8);
+    static_assert(n % kT == 0, "whole chunks per thread");
+    constexpr int kPer = n / kT;
+    w4_t v1[kPer], v2[kX2 ? kPer : 1];
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int i = int(threadIdx.x) + u * kT;
+      const int r = i / (kK / 8), c = (i % (kK / 8)) * 8;
+      // LDS row r = 16 nt + 4 g + t holds feature pair_feature(nt, g, t) with kPair
+      const int src = kPair ? (r / N1) * N1 + pair_feature((r % N1) >> 4, (r & 15) >> 2, r & 3) : r;
+      v1[u] = *reinterpret_cast<const w4_t*>(a.w1 + src * kK + c);
+      if constexpr (kX2) v2[u] = *reinterpret_cast<const w4_t*>(a.w2 + r * kK + c);
+    }
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int i = int(threadIdx.x) + u * kT;
+      const int r = i / (kK / 8), c = (i % (kK / 8)) * 8;
+      *reinterpret_cast<w4_t*>(sw1 + r * kPitch + c) = v1[u];
+      if constexpr (kX2) *reinterpret_cast<w4_t*>(sw2 + r * kPitch + c) = v2[u];
+    }
+  }
+  if constexpr (kStage2) {
+    // W3 rows (with kResidReg LDS row r = 16 ot + 4 g + t holds W3 row
+    // pair_feature(ot, g, t)); the 128-row form in one batch
+    constexpr int kFull = kParts * 128 * (N1 / 8);
+    auto w3_chunk = [&](int i, int& r, int& c) -> w4_t {
+      r = i / (N1 / 8), c = (i % (N1 / 8)) * 8;
+      const int src = kResidReg ? pair_feature(r >> 4, (r & 15) >> 2, r & 3) : r;
+      return *reinterpret_cast<const w4_t*>(a.w3 + src * N1 + c);
+    };
+    if (a.n3 == 128 && kFull % kT == 0) {
+      constexpr int kPer = kFull / kT;
+      w4_t v3[kPer];
+#pragma unroll
+      for (int u = 0; u < kPer; ++u) {
+        int r, c;
+        v3[u] = w3_chunk(int(threadIdx.x) + u * kT, r, c);
+      }
+#pragma unroll
+      for (int u = 0; u < kPer; ++u) {
+        const int i = int(threadIdx.x) + u * kT;
+        const int r = i / (N1 / 8), c = (i % (N1 / 8)) * 8;
+        *reinterpret_cast<w4_t*>(sw3 + r * S::p3 + c) = v3[u];
+      }
+    } else {
+      for (int i = threadIdx.x; i < kParts * a.n3 * (N1 / 8); i += kT) {
+        int r, c;
+        const w4_t v = w3_chunk(i, r, c);
+        *reinterpret_cast<w4_t*>(sw3 + r * S::p3 + c) = v;
+      }
+    }
+  }
+  float* sb1 = reinterpret_cast<float*>(smem + S::bias_off(a.n3));
+  float* sb3 = sb1 + N1;
+  for (int i = threadIdx.x; i < N1; i += blockDim.x) sb1[i] = a.b1 ? a.b1[i] : 0.f;
+  if constexpr (kStage2)
+    for (int i = threadIdx.x; i < a.n3; i += blockDim.x) sb3[i] = a.b3 ? a.b3[i] : 0.f;
+  __syncthreads();
+
   for (int64_t tile = blockIdx.x; tile < n_tiles; tile += G) {
     const int64_t row = row_of(tile);
     const bool live = row < a.m;
