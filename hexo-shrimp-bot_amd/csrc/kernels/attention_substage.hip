@@ -141,11 +141,6 @@ struct SubArgs {
   int64_t ldp;
 };
 
-// Features of lane group g in output tiles 2k and 2k+1 of the row projection
-// when its weight rows are staged in this order: 32 k + 8 g .. +7, one
-// 16-byte store per pair of tiles
-__device__ __forceinline__ int pair_feature(int nt, int g, int t) { return 32 * (nt >> 1) + 8 * g + 4 * (nt & 1) + t; }
-
 template <int kStages, bool kVcls, typename TX, bool kProj = false>
 __global__ void __launch_bounds__(waves_for<kStages>() * 64) attn_substage_kernel(SubArgs a) {
   static_assert(!kProj || (kStages == 1 && sizeof(TX) == 2), "the row projection follows one stage over fp16 rows");

@@ -41,6 +41,13 @@ __device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
   return pack_f16x2_unit(fminf(fmaxf(lo, -65504.f), 65504.f), fminf(fmaxf(hi, -65504.f), 65504.f));
 }
 
+// Output tiles 2k and 2k+1 of a row projection whose weight rows are staged
+// so that LDS (or fragment) row 16 nt + 4 g + t holds feature
+// pair_feature(nt, g, t): lane group g of the MFMA D fragments then holds
+// the eight consecutive features 32 k + 8 g .. +7 of its row, one 16-byte
+// store per pair of tiles instead of two 8-byte ones.
+__device__ __forceinline__ int pair_feature(int nt, int g, int t) { return 32 * (nt >> 1) + 8 * g + 4 * (nt & 1) + t; }
+
 // Eight consecutive elements of a row as fp32: one 16-byte load for bf16,
 // two for fp32.  `p` must be 16-byte aligned.
 __device__ __forceinline__ void load8(const uint16_t* p, float (&x)[8]) {

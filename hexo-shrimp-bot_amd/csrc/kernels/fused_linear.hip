@@ -119,11 +119,8 @@ struct Smem {
 template <int N1, bool kX2 = false, bool kStage2 = false>
 constexpr int threads_for() { return N1 >= 512 ? 1024 : 512; }
 
-// kPair (single stage, fp16 out): the W1 rows are staged permuted so that
-// feature tiles 2k and 2k+1 leave lane group g holding the eight consecutive
-// features 32k + 8g .. +7 of its row: one 16-byte store per pair of tiles
-// instead of two 8-byte ones.
-__device__ __forceinline__ int pair_feature(int nt, int g, int t) { return 32 * (nt >> 1) + 8 * g + 4 * (nt & 1) + t; }
+// kPair (single stage, fp16 out): the W1 rows are staged in pair_feature
+// order (common.hpp), one 16-byte store per pair of output tiles.
 
 template <typename TX, typename TX2, bool kLN, int N1, bool kX2, bool kRelu, bool kStage2, int kMode,
           bool kSplit = false, bool kPair = false>
