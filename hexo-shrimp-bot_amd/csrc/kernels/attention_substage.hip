@@ -50,6 +50,14 @@
 // order (a permutation of the rows) groups rows of similar entry counts into
 // tiles; each row's arithmetic is the same in any order, so the results are
 // bitwise those of the natural order.
+//
+// The projecting form (kProj: one stage without class values over fp16 rows,
+// the windows <- cells stage) also writes the row projection that reads the
+// updated rows next, p = fp16( LN(x) Wp^T + bp ) (the stones <- windows value
+// projection, model.py:609): after the stage the row is still in registers,
+// so its LayerNorm and the 128 x 128 product (Wp in the workgroup's free LDS,
+// rows in pair_feature order) take the place of a launch that would read it
+// back.  The arithmetic is the row GEMM's, so p is bitwise that launch's.
 #include "common.hpp"
 #include "mfma.hpp"
 #include "substage.hpp"
