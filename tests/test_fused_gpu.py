@@ -474,6 +474,19 @@ def test_substage_with_the_row_projection_matches_the_projection_launch(device, 
         ops.attention_substage_project(x16.float().to(device), s1, wp, bp)
     with pytest.raises(ValueError):
         ops.attention_substage_project(got, s1, wp, bp, out=got)
+    if n > 5:
+        # an order entry out of range: flagged, its slot skipped (row 5 is
+        # neither updated nor projected), every other row as before
+        bad = torch.arange(n, dtype=torch.int32)
+        bad[5] = n
+        got = x16.to(device)
+        proj = ops.attention_substage_project(got, s1, wp, bp, row_order=bad.to(device))
+        with pytest.raises(ValueError):
+            ops.raise_on_device_error(device)
+        keep = torch.ones(n, dtype=torch.bool)
+        keep[5] = False
+        assert torch.equal(got.cpu()[keep], ref.cpu()[keep]) and torch.equal(got.cpu()[5], x16[5])
+        assert torch.equal(proj.cpu()[keep], want.cpu()[keep])
 
 
 def test_two_substages_with_many_tiles_per_wavefront(device):
